@@ -1,0 +1,111 @@
+/*
+ * C ABI of the MI355X (gfx950) HSTU jagged attention forward.
+ *
+ * One shared library, plain pointers and sizes, no C++ or torch types.  Every entry point that
+ * launches work does so asynchronously on the HIP stream the caller passes; nothing synchronises
+ * with the host, nothing is allocated, and the sequence offsets are read on the device.
+ *
+ * Operator computed (per sequence b with tokens [s, e), n = e - s, t = num_targets[b],
+ * cap = n - t, local positions m, j in [0, n), head h):
+ *
+ *   keep(m,j)  = (m == j) or (m >= j and j < cap) or contextual(j)
+ *   S(m,j)     = alpha * sum_d q[s+m,h,d] * k[s+j,h,d]  (+ rab[h, m - j + max_seq_len - 1])
+ *   P(m,j)     = S * sigmoid(S) * scale          scale = attn_scale or 1 / max_seq_len
+ *   out[s+m,h] = sum_j keep(m,j) * P(m,j) * v[s+j,h]
+ *   out[r]     = 0 for r >= seq_offsets[B]
+ */
+#ifndef RECIR_HSTU_H_
+#define RECIR_HSTU_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RECIR_HSTU_ABI_VERSION 1
+
+/* element types of q/k (v and out follow: bf16 for BF16 and FP8_E4M3, fp32 for FP32) */
+#define RECIR_HSTU_DTYPE_BF16 0
+#define RECIR_HSTU_DTYPE_FP32 1
+#define RECIR_HSTU_DTYPE_FP8_E4M3 2 /* q,k are OCP e4m3fn bytes with per-head scales; v,out bf16 */
+
+/* flags */
+#define RECIR_HSTU_FLAG_OFFSETS_I32 0x1u          /* seq_offsets / num_targets are int32, not int64 */
+#define RECIR_HSTU_FLAG_CTX_REFERENCE 0x2u        /* contextual rule of the reference C++ fallback:
+                                                     when contextual_seq_len > 0 the keys whose
+                                                     target-clamped id is 0 are visible to all
+                                                     (kjt_split_per_feature.cpp:672-674).  Default
+                                                     rule: keys j < contextual_seq_len visible. */
+#define RECIR_HSTU_FLAG_SCALE_PER_TOKEN 0x4u      /* attn_scale is [T], indexed by the query token */
+#define RECIR_HSTU_FLAG_KERNEL_SHIFT 8            /* bits 8..15: kernel selector for tests/tuning  */
+#define RECIR_HSTU_FLAG_KERNEL_MASK 0xff00u       /* 0 auto, 1 generic, 2.. tiled variants         */
+
+/* status codes: 0 ok, negative = rejected before any launch, positive = hipError_t of a launch */
+#define RECIR_HSTU_OK 0
+#define RECIR_HSTU_ERR_INVALID_ARGUMENT (-1)
+#define RECIR_HSTU_ERR_UNSUPPORTED (-2)
+#define RECIR_HSTU_ERR_WORKSPACE (-3)
+
+/*
+ * HSTU jagged attention forward.
+ *
+ * Replaces: facebook::recir::raggedAttention, the implementation behind the operator schema
+ *   hammer::triton_ragged_attention_fwd(int N, float alpha, Tensor q, Tensor k, Tensor v,
+ *       Tensor seq_offsets, str invalid_attn_mask_type, Tensor? num_targets, Tensor? attn_scale,
+ *       int max_attn_len, int contextual_seq_len, int full_attn_size, int num_softmax_heads)
+ *   (recir/ops/kjt_split_per_feature.cpp:602-693, schema :780-783), and the packed accelerator
+ *   kernel entry pallas_jagged_hstu_attention (recir/ops/pallas/jagged_hstu_attention.py:1518-1591)
+ *   / hstu_ragged_attention_fwd_jax_fn (recir/ops/helion/jagged_hstu_attention.py:830-872).
+ *   Only the causal ("lower_triangular") mask with max_attn_len = full_attn_size =
+ *   num_softmax_heads = 0 is covered; the host wrapper rejects anything else.
+ *
+ * q, k          device, [T, H, Dqk] row-major contiguous, element type `dtype`
+ * v, out        device, [T, H, Dv]; out is written in full: rows < seq_offsets[B] get the result,
+ *               rows in [seq_offsets[B], T) are zeroed (pallas/jagged_hstu_attention.py:323-344)
+ * seq_offsets   device, [B+1] int64 (int32 with FLAG_OFFSETS_I32), non-decreasing, last <= T.
+ *               Malformed entries are clamped on the device (no fault, result unspecified).
+ * num_targets   device, [B] or NULL (= zeros)
+ * rab           device float [H, 2*max_seq_len-1] or NULL.  No counterpart in the reference.
+ * attn_scale    device float scalar, [T] with FLAG_SCALE_PER_TOKEN, or NULL (= 1/max_seq_len)
+ * q_scale,k_scale  device float [H]; FP8_E4M3 only (dequantisation factors), else NULL
+ * workspace     device scratch of at least recir_hstu_attn_fwd_workspace_bytes(...) bytes, 16-byte
+ *               aligned; contents need not be initialised; must not be shared by calls that can
+ *               overlap on the device
+ * hip_stream    hipStream_t (NULL = the null stream)
+ */
+int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                        const void* seq_offsets, const void* num_targets, const float* rab,
+                        const float* attn_scale, const float* q_scale, const float* k_scale,
+                        int32_t T, int32_t B, int32_t H, int32_t Dqk, int32_t Dv,
+                        int32_t max_seq_len, int32_t contextual_seq_len, float alpha, int32_t dtype,
+                        uint32_t flags, void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* Scratch size recir_hstu_attn_fwd needs for these sizes (upper bound over all kernel variants). */
+size_t recir_hstu_attn_fwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk,
+                                           int32_t Dv, int32_t dtype);
+
+/*
+ * Per-head symmetric fp8 quantisation of a packed bf16 [T,H,D] tensor:
+ *   scale[h] = max(max_{r,d} |x[r,h,d]|, 1e-12) / 448,  codes = e4m3fn(clamp(x / scale[h], +-448)).
+ * Replaces: quantizeFp8Rowwise (recir/ops/kjt_split_per_feature.cpp:493-502), applied per head
+ * instead of per row.  `scale` ([H] float, device) is both an output and the scratch of the amax
+ * reduction.
+ */
+int recir_hstu_quantize_e4m3_per_head(const void* x_bf16, void* codes_u8, float* scale, int32_t T,
+                                      int32_t H, int32_t D, void* hip_stream);
+
+/* Thread-local, NUL-terminated description of the last non-zero status on this thread. */
+const char* recir_hstu_last_error(void);
+
+/* RECIR_HSTU_ABI_VERSION the library was built with. */
+int recir_hstu_abi_version(void);
+
+/* Name of the kernel variant the last successful recir_hstu_attn_fwd on this thread launched. */
+const char* recir_hstu_last_kernel(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RECIR_HSTU_H_ */

@@ -1,0 +1,207 @@
+/*
+ * CPU oracle for the HSTU jagged attention forward.  TEST INFRASTRUCTURE ONLY.
+ *
+ * This file is a plain-C restatement of the reference algorithm.  It exists so
+ * that tests, the smoke check and the benchmark's CPU-baseline leg have an
+ * independent answer to compare the HIP kernels with.  The product library
+ * never links, loads or calls it.
+ *
+ * Reference lines each function follows (paths relative to the upstream tree):
+ *   hstu_oracle_keep            recir/ops/helion/jagged_hstu_attention.py:185-208, :346
+ *   hstu_oracle_keep_clamp_id   recir/ops/kjt_split_per_feature.cpp:639-674,
+ *                               recir/ops/pallas/hstu_attention.py:86-112, :404-430
+ *   hstu_oracle_attn_fwd        recir/ops/kjt_split_per_feature.cpp:602-693 (per-sequence loop,
+ *                               alpha on the scores, x*sigmoid(x), attn_scale or 1/max_seq_len,
+ *                               mask multiply, weights @ v) with the packed [T,H,Dv] output and
+ *                               zeroed tail of recir/ops/pallas/jagged_hstu_attention.py:323-344
+ *   hstu_oracle_e4m3_encode     recir/ops/kjt_split_per_feature.cpp:493-502 (clamp to +-448 then
+ *                               round-to-nearest-even cast to float8_e4m3fn)
+ *
+ * Parity pins (see tests/): the reference's compiled C++ op on seeded inputs
+ * (golden fixtures), the reference's own zero-query known-answer test, two
+ * independent closed forms of the mask compared exhaustively, closed-form
+ * special cases (single token, all-target, constant score => kept-key count),
+ * and torch's own float8_e4m3fn cast for the encoder.
+ * Parity unpinned by the reference: the relative attention bias term (the
+ * reference has no such argument) and contextual_seq_len > 1 in "prefix" mode
+ * (the reference C++ only ever unmasks key 0).  Both are pinned only by the
+ * dense closed form in tests/test_oracle.py.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define HSTU_CTX_PREFIX 0  /* keys j < ctx visible to every query               */
+#define HSTU_CTX_REFCPP 1  /* reference C++: keys whose clamped id is 0 visible  */
+
+/* keep(m, j) in the "causal and key-is-history, or diagonal" form. */
+int hstu_oracle_keep(int64_t m, int64_t j, int64_t n, int64_t t, int64_t ctx, int ctx_mode) {
+  if (m < 0 || j < 0 || m >= n || j >= n) return 0;
+  const int64_t cap = n - t;
+  int keep = (m == j) || (m >= j && j < cap);
+  if (ctx > 0) {
+    if (ctx_mode == HSTU_CTX_PREFIX) {
+      keep = keep || (j < ctx);
+    } else {
+      /* the reference compares the *clamped* key id with zero */
+      const int64_t idj = j < cap ? j : cap;
+      keep = keep || (idj == 0);
+    }
+  }
+  return keep;
+}
+
+/* Same predicate written the way the C++ fallback and the dense JAX reference
+ * build it: ids clamped to the history length, distance > 0 or identity. */
+int hstu_oracle_keep_clamp_id(int64_t m, int64_t j, int64_t n, int64_t t, int64_t ctx,
+                              int ctx_mode) {
+  if (m < 0 || j < 0 || m >= n || j >= n) return 0;
+  const int64_t bound = n - t;
+  const int64_t idm = m < bound ? m : bound;
+  const int64_t idj = j < bound ? j : bound;
+  int keep = (m == j) || (idm - idj > 0);
+  if (ctx > 0) {
+    if (ctx_mode == HSTU_CTX_PREFIX) keep = keep || (j < ctx);
+    else keep = keep || (idj == 0);
+  }
+  return keep;
+}
+
+/* Number of kept (m, j) pairs of one sequence, by brute force. */
+int64_t hstu_oracle_count_pairs(int64_t n, int64_t t, int64_t ctx, int ctx_mode) {
+  int64_t c = 0;
+  for (int64_t m = 0; m < n; ++m)
+    for (int64_t j = 0; j < n; ++j) c += hstu_oracle_keep(m, j, n, t, ctx, ctx_mode);
+  return c;
+}
+
+static float round_to_bf16(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return x; /* NaN */
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  memcpy(&x, &u, 4);
+  return x;
+}
+
+/*
+ * attn_scale_kind: 0 -> 1/max_seq_len, 1 -> attn_scale[0], 2 -> attn_scale[token of the query row].
+ * p_round: 0 keeps P in double; 1 rounds P (after the scale) to bf16 like a bf16 value tensor would
+ *          force in the reference (weights.to(v.dtype)).
+ * Returns 0, or -1 on a malformed offsets array (same condition the reference rejects).
+ */
+int hstu_oracle_attn_fwd(const float* q, const float* k, const float* v, float* out,
+                         const int64_t* seq_offsets, const int64_t* num_targets, const float* rab,
+                         int attn_scale_kind, const float* attn_scale, int64_t T, int64_t B,
+                         int64_t H, int64_t Dqk, int64_t Dv, int64_t max_seq_len, int64_t ctx,
+                         int ctx_mode, double alpha, int p_round) {
+  for (int64_t b = 0; b < B; ++b) {
+    const int64_t s = seq_offsets[b], e = seq_offsets[b + 1];
+    if (!(0 <= s && s <= e && e <= T)) return -1;
+  }
+  memset(out, 0, sizeof(float) * (size_t)(T * H * Dv));
+  const int64_t rab_w = 2 * max_seq_len - 1;
+
+#pragma omp parallel
+  {
+    double* acc = (double*)malloc(sizeof(double) * (size_t)(Dv > 0 ? Dv : 1));
+    for (int64_t b = 0; b < B; ++b) {
+      const int64_t s = seq_offsets[b], e = seq_offsets[b + 1], n = e - s;
+      const int64_t t = num_targets ? num_targets[b] : 0;
+#pragma omp for collapse(2) schedule(dynamic, 8) nowait
+      for (int64_t m = 0; m < n; ++m) {
+        for (int64_t h = 0; h < H; ++h) {
+          const float* qr = q + ((s + m) * H + h) * Dqk;
+          for (int64_t d = 0; d < Dv; ++d) acc[d] = 0.0;
+          double scale;
+          if (attn_scale_kind == 0) scale = 1.0 / (double)max_seq_len;
+          else if (attn_scale_kind == 1) scale = (double)attn_scale[0];
+          else scale = (double)attn_scale[s + m];
+          for (int64_t j = 0; j < n; ++j) {
+            if (!hstu_oracle_keep(m, j, n, t, ctx, ctx_mode)) continue;
+            const float* kr = k + ((s + j) * H + h) * Dqk;
+            double dot = 0.0;
+#pragma omp simd reduction(+ : dot)
+            for (int64_t d = 0; d < Dqk; ++d) dot += (double)qr[d] * (double)kr[d];
+            double x = dot * alpha;
+            if (rab) {
+              const int64_t idx = m - j + max_seq_len - 1;
+              if (idx >= 0 && idx < rab_w) x += (double)rab[h * rab_w + idx];
+            }
+            double p = x / (1.0 + exp(-x)) * scale;
+            if (p_round) p = (double)round_to_bf16((float)p);
+            const float* vr = v + ((s + j) * H + h) * Dv;
+#pragma omp simd
+            for (int64_t d = 0; d < Dv; ++d) acc[d] += p * (double)vr[d];
+          }
+          float* orow = out + ((s + m) * H + h) * Dv;
+          for (int64_t d = 0; d < Dv; ++d) orow[d] = (float)acc[d];
+        }
+      }
+    }
+    free(acc);
+  }
+  return 0;
+}
+
+/* float -> OCP float8 e4m3fn byte: saturate to +-448 first (the reference clamps before the cast),
+ * round to nearest even, keep subnormals, NaN -> 0x7f. */
+uint8_t hstu_oracle_e4m3_encode(float x) {
+  if (x != x) return 0x7f;
+  const uint8_t sign = signbit(x) ? 0x80 : 0x00;
+  double a = fabs((double)x);
+  if (a > 448.0) a = 448.0;
+  if (a == 0.0) return sign;
+  int ex;
+  double mant = frexp(a, &ex); /* a = mant * 2^ex, mant in [0.5, 1) */
+  int E = ex - 1;              /* a = (2*mant) * 2^E, 2*mant in [1, 2) */
+  if (E < -6) {
+    /* subnormal: multiples of 2^-9 */
+    double qv = nearbyint(a * 512.0); /* ties to even under the default rounding mode */
+    if (qv >= 8.0) return sign | 0x08; /* rounds up to the smallest normal 2^-6 */
+    return sign | (uint8_t)qv;
+  }
+  double frac = (2.0 * mant - 1.0) * 8.0; /* in [0, 8) */
+  double qf = nearbyint(frac);
+  int m3 = (int)qf;
+  if (m3 == 8) { m3 = 0; E += 1; }
+  int be = E + 7;
+  if (be > 15 || (be == 15 && m3 > 6)) { be = 15; m3 = 6; } /* 448 = 1.75 * 2^8 */
+  return sign | (uint8_t)(be << 3) | (uint8_t)m3;
+}
+
+float hstu_oracle_e4m3_decode(uint8_t b) {
+  const int sgn = b >> 7, be = (b >> 3) & 0xf, m3 = b & 7;
+  double val;
+  if (be == 15 && m3 == 7) return NAN;
+  if (be == 0) val = (double)m3 / 8.0 * ldexp(1.0, -6);
+  else val = (1.0 + (double)m3 / 8.0) * ldexp(1.0, be - 7);
+  return (float)(sgn ? -val : val);
+}
+
+/* Per-head symmetric quantisation of a packed [T,H,D] tensor: scale[h] = max(amax_h, 1e-12)/448,
+ * codes = e4m3(clamp(x / scale[h], +-448)).  Granularity is per head (not per row as in the
+ * reference helper); the arithmetic is the reference's. */
+void hstu_oracle_quant_e4m3_per_head(const float* x, uint8_t* codes, float* scale, int64_t T,
+                                     int64_t H, int64_t D) {
+  for (int64_t h = 0; h < H; ++h) {
+    float amax = 0.f;
+    for (int64_t r = 0; r < T; ++r)
+      for (int64_t d = 0; d < D; ++d) {
+        const float a = fabsf(x[(r * H + h) * D + d]);
+        if (a > amax) amax = a;
+      }
+    if (amax < 1e-12f) amax = 1e-12f;
+    scale[h] = amax / 448.0f;
+  }
+  for (int64_t r = 0; r < T; ++r)
+    for (int64_t h = 0; h < H; ++h)
+      for (int64_t d = 0; d < D; ++d) {
+        float y = x[(r * H + h) * D + d] / scale[h];
+        if (y > 448.f) y = 448.f;
+        if (y < -448.f) y = -448.f;
+        codes[(r * H + h) * D + d] = hstu_oracle_e4m3_encode(y);
+      }
+}

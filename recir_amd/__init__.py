@@ -1,0 +1,25 @@
+"""MI355X-native HSTU jagged attention forward behind RecIR's operator surface.
+
+The compute lives in ``librecir_hstu.so`` (hand-written HIP for gfx950, C ABI in
+``include/recir_hstu.h``); this package is the thin host side: a ctypes binding, the
+``torch.library`` operator with the argument list of ``hammer::triton_ragged_attention_fwd``,
+and a keyword front end with the defaults of the packed accelerator kernel it replaces.
+"""
+from .ops import (  # noqa: F401
+    hstu_jagged_attention_fwd,
+    jagged_hstu_attention,
+    jagged_hstu_attention_fp8,
+    quantize_e4m3_per_head,
+    register_swaps,
+    KERNEL_AUTO,
+    KERNEL_GENERIC,
+    KERNEL_TILED,
+)
+
+__all__ = [
+    "hstu_jagged_attention_fwd",
+    "jagged_hstu_attention",
+    "jagged_hstu_attention_fp8",
+    "quantize_e4m3_per_head",
+    "register_swaps",
+]

@@ -1,0 +1,43 @@
+"""Build step: compiles the HIP sources into ``recir_amd/librecir_hstu.so`` for gfx950."""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+_ROOT = os.path.dirname(_PKG)
+LIB_PATH = os.path.join(_PKG, "librecir_hstu.so")
+SOURCES = [os.path.join(_PKG, "csrc", "hstu_attn_fwd.hip")]
+
+
+def hipcc_path() -> str:
+    return shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+
+
+def compile_command(out: str = LIB_PATH) -> list:
+    return [
+        hipcc_path(), "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+        # no compiler-generated packed fp32 arithmetic
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wno-unused-command-line-argument",
+        "-I", os.path.join(_ROOT, "include"),
+        *SOURCES, "-o", out,
+    ]
+
+
+def build_library(verbose: bool = False) -> str:
+    """Always recompiles (seconds); returns the path of the shared library."""
+    cmd = compile_command()
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    noise = "is not a recognized feature for this target"
+    log = "\n".join(l for l in res.stdout.splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + log)
+    if verbose and log.strip():
+        print(log)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))

@@ -1,0 +1,335 @@
+"""Host side of the HSTU jagged attention forward: operator registration and front ends.
+
+``recir::hstu_jagged_attention_fwd`` keeps the positional argument list of
+``hammer::triton_ragged_attention_fwd`` (recir/ops/kjt_split_per_feature.cpp:780-783) so that
+RecIR's ``swap_ops`` (recir/lowering/op_swap.py:78-97), which rewrites only ``node.target``, can
+retarget a traced node without touching its arguments.  One trailing optional ``rab`` is added.
+The registration follows the pattern of recir/ops/seq_embedding_op.py:83-95, :238-299: a
+``torch.library`` FRAGMENT in namespace ``recir``, an opaque device implementation and a fake
+(Meta) kernel, which is what recir/lowering/partial_lower.py:414-427 requires to keep the node
+inside a lowered region.
+
+There is deliberately no CPU or eager implementation: a CPU tensor, or a missing
+``librecir_hstu.so``, raises.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+KERNEL_AUTO = 0
+KERNEL_GENERIC = 1
+KERNEL_TILED = 2
+
+_forced_kernel = KERNEL_AUTO
+_ctx_reference_rule = False
+
+
+class force_kernel:
+    """Context manager for tests and tuning: pin the kernel variant the C ABI selects."""
+
+    def __init__(self, variant: int):
+        self.variant = int(variant)
+
+    def __enter__(self):
+        global _forced_kernel
+        self._prev = _forced_kernel
+        _forced_kernel = self.variant
+        return self
+
+    def __exit__(self, *exc):
+        global _forced_kernel
+        _forced_kernel = self._prev
+        return False
+
+
+class reference_contextual_rule:
+    """Context manager: use the contextual-prefix rule of the reference C++ fallback
+    (kjt_split_per_feature.cpp:672-674: keys whose target-clamped id is 0 are visible to all)
+    instead of "keys j < contextual_seq_len are visible to all"."""
+
+    def __enter__(self):
+        global _ctx_reference_rule
+        self._prev = _ctx_reference_rule
+        _ctx_reference_rule = True
+        return self
+
+    def __exit__(self, *exc):
+        global _ctx_reference_rule
+        _ctx_reference_rule = self._prev
+        return False
+
+
+_SCHEMA = (
+    "hstu_jagged_attention_fwd(int N, float alpha, Tensor q, Tensor k, Tensor v, "
+    "Tensor seq_offsets, str invalid_attn_mask_type, Tensor? num_targets, Tensor? attn_scale, "
+    "int max_attn_len, int contextual_seq_len, int full_attn_size, int num_softmax_heads=0, "
+    "Tensor? rab=None) -> (Tensor, Tensor)"
+)
+_FP8_SCHEMA = (
+    "hstu_jagged_attention_fp8_fwd(int N, float alpha, Tensor q_fp8, Tensor k_fp8, Tensor v, "
+    "Tensor q_scale, Tensor k_scale, Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, "
+    "int contextual_seq_len, Tensor? rab=None) -> (Tensor, Tensor)"
+)
+_QUANT_SCHEMA = "hstu_quantize_e4m3_per_head(Tensor x) -> (Tensor, Tensor)"
+
+_LIBRARY = torch.library.Library("recir", "FRAGMENT")
+_LIBRARY.define(_SCHEMA)
+_LIBRARY.define(_FP8_SCHEMA)
+_LIBRARY.define(_QUANT_SCHEMA)
+
+
+def _check_common(q, k, v, seq_offsets, num_targets, max_seq_len) -> int:
+    """Shape rules of recir/ops/pallas/jagged_hstu_attention.py:1486-1515 (same messages)."""
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("q, k, and v must have shape [T, H, D]")
+    if q.shape[:2] != k.shape[:2] or q.shape[:2] != v.shape[:2]:
+        raise ValueError("q, k, and v must share packed-token and head dimensions")
+    if q.shape[2] != k.shape[2]:
+        raise ValueError("q and k must share their feature dimension")
+    if seq_offsets.dim() != 1 or seq_offsets.shape[0] < 2:
+        raise ValueError("seq_offsets must have shape [B + 1]")
+    num_sequences = seq_offsets.shape[0] - 1
+    if num_targets is not None and tuple(num_targets.shape) != (num_sequences,):
+        raise ValueError("num_targets must have shape [B]")
+    if max_seq_len <= 0:
+        raise ValueError("max_seq_len must be positive")
+    return num_sequences
+
+
+def _index_tensors(seq_offsets, num_targets):
+    """Offsets and targets as one integer width the kernels read (int64 or int32)."""
+    if seq_offsets.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"seq_offsets must be int32 or int64, got {seq_offsets.dtype}")
+    off = seq_offsets.contiguous()
+    nt = None
+    if num_targets is not None:
+        if num_targets.dtype not in (torch.int32, torch.int64):
+            raise ValueError(f"num_targets must be int32 or int64, got {num_targets.dtype}")
+        nt = num_targets.to(off.dtype).contiguous()
+    return off, nt, (_lib.FLAG_OFFSETS_I32 if off.dtype == torch.int32 else 0)
+
+
+def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale, N, alpha,
+            contextual_seq_len, dtype_code) -> torch.Tensor:
+    L = _lib.load()
+    dev = q.device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            "recir::hstu_jagged_attention_fwd runs on the GPU only (got a tensor on "
+            f"'{dev}'); this package has no CPU path")
+    for name, t in (("k", k), ("v", v), ("seq_offsets", seq_offsets)):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, q on {dev}")
+    B = _check_common(q, k, v, seq_offsets, num_targets, N)
+    T, H, Dqk = q.shape
+    Dv = v.shape[2]
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    off, nt, flags = _index_tensors(seq_offsets, num_targets)
+    if _ctx_reference_rule:
+        flags |= _lib.FLAG_CTX_REFERENCE
+    flags |= (_forced_kernel & 0xFF) << _lib.FLAG_KERNEL_SHIFT
+
+    sc = None
+    if attn_scale is not None:
+        sc = attn_scale.to(device=dev, dtype=torch.float32).contiguous()
+        if sc.dim() == 0:
+            sc = sc.reshape(1)
+        elif sc.dim() == 1 and sc.shape[0] == T:
+            flags |= _lib.FLAG_SCALE_PER_TOKEN
+        else:
+            raise ValueError("attn_scale must be a 0-d tensor or have shape [T]")
+    rb = None
+    if rab is not None:
+        if tuple(rab.shape) != (H, 2 * N - 1):
+            raise ValueError(f"rab must have shape [H, 2*max_seq_len-1] = [{H}, {2 * N - 1}]")
+        rb = rab.to(device=dev, dtype=torch.float32).contiguous()
+
+    out = torch.empty((T, H, Dv), dtype=v.dtype, device=dev)
+    if T == 0:
+        return out
+    ws_bytes = L.recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype_code)
+    ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def ptr(t):
+        return None if t is None else t.data_ptr()
+
+    with torch.cuda.device(dev):
+        rc = L.recir_hstu_attn_fwd(ptr(q), ptr(k), ptr(v), ptr(out), ptr(off), ptr(nt), ptr(rb),
+                                   ptr(sc), ptr(q_scale), ptr(k_scale), T, B, H, Dqk, Dv, int(N),
+                                   int(contextual_seq_len), float(alpha), dtype_code, flags,
+                                   ptr(ws), ws.numel(), stream)
+    if rc != 0:
+        msg = _lib.last_error()
+        if rc < 0:
+            raise ValueError(f"recir_hstu_attn_fwd rejected the call ({rc}): {msg}")
+        raise RuntimeError(f"recir_hstu_attn_fwd launch failed (hipError {rc}): {msg}")
+    return out
+
+
+def _fwd_device(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
+                max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads=0, rab=None):
+    # same rejections as the reference fallback (kjt_split_per_feature.cpp:616-622) plus the
+    # features outside the causal + target mask
+    if num_softmax_heads != 0:
+        raise ValueError("softmax attention heads are unsupported")
+    if invalid_attn_mask_type != "lower_triangular":
+        raise ValueError("only the causal mask ('lower_triangular') is supported")
+    if max_attn_len != 0 or full_attn_size != 0:
+        raise ValueError("max_attn_len and full_attn_size (semi-local attention) are unsupported")
+    if q.dtype == torch.bfloat16:
+        code = _lib.DTYPE_BF16
+    elif q.dtype == torch.float32:
+        code = _lib.DTYPE_FP32
+    else:
+        raise ValueError(f"q must be bfloat16 or float32, got {q.dtype}")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k and v must share one dtype")
+    out = _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, None, None, N, alpha,
+                  contextual_seq_len, code)
+    return out, torch.zeros((1,), dtype=torch.float32, device=q.device)
+
+
+def _fp8_fwd_device(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, num_targets,
+                    attn_scale, contextual_seq_len, rab=None):
+    ok = (torch.float8_e4m3fn, torch.uint8)
+    if q_fp8.dtype not in ok or k_fp8.dtype not in ok:
+        raise ValueError("q_fp8 and k_fp8 must be float8_e4m3fn (or its uint8 bytes)")
+    if v.dtype != torch.bfloat16:
+        raise ValueError("v must be bfloat16")
+    H = q_fp8.shape[1] if q_fp8.dim() == 3 else -1
+    for name, s in (("q_scale", q_scale), ("k_scale", k_scale)):
+        if tuple(s.shape) != (H,):
+            raise ValueError(f"{name} must have shape [H]")
+    qs = q_scale.to(device=v.device, dtype=torch.float32).contiguous()
+    ks = k_scale.to(device=v.device, dtype=torch.float32).contiguous()
+    out = _launch(q_fp8.view(torch.uint8), k_fp8.view(torch.uint8), v, seq_offsets, num_targets,
+                  attn_scale, rab, qs, ks, N, alpha, contextual_seq_len, _lib.DTYPE_FP8_E4M3)
+    return out, torch.zeros((1,), dtype=torch.float32, device=v.device)
+
+
+def _quant_device(x):
+    L = _lib.load()
+    if x.device.type != "cuda":
+        raise RuntimeError("recir::hstu_quantize_e4m3_per_head runs on the GPU only")
+    if x.dim() != 3 or x.dtype != torch.bfloat16:
+        raise ValueError("x must be a bfloat16 tensor of shape [T, H, D]")
+    x = x.contiguous()
+    T, H, D = x.shape
+    codes = torch.empty((T, H, D), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((H,), dtype=torch.float32, device=x.device)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    with torch.cuda.device(x.device):
+        rc = L.recir_hstu_quantize_e4m3_per_head(x.data_ptr(), codes.data_ptr(), scale.data_ptr(),
+                                                 T, H, D, stream)
+    if rc != 0:
+        raise (ValueError if rc < 0 else RuntimeError)(
+            f"recir_hstu_quantize_e4m3_per_head failed ({rc}): {_lib.last_error()}")
+    return codes.view(torch.float8_e4m3fn), scale
+
+
+def _no_cpu(*args, **kwargs):
+    raise RuntimeError(
+        "recir HSTU attention has no CPU implementation: the operator is backed only by the "
+        "gfx950 HIP library (librecir_hstu.so); move the tensors to the GPU")
+
+
+_LIBRARY.impl("hstu_jagged_attention_fwd", _fwd_device, "CUDA")
+_LIBRARY.impl("hstu_jagged_attention_fp8_fwd", _fp8_fwd_device, "CUDA")
+_LIBRARY.impl("hstu_quantize_e4m3_per_head", _quant_device, "CUDA")
+_LIBRARY.impl("hstu_jagged_attention_fwd", _no_cpu, "CPU")
+_LIBRARY.impl("hstu_jagged_attention_fp8_fwd", _no_cpu, "CPU")
+_LIBRARY.impl("hstu_quantize_e4m3_per_head", _no_cpu, "CPU")
+
+
+@torch.library.register_fake("recir::hstu_jagged_attention_fwd")
+def _fwd_fake(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
+              max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads=0, rab=None):
+    _check_common(q, k, v, seq_offsets, num_targets, N)
+    # packed layout is kept: dim 0 of the output is dim 0 of q (recir/compiler/batch_dim.py:309-318)
+    return v.new_empty((q.shape[0], q.shape[1], v.shape[2])), q.new_empty((1,), dtype=torch.float32)
+
+
+@torch.library.register_fake("recir::hstu_jagged_attention_fp8_fwd")
+def _fp8_fwd_fake(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, num_targets, attn_scale,
+                  contextual_seq_len, rab=None):
+    _check_common(q_fp8, k_fp8, v, seq_offsets, num_targets, N)
+    return v.new_empty((q_fp8.shape[0], q_fp8.shape[1], v.shape[2])), v.new_empty((1,), dtype=torch.float32)
+
+
+@torch.library.register_fake("recir::hstu_quantize_e4m3_per_head")
+def _quant_fake(x):
+    return x.new_empty(x.shape, dtype=torch.float8_e4m3fn), x.new_empty((x.shape[1],), dtype=torch.float32)
+
+
+hstu_jagged_attention_fwd = torch.ops.recir.hstu_jagged_attention_fwd
+
+
+def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len: int,
+                          alpha: Optional[float] = None, attn_scale=None,
+                          contextual_seq_len: int = 0, rab=None) -> torch.Tensor:
+    """Packed HSTU attention with the defaults of the accelerator entry point it replaces
+    (recir/ops/pallas/jagged_hstu_attention.py:1550-1555, recir/ops/helion/jagged_hstu_attention.py:
+    798-804): ``num_targets=None`` means no targets, ``alpha=None`` means ``1/sqrt(Dqk)``,
+    ``attn_scale=None`` means ``1/max_seq_len``.  Returns ``out [T, H, Dv]`` with rows at and
+    after ``seq_offsets[-1]`` zero.  ``attn_scale`` may be a float, a 0-d tensor or a ``[T]`` tensor.
+    """
+    _check_common(q, k, v, seq_offsets, num_targets, max_seq_len)
+    if alpha is None:
+        alpha = 1.0 / math.sqrt(q.shape[2])
+    if attn_scale is not None and not isinstance(attn_scale, torch.Tensor):
+        attn_scale = torch.tensor(float(attn_scale), dtype=torch.float32, device=q.device)
+    out, _ = hstu_jagged_attention_fwd(int(max_seq_len), float(alpha), q, k, v, seq_offsets,
+                                       "lower_triangular", num_targets, attn_scale, 0,
+                                       int(contextual_seq_len), 0, 0, rab)
+    return out
+
+
+def quantize_e4m3_per_head(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """bf16 ``[T,H,D]`` -> (float8_e4m3fn codes, float32 scale ``[H]``), scale = amax_h / 448.
+
+    The arithmetic is the reference's row-wise recipe (recir/ops/kjt_split_per_feature.cpp:493-502)
+    at per-head granularity."""
+    return torch.ops.recir.hstu_quantize_e4m3_per_head(x)
+
+
+def jagged_hstu_attention_fp8(q, k, v, seq_offsets, num_targets=None, *, max_seq_len: int,
+                              alpha: Optional[float] = None, attn_scale=None,
+                              contextual_seq_len: int = 0, rab=None) -> torch.Tensor:
+    """Inference variant: bf16 q and k are quantised per head to e4m3 on the device, the scores are
+    contracted in fp8 and dequantised with ``q_scale[h] * k_scale[h]``; v, P.V and out stay bf16."""
+    _check_common(q, k, v, seq_offsets, num_targets, max_seq_len)
+    if alpha is None:
+        alpha = 1.0 / math.sqrt(q.shape[2])
+    if attn_scale is not None and not isinstance(attn_scale, torch.Tensor):
+        attn_scale = torch.tensor(float(attn_scale), dtype=torch.float32, device=q.device)
+    q8, qs = quantize_e4m3_per_head(q)
+    k8, ks = quantize_e4m3_per_head(k)
+    out, _ = torch.ops.recir.hstu_jagged_attention_fp8_fwd(
+        int(max_seq_len), float(alpha), q8, k8, v, qs, ks, seq_offsets, num_targets, attn_scale,
+        int(contextual_seq_len), rab)
+    return out
+
+
+def register_swaps(registry) -> int:
+    """Fill a RecIR ``OpSwapRegistry`` (recir/lowering/op_swap.py:16-75) with every source operator
+    present in this process that the HIP operator can replace argument-for-argument.  Returns the
+    number of mappings added."""
+    added = 0
+    candidates = (("hammer", "triton_ragged_attention_fwd"),)
+    for ns, name in candidates:
+        try:
+            packet = getattr(getattr(torch.ops, ns), name)
+        except (AttributeError, RuntimeError):
+            continue
+        for target in (packet, getattr(packet, "default", None)):
+            if target is not None:
+                replacement = hstu_jagged_attention_fwd if target is packet else hstu_jagged_attention_fwd.default
+                registry.register(target, replacement)
+                added += 1
+    return added

@@ -1,0 +1,71 @@
+"""Writes the golden fixtures from the reference's own compiled C++ operator.
+
+Run in the development container only (needs oracle/_ref/libkjt_ref.so, built from the upstream
+checkout by `make -C oracle ref`):
+
+    python tests/golden/make_golden.py
+
+Outputs (data only):
+  tests/golden/small_cases.npz   expected out[seq_offsets[B], H, Dv] per small case
+  tests/golden/config2.npz       config 2 (bf16-rounded inputs, fp32 arithmetic): per-sequence sums,
+                                 abs-sums and 64 sampled rows
+  tests/golden/config4.npz       same for the long skewed config 4
+
+The reference operator takes contextual_seq_len as a boolean "key 0 is visible" switch
+(kjt_split_per_feature.cpp:672-674); cases with ctx > 0 therefore pin the reference rule.
+"""
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from oracle import hstu_oracle  # noqa: E402
+from recir_amd.workloads import make_config  # noqa: E402
+from tests.golden.cases import SMALL_CASES, build_inputs  # noqa: E402
+
+SAMPLED_ROWS = 64
+
+
+def run_ref(wl, scale, nt):
+    return hstu_oracle.ref_attn_fwd(wl.q, wl.k, wl.v, wl.seq_offsets, nt, max_seq_len=wl.max_seq_len,
+                                    alpha=wl.alpha, attn_scale=scale,
+                                    contextual_seq_len=wl.contextual_seq_len)
+
+
+def sampled_rows(total_rows, seed=1234):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return np.sort(rng.choice(total_rows, size=min(SAMPLED_ROWS, total_rows), replace=False))
+
+
+def checksum_fixture(config):
+    wl = make_config(config)
+    out = run_ref(wl, None, wl.num_targets).double()
+    off = wl.seq_offsets.numpy()
+    sums = np.array([out[off[b]:off[b + 1]].sum().item() for b in range(wl.B)])
+    abss = np.array([out[off[b]:off[b + 1]].abs().sum().item() for b in range(wl.B)])
+    rows = sampled_rows(int(off[-1]))
+    return dict(seq_sum=sums, seq_abs_sum=abss, rows=rows, row_values=out[rows].float().numpy(),
+                lengths=wl.lengths, T=np.int64(wl.T))
+
+
+def main():
+    torch.set_num_threads(os.cpu_count())
+    small = {}
+    for name, case in SMALL_CASES.items():
+        wl, scale, nt = build_inputs(case)
+        small[name] = run_ref(wl, scale, nt).numpy()
+        print(name, small[name].shape)
+    np.savez_compressed(os.path.join(HERE, "small_cases.npz"), **small)
+    for cfg in (2, 4):
+        fx = checksum_fixture(cfg)
+        np.savez_compressed(os.path.join(HERE, f"config{cfg}.npz"), **fx)
+        print("config", cfg, fx["row_values"].shape)
+
+
+if __name__ == "__main__":
+    main()

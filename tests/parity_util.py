@@ -1,0 +1,86 @@
+"""Shared helpers of the GPU parity tests: run the HIP operator on a workload, run the oracle on the
+same values, compare with the stated tolerances."""
+import numpy as np
+import torch
+
+# Stated tolerances (output vs the fp32 oracle on identical inputs)
+BF16_MAX_ABS = 1e-2   # absolute
+BF16_REL = 2e-2       # relative to the largest reference magnitude, and of the Frobenius norm
+FP8_MAX_ABS = 5e-2
+FP32_RTOL, FP32_ATOL = 2e-4, 2e-6
+
+
+def to_device(wl, dtype=None):
+    dt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp8": torch.bfloat16}[dtype or wl.dtype]
+    dev = torch.device("cuda:0")
+    return (wl.q.to(dev, dt), wl.k.to(dev, dt), wl.v.to(dev, dt), wl.seq_offsets.to(dev),
+            wl.num_targets.to(dev))
+
+
+def run_hip(wl, *, attn_scale=None, num_targets="default", rab="default", ctx="default", dtype=None,
+            offsets_dtype=None, fp8=False):
+    import recir_amd
+
+    q, k, v, off, nt = to_device(wl, dtype)
+    if num_targets != "default":
+        nt = num_targets
+    if offsets_dtype is not None:
+        off = off.to(offsets_dtype)
+        nt = None if nt is None else nt.to(offsets_dtype)
+    rb = wl.rab if rab == "default" else rab
+    if rb is not None:
+        rb = rb.to(q.device)
+    sc = attn_scale
+    if isinstance(sc, torch.Tensor):
+        sc = sc.to(q.device)
+    fn = recir_amd.jagged_hstu_attention_fp8 if fp8 else recir_amd.jagged_hstu_attention
+    out = fn(q, k, v, off, nt, max_seq_len=wl.max_seq_len, alpha=wl.alpha, attn_scale=sc,
+             contextual_seq_len=wl.contextual_seq_len if ctx == "default" else ctx, rab=rb)
+    torch.cuda.synchronize()
+    return out
+
+
+def run_oracle(oracle, wl, *, attn_scale=None, num_targets="default", rab="default", ctx="default",
+               ctx_mode=0, q=None, k=None, **kw):
+    nt = wl.num_targets.numpy() if num_targets == "default" else num_targets
+    rb = wl.rab if rab == "default" else rab
+    sc = attn_scale
+    if isinstance(sc, torch.Tensor):
+        sc = sc.numpy() if sc.dim() else np.float32(sc.item())
+    elif sc is not None:
+        sc = np.float32(sc)
+    return oracle.attn_fwd((wl.q if q is None else q).numpy(), (wl.k if k is None else k).numpy(),
+                           wl.v.numpy(), wl.seq_offsets.numpy(), nt, max_seq_len=wl.max_seq_len,
+                           alpha=wl.alpha, attn_scale=sc, rab=None if rb is None else rb.numpy(),
+                           contextual_seq_len=wl.contextual_seq_len if ctx == "default" else ctx,
+                           ctx_mode=ctx_mode, **kw)
+
+
+def error_stats(out, ref):
+    out = out.detach().float().cpu().numpy().astype(np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    err = np.abs(out - ref)
+    ref_max = max(np.abs(ref).max(), 1e-30) if ref.size else 1.0
+    fro = np.sqrt((err ** 2).sum() / max((ref ** 2).sum(), 1e-30)) if ref.size else 0.0
+    return dict(max_abs=float(err.max()) if err.size else 0.0,
+                rel_to_max=float(err.max() / ref_max) if err.size else 0.0, rel_fro=float(fro),
+                ref_max=float(ref_max))
+
+
+def assert_bf16_close(out, ref, what=""):
+    st = error_stats(out, ref)
+    assert st["max_abs"] <= BF16_MAX_ABS, (what, st)
+    assert st["rel_to_max"] <= BF16_REL, (what, st)
+    assert st["rel_fro"] <= BF16_REL, (what, st)
+    return st
+
+
+def assert_same_zero_structure(out, ref, end_row):
+    """Rows after the last sequence are exactly zero, and rows inside sequences are not spuriously
+    zeroed (a valid row always keeps its diagonal key)."""
+    o = out.detach().float().cpu().numpy()
+    assert not o[end_row:].any(), "tail rows must be exactly zero"
+    ref = np.asarray(ref)
+    ref_zero_rows = ~ref.reshape(ref.shape[0], -1).any(axis=1)
+    out_zero_rows = ~o.reshape(o.shape[0], -1).any(axis=1)
+    np.testing.assert_array_equal(out_zero_rows[end_row:], ref_zero_rows[end_row:])

@@ -1,0 +1,181 @@
+"""The C-ABI library: it loads without a GPU, exports every symbol the header declares, rejects bad
+arguments before any launch, and the host-side operator surface validates like the reference's."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from recir_amd import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        from recir_amd.build import build_library
+
+        build_library()
+    return _lib.load()
+
+
+def _declared_symbols():
+    text = open(os.path.join(ROOT, "include", "recir_hstu.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(recir_hstu_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_are_exported(lib):
+    from recir_amd import _lib
+
+    declared = _declared_symbols()
+    assert declared == sorted(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    assert lib.recir_hstu_abi_version() == 1
+
+
+def test_workspace_size_is_host_arithmetic(lib):
+    # one (sequence, query tile) slot per 128 packed rows plus one per sequence, 8 bytes each
+    assert lib.recir_hstu_attn_fwd_workspace_bytes(39382, 32, 4, 128, 128, 0) == 16 + 8 * (308 + 32)
+    assert lib.recir_hstu_attn_fwd_workspace_bytes(0, 0, 1, 8, 8, 1) == 16
+    assert lib.recir_hstu_attn_fwd_workspace_bytes(-1, 0, 1, 8, 8, 1) == 0
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(T=-1), "negative size"),
+    (dict(H=0), "must be positive"),
+    (dict(Dv=0), "must be positive"),
+    (dict(N=0), "max_seq_len"),
+    (dict(ctx=-2), "contextual_seq_len"),
+    (dict(dtype=9), "unknown dtype"),
+    (dict(q=None), "non-null"),
+    (dict(off=None), "seq_offsets"),
+    (dict(dtype=2), "q_scale"),
+])
+def test_invalid_arguments_are_rejected_before_launch(lib, kw, needle):
+    a = dict(q=8, k=8, v=8, out=8, off=8, T=4, B=1, H=1, Dqk=8, Dv=8, N=4, ctx=0, dtype=1)
+    a.update(kw)
+    rc = lib.recir_hstu_attn_fwd(a["q"], a["k"], a["v"], a["out"], a["off"], None, None, None, None, None,
+                                 a["T"], a["B"], a["H"], a["Dqk"], a["Dv"], a["N"], a["ctx"], 1.0,
+                                 a["dtype"], 0, None, 0, None)
+    assert rc < 0
+    assert needle in lib.recir_hstu_last_error().decode()
+
+
+def test_empty_input_is_ok_without_launch(lib):
+    rc = lib.recir_hstu_attn_fwd(None, None, None, None, None, None, None, None, None, None,
+                                 0, 0, 2, 8, 8, 4, 0, 1.0, 1, 0, None, 0, None)
+    assert rc == 0
+
+
+def test_cpu_tensors_fail_loudly():
+    import recir_amd
+
+    q = torch.zeros(4, 1, 8)
+    off = torch.tensor([0, 4])
+    with pytest.raises(RuntimeError, match="no CPU implementation"):
+        recir_amd.jagged_hstu_attention(q, q, q, off, max_seq_len=4)
+
+
+def test_shape_errors_match_reference_messages():
+    # recir/ops/pallas/tests/test_jagged_hstu_attention.py:679-690 ("shape [B]") and the validator
+    # at recir/ops/pallas/jagged_hstu_attention.py:1498-1515
+    import recir_amd
+
+    q = torch.zeros(5, 2, 8)
+    v = torch.zeros(5, 2, 6)
+    off = torch.tensor([0, 3, 5])
+    with pytest.raises(ValueError, match=r"shape \[B\]"):
+        recir_amd.jagged_hstu_attention(q, q, v, off, torch.zeros(3, dtype=torch.int64), max_seq_len=4)
+    with pytest.raises(ValueError, match=r"shape \[T, H, D\]"):
+        recir_amd.jagged_hstu_attention(q[0], q, v, off, max_seq_len=4)
+    with pytest.raises(ValueError, match="share packed-token and head"):
+        recir_amd.jagged_hstu_attention(q, q, v[:4], off, max_seq_len=4)
+    with pytest.raises(ValueError, match="feature dimension"):
+        recir_amd.jagged_hstu_attention(q, q[:, :, :4], v, off, max_seq_len=4)
+    with pytest.raises(ValueError, match=r"shape \[B \+ 1\]"):
+        recir_amd.jagged_hstu_attention(q, q, v, off[:1], max_seq_len=4)
+    with pytest.raises(ValueError, match="max_seq_len must be positive"):
+        recir_amd.jagged_hstu_attention(q, q, v, off, max_seq_len=0)
+
+
+def test_fake_kernel_and_schema():
+    """The operator traces with fake tensors (the requirement of recir/lowering/partial_lower.py:
+    414-427) and keeps the argument list of hammer::triton_ragged_attention_fwd
+    (recir/ops/kjt_split_per_feature.cpp:780-783) plus a trailing optional rab."""
+    import recir_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    schema = str(torch.ops.recir.hstu_jagged_attention_fwd.default._schema)
+    want = ("int N, float alpha, Tensor q, Tensor k, Tensor v, Tensor seq_offsets, "
+            "str invalid_attn_mask_type, Tensor? num_targets, Tensor? attn_scale, int max_attn_len, "
+            "int contextual_seq_len, int full_attn_size, int num_softmax_heads=0")
+    assert want in schema and schema.endswith("Tensor? rab=None) -> (Tensor, Tensor)")
+    with FakeTensorMode():
+        q = torch.empty(10, 2, 8, dtype=torch.bfloat16)
+        v = torch.empty(10, 2, 6, dtype=torch.bfloat16)
+        off = torch.empty(3, dtype=torch.int64)
+        out, aux = torch.ops.recir.hstu_jagged_attention_fwd(8, 0.5, q, q, v, off, "lower_triangular",
+                                                            None, None, 0, 0, 0)
+        assert out.shape == (10, 2, 6) and out.dtype == torch.bfloat16
+        assert aux.shape == (1,) and aux.dtype == torch.float32
+
+
+def test_swap_registry_retargets_a_traced_node():
+    """swap_ops rewrites node.target only (recir/lowering/op_swap.py:78-97): the replacement must
+    accept the source operator's positional arguments unchanged."""
+    import recir_amd
+
+    lib = torch.library.Library("hammer_test_src", "DEF")
+    lib.define("triton_ragged_attention_fwd(int N, float alpha, Tensor q, Tensor k, Tensor v, "
+               "Tensor seq_offsets, str invalid_attn_mask_type, Tensor? num_targets, Tensor? attn_scale, "
+               "int max_attn_len, int contextual_seq_len, int full_attn_size, int num_softmax_heads=0) "
+               "-> (Tensor, Tensor)")
+
+    @torch.library.register_fake("hammer_test_src::triton_ragged_attention_fwd")
+    def _fake(N, alpha, q, k, v, off, mt, nt, sc, a, b, c, d=0):
+        return v.new_empty(v.shape), v.new_empty((1,), dtype=torch.float32)
+
+    src = torch.ops.hammer_test_src.triton_ragged_attention_fwd.default
+
+    def f(q, k, v, off):
+        return src(8, 0.5, q, k, v, off, "lower_triangular", None, None, 0, 0, 0)[0]
+
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    q = torch.empty(10, 2, 8, dtype=torch.bfloat16)
+    gm = make_fx(f, tracing_mode="fake")(q, q, q, torch.empty(3, dtype=torch.int64))
+    swapped = 0
+    for node in gm.graph.nodes:  # what swap_ops does
+        if node.op == "call_function" and node.target is src:
+            node.target = recir_amd.hstu_jagged_attention_fwd.default
+            swapped += 1
+    gm.recompile()
+    assert swapped == 1
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        qq = torch.empty(10, 2, 8, dtype=torch.bfloat16)
+        out = gm(qq, qq, qq, torch.empty(3, dtype=torch.int64))
+    assert out.shape == (10, 2, 8)
+
+
+def test_register_swaps_fills_a_registry():
+    import recir_amd
+
+    class Registry:  # same surface as recir.lowering.op_swap.OpSwapRegistry.register
+        def __init__(self):
+            self.map = {}
+
+        def register(self, source_op, replace_op):
+            self.map[source_op] = replace_op
+
+    reg = Registry()
+    n = recir_amd.register_swaps(reg)
+    assert n == len(reg.map)  # 0 unless the reference's hammer op is loaded in this process

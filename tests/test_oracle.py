@@ -1,0 +1,217 @@
+"""The oracle pinned against the reference: its compiled operator's golden vectors, its own
+known-answer test, closed forms, and a second independent restatement.
+
+A dropped term, wrong sign, wrong index or transposed operand in oracle/hstu_oracle.c fails at least
+one of: the golden vectors (full values), the constant-score count test (mask and offsets), the
+single-token closed form (alpha, silu, scale), or the rab shift test (index convention).
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from tests.golden.cases import SMALL_CASES, build_inputs
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _run_case(oracle, case, ctx_mode=None, **kw):
+    wl, scale, nt = build_inputs(case)
+    sc = None
+    if scale is not None:
+        sc = scale.numpy() if scale.dim() else np.float32(scale.item())
+    mode = oracle.CTX_REFCPP if ctx_mode is None else ctx_mode
+    out = oracle.attn_fwd(wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                          None if nt is None else nt.numpy(), max_seq_len=wl.max_seq_len,
+                          alpha=wl.alpha, attn_scale=sc, contextual_seq_len=case["ctx"],
+                          ctx_mode=mode, **kw)
+    return wl, out
+
+
+@pytest.mark.parametrize("name", sorted(SMALL_CASES))
+def test_oracle_matches_reference_golden(oracle, name):
+    golden = np.load(os.path.join(GOLDEN, "small_cases.npz"))[name]
+    wl, out = _run_case(oracle, SMALL_CASES[name])
+    end = int(wl.seq_offsets[-1])
+    assert golden.shape == (end, wl.H, wl.v.shape[2])  # the C++ op returns seq_offsets[B] rows
+    np.testing.assert_allclose(out[:end], golden, rtol=2e-5, atol=2e-6)
+    assert not out[end:].any()  # packed form: rows after the last sequence are exactly zero
+
+
+@pytest.mark.parametrize("config", [2, 4])
+def test_oracle_matches_reference_checksums_at_full_size(oracle, config):
+    from recir_amd.workloads import make_config
+
+    fx = np.load(os.path.join(GOLDEN, f"config{config}.npz"))
+    wl = make_config(config)
+    assert wl.T == int(fx["T"]) and wl.lengths.tolist() == fx["lengths"].tolist()
+    out = oracle.attn_fwd(wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                          wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha)
+    np.testing.assert_allclose(out[fx["rows"]], fx["row_values"], rtol=1e-4, atol=1e-7)
+    off = wl.seq_offsets.numpy()
+    for b in range(wl.B):
+        seg = out[off[b]:off[b + 1]].astype(np.float64)
+        assert abs(seg.sum() - fx["seq_sum"][b]) <= 1e-5 * fx["seq_abs_sum"][b]
+        assert abs(np.abs(seg).sum() - fx["seq_abs_sum"][b]) <= 1e-5 * fx["seq_abs_sum"][b]
+
+
+def test_live_reference_operator_when_built(oracle):
+    """Compare against oracle/_ref directly on a fresh seed (skipped where _ref is not built)."""
+    if not oracle.ref_available():
+        pytest.skip("oracle/_ref not built")
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([11, 0, 4, 30], [3, 0, 4, 7], 3, 16, 10, max_seq_len=32, alpha=0.2, seed=77)
+    ref = oracle.ref_attn_fwd(wl.q, wl.k, wl.v, wl.seq_offsets, wl.num_targets, max_seq_len=32, alpha=0.2).numpy()
+    out = oracle.attn_fwd(wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                          wl.num_targets.numpy(), max_seq_len=32, alpha=0.2)
+    np.testing.assert_allclose(out, ref, rtol=2e-5, atol=2e-6)
+
+
+def test_reference_known_answer_zero_query(oracle):
+    # recir/ops/tests/KjtSplitPerFeatureTest.cpp RaggedAttentionTest: q = k = 0, v = [2, 3] -> zeros
+    q = np.zeros((2, 1, 1), np.float32)
+    v = np.array([2.0, 3.0], np.float32).reshape(2, 1, 1)
+    out = oracle.attn_fwd(q, q, v, [0, 2], None, max_seq_len=2, alpha=1.0)
+    assert out.shape == (2, 1, 1) and not out.any()
+
+
+def test_zero_keys_give_zero(oracle):
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((9, 2, 4)).astype(np.float32)
+    v = rng.standard_normal((9, 2, 3)).astype(np.float32)
+    out = oracle.attn_fwd(q, np.zeros_like(q), v, [0, 4, 9], [1, 2], max_seq_len=8, alpha=0.5)
+    assert not out.any()
+
+
+def test_single_token_closed_form(oracle):
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((3, 2, 5)).astype(np.float32)
+    k = rng.standard_normal((3, 2, 5)).astype(np.float32)
+    v = rng.standard_normal((3, 2, 4)).astype(np.float32)
+    alpha, N = 0.37, 7
+    out = oracle.attn_fwd(q, k, v, [0, 1, 2, 3], [0, 1, 0], max_seq_len=N, alpha=alpha)
+    x = alpha * (q.astype(np.float64) * k).sum(-1)
+    want = (x / (1 + np.exp(-x)) / N)[..., None] * v
+    np.testing.assert_allclose(out, want, rtol=1e-6, atol=1e-7)
+
+
+def test_all_target_sequence_is_per_token(oracle):
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal((6, 1, 5)).astype(np.float32)
+    k = rng.standard_normal((6, 1, 5)).astype(np.float32)
+    v = rng.standard_normal((6, 1, 4)).astype(np.float32)
+    out = oracle.attn_fwd(q, k, v, [0, 6], [6], max_seq_len=6, alpha=1.0, attn_scale=np.float32(0.5))
+    x = (q.astype(np.float64) * k).sum(-1)
+    want = (x / (1 + np.exp(-x)) * 0.5)[..., None] * v
+    np.testing.assert_allclose(out, want, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("ctx", [0, 3])
+def test_constant_score_counts_kept_keys(oracle, ctx):
+    """q rows equal, k rows equal, v = 1  =>  out[m] = scale * silu(c) * (#kept keys of row m)."""
+    lengths, targets = [9, 0, 5, 1], [3, 0, 5, 0]
+    T, D = sum(lengths), 4
+    q = np.full((T, 1, D), 0.5, np.float32)
+    k = np.full((T, 1, D), 0.25, np.float32)
+    v = np.ones((T, 1, 2), np.float32)
+    alpha, N = 2.0, 16
+    c = alpha * D * 0.5 * 0.25
+    unit = c / (1 + math.exp(-c)) / N
+    off = np.concatenate([[0], np.cumsum(lengths)])
+    out = oracle.attn_fwd(q, k, v, off, targets, max_seq_len=N, alpha=alpha, contextual_seq_len=ctx)
+    for b, (n, t) in enumerate(zip(lengths, targets)):
+        cap = n - t
+        for m in range(n):
+            cnt = (m + 1) if m < cap else (cap + 1)
+            if ctx:  # prefix keys j < ctx not already kept
+                cnt += sum(1 for j in range(min(ctx, n)) if not ((m == j) or (m >= j and j < cap)))
+            np.testing.assert_allclose(out[off[b] + m, 0], unit * cnt, rtol=1e-6)
+
+
+def test_loop_form_matches_padded_form(oracle):
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([13, 0, 7, 21, 1], [2, 0, 7, 5, 0], 3, 12, 9, max_seq_len=24, alpha=0.3, seed=5,
+                     with_rab=True, rab_std=0.5, tail_rows=2, contextual_seq_len=3)
+    args = (wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(), wl.num_targets.numpy())
+    for kw in (dict(), dict(rab=wl.rab.numpy()), dict(contextual_seq_len=3),
+               dict(attn_scale=np.float32(0.21)), dict(rab=wl.rab.numpy(), contextual_seq_len=3),
+               dict(attn_scale=np.linspace(0.1, 1.0, wl.T).astype(np.float32))):
+        a = oracle.attn_fwd(*args, max_seq_len=24, alpha=0.3, **kw)
+        b = oracle.attn_fwd_padded(*args, max_seq_len=24, alpha=0.3, **kw)
+        np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6)
+
+
+def test_rab_index_convention(oracle):
+    """rab[h, m - j + N - 1]: a bias that is a delta at distance d only changes pairs with m - j = d."""
+    n, N, D = 6, 8, 3
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((n, 1, D)).astype(np.float32)
+    k = rng.standard_normal((n, 1, D)).astype(np.float32)
+    v = np.eye(n, dtype=np.float32).reshape(n, 1, n)  # out[m, j] = P(m, j)
+    base = oracle.attn_fwd(q, k, v, [0, n], None, max_seq_len=N, alpha=1.0)
+    zero = oracle.attn_fwd(q, k, v, [0, n], None, max_seq_len=N, alpha=1.0, rab=np.zeros((1, 2 * N - 1)))
+    np.testing.assert_array_equal(base, zero)
+    for d in (0, 2, 5):
+        rab = np.zeros((1, 2 * N - 1), np.float32)
+        rab[0, d + N - 1] = 1.5
+        out = oracle.attn_fwd(q, k, v, [0, n], None, max_seq_len=N, alpha=1.0, rab=rab)
+        changed = np.argwhere(np.abs(out - base)[:, 0, :] > 1e-9)
+        x = (q[:, 0] @ k[:, 0].T).astype(np.float64)
+        for m in range(n):
+            for j in range(n):
+                if m - j == d and j <= m:
+                    xv = x[m, j] + 1.5
+                    np.testing.assert_allclose(out[m, 0, j], xv / (1 + math.exp(-xv)) / N, rtol=1e-5, atol=1e-7)
+        assert all(m - j == d for m, j in changed)
+
+
+def test_linearity_and_scale_folding(oracle):
+    """alpha may be folded into q and the scale into v (helion/jagged_hstu_attention.py:29-45)."""
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([10, 6], [3, 0], 2, 8, 5, max_seq_len=10, alpha=0.25, seed=9)
+    a = (wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(), wl.num_targets.numpy())
+    ref = oracle.attn_fwd(*a, max_seq_len=10, alpha=0.25, attn_scale=np.float32(0.1))
+    folded = oracle.attn_fwd(a[0] * 0.25, a[1], a[2] * 0.1, a[3], a[4], max_seq_len=10, alpha=1.0,
+                             attn_scale=np.float32(1.0))
+    np.testing.assert_allclose(ref, folded, rtol=1e-5, atol=1e-7)
+    two = oracle.attn_fwd(a[0], a[1], 2 * a[2], a[3], a[4], max_seq_len=10, alpha=0.25, attn_scale=np.float32(0.1))
+    np.testing.assert_allclose(two, 2 * ref, rtol=1e-6, atol=1e-7)
+
+
+def test_invalid_offsets_rejected(oracle):
+    q = np.zeros((4, 1, 2), np.float32)
+    for off in ([0, 5], [2, 1], [-1, 3]):
+        with pytest.raises(ValueError):
+            oracle.attn_fwd(q, q, q, off, None, max_seq_len=8, alpha=1.0)
+
+
+def test_e4m3_encoder_matches_torch_cast(oracle):
+    """The C encoder against torch's own float8_e4m3fn cast (what the reference quantiser calls,
+    kjt_split_per_feature.cpp:499-500) on a dense sweep including ties, subnormals and saturation."""
+    vals = np.concatenate([
+        np.linspace(-460, 460, 20001), np.linspace(-2, 2, 20001), np.linspace(-0.04, 0.04, 20001),
+        [0.0, -0.0, 448.0, -448.0, 2 ** -9, 2 ** -10, 1.5 * 2 ** -9, 2.5 * 2 ** -9, 0.3, 449.0],
+    ]).astype(np.float32)
+    mine = oracle.e4m3_encode(vals)
+    theirs = torch.from_numpy(vals).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(mine, theirs)
+    codes = np.arange(256, dtype=np.uint8)
+    dec = oracle.e4m3_decode(codes)
+    tdec = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(np.nan_to_num(dec, nan=-1.0), np.nan_to_num(tdec, nan=-1.0))
+
+
+def test_per_head_quantiser_follows_reference_recipe(oracle):
+    g = torch.Generator().manual_seed(4)
+    x = (torch.randn(37, 3, 16, generator=g) * torch.tensor([0.1, 1.0, 30.0]).view(1, 3, 1)).bfloat16().float()
+    codes, scale = oracle.quant_e4m3_per_head(x.numpy())
+    amax = x.abs().amax(dim=(0, 2)).clamp_min(1e-12)
+    tscale = amax / 448.0
+    np.testing.assert_array_equal(scale, tscale.numpy())
+    tcodes = (x / tscale.view(1, 3, 1)).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(codes, tcodes)
