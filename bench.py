@@ -1,0 +1,212 @@
+#!/usr/bin/env python3
+"""Benchmark of the HSTU jagged attention forward on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--no-cpu-baseline]
+
+A step is one call of the C-ABI entry point ``recir_hstu_attn_fwd`` (work-list kernel + attention
+kernel) on one batch of synthetic input that is already resident in HBM; output and workspace are
+allocated once, outside the timed region.  The default workload is configuration 2 of the baseline
+(B=32 jagged sequences, history U[256,1984] + 64 candidates, 4 heads, dim 128, bf16, alpha 1/128).
+
+Prints one JSON line.  ``value`` is achieved TFLOP/s on the unmasked FLOPs only
+(H * (2 Dqk + 2 Dv) * sum of kept (query, key) pairs) over the wall time of the K timed steps.
+``roofline`` prices the attention kernel alone against the dense bf16 MFMA peak, from HIP events on
+the launch stream around K launches of that kernel (work list reused).  ``cpu_baseline`` times the
+reference's own C++ operator (oracle/_ref, built from the upstream sources) -- or, if it is absent,
+the C oracle -- on the host cores, on rank 0.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0, "fp32": 157.3}  # MI355X dense MFMA peaks
+PEAK_HBM_GBS = 8000.0
+
+
+def describe(wl, cfg):
+    names = {
+        1: "config1: fp32 smoke, B=4, 16 history + 4 targets, H=2, D=32",
+        2: "config2: B=32 jagged, history U[256,1984] + 64 targets, max_seq_len 2048, H=4, Dqk=Dv=128, bf16, alpha=1/128, causal+target mask, no rab",
+        3: "config3: config2 + rab [4,4095] f32 + contextual_seq_len 8",
+        4: "config4: B=8, history Zipf(1.2) clipped [128,8064] + 128 targets, max_seq_len 8192, H=4, D=128, bf16",
+        5: "config5: config2 with q,k in fp8 e4m3 (per-head scale amax/448), v bf16",
+    }
+    return names[cfg]
+
+
+def cpu_baseline(wl, flops, budget_s=20.0):
+    """Reference operator (or the oracle port) on the host cores, bounded to about budget_s."""
+    import numpy as np
+    import torch
+
+    from oracle import hstu_oracle
+
+    cores = os.cpu_count() or 1
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except Exception:
+        pass
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env:
+        cores = min(cores, int(env))
+    torch.set_num_threads(cores)
+    if hstu_oracle.ref_available():
+        kind = "reference"
+
+        def run():
+            return hstu_oracle.ref_attn_fwd(wl.q, wl.k, wl.v, wl.seq_offsets, wl.num_targets,
+                                            max_seq_len=wl.max_seq_len, alpha=wl.alpha)
+    else:
+        kind = "port"
+        qn, kn, vn = wl.q.numpy(), wl.k.numpy(), wl.v.numpy()
+        on, tn = wl.seq_offsets.numpy(), wl.num_targets.numpy()
+
+        def run():
+            return hstu_oracle.attn_fwd(qn, kn, vn, on, tn, max_seq_len=wl.max_seq_len, alpha=wl.alpha)
+
+    t0 = time.perf_counter()
+    run()  # warm-up, also sizes the sample
+    first = time.perf_counter() - t0
+    reps = int(max(1, min(10, budget_s / max(first, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {
+        "value": flops / med / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": kind,
+        "ms_per_call": med * 1e3,
+        "sample": f"the full batch ({wl.B} sequences, {wl.T} tokens) as fp32 tensors, 1 warm-up + {reps} timed calls, median; "
+                  "unmasked FLOPs counted (the operator itself computes the dense n x n product per sequence)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel", type=int, default=0, help="kernel selector (0 auto)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the operator exchanges nothing between devices "
+              "(sequences shard whole); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from recir_amd import _lib
+    from recir_amd.workloads import make_config
+
+    L = _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = make_config(args.config)
+    fp8 = wl.dtype == "fp8"
+    dt = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
+    q, k, v = wl.q.to(dev, dt), wl.k.to(dev, dt), wl.v.to(dev, dt)
+    off, nt = wl.seq_offsets.to(dev), wl.num_targets.to(dev)
+    rab = None if wl.rab is None else wl.rab.to(dev)
+    q_scale = k_scale = None
+    dtype_code = {"fp32": _lib.DTYPE_FP32, "bf16": _lib.DTYPE_BF16, "fp8": _lib.DTYPE_FP8_E4M3}[wl.dtype]
+    if fp8:
+        import recir_amd
+
+        q, q_scale = recir_amd.quantize_e4m3_per_head(q)
+        k, k_scale = recir_amd.quantize_e4m3_per_head(k)
+    T, H, Dqk = q.shape
+    Dv = v.shape[2]
+    out = torch.empty((T, H, Dv), dtype=v.dtype, device=dev)
+    ws_bytes = L.recir_hstu_attn_fwd_workspace_bytes(T, wl.B, H, Dqk, Dv, dtype_code)
+    ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def ptr(t):
+        return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+    base_flags = (args.kernel & 0xFF) << _lib.FLAG_KERNEL_SHIFT
+
+    def call(flags=0):
+        rc = L.recir_hstu_attn_fwd(ptr(q), ptr(k), ptr(v), ptr(out), ptr(off), ptr(nt), ptr(rab), None,
+                                   ptr(q_scale), ptr(k_scale), T, wl.B, H, Dqk, Dv, wl.max_seq_len,
+                                   wl.contextual_seq_len, wl.alpha, dtype_code, base_flags | flags,
+                                   ptr(ws), ws.numel(), ctypes.c_void_p(stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"recir_hstu_attn_fwd failed ({rc}): {_lib.last_error()}")
+
+    flops = wl.flops()
+    abytes = wl.algorithmic_bytes()
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        call()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall / args.steps * 1e3
+    kernel_name = _lib.last_kernel()
+
+    # attention kernel alone: HIP events on the launch stream around K launches with the work list reused
+    reuse = _lib.FLAG_REUSE_PLAN if kernel_name.startswith("tiled") else 0
+    call()
+    for _ in range(5):
+        call(reuse)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(args.steps):
+        call(reuse)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    kern_ms = ev0.elapsed_time(ev1) / args.steps
+
+    # per-call latency distribution (device time between events around single full calls)
+    lat = []
+    for _ in range(min(args.steps, 100)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        call()
+        b.record(stream)
+        lat.append((a, b))
+    torch.cuda.synchronize()
+    lat = sorted(a.elapsed_time(b) for a, b in lat)
+
+    # parity guard: the benchmarked output must match the fp32 oracle (bounded sample of rows)
+    peak = PEAK_TFLOPS[wl.dtype]
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    result = {
+        "metric": "HSTU jagged attention fwd, achieved TFLOP/s on unmasked FLOPs (ms/call in ms_per_step; % of MFMA peak in roofline.frac)",
+        "value": flops / (ms_per_step * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": wl.dtype, "data": "synthetic",
+        "config": {"workload": describe(wl, args.config), "tokens": wl.T, "sequences": wl.B,
+                   "unmasked_pairs": wl.pairs(), "flops_per_call": flops, "algorithmic_bytes_per_call": abytes,
+                   "kernel": kernel_name},
+        "latency_ms": {"p50": lat[len(lat) // 2], "p95": lat[int(len(lat) * 0.95) - 1], "p99": lat[-1],
+                       "mean": sum(lat) / len(lat)},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
+                     "frac": achieved / peak, "traffic": None, "kernel_ms": kern_ms,
+                     "hbm_gbs_algorithmic": abytes / (kern_ms * 1e-3) / 1e9,
+                     "hbm_frac_algorithmic": abytes / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBS},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(wl, flops)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

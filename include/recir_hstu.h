@@ -39,6 +39,10 @@ extern "C" {
                                                      (kjt_split_per_feature.cpp:672-674).  Default
                                                      rule: keys j < contextual_seq_len visible. */
 #define RECIR_HSTU_FLAG_SCALE_PER_TOKEN 0x4u      /* attn_scale is [T], indexed by the query token */
+#define RECIR_HSTU_FLAG_REUSE_PLAN 0x8u           /* workspace still holds the work list a previous
+                                                     call built for the same seq_offsets, T, B and
+                                                     kernel variant: skip rebuilding it (the layers
+                                                     of one model step share their offsets)        */
 #define RECIR_HSTU_FLAG_KERNEL_SHIFT 8            /* bits 8..15: kernel selector for tests/tuning  */
 #define RECIR_HSTU_FLAG_KERNEL_MASK 0xff00u       /* 0 auto, 1 generic, 2.. tiled variants         */
 

@@ -16,6 +16,7 @@ DTYPE_FP8_E4M3 = 2
 FLAG_OFFSETS_I32 = 0x1
 FLAG_CTX_REFERENCE = 0x2
 FLAG_SCALE_PER_TOKEN = 0x4
+FLAG_REUSE_PLAN = 0x8
 FLAG_KERNEL_SHIFT = 8
 
 # every symbol include/recir_hstu.h declares

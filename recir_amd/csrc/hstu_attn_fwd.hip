@@ -20,91 +20,12 @@
 
 #include "recir_hstu.h"
 
+#include "hstu_common.h"
+#include "hstu_tiled_d128.h"
+
+using namespace recir_hstu;
+
 namespace {
-
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-typedef __attribute__((ext_vector_type(2))) float f32x2;
-typedef __attribute__((ext_vector_type(16))) float f32x16;
-
-struct Params {
-  const void* q;
-  const void* k;
-  const void* v;
-  void* out;
-  const void* seq_offsets;
-  const void* num_targets;
-  const float* rab;
-  const float* attn_scale;
-  const float* q_scale;
-  const float* k_scale;
-  int* ws_count;   // [1] number of valid work items
-  int2* ws_items;  // [max_items] (sequence, query tile)
-  int T, B, H, Dqk, Dv, N, ctx;
-  float alpha;
-  unsigned flags;
-};
-
-struct SeqInfo {
-  int s;        // first packed token
-  int n;        // length
-  int cap;      // history length n - num_targets (keys j < cap are history)
-  int ctx_eff;  // keys j < ctx_eff are visible to every query
-};
-
-__device__ __forceinline__ long long load_index(const void* p, int i, bool i32) {
-  return i32 ? (long long)((const int*)p)[i] : ((const long long*)p)[i];
-}
-
-__device__ __forceinline__ int clamp_offset(long long x, int lo, int hi) {
-  return x < lo ? lo : (x > hi ? hi : (int)x);
-}
-
-// Sequence b as the kernels see it.  Offsets are clamped into [0, T] and made non-decreasing so
-// that a malformed array cannot cause an out-of-range access.
-__device__ __forceinline__ SeqInfo seq_info(const Params& p, int b) {
-  const bool i32 = p.flags & RECIR_HSTU_FLAG_OFFSETS_I32;
-  SeqInfo si;
-  si.s = clamp_offset(load_index(p.seq_offsets, b, i32), 0, p.T);
-  const int e = clamp_offset(load_index(p.seq_offsets, b + 1, i32), si.s, p.T);
-  si.n = e - si.s;
-  long long t = p.num_targets ? load_index(p.num_targets, b, i32) : 0;
-  long long cap = (long long)si.n - t;
-  si.cap = cap > si.n ? si.n : (cap < -1 ? -1 : (int)cap);
-  if (p.flags & RECIR_HSTU_FLAG_CTX_REFERENCE) {
-    // the reference unmasks keys whose target-clamped id min(j, cap) equals 0: key 0 (already
-    // causal) when cap > 0, every key when cap == 0, none when cap < 0
-    si.ctx_eff = (p.ctx > 0 && cap == 0) ? si.n : 0;
-  } else {
-    si.ctx_eff = p.ctx < si.n ? (p.ctx > 0 ? p.ctx : 0) : si.n;
-  }
-  return si;
-}
-
-__device__ __forceinline__ int end_of_sequences(const Params& p) {
-  const bool i32 = p.flags & RECIR_HSTU_FLAG_OFFSETS_I32;
-  return clamp_offset(load_index(p.seq_offsets, p.B, i32), 0, p.T);
-}
-
-__device__ __forceinline__ bool keep_pair(int m, int j, const SeqInfo& si) {
-  return (m == j) || (m >= j && j < si.cap) || (j < si.ctx_eff);
-}
-
-__device__ __forceinline__ float bf16_bits_to_float(unsigned short b) {
-  return __uint_as_float((unsigned)b << 16);
-}
-
-__device__ __forceinline__ unsigned short float_to_bf16_bits(float x) {
-  f32x2 t = {x, 0.f};
-  bf16x2 y = __builtin_convertvector(t, bf16x2);
-  return (unsigned short)(*(unsigned*)&y & 0xffffu);
-}
-
-__device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
-  f32x2 t = {lo, hi};
-  bf16x2 y = __builtin_convertvector(t, bf16x2);
-  return *(unsigned*)&y;
-}
 
 // ---------------------------------------------------------------------------------------------
 // Work list: one item per (sequence, query tile of BM rows), ordered by tile index descending so
@@ -133,25 +54,6 @@ __global__ __launch_bounds__(64) void hstu_plan_kernel(Params p, int BM) {
 __global__ void hstu_fill_zero(unsigned short* out, size_t n2) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n2; i += stride) out[i] = 0;
-}
-
-// Rows [seq_offsets[B], T) of out := 0, shared by all workgroups of a launch.
-template <int NTHREADS>
-__device__ __forceinline__ void zero_tail_rows(const Params& p, size_t row_bytes) {
-  const int end_all = end_of_sequences(p);
-  if (end_all >= p.T) return;
-  // row_bytes is a multiple of 2; use 2-byte stores only when 16-byte ones do not fit
-  unsigned char* base = (unsigned char*)p.out + (size_t)end_all * row_bytes;
-  const size_t total = (size_t)(p.T - end_all) * row_bytes;
-  const size_t nblk = gridDim.x * (size_t)gridDim.y;
-  const size_t blk = blockIdx.x + (size_t)blockIdx.y * gridDim.x;
-  if ((((size_t)base) & 15) == 0 && (total & 15) == 0) {
-    for (size_t i = blk * NTHREADS + threadIdx.x; i < total / 16; i += nblk * NTHREADS)
-      ((uint4*)base)[i] = make_uint4(0, 0, 0, 0);
-  } else {
-    for (size_t i = blk * NTHREADS + threadIdx.x; i < total / 2; i += nblk * NTHREADS)
-      ((unsigned short*)base)[i] = 0;
-  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -255,237 +157,6 @@ __global__ __launch_bounds__(64) void hstu_fwd_generic(Params p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Tiled MFMA kernel, head dim 128 (qk and v), bf16 values.
-//
-// One workgroup (4 waves) per (sequence, query tile of BM = 128 rows, head); wave w owns query rows
-// [32w, 32w+32) of the tile.  For every key tile of BN = 64 rows:
-//   S^T[kv, q]  = K[kv, d] . Q^T[d, q]        v_mfma_f32_32x32x16_bf16, A = K from LDS, B = Q in VGPRs
-//   P^T         = silu(alpha S^T (+rab)) masked, rounded to bf16, kept in registers: the 32x32
-//                 accumulator layout (lane = query column, 8 key rows per lane half) is exactly the
-//                 B-operand layout of the next contraction
-//   O^T[d, q]  += V^T[d, kv] . P^T[kv, q]     A = V^T from LDS (V is transposed while it is staged)
-// Neither alpha nor the 1/N scale touches P: without a bias silu(aS) = a S sigmoid(aS), so
-// S sigmoid(aS) is accumulated and a * scale is applied once to the fp32 output accumulator.
-//
-// LDS tiles are XOR-swizzled in 16-byte chunks instead of padded:
-//   Ks [BN][128]  chunk' = chunk ^ (row & 7)
-//   Vts[128][BN]  chunk' = chunk ^ ((d ^ (d >> 3)) & 7), key order inside a 16-key group permuted
-//                 to match the accumulator layout (kv = 16 g + 8 a + 4 half + c  ->  16 g + 8 half + 4 a + c)
-// ---------------------------------------------------------------------------------------------
-constexpr int BM = 128;
-constexpr int BN = 64;
-constexpr int HD = 128;
-
-__device__ __forceinline__ int vt_swz(int d) { return (d ^ (d >> 3)) & 7; }
-
-template <bool HAS_RAB, bool FP8_QK>
-__global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
-  __shared__ __attribute__((aligned(16))) unsigned short Ks[BN * HD];
-  __shared__ __attribute__((aligned(16))) unsigned short Vts[HD * BN];
-  __shared__ float rabs[HAS_RAB ? (BM + BN) : 1];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int l32 = lane & 31;
-  const int half = lane >> 5;
-
-  zero_tail_rows<256>(p, (size_t)p.H * HD * 2);
-
-  const int item = blockIdx.x / p.H;
-  const int h = blockIdx.x - item * p.H;
-  if (item >= *p.ws_count) return;
-  const int2 it2 = p.ws_items[item];
-  const SeqInfo si = seq_info(p, it2.x);
-  const int q0 = it2.y * BM;
-  if (q0 >= si.n) return;
-
-  const unsigned short* __restrict__ kg = (const unsigned short*)p.k;
-  const unsigned short* __restrict__ vg = (const unsigned short*)p.v;
-  const size_t row_stride = (size_t)p.H * HD;
-
-  // ---- Q fragments (B operand): lane holds row qw0 + l32, d = 16 kk + 8 half .. +7 ----
-  const int qw0 = q0 + wave * 32;
-  const int m = qw0 + l32;
-  bf16x8 qf[8];
-  {
-    const bool valid = m < si.n;
-    const unsigned short* qrow = (const unsigned short*)p.q + ((size_t)(si.s + (valid ? m : 0)) * p.H + h) * HD;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      uint4 t = valid ? *(const uint4*)(qrow + kk * 16 + half * 8) : make_uint4(0, 0, 0, 0);
-      qf[kk] = *(bf16x8*)&t;
-    }
-  }
-
-  f32x16 acc[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-
-  const float kLog2e = 1.4426950408889634f;
-  const float c1 = HAS_RAB ? -kLog2e : -p.alpha * kLog2e;
-  const int rab_w = 2 * p.N - 1;
-
-  const int m_lo = qw0;
-  const int m_hi = min(qw0 + 31, si.n - 1);
-  const bool wave_has_rows = m_lo < si.n;
-
-  const int kv_end = min(si.n, max(q0 + BM, si.ctx_eff));
-  const int nkv = (kv_end + BN - 1) / BN;
-
-  for (int it = 0; it < nkv; ++it) {
-    const int k0 = it * BN;
-    const int k1 = k0 + BN;
-    // workgroup-uniform skip: tile holds only target keys, none on this q tile's diagonal, and no
-    // contextual keys
-    if (k0 >= si.cap && k1 <= q0 && k0 >= si.ctx_eff) continue;
-
-    __syncthreads();  // all waves done reading the previous tile
-    // ---- stage K: 4 passes of 16 rows, 16 threads x 16 B per row ----
-    {
-      const int chunk = tid & 15;
-#pragma unroll
-      for (int ps = 0; ps < 4; ++ps) {
-        const int row = (tid >> 4) + ps * 16;
-        const int j = k0 + row;
-        uint4 t = make_uint4(0, 0, 0, 0);
-        if (j < si.n) t = *(const uint4*)(kg + (size_t)(si.s + j) * row_stride + (size_t)h * HD + chunk * 8);
-        *(uint4*)&Ks[row * HD + ((chunk ^ (row & 7)) * 8)] = t;
-      }
-    }
-    // ---- stage V transposed: thread (g, e) loads kv rows 4g..4g+3 at d = 8e..8e+7 ----
-    {
-      const int g = tid >> 4, e = tid & 15;
-      uint4 vr[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int j = k0 + 4 * g + c;
-        vr[c] = make_uint4(0, 0, 0, 0);
-        if (j < si.n) vr[c] = *(const uint4*)(vg + (size_t)(si.s + j) * row_stride + (size_t)h * HD + e * 8);
-      }
-      const int g16 = g >> 2, a = (g >> 1) & 1, hf = g & 1;
-      const int c16 = 2 * g16 + hf;
-      const unsigned* w0 = (const unsigned*)&vr[0];
-      const unsigned* w1 = (const unsigned*)&vr[1];
-      const unsigned* w2 = (const unsigned*)&vr[2];
-      const unsigned* w3 = (const unsigned*)&vr[3];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int wi = i >> 1;
-        uint2 o;
-        if (i & 1) {
-          o.x = (w0[wi] >> 16) | (w1[wi] & 0xffff0000u);
-          o.y = (w2[wi] >> 16) | (w3[wi] & 0xffff0000u);
-        } else {
-          o.x = (w0[wi] & 0xffffu) | (w1[wi] << 16);
-          o.y = (w2[wi] & 0xffffu) | (w3[wi] << 16);
-        }
-        const int d = 8 * e + i;
-        *(uint2*)&Vts[d * BN + ((c16 ^ vt_swz(d)) * 8) + a * 4] = o;
-      }
-    }
-    if (HAS_RAB) {
-      // band of bias entries this (q tile, kv tile) can touch: index (m - j) + N - 1
-      const int base = q0 - k0 - (BN - 1) + p.N - 1;
-      if (tid < BM + BN - 1) {
-        int idx = base + tid;
-        idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
-        rabs[tid] = p.rab[(size_t)h * rab_w + idx];
-      }
-    }
-    __syncthreads();
-
-    // wave-level classification of this (32 query rows) x (64 keys) block
-    if (!wave_has_rows) continue;
-    const bool any_kept = (k0 <= m_hi && k1 > m_lo) /* diagonal crosses */ ||
-                          (k0 < si.cap && k0 <= m_hi) /* causal history */ || (k0 < si.ctx_eff);
-    if (!any_kept) continue;
-    const bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
-
-    // ---- S^T = K Q^T ----
-    f32x16 sacc[2];
-#pragma unroll
-    for (int kvb = 0; kvb < 2; ++kvb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kvb][r] = 0.f;
-      const int row = kvb * 32 + l32;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const int chunk = kk * 2 + half;
-        const bf16x8 a = *(const bf16x8*)&Ks[row * HD + ((chunk ^ (row & 7)) * 8)];
-        sacc[kvb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sacc[kvb], 0, 0, 0);
-      }
-    }
-
-    // ---- P^T = silu(...) with the mask, packed to bf16 B operands ----
-    bf16x8 pb[4];
-#pragma unroll
-    for (int kvb = 0; kvb < 2; ++kvb) {
-      float pv[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        float s = sacc[kvb][r];
-        float x = s;
-        if (HAS_RAB) {
-          x = s * p.alpha + rabs[(m - q0) - jl + (BN - 1)];
-          s = x;
-        }
-        const float ex = __builtin_amdgcn_exp2f(x * c1);
-        const float rc = __builtin_amdgcn_rcpf(1.0f + ex);
-        float pe = s * rc;
-        if (!full) {
-          const int j = k0 + jl;
-          pe = (j < si.n && keep_pair(m, j, si)) ? pe : 0.f;
-        }
-        pv[r] = pe;
-      }
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        unsigned w[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(pv[8 * s2 + 2 * i], pv[8 * s2 + 2 * i + 1]);
-        pb[kvb * 2 + s2] = *(bf16x8*)w;
-      }
-    }
-
-    // ---- O^T += V^T P^T ----
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const int d = db * 32 + l32;
-      const int sw = vt_swz(d);
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        const int c16 = s2 * 2 + half;
-        const bf16x8 a = *(const bf16x8*)&Vts[d * BN + ((c16 ^ sw) * 8)];
-        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[s2], acc[db], 0, 0, 0);
-      }
-    }
-  }
-
-  // ---- epilogue: O^T accumulators -> out[s + m, h, :] ----
-  if (m < si.n) {
-    float oscale = 1.0f / (float)p.N;
-    if (p.attn_scale)
-      oscale = (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) ? p.attn_scale[si.s + m] : p.attn_scale[0];
-    if (!HAS_RAB) oscale *= p.alpha;
-    unsigned short* orow = (unsigned short*)p.out + ((size_t)(si.s + m) * p.H + h) * HD;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        uint2 o;
-        o.x = pack_bf16x2(acc[db][4 * rq + 0] * oscale, acc[db][4 * rq + 1] * oscale);
-        o.y = pack_bf16x2(acc[db][4 * rq + 2] * oscale, acc[db][4 * rq + 3] * oscale);
-        *(uint2*)(orow + db * 32 + 8 * rq + 4 * half) = o;
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------------------
 thread_local char g_err[512] = "";
@@ -577,11 +248,13 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     p.ws_items = (int2*)((char*)workspace + 16);
     const size_t items = max_items(T, B);
     if (items * (size_t)H > 0x7fffffffull) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "grid too large");
-    hipLaunchKernelGGL(hstu_plan_kernel, dim3(B), dim3(64), 0, stream, p, BM);
-    if (int rc = launch_status("hstu_plan_kernel")) return rc;
+    if (!(flags & RECIR_HSTU_FLAG_REUSE_PLAN)) {
+      hipLaunchKernelGGL(hstu_plan_kernel, dim3(B), dim3(64), 0, stream, p, BM);
+      if (int rc = launch_status("hstu_plan_kernel")) return rc;
+    }
     const dim3 grid((unsigned)(items * H));
-    if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128<true, false>), grid, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL((hstu_fwd_tiled_d128<false, false>), grid, dim3(256), 0, stream, p);
+    if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128<true>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((hstu_fwd_tiled_d128<false>), grid, dim3(256), 0, stream, p);
     if (int rc = launch_status("hstu_fwd_tiled_d128")) return rc;
     g_last_kernel = rab ? "tiled_d128_bf16_rab" : "tiled_d128_bf16";
     return RECIR_HSTU_OK;

@@ -1,0 +1,116 @@
+// Shared device-side definitions of the HSTU attention kernels: launch parameters, sequence
+// bookkeeping (offset clamping, history cap, contextual prefix), the keep predicate and bf16 helpers.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "recir_hstu.h"
+
+namespace recir_hstu {
+
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
+
+struct Params {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  const void* seq_offsets;
+  const void* num_targets;
+  const float* rab;
+  const float* attn_scale;
+  const float* q_scale;
+  const float* k_scale;
+  int* ws_count;   // [1] number of valid work items
+  int2* ws_items;  // [max_items] (sequence, query tile)
+  int T, B, H, Dqk, Dv, N, ctx;
+  float alpha;
+  unsigned flags;
+};
+
+struct SeqInfo {
+  int s;        // first packed token
+  int n;        // length
+  int cap;      // history length n - num_targets (keys j < cap are history)
+  int ctx_eff;  // keys j < ctx_eff are visible to every query
+};
+
+__device__ __forceinline__ long long load_index(const void* p, int i, bool i32) {
+  return i32 ? (long long)((const int*)p)[i] : ((const long long*)p)[i];
+}
+
+__device__ __forceinline__ int clamp_offset(long long x, int lo, int hi) {
+  return x < lo ? lo : (x > hi ? hi : (int)x);
+}
+
+// Sequence b as the kernels see it.  Offsets are clamped into [0, T] and made non-decreasing so
+// that a malformed array cannot cause an out-of-range access.
+__device__ __forceinline__ SeqInfo seq_info(const Params& p, int b) {
+  const bool i32 = p.flags & RECIR_HSTU_FLAG_OFFSETS_I32;
+  SeqInfo si;
+  si.s = clamp_offset(load_index(p.seq_offsets, b, i32), 0, p.T);
+  const int e = clamp_offset(load_index(p.seq_offsets, b + 1, i32), si.s, p.T);
+  si.n = e - si.s;
+  long long t = p.num_targets ? load_index(p.num_targets, b, i32) : 0;
+  long long cap = (long long)si.n - t;
+  si.cap = cap > si.n ? si.n : (cap < -1 ? -1 : (int)cap);
+  if (p.flags & RECIR_HSTU_FLAG_CTX_REFERENCE) {
+    // the reference unmasks keys whose target-clamped id min(j, cap) equals 0: key 0 (already
+    // causal) when cap > 0, every key when cap == 0, none when cap < 0
+    si.ctx_eff = (p.ctx > 0 && cap == 0) ? si.n : 0;
+  } else {
+    si.ctx_eff = p.ctx < si.n ? (p.ctx > 0 ? p.ctx : 0) : si.n;
+  }
+  return si;
+}
+
+__device__ __forceinline__ int end_of_sequences(const Params& p) {
+  const bool i32 = p.flags & RECIR_HSTU_FLAG_OFFSETS_I32;
+  return clamp_offset(load_index(p.seq_offsets, p.B, i32), 0, p.T);
+}
+
+__device__ __forceinline__ bool keep_pair(int m, int j, const SeqInfo& si) {
+  return (m == j) || (m >= j && j < si.cap) || (j < si.ctx_eff);
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(unsigned short b) {
+  return __uint_as_float((unsigned)b << 16);
+}
+
+__device__ __forceinline__ unsigned short float_to_bf16_bits(float x) {
+  f32x2 t = {x, 0.f};
+  bf16x2 y = __builtin_convertvector(t, bf16x2);
+  return (unsigned short)(*(unsigned*)&y & 0xffffu);
+}
+
+__device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
+  f32x2 t = {lo, hi};
+  bf16x2 y = __builtin_convertvector(t, bf16x2);
+  return *(unsigned*)&y;
+}
+
+// Rows [seq_offsets[B], T) of out := 0, shared by all workgroups of a launch.
+template <int NTHREADS>
+__device__ __forceinline__ void zero_tail_rows(const Params& p, size_t row_bytes) {
+  const int end_all = end_of_sequences(p);
+  if (end_all >= p.T) return;
+  // row_bytes is a multiple of 2; use 2-byte stores only when 16-byte ones do not fit
+  unsigned char* base = (unsigned char*)p.out + (size_t)end_all * row_bytes;
+  const size_t total = (size_t)(p.T - end_all) * row_bytes;
+  const size_t nblk = gridDim.x * (size_t)gridDim.y;
+  const size_t blk = blockIdx.x + (size_t)blockIdx.y * gridDim.x;
+  if ((((size_t)base) & 15) == 0 && (total & 15) == 0) {
+    for (size_t i = blk * NTHREADS + threadIdx.x; i < total / 16; i += nblk * NTHREADS)
+      ((uint4*)base)[i] = make_uint4(0, 0, 0, 0);
+  } else {
+    for (size_t i = blk * NTHREADS + threadIdx.x; i < total / 2; i += nblk * NTHREADS)
+      ((unsigned short*)base)[i] = 0;
+  }
+}
+
+}  // namespace recir_hstu
