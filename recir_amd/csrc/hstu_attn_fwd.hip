@@ -21,35 +21,12 @@
 #include "recir_hstu.h"
 
 #include "hstu_common.h"
+#include "hstu_plan.h"
 #include "hstu_tiled_d128.h"
 
 using namespace recir_hstu;
 
 namespace {
-
-// ---------------------------------------------------------------------------------------------
-// Work list: one item per (sequence, query tile of BM rows), ordered by tile index descending so
-// that the tiles with the longest causal prefix are launched first.
-// ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void hstu_plan_kernel(Params p, int BM) {
-  const int b = blockIdx.x;
-  const SeqInfo si = seq_info(p, b);
-  const int my_tiles = (si.n + BM - 1) / BM;
-  for (int t = threadIdx.x; t < my_tiles; t += blockDim.x) {
-    int rank = 0;
-    for (int b2 = 0; b2 < p.B; ++b2) {
-      const SeqInfo s2 = seq_info(p, b2);
-      const int nt2 = (s2.n + BM - 1) / BM;
-      rank += max(0, nt2 - 1 - t) + ((b2 < b && nt2 > t) ? 1 : 0);
-    }
-    p.ws_items[rank] = make_int2(b, t);
-  }
-  if (b == 0 && threadIdx.x == 0) {
-    int total = 0;
-    for (int b2 = 0; b2 < p.B; ++b2) total += (seq_info(p, b2).n + BM - 1) / BM;
-    *p.ws_count = total;
-  }
-}
 
 __global__ void hstu_fill_zero(unsigned short* out, size_t n2) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -176,7 +153,9 @@ int launch_status(const char* what) {
   return 0;
 }
 
-size_t max_items(int T, int B) { return (size_t)((T + BM - 1) / BM) + (size_t)B; }
+// upper bound on the (sequence, query tile, head) items of a call
+size_t max_items(int T, int B, int H) { return ((size_t)((T + BM - 1) / BM) + (size_t)B) * (size_t)H; }
+constexpr size_t WS_HEADER = 64;
 
 }  // namespace
 
@@ -188,9 +167,10 @@ const char* recir_hstu_last_kernel(void) { return g_last_kernel; }
 
 size_t recir_hstu_attn_fwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk, int32_t Dv,
                                            int32_t dtype) {
-  (void)H; (void)Dqk; (void)Dv; (void)dtype;
-  if (T < 0 || B < 0) return 0;
-  return 16 + sizeof(int2) * max_items(T, B);
+  (void)Dqk; (void)Dv; (void)dtype;
+  if (T < 0 || B < 0 || H <= 0) return 0;
+  // list lengths + NUM_XCD work lists, each able to hold every item of the call
+  return WS_HEADER + sizeof(WorkItem) * max_items(T, B, H) * NUM_XCD;
 }
 
 int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
@@ -244,15 +224,27 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     if (!workspace || workspace_bytes < need || ((size_t)workspace & 15))
       return fail(RECIR_HSTU_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu at %p", need,
                   workspace_bytes, workspace);
-    p.ws_count = (int*)workspace;
-    p.ws_items = (int2*)((char*)workspace + 16);
-    const size_t items = max_items(T, B);
-    if (items * (size_t)H > 0x7fffffffull) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "grid too large");
+    const size_t items = max_items(T, B, H);
+    p.ws_counts = (int*)workspace;
+    p.ws_items = (WorkItem*)((char*)workspace + WS_HEADER);
+    p.items_cap = (int)items;
+    // slots per XCD the launch covers: an even share of the items plus the imbalance the dealing of
+    // whole (sequence, head) pairs can leave (about one sequence's worth of tiles); longer lists,
+    // possible only with sequences above max_seq_len, are walked by the workgroups' stride loop
+    const size_t per_seq = (size_t)(max_seq_len + BM - 1) / BM;
+    size_t slots = (items + NUM_XCD - 1) / NUM_XCD + 2 * per_seq + 1;
+    if (slots > items) slots = items;
+    if (slots < 1) slots = 1;
+    if (items > 0x7fffffffull || slots * NUM_XCD > 0x7fffffffull) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "grid too large");
+    p.grid_slots = (int)slots;
     if (!(flags & RECIR_HSTU_FLAG_REUSE_PLAN)) {
-      hipLaunchKernelGGL(hstu_plan_kernel, dim3(B), dim3(64), 0, stream, p, BM);
+      if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS)
+        hipLaunchKernelGGL(hstu_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, p, BM);
+      else
+        hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, p, BM);
       if (int rc = launch_status("hstu_plan_kernel")) return rc;
     }
-    const dim3 grid((unsigned)(items * H));
+    const dim3 grid((unsigned)(slots * NUM_XCD));
     if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128<true>), grid, dim3(256), 0, stream, p);
     else hipLaunchKernelGGL((hstu_fwd_tiled_d128<false>), grid, dim3(256), 0, stream, p);
     if (int rc = launch_status("hstu_fwd_tiled_d128")) return rc;
@@ -272,6 +264,14 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
   g_last_kernel = dtype == RECIR_HSTU_DTYPE_BF16 ? "generic_bf16" : "generic_fp32";
   return RECIR_HSTU_OK;
 }
+
+#ifdef HSTU_TRACE
+// Debug build only (never part of the shipped library): select the traced workgroup / read stamps.
+int recir_hstu_debug_trace(int block, void* host_dst) {
+  if (host_dst) return (int)hipMemcpyFromSymbol(host_dst, HIP_SYMBOL(recir_hstu::g_trace), sizeof(recir_hstu::g_trace));
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(recir_hstu::g_trace_block), &block, sizeof(int));
+}
+#endif
 
 int recir_hstu_quantize_e4m3_per_head(const void* x_bf16, void* codes_u8, float* scale, int32_t T,
                                       int32_t H, int32_t D, void* hip_stream) {

@@ -15,6 +15,22 @@ typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
 typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
 
+// MI355X: 8 accelerator dies (XCDs), each with its own L2; workgroup i of a launch runs on XCD i % 8.
+constexpr int NUM_XCD = 8;
+
+// One unit of work of the tiled kernels: a query tile of one (sequence, head), with everything the
+// workgroup needs about its sequence so that it starts with a single uniform load.
+struct WorkItem {
+  int s;        // first packed token of the sequence
+  int n;        // sequence length
+  int cap;      // history length (n - num_targets), clamped to [-1, n]
+  int ctx_eff;  // keys j < ctx_eff are visible to every query
+  int q0;       // first query row of the tile
+  int h;        // head
+  int b;        // sequence index
+  int pad;
+};
+
 struct Params {
   const void* q;
   const void* k;
@@ -26,8 +42,10 @@ struct Params {
   const float* attn_scale;
   const float* q_scale;
   const float* k_scale;
-  int* ws_count;   // [1] number of valid work items
-  int2* ws_items;  // [max_items] (sequence, query tile)
+  int* ws_counts;             // [NUM_XCD] length of each per-XCD work list
+  struct WorkItem* ws_items;  // [NUM_XCD][items_cap]
+  int items_cap;              // capacity of one per-XCD list
+  int grid_slots;             // slots per XCD the launch covers (gridDim.x = NUM_XCD * grid_slots)
   int T, B, H, Dqk, Dv, N, ctx;
   float alpha;
   unsigned flags;

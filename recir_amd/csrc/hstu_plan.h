@@ -1,0 +1,149 @@
+// Work-list construction for the tiled kernels.
+//
+// Goals: (1) every query tile of one (sequence, head) runs on the same XCD, so that the K and V rows
+// of that pair are fetched into exactly one L2; (2) the eight per-XCD lists carry equal work;
+// (3) inside a list the query tiles with the longest causal prefix come first, so that the tail of
+// the launch consists of short work.
+//
+// Sequences are ranked by their number of query tiles (descending); pair (rank r, head h) gets the
+// running index pr = r * H + h and is dealt to the XCDs in boustrophedon order
+// (0..7, 7..0, 0..7, ...), which keeps the list sums within one pair's work of each other.  Inside a
+// list, items are ordered by query-tile index descending, ties in dealing order.
+#pragma once
+#include "hstu_common.h"
+
+namespace recir_hstu {
+
+constexpr int PLAN_THREADS = 1024;
+constexpr int PLAN_MAX_B = 1024;      // fast path: sequences ...
+constexpr int PLAN_MAX_PAIRS = 4096;  // ... (sequence, head) pairs ...
+constexpr int PLAN_MAX_TILES = 256;   // ... and query tiles per sequence that fit the LDS tables
+
+__device__ __forceinline__ int snake_xcd(int pr) {
+  const int pos = pr % NUM_XCD;
+  return ((pr / NUM_XCD) & 1) ? NUM_XCD - 1 - pos : pos;
+}
+// position of pair pr inside its XCD list (pairs 16 k + x and 16 k + 15 - x, in that order)
+__device__ __forceinline__ int snake_slot(int pr) {
+  return 2 * (pr / (2 * NUM_XCD)) + ((pr % (2 * NUM_XCD)) >= NUM_XCD ? 1 : 0);
+}
+
+__device__ __forceinline__ void fill_item(WorkItem& w, const SeqInfo& si, int q0, int h, int b) {
+  w.s = si.s; w.n = si.n; w.cap = si.cap; w.ctx_eff = si.ctx_eff;
+  w.q0 = q0; w.h = h; w.b = b; w.pad = 0;
+}
+
+// Fast path: everything in LDS, one block.
+__global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int bm) {
+  __shared__ int nt[PLAN_MAX_B];          // query tiles of sequence b
+  __shared__ int seq_of_rank[PLAN_MAX_B];
+  __shared__ int nt_by_rank[PLAN_MAX_B];
+  __shared__ int xnt[NUM_XCD][PLAN_MAX_PAIRS / NUM_XCD + 2];  // tiles of the k-th pair of list x
+  __shared__ int above[NUM_XCD][PLAN_MAX_TILES + 1];          // tiles of list x with index > t
+  __shared__ int tmax_s;
+  const int tid = threadIdx.x;
+  const int B = p.B, H = p.H;
+  const int pairs = B * H;
+  const int per_list = (pairs + NUM_XCD - 1) / NUM_XCD + 1;  // upper bound on pairs per list
+
+  if (tid == 0) tmax_s = 0;
+  for (int i = tid; i < NUM_XCD * (PLAN_MAX_PAIRS / NUM_XCD + 2); i += PLAN_THREADS) (&xnt[0][0])[i] = 0;
+  __syncthreads();
+  for (int b = tid; b < B; b += PLAN_THREADS) {
+    const int v = (seq_info(p, b).n + bm - 1) / bm;
+    nt[b] = v;
+    atomicMax(&tmax_s, v);
+  }
+  __syncthreads();
+  for (int b = tid; b < B; b += PLAN_THREADS) {
+    const int mine = nt[b];
+    int r = 0;
+    for (int b2 = 0; b2 < B; ++b2) {
+      const int o = nt[b2];
+      r += (o > mine) || (o == mine && b2 < b);
+    }
+    seq_of_rank[r] = b;
+    nt_by_rank[r] = mine;
+  }
+  __syncthreads();
+  for (int r = tid; r < B; r += PLAN_THREADS) {
+    const int v = nt_by_rank[r];
+    for (int h = 0; h < H; ++h) {
+      const int pr = r * H + h;
+      xnt[snake_xcd(pr)][snake_slot(pr)] = v;
+    }
+  }
+  __syncthreads();
+  const int tmax = tmax_s;
+  auto tiles_above = [&](int x, int t) {
+    int a = 0;
+    for (int k = 0; k < per_list; ++k) a += max(0, xnt[x][k] - 1 - t);
+    return a;
+  };
+  const int ttab = min(tmax, PLAN_MAX_TILES) + 1;  // tabulated tile indices; beyond: computed in place
+  for (int i = tid; i < NUM_XCD * ttab; i += PLAN_THREADS) {
+    const int x = i / ttab, t = i - x * ttab;
+    above[x][t] = tiles_above(x, t);
+  }
+  __syncthreads();
+  // one thread per (rank, tile); the heads of a sequence share everything but the list
+  for (int i = tid; i < B * tmax; i += PLAN_THREADS) {
+    const int r = i / tmax, t = i - r * tmax;
+    const int my_nt = nt_by_rank[r];
+    if (t >= my_nt) continue;
+    const int b = seq_of_rank[r];
+    const SeqInfo si = seq_info(p, b);
+    for (int h = 0; h < H; ++h) {
+      const int pr = r * H + h;
+      const int x = snake_xcd(pr), k = snake_slot(pr);
+      int pos = t < ttab ? above[x][t] : tiles_above(x, t);
+      for (int k2 = 0; k2 < k; ++k2) pos += xnt[x][k2] > t;
+      WorkItem w;
+      fill_item(w, si, t * bm, h, b);
+      p.ws_items[(size_t)x * p.items_cap + pos] = w;
+    }
+  }
+  if (tid < NUM_XCD) {
+    int total = 0;
+    for (int k = 0; k < per_list; ++k) total += xnt[tid][k];
+    p.ws_counts[tid] = total;
+  }
+}
+
+// General path for batches beyond the LDS tables: no ranking, pairs dealt in input order, list
+// positions computed from global memory.  Slow (quadratic in the number of pairs) but only used for
+// batches whose attention work dwarfs it.
+__global__ __launch_bounds__(256) void hstu_plan_kernel_general(Params p, int bm) {
+  const int H = p.H;
+  const int pairs = p.B * H;
+  const int rounds = (pairs + 2 * NUM_XCD - 1) / (2 * NUM_XCD);
+  for (int pr = blockIdx.x * blockDim.x + threadIdx.x; pr < pairs; pr += gridDim.x * blockDim.x) {
+    const int b = pr / H, h = pr - b * H;
+    const SeqInfo si = seq_info(p, b);
+    const int my_nt = (si.n + bm - 1) / bm;
+    const int x = snake_xcd(pr);
+    for (int t = 0; t < my_nt; ++t) {
+      int pos = 0;
+      for (int k16 = 0; k16 < rounds; ++k16) {
+        for (int side = 0; side < 2; ++side) {
+          const int o = k16 * 2 * NUM_XCD + (side ? 2 * NUM_XCD - 1 - x : x);
+          if (o >= pairs) continue;
+          const int nt2 = (seq_info(p, o / H).n + bm - 1) / bm;
+          pos += max(0, nt2 - 1 - t) + ((o < pr && nt2 > t) ? 1 : 0);
+        }
+      }
+      WorkItem w;
+      fill_item(w, si, t * bm, h, b);
+      p.ws_items[(size_t)x * p.items_cap + pos] = w;
+    }
+  }
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
+  if (x < NUM_XCD) {
+    int total = 0;
+    for (int pr = 0; pr < pairs; ++pr)
+      if (snake_xcd(pr) == x) total += (seq_info(p, pr / H).n + bm - 1) / bm;
+    p.ws_counts[x] = total;
+  }
+}
+
+}  // namespace recir_hstu

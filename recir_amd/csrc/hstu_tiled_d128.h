@@ -19,6 +19,8 @@
 //   Vts[128][BN]  chunk' = chunk ^ ((d ^ (d >> 3)) & 7), key order inside a 16-key group permuted
 //                 to match the accumulator layout (kv = 16 g + 8 a + 4 half + c  ->  16 g + 8 half + 4 a + c)
 #pragma once
+#include <type_traits>
+
 #include "hstu_common.h"
 
 namespace recir_hstu {
@@ -26,11 +28,27 @@ namespace recir_hstu {
 constexpr int BM = 128;
 constexpr int BN = 64;
 constexpr int HD = 128;
+constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ int vt_swz(int d) { return (d ^ (d >> 3)) & 7; }
 
 // One thread's share of a staged K/V tile (kept as named members, not arrays, so that it lives in
 // registers whatever the control flow around it looks like).
+#ifdef HSTU_TRACE
+// Debug build only: per-wave phase timestamps of one workgroup (see _work tooling).
+__device__ unsigned long long g_trace[4 * 64 * 8];
+__device__ int g_trace_block = 0;
+#define HSTU_STAMP(slot)                                                                  \
+  do {                                                                                    \
+    __builtin_amdgcn_sched_barrier(0);                                                    \
+    if (trace_on && lane == 0 && trace_it < 64)                                           \
+      g_trace[(wave * 64 + trace_it) * 8 + (slot)] = __builtin_readcyclecounter();        \
+    __builtin_amdgcn_sched_barrier(0);                                                    \
+  } while (0)
+#else
+#define HSTU_STAMP(slot) do { } while (0)
+#endif
+
 struct TileRegs {
   u32x4 k0, k1, k2, k3;
   u32x4 v0, v1, v2, v3;
@@ -51,13 +69,17 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
 
   zero_tail_rows<256>(p, (size_t)p.H * HD * 2);
 
-  const int item = blockIdx.x / p.H;
-  const int h = blockIdx.x - item * p.H;
-  if (item >= *p.ws_count) return;
-  const int2 it2 = p.ws_items[item];
-  const SeqInfo si = seq_info(p, it2.x);
-  const int q0 = it2.y * BM;
-  if (q0 >= si.n) return;
+  // Work list of the XCD this workgroup runs on.  Normally one item per workgroup; the stride loop
+  // only matters when a list is longer than the launch assumed (sequences above max_seq_len).
+  const int xcd = blockIdx.x % NUM_XCD;
+  const int list_len = p.ws_counts[xcd];
+  const WorkItem* __restrict__ list = p.ws_items + (size_t)xcd * p.items_cap;
+  for (int slot = blockIdx.x / NUM_XCD; slot < list_len; slot += p.grid_slots) {
+  const WorkItem wi = list[slot];
+  SeqInfo si;
+  si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
+  const int q0 = wi.q0;
+  const int h = wi.h;
 
   const size_t row_stride = (size_t)p.H * HD;
   const unsigned short* __restrict__ kg = (const unsigned short*)p.k + (size_t)si.s * row_stride + (size_t)h * HD;
@@ -66,17 +88,25 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
   const float* __restrict__ rabg = HAS_RAB ? p.rab + (size_t)h * rab_w : nullptr;
 
   // ---- Q fragments (B operand): lane holds row qw0 + l32, d = 16 kk + 8 half .. +7 ----
+  // q is pre-multiplied by alpha * log2(e) (rounded back to bf16), so the score accumulator holds
+  // u = x * log2(e) directly, sigmoid needs exp2(-u) with no multiply, and u * sigmoid(x) is
+  // accumulated; the constant 1 / log2(e) goes into the output scale.
   const int qw0 = q0 + wave * 32;
   const int m = qw0 + l32;
   bf16x8 qf[8];
   {
     const bool valid = m < si.n;
     const unsigned short* qrow = (const unsigned short*)p.q + ((size_t)(si.s + (valid ? m : 0)) * p.H + h) * HD;
+    const float qmul = p.alpha * kLog2e;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
       const u32x4 zero4 = {0u, 0u, 0u, 0u};
       const u32x4 t = valid ? *(const u32x4*)(qrow + kk * 16 + half * 8) : zero4;
-      qf[kk] = __builtin_bit_cast(bf16x8, t);
+      u32x4 sc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sc[i] = pack_bf16x2(__uint_as_float(t[i] << 16) * qmul, __uint_as_float(t[i] & 0xffff0000u) * qmul);
+      qf[kk] = __builtin_bit_cast(bf16x8, sc);
     }
   }
 
@@ -86,8 +116,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 
-  const float kLog2e = 1.4426950408889634f;
-  const float c1 = HAS_RAB ? -kLog2e : -p.alpha * kLog2e;
 
   const int m_lo = qw0;
   const int m_hi = min(qw0 + 31, si.n - 1);
@@ -102,6 +130,10 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
   const int skip_b = q0 / BN;
   const bool has_skip = skip_a < skip_b;
 
+#ifdef HSTU_TRACE
+  const bool trace_on = (int)blockIdx.x == g_trace_block;
+  int trace_it = 0;
+#endif
   // staging roles of this thread
   const int k_chunk = tid & 15, k_row0 = tid >> 4;        // K: rows k_row0 + 16 ps, 16-byte chunk
   const int v_g = tid >> 4, v_e = tid & 15;               // V: rows 4 v_g .. +3, d = 8 v_e .. +7
@@ -123,6 +155,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
     unsigned ko0 = k_off0, ko1 = k_off0 + 16 * row_bytes, ko2 = k_off0 + 32 * row_bytes, ko3 = k_off0 + 48 * row_bytes;
     unsigned vo0 = v_off0, vo1 = v_off0 + row_bytes, vo2 = v_off0 + 2 * row_bytes, vo3 = v_off0 + 3 * row_bytes;
     if (k0 + BN > si.n) {
+      asm volatile("" ::: "memory");   // keep this a branch: the multiplies below must stay off the steady-state path
       const int last = si.n - 1 - k0;  // >= 0: a tile is only visited when k0 < n
       const unsigned kc = (unsigned)k_chunk * 16u, vc = (unsigned)v_e * 16u;
       ko0 = (unsigned)min(k_row0, last) * row_bytes + kc;
@@ -146,7 +179,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
       // band of bias entries this (q tile, kv tile) can touch: index (m - j) + N - 1
       int idx = q0 - k0 - (BN - 1) + p.N - 1 + tid;
       idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
-      tr.rab = (tid < BM + BN - 1) ? rabg[idx] : 0.f;
+      tr.rab = (tid < BM + BN - 1) ? rabg[idx] * kLog2e : 0.f;
     }
   };
 
@@ -191,6 +224,97 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
   const unsigned ks_rd = (unsigned)l32 * (HD * 2) + (unsigned)((half ^ (l32 & 7)) * 16);
   const unsigned vt_rd = (unsigned)l32 * (BN * 2) + (unsigned)((half ^ vt_swz(l32)) * 16);
 
+  // silu + mask + bf16 packing of one 32 x 32 score block (accumulator layout) into two B operands
+  auto silu_pack = [&](auto masked_tag, const f32x16& sv, int k0, int kvb, int buf, bf16x8& o0,
+                       bf16x8& o1) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    f32x16 pv;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+      float s = sv[r];
+      if (HAS_RAB) s += rabs[buf][(m - q0) - jl + (BN - 1)];  // bias staged pre-multiplied by log2(e)
+      const float ex = __builtin_amdgcn_exp2f(-s);
+      float pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
+      if (MASKED) {
+        const int j = k0 + jl;
+        // branch-free keep(m, j) & (j < n)
+        const bool kp = ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
+        pe = kp ? pe : 0.f;
+      }
+      pv[r] = pe;
+    }
+    u32x4 w0, w1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w0[i] = pack_bf16x2(pv[2 * i], pv[2 * i + 1]);
+      w1[i] = pack_bf16x2(pv[8 + 2 * i], pv[8 + 2 * i + 1]);
+    }
+    o0 = __builtin_bit_cast(bf16x8, w0);
+    o1 = __builtin_bit_cast(bf16x8, w1);
+  };
+
+  // One (32 query rows) x (64 keys) block of this wave.  The code is laid out in four stages of
+  // eight MFMAs; the VALU work of one stage is independent of that stage's MFMAs, and the
+  // scheduling fences keep the two streams interleaved so the matrix pipe runs in the shadow of
+  // the SiLU arithmetic:
+  //   0: S0 = K[0:32] Q^T          |  -
+  //   A: S1 = K[32:64] Q^T         |  P0 = silu(S0)
+  //   B: O += V^T[:, 0:32] P0      |  P1 = silu(S1)
+  //   C: O += V^T[:, 32:64] P1     |  (caller: register -> LDS staging of the next tile)
+  auto tile_body = [&](auto masked_tag, int k0, int buf) __attribute__((always_inline)) {
+    const char* kb = (const char*)&Ks[buf][0];
+    const char* vb = (const char*)&Vts[buf][0];
+    const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    auto k_frag = [&](int kvb, int kk) __attribute__((always_inline)) {
+      return *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)((kk & 3) * 32)) + (kk >> 2) * 128);
+    };
+    auto v_frag = [&](int db, int s2) __attribute__((always_inline)) {
+      return *(const bf16x8*)(vb + db * 32 * BN * 2 + (vt_rd ^ (unsigned)((s2 * 32) ^ ((db & 1) * 64))));
+    };
+    f32x16 s0, s1;
+    bf16x8 pb0, pb1, pb2, pb3;
+    // stage 0
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(0, kk), qf[kk], kk == 0 ? zero : s0, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // stage A
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(1, kk), qf[kk], kk == 0 ? zero : s1, 0, 0, 0);
+    silu_pack(masked_tag, s0, k0, 0, buf, pb0, pb1);
+    // MFMAs issue in pairs: the second of a back-to-back pair costs less issue time than a
+    // lone one, and the pair's 64 pipe cycles cover the VALU batch that follows
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // 10 VALU
+      __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);   // 8 transcendental
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // stage B
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 0), pb0, acc[db], 0, 0, 0);
+      acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 1), pb1, acc[db], 0, 0, 0);
+    }
+    silu_pack(masked_tag, s1, k0, 1, buf, pb2, pb3);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+      __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // stage C
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 2), pb2, acc[db], 0, 0, 0);
+      acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 3), pb3, acc[db], 0, 0, 0);
+    }
+  };
+
   auto compute_tile = [&](int it, int buf) __attribute__((always_inline)) {
     const int k0 = it * BN;
     const int k1 = k0 + BN;
@@ -200,84 +324,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
                           (k0 < si.cap && k0 <= m_hi) /* causal history */ || (k0 < si.ctx_eff);
     if (!any_kept) return;
     const bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
-
-    // ---- S^T = K Q^T ----
-    f32x16 sacc[2];
-    const char* kb = (const char*)&Ks[buf][0];
-#pragma unroll
-    for (int kvb = 0; kvb < 2; ++kvb) {
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const bf16x8 a = *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)((kk & 3) * 32)) + (kk >> 2) * 128);
-        if (kk == 0) {
-          const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-          sacc[kvb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], zero, 0, 0, 0);
-        } else {
-          sacc[kvb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sacc[kvb], 0, 0, 0);
-        }
-      }
-    }
-
-    // ---- P^T = silu(...) (mask on partial tiles only), packed to bf16 B operands ----
-    bf16x8 pb[4];
-    if (full) {
-#pragma unroll
-      for (int kvb = 0; kvb < 2; ++kvb) {
-        f32x16 pv;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float s = sacc[kvb][r];
-          if (HAS_RAB) {
-            const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            s = s * p.alpha + rabs[buf][(m - q0) - jl + (BN - 1)];
-          }
-          const float ex = __builtin_amdgcn_exp2f(s * c1);
-          pv[r] = s * __builtin_amdgcn_rcpf(1.0f + ex);
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          u32x4 w;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(pv[8 * s2 + 2 * i], pv[8 * s2 + 2 * i + 1]);
-          pb[kvb * 2 + s2] = __builtin_bit_cast(bf16x8, w);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int kvb = 0; kvb < 2; ++kvb) {
-        f32x16 pv;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const int j = k0 + jl;
-          float s = sacc[kvb][r];
-          if (HAS_RAB) s = s * p.alpha + rabs[buf][(m - q0) - jl + (BN - 1)];
-          const float ex = __builtin_amdgcn_exp2f(s * c1);
-          const float pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
-          // branch-free keep(m, j) & (j < n)
-          const bool kp = ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
-          pv[r] = kp ? pe : 0.f;
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          u32x4 w;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(pv[8 * s2 + 2 * i], pv[8 * s2 + 2 * i + 1]);
-          pb[kvb * 2 + s2] = __builtin_bit_cast(bf16x8, w);
-        }
-      }
-    }
-
-    // ---- O^T += V^T P^T ----
-    const char* vb = (const char*)&Vts[buf][0];
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        const bf16x8 a = *(const bf16x8*)(vb + db * 32 * BN * 2 + (vt_rd ^ (unsigned)((s2 * 32) ^ ((db & 1) * 64))));
-        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[s2], acc[db], 0, 0, 0);
-      }
-    }
+    if (full) tile_body(std::false_type{}, k0, buf);
+    else tile_body(std::true_type{}, k0, buf);
   };
 
   auto next_tile = [&](int it) { return (has_skip && it + 1 == skip_a) ? skip_b : it + 1; };
@@ -292,14 +340,26 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
     int nxt = next_tile(it);
     if (nxt < nkv) load_tile(nxt, tr);
     while (true) {
+      HSTU_STAMP(0);
       compute_tile(it, buf);
+      HSTU_STAMP(4);
       if (nxt >= nkv) break;
+#ifdef HSTU_TRACE
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      HSTU_STAMP(1);
+#endif
       store_tile(buf ^ 1, tr);
+      HSTU_STAMP(5);
       __syncthreads();
+      HSTU_STAMP(6);
       it = nxt;
       buf ^= 1;
       nxt = next_tile(it);
       if (nxt < nkv) load_tile(nxt, tr);
+      HSTU_STAMP(7);
+#ifdef HSTU_TRACE
+      ++trace_it;
+#endif
     }
   }
 
@@ -308,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
     float oscale = 1.0f / (float)p.N;
     if (p.attn_scale)
       oscale = (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) ? p.attn_scale[si.s + m] : p.attn_scale[0];
-    if (!HAS_RAB) oscale *= p.alpha;
+    oscale *= 1.0f / kLog2e;
     unsigned short* orow = (unsigned short*)p.out + ((size_t)(si.s + m) * p.H + h) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -321,6 +381,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
       }
     }
   }
+  __syncthreads();  // LDS buffers are reused by the next item
+  }  // work items
 }
 
 }  // namespace recir_hstu

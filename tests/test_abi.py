@@ -41,9 +41,10 @@ def test_abi_version(lib):
 
 
 def test_workspace_size_is_host_arithmetic(lib):
-    # one (sequence, query tile) slot per 128 packed rows plus one per sequence, 8 bytes each
-    assert lib.recir_hstu_attn_fwd_workspace_bytes(39382, 32, 4, 128, 128, 0) == 16 + 8 * (308 + 32)
-    assert lib.recir_hstu_attn_fwd_workspace_bytes(0, 0, 1, 8, 8, 1) == 16
+    # a 64-byte header plus 8 per-XCD lists of 32-byte items, each list able to hold every
+    # (sequence, query tile, head) item: (ceil(T/128) + B) * H of them
+    assert lib.recir_hstu_attn_fwd_workspace_bytes(39382, 32, 4, 128, 128, 0) == 64 + 32 * (308 + 32) * 4 * 8
+    assert lib.recir_hstu_attn_fwd_workspace_bytes(0, 0, 1, 8, 8, 1) == 64
     assert lib.recir_hstu_attn_fwd_workspace_bytes(-1, 0, 1, 8, 8, 1) == 0
 
 

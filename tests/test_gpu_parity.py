@@ -235,6 +235,31 @@ def test_generic_kernel_head_dims(oracle, shape):
     assert st["rel_to_max"] <= 3e-2, st  # v is also rounded to bf16 here
 
 
+def test_many_short_sequences_use_the_general_work_list(oracle):
+    """More sequences than the single-block work-list builder tabulates (1024)."""
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    rng = np.random.default_rng(5)
+    lengths = rng.integers(0, 40, size=1300)
+    lengths[7] = 300
+    targets = np.minimum(rng.integers(0, 4, size=1300), lengths)
+    wl = make_jagged(lengths, targets, 2, 128, 128, max_seq_len=320, alpha=1 / 128, dtype="bf16", seed=11)
+    out = run_hip(wl)
+    assert _lib.last_kernel().startswith("tiled_d128")
+    assert_bf16_close(out, run_oracle(oracle, wl), "B=1300")
+
+
+def test_sequences_longer_than_max_seq_len_do_not_break_the_work_list(oracle):
+    """Out of contract (n > max_seq_len), but the launch must stay in bounds: the work lists are
+    then longer than the grid assumes and the workgroups loop over them."""
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([3000, 40, 1500], [10, 0, 0], 1, 128, 128, max_seq_len=256, alpha=1 / 128, dtype="bf16", seed=12)
+    out = run_hip(wl)
+    assert_bf16_close(out, run_oracle(oracle, wl), "n > N")
+
+
 def test_rab_zero_is_identical_to_no_rab():
     from recir_amd.workloads import make_jagged
 
