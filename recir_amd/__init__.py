@@ -14,6 +14,7 @@ from .ops import (  # noqa: F401
     KERNEL_AUTO,
     KERNEL_GENERIC,
     KERNEL_TILED,
+    KERNEL_TILED_DIRECT,
 )
 
 __all__ = [

@@ -23,6 +23,7 @@
 #include "hstu_common.h"
 #include "hstu_plan.h"
 #include "hstu_tiled_d128.h"
+#include "hstu_tiled_d128_dl.h"
 
 using namespace recir_hstu;
 
@@ -245,10 +246,16 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
       if (int rc = launch_status("hstu_plan_kernel")) return rc;
     }
     const dim3 grid((unsigned)(slots * NUM_XCD));
-    if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128<true>), grid, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL((hstu_fwd_tiled_d128<false>), grid, dim3(256), 0, stream, p);
+    if (variant == 2) {  // register-staged tiles (kept for comparison and tiling-invariance tests)
+      if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128<true>), grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL((hstu_fwd_tiled_d128<false>), grid, dim3(256), 0, stream, p);
+      g_last_kernel = rab ? "tiled_d128_bf16_regstage_rab" : "tiled_d128_bf16_regstage";
+    } else {
+      if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<true>), grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<false>), grid, dim3(256), 0, stream, p);
+      g_last_kernel = rab ? "tiled_d128_bf16_rab" : "tiled_d128_bf16";
+    }
     if (int rc = launch_status("hstu_fwd_tiled_d128")) return rc;
-    g_last_kernel = rab ? "tiled_d128_bf16_rab" : "tiled_d128_bf16";
     return RECIR_HSTU_OK;
   }
 

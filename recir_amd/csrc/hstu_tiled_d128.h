@@ -49,6 +49,10 @@ __device__ int g_trace_block = 0;
 #define HSTU_STAMP(slot) do { } while (0)
 #endif
 
+#ifndef HSTU_EXP
+#define HSTU_EXP 0  // debug builds only: bit mask that removes pieces of the kernel for timing studies
+#endif
+
 struct TileRegs {
   u32x4 k0, k1, k2, k3;
   u32x4 v0, v1, v2, v3;
@@ -60,6 +64,10 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
   __shared__ __attribute__((aligned(16))) unsigned short Ks[2][BN * HD];
   __shared__ __attribute__((aligned(16))) unsigned short Vts[2][HD * BN];
   __shared__ float rabs[2][HAS_RAB ? (BM + BN) : 1];
+#if HSTU_EXP & 64
+  __shared__ char occupancy_pad[40000];  // debug builds only: forces one workgroup per CU
+  if (p.T < 0) occupancy_pad[threadIdx.x] = 1;
+#endif
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -234,8 +242,13 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
       const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
       float s = sv[r];
       if (HAS_RAB) s += rabs[buf][(m - q0) - jl + (BN - 1)];  // bias staged pre-multiplied by log2(e)
-      const float ex = __builtin_amdgcn_exp2f(-s);
-      float pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
+      float pe;
+      if (HSTU_EXP & 1) {
+        pe = s;
+      } else {
+        const float ex = __builtin_amdgcn_exp2f(-s);
+        pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
+      }
       if (MASKED) {
         const int j = k0 + jl;
         // branch-free keep(m, j) & (j < n)
@@ -276,12 +289,13 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
     bf16x8 pb0, pb1, pb2, pb3;
     // stage 0
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
+    for (int kk = 0; kk < ((HSTU_EXP & 8) ? 1 : 8); ++kk)
       s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(0, kk), qf[kk], kk == 0 ? zero : s0, 0, 0, 0);
+    HSTU_STAMP(1);
     __builtin_amdgcn_sched_barrier(0);
     // stage A
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
+    for (int kk = 0; kk < ((HSTU_EXP & 8) ? 1 : 8); ++kk)
       s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(1, kk), qf[kk], kk == 0 ? zero : s1, 0, 0, 0);
     silu_pack(masked_tag, s0, k0, 0, buf, pb0, pb1);
     // MFMAs issue in pairs: the second of a back-to-back pair costs less issue time than a
@@ -292,10 +306,11 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
       __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // 10 VALU
       __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);   // 8 transcendental
     }
+    HSTU_STAMP(2);
     __builtin_amdgcn_sched_barrier(0);
     // stage B
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < ((HSTU_EXP & 4) ? 1 : 4); ++db) {
       acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 0), pb0, acc[db], 0, 0, 0);
       acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 1), pb1, acc[db], 0, 0, 0);
     }
@@ -306,10 +321,11 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
       __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
       __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);
     }
+    HSTU_STAMP(3);
     __builtin_amdgcn_sched_barrier(0);
     // stage C
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < ((HSTU_EXP & 4) ? 1 : 4); ++db) {
       acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 2), pb2, acc[db], 0, 0, 0);
       acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 3), pb3, acc[db], 0, 0, 0);
     }
@@ -344,18 +360,14 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
       compute_tile(it, buf);
       HSTU_STAMP(4);
       if (nxt >= nkv) break;
-#ifdef HSTU_TRACE
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      HSTU_STAMP(1);
-#endif
-      store_tile(buf ^ 1, tr);
+      if (!(HSTU_EXP & 2)) store_tile(buf ^ 1, tr);
       HSTU_STAMP(5);
-      __syncthreads();
+      if (!(HSTU_EXP & 16)) __syncthreads();
       HSTU_STAMP(6);
       it = nxt;
       buf ^= 1;
       nxt = next_tile(it);
-      if (nxt < nkv) load_tile(nxt, tr);
+      if (!(HSTU_EXP & (2 | 32)) && nxt < nkv) load_tile(nxt, tr);
       HSTU_STAMP(7);
 #ifdef HSTU_TRACE
       ++trace_it;

@@ -1,0 +1,388 @@
+// Tiled MFMA kernel of the HSTU attention forward, head dim 128 (qk and v), bf16 values, with K and
+// V tiles copied global -> LDS directly (no register staging) and V^T fragments produced by the
+// LDS transposing read.
+//
+// One workgroup (4 waves) per (sequence, query tile of BM = 128 rows, head); wave w owns query rows
+// [32w, 32w+32) of the tile.  For every key tile of BN = 64 rows:
+//   S^T[kv, q]  = K[kv, d] . Q^T[d, q]        v_mfma_f32_32x32x16_bf16, A = K from LDS, B = Q in VGPRs
+//   P^T         = silu(S^T (+rab)) masked, rounded to bf16, kept in registers: the 32x32 accumulator
+//                 layout (lane = query column, 8 key rows per lane half) is exactly the B-operand
+//                 layout of the next contraction
+//   O^T[d, q]  += V^T[d, kv] . P^T[kv, q]     A = V^T, read from the row-major V tile with
+//                 ds_read_b64_tr_b16 (each 16-lane group transposes a 4 x 16 block)
+// q is pre-multiplied by alpha * log2(e), so sigmoid needs exp2(-u) only and the constant factors
+// (1 / log2(e), the 1/N scale) are applied once to the fp32 output accumulator.
+//
+// Pipeline: two LDS stages.  The global_load_lds of tile i+1 are issued while the first MFMAs of
+// tile i run and must have landed (vmcnt) before the barrier that ends tile i.
+//
+// LDS layouts (both tiles are [BN rows][256 bytes], swizzled in place of padding):
+//   K  16-byte chunk c of row r sits at chunk c ^ (r & 7)         (ds_read_b128 of 8 rows: all banks)
+//   V  32-byte slot  s of row r sits at slot  s ^ (r & 3)         (transposing read of 4 rows x 32 B:
+//                                                                  all banks)
+// A global_load_lds instruction writes 64 lanes x 16 bytes to consecutive LDS addresses, so the
+// swizzle is applied to the global address each lane fetches.
+#pragma once
+#include <type_traits>
+
+#include "hstu_common.h"
+#include "hstu_tiled_d128.h"  // BM, BN, HD, kLog2e
+
+namespace recir_hstu {
+
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef __attribute__((ext_vector_type(8))) short i16x8;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+template <bool HAS_RAB>
+__global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
+  // The two pipeline stages are separate objects and every access names its stage at compile time:
+  // the compiler then knows that an LDS read of one stage cannot alias the global -> LDS copies in
+  // flight into the other, and does not wait for them.
+  __shared__ __attribute__((aligned(1024))) unsigned short Ks0[BN * HD];
+  __shared__ __attribute__((aligned(1024))) unsigned short Ks1[BN * HD];
+  __shared__ __attribute__((aligned(1024))) unsigned short Vs0[BN * HD];
+  __shared__ __attribute__((aligned(1024))) unsigned short Vs1[BN * HD];
+  __shared__ float rabs0[HAS_RAB ? (BM + BN) : 1];
+  __shared__ float rabs1[HAS_RAB ? (BM + BN) : 1];
+#if HSTU_EXP & 64
+  __shared__ char occupancy_pad[40000];  // debug builds only: forces one workgroup per CU
+  if (p.T < 0) occupancy_pad[threadIdx.x] = 1;
+#endif
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int half = lane >> 5;
+
+  zero_tail_rows<256>(p, (size_t)p.H * HD * 2);
+
+  // ---- per-lane constants of the LDS access patterns ----
+  // K fragment (ds_read_b128): row 32 kvb + l32, chunk (2 kk + half) ^ (l32 & 7); kk and kk + 4 differ
+  // by 128 bytes, kk & 3 enters as an XOR of address bits 5..6
+  const unsigned ks_rd = (unsigned)l32 * (HD * 2) + (unsigned)((half ^ (l32 & 7)) * 16);
+  // V^T fragment (two ds_read_b64_tr_b16): source lane s = lane & 15 of a 16-lane group supplies the
+  // 8 bytes at row 4 half + (s >> 2) (+ 16 s2 + 8 rd), d = 32 db + 16 dgrp + 4 (s & 3) .. +3
+  const int tr_s = lane & 15, tr_r = tr_s >> 2, tr_c = tr_s & 3, tr_dgrp = (lane >> 4) & 1;
+  const unsigned vt_base = (unsigned)(4 * half + tr_r) * (HD * 2) + (unsigned)((tr_dgrp ^ (tr_r & 1)) * 32) + (unsigned)tr_c * 8u;
+  const unsigned vt_rd_e = vt_base + (unsigned)((tr_r >> 1) * 64);  // even db: slot bit 1 flipped upwards
+  const unsigned vt_rd_o = vt_base - (unsigned)((tr_r >> 1) * 64);  // odd db: downwards
+  // global -> LDS copies: instruction j of a tile (16 per matrix, wave w issues j = 4 w + ps) fills rows
+  // 4 j .. 4 j + 3; lane i lands at row 4 j + (i >> 4), physical chunk i & 15
+  const int ld_row = lane >> 4, ld_chunk = lane & 15;
+
+  // Work list of the XCD this workgroup runs on.  Normally one item per workgroup; the stride loop
+  // only matters when a list is longer than the launch assumed (sequences above max_seq_len).
+  const int xcd = blockIdx.x % NUM_XCD;
+  const int list_len = p.ws_counts[xcd];
+  const WorkItem* __restrict__ list = p.ws_items + (size_t)xcd * p.items_cap;
+  for (int slot = blockIdx.x / NUM_XCD; slot < list_len; slot += p.grid_slots) {
+    const WorkItem wi = list[slot];
+    SeqInfo si;
+    si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
+    const int q0 = wi.q0;
+    const int h = wi.h;
+
+    const unsigned row_bytes = (unsigned)p.H * HD * 2u;
+    const char* __restrict__ kgb = (const char*)p.k + ((size_t)si.s * p.H + h) * (HD * 2);
+    const char* __restrict__ vgb = (const char*)p.v + ((size_t)si.s * p.H + h) * (HD * 2);
+    const int rab_w = 2 * p.N - 1;
+    const float* __restrict__ rabg = HAS_RAB ? p.rab + (size_t)h * rab_w : nullptr;
+
+    // logical 16-byte chunk each lane fetches so that the swizzled layout comes out
+    const unsigned k_off_e = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ ld_row) * 16);        // rows 8a + 0..3
+    const unsigned k_off_o = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ (4 + ld_row)) * 16);  // rows 8a + 4..7
+    const unsigned v_off = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ (2 * ld_row)) * 16);
+
+    const int qw0 = q0 + wave * 32;
+    const int m = qw0 + l32;
+    const int m_lo = qw0;
+    const int m_hi = min(qw0 + 31, si.n - 1);
+    const bool wave_has_rows = m_lo < si.n;
+
+    // key tiles [0, nkv) minus the run [skip_a, skip_b) that holds only target keys off this query
+    // tile's diagonal (and no contextual key)
+    const int kv_end = min(si.n, max(q0 + BM, si.ctx_eff));
+    const int nkv = (kv_end + BN - 1) / BN;
+    const int cap0 = si.cap > 0 ? si.cap : 0;
+    const int skip_a = (max(cap0, si.ctx_eff) + BN - 1) / BN;
+    const int skip_b = q0 / BN;
+    const bool has_skip = skip_a < skip_b;
+    auto next_tile = [&](int it) { return (has_skip && it + 1 == skip_a) ? skip_b : it + 1; };
+
+    // Copies of one tile: 4 + 4 instructions per wave.  Rows at or past the end of the sequence
+    // (last, partial tile only) re-read the sequence's last row; the mask zeroes their contribution.
+    auto issue_tile = [&](int it, auto buf_tag) __attribute__((always_inline)) {
+      constexpr int BUF = decltype(buf_tag)::value;
+      unsigned short* Kd = BUF ? Ks1 : Ks0;
+      unsigned short* Vd = BUF ? Vs1 : Vs0;
+      float* rabd = BUF ? rabs1 : rabs0;
+      const int k0 = it * BN;
+      const char* kt = kgb + (size_t)k0 * row_bytes;
+      const char* vt = vgb + (size_t)k0 * row_bytes;
+      const bool whole = k0 + BN <= si.n;
+      const int last = si.n - 1 - k0;
+#pragma unroll
+      for (int ps = 0; ps < 4; ++ps) {
+        const int r0 = 4 * (4 * wave + ps);  // first row this instruction fills
+        unsigned ko = (ps & 1) ? k_off_o : k_off_e;
+        unsigned vo = v_off;
+        const char* kr = kt + (size_t)r0 * row_bytes;
+        const char* vr = vt + (size_t)r0 * row_bytes;
+        if (!whole) {
+          asm volatile("" ::: "memory");  // keep the clamping arithmetic off the steady-state path
+          const int row = min(r0 + ld_row, last);
+          ko = (unsigned)row * row_bytes + (unsigned)((ld_chunk ^ ((r0 + ld_row) & 7)) * 16);
+          vo = (unsigned)row * row_bytes + (unsigned)((ld_chunk ^ (2 * ld_row)) * 16);
+          kr = kt;
+          vr = vt;
+        }
+        __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)&Kd[r0 * HD], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const unsigned*)(vr + vo), (lds_void*)&Vd[r0 * HD], 16, 0, 0);
+      }
+      if (HAS_RAB) {
+        // band of bias entries this (q tile, kv tile) can touch: index (m - j) + N - 1, staged
+        // pre-multiplied by log2(e); plain stores, ordered by the barrier that publishes the tile
+        int idx = q0 - k0 - (BN - 1) + p.N - 1 + tid;
+        idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
+        if (tid < BM + BN - 1) rabd[tid] = rabg[idx] * kLog2e;
+      }
+    };
+
+    // first tile in flight before anything else is waited for
+    int it = (has_skip && skip_a == 0) ? skip_b : 0;
+    if (it < nkv) issue_tile(it, std::integral_constant<int, 0>{});
+
+    // ---- Q fragments (B operand): lane holds row qw0 + l32, d = 16 kk + 8 half .. +7 ----
+    bf16x8 qf[8];
+    {
+      const bool valid = m < si.n;
+      const unsigned short* qrow = (const unsigned short*)p.q + ((size_t)(si.s + (valid ? m : 0)) * p.H + h) * HD;
+      const float qmul = p.alpha * kLog2e;
+      u32x4 t[8];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const u32x4 zero4 = {0u, 0u, 0u, 0u};
+        t[kk] = valid ? *(const u32x4*)(qrow + kk * 16 + half * 8) : zero4;
+      }
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        u32x4 sc;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sc[i] = pack_bf16x2(__uint_as_float(t[kk][i] << 16) * qmul, __uint_as_float(t[kk][i] & 0xffff0000u) * qmul);
+        qf[kk] = __builtin_bit_cast(bf16x8, sc);
+      }
+    }
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+
+    // silu + mask + bf16 packing of one 32 x 32 score block (accumulator layout) into two B operands
+    auto silu_pack = [&](auto masked_tag, const f32x16& sv, int k0, int kvb, const float* rabt, bf16x8& o0,
+                         bf16x8& o1) __attribute__((always_inline)) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      f32x16 pv;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        float s = sv[r];
+        if (HAS_RAB) s += rabt[(m - q0) - jl + (BN - 1)];
+        const float ex = __builtin_amdgcn_exp2f(-s);
+        float pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
+        if (MASKED) {
+          const int j = k0 + jl;
+          // branch-free keep(m, j) & (j < n)
+          const bool kp = ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
+          pe = kp ? pe : 0.f;
+        }
+        pv[r] = pe;
+      }
+      u32x4 w0, w1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w0[i] = pack_bf16x2(pv[2 * i], pv[2 * i + 1]);
+        w1[i] = pack_bf16x2(pv[8 + 2 * i], pv[8 + 2 * i + 1]);
+      }
+      o0 = __builtin_bit_cast(bf16x8, w0);
+      o1 = __builtin_bit_cast(bf16x8, w1);
+    };
+
+    // One (32 query rows) x (64 keys) block of this wave in four stages of eight MFMAs; the VALU
+    // work of a stage is independent of that stage's MFMAs and the scheduling groups interleave them:
+    //   0: S0 = K[0:32] Q^T          |  copies of the next tile are issued
+    //   A: S1 = K[32:64] Q^T         |  P0 = silu(S0)
+    //   B: O += V^T[:, 0:32] P0      |  P1 = silu(S1)
+    //   C: O += V^T[:, 32:64] P1     |
+    auto tile_body = [&](auto masked_tag, auto buf_tag, int k0, int nxt) __attribute__((always_inline)) {
+      constexpr int BUF = decltype(buf_tag)::value;
+      const char* kb = (const char*)(BUF ? Ks1 : Ks0);
+      const char* vb = (const char*)(BUF ? Vs1 : Vs0);
+      const float* rabt = BUF ? rabs1 : rabs0;
+      const std::integral_constant<int, BUF ^ 1> other{};
+      const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      auto k_frag = [&](int kvb, int kk) __attribute__((always_inline)) {
+        return *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)((kk & 3) * 32)) + (kk >> 2) * 128);
+      };
+      auto v_frag = [&](int db, int s2) __attribute__((always_inline)) {
+        const char* a = vb + ((db & 1) ? vt_rd_o : vt_rd_e) + db * 64 + s2 * 16 * HD * 2;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)a);
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a + 8 * HD * 2));
+        const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return __builtin_bit_cast(bf16x8, both);
+      };
+      f32x16 s0, s1;
+      bf16x8 pb0, pb1, pb2, pb3;
+      // The 32 MFMAs of the block run as eight groups of four.  The LDS fragments of group g + 1 are
+      // fetched while group g computes (two alternating sets of four registers-quads), so that no
+      // MFMA waits for an LDS round trip; only the reads that open the tile are exposed.
+      //   groups 0,1: S0 (K rows 0..31)    groups 2,3: S1 (K rows 32..63)   | P0 = silu(S0) over 2,3
+      //   groups 4,5: O += V^T[:, 0:32] P0                                  | P1 = silu(S1) over 4,5
+      //   groups 6,7: O += V^T[:, 32:64] P1
+      auto load_group = [&](int g, bf16x8 (&f)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (g < 4) f[i] = k_frag(g >> 1, (g & 1) * 4 + i);
+          else f[i] = v_frag(((g & 1) * 2) + (i >> 1), ((g - 4) >> 1) * 2 + (i & 1));
+        }
+      };
+      auto mfma_group = [&](int g, const bf16x8 (&f)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (g < 2) {
+            const int kk = g * 4 + i;
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], qf[kk], kk == 0 ? zero : s0, 0, 0, 0);
+          } else if (g < 4) {
+            const int kk = (g - 2) * 4 + i;
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], qf[kk], kk == 0 ? zero : s1, 0, 0, 0);
+          } else {
+            const int db = ((g & 1) * 2) + (i >> 1);
+            const int s2 = ((g - 4) >> 1) * 2 + (i & 1);
+            const bf16x8& pb = s2 == 0 ? pb0 : (s2 == 1 ? pb1 : (s2 == 2 ? pb2 : pb3));
+            acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], pb, acc[db], 0, 0, 0);
+          }
+        }
+      };
+      bf16x8 fa[4], fb[4];
+      load_group(0, fa);
+      if (nxt < nkv) issue_tile(nxt, other);
+      load_group(1, fb);
+      mfma_group(0, fa);
+      __builtin_amdgcn_sched_barrier(0);
+      load_group(2, fa);
+      mfma_group(1, fb);
+      __builtin_amdgcn_sched_barrier(0);
+      // groups 2 and 3 with silu(S0)
+      load_group(3, fb);
+      mfma_group(2, fa);
+      silu_pack(masked_tag, s0, k0, 0, rabt, pb0, pb1);
+      load_group(4, fa);
+      mfma_group(3, fb);
+      // MFMAs issue in pairs: the second of a back-to-back pair costs less issue time than a lone one
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // fragment reads of group 3 (8 for V)
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // 10 VALU
+        __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);   // 8 transcendental
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);   // fragment reads of group 4
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+        __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // groups 4 and 5 with silu(S1)
+      load_group(5, fb);
+      mfma_group(4, fa);
+      silu_pack(masked_tag, s1, k0, 1, rabt, pb2, pb3);
+      load_group(6, fa);
+      mfma_group(5, fb);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+        __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+        __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      load_group(7, fb);
+      mfma_group(6, fa);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_group(7, fb);
+    };
+
+    auto compute_tile = [&](int it, auto buf_tag, int nxt) __attribute__((always_inline)) {
+      constexpr int BUF = decltype(buf_tag)::value;
+      const int k0 = it * BN;
+      const int k1 = k0 + BN;
+      // wave-level classification of this (32 query rows) x (64 keys) block
+      const bool any_kept = wave_has_rows && ((k0 <= m_hi && k1 > m_lo) /* diagonal crosses */ ||
+                                              (k0 < si.cap && k0 <= m_hi) /* causal history */ ||
+                                              (k0 < si.ctx_eff));
+      if (!any_kept) {
+        if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, BUF ^ 1>{});  // this wave still copies its share
+        return;
+      }
+      const bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
+      if (full) tile_body(std::false_type{}, buf_tag, k0, nxt);
+      else tile_body(std::true_type{}, buf_tag, k0, nxt);
+    };
+
+    if (it < nkv) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      // two tiles per trip so that the stage index is a compile-time constant
+      while (true) {
+        int nxt = next_tile(it);
+        compute_tile(it, std::integral_constant<int, 0>{}, nxt);
+        if (nxt >= nkv) break;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile nxt have landed
+        __syncthreads();                                   // ... and everybody's; tile it is no longer read
+        it = nxt;
+        nxt = next_tile(it);
+        compute_tile(it, std::integral_constant<int, 1>{}, nxt);
+        if (nxt >= nkv) break;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        it = nxt;
+      }
+    }
+
+    // ---- epilogue: O^T accumulators -> out[s + m, h, :] ----
+    if (m < si.n) {
+      float oscale = 1.0f / (float)p.N;
+      if (p.attn_scale)
+        oscale = (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) ? p.attn_scale[si.s + m] : p.attn_scale[0];
+      oscale *= 1.0f / kLog2e;
+      unsigned short* orow = (unsigned short*)p.out + ((size_t)(si.s + m) * p.H + h) * HD;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          u32x2 o;
+          o.x = pack_bf16x2(acc[db][4 * rq + 0] * oscale, acc[db][4 * rq + 1] * oscale);
+          o.y = pack_bf16x2(acc[db][4 * rq + 2] * oscale, acc[db][4 * rq + 3] * oscale);
+          *(u32x2*)(orow + db * 32 + 8 * rq + 4 * half) = o;
+        }
+      }
+    }
+    __syncthreads();  // LDS buffers are reused by the next item
+  }  // work items
+}
+
+}  // namespace recir_hstu

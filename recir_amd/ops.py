@@ -23,7 +23,8 @@ from . import _lib
 
 KERNEL_AUTO = 0
 KERNEL_GENERIC = 1
-KERNEL_TILED = 2
+KERNEL_TILED = 2         # tiled MFMA kernel, K/V staged through registers
+KERNEL_TILED_DIRECT = 3  # tiled MFMA kernel, K/V copied global -> LDS directly (the default)
 
 _forced_kernel = KERNEL_AUTO
 _ctx_reference_rule = False

@@ -94,9 +94,13 @@ def test_tiled_and_generic_kernels_agree(oracle, config):
     wl = make_jagged([300, 129, 64, 1, 0, 517], [40, 129, 0, 0, 0, 6], 2, 128, 128, max_seq_len=600,
                      alpha=1.0 / 128, dtype="bf16", seed=config, with_rab=(config == 3),
                      contextual_seq_len=8 if config == 3 else 0, tail_rows=7)
-    with ops.force_kernel(ops.KERNEL_TILED):
+    with ops.force_kernel(ops.KERNEL_TILED_DIRECT):
         a = run_hip(wl)
-        assert _lib.last_kernel().startswith("tiled_d128")
+        assert _lib.last_kernel().startswith("tiled_d128") and "regstage" not in _lib.last_kernel()
+    with ops.force_kernel(ops.KERNEL_TILED):
+        a2 = run_hip(wl)
+        assert "regstage" in _lib.last_kernel()
+    assert torch.equal(a, a2)  # same arithmetic in the same order: only the staging differs
     with ops.force_kernel(ops.KERNEL_GENERIC):
         b = run_hip(wl)
         assert _lib.last_kernel() == "generic_bf16"
@@ -108,7 +112,7 @@ def test_tiled_and_generic_kernels_agree(oracle, config):
     np.testing.assert_array_equal(za, zb)
 
 
-@pytest.mark.parametrize("kernel", ["tiled", "generic"])
+@pytest.mark.parametrize("kernel", ["tiled", "tiled_regstage", "generic"])
 @pytest.mark.parametrize("ctx", [0, 5, 200])
 def test_mask_is_bit_exact(oracle, kernel, ctx):
     """Positive constant scores and one-hot values make out[m, c] non-zero exactly when row m keeps a
@@ -127,7 +131,8 @@ def test_mask_is_bit_exact(oracle, kernel, ctx):
     for b, n in enumerate(lengths):
         for j in range(n):
             wl.v[off[b] + j, 0, j % 128] = 1.0
-    with ops.force_kernel(ops.KERNEL_TILED if kernel == "tiled" else ops.KERNEL_GENERIC):
+    variant = {"tiled": ops.KERNEL_TILED_DIRECT, "tiled_regstage": ops.KERNEL_TILED, "generic": ops.KERNEL_GENERIC}[kernel]
+    with ops.force_kernel(variant):
         out = run_hip(wl).float().cpu().numpy()
     want = np.zeros((wl.T, 128), dtype=bool)
     for b, (n, t) in enumerate(zip(lengths, targets)):
