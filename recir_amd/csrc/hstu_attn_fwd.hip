@@ -29,6 +29,63 @@ using namespace recir_hstu;
 
 namespace {
 
+// ---------------------------------------------------------------------------------------------
+// Per-head e4m3 quantiser: amax per head (bf16 magnitudes compare as integers), scale = amax / 448,
+// codes = e4m3(clamp(x / scale)).  Eight elements (16 bytes) per thread; D is a multiple of 8.
+// ---------------------------------------------------------------------------------------------
+__global__ void hstu_quant_clear(unsigned* amax_bits, int H) {
+  for (int h = threadIdx.x; h < H; h += blockDim.x) amax_bits[h] = 0u;
+}
+
+__global__ __launch_bounds__(256) void hstu_quant_amax(const u32x4* x, unsigned* amax_bits, size_t n8, int H, int D8) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+    const u32x4 v = x[i];
+    unsigned mx = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      mx = max(mx, (v[j] << 16) & 0x7fffffffu);
+      mx = max(mx, v[j] & 0x7fff0000u);
+    }
+    const int h = (int)((i / D8) % H);
+    // wave-level reduction when the whole wave sits in one head (D8 >= 64 is not required for correctness)
+    atomicMax(&amax_bits[h], mx);
+  }
+}
+
+__global__ void hstu_quant_finalize(float* scale, int H) {
+  for (int h = threadIdx.x; h < H; h += blockDim.x) {
+    const float amax = __uint_as_float(((unsigned*)scale)[h]);
+    scale[h] = fmaxf(amax, 1e-12f) / 448.0f;
+  }
+}
+
+__global__ __launch_bounds__(256) void hstu_quant_encode(const u32x4* x, u32x2* codes, const float* scale, size_t n8, int H, int D8) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+    const u32x4 v = x[i];
+    const float sc = scale[(i / D8) % H];
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      y[2 * j] = __uint_as_float(v[j] << 16) / sc;
+      y[2 * j + 1] = __uint_as_float(v[j] & 0xffff0000u) / sc;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = fminf(fmaxf(y[j], -448.0f), 448.0f);
+    u32x2 o;
+    int w = 0;
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], w, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
+    o.x = (unsigned)w;
+    w = 0;
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], w, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], w, true);
+    o.y = (unsigned)w;
+    codes[i] = o;
+  }
+}
+
 __global__ void hstu_fill_zero(unsigned short* out, size_t n2) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n2; i += stride) out[i] = 0;
@@ -213,10 +270,12 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     return RECIR_HSTU_OK;
   }
 
-  const bool tiled_ok = dtype == RECIR_HSTU_DTYPE_BF16 && Dqk == HD && Dv == HD &&
+  const bool fp8 = dtype == RECIR_HSTU_DTYPE_FP8_E4M3;
+  const bool tiled_ok = (dtype == RECIR_HSTU_DTYPE_BF16 || fp8) && Dqk == HD && Dv == HD &&
                         (((size_t)q | (size_t)k | (size_t)v | (size_t)out) & 15) == 0;
   bool use_tiled = tiled_ok;
-  if (variant == 1) use_tiled = false;
+  if (variant == 1 && !fp8) use_tiled = false;
+  if (fp8 && variant == 2) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "fp8 q/k runs on the direct-to-LDS tiled kernel only");
   if (variant >= 2 && !tiled_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "tiled kernel needs bf16, Dqk = Dv = 128 and 16-byte aligned tensors");
 
@@ -251,9 +310,15 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
       else hipLaunchKernelGGL((hstu_fwd_tiled_d128<false>), grid, dim3(256), 0, stream, p);
       g_last_kernel = rab ? "tiled_d128_bf16_regstage_rab" : "tiled_d128_bf16_regstage";
     } else {
-      if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<true>), grid, dim3(256), 0, stream, p);
-      else hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<false>), grid, dim3(256), 0, stream, p);
-      g_last_kernel = rab ? "tiled_d128_bf16_rab" : "tiled_d128_bf16";
+      if (dtype == RECIR_HSTU_DTYPE_FP8_E4M3) {
+        if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<true, true>), grid, dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<false, true>), grid, dim3(256), 0, stream, p);
+        g_last_kernel = rab ? "tiled_d128_fp8qk_rab" : "tiled_d128_fp8qk";
+      } else {
+        if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<true, false>), grid, dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<false, false>), grid, dim3(256), 0, stream, p);
+        g_last_kernel = rab ? "tiled_d128_bf16_rab" : "tiled_d128_bf16";
+      }
     }
     if (int rc = launch_status("hstu_fwd_tiled_d128")) return rc;
     return RECIR_HSTU_OK;
@@ -282,8 +347,28 @@ int recir_hstu_debug_trace(int block, void* host_dst) {
 
 int recir_hstu_quantize_e4m3_per_head(const void* x_bf16, void* codes_u8, float* scale, int32_t T,
                                       int32_t H, int32_t D, void* hip_stream) {
-  (void)x_bf16; (void)codes_u8; (void)scale; (void)T; (void)H; (void)D; (void)hip_stream;
-  return fail(RECIR_HSTU_ERR_UNSUPPORTED, "fp8 quantiser not built yet");
+  hipStream_t stream = (hipStream_t)hip_stream;
+  if (T < 0 || H <= 0 || D <= 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "bad sizes: T=%d H=%d D=%d", T, H, D);
+  if (!scale) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "scale must be non-null");
+  if (D % 8 != 0) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "D must be a multiple of 8, got %d", D);
+  if (T > 0 && (!x_bf16 || !codes_u8)) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "x and codes must be non-null");
+  if ((((size_t)x_bf16) & 15) || (((size_t)codes_u8) & 7))
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "x must be 16-byte and codes 8-byte aligned");
+  const size_t n8 = (size_t)T * H * (D / 8);
+  const unsigned blocks = (unsigned)((n8 + 255) / 256 < 4096 ? (n8 + 255) / 256 : 4096);
+  hipLaunchKernelGGL(hstu_quant_clear, dim3(1), dim3(256), 0, stream, (unsigned*)scale, H);
+  if (int rc = launch_status("hstu_quant_clear")) return rc;
+  if (n8 > 0) {
+    hipLaunchKernelGGL(hstu_quant_amax, dim3(blocks), dim3(256), 0, stream, (const u32x4*)x_bf16, (unsigned*)scale, n8, H, D / 8);
+    if (int rc = launch_status("hstu_quant_amax")) return rc;
+  }
+  hipLaunchKernelGGL(hstu_quant_finalize, dim3(1), dim3(256), 0, stream, scale, H);
+  if (int rc = launch_status("hstu_quant_finalize")) return rc;
+  if (n8 > 0) {
+    hipLaunchKernelGGL(hstu_quant_encode, dim3(blocks), dim3(256), 0, stream, (const u32x4*)x_bf16, (u32x2*)codes_u8, scale, n8, H, D / 8);
+    if (int rc = launch_status("hstu_quant_encode")) return rc;
+  }
+  return RECIR_HSTU_OK;
 }
 
 }  // extern "C"

@@ -35,7 +35,13 @@ typedef __attribute__((ext_vector_type(8))) short i16x8;
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-template <bool HAS_RAB>
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+
+// FP8: q and k are OCP e4m3 bytes ([T, H, 128] of one byte each) with per-head dequantisation factors;
+// the scores come from v_mfma_scale_f32_32x32x64_f8f6f4 (two per 32 x 32 block, unit block scales) and
+// are multiplied by alpha * q_scale[h] * k_scale[h] * log2(e) in fp32; v, P and the second
+// contraction stay bf16.  The K tile is then [BN rows][128 bytes], chunk c of row r at c ^ (r & 7).
+template <bool HAS_RAB, bool FP8>
 __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
   // The two pipeline stages are separate objects and every access names its stage at compile time:
   // the compiler then knows that an LDS read of one stage cannot alias the global -> LDS copies in
@@ -72,7 +78,15 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
   // global -> LDS copies: instruction j of a tile (16 per matrix, wave w issues j = 4 w + ps) fills rows
   // 4 j .. 4 j + 3; lane i lands at row 4 j + (i >> 4), physical chunk i & 15
   const int ld_row = lane >> 4, ld_chunk = lane & 15;
+  // fp8 K: fragment = 32 bytes at row 32 kvb + l32, chunks (4 st + 2 half + {0, 1}) ^ (l32 & 7); a copy
+  // instruction fills 8 rows of 128 bytes, lane i lands at row 8 j + (i >> 3), physical chunk i & 7
+  const unsigned k8_rd = (unsigned)l32 * 128u + (unsigned)(((2 * half) ^ (l32 & 7)) * 16);
+  const int ld8_row = lane >> 3, ld8_chunk = lane & 7;
 
+#ifdef HSTU_TRACE
+  const bool trace_on = (int)blockIdx.x == g_trace_block;
+  int trace_it = 0;
+#endif
   // Work list of the XCD this workgroup runs on.  Normally one item per workgroup; the stride loop
   // only matters when a list is longer than the launch assumed (sequences above max_seq_len).
   const int xcd = blockIdx.x % NUM_XCD;
@@ -85,8 +99,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     const int q0 = wi.q0;
     const int h = wi.h;
 
-    const unsigned row_bytes = (unsigned)p.H * HD * 2u;
-    const char* __restrict__ kgb = (const char*)p.k + ((size_t)si.s * p.H + h) * (HD * 2);
+    const unsigned row_bytes = (unsigned)p.H * HD * 2u;                   // bf16 rows (v, and k unless FP8)
+    const unsigned krow_bytes = FP8 ? (unsigned)p.H * HD : row_bytes;
+    const char* __restrict__ kgb = (const char*)p.k + ((size_t)si.s * p.H + h) * (FP8 ? HD : HD * 2);
     const char* __restrict__ vgb = (const char*)p.v + ((size_t)si.s * p.H + h) * (HD * 2);
     const int rab_w = 2 * p.N - 1;
     const float* __restrict__ rabg = HAS_RAB ? p.rab + (size_t)h * rab_w : nullptr;
@@ -95,6 +110,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     const unsigned k_off_e = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ ld_row) * 16);        // rows 8a + 0..3
     const unsigned k_off_o = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ (4 + ld_row)) * 16);  // rows 8a + 4..7
     const unsigned v_off = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ (2 * ld_row)) * 16);
+    const unsigned k8_off = (unsigned)ld8_row * krow_bytes + (unsigned)((ld8_chunk ^ ld8_row) * 16);
 
     const int qw0 = q0 + wave * 32;
     const int m = qw0 + l32;
@@ -120,7 +136,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       unsigned short* Vd = BUF ? Vs1 : Vs0;
       float* rabd = BUF ? rabs1 : rabs0;
       const int k0 = it * BN;
-      const char* kt = kgb + (size_t)k0 * row_bytes;
+      const char* kt = kgb + (size_t)k0 * krow_bytes;
       const char* vt = vgb + (size_t)k0 * row_bytes;
       const bool whole = k0 + BN <= si.n;
       const int last = si.n - 1 - k0;
@@ -129,18 +145,32 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         const int r0 = 4 * (4 * wave + ps);  // first row this instruction fills
         unsigned ko = (ps & 1) ? k_off_o : k_off_e;
         unsigned vo = v_off;
-        const char* kr = kt + (size_t)r0 * row_bytes;
+        const char* kr = kt + (size_t)r0 * krow_bytes;
         const char* vr = vt + (size_t)r0 * row_bytes;
         if (!whole) {
           asm volatile("" ::: "memory");  // keep the clamping arithmetic off the steady-state path
           const int row = min(r0 + ld_row, last);
-          ko = (unsigned)row * row_bytes + (unsigned)((ld_chunk ^ ((r0 + ld_row) & 7)) * 16);
+          ko = (unsigned)row * krow_bytes + (unsigned)((ld_chunk ^ ((r0 + ld_row) & 7)) * 16);
           vo = (unsigned)row * row_bytes + (unsigned)((ld_chunk ^ (2 * ld_row)) * 16);
           kr = kt;
           vr = vt;
         }
-        __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)&Kd[r0 * HD], 16, 0, 0);
+        if (!FP8) __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)&Kd[r0 * HD], 16, 0, 0);
         __builtin_amdgcn_global_load_lds((const unsigned*)(vr + vo), (lds_void*)&Vd[r0 * HD], 16, 0, 0);
+      }
+      if (FP8) {
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps) {
+          const int r0 = 8 * (2 * wave + ps);
+          unsigned ko = k8_off;
+          const char* kr = kt + (size_t)r0 * krow_bytes;
+          if (!whole) {
+            asm volatile("" ::: "memory");
+            ko = (unsigned)min(r0 + ld8_row, last) * krow_bytes + (unsigned)((ld8_chunk ^ ld8_row) * 16);
+            kr = kt;
+          }
+          __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)((char*)Kd + r0 * 128), 16, 0, 0);
+        }
       }
       if (HAS_RAB) {
         // band of bias entries this (q tile, kv tile) can touch: index (m - j) + N - 1, staged
@@ -155,25 +185,41 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     int it = (has_skip && skip_a == 0) ? skip_b : 0;
     if (it < nkv) issue_tile(it, std::integral_constant<int, 0>{});
 
-    // ---- Q fragments (B operand): lane holds row qw0 + l32, d = 16 kk + 8 half .. +7 ----
-    bf16x8 qf[8];
+    // ---- Q fragments (B operand): lane holds row qw0 + l32 ----
+    // bf16: d = 16 kk + 8 half .. +7, pre-multiplied by alpha * log2(e) and rounded back to bf16
+    // fp8 : d = 64 st + 32 half .. +31 (raw bytes); the factor goes onto the fp32 scores instead
+    bf16x8 qf[FP8 ? 1 : 8];
+    i32x8 q8[FP8 ? 2 : 1];
+    float s_mul = 1.0f;  // fp8: alpha * q_scale[h] * k_scale[h] * log2(e)
     {
       const bool valid = m < si.n;
-      const unsigned short* qrow = (const unsigned short*)p.q + ((size_t)(si.s + (valid ? m : 0)) * p.H + h) * HD;
-      const float qmul = p.alpha * kLog2e;
-      u32x4 t[8];
+      if constexpr (FP8) {
+        s_mul = p.alpha * p.q_scale[h] * p.k_scale[h] * kLog2e;
+        const char* qrow = (const char*)p.q + ((size_t)(si.s + (valid ? m : 0)) * p.H + h) * HD;
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const u32x4 zero4 = {0u, 0u, 0u, 0u};
-        t[kk] = valid ? *(const u32x4*)(qrow + kk * 16 + half * 8) : zero4;
-      }
+        for (int st = 0; st < 2; ++st) {
+          const u32x4 zero4 = {0u, 0u, 0u, 0u};
+          const u32x4 lo = valid ? *(const u32x4*)(qrow + 64 * st + 32 * half) : zero4;
+          const u32x4 hi = valid ? *(const u32x4*)(qrow + 64 * st + 32 * half + 16) : zero4;
+          q8[st] = (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+      } else {
+        const unsigned short* qrow = (const unsigned short*)p.q + ((size_t)(si.s + (valid ? m : 0)) * p.H + h) * HD;
+        const float qmul = p.alpha * kLog2e;
+        u32x4 t[8];
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        u32x4 sc;
+        for (int kk = 0; kk < 8; ++kk) {
+          const u32x4 zero4 = {0u, 0u, 0u, 0u};
+          t[kk] = valid ? *(const u32x4*)(qrow + kk * 16 + half * 8) : zero4;
+        }
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          sc[i] = pack_bf16x2(__uint_as_float(t[kk][i] << 16) * qmul, __uint_as_float(t[kk][i] & 0xffff0000u) * qmul);
-        qf[kk] = __builtin_bit_cast(bf16x8, sc);
+        for (int kk = 0; kk < 8; ++kk) {
+          u32x4 sc;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            sc[i] = pack_bf16x2(__uint_as_float(t[kk][i] << 16) * qmul, __uint_as_float(t[kk][i] & 0xffff0000u) * qmul);
+          qf[kk] = __builtin_bit_cast(bf16x8, sc);
+        }
       }
     }
 
@@ -192,6 +238,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       for (int r = 0; r < 16; ++r) {
         const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
         float s = sv[r];
+        if (FP8) s *= s_mul;
         if (HAS_RAB) s += rabt[(m - q0) - jl + (BN - 1)];
         const float ex = __builtin_amdgcn_exp2f(-s);
         float pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
@@ -255,11 +302,11 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           if (g < 2) {
-            const int kk = g * 4 + i;
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], qf[kk], kk == 0 ? zero : s0, 0, 0, 0);
+            const int kk = FP8 ? 0 : g * 4 + i;
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], qf[kk], (g * 4 + i) == 0 ? zero : s0, 0, 0, 0);
           } else if (g < 4) {
-            const int kk = (g - 2) * 4 + i;
-            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], qf[kk], kk == 0 ? zero : s1, 0, 0, 0);
+            const int kk = FP8 ? 0 : (g - 2) * 4 + i;
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], qf[kk], ((g - 2) * 4 + i) == 0 ? zero : s1, 0, 0, 0);
           } else {
             const int db = ((g & 1) * 2) + (i >> 1);
             const int s2 = ((g - 4) >> 1) * 2 + (i & 1);
@@ -269,6 +316,26 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         }
       };
       bf16x8 fa[4], fb[4];
+      if constexpr (FP8) {
+        // scores: two K = 64 MFMAs per 32 x 32 block; fragment = two 16-byte reads
+        auto k8_frag = [&](int kvb, int st) __attribute__((always_inline)) {
+          const char* a = kb + kvb * 32 * 128;
+          const u32x4 lo = *(const u32x4*)(a + (k8_rd ^ (unsigned)((4 * st) * 16)));
+          const u32x4 hi = *(const u32x4*)(a + (k8_rd ^ (unsigned)((4 * st + 1) * 16)));
+          return (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        };
+        const i32x8 ka0 = k8_frag(0, 0), ka1 = k8_frag(0, 1);
+        if (nxt < nkv) issue_tile(nxt, other);
+        const i32x8 kb0 = k8_frag(1, 0), kb1 = k8_frag(1, 1);
+        s0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ka0, q8[0], zero, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+        s0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ka1, q8[1], s0, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+        HSTU_STAMP(1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_group(4, fa);
+        s1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kb0, q8[0], zero, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+        s1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kb1, q8[1], s1, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+        silu_pack(masked_tag, s0, k0, 0, rabt, pb0, pb1);
+      } else {
       load_group(0, fa);
       if (nxt < nkv) issue_tile(nxt, other);
       load_group(1, fb);
@@ -276,6 +343,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       __builtin_amdgcn_sched_barrier(0);
       load_group(2, fa);
       mfma_group(1, fb);
+      HSTU_STAMP(1);
       __builtin_amdgcn_sched_barrier(0);
       // groups 2 and 3 with silu(S0)
       load_group(3, fb);
@@ -298,6 +366,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
         __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);
       }
+      }
+      HSTU_STAMP(2);
       __builtin_amdgcn_sched_barrier(0);
       // groups 4 and 5 with silu(S1)
       load_group(5, fb);
@@ -319,6 +389,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
         __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);
       }
+      HSTU_STAMP(3);
       __builtin_amdgcn_sched_barrier(0);
       load_group(7, fb);
       mfma_group(6, fa);
@@ -349,16 +420,32 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       // two tiles per trip so that the stage index is a compile-time constant
       while (true) {
         int nxt = next_tile(it);
+        HSTU_STAMP(0);
         compute_tile(it, std::integral_constant<int, 0>{}, nxt);
+        HSTU_STAMP(4);
         if (nxt >= nkv) break;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile nxt have landed
+        HSTU_STAMP(5);
         __syncthreads();                                   // ... and everybody's; tile it is no longer read
+        HSTU_STAMP(6);
+        HSTU_STAMP(7);
+#ifdef HSTU_TRACE
+        ++trace_it;
+#endif
         it = nxt;
         nxt = next_tile(it);
+        HSTU_STAMP(0);
         compute_tile(it, std::integral_constant<int, 1>{}, nxt);
+        HSTU_STAMP(4);
         if (nxt >= nkv) break;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        HSTU_STAMP(5);
         __syncthreads();
+        HSTU_STAMP(6);
+        HSTU_STAMP(7);
+#ifdef HSTU_TRACE
+        ++trace_it;
+#endif
         it = nxt;
       }
     }

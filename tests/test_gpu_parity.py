@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from tests.golden.cases import SMALL_CASES, build_inputs
-from tests.parity_util import (FP32_ATOL, FP32_RTOL, assert_bf16_close, assert_same_zero_structure,
+from tests.parity_util import (FP8_MAX_ABS, FP32_ATOL, FP32_RTOL, assert_bf16_close, assert_same_zero_structure,
                                error_stats, run_hip, run_oracle, to_device)
 
 pytestmark = pytest.mark.gpu
@@ -304,3 +304,58 @@ def test_runs_on_the_callers_stream():
         out = recir_amd.jagged_hstu_attention(q, k, v, off, nt, max_seq_len=2048, alpha=wl.alpha)
     s.synchronize()
     assert torch.equal(out, base)
+
+
+def test_fp8_quantiser_is_bit_exact(oracle):
+    """Per-head scales and e4m3 codes against the C restatement of the reference recipe
+    (kjt_split_per_feature.cpp:493-502), which is itself pinned to torch's float8_e4m3fn cast."""
+    import recir_amd
+
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(301, 3, 128, generator=g) * torch.tensor([0.05, 1.0, 40.0]).view(1, 3, 1)).bfloat16()
+    x[5, 1, 7] = 0.0
+    codes, scale = recir_amd.quantize_e4m3_per_head(x.cuda())
+    want_codes, want_scale = oracle.quant_e4m3_per_head(x.float().numpy())
+    np.testing.assert_array_equal(scale.cpu().numpy(), want_scale)
+    np.testing.assert_array_equal(codes.view(torch.uint8).cpu().numpy(), want_codes)
+    assert codes.dtype == torch.float8_e4m3fn
+
+
+def _fp8_reference(oracle, wl):
+    """fp32 oracle on the dequantised q, k: S = alpha * sq[h] * sk[h] * (Q8 . K8^T)."""
+    q8, qs = oracle.quant_e4m3_per_head(wl.q.numpy())
+    k8, ks = oracle.quant_e4m3_per_head(wl.k.numpy())
+    qd = torch.from_numpy(oracle.e4m3_decode(q8) * qs.reshape(1, -1, 1))
+    kd = torch.from_numpy(oracle.e4m3_decode(k8) * ks.reshape(1, -1, 1))
+    return run_oracle(oracle, wl, q=qd, k=kd)
+
+
+@pytest.mark.parametrize("with_rab", [False, True])
+def test_fp8_small_case(oracle, with_rab):
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([300, 129, 64, 1, 0, 517], [40, 129, 0, 0, 0, 6], 2, 128, 128, max_seq_len=600,
+                     alpha=1.0 / 128, dtype="fp8", seed=21, with_rab=with_rab, rab_std=0.3,
+                     contextual_seq_len=8 if with_rab else 0, tail_rows=5)
+    out = run_hip(wl, fp8=True)
+    assert _lib.last_kernel().startswith("tiled_d128_fp8qk")
+    # against the same quantised operands: only bf16-level differences remain
+    assert_bf16_close(out, _fp8_reference(oracle, wl), "fp8 vs dequantised oracle")
+    # against the unquantised fp32 reference: the stated fp8 tolerance
+    st = error_stats(out, run_oracle(oracle, wl))
+    assert st["max_abs"] <= FP8_MAX_ABS, st
+    assert not out[int(wl.seq_offsets[-1]):].any()
+
+
+def test_config5_fp8_matches_oracle(oracle):
+    from recir_amd.workloads import make_config
+
+    wl = make_config(5)
+    out = run_hip(wl, fp8=True)
+    st_q = assert_bf16_close(out, _fp8_reference(oracle, wl), "config5 vs dequantised oracle")
+    st = error_stats(out, run_oracle(oracle, wl))
+    print("config5 vs dequantised:", st_q, " vs fp32 reference:", st)
+    assert st["max_abs"] <= FP8_MAX_ABS, st
+    assert st["rel_fro"] <= 5e-2, st  # relative form of the same bound (outputs are O(1e-3))
+    assert_same_zero_structure(out, run_oracle(oracle, wl), int(wl.seq_offsets[-1]))
