@@ -100,6 +100,14 @@ size_t recir_hstu_attn_fwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int3
 int recir_hstu_quantize_e4m3_per_head(const void* x_bf16, void* codes_u8, float* scale, int32_t T,
                                       int32_t H, int32_t D, void* hip_stream);
 
+/*
+ * Measurement aid, no counterpart in the reference: a plain device-to-device copy of `bytes` bytes
+ * (multiple of 16, both pointers 16-byte aligned) by one kernel.  Hardware counters that are read
+ * for the attention kernel (FETCH_SIZE, WRITE_SIZE) are scaled by what they read for this copy,
+ * whose traffic is known exactly.
+ */
+int recir_hstu_calibration_copy(void* dst, const void* src, size_t bytes, void* hip_stream);
+
 /* Thread-local, NUL-terminated description of the last non-zero status on this thread. */
 const char* recir_hstu_last_error(void);
 

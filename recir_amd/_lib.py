@@ -24,6 +24,7 @@ EXPORTS = (
     "recir_hstu_attn_fwd",
     "recir_hstu_attn_fwd_workspace_bytes",
     "recir_hstu_quantize_e4m3_per_head",
+    "recir_hstu_calibration_copy",
     "recir_hstu_last_error",
     "recir_hstu_abi_version",
     "recir_hstu_last_kernel",
@@ -54,6 +55,8 @@ def load() -> ctypes.CDLL:
     L.recir_hstu_attn_fwd_workspace_bytes.restype = sz
     L.recir_hstu_quantize_e4m3_per_head.argtypes = [vp, vp, vp, i32, i32, i32, vp]
     L.recir_hstu_quantize_e4m3_per_head.restype = ctypes.c_int
+    L.recir_hstu_calibration_copy.argtypes = [vp, vp, sz, vp]
+    L.recir_hstu_calibration_copy.restype = ctypes.c_int
     L.recir_hstu_last_error.argtypes = []
     L.recir_hstu_last_error.restype = ctypes.c_char_p
     L.recir_hstu_last_kernel.argtypes = []

@@ -86,6 +86,11 @@ __global__ __launch_bounds__(256) void hstu_quant_encode(const u32x4* x, u32x2* 
   }
 }
 
+__global__ __launch_bounds__(256) void hstu_calibration_copy(u32x4* dst, const u32x4* src, size_t n16) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
 __global__ void hstu_fill_zero(unsigned short* out, size_t n2) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n2; i += stride) out[i] = 0;
@@ -344,6 +349,15 @@ int recir_hstu_debug_trace(int block, void* host_dst) {
   return (int)hipMemcpyToSymbol(HIP_SYMBOL(recir_hstu::g_trace_block), &block, sizeof(int));
 }
 #endif
+
+int recir_hstu_calibration_copy(void* dst, const void* src, size_t bytes, void* hip_stream) {
+  if (!dst || !src || (bytes & 15) || (((size_t)dst | (size_t)src) & 15))
+    return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "calibration copy needs 16-byte aligned pointers and size");
+  if (bytes == 0) return RECIR_HSTU_OK;
+  hipLaunchKernelGGL(hstu_calibration_copy, dim3(4096), dim3(256), 0, (hipStream_t)hip_stream, (u32x4*)dst,
+                     (const u32x4*)src, bytes / 16);
+  return launch_status("hstu_calibration_copy");
+}
 
 int recir_hstu_quantize_e4m3_per_head(const void* x_bf16, void* codes_u8, float* scale, int32_t T,
                                       int32_t H, int32_t D, void* hip_stream) {
