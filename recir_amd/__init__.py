@@ -15,6 +15,7 @@ from .ops import (  # noqa: F401
     KERNEL_GENERIC,
     KERNEL_TILED,
     KERNEL_TILED_DIRECT,
+    KERNEL_TILED_W64,
 )
 
 __all__ = [

@@ -24,6 +24,7 @@
 #include "hstu_plan.h"
 #include "hstu_tiled_d128.h"
 #include "hstu_tiled_d128_dl.h"
+#include "hstu_tiled_d128_w64.h"
 
 using namespace recir_hstu;
 
@@ -293,23 +294,40 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     p.ws_counts = (int*)workspace;
     p.ws_items = (WorkItem*)((char*)workspace + WS_HEADER);
     p.items_cap = (int)items;
+    // query rows per workgroup: 256 for the 64-rows-per-wave kernel, else 128
+    const bool w64 = variant == 4;
+    const int bm = w64 ? BM2 : BM;
     // slots per XCD the launch covers: an even share of the items plus the imbalance the dealing of
     // whole (sequence, head) pairs can leave (about one sequence's worth of tiles); longer lists,
     // possible only with sequences above max_seq_len, are walked by the workgroups' stride loop
-    const size_t per_seq = (size_t)(max_seq_len + BM - 1) / BM;
-    size_t slots = (items + NUM_XCD - 1) / NUM_XCD + 2 * per_seq + 1;
-    if (slots > items) slots = items;
+    const size_t per_seq = (size_t)(max_seq_len + bm - 1) / bm;
+    const size_t items_bm = ((size_t)((T + bm - 1) / bm) + (size_t)B) * (size_t)H;
+    size_t slots = (items_bm + NUM_XCD - 1) / NUM_XCD + 2 * per_seq + 1;
+    if (slots > items_bm) slots = items_bm;
     if (slots < 1) slots = 1;
     if (items > 0x7fffffffull || slots * NUM_XCD > 0x7fffffffull) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "grid too large");
     p.grid_slots = (int)slots;
     if (!(flags & RECIR_HSTU_FLAG_REUSE_PLAN)) {
       if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS)
-        hipLaunchKernelGGL(hstu_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, p, BM);
+        hipLaunchKernelGGL(hstu_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, p, bm);
       else
-        hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, p, BM);
+        hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, p, bm);
       if (int rc = launch_status("hstu_plan_kernel")) return rc;
     }
     const dim3 grid((unsigned)(slots * NUM_XCD));
+    if (w64) {
+      if (dtype == RECIR_HSTU_DTYPE_FP8_E4M3) {
+        if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_w64<true, true>), grid, dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((hstu_fwd_tiled_d128_w64<false, true>), grid, dim3(256), 0, stream, p);
+        g_last_kernel = rab ? "tiled_d128_w64_fp8qk_rab" : "tiled_d128_w64_fp8qk";
+      } else {
+        if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_w64<true, false>), grid, dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((hstu_fwd_tiled_d128_w64<false, false>), grid, dim3(256), 0, stream, p);
+        g_last_kernel = rab ? "tiled_d128_w64_bf16_rab" : "tiled_d128_w64_bf16";
+      }
+      if (int rc = launch_status("hstu_fwd_tiled_d128_w64")) return rc;
+      return RECIR_HSTU_OK;
+    }
     if (variant == 2) {  // register-staged tiles (kept for comparison and tiling-invariance tests)
       if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128<true>), grid, dim3(256), 0, stream, p);
       else hipLaunchKernelGGL((hstu_fwd_tiled_d128<false>), grid, dim3(256), 0, stream, p);

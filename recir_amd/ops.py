@@ -24,7 +24,8 @@ from . import _lib
 KERNEL_AUTO = 0
 KERNEL_GENERIC = 1
 KERNEL_TILED = 2         # tiled MFMA kernel, K/V staged through registers
-KERNEL_TILED_DIRECT = 3  # tiled MFMA kernel, K/V copied global -> LDS directly (the default)
+KERNEL_TILED_DIRECT = 3  # tiled MFMA kernel, K/V copied global -> LDS directly
+KERNEL_TILED_W64 = 4     # tiled MFMA kernel, 64 query rows per wave, four-stage LDS ring
 
 _forced_kernel = KERNEL_AUTO
 _ctx_reference_rule = False

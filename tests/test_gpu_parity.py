@@ -101,6 +101,13 @@ def test_tiled_and_generic_kernels_agree(oracle, config):
         a2 = run_hip(wl)
         assert "regstage" in _lib.last_kernel()
     assert torch.equal(a, a2)  # same arithmetic in the same order: only the staging differs
+    with ops.force_kernel(ops.KERNEL_TILED_W64):
+        a3 = run_hip(wl)
+        assert "w64" in _lib.last_kernel()
+    if config == 3:  # the bias is added with one fused multiply-add there: last-bit differences
+        assert error_stats(a3, a.float().cpu().numpy())["rel_to_max"] <= 2 ** -7
+    else:
+        assert torch.equal(a, a3)  # 64 rows per wave: same per-row arithmetic again
     with ops.force_kernel(ops.KERNEL_GENERIC):
         b = run_hip(wl)
         assert _lib.last_kernel() == "generic_bf16"
@@ -112,7 +119,7 @@ def test_tiled_and_generic_kernels_agree(oracle, config):
     np.testing.assert_array_equal(za, zb)
 
 
-@pytest.mark.parametrize("kernel", ["tiled", "tiled_regstage", "generic"])
+@pytest.mark.parametrize("kernel", ["tiled", "tiled_regstage", "tiled_w64", "generic"])
 @pytest.mark.parametrize("ctx", [0, 5, 200])
 def test_mask_is_bit_exact(oracle, kernel, ctx):
     """Positive constant scores and one-hot values make out[m, c] non-zero exactly when row m keeps a
@@ -131,7 +138,7 @@ def test_mask_is_bit_exact(oracle, kernel, ctx):
     for b, n in enumerate(lengths):
         for j in range(n):
             wl.v[off[b] + j, 0, j % 128] = 1.0
-    variant = {"tiled": ops.KERNEL_TILED_DIRECT, "tiled_regstage": ops.KERNEL_TILED, "generic": ops.KERNEL_GENERIC}[kernel]
+    variant = {"tiled": ops.KERNEL_TILED_DIRECT, "tiled_regstage": ops.KERNEL_TILED, "tiled_w64": ops.KERNEL_TILED_W64, "generic": ops.KERNEL_GENERIC}[kernel]
     with ops.force_kernel(variant):
         out = run_hip(wl).float().cpu().numpy()
     want = np.zeros((wl.T, 128), dtype=bool)
@@ -359,3 +366,18 @@ def test_config5_fp8_matches_oracle(oracle):
     assert st["max_abs"] <= FP8_MAX_ABS, st
     assert st["rel_fro"] <= 5e-2, st  # relative form of the same bound (outputs are O(1e-3))
     assert_same_zero_structure(out, run_oracle(oracle, wl), int(wl.seq_offsets[-1]))
+
+
+@pytest.mark.parametrize("config", [2, 3, 4, 5])
+def test_w64_kernel_full_size(oracle, config):
+    """The 64-rows-per-wave kernel on the full-size configurations, against the oracle."""
+    from recir_amd import _lib, ops
+    from recir_amd.workloads import make_config
+
+    wl = make_config(config)
+    with ops.force_kernel(ops.KERNEL_TILED_W64):
+        out = run_hip(wl, fp8=(config == 5))
+    assert "w64" in _lib.last_kernel()
+    ref = _fp8_reference(oracle, wl) if config == 5 else run_oracle(oracle, wl)
+    assert_bf16_close(out, ref, f"w64 config{config}")
+    assert_same_zero_structure(out, ref, int(wl.seq_offsets[-1]))
