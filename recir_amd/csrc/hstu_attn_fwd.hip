@@ -362,6 +362,9 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
 
 #ifdef HSTU_TRACE
 // Debug build only (never part of the shipped library): select the traced workgroup / read stamps.
+int recir_hstu_debug_item_trace(void* host_dst) {
+  return (int)hipMemcpyFromSymbol(host_dst, HIP_SYMBOL(recir_hstu::g_item_trace), sizeof(recir_hstu::g_item_trace));
+}
 int recir_hstu_debug_trace(int block, void* host_dst) {
   if (host_dst) return (int)hipMemcpyFromSymbol(host_dst, HIP_SYMBOL(recir_hstu::g_trace), sizeof(recir_hstu::g_trace));
   return (int)hipMemcpyToSymbol(HIP_SYMBOL(recir_hstu::g_trace_block), &block, sizeof(int));

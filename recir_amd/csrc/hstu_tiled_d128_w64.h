@@ -27,15 +27,34 @@
 
 namespace recir_hstu {
 
+#ifndef W64_ABL
+#define W64_ABL 0   // debug builds only: bit mask of parts to leave out (timing experiments)
+#endif
+#ifdef HSTU_TRACE
+// Debug build only: wall-clock stamps (100 MHz) of the phases of every workgroup's first item.
+__device__ unsigned long long g_item_trace[4096 * 4 * 8];
+#define W64_ITEM_STAMP(k)                                                                      \
+  do {                                                                                         \
+    __builtin_amdgcn_sched_barrier(0);                                                         \
+    if (lane == 0 && blockIdx.x < 4096 && slot == (int)(blockIdx.x / NUM_XCD))                 \
+      g_item_trace[(blockIdx.x * 4 + wave) * 8 + (k)] = wall_clock64();                        \
+    __builtin_amdgcn_sched_barrier(0);                                                         \
+  } while (0)
+#else
+#define W64_ITEM_STAMP(k) do { } while (0)
+#endif
 constexpr int BM2 = 256;     // query rows per workgroup
 constexpr int W64_STAGES = 4;
+constexpr bool W64_Q_IN_ACC = false;
 constexpr int W64_DIST = 3;  // tiles of prefetch distance
 
 // one global -> LDS copy of 64 lanes x 16 bytes; lds_addr is wave-uniform
 __device__ __forceinline__ void dma16(const void* gbase, unsigned voff, unsigned lds_addr) {
+  if (W64_ABL & 8) return;
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_addr), "v"(voff), "s"(gbase) : "memory");
 }
 __device__ __forceinline__ void dma4(const void* gbase, unsigned voff, unsigned lds_addr) {
+  if (W64_ABL & 8) return;
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_addr), "v"(voff), "s"(gbase) : "memory");
 }
 
@@ -70,10 +89,15 @@ __global__ __launch_bounds__(256, 1) void hstu_fwd_tiled_d128_w64(Params p) {
   const unsigned v_lds0 = (unsigned)(size_t)&Vring[0][0];
   const unsigned r_lds0 = (unsigned)(size_t)&rab_ring[0][0];
 
+#ifdef HSTU_TRACE
+  const bool trace_on = (int)blockIdx.x == g_trace_block;
+  int trace_it = 0;
+#endif
   const int xcd = blockIdx.x % NUM_XCD;
   const int list_len = p.ws_counts[xcd];
   const WorkItem* __restrict__ list = p.ws_items + (size_t)xcd * p.items_cap;
   for (int slot = blockIdx.x / NUM_XCD; slot < list_len; slot += p.grid_slots) {
+    W64_ITEM_STAMP(0);
     const WorkItem wi = list[slot];
     SeqInfo si;
     si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
@@ -205,14 +229,19 @@ __global__ __launch_bounds__(256, 1) void hstu_fwd_tiled_d128_w64(Params p) {
             sc[i] = pack_bf16x2(__uint_as_float(t[i] << 16) * qmul, __uint_as_float(t[i] & 0xffff0000u) * qmul);
           qf[qb][kk] = __builtin_bit_cast(bf16x8, sc);
           // Q is only ever an MFMA operand from here on: park it in the accumulation register file
-          asm volatile("" : "+a"(qf[qb][kk]));
+          if (W64_Q_IN_ACC) asm volatile("" : "+a"(qf[qb][kk]));
         }
       }
     }
     // the q loads above are ordinary vector loads issued after the first copies: once their data
     // has been used, everything issued before them has landed as well.  Make that explicit so the
     // counting below starts from a known state.
+    W64_ITEM_STAMP(1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    W64_ITEM_STAMP(2);
+#ifdef HSTU_TRACE
+    const long long trace_c2 = clock64();
+#endif
 
     f32x16 acc[2][4];
 #pragma unroll
@@ -221,6 +250,12 @@ __global__ __launch_bounds__(256, 1) void hstu_fwd_tiled_d128_w64(Params p) {
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[qb][i][r] = 0.f;
+    // the output accumulators are only ever MFMA operands until the epilogue: start them out in
+    // the accumulation register file
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) asm volatile("" : "+a"(acc[qb][db]));
 
     // silu + mask + bf16 packing of one 32 x 32 score block into two B operands
     auto silu_pack = [&](auto masked_tag, const f32x16& sv, int m, int k0, int kvb, const float* rabt,
@@ -385,6 +420,101 @@ __global__ __launch_bounds__(256, 1) void hstu_fwd_tiled_d128_w64(Params p) {
       mfma_group(7, fb);
     };
 
+    // bf16 path: one (64 query rows) x (64 keys) block as 64 slots of one MFMA each, in program
+    // order (a scheduling barrier closes every slot), with the LDS reads and the SiLU work of
+    // other blocks placed into the slots by hand:
+    //   slots  0..7   S0a = K[0:32] Qa^T     8..15  S0b = K[0:32] Qb^T      (a, b: the two row blocks)
+    //   slots 16..23  S1a = K[32:64] Qa^T   24..31  S1b = K[32:64] Qb^T
+    //   slots 32..39  Oa += V^T[:, 0:32] P0a    40..47  Ob += V^T[:, 0:32] P0b
+    //   slots 48..55  Oa += V^T[:, 32:64] P1a   56..63  Ob += V^T[:, 32:64] P1b
+    // Each fragment is read once and feeds both row blocks: buffer FA holds K[0:32] (slots 0..15),
+    // then V^T[:, 0:32] (32..47); FB holds K[32:64] (16..31), then V^T[:, 32:64] (48..63).
+    // The 32 SiLU units (two scores each, in the order S0a S0b S1a S1b) are spread over slots
+    // 10..55, which keeps every unit after the MFMA chain that produces its scores and before the
+    // MFMA that consumes its packed result.
+    auto tile_body_slots = [&](auto masked_tag, int k0, int st) __attribute__((always_inline)) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      const char* kb = (const char*)&Kring[0][0] + st * (BN * HD * 2);
+      const char* vb = (const char*)&Vring[0][0] + st * (BN * HD * 2);
+      const float* rabt = &rab_ring[0][0] + (HAS_RAB ? st * RAB_BAND : 0);
+      const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      auto k_frag = [&](int kvb, int kk) __attribute__((always_inline)) {
+        return *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)((kk & 3) * 32)) + (kk >> 2) * 128);
+      };
+      auto v_frag = [&](int db, int s2) __attribute__((always_inline)) {
+        const char* a = vb + ((db & 1) ? vt_rd_o : vt_rd_e) + db * 64 + s2 * 16 * HD * 2;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)a);
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a + 8 * HD * 2));
+        const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return __builtin_bit_cast(bf16x8, both);
+      };
+      f32x16 sc[4];        // S0a S0b S1a S1b
+      unsigned pw[4][8];   // packed P of the same four blocks: words 0..3 = keys 0..15, 4..7 = keys 16..31 of the block
+      bf16x8 FA[8], FB[8];
+      auto silu_unit = [&](int u) __attribute__((always_inline)) {
+        const int blk = u >> 3, e = u & 7;
+        const int qb = blk & 1, kvb = blk >> 1;
+        const int m = ma + 32 * qb;
+        float pe[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int r = 2 * e + t;
+          const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          float sv = sc[blk][r];
+          if (HAS_RAB) sv = fmaf(rabt[(m - q0) - jl + (BN - 1)], kLog2e, sv);
+          const float ex = __builtin_amdgcn_exp2f(-sv);
+          float pv = sv * __builtin_amdgcn_rcpf(1.0f + ex);
+          if (MASKED) {
+            const int j = k0 + jl;
+            const bool kp = ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
+            pv = kp ? pv : 0.f;
+          }
+          pe[t] = pv;
+        }
+        pw[blk][e] = pack_bf16x2(pe[0], pe[1]);
+        if (W64_ABL & 1) pw[blk][e] = 0x3f803f80u;
+      };
+      auto p_frag = [&](int blk, int s2l) __attribute__((always_inline)) {
+        const u32x4 w = {pw[blk][4 * s2l + 0], pw[blk][4 * s2l + 1], pw[blk][4 * s2l + 2], pw[blk][4 * s2l + 3]};
+        return __builtin_bit_cast(bf16x8, w);
+      };
+      constexpr int U_FIRST = 10, U_LAST = 56, U_SPAN = U_LAST - U_FIRST;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) FA[kk] = (W64_ABL & 2) ? qf[1][kk] : k_frag(0, kk);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < 64; ++s) {
+        // LDS reads of later slots
+        if (W64_ABL & 2) {
+          if (s < 8) FB[s] = qf[0][s];
+        } else if (s < 8) {
+          FB[s] = k_frag(1, s);
+        } else if (s >= 16 && s < 32) {
+          if (((s - 16) & 1) == 0) { const int f = (s - 16) >> 1; FA[f] = v_frag(f >> 1, f & 1); }
+        } else if (s >= 32 && s < 48) {
+          if (((s - 32) & 1) == 0) { const int f = (s - 32) >> 1; FB[f] = v_frag(f >> 1, 2 + (f & 1)); }
+        }
+        // the MFMA of this slot
+        if (s < 32) {
+          const int blk = s >> 3, kk = s & 7;
+          const int qb = blk & 1, kvb = blk >> 1;
+          sc[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kvb ? FB[kk] : FA[kk], qf[qb][kk], kk == 0 ? zero : sc[blk], 0, 0, 0);
+        } else {
+          const int i = s & 7, qb = (s >> 3) & 1, kvb = (s - 32) >> 4;
+          const int db = i >> 1, s2l = i & 1;
+          acc[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kvb ? FB[i] : FA[i], p_frag(2 * kvb + qb, s2l), acc[qb][db], 0, 0, 0);
+        }
+        // SiLU units of this slot
+        if (s >= U_FIRST && s < U_LAST) {
+          const int u0 = ((s - U_FIRST) * 32) / U_SPAN, u1 = ((s + 1 - U_FIRST) * 32) / U_SPAN;
+#pragma unroll
+          for (int u = u0; u < u1; ++u) silu_unit(u);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if ((W64_ABL & 1) && s == 63) asm volatile("" ::"a"(sc[0]), "a"(sc[1]), "a"(sc[2]), "a"(sc[3]));
+      }
+    };
+
     auto compute_tile = [&](int itc, int st) __attribute__((always_inline)) {
       const int k0 = itc * BN;
       const int k1 = k0 + BN;
@@ -392,18 +522,26 @@ __global__ __launch_bounds__(256, 1) void hstu_fwd_tiled_d128_w64(Params p) {
                                               (k0 < si.ctx_eff));
       if (!any_kept) return;
       const bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);
-      if (full) tile_body(std::false_type{}, k0, st);
-      else tile_body(std::true_type{}, k0, st);
+      if constexpr (FP8) {
+        if (full) tile_body(std::false_type{}, k0, st);
+        else tile_body(std::true_type{}, k0, st);
+      } else {
+        if (full) tile_body_slots(std::false_type{}, k0, st);
+        else tile_body_slots(std::true_type{}, k0, st);
+      }
     };
 
     // ---- main loop: wait for tile `it`, publish it, refill the ring, compute ----
     int st = 0;
     while (it < nkv) {
+      HSTU_STAMP(0);
       // this wave's copies of tile `it` have landed when at most (issued - 1) tiles are in flight
       if (issued >= 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_TILE) : "memory");
       else if (issued == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_PER_TILE) : "memory");
       else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();  // tile `it` visible to all waves; tile it - 1 no longer read by anyone
+      HSTU_STAMP(1);
+      if (!(W64_ABL & 16)) __syncthreads();  // tile `it` visible to all waves; tile it - 1 no longer read by anyone
+      HSTU_STAMP(2);
       --issued;
       if (it_issue < nkv) {
         issue_tile(it_issue, st_issue);
@@ -411,12 +549,25 @@ __global__ __launch_bounds__(256, 1) void hstu_fwd_tiled_d128_w64(Params p) {
         st_issue = (st_issue + 1) & (W64_STAGES - 1);
         ++issued;
       }
+      HSTU_STAMP(3);
       compute_tile(it, st);
+      HSTU_STAMP(7);
+#ifdef HSTU_TRACE
+      ++trace_it;
+#endif
       it = next_tile(it);
       st = (st + 1) & (W64_STAGES - 1);
     }
 
+    W64_ITEM_STAMP(3);
+#ifdef HSTU_TRACE
+    const long long trace_c3 = clock64();
+#endif
     // ---- epilogue ----
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) asm volatile("" : "+a"(acc[qb][db]));
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const int m = ma + 32 * qb;
@@ -438,7 +589,24 @@ __global__ __launch_bounds__(256, 1) void hstu_fwd_tiled_d128_w64(Params p) {
         }
       }
     }
+#ifdef HSTU_TRACE
+    if (lane == 0 && blockIdx.x < 4096 && slot == (int)(blockIdx.x / NUM_XCD))
+      g_item_trace[(blockIdx.x * 4 + wave) * 8 + 4] = (unsigned long long)(trace_c3 - trace_c2);
+#endif
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // known state for the next item's copy counting
+    W64_ITEM_STAMP(5);
+    if (lane == 0) {
+#ifdef HSTU_TRACE
+      if (blockIdx.x < 4096 && slot == (int)(blockIdx.x / NUM_XCD)) {
+        unsigned hwid;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        g_item_trace[(blockIdx.x * 4 + wave) * 8 + 6] = ((unsigned long long)xcc << 32) | hwid;
+        g_item_trace[(blockIdx.x * 4 + wave) * 8 + 7] = (unsigned long long)nkv;
+      }
+#endif
+    }
     __syncthreads();                                   // ring slots are reused by the next item
   }  // work items
 }
