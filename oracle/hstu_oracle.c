@@ -1,5 +1,5 @@
 /*
- * CPU oracle for the HSTU jagged attention forward.  TEST INFRASTRUCTURE ONLY.
+ * CPU oracle for the HSTU jagged attention forward and backward.  TEST INFRASTRUCTURE ONLY.
  *
  * This file is a plain-C restatement of the reference algorithm.  It exists so
  * that tests, the smoke check and the benchmark's CPU-baseline leg have an
@@ -14,6 +14,10 @@
  *                               alpha on the scores, x*sigmoid(x), attn_scale or 1/max_seq_len,
  *                               mask multiply, weights @ v) with the packed [T,H,Dv] output and
  *                               zeroed tail of recir/ops/pallas/jagged_hstu_attention.py:323-344
+ *   hstu_oracle_attn_bwd        the gradient formulas of recir/ops/helion/jagged_hstu_attention.py:16-27
+ *                               (dP = dO V^T, dV = P^T dO, dS = dP keep scale silu'(S),
+ *                               dQ = alpha dS K, dK = alpha dS^T Q, silu'(x) = sig(x)(1 + x(1 - sig(x))))
+ *                               with the zeroed tail rows of :916-920
  *   hstu_oracle_e4m3_encode     recir/ops/kjt_split_per_feature.cpp:493-502 (clamp to +-448 then
  *                               round-to-nearest-even cast to float8_e4m3fn)
  *
@@ -22,6 +26,10 @@
  * independent closed forms of the mask compared exhaustively, closed-form
  * special cases (single token, all-target, constant score => kept-key count),
  * and torch's own float8_e4m3fn cast for the encoder.
+ * The backward is pinned the way the reference pins its own kernels
+ * (recir/ops/helion/jagged_hstu_attention.py:260-280, autograd through the forward): against
+ * torch autograd through the reference's compiled C++ forward op, against torch autograd through
+ * a dense torch restatement, and against central finite differences of the forward oracle.
  * Parity unpinned by the reference: the relative attention bias term (the
  * reference has no such argument) and contextual_seq_len > 1 in "prefix" mode
  * (the reference C++ only ever unmasks key 0).  Both are pinned only by the
@@ -142,6 +150,88 @@ int hstu_oracle_attn_fwd(const float* q, const float* k, const float* v, float* 
       }
     }
     free(acc);
+  }
+  return 0;
+}
+
+/*
+ * Gradients of hstu_oracle_attn_fwd with respect to q, k and v for an upstream gradient dout
+ * [T,H,Dv].  attn_scale_kind as in the forward.  Accumulation in double; dq, dk, dv are written in
+ * full (rows at and after seq_offsets[B] are zero).  The score bias rab enters S but no gradient is
+ * produced for it.
+ * p_round: 1 rounds P and dS to bf16 before they are used as matmul operands (what a bf16 kernel
+ *          does); 0 keeps them in double.
+ */
+int hstu_oracle_attn_bwd(const float* dout, const float* q, const float* k, const float* v, float* dq,
+                         float* dk, float* dv, const int64_t* seq_offsets,
+                         const int64_t* num_targets, const float* rab, int attn_scale_kind,
+                         const float* attn_scale, int64_t T, int64_t B, int64_t H, int64_t Dqk,
+                         int64_t Dv, int64_t max_seq_len, int64_t ctx, int ctx_mode, double alpha,
+                         int p_round) {
+  for (int64_t b = 0; b < B; ++b) {
+    const int64_t s = seq_offsets[b], e = seq_offsets[b + 1];
+    if (!(0 <= s && s <= e && e <= T)) return -1;
+  }
+  memset(dq, 0, sizeof(float) * (size_t)(T * H * Dqk));
+  memset(dk, 0, sizeof(float) * (size_t)(T * H * Dqk));
+  memset(dv, 0, sizeof(float) * (size_t)(T * H * Dv));
+  const int64_t rab_w = 2 * max_seq_len - 1;
+
+  /* one (sequence, head) per task: every output row is owned by exactly one task */
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+  for (int64_t b = 0; b < B; ++b) {
+    for (int64_t h = 0; h < H; ++h) {
+      const int64_t s = seq_offsets[b], e = seq_offsets[b + 1], n = e - s;
+      const int64_t t = num_targets ? num_targets[b] : 0;
+      if (n <= 0) continue;
+      double* adq = (double*)calloc((size_t)(n * Dqk), sizeof(double));
+      double* adk = (double*)calloc((size_t)(n * Dqk), sizeof(double));
+      double* adv = (double*)calloc((size_t)(n * Dv), sizeof(double));
+      for (int64_t m = 0; m < n; ++m) {
+        const float* qr = q + ((s + m) * H + h) * Dqk;
+        const float* gr = dout + ((s + m) * H + h) * Dv;
+        double scale;
+        if (attn_scale_kind == 0) scale = 1.0 / (double)max_seq_len;
+        else if (attn_scale_kind == 1) scale = (double)attn_scale[0];
+        else scale = (double)attn_scale[s + m];
+        for (int64_t j = 0; j < n; ++j) {
+          if (!hstu_oracle_keep(m, j, n, t, ctx, ctx_mode)) continue;
+          const float* kr = k + ((s + j) * H + h) * Dqk;
+          const float* vr = v + ((s + j) * H + h) * Dv;
+          double dot = 0.0;
+          for (int64_t d = 0; d < Dqk; ++d) dot += (double)qr[d] * (double)kr[d];
+          double x = dot * alpha;
+          if (rab) {
+            const int64_t idx = m - j + max_seq_len - 1;
+            if (idx >= 0 && idx < rab_w) x += (double)rab[h * rab_w + idx];
+          }
+          const double sig = 1.0 / (1.0 + exp(-x));
+          double p = x * sig * scale;
+          double dp = 0.0;
+          for (int64_t d = 0; d < Dv; ++d) dp += (double)gr[d] * (double)vr[d];
+          double ds = dp * scale * sig * (1.0 + x * (1.0 - sig));
+          if (p_round) {
+            p = (double)round_to_bf16((float)p);
+            ds = (double)round_to_bf16((float)ds);
+          }
+          for (int64_t d = 0; d < Dv; ++d) adv[j * Dv + d] += p * (double)gr[d];
+          for (int64_t d = 0; d < Dqk; ++d) {
+            adq[m * Dqk + d] += ds * (double)kr[d];
+            adk[j * Dqk + d] += ds * (double)qr[d];
+          }
+        }
+      }
+      for (int64_t m = 0; m < n; ++m) {
+        for (int64_t d = 0; d < Dqk; ++d) {
+          dq[((s + m) * H + h) * Dqk + d] = (float)(alpha * adq[m * Dqk + d]);
+          dk[((s + m) * H + h) * Dqk + d] = (float)(alpha * adk[m * Dqk + d]);
+        }
+        for (int64_t d = 0; d < Dv; ++d) dv[((s + m) * H + h) * Dv + d] = (float)adv[m * Dv + d];
+      }
+      free(adq);
+      free(adk);
+      free(adv);
+    }
   }
   return 0;
 }

@@ -55,6 +55,8 @@ def lib() -> ctypes.CDLL:
         L.hstu_oracle_attn_fwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, c_int, vp,
                                            i64, i64, i64, i64, i64, i64, i64, c_int, dbl, c_int]
         L.hstu_oracle_attn_fwd.restype = c_int
+        L.hstu_oracle_attn_bwd.argtypes = [vp] * 10 + [c_int, vp] + [i64] * 7 + [c_int, ctypes.c_double, c_int]
+        L.hstu_oracle_attn_bwd.restype = c_int
         L.hstu_oracle_e4m3_encode.argtypes = [ctypes.c_float]
         L.hstu_oracle_e4m3_encode.restype = ctypes.c_uint8
         L.hstu_oracle_e4m3_decode.argtypes = [ctypes.c_uint8]
@@ -118,6 +120,42 @@ def attn_fwd(q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn
     if rc != 0:
         raise ValueError("invalid jagged range in seq_offsets")
     return out
+
+
+def attn_bwd(dout, q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn_scale=None,
+             rab=None, contextual_seq_len=0, ctx_mode=CTX_PREFIX, round_bf16=False):
+    """Gradients (dq, dk, dv) of ``attn_fwd`` for the upstream gradient ``dout`` [T,H,Dv]; float32 arrays.
+
+    Same argument conventions as ``attn_fwd``.  ``round_bf16`` rounds P and dS to bf16 before the
+    products that consume them (what a bf16 kernel does).  No gradient is produced for ``rab``.
+    """
+    dout, q, k, v = _f32(dout), _f32(q), _f32(k), _f32(v)
+    T, H, Dqk = q.shape
+    Dv = v.shape[2]
+    assert k.shape == q.shape and v.shape[:2] == (T, H) and dout.shape == v.shape
+    off = np.ascontiguousarray(np.asarray(seq_offsets, dtype=np.int64))
+    B = off.shape[0] - 1
+    nt = None if num_targets is None else np.ascontiguousarray(np.asarray(num_targets, dtype=np.int64))
+    rb = None
+    if rab is not None:
+        rb = _f32(rab)
+        assert rb.shape == (H, 2 * max_seq_len - 1)
+    kind, sc = 0, None
+    if attn_scale is not None:
+        sc = _f32(attn_scale).reshape(-1)
+        kind = 1 if sc.size == 1 and np.ndim(attn_scale) == 0 else 2
+        if kind == 2:
+            assert sc.shape == (T,)
+    dq = np.empty((T, H, Dqk), dtype=np.float32)
+    dk = np.empty((T, H, Dqk), dtype=np.float32)
+    dv = np.empty((T, H, Dv), dtype=np.float32)
+    rc = lib().hstu_oracle_attn_bwd(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv),
+                                    _ptr(off), _ptr(nt), _ptr(rb), kind, _ptr(sc), T, B, H, Dqk, Dv,
+                                    int(max_seq_len), int(contextual_seq_len), int(ctx_mode),
+                                    float(alpha), 1 if round_bf16 else 0)
+    if rc != 0:
+        raise ValueError("invalid jagged range in seq_offsets")
+    return dq, dk, dv
 
 
 def keep_mask_dense(max_seq_len, lengths, num_targets, contextual_seq_len=0):

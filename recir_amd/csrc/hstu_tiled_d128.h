@@ -48,6 +48,19 @@ __device__ int g_trace_block = 0;
 #else
 #define HSTU_STAMP(slot) do { } while (0)
 #endif
+#ifdef HSTU_TRACE
+// Debug build only: wall-clock stamps (100 MHz) of the phases of every workgroup's first item.
+__device__ unsigned long long g_item_trace[4096 * 4 * 8];
+#define HSTU_ITEM_STAMP(k)                                                                      \
+  do {                                                                                         \
+    __builtin_amdgcn_sched_barrier(0);                                                         \
+    if (lane == 0 && blockIdx.x < 4096 && slot == (int)(blockIdx.x / NUM_XCD))                 \
+      g_item_trace[(blockIdx.x * 4 + wave) * 8 + (k)] = wall_clock64();                        \
+    __builtin_amdgcn_sched_barrier(0);                                                         \
+  } while (0)
+#else
+#define HSTU_ITEM_STAMP(k) do { } while (0)
+#endif
 
 #ifndef HSTU_EXP
 #define HSTU_EXP 0  // debug builds only: bit mask that removes pieces of the kernel for timing studies

@@ -93,6 +93,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
   const int list_len = p.ws_counts[xcd];
   const WorkItem* __restrict__ list = p.ws_items + (size_t)xcd * p.items_cap;
   for (int slot = blockIdx.x / NUM_XCD; slot < list_len; slot += p.grid_slots) {
+    HSTU_ITEM_STAMP(0);
     const WorkItem wi = list[slot];
     SeqInfo si;
     si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
@@ -414,9 +415,11 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       else tile_body(std::true_type{}, buf_tag, k0, nxt);
     };
 
+    HSTU_ITEM_STAMP(1);
     if (it < nkv) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      HSTU_ITEM_STAMP(2);
       // two tiles per trip so that the stage index is a compile-time constant
       while (true) {
         int nxt = next_tile(it);
@@ -450,6 +453,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       }
     }
 
+    HSTU_ITEM_STAMP(3);
     // ---- epilogue: O^T accumulators -> out[s + m, h, :] ----
     if (m < si.n) {
       float oscale = 1.0f / (float)p.N;
@@ -468,7 +472,18 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         }
       }
     }
+    HSTU_ITEM_STAMP(4);
     __syncthreads();  // LDS buffers are reused by the next item
+    HSTU_ITEM_STAMP(5);
+#ifdef HSTU_TRACE
+    if (lane == 0 && blockIdx.x < 4096 && slot == (int)(blockIdx.x / NUM_XCD)) {
+      unsigned hwid, xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+      g_item_trace[(blockIdx.x * 4 + wave) * 8 + 6] = ((unsigned long long)xcc << 32) | hwid;
+      g_item_trace[(blockIdx.x * 4 + wave) * 8 + 7] = (unsigned long long)nkv;
+    }
+#endif
   }  // work items
 }
 

@@ -30,19 +30,6 @@ namespace recir_hstu {
 #ifndef W64_ABL
 #define W64_ABL 0   // debug builds only: bit mask of parts to leave out (timing experiments)
 #endif
-#ifdef HSTU_TRACE
-// Debug build only: wall-clock stamps (100 MHz) of the phases of every workgroup's first item.
-__device__ unsigned long long g_item_trace[4096 * 4 * 8];
-#define W64_ITEM_STAMP(k)                                                                      \
-  do {                                                                                         \
-    __builtin_amdgcn_sched_barrier(0);                                                         \
-    if (lane == 0 && blockIdx.x < 4096 && slot == (int)(blockIdx.x / NUM_XCD))                 \
-      g_item_trace[(blockIdx.x * 4 + wave) * 8 + (k)] = wall_clock64();                        \
-    __builtin_amdgcn_sched_barrier(0);                                                         \
-  } while (0)
-#else
-#define W64_ITEM_STAMP(k) do { } while (0)
-#endif
 constexpr int BM2 = 256;     // query rows per workgroup
 constexpr int W64_STAGES = 4;
 constexpr bool W64_Q_IN_ACC = false;
@@ -97,7 +84,7 @@ __global__ __launch_bounds__(256, 1) void hstu_fwd_tiled_d128_w64(Params p) {
   const int list_len = p.ws_counts[xcd];
   const WorkItem* __restrict__ list = p.ws_items + (size_t)xcd * p.items_cap;
   for (int slot = blockIdx.x / NUM_XCD; slot < list_len; slot += p.grid_slots) {
-    W64_ITEM_STAMP(0);
+    HSTU_ITEM_STAMP(0);
     const WorkItem wi = list[slot];
     SeqInfo si;
     si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
@@ -236,9 +223,9 @@ __global__ __launch_bounds__(256, 1) void hstu_fwd_tiled_d128_w64(Params p) {
     // the q loads above are ordinary vector loads issued after the first copies: once their data
     // has been used, everything issued before them has landed as well.  Make that explicit so the
     // counting below starts from a known state.
-    W64_ITEM_STAMP(1);
+    HSTU_ITEM_STAMP(1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    W64_ITEM_STAMP(2);
+    HSTU_ITEM_STAMP(2);
 #ifdef HSTU_TRACE
     const long long trace_c2 = clock64();
 #endif
@@ -559,7 +546,7 @@ __global__ __launch_bounds__(256, 1) void hstu_fwd_tiled_d128_w64(Params p) {
       st = (st + 1) & (W64_STAGES - 1);
     }
 
-    W64_ITEM_STAMP(3);
+    HSTU_ITEM_STAMP(3);
 #ifdef HSTU_TRACE
     const long long trace_c3 = clock64();
 #endif
@@ -594,7 +581,7 @@ __global__ __launch_bounds__(256, 1) void hstu_fwd_tiled_d128_w64(Params p) {
       g_item_trace[(blockIdx.x * 4 + wave) * 8 + 4] = (unsigned long long)(trace_c3 - trace_c2);
 #endif
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // known state for the next item's copy counting
-    W64_ITEM_STAMP(5);
+    HSTU_ITEM_STAMP(5);
     if (lane == 0) {
 #ifdef HSTU_TRACE
       if (blockIdx.x < 4096 && slot == (int)(blockIdx.x / NUM_XCD)) {

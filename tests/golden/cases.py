@@ -63,3 +63,14 @@ def build_inputs(case):
         scale = torch.tensor(case["attn_scale"], dtype=torch.float32)
     nt = None if case["no_targets"] else wl.num_targets
     return wl, scale, nt
+
+
+def upstream_gradient(case, wl):
+    """Seeded upstream gradient dout [T,H,Dv] of a case (bf16-representable when the inputs are)."""
+    import torch
+
+    g = torch.Generator().manual_seed(7000 + case["seed"])
+    dout = torch.randn(wl.T, wl.H, wl.v.shape[2], generator=g)
+    if case["bf16_inputs"]:
+        dout = dout.to(torch.bfloat16).float()
+    return dout

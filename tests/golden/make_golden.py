@@ -7,6 +7,9 @@ checkout by `make -C oracle ref`):
 
 Outputs (data only):
   tests/golden/small_cases.npz   expected out[seq_offsets[B], H, Dv] per small case
+  tests/golden/small_cases_bwd.npz  per small case, dq/dk/dv from torch autograd through the same
+                                 operator for a seeded upstream gradient (the reference's own
+                                 definition of its backward oracle, helion jagged_hstu_attention.py:260-280)
   tests/golden/config2.npz       config 2 (bf16-rounded inputs, fp32 arithmetic): per-sequence sums,
                                  abs-sums and 64 sampled rows
   tests/golden/config4.npz       same for the long skewed config 4
@@ -37,6 +40,16 @@ def run_ref(wl, scale, nt):
                                     contextual_seq_len=wl.contextual_seq_len)
 
 
+def run_ref_bwd(wl, scale, nt, dout):
+    """(dq, dk, dv) by autograd through the reference operator; rows after seq_offsets[B] get no gradient."""
+    q, k, v = (t.detach().clone().requires_grad_(True) for t in (wl.q, wl.k, wl.v))
+    out = hstu_oracle.ref_attn_fwd(q, k, v, wl.seq_offsets, nt, max_seq_len=wl.max_seq_len,
+                                   alpha=wl.alpha, attn_scale=scale,
+                                   contextual_seq_len=wl.contextual_seq_len)
+    out.backward(dout[: out.shape[0]])
+    return q.grad, k.grad, v.grad
+
+
 def sampled_rows(total_rows, seed=1234):
     rng = np.random.Generator(np.random.PCG64(seed))
     return np.sort(rng.choice(total_rows, size=min(SAMPLED_ROWS, total_rows), replace=False))
@@ -61,6 +74,16 @@ def main():
         small[name] = run_ref(wl, scale, nt).numpy()
         print(name, small[name].shape)
     np.savez_compressed(os.path.join(HERE, "small_cases.npz"), **small)
+    from tests.golden.cases import upstream_gradient  # noqa: E402
+
+    bwd = {}
+    for name, case in SMALL_CASES.items():
+        if case["Dqk"] >= 128:
+            continue  # keeps the fixture small; these shapes are compared with the live operator
+        wl, scale, nt = build_inputs(case)
+        dq, dk, dv = run_ref_bwd(wl, scale, nt, upstream_gradient(case, wl))
+        bwd[name + "/dq"], bwd[name + "/dk"], bwd[name + "/dv"] = dq.numpy(), dk.numpy(), dv.numpy()
+    np.savez_compressed(os.path.join(HERE, "small_cases_bwd.npz"), **bwd)
     for cfg in (2, 4):
         fx = checksum_fixture(cfg)
         np.savez_compressed(os.path.join(HERE, f"config{cfg}.npz"), **fx)
