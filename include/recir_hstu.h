@@ -1,5 +1,5 @@
 /*
- * C ABI of the MI355X (gfx950) HSTU jagged attention forward.
+ * C ABI of the MI355X (gfx950) HSTU jagged attention forward and backward.
  *
  * One shared library, plain pointers and sizes, no C++ or torch types.  Every entry point that
  * launches work does so asynchronously on the HIP stream the caller passes; nothing synchronises
@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RECIR_HSTU_ABI_VERSION 1
+#define RECIR_HSTU_ABI_VERSION 2
 
 /* element types of q/k (v and out follow: bf16 for BF16 and FP8_E4M3, fp32 for FP32) */
 #define RECIR_HSTU_DTYPE_BF16 0
@@ -88,6 +88,35 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
 
 /* Scratch size recir_hstu_attn_fwd needs for these sizes (upper bound over all kernel variants). */
 size_t recir_hstu_attn_fwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk,
+                                           int32_t Dv, int32_t dtype);
+
+/*
+ * HSTU jagged attention backward: gradients of recir_hstu_attn_fwd with respect to q, k and v.
+ *
+ * Replaces: hstu_ragged_attention_bwd_jax_fn (recir/ops/helion/jagged_hstu_attention.py:875-920,
+ *   kernels :356-570, formulas :16-27) and pallas_jagged_hstu_attention_backward with its dQ and
+ *   fused dK/dV kernels (recir/ops/pallas/jagged_hstu_attention.py:724-1339); the numerical
+ *   definition is autograd through the forward (helion/jagged_hstu_attention.py:260-280).
+ *
+ *   dP = dO V^T,  dV = P^T dO,  dS = dP keep scale silu'(S),  dQ = alpha dS K,  dK = alpha dS^T Q
+ *
+ * dout          device, [T, H, Dv], the gradient of the forward's out; rows >= seq_offsets[B] ignored
+ * q, k, v       the forward's inputs (bf16 or fp32; FP8_E4M3 is not supported)
+ * dq, dk        device, [T, H, Dqk]; dv device, [T, H, Dv]; same element type as q; written in full
+ *               (rows >= seq_offsets[B] zeroed, recir/ops/helion/jagged_hstu_attention.py:916-920)
+ * rab           enters S as in the forward; no gradient is produced for it
+ * attn_scale, flags, sizes, workspace, hip_stream: as for the forward; workspace of at least
+ *               recir_hstu_attn_bwd_workspace_bytes(...) bytes
+ */
+int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const void* v, void* dq,
+                        void* dk, void* dv, const void* seq_offsets, const void* num_targets,
+                        const float* rab, const float* attn_scale, int32_t T, int32_t B, int32_t H,
+                        int32_t Dqk, int32_t Dv, int32_t max_seq_len, int32_t contextual_seq_len,
+                        float alpha, int32_t dtype, uint32_t flags, void* workspace,
+                        size_t workspace_bytes, void* hip_stream);
+
+/* Scratch size recir_hstu_attn_bwd needs for these sizes. */
+size_t recir_hstu_attn_bwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk,
                                            int32_t Dv, int32_t dtype);
 
 /*

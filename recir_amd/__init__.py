@@ -1,4 +1,4 @@
-"""MI355X-native HSTU jagged attention forward behind RecIR's operator surface.
+"""MI355X-native HSTU jagged attention (forward and backward) behind RecIR's operator surface.
 
 The compute lives in ``librecir_hstu.so`` (hand-written HIP for gfx950, C ABI in
 ``include/recir_hstu.h``); this package is the thin host side: a ctypes binding, the
@@ -7,7 +7,9 @@ and a keyword front end with the defaults of the packed accelerator kernel it re
 """
 from .ops import (  # noqa: F401
     hstu_jagged_attention_fwd,
+    hstu_jagged_attention_bwd,
     jagged_hstu_attention,
+    jagged_hstu_attention_backward,
     jagged_hstu_attention_fp8,
     quantize_e4m3_per_head,
     register_swaps,
@@ -20,7 +22,9 @@ from .ops import (  # noqa: F401
 
 __all__ = [
     "hstu_jagged_attention_fwd",
+    "hstu_jagged_attention_bwd",
     "jagged_hstu_attention",
+    "jagged_hstu_attention_backward",
     "jagged_hstu_attention_fp8",
     "quantize_e4m3_per_head",
     "register_swaps",

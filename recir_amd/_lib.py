@@ -7,7 +7,7 @@ import os
 _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "librecir_hstu.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_BF16 = 0
 DTYPE_FP32 = 1
@@ -23,6 +23,8 @@ FLAG_KERNEL_SHIFT = 8
 EXPORTS = (
     "recir_hstu_attn_fwd",
     "recir_hstu_attn_fwd_workspace_bytes",
+    "recir_hstu_attn_bwd",
+    "recir_hstu_attn_bwd_workspace_bytes",
     "recir_hstu_quantize_e4m3_per_head",
     "recir_hstu_calibration_copy",
     "recir_hstu_last_error",
@@ -53,6 +55,10 @@ def load() -> ctypes.CDLL:
     L.recir_hstu_attn_fwd.restype = ctypes.c_int
     L.recir_hstu_attn_fwd_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     L.recir_hstu_attn_fwd_workspace_bytes.restype = sz
+    L.recir_hstu_attn_bwd.argtypes = [vp] * 11 + [i32] * 7 + [f32, i32, u32, vp, sz, vp]
+    L.recir_hstu_attn_bwd.restype = ctypes.c_int
+    L.recir_hstu_attn_bwd_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
+    L.recir_hstu_attn_bwd_workspace_bytes.restype = sz
     L.recir_hstu_quantize_e4m3_per_head.argtypes = [vp, vp, vp, i32, i32, i32, vp]
     L.recir_hstu_quantize_e4m3_per_head.restype = ctypes.c_int
     L.recir_hstu_calibration_copy.argtypes = [vp, vp, sz, vp]

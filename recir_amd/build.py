@@ -8,7 +8,7 @@ import subprocess
 _PKG = os.path.dirname(os.path.abspath(__file__))
 _ROOT = os.path.dirname(_PKG)
 LIB_PATH = os.path.join(_PKG, "librecir_hstu.so")
-SOURCES = [os.path.join(_PKG, "csrc", "hstu_attn_fwd.hip")]
+SOURCES = [os.path.join(_PKG, "csrc", "hstu_attn.hip")]
 
 
 def hipcc_path() -> str:

@@ -10,6 +10,7 @@
 //   hstu_plan_kernel        (sequence, query-tile) work list, heaviest tiles first
 //   hstu_fwd_tiled_d128     bf16 / fp8-qk tiled MFMA kernel, head dim 128
 //   hstu_fwd_generic        any head dim, fp32 or bf16, one wave per (token, head)
+//   hstu_bwd_generic_dq / hstu_bwd_generic_dkv   backward, any head dim, one wave per (token, head)
 //   hstu_fill_zero          out := 0 when there are no sequences
 //   hstu_amax_per_head / hstu_quant_e4m3_per_head   per-head fp8 quantiser
 #include <hip/hip_runtime.h>
@@ -25,6 +26,7 @@
 #include "hstu_tiled_d128.h"
 #include "hstu_tiled_d128_dl.h"
 #include "hstu_tiled_d128_w64.h"
+#include "hstu_bwd_generic.h"
 
 using namespace recir_hstu;
 
@@ -103,12 +105,6 @@ __global__ void hstu_fill_zero(unsigned short* out, size_t n2) {
 // Precision ladder: operands -> fp32 scores -> SiLU in fp32 -> P rounded to the value type ->
 // fp32 accumulate -> output type.
 // ---------------------------------------------------------------------------------------------
-template <bool BF16>
-__device__ __forceinline__ float load_elem(const void* base, size_t idx) {
-  if (BF16) return bf16_bits_to_float(((const unsigned short*)base)[idx]);
-  return ((const float*)base)[idx];
-}
-
 constexpr int GENERIC_MAX_D = 512;
 
 template <bool BF16>
@@ -357,6 +353,74 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
   else hipLaunchKernelGGL(hstu_fwd_generic<false>, grid, dim3(64), 0, stream, p);
   if (int rc = launch_status("hstu_fwd_generic")) return rc;
   g_last_kernel = dtype == RECIR_HSTU_DTYPE_BF16 ? "generic_bf16" : "generic_fp32";
+  return RECIR_HSTU_OK;
+}
+
+size_t recir_hstu_attn_bwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk, int32_t Dv,
+                                           int32_t dtype) {
+  // two work lists: query tiles for dQ, key tiles for dK/dV
+  return 2 * ((recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype) + 255) & ~(size_t)255);
+}
+
+int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const void* v, void* dq,
+                        void* dk, void* dv, const void* seq_offsets, const void* num_targets,
+                        const float* rab, const float* attn_scale, int32_t T, int32_t B, int32_t H,
+                        int32_t Dqk, int32_t Dv, int32_t max_seq_len, int32_t contextual_seq_len,
+                        float alpha, int32_t dtype, uint32_t flags, void* workspace,
+                        size_t workspace_bytes, void* hip_stream) {
+  hipStream_t stream = (hipStream_t)hip_stream;
+  (void)workspace; (void)workspace_bytes;
+  if (T < 0 || B < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "negative size: T=%d B=%d", T, B);
+  if (H <= 0 || Dqk <= 0 || Dv <= 0)
+    return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "H, Dqk, Dv must be positive: H=%d Dqk=%d Dv=%d", H, Dqk, Dv);
+  if (max_seq_len <= 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "max_seq_len must be positive, got %d", max_seq_len);
+  if (contextual_seq_len < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "contextual_seq_len must be >= 0, got %d", contextual_seq_len);
+  if (dtype != RECIR_HSTU_DTYPE_BF16 && dtype != RECIR_HSTU_DTYPE_FP32)
+    return fail(dtype == RECIR_HSTU_DTYPE_FP8_E4M3 ? RECIR_HSTU_ERR_UNSUPPORTED : RECIR_HSTU_ERR_INVALID_ARGUMENT,
+                "backward supports bf16 and fp32 tensors, got dtype %d", dtype);
+  if (T == 0) return RECIR_HSTU_OK;
+  if (!dout || !q || !k || !v || !dq || !dk || !dv)
+    return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "dout, q, k, v, dq, dk, dv must be non-null");
+  if (!seq_offsets) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "seq_offsets must be non-null");
+
+  BwdParams bp;
+  memset(&bp, 0, sizeof(bp));
+  Params& p = bp.f;
+  p.q = q; p.k = k; p.v = v;
+  p.seq_offsets = seq_offsets; p.num_targets = num_targets;
+  p.rab = rab; p.attn_scale = attn_scale;
+  p.T = T; p.B = B; p.H = H; p.Dqk = Dqk; p.Dv = Dv; p.N = max_seq_len; p.ctx = contextual_seq_len;
+  p.alpha = alpha; p.flags = flags;
+  bp.dout = dout; bp.dq = dq; bp.dk = dk; bp.dv = dv;
+
+  const bool bf16 = dtype == RECIR_HSTU_DTYPE_BF16;
+  const size_t esz = bf16 ? 2 : 4;
+  if (B == 0) {
+    void* outs[3] = {dq, dk, dv};
+    const int dims[3] = {Dqk, Dqk, Dv};
+    for (int i = 0; i < 3; ++i) {
+      const size_t bytes = (size_t)T * H * dims[i] * esz;
+      hipLaunchKernelGGL(hstu_fill_zero, dim3(1024), dim3(256), 0, stream, (unsigned short*)outs[i], bytes / 2);
+      if (int rc = launch_status("hstu_fill_zero")) return rc;
+    }
+    g_last_kernel = "fill_zero";
+    return RECIR_HSTU_OK;
+  }
+  if (Dqk > BWD_GENERIC_MAX_D || Dv > BWD_GENERIC_MAX_D)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "head dims above %d are not supported (Dqk=%d Dv=%d)", BWD_GENERIC_MAX_D, Dqk, Dv);
+  if ((unsigned)H > 65535u) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "more than 65535 heads");
+  const dim3 grid((unsigned)T, (unsigned)H);
+  if (bf16) {
+    hipLaunchKernelGGL(hstu_bwd_generic_dq<true>, grid, dim3(64), 0, stream, bp);
+    if (int rc = launch_status("hstu_bwd_generic_dq")) return rc;
+    hipLaunchKernelGGL(hstu_bwd_generic_dkv<true>, grid, dim3(64), 0, stream, bp);
+  } else {
+    hipLaunchKernelGGL(hstu_bwd_generic_dq<false>, grid, dim3(64), 0, stream, bp);
+    if (int rc = launch_status("hstu_bwd_generic_dq")) return rc;
+    hipLaunchKernelGGL(hstu_bwd_generic_dkv<false>, grid, dim3(64), 0, stream, bp);
+  }
+  if (int rc = launch_status("hstu_bwd_generic_dkv")) return rc;
+  g_last_kernel = bf16 ? "bwd_generic_bf16" : "bwd_generic_fp32";
   return RECIR_HSTU_OK;
 }
 

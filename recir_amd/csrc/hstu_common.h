@@ -112,13 +112,13 @@ __device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
   return *(unsigned*)&y;
 }
 
-// Rows [seq_offsets[B], T) of out := 0, shared by all workgroups of a launch.
+// Rows [seq_offsets[B], T) of a [T, ...] tensor := 0, shared by all workgroups of a launch.
 template <int NTHREADS>
-__device__ __forceinline__ void zero_tail_rows(const Params& p, size_t row_bytes) {
+__device__ __forceinline__ void zero_tail_rows_of(const Params& p, void* tensor, size_t row_bytes) {
   const int end_all = end_of_sequences(p);
   if (end_all >= p.T) return;
   // row_bytes is a multiple of 2; use 2-byte stores only when 16-byte ones do not fit
-  unsigned char* base = (unsigned char*)p.out + (size_t)end_all * row_bytes;
+  unsigned char* base = (unsigned char*)tensor + (size_t)end_all * row_bytes;
   const size_t total = (size_t)(p.T - end_all) * row_bytes;
   const size_t nblk = gridDim.x * (size_t)gridDim.y;
   const size_t blk = blockIdx.x + (size_t)blockIdx.y * gridDim.x;
@@ -130,5 +130,32 @@ __device__ __forceinline__ void zero_tail_rows(const Params& p, size_t row_bytes
       ((unsigned short*)base)[i] = 0;
   }
 }
+
+template <int NTHREADS>
+__device__ __forceinline__ void zero_tail_rows(const Params& p, size_t row_bytes) {
+  zero_tail_rows_of<NTHREADS>(p, p.out, row_bytes);
+}
+
+template <bool BF16>
+__device__ __forceinline__ float load_elem(const void* base, size_t idx) {
+  if (BF16) return bf16_bits_to_float(((const unsigned short*)base)[idx]);
+  return ((const float*)base)[idx];
+}
+
+template <bool BF16>
+__device__ __forceinline__ void store_elem(void* base, size_t idx, float x) {
+  if (BF16) ((unsigned short*)base)[idx] = float_to_bf16_bits(x);
+  else ((float*)base)[idx] = x;
+}
+
+// Arguments of the backward kernels: the forward's inputs (f.out unused) plus the upstream
+// gradient and the three gradients to write.
+struct BwdParams {
+  Params f;
+  const void* dout;  // [T,H,Dv]
+  void* dq;          // [T,H,Dqk]
+  void* dk;          // [T,H,Dqk]
+  void* dv;          // [T,H,Dv]
+};
 
 }  // namespace recir_hstu

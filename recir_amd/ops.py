@@ -1,4 +1,4 @@
-"""Host side of the HSTU jagged attention forward: operator registration and front ends.
+"""Host side of the HSTU jagged attention (forward and backward): operator registration and front ends.
 
 ``recir::hstu_jagged_attention_fwd`` keeps the positional argument list of
 ``hammer::triton_ragged_attention_fwd`` (recir/ops/kjt_split_per_feature.cpp:780-783) so that
@@ -78,11 +78,17 @@ _FP8_SCHEMA = (
     "int contextual_seq_len, Tensor? rab=None) -> (Tensor, Tensor)"
 )
 _QUANT_SCHEMA = "hstu_quantize_e4m3_per_head(Tensor x) -> (Tensor, Tensor)"
+_BWD_SCHEMA = (
+    "hstu_jagged_attention_bwd(Tensor dout, int N, float alpha, Tensor q, Tensor k, Tensor v, "
+    "Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, int contextual_seq_len, "
+    "Tensor? rab=None) -> (Tensor, Tensor, Tensor)"
+)
 
 _LIBRARY = torch.library.Library("recir", "FRAGMENT")
 _LIBRARY.define(_SCHEMA)
 _LIBRARY.define(_FP8_SCHEMA)
 _LIBRARY.define(_QUANT_SCHEMA)
+_LIBRARY.define(_BWD_SCHEMA)
 
 
 def _check_common(q, k, v, seq_offsets, num_targets, max_seq_len) -> int:
@@ -116,26 +122,22 @@ def _index_tensors(seq_offsets, num_targets):
     return off, nt, (_lib.FLAG_OFFSETS_I32 if off.dtype == torch.int32 else 0)
 
 
-def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale, N, alpha,
-            contextual_seq_len, dtype_code) -> torch.Tensor:
-    L = _lib.load()
+def _prepare(opname, q, k, v, seq_offsets, num_targets, attn_scale, rab, N):
+    """Checks and device-side argument tensors shared by the forward and backward launches."""
     dev = q.device
     if dev.type != "cuda":
         raise RuntimeError(
-            "recir::hstu_jagged_attention_fwd runs on the GPU only (got a tensor on "
+            f"recir::{opname} runs on the GPU only (got a tensor on "
             f"'{dev}'); this package has no CPU path")
     for name, t in (("k", k), ("v", v), ("seq_offsets", seq_offsets)):
         if t.device != dev:
             raise ValueError(f"{name} is on {t.device}, q on {dev}")
     B = _check_common(q, k, v, seq_offsets, num_targets, N)
-    T, H, Dqk = q.shape
-    Dv = v.shape[2]
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    T, H, _ = q.shape
     off, nt, flags = _index_tensors(seq_offsets, num_targets)
     if _ctx_reference_rule:
         flags |= _lib.FLAG_CTX_REFERENCE
     flags |= (_forced_kernel & 0xFF) << _lib.FLAG_KERNEL_SHIFT
-
     sc = None
     if attn_scale is not None:
         sc = attn_scale.to(device=dev, dtype=torch.float32).contiguous()
@@ -150,28 +152,86 @@ def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale
         if tuple(rab.shape) != (H, 2 * N - 1):
             raise ValueError(f"rab must have shape [H, 2*max_seq_len-1] = [{H}, {2 * N - 1}]")
         rb = rab.to(device=dev, dtype=torch.float32).contiguous()
+    return B, off, nt, sc, rb, flags
 
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _raise_status(entry, rc):
+    msg = _lib.last_error()
+    if rc < 0:
+        raise ValueError(f"{entry} rejected the call ({rc}): {msg}")
+    raise RuntimeError(f"{entry} launch failed (hipError {rc}): {msg}")
+
+
+def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale, N, alpha,
+            contextual_seq_len, dtype_code) -> torch.Tensor:
+    L = _lib.load()
+    dev = q.device
+    B, off, nt, sc, rb, flags = _prepare("hstu_jagged_attention_fwd", q, k, v, seq_offsets, num_targets,
+                                         attn_scale, rab, N)
+    T, H, Dqk = q.shape
+    Dv = v.shape[2]
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     out = torch.empty((T, H, Dv), dtype=v.dtype, device=dev)
     if T == 0:
         return out
     ws_bytes = L.recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype_code)
     ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
-
-    def ptr(t):
-        return None if t is None else t.data_ptr()
-
     with torch.cuda.device(dev):
-        rc = L.recir_hstu_attn_fwd(ptr(q), ptr(k), ptr(v), ptr(out), ptr(off), ptr(nt), ptr(rb),
-                                   ptr(sc), ptr(q_scale), ptr(k_scale), T, B, H, Dqk, Dv, int(N),
+        rc = L.recir_hstu_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(off), _ptr(nt), _ptr(rb),
+                                   _ptr(sc), _ptr(q_scale), _ptr(k_scale), T, B, H, Dqk, Dv, int(N),
                                    int(contextual_seq_len), float(alpha), dtype_code, flags,
-                                   ptr(ws), ws.numel(), stream)
+                                   _ptr(ws), ws.numel(), stream)
     if rc != 0:
-        msg = _lib.last_error()
-        if rc < 0:
-            raise ValueError(f"recir_hstu_attn_fwd rejected the call ({rc}): {msg}")
-        raise RuntimeError(f"recir_hstu_attn_fwd launch failed (hipError {rc}): {msg}")
+        _raise_status("recir_hstu_attn_fwd", rc)
     return out
+
+
+def _dtype_code(q, k, v):
+    if q.dtype == torch.bfloat16:
+        code = _lib.DTYPE_BF16
+    elif q.dtype == torch.float32:
+        code = _lib.DTYPE_FP32
+    else:
+        raise ValueError(f"q must be bfloat16 or float32, got {q.dtype}")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k and v must share one dtype")
+    return code
+
+
+def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
+                rab=None):
+    L = _lib.load()
+    dev = q.device
+    code = _dtype_code(q, k, v)
+    B, off, nt, sc, rb, flags = _prepare("hstu_jagged_attention_bwd", q, k, v, seq_offsets, num_targets,
+                                         attn_scale, rab, N)
+    if dout.shape != v.shape:
+        raise ValueError("dout must have the shape of v, [T, H, Dv]")
+    if dout.device != dev:
+        raise ValueError(f"dout is on {dout.device}, q on {dev}")
+    T, H, Dqk = q.shape
+    Dv = v.shape[2]
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    dout = dout.to(q.dtype).contiguous()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    if T == 0:
+        return dq, dk, dv
+    ws_bytes = L.recir_hstu_attn_bwd_workspace_bytes(T, B, H, Dqk, Dv, code)
+    ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    with torch.cuda.device(dev):
+        rc = L.recir_hstu_attn_bwd(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv),
+                                   _ptr(off), _ptr(nt), _ptr(rb), _ptr(sc), T, B, H, Dqk, Dv, int(N),
+                                   int(contextual_seq_len), float(alpha), code, flags, _ptr(ws),
+                                   ws.numel(), stream)
+    if rc != 0:
+        _raise_status("recir_hstu_attn_bwd", rc)
+    return dq, dk, dv
 
 
 def _fwd_device(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
@@ -184,14 +244,7 @@ def _fwd_device(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targ
         raise ValueError("only the causal mask ('lower_triangular') is supported")
     if max_attn_len != 0 or full_attn_size != 0:
         raise ValueError("max_attn_len and full_attn_size (semi-local attention) are unsupported")
-    if q.dtype == torch.bfloat16:
-        code = _lib.DTYPE_BF16
-    elif q.dtype == torch.float32:
-        code = _lib.DTYPE_FP32
-    else:
-        raise ValueError(f"q must be bfloat16 or float32, got {q.dtype}")
-    if k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError("q, k and v must share one dtype")
+    code = _dtype_code(q, k, v)
     out = _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, None, None, N, alpha,
                   contextual_seq_len, code)
     return out, torch.zeros((1,), dtype=torch.float32, device=q.device)
@@ -244,6 +297,8 @@ def _no_cpu(*args, **kwargs):
 _LIBRARY.impl("hstu_jagged_attention_fwd", _fwd_device, "CUDA")
 _LIBRARY.impl("hstu_jagged_attention_fp8_fwd", _fp8_fwd_device, "CUDA")
 _LIBRARY.impl("hstu_quantize_e4m3_per_head", _quant_device, "CUDA")
+_LIBRARY.impl("hstu_jagged_attention_bwd", _bwd_device, "CUDA")
+_LIBRARY.impl("hstu_jagged_attention_bwd", _no_cpu, "CPU")
 _LIBRARY.impl("hstu_jagged_attention_fwd", _no_cpu, "CPU")
 _LIBRARY.impl("hstu_jagged_attention_fp8_fwd", _no_cpu, "CPU")
 _LIBRARY.impl("hstu_quantize_e4m3_per_head", _no_cpu, "CPU")
@@ -269,7 +324,35 @@ def _quant_fake(x):
     return x.new_empty(x.shape, dtype=torch.float8_e4m3fn), x.new_empty((x.shape[1],), dtype=torch.float32)
 
 
+@torch.library.register_fake("recir::hstu_jagged_attention_bwd")
+def _bwd_fake(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab=None):
+    _check_common(q, k, v, seq_offsets, num_targets, N)
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _setup_context(ctx, inputs, output):
+    (N, alpha, q, k, v, seq_offsets, _mask_type, num_targets, attn_scale, _max_attn_len,
+     contextual_seq_len, _full_attn_size, _num_softmax_heads, rab) = inputs
+    ctx.save_for_backward(q, k, v, seq_offsets, num_targets, attn_scale, rab)
+    ctx.hstu_args = (int(N), float(alpha), int(contextual_seq_len))
+
+
+def _autograd_backward(ctx, grad_out, _grad_aux):
+    q, k, v, seq_offsets, num_targets, attn_scale, rab = ctx.saved_tensors
+    N, alpha, contextual_seq_len = ctx.hstu_args
+    dq, dk, dv = torch.ops.recir.hstu_jagged_attention_bwd(
+        grad_out, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab)
+    # one gradient slot per forward argument; attn_scale and rab receive none
+    return (None, None, dq, dk, dv, None, None, None, None, None, None, None, None, None)
+
+
+# gradients of q, k and v flow through the backward operator (the reference attaches its backward
+# the same way: recir/ops/pallas/hstu_attention.py:451-459, custom vjp around the kernels)
+torch.library.register_autograd("recir::hstu_jagged_attention_fwd", _autograd_backward,
+                                setup_context=_setup_context)
+
 hstu_jagged_attention_fwd = torch.ops.recir.hstu_jagged_attention_fwd
+hstu_jagged_attention_bwd = torch.ops.recir.hstu_jagged_attention_bwd
 
 
 def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len: int,
@@ -290,6 +373,24 @@ def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len
                                        "lower_triangular", num_targets, attn_scale, 0,
                                        int(contextual_seq_len), 0, 0, rab)
     return out
+
+
+def jagged_hstu_attention_backward(dout, q, k, v, seq_offsets, num_targets=None, attn_scale=None, *,
+                                   max_seq_len: int, alpha: Optional[float] = None,
+                                   contextual_seq_len: int = 0, rab=None):
+    """``(dq, dk, dv)`` of ``jagged_hstu_attention`` for the upstream gradient ``dout [T, H, Dv]``;
+    argument order and defaults of ``pallas_jagged_hstu_attention_backward``
+    (recir/ops/pallas/jagged_hstu_attention.py:1343-1358; called that way by its own test,
+    recir/ops/pallas/tests/test_jagged_hstu_attention.py:248-262) and of ``hstu_ragged_attention_bwd_jax_fn``
+    (recir/ops/helion/jagged_hstu_attention.py:875-920).  Rows at and after ``seq_offsets[-1]`` of
+    the three gradients are zero.  No gradient is produced for ``rab`` or ``attn_scale``."""
+    _check_common(q, k, v, seq_offsets, num_targets, max_seq_len)
+    if alpha is None:
+        alpha = 1.0 / math.sqrt(q.shape[2])
+    if attn_scale is not None and not isinstance(attn_scale, torch.Tensor):
+        attn_scale = torch.tensor(float(attn_scale), dtype=torch.float32, device=q.device)
+    return hstu_jagged_attention_bwd(dout, int(max_seq_len), float(alpha), q, k, v, seq_offsets,
+                                     num_targets, attn_scale, int(contextual_seq_len), rab)
 
 
 def quantize_e4m3_per_head(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:

@@ -37,7 +37,7 @@ def test_header_symbols_are_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.recir_hstu_abi_version() == 1
+    assert lib.recir_hstu_abi_version() == 2
 
 
 def test_workspace_size_is_host_arithmetic(lib):
@@ -67,6 +67,44 @@ def test_invalid_arguments_are_rejected_before_launch(lib, kw, needle):
                                  a["dtype"], 0, None, 0, None)
     assert rc < 0
     assert needle in lib.recir_hstu_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(T=-1), "negative size"),
+    (dict(H=0), "must be positive"),
+    (dict(N=0), "max_seq_len"),
+    (dict(dtype=2), "bf16 and fp32"),
+    (dict(dq=None), "non-null"),
+    (dict(off=None), "seq_offsets"),
+])
+def test_backward_invalid_arguments_are_rejected_before_launch(lib, kw, needle):
+    a = dict(dout=8, q=8, k=8, v=8, dq=8, dk=8, dv=8, off=8, T=4, B=1, H=1, Dqk=8, Dv=8, N=4, ctx=0, dtype=1)
+    a.update(kw)
+    rc = lib.recir_hstu_attn_bwd(a["dout"], a["q"], a["k"], a["v"], a["dq"], a["dk"], a["dv"], a["off"], None,
+                                 None, None, a["T"], a["B"], a["H"], a["Dqk"], a["Dv"], a["N"], a["ctx"], 1.0,
+                                 a["dtype"], 0, None, 0, None)
+    assert rc < 0
+    assert needle in lib.recir_hstu_last_error().decode()
+
+
+def test_backward_fake_kernel_and_autograd_wiring():
+    """The backward operator traces with fake tensors, and the forward operator has an autograd
+    formula that routes q, k, v gradients through it."""
+    import recir_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q = torch.empty(10, 2, 8, dtype=torch.bfloat16, requires_grad=True)
+        v = torch.empty(10, 2, 6, dtype=torch.bfloat16, requires_grad=True)
+        off = torch.empty(3, dtype=torch.int64)
+        dq, dk, dv = torch.ops.recir.hstu_jagged_attention_bwd(torch.empty_like(v), 8, 0.5, q, q, v, off,
+                                                               None, None, 0)
+        assert dq.shape == q.shape and dk.shape == q.shape and dv.shape == v.shape
+        out, _ = torch.ops.recir.hstu_jagged_attention_fwd(8, 0.5, q, q, v, off, "lower_triangular",
+                                                          None, None, 0, 0, 0)
+        assert out.requires_grad
+        out.sum().backward()
+        assert q.grad.shape == q.shape and v.grad.shape == v.shape
 
 
 def test_empty_input_is_ok_without_launch(lib):
