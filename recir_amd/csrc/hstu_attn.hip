@@ -11,6 +11,7 @@
 //   hstu_fwd_tiled_d128     bf16 / fp8-qk tiled MFMA kernel, head dim 128
 //   hstu_fwd_generic        any head dim, fp32 or bf16, one wave per (token, head)
 //   hstu_bwd_generic_dq / hstu_bwd_generic_dkv   backward, any head dim, one wave per (token, head)
+//   hstu_bwd_dq_d128 / hstu_bwd_dkv_d128         backward, bf16 tiled MFMA kernels, head dim 128
 //   hstu_fill_zero          out := 0 when there are no sequences
 //   hstu_amax_per_head / hstu_quant_e4m3_per_head   per-head fp8 quantiser
 #include <hip/hip_runtime.h>
@@ -27,6 +28,7 @@
 #include "hstu_tiled_d128_dl.h"
 #include "hstu_tiled_d128_w64.h"
 #include "hstu_bwd_generic.h"
+#include "hstu_bwd_d128.h"
 
 using namespace recir_hstu;
 
@@ -305,9 +307,9 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     p.grid_slots = (int)slots;
     if (!(flags & RECIR_HSTU_FLAG_REUSE_PLAN)) {
       if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS)
-        hipLaunchKernelGGL(hstu_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, p, bm);
+        hipLaunchKernelGGL(hstu_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, p, bm, 0);
       else
-        hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, p, bm);
+        hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, p, bm, 0);
       if (int rc = launch_status("hstu_plan_kernel")) return rc;
     }
     const dim3 grid((unsigned)(slots * NUM_XCD));
@@ -369,7 +371,6 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
                         float alpha, int32_t dtype, uint32_t flags, void* workspace,
                         size_t workspace_bytes, void* hip_stream) {
   hipStream_t stream = (hipStream_t)hip_stream;
-  (void)workspace; (void)workspace_bytes;
   if (T < 0 || B < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "negative size: T=%d B=%d", T, B);
   if (H <= 0 || Dqk <= 0 || Dv <= 0)
     return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "H, Dqk, Dv must be positive: H=%d Dqk=%d Dv=%d", H, Dqk, Dv);
@@ -409,6 +410,51 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   if (Dqk > BWD_GENERIC_MAX_D || Dv > BWD_GENERIC_MAX_D)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "head dims above %d are not supported (Dqk=%d Dv=%d)", BWD_GENERIC_MAX_D, Dqk, Dv);
   if ((unsigned)H > 65535u) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "more than 65535 heads");
+  const unsigned variant = (flags & RECIR_HSTU_FLAG_KERNEL_MASK) >> RECIR_HSTU_FLAG_KERNEL_SHIFT;
+  // the tiled kernels cover bf16, head dim 128, a scalar output scale and no score bias
+  const bool tiled_ok = bf16 && Dqk == HD && Dv == HD && !rab && !(flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) &&
+                        (((size_t)dout | (size_t)q | (size_t)k | (size_t)v | (size_t)dq | (size_t)dk | (size_t)dv) & 15) == 0;
+  if (variant >= 2 && !tiled_ok)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "tiled backward needs bf16, Dqk = Dv = 128, 16-byte aligned tensors, "
+                "a scalar attn_scale and no rab");
+  if (tiled_ok && variant != 1) {
+    const size_t half_ws = (recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype) + 255) & ~(size_t)255;
+    if (!workspace || workspace_bytes < 2 * half_ws || ((size_t)workspace & 15))
+      return fail(RECIR_HSTU_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu at %p",
+                  2 * half_ws, workspace_bytes, workspace);
+    const size_t items = max_items(T, B, H);
+    const size_t per_seq = (size_t)(max_seq_len + BWD_BM - 1) / BWD_BM;
+    const size_t items_bm = ((size_t)((T + BWD_BM - 1) / BWD_BM) + (size_t)B) * (size_t)H;
+    size_t slots = (items_bm + NUM_XCD - 1) / NUM_XCD + 2 * per_seq + 1;
+    if (slots > items_bm) slots = items_bm;
+    if (slots < 1) slots = 1;
+    if (items > 0x7fffffffull || slots * NUM_XCD > 0x7fffffffull) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "grid too large");
+    // two work lists: query tiles (heaviest = last tile of a sequence) and key tiles (heaviest = first)
+    BwdParams bq = bp, bk = bp;
+    bq.f.ws_counts = (int*)workspace;
+    bq.f.ws_items = (WorkItem*)((char*)workspace + WS_HEADER);
+    bk.f.ws_counts = (int*)((char*)workspace + half_ws);
+    bk.f.ws_items = (WorkItem*)((char*)workspace + half_ws + WS_HEADER);
+    bq.f.items_cap = bk.f.items_cap = (int)items;
+    bq.f.grid_slots = bk.f.grid_slots = (int)slots;
+    if (!(flags & RECIR_HSTU_FLAG_REUSE_PLAN)) {
+      for (int rev = 0; rev < 2; ++rev) {
+        const Params& pp = rev ? bk.f : bq.f;
+        if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS)
+          hipLaunchKernelGGL(hstu_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, pp, BWD_BM, rev);
+        else
+          hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, pp, BWD_BM, rev);
+        if (int rc = launch_status("hstu_plan_kernel")) return rc;
+      }
+    }
+    const dim3 grid((unsigned)(slots * NUM_XCD));
+    hipLaunchKernelGGL(hstu_bwd_dkv_d128, grid, dim3(256), 0, stream, bk);
+    if (int rc = launch_status("hstu_bwd_dkv_d128")) return rc;
+    hipLaunchKernelGGL(hstu_bwd_dq_d128, grid, dim3(256), 0, stream, bq);
+    if (int rc = launch_status("hstu_bwd_dq_d128")) return rc;
+    g_last_kernel = "bwd_tiled_d128_bf16";
+    return RECIR_HSTU_OK;
+  }
   const dim3 grid((unsigned)T, (unsigned)H);
   if (bf16) {
     hipLaunchKernelGGL(hstu_bwd_generic_dq<true>, grid, dim3(64), 0, stream, bp);

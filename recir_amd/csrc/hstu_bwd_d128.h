@@ -1,0 +1,467 @@
+// Tiled MFMA kernels of the HSTU attention backward, head dim 128 (qk and v), bf16 tensors,
+// scalar output scale, no score bias.
+//
+// Two kernels, as in the reference (recir/ops/pallas/jagged_hstu_attention.py:724-1339 and
+// recir/ops/helion/jagged_hstu_attention.py:356-570): every gradient row has one writer.
+//
+//   hstu_bwd_dq_d128   one workgroup (4 waves x 32 query rows) per (sequence, head, 128-row query
+//                      tile); walks the key tiles of 64 rows the forward walks.  Per 32-key block:
+//                        S^T  = K Q^T        A = K rows from LDS,   B = Q (registers)
+//                        dP^T = V dO^T       A = V rows from LDS,   B = dO (registers)
+//                        dS^T = dP^T keep silu'(S^T), rounded to bf16 in registers: the 32 x 32
+//                               accumulator layout is the B-operand layout of the next product
+//                        dQ^T += K^T dS^T    A = K^T, transposing LDS read of the same K tile
+//   hstu_bwd_dkv_d128  one workgroup (4 waves x 32 key rows) per (sequence, head, 128-row key tile);
+//                      walks the query tiles of 64 rows that see those keys.  Per 32-query block:
+//                        S  = Q K^T          A = Q rows from LDS,   B = K (registers)
+//                        dP = dO V^T         A = dO rows from LDS,  B = V (registers)
+//                        P  = silu(S) keep, dS = dP keep silu'(S), both rounded to bf16
+//                        dV^T += dO^T P      A = dO^T, transposing LDS read of the dO tile
+//                        dK^T += Q^T dS      A = Q^T, transposing LDS read of the Q tile
+// The operand that multiplies the scores (Q in the first kernel, K in the second) is pre-multiplied
+// by alpha * log2(e) and rounded back to bf16, so sigmoid needs exp2 only; alpha and the output
+// scale are applied once to the fp32 accumulators.
+//
+// LDS tile layout, shared by all four staged matrices: [64 rows][256 bytes], 16-byte chunk c of row
+// r stored at chunk c ^ f(r & 7) with f(r) = ((r & 3) << 1) | (r >> 2).  Eight consecutive rows then
+// put one logical chunk on all banks (ds_read_b128 fragments), and four consecutive rows put one
+// logical 32-byte slot on all banks (ds_read_b64_tr_b16 fragments), so both read patterns of a
+// tile are free of bank conflicts.  Tiles travel HBM -> LDS with global_load_lds_dwordx4 (64 lanes
+// x 16 bytes land on consecutive LDS addresses; the swizzle is applied to the address each lane
+// fetches), two stages, one barrier per tile.
+#pragma once
+#include <type_traits>
+
+#include "hstu_common.h"
+#include "hstu_tiled_d128.h"     // HD, kLog2e
+#include "hstu_tiled_d128_dl.h"  // i16x4, i16x8, lds_void, lds_i16x4
+
+namespace recir_hstu {
+
+constexpr int BWD_BM = 128;  // rows a workgroup owns (query rows for dQ, key rows for dK/dV)
+constexpr int BWD_BN = 64;   // rows of a staged tile
+constexpr float kLn2 = 0.6931471805599453f;
+
+// per-lane constants of the LDS access patterns
+struct BwdLanes {
+  unsigned rd;        // ds_read_b128 fragment: row l32 of a 32-row block, chunk (2 kk + half)
+  unsigned tr_e;      // transposing fragment, even 32-column block
+  unsigned tr_o;      // ... odd block
+  int ld_row;         // row (0..3) and physical chunk a lane fills in one copy instruction
+  int ld_chunk;
+  unsigned ld_swz_e;  // logical chunk fetched for copy instructions with even / odd index
+  unsigned ld_swz_o;
+};
+
+__device__ __forceinline__ BwdLanes bwd_lanes(int lane) {
+  const int l32 = lane & 31, half = lane >> 5;
+  BwdLanes c;
+  const unsigned f = (unsigned)(((l32 & 3) << 1) | ((l32 >> 2) & 1));
+  c.rd = (unsigned)l32 * 256u + (((unsigned)half ^ f) * 16u);
+  // transposing read: source lane s = lane & 15 of a 16-lane group supplies the 8 bytes at row
+  // 4 half + (s >> 2) (+ 16 per k-step + 8 for the second read) and columns
+  // 32 db + 16 dgrp + 4 (s & 3) .. + 3; the row's swizzle value is ((s >> 2) << 1) | half
+  const int s = lane & 15, tr_r = s >> 2, tr_c = s & 3, dgrp = (lane >> 4) & 1;
+  const unsigned x = (unsigned)(2 * dgrp + (tr_c >> 1)) ^ (unsigned)((tr_r << 1) | half);
+  const unsigned row = (unsigned)(4 * half + tr_r) * 256u + (unsigned)(tr_c & 1) * 8u;
+  c.tr_e = row + x * 16u;
+  c.tr_o = row + (x ^ 4u) * 16u - 64u;
+  c.ld_row = lane >> 4;
+  c.ld_chunk = lane & 15;
+  c.ld_swz_e = (unsigned)(c.ld_chunk ^ (c.ld_row << 1));
+  c.ld_swz_o = (unsigned)(c.ld_chunk ^ ((c.ld_row << 1) | 1));
+  return c;
+}
+
+// A-operand fragment of rows [32 blk, 32 blk + 32) x columns [16 kk, 16 kk + 16) of a staged tile
+__device__ __forceinline__ bf16x8 bwd_row_frag(const char* tile, const BwdLanes& c, int blk, int kk) {
+  return *(const bf16x8*)(tile + blk * 32 * 256 + (c.rd ^ (unsigned)((kk & 3) * 32)) + (kk >> 2) * 128);
+}
+
+// A-operand fragment of the transposed tile: columns [32 db, 32 db + 32) x rows [16 s2, 16 s2 + 16)
+__device__ __forceinline__ bf16x8 bwd_tr_frag(const char* tile, const BwdLanes& c, int db, int s2) {
+  const char* a = tile + ((db & 1) ? c.tr_o : c.tr_e) + db * 64 + s2 * 16 * 256;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)a);
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a + 8 * 256));
+  const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, both);
+}
+
+// This wave's share (4 of 16 instructions) of the copy of rows [r_first, r_first + 64) of a
+// [rows, H, 128] bf16 matrix into a staged tile.  Rows past `last` (relative to r_first) re-read
+// row `last`; what they contribute is masked by the caller.
+__device__ __forceinline__ void bwd_issue_rows(const char* gbase, unsigned row_bytes, int last, unsigned short* tile,
+                                               const BwdLanes& c, int wave) {
+#pragma unroll
+  for (int ps = 0; ps < 4; ++ps) {
+    const int j = 4 * wave + ps;
+    const int row = min(4 * j + c.ld_row, last);
+    const unsigned chunk = (ps & 1) ? c.ld_swz_o : c.ld_swz_e;
+    const char* src = gbase + (size_t)row * row_bytes + chunk * 16u;
+    __builtin_amdgcn_global_load_lds((const unsigned*)src, (lds_void*)&tile[j * 512], 16, 0, 0);
+  }
+}
+
+// B-operand fragments of one [*, H, 128] bf16 row: columns 16 kk + 8 half .. + 7, optionally
+// multiplied by `mul` and rounded back to bf16
+__device__ __forceinline__ void bwd_load_row_frags(const void* base, size_t row, int H, int h, int half, bool valid,
+                                                   bool scaled, float mul, bf16x8 (&f)[8]) {
+  const unsigned short* src = (const unsigned short*)base + ((size_t)(valid ? row : 0) * H + h) * HD;
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  u32x4 t[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) t[kk] = valid ? *(const u32x4*)(src + kk * 16 + half * 8) : zero4;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    u32x4 sc = t[kk];
+    if (scaled) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sc[i] = pack_bf16x2(__uint_as_float(t[kk][i] << 16) * mul, __uint_as_float(t[kk][i] & 0xffff0000u) * mul);
+    }
+    f[kk] = __builtin_bit_cast(bf16x8, sc);
+  }
+}
+
+__device__ __forceinline__ float bwd_output_scale(const Params& p) {
+  return p.attn_scale ? p.attn_scale[0] : 1.0f / (float)p.N;
+}
+
+// ---------------------------------------------------------------------------------------------
+// dQ
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void hstu_bwd_dq_d128(BwdParams bp) {
+  const Params& p = bp.f;
+  __shared__ __attribute__((aligned(1024))) unsigned short Ks0[BWD_BN * HD];
+  __shared__ __attribute__((aligned(1024))) unsigned short Ks1[BWD_BN * HD];
+  __shared__ __attribute__((aligned(1024))) unsigned short Vs0[BWD_BN * HD];
+  __shared__ __attribute__((aligned(1024))) unsigned short Vs1[BWD_BN * HD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int half = lane >> 5;
+  const BwdLanes lc = bwd_lanes(lane);
+
+  zero_tail_rows_of<256>(p, bp.dq, (size_t)p.H * HD * 2);
+
+  const int xcd = blockIdx.x % NUM_XCD;
+  const int list_len = p.ws_counts[xcd];
+  const WorkItem* __restrict__ list = p.ws_items + (size_t)xcd * p.items_cap;
+  for (int slot = blockIdx.x / NUM_XCD; slot < list_len; slot += p.grid_slots) {
+    const WorkItem wi = list[slot];
+    SeqInfo si;
+    si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
+    const int q0 = wi.q0;
+    const int h = wi.h;
+    const unsigned row_bytes = (unsigned)p.H * HD * 2u;
+    const char* __restrict__ kgb = (const char*)p.k + ((size_t)si.s * p.H + h) * (HD * 2);
+    const char* __restrict__ vgb = (const char*)p.v + ((size_t)si.s * p.H + h) * (HD * 2);
+
+    const int qw0 = q0 + wave * 32;
+    const int m = qw0 + l32;
+    const int m_lo = qw0;
+    const int m_hi = min(qw0 + 31, si.n - 1);
+    const bool wave_has_rows = m_lo < si.n;
+
+    // key tiles [0, nkv) minus the run [skip_a, skip_b) that holds only target keys off this query
+    // tile's diagonal (and no contextual key): the tiles the forward walks
+    const int kv_end = min(si.n, max(q0 + BWD_BM, si.ctx_eff));
+    const int nkv = (kv_end + BWD_BN - 1) / BWD_BN;
+    const int cap0 = si.cap > 0 ? si.cap : 0;
+    const int skip_a = (max(cap0, si.ctx_eff) + BWD_BN - 1) / BWD_BN;
+    const int skip_b = q0 / BWD_BN;
+    const bool has_skip = skip_a < skip_b;
+    auto next_tile = [&](int it) { return (has_skip && it + 1 == skip_a) ? skip_b : it + 1; };
+
+    auto issue_tile = [&](int it, auto buf_tag) __attribute__((always_inline)) {
+      constexpr int BUF = decltype(buf_tag)::value;
+      const int k0 = it * BWD_BN;
+      const int last = si.n - 1 - k0;
+      bwd_issue_rows(kgb + (size_t)k0 * row_bytes, row_bytes, last, BUF ? Ks1 : Ks0, lc, wave);
+      bwd_issue_rows(vgb + (size_t)k0 * row_bytes, row_bytes, last, BUF ? Vs1 : Vs0, lc, wave);
+    };
+
+    int it = (has_skip && skip_a == 0) ? skip_b : 0;
+    if (it < nkv) issue_tile(it, std::integral_constant<int, 0>{});
+
+    bf16x8 qf[8], gf[8];
+    bwd_load_row_frags(p.q, (size_t)si.s + m, p.H, h, half, m < si.n, true, p.alpha * kLog2e, qf);
+    bwd_load_row_frags(bp.dout, (size_t)si.s + m, p.H, h, half, m < si.n, false, 1.0f, gf);
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+
+    auto tile_body = [&](auto masked_tag, auto buf_tag, int k0) __attribute__((always_inline)) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      constexpr int BUF = decltype(buf_tag)::value;
+      const char* kb = (const char*)(BUF ? Ks1 : Ks0);
+      const char* vb = (const char*)(BUF ? Vs1 : Vs0);
+      const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kvb = 0; kvb < 2; ++kvb) {
+        f32x16 st = zero, dpt = zero;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(kb, lc, kvb, kk), qf[kk], st, 0, 0, 0);
+          dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(vb, lc, kvb, kk), gf[kk], dpt, 0, 0, 0);
+        }
+        // dS^T = dP^T silu'(S^T) on the kept pairs; element r of the block is key
+        // 32 kvb + 8 (r / 4) + 4 half + r % 4 for this lane's query row
+        u32x4 w0, w1;
+        float ds[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float u = st[r];
+          const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
+          const float sv = u * kLn2;
+          float g = dpt[r] * (sig * (1.0f + sv * (1.0f - sig)));
+          if (MASKED) {
+            const int j = k0 + kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            const bool kp = ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
+            g = kp ? g : 0.f;
+          }
+          ds[r] = g;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          w0[i] = pack_bf16x2(ds[2 * i], ds[2 * i + 1]);
+          w1[i] = pack_bf16x2(ds[8 + 2 * i], ds[8 + 2 * i + 1]);
+        }
+        const bf16x8 b0 = __builtin_bit_cast(bf16x8, w0), b1 = __builtin_bit_cast(bf16x8, w1);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(kb, lc, db, 2 * kvb), b0, acc[db], 0, 0, 0);
+          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(kb, lc, db, 2 * kvb + 1), b1, acc[db], 0, 0, 0);
+        }
+      }
+    };
+
+    auto compute_tile = [&](int itc, auto buf_tag) __attribute__((always_inline)) {
+      const int k0 = itc * BWD_BN;
+      const int k1 = k0 + BWD_BN;
+      const bool any_kept = wave_has_rows && ((k0 <= m_hi && k1 > m_lo) || (k0 < si.cap && k0 <= m_hi) ||
+                                              (k0 < si.ctx_eff));
+      if (!any_kept) return;
+      const bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
+      if (full) tile_body(std::false_type{}, buf_tag, k0);
+      else tile_body(std::true_type{}, buf_tag, k0);
+    };
+
+    // two tiles per trip so that the stage index is a compile-time constant
+    while (it < nkv) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile `it` have landed
+      __syncthreads();                                   // everybody's; the other stage is free again
+      int nxt = next_tile(it);
+      if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, 1>{});
+      compute_tile(it, std::integral_constant<int, 0>{});
+      it = nxt;
+      if (it >= nkv) break;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      nxt = next_tile(it);
+      if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, 0>{});
+      compute_tile(it, std::integral_constant<int, 1>{});
+      it = nxt;
+    }
+
+    // dQ^T accumulators -> dq[s + m, h, :]; element 4 rq + i of block db is column 32 db + 8 rq + 4 half + i
+    if (m < si.n) {
+      const float oscale = p.alpha * bwd_output_scale(p);
+      unsigned short* orow = (unsigned short*)bp.dq + ((size_t)(si.s + m) * p.H + h) * HD;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          u32x2 o;
+          o.x = pack_bf16x2(acc[db][4 * rq + 0] * oscale, acc[db][4 * rq + 1] * oscale);
+          o.y = pack_bf16x2(acc[db][4 * rq + 2] * oscale, acc[db][4 * rq + 3] * oscale);
+          *(u32x2*)(orow + db * 32 + 8 * rq + 4 * half) = o;
+        }
+      }
+    }
+    __syncthreads();  // LDS stages are reused by the next item
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// dK, dV
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
+  const Params& p = bp.f;
+  __shared__ __attribute__((aligned(1024))) unsigned short Qs0[BWD_BN * HD];
+  __shared__ __attribute__((aligned(1024))) unsigned short Qs1[BWD_BN * HD];
+  __shared__ __attribute__((aligned(1024))) unsigned short Gs0[BWD_BN * HD];
+  __shared__ __attribute__((aligned(1024))) unsigned short Gs1[BWD_BN * HD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int half = lane >> 5;
+  const BwdLanes lc = bwd_lanes(lane);
+
+  zero_tail_rows_of<256>(p, bp.dk, (size_t)p.H * HD * 2);
+  zero_tail_rows_of<256>(p, bp.dv, (size_t)p.H * HD * 2);
+
+  const int xcd = blockIdx.x % NUM_XCD;
+  const int list_len = p.ws_counts[xcd];
+  const WorkItem* __restrict__ list = p.ws_items + (size_t)xcd * p.items_cap;
+  for (int slot = blockIdx.x / NUM_XCD; slot < list_len; slot += p.grid_slots) {
+    const WorkItem wi = list[slot];
+    SeqInfo si;
+    si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
+    const int j0 = wi.q0;  // first key row of this workgroup's tile
+    const int h = wi.h;
+    const unsigned row_bytes = (unsigned)p.H * HD * 2u;
+    const char* __restrict__ qgb = (const char*)p.q + ((size_t)si.s * p.H + h) * (HD * 2);
+    const char* __restrict__ ggb = (const char*)bp.dout + ((size_t)si.s * p.H + h) * (HD * 2);
+
+    const int jw0 = j0 + wave * 32;
+    const int j = jw0 + l32;  // this lane's key row
+    const int j_lo = jw0;
+    const int j_hi = min(jw0 + 31, si.n - 1);
+    const bool wave_has_rows = j_lo < si.n;
+
+    // Query tiles that see a key of [j0, j0 + 128): from the diagonal (from 0 when the tile holds a
+    // contextual key) to the end of the sequence when the tile holds a history key, else through
+    // the diagonal only.
+    const int j_end = min(j0 + BWD_BM, si.n);
+    const bool has_ctx = j0 < si.ctx_eff;
+    const bool has_hist = j0 < si.cap;
+    const int t_first = has_ctx ? 0 : j0 / BWD_BN;
+    const int t_last = (has_hist || has_ctx) ? (si.n - 1) / BWD_BN : (j_end - 1) / BWD_BN;  // inclusive
+    const int nq = t_last + 1;
+
+    auto issue_tile = [&](int it, auto buf_tag) __attribute__((always_inline)) {
+      constexpr int BUF = decltype(buf_tag)::value;
+      const int m0 = it * BWD_BN;
+      const int last = si.n - 1 - m0;
+      bwd_issue_rows(qgb + (size_t)m0 * row_bytes, row_bytes, last, BUF ? Qs1 : Qs0, lc, wave);
+      bwd_issue_rows(ggb + (size_t)m0 * row_bytes, row_bytes, last, BUF ? Gs1 : Gs0, lc, wave);
+    };
+
+    int it = t_first;
+    if (it < nq) issue_tile(it, std::integral_constant<int, 0>{});
+
+    bf16x8 kf[8], vf[8];
+    bwd_load_row_frags(p.k, (size_t)si.s + j, p.H, h, half, j < si.n, true, p.alpha * kLog2e, kf);
+    bwd_load_row_frags(p.v, (size_t)si.s + j, p.H, h, half, j < si.n, false, 1.0f, vf);
+
+    f32x16 acck[4], accv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acck[i][r] = accv[i][r] = 0.f;
+
+    auto tile_body = [&](auto masked_tag, auto buf_tag, int m0) __attribute__((always_inline)) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      constexpr int BUF = decltype(buf_tag)::value;
+      const char* qb = (const char*)(BUF ? Qs1 : Qs0);
+      const char* gb = (const char*)(BUF ? Gs1 : Gs0);
+      const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int qb32 = 0; qb32 < 2; ++qb32) {
+        f32x16 s = zero, dp = zero;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(qb, lc, qb32, kk), kf[kk], s, 0, 0, 0);
+          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(gb, lc, qb32, kk), vf[kk], dp, 0, 0, 0);
+        }
+        // element r of the block is query row m0 + 32 qb32 + 8 (r / 4) + 4 half + r % 4, this lane's key
+        float pv[16], ds[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float u = s[r];
+          const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
+          const float sv = u * kLn2;
+          float pe = sv * sig;
+          float g = dp[r] * (sig * (1.0f + sv * (1.0f - sig)));
+          if (MASKED) {
+            const int m = m0 + qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            const bool kp = ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (m < si.n);
+            pe = kp ? pe : 0.f;
+            g = kp ? g : 0.f;
+          }
+          pv[r] = pe;
+          ds[r] = g;
+        }
+        u32x4 p0, p1, d0, d1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p0[i] = pack_bf16x2(pv[2 * i], pv[2 * i + 1]);
+          p1[i] = pack_bf16x2(pv[8 + 2 * i], pv[8 + 2 * i + 1]);
+          d0[i] = pack_bf16x2(ds[2 * i], ds[2 * i + 1]);
+          d1[i] = pack_bf16x2(ds[8 + 2 * i], ds[8 + 2 * i + 1]);
+        }
+        const bf16x8 pb0 = __builtin_bit_cast(bf16x8, p0), pb1 = __builtin_bit_cast(bf16x8, p1);
+        const bf16x8 db0 = __builtin_bit_cast(bf16x8, d0), db1 = __builtin_bit_cast(bf16x8, d1);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          accv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(gb, lc, db, 2 * qb32), pb0, accv[db], 0, 0, 0);
+          accv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(gb, lc, db, 2 * qb32 + 1), pb1, accv[db], 0, 0, 0);
+          acck[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(qb, lc, db, 2 * qb32), db0, acck[db], 0, 0, 0);
+          acck[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(qb, lc, db, 2 * qb32 + 1), db1, acck[db], 0, 0, 0);
+        }
+      }
+    };
+
+    auto compute_tile = [&](int itc, auto buf_tag) __attribute__((always_inline)) {
+      const int m0 = itc * BWD_BN;
+      const int m1 = min(m0 + BWD_BN, si.n);  // exclusive
+      // any pair of (query tile, this wave's keys) kept?
+      const bool any_kept = wave_has_rows && ((m0 <= j_hi && m1 > j_lo) ||           // diagonal
+                                              (j_lo < si.cap && m1 - 1 >= j_lo) ||  // history key, later query
+                                              (j_lo < si.ctx_eff));                  // contextual key
+      if (!any_kept) return;
+      // every pair kept: all keys are history keys (or contextual) below every query row, tile whole
+      const bool full = (m0 + BWD_BN <= si.n) && (jw0 + 31 < si.n) &&
+                        ((jw0 + 31 <= m0 && jw0 + 31 < si.cap) || (jw0 + 31 < si.ctx_eff));
+      if (full) tile_body(std::false_type{}, buf_tag, m0);
+      else tile_body(std::true_type{}, buf_tag, m0);
+    };
+
+    while (it < nq) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      int nxt = it + 1;
+      if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 1>{});
+      compute_tile(it, std::integral_constant<int, 0>{});
+      it = nxt;
+      if (it >= nq) break;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      nxt = it + 1;
+      if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 0>{});
+      compute_tile(it, std::integral_constant<int, 1>{});
+      it = nxt;
+    }
+
+    if (j < si.n) {
+      const float vscale = bwd_output_scale(p);
+      const float kscale = p.alpha * vscale;
+      unsigned short* krow = (unsigned short*)bp.dk + ((size_t)(si.s + j) * p.H + h) * HD;
+      unsigned short* vrow = (unsigned short*)bp.dv + ((size_t)(si.s + j) * p.H + h) * HD;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          u32x2 o;
+          o.x = pack_bf16x2(acck[db][4 * rq + 0] * kscale, acck[db][4 * rq + 1] * kscale);
+          o.y = pack_bf16x2(acck[db][4 * rq + 2] * kscale, acck[db][4 * rq + 3] * kscale);
+          *(u32x2*)(krow + db * 32 + 8 * rq + 4 * half) = o;
+          o.x = pack_bf16x2(accv[db][4 * rq + 0] * vscale, accv[db][4 * rq + 1] * vscale);
+          o.y = pack_bf16x2(accv[db][4 * rq + 2] * vscale, accv[db][4 * rq + 3] * vscale);
+          *(u32x2*)(vrow + db * 32 + 8 * rq + 4 * half) = o;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace recir_hstu

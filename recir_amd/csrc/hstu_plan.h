@@ -9,6 +9,10 @@
 // running index pr = r * H + h and is dealt to the XCDs in boustrophedon order
 // (0..7, 7..0, 0..7, ...), which keeps the list sums within one pair's work of each other.  Inside a
 // list, items are ordered by query-tile index descending, ties in dealing order.
+//
+// With `reverse` set the item at the position of tile index t carries tile nt - 1 - t instead: the
+// backward's key-tile kernel, whose work grows towards the start of a sequence, gets the same
+// heaviest-first order.
 #pragma once
 #include "hstu_common.h"
 
@@ -34,7 +38,7 @@ __device__ __forceinline__ void fill_item(WorkItem& w, const SeqInfo& si, int q0
 }
 
 // Fast path: everything in LDS, one block.
-__global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int bm) {
+__global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int bm, int reverse) {
   __shared__ int nt[PLAN_MAX_B];          // query tiles of sequence b
   __shared__ int seq_of_rank[PLAN_MAX_B];
   __shared__ int nt_by_rank[PLAN_MAX_B];
@@ -99,7 +103,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int b
       int pos = t < ttab ? above[x][t] : tiles_above(x, t);
       for (int k2 = 0; k2 < k; ++k2) pos += xnt[x][k2] > t;
       WorkItem w;
-      fill_item(w, si, t * bm, h, b);
+      fill_item(w, si, (reverse ? my_nt - 1 - t : t) * bm, h, b);
       p.ws_items[(size_t)x * p.items_cap + pos] = w;
     }
   }
@@ -113,7 +117,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int b
 // General path for batches beyond the LDS tables: no ranking, pairs dealt in input order, list
 // positions computed from global memory.  Slow (quadratic in the number of pairs) but only used for
 // batches whose attention work dwarfs it.
-__global__ __launch_bounds__(256) void hstu_plan_kernel_general(Params p, int bm) {
+__global__ __launch_bounds__(256) void hstu_plan_kernel_general(Params p, int bm, int reverse) {
   const int H = p.H;
   const int pairs = p.B * H;
   const int rounds = (pairs + 2 * NUM_XCD - 1) / (2 * NUM_XCD);
@@ -133,7 +137,7 @@ __global__ __launch_bounds__(256) void hstu_plan_kernel_general(Params p, int bm
         }
       }
       WorkItem w;
-      fill_item(w, si, t * bm, h, b);
+      fill_item(w, si, (reverse ? my_nt - 1 - t : t) * bm, h, b);
       p.ws_items[(size_t)x * p.items_cap + pos] = w;
     }
   }

@@ -83,6 +83,12 @@ def test_small_cases_match_backward_oracle_and_golden(oracle, name):
             gotb = run_hip_bwd(wl, dout, attn_scale=scale, num_targets=ntd, dtype="bf16")
         assert all(g.dtype == torch.bfloat16 for g in gotb)
         assert_grads_close(gotb, want, end, BF16_REL, name + " bf16")
+        from recir_amd import _lib
+        assert _lib.last_kernel() == "bwd_tiled_d128_bf16"
+        with ops.reference_contextual_rule(), ops.force_kernel(ops.KERNEL_GENERIC):
+            gotg = run_hip_bwd(wl, dout, attn_scale=scale, num_targets=ntd, dtype="bf16")
+        assert _lib.last_kernel() == "bwd_generic_bf16"
+        assert_grads_close(gotg, want, end, BF16_REL, name + " bf16 generic")
 
 
 @pytest.mark.parametrize("ctx,with_rab,per_token", [(0, True, False), (5, True, True), (3, False, True)])
@@ -134,3 +140,48 @@ def test_backward_of_empty_batch_and_zero_gradient():
     off = torch.tensor([0, 6], device=dev)
     dq, dk, dv = recir_amd.jagged_hstu_attention_backward(torch.zeros_like(q), q, q, q, off, max_seq_len=8)
     assert not dq.any() and not dk.any() and not dv.any()
+
+
+def _mid_workload(seed, lengths, targets, ctx=0):
+    from recir_amd.workloads import make_jagged
+
+    return make_jagged(lengths, targets, 2, 128, 128, max_seq_len=max(lengths) + 8, alpha=1.0 / 128, dtype="bf16",
+                       seed=seed, contextual_seq_len=ctx, tail_rows=5)
+
+
+@pytest.mark.parametrize("ctx", [0, 70])
+def test_tiled_backward_matches_oracle_on_ragged_tiles(oracle, ctx):
+    """Lengths around every tile boundary (64, 128), targets straddling tiles, an all-target and an
+    empty sequence, contextual keys past one tile."""
+    from recir_amd import _lib
+
+    lengths = [1, 63, 64, 65, 127, 128, 129, 0, 191, 257, 330, 90]
+    targets = [0, 3, 64, 1, 100, 0, 129, 0, 60, 2, 200, 90]
+    wl = _mid_workload(31 + ctx, lengths, targets, ctx)
+    g = torch.Generator().manual_seed(9)
+    dout = torch.randn(wl.T, wl.H, 128, generator=g).to(torch.bfloat16).float()
+    scale = torch.tensor(0.02)
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                           attn_scale=np.float32(0.02), contextual_seq_len=ctx)
+    got = run_hip_bwd(wl, dout, attn_scale=scale)
+    assert _lib.last_kernel() == "bwd_tiled_d128_bf16"
+    assert_grads_close(got, want, int(wl.seq_offsets[-1]), BF16_REL, f"ragged ctx{ctx}")
+
+
+def test_tiled_backward_agrees_with_generic_at_full_size():
+    """Config 2 (B=32, up to 2048 tokens per sequence): the tiled MFMA kernels against the generic
+    fp32-arithmetic kernels on the same bf16 tensors."""
+    from recir_amd import _lib, ops
+    from recir_amd.workloads import make_config
+
+    wl = make_config(2)
+    g = torch.Generator().manual_seed(3)
+    dout = torch.randn(wl.T, wl.H, 128, generator=g)
+    got = run_hip_bwd(wl, dout)
+    assert _lib.last_kernel() == "bwd_tiled_d128_bf16"
+    with ops.force_kernel(ops.KERNEL_GENERIC):
+        ref = run_hip_bwd(wl, dout)
+    assert _lib.last_kernel() == "bwd_generic_bf16"
+    end = int(wl.seq_offsets[-1])
+    assert_grads_close(got, [r.float().cpu().numpy() for r in ref], end, BF16_REL, "config2")
