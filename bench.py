@@ -109,6 +109,66 @@ def measured_traffic(config, kernel_name):
     return traffic if kernel == kernel_name else None
 
 
+def bench_backward(args, wl, L, dev):
+    """One step = one call of recir_hstu_attn_bwd (work lists + dK/dV kernel + dQ kernel), inputs
+    resident in HBM.  FLOPs: five products of 2 D per kept pair and head (dP, dV, dQ, dK and the
+    recomputed S counted once), i.e. 2.5 x the forward's."""
+    import torch
+
+    from recir_amd import _lib
+
+    if wl.dtype not in ("bf16", "fp32") or wl.rab is not None:
+        print("--backward supports the bf16/fp32 configurations without a score bias", file=sys.stderr)
+        sys.exit(2)
+    dt = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
+    q, k, v = wl.q.to(dev, dt), wl.k.to(dev, dt), wl.v.to(dev, dt)
+    g = torch.Generator().manual_seed(1)
+    dout = torch.randn(wl.T, wl.H, v.shape[2], generator=g).to(dev, dt)
+    off, nt = wl.seq_offsets.to(dev), wl.num_targets.to(dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    T, H, Dqk = q.shape
+    Dv = v.shape[2]
+    code = _lib.DTYPE_FP32 if wl.dtype == "fp32" else _lib.DTYPE_BF16
+    ws = torch.empty((max(L.recir_hstu_attn_bwd_workspace_bytes(T, wl.B, H, Dqk, Dv, code), 16),), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    flags0 = (args.kernel & 0xFF) << _lib.FLAG_KERNEL_SHIFT
+
+    def call(flags=0):
+        rc = L.recir_hstu_attn_bwd(dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), dq.data_ptr(),
+                                   dk.data_ptr(), dv.data_ptr(), off.data_ptr(), nt.data_ptr(), None, None,
+                                   T, wl.B, H, Dqk, Dv, wl.max_seq_len, wl.contextual_seq_len, wl.alpha, code,
+                                   flags0 | flags, ws.data_ptr(), ws.numel(), ctypes.c_void_p(stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"recir_hstu_attn_bwd failed ({rc}): {_lib.last_error()}")
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        call()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(args.steps):
+        call(_lib.FLAG_REUSE_PLAN)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    kern_ms = ev0.elapsed_time(ev1) / args.steps
+    flops = wl.flops() * 2.5
+    peak = PEAK_TFLOPS[wl.dtype]
+    print(json.dumps({
+        "metric": "HSTU jagged attention bwd (dq, dk, dv), achieved TFLOP/s on unmasked FLOPs (5 products per pair)",
+        "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": wl.dtype, "data": "synthetic",
+        "config": {"workload": describe(wl, args.config), "flops_per_call": flops, "kernel": _lib.last_kernel()},
+        "roofline": {"bound": "mfma", "achieved": flops / (kern_ms * 1e-3) / 1e12, "peak": peak, "unit": "TFLOP/s",
+                     "frac": flops / (kern_ms * 1e-3) / 1e12 / peak, "traffic": None, "kernel_ms": kern_ms},
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -117,6 +177,9 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", type=int, default=0, help="kernel selector (0 auto)")
+    ap.add_argument("--backward", action="store_true",
+                    help="measure the backward entry point (dq, dk, dv) instead of the forward; "
+                         "prints its own JSON line (not the headline metric)")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="BYTES",
                     help="only launch the library's plain copy kernel on BYTES bytes a few times "
                          "(for scaling FETCH_SIZE / WRITE_SIZE counter readings) and exit")
@@ -146,6 +209,8 @@ def main():
         print(json.dumps({"calibration_copy_bytes": n, "launches": 5}))
         return
     wl = make_config(args.config)
+    if args.backward:
+        return bench_backward(args, wl, L, dev)
     fp8 = wl.dtype == "fp8"
     dt = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
     q, k, v = wl.q.to(dev, dt), wl.k.to(dev, dt), wl.v.to(dev, dt)

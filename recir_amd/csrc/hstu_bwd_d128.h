@@ -38,6 +38,11 @@
 
 namespace recir_hstu {
 
+// Waves per SIMD the dQ kernel is compiled for.  At two (256 registers per wave) the compiler spills
+// about 300 registers and the kernel runs three times slower than at one.
+#ifndef BWD_DQ_OCC
+#define BWD_DQ_OCC 1
+#endif
 constexpr int BWD_BM = 128;  // rows a workgroup owns (query rows for dQ, key rows for dK/dV)
 constexpr int BWD_BN = 64;   // rows of a staged tile
 constexpr float kLn2 = 0.6931471805599453f;
@@ -130,7 +135,7 @@ __device__ __forceinline__ float bwd_output_scale(const Params& p) {
 // ---------------------------------------------------------------------------------------------
 // dQ
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 2) void hstu_bwd_dq_d128(BwdParams bp) {
+__global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp) {
   const Params& p = bp.f;
   __shared__ __attribute__((aligned(1024))) unsigned short Ks0[BWD_BN * HD];
   __shared__ __attribute__((aligned(1024))) unsigned short Ks1[BWD_BN * HD];
@@ -192,9 +197,13 @@ __global__ __launch_bounds__(256, 2) void hstu_bwd_dq_d128(BwdParams bp) {
 
     f32x16 acc[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+      // the accumulators are MFMA operands only until the epilogue: start them out in the
+      // accumulation registers, which leaves the 128 ordinary ones to everything else
+      asm volatile("" : "+a"(acc[i]));
+    }
 
     auto tile_body = [&](auto masked_tag, auto buf_tag, int k0) __attribute__((always_inline)) {
       constexpr bool MASKED = decltype(masked_tag)::value;
