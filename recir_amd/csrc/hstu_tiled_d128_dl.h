@@ -131,15 +131,16 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 
     // Copies of one tile: 4 + 4 instructions per wave.  Rows at or past the end of the sequence
     // (last, partial tile only) re-read the sequence's last row; the mask zeroes their contribution.
-    auto issue_tile = [&](int it, auto buf_tag) __attribute__((always_inline)) {
+    auto issue_tile_as = [&](int it, auto buf_tag, auto whole_tag) __attribute__((always_inline)) {
       constexpr int BUF = decltype(buf_tag)::value;
+      constexpr bool KNOWN_WHOLE = decltype(whole_tag)::value;  // caller guarantees k0 + BN <= n
       unsigned short* Kd = BUF ? Ks1 : Ks0;
       unsigned short* Vd = BUF ? Vs1 : Vs0;
       float* rabd = BUF ? rabs1 : rabs0;
       const int k0 = it * BN;
       const char* kt = kgb + (size_t)k0 * krow_bytes;
       const char* vt = vgb + (size_t)k0 * row_bytes;
-      const bool whole = k0 + BN <= si.n;
+      const bool whole = KNOWN_WHOLE || k0 + BN <= si.n;
       const int last = si.n - 1 - k0;
 #pragma unroll
       for (int ps = 0; ps < 4; ++ps) {
@@ -180,6 +181,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
         if (tid < BM + BN - 1) rabd[tid] = rabg[idx] * kLog2e;
       }
+    };
+    auto issue_tile = [&](int it, auto buf_tag) __attribute__((always_inline)) {
+      issue_tile_as(it, buf_tag, std::false_type{});
     };
 
     // first tile in flight before anything else is waited for
@@ -267,8 +271,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     //   A: S1 = K[32:64] Q^T         |  P0 = silu(S0)
     //   B: O += V^T[:, 0:32] P0      |  P1 = silu(S1)
     //   C: O += V^T[:, 32:64] P1     |
-    auto tile_body = [&](auto masked_tag, auto buf_tag, int k0, int nxt) __attribute__((always_inline)) {
+    auto tile_body = [&](auto masked_tag, auto buf_tag, int k0, int nxt, auto fast_tag) __attribute__((always_inline)) {
       constexpr int BUF = decltype(buf_tag)::value;
+      constexpr bool FAST = decltype(fast_tag)::value;  // the next tile exists and is whole
       const char* kb = (const char*)(BUF ? Ks1 : Ks0);
       const char* vb = (const char*)(BUF ? Vs1 : Vs0);
       const float* rabt = BUF ? rabs1 : rabs0;
@@ -326,7 +331,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           return (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
         };
         const i32x8 ka0 = k8_frag(0, 0), ka1 = k8_frag(0, 1);
-        if (nxt < nkv) issue_tile(nxt, other);
+        if constexpr (FAST) issue_tile_as(nxt, other, std::true_type{}); else if (nxt < nkv) issue_tile(nxt, other);
         const i32x8 kb0 = k8_frag(1, 0), kb1 = k8_frag(1, 1);
         s0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ka0, q8[0], zero, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
         s0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ka1, q8[1], s0, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
@@ -338,7 +343,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         silu_pack(masked_tag, s0, k0, 0, rabt, pb0, pb1);
       } else {
       load_group(0, fa);
-      if (nxt < nkv) issue_tile(nxt, other);
+      if constexpr (FAST) issue_tile_as(nxt, other, std::true_type{}); else if (nxt < nkv) issue_tile(nxt, other);
       load_group(1, fb);
       mfma_group(0, fa);
       __builtin_amdgcn_sched_barrier(0);
@@ -411,15 +416,34 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         return;
       }
       const bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
-      if (full) tile_body(std::false_type{}, buf_tag, k0, nxt);
-      else tile_body(std::true_type{}, buf_tag, k0, nxt);
+      if (full) tile_body(std::false_type{}, buf_tag, k0, nxt, std::false_type{});
+      else tile_body(std::true_type{}, buf_tag, k0, nxt, std::false_type{});
     };
+
+    // Leading tiles this wave runs without classifying them: unmasked for all of its rows
+    // (64 t + 63 <= m_lo and 64 t + 64 <= cap), inside the first contiguous run of the walk, and
+    // followed by a tile that exists and is whole.  Taken in pairs (stage 0, stage 1).
+    int fast_pairs = 0;
+    if (wave_has_rows && it == 0) {
+      const int run_end = has_skip ? skip_a : nkv;
+      int fast_end = min(min((m_lo + 1) / BN, cap0 / BN), min(run_end - 1, si.n / BN - 1));
+      fast_pairs = max(fast_end, 0) / 2;
+    }
 
     HSTU_ITEM_STAMP(1);
     if (it < nkv) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       HSTU_ITEM_STAMP(2);
+      for (int pi = 0; pi < fast_pairs; ++pi) {
+        tile_body(std::false_type{}, std::integral_constant<int, 0>{}, it * BN, it + 1, std::true_type{});
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        tile_body(std::false_type{}, std::integral_constant<int, 1>{}, (it + 1) * BN, it + 2, std::true_type{});
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        it += 2;
+      }
       // two tiles per trip so that the stage index is a compile-time constant
       while (true) {
         int nxt = next_tile(it);
