@@ -295,6 +295,8 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     // query rows per workgroup: 256 for the 64-rows-per-wave kernel, else 128
     const bool w64 = variant == 4;
     const int bm = w64 ? BM2 : BM;
+    // only the direct-to-LDS kernel reads the row bound of an item
+    const int plan_mode = (variant == 0 || variant == 3) ? PLAN_SHIFT_ODD : 0;
     // slots per XCD the launch covers: an even share of the items plus the imbalance the dealing of
     // whole (sequence, head) pairs can leave (about one sequence's worth of tiles); longer lists,
     // possible only with sequences above max_seq_len, are walked by the workgroups' stride loop
@@ -307,9 +309,9 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     p.grid_slots = (int)slots;
     if (!(flags & RECIR_HSTU_FLAG_REUSE_PLAN)) {
       if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS)
-        hipLaunchKernelGGL(hstu_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, p, bm, 0);
+        hipLaunchKernelGGL(hstu_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, p, bm, plan_mode);
       else
-        hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, p, bm, 0);
+        hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, p, bm, plan_mode);
       if (int rc = launch_status("hstu_plan_kernel")) return rc;
     }
     const dim3 grid((unsigned)(slots * NUM_XCD));
@@ -441,9 +443,9 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
       for (int rev = 0; rev < 2; ++rev) {
         const Params& pp = rev ? bk.f : bq.f;
         if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS)
-          hipLaunchKernelGGL(hstu_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, pp, BWD_BM, rev);
+          hipLaunchKernelGGL(hstu_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, pp, BWD_BM, rev ? PLAN_REVERSE : PLAN_SHIFT_ODD);
         else
-          hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, pp, BWD_BM, rev);
+          hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, pp, BWD_BM, rev ? PLAN_REVERSE : PLAN_SHIFT_ODD);
         if (int rc = launch_status("hstu_plan_kernel")) return rc;
       }
     }

@@ -159,6 +159,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     SeqInfo si;
     si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
     const int q0 = wi.q0;
+    const int q_end = wi.q_end;  // rows [q0, q_end) belong to this item
     const int h = wi.h;
     const unsigned row_bytes = (unsigned)p.H * HD * 2u;
     const char* __restrict__ kgb = (const char*)p.k + ((size_t)si.s * p.H + h) * (HD * 2);
@@ -167,12 +168,12 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     const int qw0 = q0 + wave * 32;
     const int m = qw0 + l32;
     const int m_lo = qw0;
-    const int m_hi = min(qw0 + 31, si.n - 1);
-    const bool wave_has_rows = m_lo < si.n;
+    const int m_hi = min(qw0 + 31, q_end - 1);
+    const bool wave_has_rows = m_lo < q_end;
 
     // key tiles [0, nkv) minus the run [skip_a, skip_b) that holds only target keys off this query
     // tile's diagonal (and no contextual key): the tiles the forward walks
-    const int kv_end = min(si.n, max(q0 + BWD_BM, si.ctx_eff));
+    const int kv_end = min(si.n, max(q_end, si.ctx_eff));
     const int nkv = (kv_end + BWD_BN - 1) / BWD_BN;
     const int cap0 = si.cap > 0 ? si.cap : 0;
     const int skip_a = (max(cap0, si.ctx_eff) + BWD_BN - 1) / BWD_BN;
@@ -192,8 +193,8 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     if (it < nkv) issue_tile(it, std::integral_constant<int, 0>{});
 
     bf16x8 qf[8], gf[8];
-    bwd_load_row_frags(p.q, (size_t)si.s + m, p.H, h, half, m < si.n, true, p.alpha * kLog2e, qf);
-    bwd_load_row_frags(bp.dout, (size_t)si.s + m, p.H, h, half, m < si.n, false, 1.0f, gf);
+    bwd_load_row_frags(p.q, (size_t)si.s + m, p.H, h, half, m < q_end, true, p.alpha * kLog2e, qf);
+    bwd_load_row_frags(bp.dout, (size_t)si.s + m, p.H, h, half, m < q_end, false, 1.0f, gf);
 
     f32x16 acc[4];
 #pragma unroll
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     }
 
     // dQ^T accumulators -> dq[s + m, h, :]; element 4 rq + i of block db is column 32 db + 8 rq + 4 half + i
-    if (m < si.n) {
+    if (m < q_end) {
       const float oscale = p.alpha * bwd_output_scale(p);
       unsigned short* orow = (unsigned short*)bp.dq + ((size_t)(si.s + m) * p.H + h) * HD;
 #pragma unroll

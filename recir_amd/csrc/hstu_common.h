@@ -28,7 +28,7 @@ struct WorkItem {
   int q0;       // first query row of the tile
   int h;        // head
   int b;        // sequence index
-  int pad;
+  int q_end;    // one past the last query row of the tile (<= n)
 };
 
 struct Params {

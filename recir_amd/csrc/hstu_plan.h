@@ -10,7 +10,7 @@
 // (0..7, 7..0, 0..7, ...), which keeps the list sums within one pair's work of each other.  Inside a
 // list, items are ordered by query-tile index descending, ties in dealing order.
 //
-// With `reverse` set the item at the position of tile index t carries tile nt - 1 - t instead: the
+// With PLAN_REVERSE the item at the position of tile index t carries tile nt - 1 - t instead: the
 // backward's key-tile kernel, whose work grows towards the start of a sequence, gets the same
 // heaviest-first order.
 #pragma once
@@ -32,13 +32,33 @@ __device__ __forceinline__ int snake_slot(int pr) {
   return 2 * (pr / (2 * NUM_XCD)) + ((pr % (2 * NUM_XCD)) >= NUM_XCD ? 1 : 0);
 }
 
-__device__ __forceinline__ void fill_item(WorkItem& w, const SeqInfo& si, int q0, int h, int b) {
+constexpr int PLAN_REVERSE = 1;     // item at the position of tile t carries tile nt - 1 - t
+constexpr int PLAN_SHIFT_ODD = 2;   // see tile_rows
+
+// Rows [q0, q_end) of tile t of a sequence of n rows cut into tiles of bm rows.  Plain cut:
+// [t bm, t bm + bm).  With PLAN_SHIFT_ODD and an odd number of half tiles, tile 0 holds the first
+// half tile only and the others follow it: the half-empty workgroup is then the one with the
+// shortest causal prefix instead of the one with the longest.
+__device__ __forceinline__ void tile_rows(int n, int bm, int t, int mode, int& q0, int& q_end) {
+  const int half = bm >> 1;
+  if ((mode & PLAN_SHIFT_ODD) && (((n + half - 1) / half) & 1)) {
+    q0 = t == 0 ? 0 : half + (t - 1) * bm;
+    q_end = t == 0 ? half : q0 + bm;
+  } else {
+    q0 = t * bm;
+    q_end = q0 + bm;
+  }
+  q_end = min(q_end, n);
+}
+
+__device__ __forceinline__ void fill_item(WorkItem& w, const SeqInfo& si, int bm, int t, int nt, int mode, int h, int b) {
   w.s = si.s; w.n = si.n; w.cap = si.cap; w.ctx_eff = si.ctx_eff;
-  w.q0 = q0; w.h = h; w.b = b; w.pad = 0;
+  w.h = h; w.b = b;
+  tile_rows(si.n, bm, (mode & PLAN_REVERSE) ? nt - 1 - t : t, mode, w.q0, w.q_end);
 }
 
 // Fast path: everything in LDS, one block.
-__global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int bm, int reverse) {
+__global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int bm, int mode) {
   __shared__ int nt[PLAN_MAX_B];          // query tiles of sequence b
   __shared__ int seq_of_rank[PLAN_MAX_B];
   __shared__ int nt_by_rank[PLAN_MAX_B];
@@ -103,7 +123,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int b
       int pos = t < ttab ? above[x][t] : tiles_above(x, t);
       for (int k2 = 0; k2 < k; ++k2) pos += xnt[x][k2] > t;
       WorkItem w;
-      fill_item(w, si, (reverse ? my_nt - 1 - t : t) * bm, h, b);
+      fill_item(w, si, bm, t, my_nt, mode, h, b);
       p.ws_items[(size_t)x * p.items_cap + pos] = w;
     }
   }
@@ -117,7 +137,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int b
 // General path for batches beyond the LDS tables: no ranking, pairs dealt in input order, list
 // positions computed from global memory.  Slow (quadratic in the number of pairs) but only used for
 // batches whose attention work dwarfs it.
-__global__ __launch_bounds__(256) void hstu_plan_kernel_general(Params p, int bm, int reverse) {
+__global__ __launch_bounds__(256) void hstu_plan_kernel_general(Params p, int bm, int mode) {
   const int H = p.H;
   const int pairs = p.B * H;
   const int rounds = (pairs + 2 * NUM_XCD - 1) / (2 * NUM_XCD);
@@ -137,7 +157,7 @@ __global__ __launch_bounds__(256) void hstu_plan_kernel_general(Params p, int bm
         }
       }
       WorkItem w;
-      fill_item(w, si, (reverse ? my_nt - 1 - t : t) * bm, h, b);
+      fill_item(w, si, bm, t, my_nt, mode, h, b);
       p.ws_items[(size_t)x * p.items_cap + pos] = w;
     }
   }

@@ -98,6 +98,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     SeqInfo si;
     si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
     const int q0 = wi.q0;
+    const int q_end = wi.q_end;  // rows [q0, q_end) belong to this item
     const int h = wi.h;
 
     const unsigned row_bytes = (unsigned)p.H * HD * 2u;                   // bf16 rows (v, and k unless FP8)
@@ -116,12 +117,12 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     const int qw0 = q0 + wave * 32;
     const int m = qw0 + l32;
     const int m_lo = qw0;
-    const int m_hi = min(qw0 + 31, si.n - 1);
-    const bool wave_has_rows = m_lo < si.n;
+    const int m_hi = min(qw0 + 31, q_end - 1);
+    const bool wave_has_rows = m_lo < q_end;
 
     // key tiles [0, nkv) minus the run [skip_a, skip_b) that holds only target keys off this query
     // tile's diagonal (and no contextual key)
-    const int kv_end = min(si.n, max(q0 + BM, si.ctx_eff));
+    const int kv_end = min(si.n, max(q_end, si.ctx_eff));
     const int nkv = (kv_end + BN - 1) / BN;
     const int cap0 = si.cap > 0 ? si.cap : 0;
     const int skip_a = (max(cap0, si.ctx_eff) + BN - 1) / BN;
@@ -197,7 +198,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     i32x8 q8[FP8 ? 2 : 1];
     float s_mul = 1.0f;  // fp8: alpha * q_scale[h] * k_scale[h] * log2(e)
     {
-      const bool valid = m < si.n;
+      const bool valid = m < q_end;
       if constexpr (FP8) {
         s_mul = p.alpha * p.q_scale[h] * p.k_scale[h] * kLog2e;
         const char* qrow = (const char*)p.q + ((size_t)(si.s + (valid ? m : 0)) * p.H + h) * HD;
@@ -479,7 +480,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 
     HSTU_ITEM_STAMP(3);
     // ---- epilogue: O^T accumulators -> out[s + m, h, :] ----
-    if (m < si.n) {
+    if (m < q_end) {
       float oscale = 1.0f / (float)p.N;
       if (p.attn_scale)
         oscale = (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) ? p.attn_scale[si.s + m] : p.attn_scale[0];
