@@ -65,6 +65,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int b
   __shared__ int xnt[NUM_XCD][PLAN_MAX_PAIRS / NUM_XCD + 2];  // tiles of the k-th pair of list x
   __shared__ int above[NUM_XCD][PLAN_MAX_TILES + 1];          // tiles of list x with index > t
   __shared__ int tmax_s;
+  __shared__ int seq_s[PLAN_MAX_B], seq_n[PLAN_MAX_B], seq_cap[PLAN_MAX_B], seq_ctx[PLAN_MAX_B];
   const int tid = threadIdx.x;
   const int B = p.B, H = p.H;
   const int pairs = B * H;
@@ -74,7 +75,9 @@ __global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int b
   for (int i = tid; i < NUM_XCD * (PLAN_MAX_PAIRS / NUM_XCD + 2); i += PLAN_THREADS) (&xnt[0][0])[i] = 0;
   __syncthreads();
   for (int b = tid; b < B; b += PLAN_THREADS) {
-    const int v = (seq_info(p, b).n + bm - 1) / bm;
+    const SeqInfo si = seq_info(p, b);  // kept in LDS: the item phase needs it again
+    seq_s[b] = si.s; seq_n[b] = si.n; seq_cap[b] = si.cap; seq_ctx[b] = si.ctx_eff;
+    const int v = (si.n + bm - 1) / bm;
     nt[b] = v;
     atomicMax(&tmax_s, v);
   }
@@ -116,7 +119,8 @@ __global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int b
     const int my_nt = nt_by_rank[r];
     if (t >= my_nt) continue;
     const int b = seq_of_rank[r];
-    const SeqInfo si = seq_info(p, b);
+    SeqInfo si;
+    si.s = seq_s[b]; si.n = seq_n[b]; si.cap = seq_cap[b]; si.ctx_eff = seq_ctx[b];
     for (int h = 0; h < H; ++h) {
       const int pr = r * H + h;
       const int x = snake_xcd(pr), k = snake_slot(pr);
