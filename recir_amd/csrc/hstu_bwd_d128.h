@@ -38,10 +38,10 @@
 
 namespace recir_hstu {
 
-// Waves per SIMD the dQ kernel is compiled for.  At two (256 registers per wave) the compiler spills
-// about 300 registers and the kernel runs three times slower than at one.
+// Waves per SIMD the dQ kernel is compiled for.  Two fit once the phases of its tile body are fenced
+// (the compiler otherwise hoists every fragment read to the top and spills).
 #ifndef BWD_DQ_OCC
-#define BWD_DQ_OCC 1
+#define BWD_DQ_OCC 2
 #endif
 constexpr int BWD_BM = 128;  // rows a workgroup owns (query rows for dQ, key rows for dK/dV)
 constexpr int BWD_BN = 64;   // rows of a staged tile
@@ -201,9 +201,11 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+#if BWD_DQ_OCC == 1
       // the accumulators are MFMA operands only until the epilogue: start them out in the
-      // accumulation registers, which leaves the 128 ordinary ones to everything else
+      // accumulation registers
       asm volatile("" : "+a"(acc[i]));
+#endif
     }
 
     auto tile_body = [&](auto masked_tag, auto buf_tag, int k0) __attribute__((always_inline)) {
@@ -215,11 +217,16 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
 #pragma unroll
       for (int kvb = 0; kvb < 2; ++kvb) {
         f32x16 st = zero, dpt = zero;
+        // phases are fenced so that the fragment reads of one are not hoisted over the previous one
+        // (keeps the live registers within the two-waves-per-SIMD budget)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
           st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(kb, lc, kvb, kk), qf[kk], st, 0, 0, 0);
           dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(vb, lc, kvb, kk), gf[kk], dpt, 0, 0, 0);
+          if (kk == 3) __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_sched_barrier(0);
         // dS^T = dP^T silu'(S^T) on the kept pairs; element r of the block is key
         // 32 kvb + 8 (r / 4) + 4 half + r % 4 for this lane's query row
         u32x4 w0, w1;
@@ -243,11 +250,14 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
           w1[i] = pack_bf16x2(ds[8 + 2 * i], ds[8 + 2 * i + 1]);
         }
         const bf16x8 b0 = __builtin_bit_cast(bf16x8, w0), b1 = __builtin_bit_cast(bf16x8, w1);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
           acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(kb, lc, db, 2 * kvb), b0, acc[db], 0, 0, 0);
           acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(kb, lc, db, 2 * kvb + 1), b1, acc[db], 0, 0, 0);
+          if (db == 1) __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     };
 
