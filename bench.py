@@ -39,6 +39,7 @@ def describe(wl, cfg):
         3: "config3: config2 + rab [4,4095] f32 + contextual_seq_len 8",
         4: "config4: B=8, history Zipf(1.2) clipped [128,8064] + 128 targets, max_seq_len 8192, H=4, D=128, bf16",
         5: "config5: config2 with q,k in fp8 e4m3 (per-head scale amax/448), v bf16",
+        6: "config6: config2 with the semi-local mask (max_attn_len 256, full_attn_size 256)",
     }
     return names[cfg]
 
@@ -136,8 +137,8 @@ def bench_backward(args, wl, L, dev):
     def call(flags=0):
         rc = L.recir_hstu_attn_bwd(dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), dq.data_ptr(),
                                    dk.data_ptr(), dv.data_ptr(), off.data_ptr(), nt.data_ptr(), None, None,
-                                   T, wl.B, H, Dqk, Dv, wl.max_seq_len, wl.contextual_seq_len, wl.alpha, code,
-                                   flags0 | flags, ws.data_ptr(), ws.numel(), ctypes.c_void_p(stream.cuda_stream))
+                                   T, wl.B, H, Dqk, Dv, wl.max_seq_len, wl.contextual_seq_len, wl.max_attn_len,
+                                   wl.full_attn_size, wl.alpha, code, flags0 | flags, ws.data_ptr(), ws.numel(), ctypes.c_void_p(stream.cuda_stream))
         if rc != 0:
             raise RuntimeError(f"recir_hstu_attn_bwd failed ({rc}): {_lib.last_error()}")
 
@@ -174,7 +175,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", type=int, default=0, help="kernel selector (0 auto)")
     ap.add_argument("--backward", action="store_true",
@@ -238,7 +239,8 @@ def main():
     def call(flags=0):
         rc = L.recir_hstu_attn_fwd(ptr(q), ptr(k), ptr(v), ptr(out), ptr(off), ptr(nt), ptr(rab), None,
                                    ptr(q_scale), ptr(k_scale), T, wl.B, H, Dqk, Dv, wl.max_seq_len,
-                                   wl.contextual_seq_len, wl.alpha, dtype_code, base_flags | flags,
+                                   wl.contextual_seq_len, wl.max_attn_len, wl.full_attn_size, wl.alpha,
+                                   dtype_code, base_flags | flags,
                                    ptr(ws), ws.numel(), ctypes.c_void_p(stream.cuda_stream))
         if rc != 0:
             raise RuntimeError(f"recir_hstu_attn_fwd failed ({rc}): {_lib.last_error()}")

@@ -8,7 +8,10 @@
  * Operator computed (per sequence b with tokens [s, e), n = e - s, t = num_targets[b],
  * cap = n - t, local positions m, j in [0, n), head h):
  *
- *   keep(m,j)  = (m == j) or (m >= j and j < cap) or contextual(j)
+ *   keep(m,j)  = (m == j) or (m >= j and j < cap) or contextual(j)                 [causal]
+ *   with max_attn_len A > 0 (semi-local, kjt_split_per_feature.cpp:654-668), i = min(m, cap):
+ *   keep(m,j)  = (m == j) or (j < i and (i - j <= A or (full_attn_size F > 0 and i >= cap - F)))
+ *                or contextual(j)
  *   S(m,j)     = alpha * sum_d q[s+m,h,d] * k[s+j,h,d]  (+ rab[h, m - j + max_seq_len - 1])
  *   P(m,j)     = S * sigmoid(S) * scale          scale = attn_scale or 1 / max_seq_len
  *   out[s+m,h] = sum_j keep(m,j) * P(m,j) * v[s+j,h]
@@ -24,7 +27,7 @@
 extern "C" {
 #endif
 
-#define RECIR_HSTU_ABI_VERSION 2
+#define RECIR_HSTU_ABI_VERSION 3
 
 /* element types of q/k (v and out follow: bf16 for BF16 and FP8_E4M3, fp32 for FP32) */
 #define RECIR_HSTU_DTYPE_BF16 0
@@ -62,8 +65,8 @@ extern "C" {
  *   (recir/ops/kjt_split_per_feature.cpp:602-693, schema :780-783), and the packed accelerator
  *   kernel entry pallas_jagged_hstu_attention (recir/ops/pallas/jagged_hstu_attention.py:1518-1591)
  *   / hstu_ragged_attention_fwd_jax_fn (recir/ops/helion/jagged_hstu_attention.py:830-872).
- *   Only the causal ("lower_triangular") mask with max_attn_len = full_attn_size =
- *   num_softmax_heads = 0 is covered; the host wrapper rejects anything else.
+ *   The causal ("lower_triangular") mask with num_softmax_heads = 0 is covered, plain or
+ *   semi-local (max_attn_len, full_attn_size); the host wrapper rejects anything else.
  *
  * q, k          device, [T, H, Dqk] row-major contiguous, element type `dtype`
  * v, out        device, [T, H, Dv]; out is written in full: rows < seq_offsets[B] get the result,
@@ -74,6 +77,8 @@ extern "C" {
  * rab           device float [H, 2*max_seq_len-1] or NULL.  No counterpart in the reference.
  * attn_scale    device float scalar, [T] with FLAG_SCALE_PER_TOKEN, or NULL (= 1/max_seq_len)
  * q_scale,k_scale  device float [H]; FP8_E4M3 only (dequantisation factors), else NULL
+ * max_attn_len, full_attn_size   >= 0; 0, 0 is the plain causal mask; full_attn_size is ignored
+ *               when max_attn_len is 0 (as in the reference)
  * workspace     device scratch of at least recir_hstu_attn_fwd_workspace_bytes(...) bytes, 16-byte
  *               aligned; contents need not be initialised; must not be shared by calls that can
  *               overlap on the device
@@ -83,8 +88,9 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
                         const void* seq_offsets, const void* num_targets, const float* rab,
                         const float* attn_scale, const float* q_scale, const float* k_scale,
                         int32_t T, int32_t B, int32_t H, int32_t Dqk, int32_t Dv,
-                        int32_t max_seq_len, int32_t contextual_seq_len, float alpha, int32_t dtype,
-                        uint32_t flags, void* workspace, size_t workspace_bytes, void* hip_stream);
+                        int32_t max_seq_len, int32_t contextual_seq_len, int32_t max_attn_len,
+                        int32_t full_attn_size, float alpha, int32_t dtype, uint32_t flags,
+                        void* workspace, size_t workspace_bytes, void* hip_stream);
 
 /* Scratch size recir_hstu_attn_fwd needs for these sizes (upper bound over all kernel variants). */
 size_t recir_hstu_attn_fwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk,
@@ -112,8 +118,8 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
                         void* dk, void* dv, const void* seq_offsets, const void* num_targets,
                         const float* rab, const float* attn_scale, int32_t T, int32_t B, int32_t H,
                         int32_t Dqk, int32_t Dv, int32_t max_seq_len, int32_t contextual_seq_len,
-                        float alpha, int32_t dtype, uint32_t flags, void* workspace,
-                        size_t workspace_bytes, void* hip_stream);
+                        int32_t max_attn_len, int32_t full_attn_size, float alpha, int32_t dtype,
+                        uint32_t flags, void* workspace, size_t workspace_bytes, void* hip_stream);
 
 /* Scratch size recir_hstu_attn_bwd needs for these sizes. */
 size_t recir_hstu_attn_bwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk,

@@ -10,6 +10,10 @@
  *   hstu_oracle_keep            recir/ops/helion/jagged_hstu_attention.py:185-208, :346
  *   hstu_oracle_keep_clamp_id   recir/ops/kjt_split_per_feature.cpp:639-674,
  *                               recir/ops/pallas/hstu_attention.py:86-112, :404-430
+ *   hstu_oracle_keep_sl, hstu_oracle_keep_sl_clamp_id
+ *                               the semi-local mask (max_attn_len, full_attn_size) of
+ *                               recir/ops/kjt_split_per_feature.cpp:654-668 and
+ *                               recir/ops/helion/jagged_hstu_attention.py:124-147
  *   hstu_oracle_attn_fwd        recir/ops/kjt_split_per_feature.cpp:602-693 (per-sequence loop,
  *                               alpha on the scores, x*sigmoid(x), attn_scale or 1/max_seq_len,
  *                               mask multiply, weights @ v) with the packed [T,H,Dv] output and
@@ -76,6 +80,70 @@ int hstu_oracle_keep_clamp_id(int64_t m, int64_t j, int64_t n, int64_t t, int64_
   return keep;
 }
 
+/*
+ * Semi-local variant (max_attn_len A > 0): a history key is visible to a query when it lies within
+ * the last A positions before the query's target-clamped id, or -- with full_attn_size F > 0 --
+ * when the query's clamped id is in the last F history positions or beyond (those rows keep full
+ * causal attention).  A == 0 is the plain causal mask (F is then ignored, as in the reference).
+ * Written as "history key, and near or full-tail row".
+ */
+int hstu_oracle_keep_sl(int64_t m, int64_t j, int64_t n, int64_t t, int64_t ctx, int ctx_mode,
+                        int64_t A, int64_t F) {
+  if (A <= 0) return hstu_oracle_keep(m, j, n, t, ctx, ctx_mode);
+  if (m < 0 || j < 0 || m >= n || j >= n) return 0;
+  const int64_t cap = n - t;
+  const int64_t idm = m < cap ? m : cap;
+  const int hist = j < idm; /* implies j < cap */
+  const int near = idm - j <= A;
+  const int tail = F > 0 && idm >= cap - F;
+  int keep = (m == j) || (hist && (near || tail));
+  if (ctx > 0) {
+    if (ctx_mode == HSTU_CTX_PREFIX) {
+      keep = keep || (j < ctx);
+    } else {
+      const int64_t idj = j < cap ? j : cap;
+      keep = keep || (idj == 0);
+    }
+  }
+  return keep;
+}
+
+/* The same mask built the way the reference C++ builds it (kjt_split_per_feature.cpp:639-674):
+ * clamped ids, distance window, and the "global" rows/columns zeroed below the boundary. */
+int hstu_oracle_keep_sl_clamp_id(int64_t m, int64_t j, int64_t n, int64_t t, int64_t ctx,
+                                 int ctx_mode, int64_t A, int64_t F) {
+  if (m < 0 || j < 0 || m >= n || j >= n) return 0;
+  const int64_t bound = n - t;
+  const int64_t idm = m < bound ? m : bound;
+  const int64_t idj = j < bound ? j : bound;
+  const int64_t distance = idm - idj;
+  int keep = (m == j);
+  if (A > 0) {
+    keep = keep || (distance > 0 && distance <= A);
+    if (F > 0) {
+      const int64_t boundary = bound - F;
+      const int64_t gr = idm < boundary ? 0 : idm;
+      const int64_t gc = idj < boundary ? 0 : idj;
+      keep = keep || (gr - gc > 0);
+    }
+  } else {
+    keep = keep || (distance > 0);
+  }
+  if (ctx > 0) {
+    if (ctx_mode == HSTU_CTX_PREFIX) keep = keep || (j < ctx);
+    else keep = keep || (idj == 0);
+  }
+  return keep;
+}
+
+int64_t hstu_oracle_count_pairs_sl(int64_t n, int64_t t, int64_t ctx, int ctx_mode, int64_t A,
+                                   int64_t F) {
+  int64_t c = 0;
+  for (int64_t m = 0; m < n; ++m)
+    for (int64_t j = 0; j < n; ++j) c += hstu_oracle_keep_sl(m, j, n, t, ctx, ctx_mode, A, F);
+  return c;
+}
+
 /* Number of kept (m, j) pairs of one sequence, by brute force. */
 int64_t hstu_oracle_count_pairs(int64_t n, int64_t t, int64_t ctx, int ctx_mode) {
   int64_t c = 0;
@@ -100,11 +168,12 @@ static float round_to_bf16(float x) {
  *          force in the reference (weights.to(v.dtype)).
  * Returns 0, or -1 on a malformed offsets array (same condition the reference rejects).
  */
-int hstu_oracle_attn_fwd(const float* q, const float* k, const float* v, float* out,
-                         const int64_t* seq_offsets, const int64_t* num_targets, const float* rab,
-                         int attn_scale_kind, const float* attn_scale, int64_t T, int64_t B,
-                         int64_t H, int64_t Dqk, int64_t Dv, int64_t max_seq_len, int64_t ctx,
-                         int ctx_mode, double alpha, int p_round) {
+int hstu_oracle_attn_fwd_sl(const float* q, const float* k, const float* v, float* out,
+                            const int64_t* seq_offsets, const int64_t* num_targets, const float* rab,
+                            int attn_scale_kind, const float* attn_scale, int64_t T, int64_t B,
+                            int64_t H, int64_t Dqk, int64_t Dv, int64_t max_seq_len, int64_t ctx,
+                            int ctx_mode, double alpha, int p_round, int64_t max_attn_len,
+                            int64_t full_attn_size) {
   for (int64_t b = 0; b < B; ++b) {
     const int64_t s = seq_offsets[b], e = seq_offsets[b + 1];
     if (!(0 <= s && s <= e && e <= T)) return -1;
@@ -128,7 +197,7 @@ int hstu_oracle_attn_fwd(const float* q, const float* k, const float* v, float* 
           else if (attn_scale_kind == 1) scale = (double)attn_scale[0];
           else scale = (double)attn_scale[s + m];
           for (int64_t j = 0; j < n; ++j) {
-            if (!hstu_oracle_keep(m, j, n, t, ctx, ctx_mode)) continue;
+            if (!hstu_oracle_keep_sl(m, j, n, t, ctx, ctx_mode, max_attn_len, full_attn_size)) continue;
             const float* kr = k + ((s + j) * H + h) * Dqk;
             double dot = 0.0;
 #pragma omp simd reduction(+ : dot)
@@ -162,12 +231,12 @@ int hstu_oracle_attn_fwd(const float* q, const float* k, const float* v, float* 
  * p_round: 1 rounds P and dS to bf16 before they are used as matmul operands (what a bf16 kernel
  *          does); 0 keeps them in double.
  */
-int hstu_oracle_attn_bwd(const float* dout, const float* q, const float* k, const float* v, float* dq,
-                         float* dk, float* dv, const int64_t* seq_offsets,
-                         const int64_t* num_targets, const float* rab, int attn_scale_kind,
-                         const float* attn_scale, int64_t T, int64_t B, int64_t H, int64_t Dqk,
-                         int64_t Dv, int64_t max_seq_len, int64_t ctx, int ctx_mode, double alpha,
-                         int p_round) {
+int hstu_oracle_attn_bwd_sl(const float* dout, const float* q, const float* k, const float* v, float* dq,
+                            float* dk, float* dv, const int64_t* seq_offsets,
+                            const int64_t* num_targets, const float* rab, int attn_scale_kind,
+                            const float* attn_scale, int64_t T, int64_t B, int64_t H, int64_t Dqk,
+                            int64_t Dv, int64_t max_seq_len, int64_t ctx, int ctx_mode, double alpha,
+                            int p_round, int64_t max_attn_len, int64_t full_attn_size) {
   for (int64_t b = 0; b < B; ++b) {
     const int64_t s = seq_offsets[b], e = seq_offsets[b + 1];
     if (!(0 <= s && s <= e && e <= T)) return -1;
@@ -195,7 +264,7 @@ int hstu_oracle_attn_bwd(const float* dout, const float* q, const float* k, cons
         else if (attn_scale_kind == 1) scale = (double)attn_scale[0];
         else scale = (double)attn_scale[s + m];
         for (int64_t j = 0; j < n; ++j) {
-          if (!hstu_oracle_keep(m, j, n, t, ctx, ctx_mode)) continue;
+          if (!hstu_oracle_keep_sl(m, j, n, t, ctx, ctx_mode, max_attn_len, full_attn_size)) continue;
           const float* kr = k + ((s + j) * H + h) * Dqk;
           const float* vr = v + ((s + j) * H + h) * Dv;
           double dot = 0.0;
@@ -234,6 +303,27 @@ int hstu_oracle_attn_bwd(const float* dout, const float* q, const float* k, cons
     }
   }
   return 0;
+}
+
+/* Causal forms (max_attn_len = full_attn_size = 0). */
+int hstu_oracle_attn_fwd(const float* q, const float* k, const float* v, float* out,
+                         const int64_t* seq_offsets, const int64_t* num_targets, const float* rab,
+                         int attn_scale_kind, const float* attn_scale, int64_t T, int64_t B,
+                         int64_t H, int64_t Dqk, int64_t Dv, int64_t max_seq_len, int64_t ctx,
+                         int ctx_mode, double alpha, int p_round) {
+  return hstu_oracle_attn_fwd_sl(q, k, v, out, seq_offsets, num_targets, rab, attn_scale_kind, attn_scale,
+                                 T, B, H, Dqk, Dv, max_seq_len, ctx, ctx_mode, alpha, p_round, 0, 0);
+}
+
+int hstu_oracle_attn_bwd(const float* dout, const float* q, const float* k, const float* v, float* dq,
+                         float* dk, float* dv, const int64_t* seq_offsets,
+                         const int64_t* num_targets, const float* rab, int attn_scale_kind,
+                         const float* attn_scale, int64_t T, int64_t B, int64_t H, int64_t Dqk,
+                         int64_t Dv, int64_t max_seq_len, int64_t ctx, int ctx_mode, double alpha,
+                         int p_round) {
+  return hstu_oracle_attn_bwd_sl(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, rab, attn_scale_kind,
+                                 attn_scale, T, B, H, Dqk, Dv, max_seq_len, ctx, ctx_mode, alpha, p_round,
+                                 0, 0);
 }
 
 /* float -> OCP float8 e4m3fn byte: saturate to +-448 first (the reference clamps before the cast),

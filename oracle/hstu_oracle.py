@@ -57,6 +57,16 @@ def lib() -> ctypes.CDLL:
         L.hstu_oracle_attn_fwd.restype = c_int
         L.hstu_oracle_attn_bwd.argtypes = [vp] * 10 + [c_int, vp] + [i64] * 7 + [c_int, ctypes.c_double, c_int]
         L.hstu_oracle_attn_bwd.restype = c_int
+        L.hstu_oracle_attn_fwd_sl.argtypes = L.hstu_oracle_attn_fwd.argtypes + [i64, i64]
+        L.hstu_oracle_attn_fwd_sl.restype = c_int
+        L.hstu_oracle_attn_bwd_sl.argtypes = L.hstu_oracle_attn_bwd.argtypes + [i64, i64]
+        L.hstu_oracle_attn_bwd_sl.restype = c_int
+        for name in ("hstu_oracle_keep_sl", "hstu_oracle_keep_sl_clamp_id"):
+            fn = getattr(L, name)
+            fn.argtypes = [i64, i64, i64, i64, i64, c_int, i64, i64]
+            fn.restype = c_int
+        L.hstu_oracle_count_pairs_sl.argtypes = [i64, i64, i64, c_int, i64, i64]
+        L.hstu_oracle_count_pairs_sl.restype = i64
         L.hstu_oracle_e4m3_encode.argtypes = [ctypes.c_float]
         L.hstu_oracle_e4m3_encode.restype = ctypes.c_uint8
         L.hstu_oracle_e4m3_decode.argtypes = [ctypes.c_uint8]
@@ -69,6 +79,18 @@ def lib() -> ctypes.CDLL:
 
 def keep(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX) -> bool:
     return bool(lib().hstu_oracle_keep(m, j, n, t, ctx, ctx_mode))
+
+
+def keep_sl(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX, max_attn_len=0, full_attn_size=0) -> bool:
+    return bool(lib().hstu_oracle_keep_sl(m, j, n, t, ctx, ctx_mode, max_attn_len, full_attn_size))
+
+
+def keep_sl_clamp_id(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX, max_attn_len=0, full_attn_size=0) -> bool:
+    return bool(lib().hstu_oracle_keep_sl_clamp_id(m, j, n, t, ctx, ctx_mode, max_attn_len, full_attn_size))
+
+
+def count_pairs_sl(n, t, ctx=0, ctx_mode=CTX_PREFIX, max_attn_len=0, full_attn_size=0) -> int:
+    return int(lib().hstu_oracle_count_pairs_sl(n, t, ctx, ctx_mode, max_attn_len, full_attn_size))
 
 
 def keep_clamp_id(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX) -> bool:
@@ -88,7 +110,8 @@ def _ptr(a):
 
 
 def attn_fwd(q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn_scale=None,
-             rab=None, contextual_seq_len=0, ctx_mode=CTX_PREFIX, round_p_bf16=False):
+             rab=None, contextual_seq_len=0, ctx_mode=CTX_PREFIX, round_p_bf16=False,
+             max_attn_len=0, full_attn_size=0):
     """Per-sequence loop oracle.  q,k [T,H,Dqk], v [T,H,Dv] float arrays -> out [T,H,Dv] float32.
 
     ``attn_scale``: None (1/max_seq_len), a python/0-d scalar, or a [T] per-token array.
@@ -113,17 +136,18 @@ def attn_fwd(q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn
         if kind == 2:
             assert sc.shape == (T,)
     out = np.empty((T, H, Dv), dtype=np.float32)
-    rc = lib().hstu_oracle_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(off), _ptr(nt),
-                                    _ptr(rb), kind, _ptr(sc), T, B, H, Dqk, Dv, int(max_seq_len),
-                                    int(contextual_seq_len), int(ctx_mode), float(alpha),
-                                    1 if round_p_bf16 else 0)
+    rc = lib().hstu_oracle_attn_fwd_sl(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(off), _ptr(nt),
+                                       _ptr(rb), kind, _ptr(sc), T, B, H, Dqk, Dv, int(max_seq_len),
+                                       int(contextual_seq_len), int(ctx_mode), float(alpha),
+                                       1 if round_p_bf16 else 0, int(max_attn_len), int(full_attn_size))
     if rc != 0:
         raise ValueError("invalid jagged range in seq_offsets")
     return out
 
 
 def attn_bwd(dout, q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn_scale=None,
-             rab=None, contextual_seq_len=0, ctx_mode=CTX_PREFIX, round_bf16=False):
+             rab=None, contextual_seq_len=0, ctx_mode=CTX_PREFIX, round_bf16=False,
+             max_attn_len=0, full_attn_size=0):
     """Gradients (dq, dk, dv) of ``attn_fwd`` for the upstream gradient ``dout`` [T,H,Dv]; float32 arrays.
 
     Same argument conventions as ``attn_fwd``.  ``round_bf16`` rounds P and dS to bf16 before the
@@ -149,10 +173,11 @@ def attn_bwd(dout, q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha
     dq = np.empty((T, H, Dqk), dtype=np.float32)
     dk = np.empty((T, H, Dqk), dtype=np.float32)
     dv = np.empty((T, H, Dv), dtype=np.float32)
-    rc = lib().hstu_oracle_attn_bwd(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv),
-                                    _ptr(off), _ptr(nt), _ptr(rb), kind, _ptr(sc), T, B, H, Dqk, Dv,
-                                    int(max_seq_len), int(contextual_seq_len), int(ctx_mode),
-                                    float(alpha), 1 if round_bf16 else 0)
+    rc = lib().hstu_oracle_attn_bwd_sl(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv),
+                                       _ptr(off), _ptr(nt), _ptr(rb), kind, _ptr(sc), T, B, H, Dqk, Dv,
+                                       int(max_seq_len), int(contextual_seq_len), int(ctx_mode),
+                                       float(alpha), 1 if round_bf16 else 0, int(max_attn_len),
+                                       int(full_attn_size))
     if rc != 0:
         raise ValueError("invalid jagged range in seq_offsets")
     return dq, dk, dv
@@ -287,9 +312,10 @@ def ref_op():
 
 
 def ref_attn_fwd(q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn_scale=None,
-                 contextual_seq_len=0):
+                 contextual_seq_len=0, max_attn_len=0, full_attn_size=0):
     """Run the reference C++ op on torch CPU tensors; returns out [seq_offsets[-1], H, Dv]."""
     op = ref_op()
     out, _aux = op(int(max_seq_len), float(alpha), q, k, v, seq_offsets, "lower_triangular",
-                   num_targets, attn_scale, 0, int(contextual_seq_len), 0, 0)
+                   num_targets, attn_scale, int(max_attn_len), int(contextual_seq_len),
+                   int(full_attn_size), 0)
     return out

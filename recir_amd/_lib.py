@@ -7,7 +7,7 @@ import os
 _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "librecir_hstu.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_BF16 = 0
 DTYPE_FP32 = 1
@@ -51,11 +51,11 @@ def load() -> ctypes.CDLL:
     L = ctypes.CDLL(LIB_PATH)
     vp, i32, u32, f32, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32, ctypes.c_float, ctypes.c_size_t
     L.recir_hstu_attn_fwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
-                                      i32, i32, i32, i32, i32, i32, i32, f32, i32, u32, vp, sz, vp]
+                                      i32, i32, i32, i32, i32, i32, i32, i32, i32, f32, i32, u32, vp, sz, vp]
     L.recir_hstu_attn_fwd.restype = ctypes.c_int
     L.recir_hstu_attn_fwd_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     L.recir_hstu_attn_fwd_workspace_bytes.restype = sz
-    L.recir_hstu_attn_bwd.argtypes = [vp] * 11 + [i32] * 7 + [f32, i32, u32, vp, sz, vp]
+    L.recir_hstu_attn_bwd.argtypes = [vp] * 11 + [i32] * 9 + [f32, i32, u32, vp, sz, vp]
     L.recir_hstu_attn_bwd.restype = ctypes.c_int
     L.recir_hstu_attn_bwd_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     L.recir_hstu_attn_bwd_workspace_bytes.restype = sz

@@ -219,6 +219,17 @@ int launch_status(const char* what) {
 size_t max_items(int T, int B, int H) { return ((size_t)((T + BM - 1) / BM) + (size_t)B) * (size_t)H; }
 constexpr size_t WS_HEADER = 64;
 
+template <bool FP8>
+void launch_dl(bool has_rab, bool semi, dim3 grid, hipStream_t stream, const Params& p) {
+  if (semi) {
+    if (has_rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<true, FP8, true>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<false, FP8, true>), grid, dim3(256), 0, stream, p);
+  } else {
+    if (has_rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<true, FP8, false>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<false, FP8, false>), grid, dim3(256), 0, stream, p);
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -239,10 +250,14 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
                         const void* seq_offsets, const void* num_targets, const float* rab,
                         const float* attn_scale, const float* q_scale, const float* k_scale,
                         int32_t T, int32_t B, int32_t H, int32_t Dqk, int32_t Dv,
-                        int32_t max_seq_len, int32_t contextual_seq_len, float alpha, int32_t dtype,
-                        uint32_t flags, void* workspace, size_t workspace_bytes, void* hip_stream) {
+                        int32_t max_seq_len, int32_t contextual_seq_len, int32_t max_attn_len,
+                        int32_t full_attn_size, float alpha, int32_t dtype, uint32_t flags,
+                        void* workspace, size_t workspace_bytes, void* hip_stream) {
   hipStream_t stream = (hipStream_t)hip_stream;
   if (T < 0 || B < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "negative size: T=%d B=%d", T, B);
+  if (max_attn_len < 0 || full_attn_size < 0)
+    return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "max_attn_len and full_attn_size must be >= 0, got %d and %d",
+                max_attn_len, full_attn_size);
   if (H <= 0 || Dqk <= 0 || Dv <= 0)
     return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "H, Dqk, Dv must be positive: H=%d Dqk=%d Dv=%d", H, Dqk, Dv);
   if (max_seq_len <= 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "max_seq_len must be positive, got %d", max_seq_len);
@@ -263,6 +278,8 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
   p.rab = rab; p.attn_scale = attn_scale; p.q_scale = q_scale; p.k_scale = k_scale;
   p.T = T; p.B = B; p.H = H; p.Dqk = Dqk; p.Dv = Dv; p.N = max_seq_len; p.ctx = contextual_seq_len;
   p.alpha = alpha; p.flags = flags;
+  p.max_attn_len = max_attn_len; p.full_attn_size = full_attn_size;
+  const bool semi = max_attn_len > 0;
 
   const size_t esz = dtype == RECIR_HSTU_DTYPE_FP32 ? 4 : 2;
   if (B == 0) {
@@ -282,6 +299,8 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
   if (fp8 && variant == 2) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "fp8 q/k runs on the direct-to-LDS tiled kernel only");
   if (variant >= 2 && !tiled_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "tiled kernel needs bf16, Dqk = Dv = 128 and 16-byte aligned tensors");
+  if (semi && (variant == 2 || variant == 4))
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "the semi-local mask runs on the direct-to-LDS tiled kernel or the generic one");
 
   if (use_tiled) {
     const size_t need = recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype);
@@ -334,12 +353,10 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
       g_last_kernel = rab ? "tiled_d128_bf16_regstage_rab" : "tiled_d128_bf16_regstage";
     } else {
       if (dtype == RECIR_HSTU_DTYPE_FP8_E4M3) {
-        if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<true, true>), grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<false, true>), grid, dim3(256), 0, stream, p);
+        launch_dl<true>(rab != nullptr, semi, grid, stream, p);
         g_last_kernel = rab ? "tiled_d128_fp8qk_rab" : "tiled_d128_fp8qk";
       } else {
-        if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<true, false>), grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((hstu_fwd_tiled_d128_dl<false, false>), grid, dim3(256), 0, stream, p);
+        launch_dl<false>(rab != nullptr, semi, grid, stream, p);
         g_last_kernel = rab ? "tiled_d128_bf16_rab" : "tiled_d128_bf16";
       }
     }
@@ -370,10 +387,13 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
                         void* dk, void* dv, const void* seq_offsets, const void* num_targets,
                         const float* rab, const float* attn_scale, int32_t T, int32_t B, int32_t H,
                         int32_t Dqk, int32_t Dv, int32_t max_seq_len, int32_t contextual_seq_len,
-                        float alpha, int32_t dtype, uint32_t flags, void* workspace,
-                        size_t workspace_bytes, void* hip_stream) {
+                        int32_t max_attn_len, int32_t full_attn_size, float alpha, int32_t dtype,
+                        uint32_t flags, void* workspace, size_t workspace_bytes, void* hip_stream) {
   hipStream_t stream = (hipStream_t)hip_stream;
   if (T < 0 || B < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "negative size: T=%d B=%d", T, B);
+  if (max_attn_len < 0 || full_attn_size < 0)
+    return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "max_attn_len and full_attn_size must be >= 0, got %d and %d",
+                max_attn_len, full_attn_size);
   if (H <= 0 || Dqk <= 0 || Dv <= 0)
     return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "H, Dqk, Dv must be positive: H=%d Dqk=%d Dv=%d", H, Dqk, Dv);
   if (max_seq_len <= 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "max_seq_len must be positive, got %d", max_seq_len);
@@ -394,6 +414,8 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   p.rab = rab; p.attn_scale = attn_scale;
   p.T = T; p.B = B; p.H = H; p.Dqk = Dqk; p.Dv = Dv; p.N = max_seq_len; p.ctx = contextual_seq_len;
   p.alpha = alpha; p.flags = flags;
+  p.max_attn_len = max_attn_len; p.full_attn_size = full_attn_size;
+  const bool semi = max_attn_len > 0;
   bp.dout = dout; bp.dq = dq; bp.dk = dk; bp.dv = dv;
 
   const bool bf16 = dtype == RECIR_HSTU_DTYPE_BF16;
@@ -450,9 +472,11 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
       }
     }
     const dim3 grid((unsigned)(slots * NUM_XCD));
-    hipLaunchKernelGGL(hstu_bwd_dkv_d128, grid, dim3(256), 0, stream, bk);
+    if (semi) hipLaunchKernelGGL(hstu_bwd_dkv_d128<true>, grid, dim3(256), 0, stream, bk);
+    else hipLaunchKernelGGL(hstu_bwd_dkv_d128<false>, grid, dim3(256), 0, stream, bk);
     if (int rc = launch_status("hstu_bwd_dkv_d128")) return rc;
-    hipLaunchKernelGGL(hstu_bwd_dq_d128, grid, dim3(256), 0, stream, bq);
+    if (semi) hipLaunchKernelGGL(hstu_bwd_dq_d128<true>, grid, dim3(256), 0, stream, bq);
+    else hipLaunchKernelGGL(hstu_bwd_dq_d128<false>, grid, dim3(256), 0, stream, bq);
     if (int rc = launch_status("hstu_bwd_dq_d128")) return rc;
     g_last_kernel = "bwd_tiled_d128_bf16";
     return RECIR_HSTU_OK;

@@ -135,6 +135,8 @@ __device__ __forceinline__ float bwd_output_scale(const Params& p) {
 // ---------------------------------------------------------------------------------------------
 // dQ
 // ---------------------------------------------------------------------------------------------
+// SEMI: semi-local mask (max_attn_len > 0), as in the forward kernel.
+template <bool SEMI>
 __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp) {
   const Params& p = bp.f;
   __shared__ __attribute__((aligned(1024))) unsigned short Ks0[BWD_BN * HD];
@@ -158,6 +160,8 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     const WorkItem wi = list[slot];
     SeqInfo si;
     si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
+    si.win = WIN_ALL; si.tail0 = 0x7fffffff;
+    if (SEMI) mask_window(p, si.cap, si.win, si.tail0);
     const int q0 = wi.q0;
     const int q_end = wi.q_end;  // rows [q0, q_end) belong to this item
     const int h = wi.h;
@@ -170,6 +174,10 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     const int m_lo = qw0;
     const int m_hi = min(qw0 + 31, q_end - 1);
     const bool wave_has_rows = m_lo < q_end;
+    const int idm = min(m, si.cap);
+    const bool tail_row = idm >= si.tail0;
+    const int idlo_w = min(m_lo, si.cap), idhi_w = min(m_hi, si.cap);
+    const bool wave_has_tail = idhi_w >= si.tail0;
 
     // key tiles [0, nkv) minus the run [skip_a, skip_b) that holds only target keys off this query
     // tile's diagonal (and no contextual key): the tiles the forward walks
@@ -189,7 +197,9 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       bwd_issue_rows(vgb + (size_t)k0 * row_bytes, row_bytes, last, BUF ? Vs1 : Vs0, lc, wave);
     };
 
-    int it = (has_skip && skip_a == 0) ? skip_b : 0;
+    int it0 = 0;  // semi-local: key tiles below the first row's window are not walked
+    if (SEMI && si.ctx_eff <= 0 && min(q_end - 1, si.cap) < si.tail0) it0 = max(min(q0, si.cap) - si.win, 0) / BWD_BN;
+    int it = (has_skip && it0 >= skip_a) ? max(it0, skip_b) : it0;
     if (it < nkv) issue_tile(it, std::integral_constant<int, 0>{});
 
     bf16x8 qf[8], gf[8];
@@ -239,7 +249,8 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
           float g = dpt[r] * (sig * (1.0f + sv * (1.0f - sig)));
           if (MASKED) {
             const int j = k0 + kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            const bool kp = ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
+            const bool kp = SEMI ? ((m == j) | ((j < idm) & ((idm - j <= si.win) | tail_row)) | (j < si.ctx_eff)) & (j < si.n)
+                                 : ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
             g = kp ? g : 0.f;
           }
           ds[r] = g;
@@ -264,10 +275,14 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     auto compute_tile = [&](int itc, auto buf_tag) __attribute__((always_inline)) {
       const int k0 = itc * BWD_BN;
       const int k1 = k0 + BWD_BN;
-      const bool any_kept = wave_has_rows && ((k0 <= m_hi && k1 > m_lo) || (k0 < si.cap && k0 <= m_hi) ||
-                                              (k0 < si.ctx_eff));
+      bool any_kept = wave_has_rows && ((k0 <= m_hi && k1 > m_lo) || (k0 < si.cap && k0 <= m_hi) ||
+                                        (k0 < si.ctx_eff));
+      if (SEMI)
+        any_kept = wave_has_rows && ((k0 <= m_hi && k1 > m_lo) || (k0 < si.ctx_eff) ||
+                                     (k0 < idhi_w && (wave_has_tail || k1 > idlo_w - si.win)));
       if (!any_kept) return;
-      const bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
+      bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
+      if (SEMI) full = full && (idlo_w >= si.tail0 || k0 >= idhi_w - si.win);
       if (full) tile_body(std::false_type{}, buf_tag, k0);
       else tile_body(std::true_type{}, buf_tag, k0);
     };
@@ -311,6 +326,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
 // ---------------------------------------------------------------------------------------------
 // dK, dV
 // ---------------------------------------------------------------------------------------------
+template <bool SEMI>
 __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
   const Params& p = bp.f;
   __shared__ __attribute__((aligned(1024))) unsigned short Qs0[BWD_BN * HD];
@@ -335,6 +351,8 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     const WorkItem wi = list[slot];
     SeqInfo si;
     si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
+    si.win = WIN_ALL; si.tail0 = 0x7fffffff;
+    if (SEMI) mask_window(p, si.cap, si.win, si.tail0);
     const int j0 = wi.q0;  // first key row of this workgroup's tile
     const int h = wi.h;
     const unsigned row_bytes = (unsigned)p.H * HD * 2u;
@@ -403,7 +421,9 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
           float g = dp[r] * (sig * (1.0f + sv * (1.0f - sig)));
           if (MASKED) {
             const int m = m0 + qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            const bool kp = ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (m < si.n);
+            const int idm = min(m, si.cap);
+            const bool kp = SEMI ? ((m == j) | ((j < idm) & ((idm - j <= si.win) | (idm >= si.tail0))) | (j < si.ctx_eff)) & (m < si.n)
+                                 : ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (m < si.n);
             pe = kp ? pe : 0.f;
             g = kp ? g : 0.f;
           }
@@ -434,13 +454,22 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       const int m0 = itc * BWD_BN;
       const int m1 = min(m0 + BWD_BN, si.n);  // exclusive
       // any pair of (query tile, this wave's keys) kept?
-      const bool any_kept = wave_has_rows && ((m0 <= j_hi && m1 > j_lo) ||           // diagonal
-                                              (j_lo < si.cap && m1 - 1 >= j_lo) ||  // history key, later query
-                                              (j_lo < si.ctx_eff));                  // contextual key
+      bool any_kept = wave_has_rows && ((m0 <= j_hi && m1 > j_lo) ||           // diagonal
+                                        (j_lo < si.cap && m1 - 1 >= j_lo) ||  // history key, later query
+                                        (j_lo < si.ctx_eff));                  // contextual key
+      if (SEMI) {
+        // a history key counts only for rows whose window reaches it or rows of the full-attention tail
+        const int id0 = min(m0, si.cap), id1 = min(m1 - 1, si.cap);
+        any_kept = wave_has_rows && ((m0 <= j_hi && m1 > j_lo) || (j_lo < si.ctx_eff) ||
+                                     (j_lo < si.cap && m1 - 1 >= j_lo && (id0 - j_hi <= si.win || id1 >= si.tail0)));
+      }
       if (!any_kept) return;
       // every pair kept: all keys are history keys (or contextual) below every query row, tile whole
-      const bool full = (m0 + BWD_BN <= si.n) && (jw0 + 31 < si.n) &&
-                        ((jw0 + 31 <= m0 && jw0 + 31 < si.cap) || (jw0 + 31 < si.ctx_eff));
+      bool full = (m0 + BWD_BN <= si.n) && (jw0 + 31 < si.n) &&
+                  ((jw0 + 31 <= m0 && jw0 + 31 < si.cap) || (jw0 + 31 < si.ctx_eff));
+      if (SEMI)
+        full = full && ((jw0 + 31 < si.ctx_eff) || min(m0, si.cap) >= si.tail0 ||
+                        min(m0 + BWD_BN - 1, si.cap) - jw0 <= si.win);
       if (full) tile_body(std::false_type{}, buf_tag, m0);
       else tile_body(std::true_type{}, buf_tag, m0);
     };

@@ -47,6 +47,9 @@ struct Params {
   int items_cap;              // capacity of one per-XCD list
   int grid_slots;             // slots per XCD the launch covers (gridDim.x = NUM_XCD * grid_slots)
   int T, B, H, Dqk, Dv, N, ctx;
+  int max_attn_len;    // > 0: semi-local window over the history keys
+  int full_attn_size;  // > 0 (with max_attn_len > 0): rows in or after the last full_attn_size history
+                       //      positions keep full causal attention
   float alpha;
   unsigned flags;
 };
@@ -56,7 +59,16 @@ struct SeqInfo {
   int n;        // length
   int cap;      // history length n - num_targets (keys j < cap are history)
   int ctx_eff;  // keys j < ctx_eff are visible to every query
+  int win;      // a history key j is visible to row m when min(m, cap) - j <= win ...
+  int tail0;    // ... or when min(m, cap) >= tail0 (causal mask: win is huge)
 };
+
+constexpr int WIN_ALL = 0x3fffffff;
+
+// window and full-attention boundary of a sequence with history length cap
+// (recir/ops/kjt_split_per_feature.cpp:654-668: distance window on the target-clamped ids, rows at
+// or beyond cap - full_attn_size see the whole history; full_attn_size is ignored without a window)
+__device__ __forceinline__ void mask_window(const struct Params& p, int cap, int& win, int& tail0);
 
 __device__ __forceinline__ long long load_index(const void* p, int i, bool i32) {
   return i32 ? (long long)((const int*)p)[i] : ((const long long*)p)[i];
@@ -78,13 +90,20 @@ __device__ __forceinline__ SeqInfo seq_info(const Params& p, int b) {
   long long cap = (long long)si.n - t;
   si.cap = cap > si.n ? si.n : (cap < -1 ? -1 : (int)cap);
   if (p.flags & RECIR_HSTU_FLAG_CTX_REFERENCE) {
-    // the reference unmasks keys whose target-clamped id min(j, cap) equals 0: key 0 (already
-    // causal) when cap > 0, every key when cap == 0, none when cap < 0
-    si.ctx_eff = (p.ctx > 0 && cap == 0) ? si.n : 0;
+    // the reference unmasks keys whose target-clamped id min(j, cap) equals 0: key 0 when cap > 0
+    // (causal anyway, but outside the window of far rows under the semi-local mask), every key
+    // when cap == 0, none when cap < 0
+    si.ctx_eff = p.ctx > 0 ? (cap == 0 ? si.n : (cap > 0 && si.n > 0 ? 1 : 0)) : 0;
   } else {
     si.ctx_eff = p.ctx < si.n ? (p.ctx > 0 ? p.ctx : 0) : si.n;
   }
+  mask_window(p, si.cap, si.win, si.tail0);
   return si;
+}
+
+__device__ __forceinline__ void mask_window(const Params& p, int cap, int& win, int& tail0) {
+  win = p.max_attn_len > 0 ? p.max_attn_len : WIN_ALL;
+  tail0 = (p.max_attn_len > 0 && p.full_attn_size > 0) ? cap - p.full_attn_size : 0x7fffffff;
 }
 
 __device__ __forceinline__ int end_of_sequences(const Params& p) {
@@ -93,7 +112,8 @@ __device__ __forceinline__ int end_of_sequences(const Params& p) {
 }
 
 __device__ __forceinline__ bool keep_pair(int m, int j, const SeqInfo& si) {
-  return (m == j) || (m >= j && j < si.cap) || (j < si.ctx_eff);
+  const int idm = min(m, si.cap);
+  return (m == j) || (j < idm && (idm - j <= si.win || idm >= si.tail0)) || (j < si.ctx_eff);
 }
 
 __device__ __forceinline__ float bf16_bits_to_float(unsigned short b) {

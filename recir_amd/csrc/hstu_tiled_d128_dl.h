@@ -41,7 +41,9 @@ typedef __attribute__((ext_vector_type(8))) int i32x8;
 // the scores come from v_mfma_scale_f32_32x32x64_f8f6f4 (two per 32 x 32 block, unit block scales) and
 // are multiplied by alpha * q_scale[h] * k_scale[h] * log2(e) in fp32; v, P and the second
 // contraction stay bf16.  The K tile is then [BN rows][128 bytes], chunk c of row r at c ^ (r & 7).
-template <bool HAS_RAB, bool FP8>
+// SEMI: the semi-local mask (max_attn_len > 0) -- window test in the partial tiles, key tiles below
+// every row's window not walked; the causal instantiation carries none of it.
+template <bool HAS_RAB, bool FP8, bool SEMI>
 __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
   // The two pipeline stages are separate objects and every access names its stage at compile time:
   // the compiler then knows that an LDS read of one stage cannot alias the global -> LDS copies in
@@ -97,6 +99,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     const WorkItem wi = list[slot];
     SeqInfo si;
     si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
+    si.win = WIN_ALL; si.tail0 = 0x7fffffff;
+    if (SEMI) mask_window(p, si.cap, si.win, si.tail0);
     const int q0 = wi.q0;
     const int q_end = wi.q_end;  // rows [q0, q_end) belong to this item
     const int h = wi.h;
@@ -119,6 +123,11 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     const int m_lo = qw0;
     const int m_hi = min(qw0 + 31, q_end - 1);
     const bool wave_has_rows = m_lo < q_end;
+    // semi-local: target-clamped position of this lane's row and of the wave's first and last row
+    const int idm = min(m, si.cap);
+    const bool tail_row = idm >= si.tail0;
+    const int idlo_w = min(m_lo, si.cap), idhi_w = min(m_hi, si.cap);
+    const bool wave_has_tail = idhi_w >= si.tail0;
 
     // key tiles [0, nkv) minus the run [skip_a, skip_b) that holds only target keys off this query
     // tile's diagonal (and no contextual key)
@@ -188,7 +197,11 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     };
 
     // first tile in flight before anything else is waited for
-    int it = (has_skip && skip_a == 0) ? skip_b : 0;
+    // semi-local: key tiles below the window of the workgroup's first row are not walked unless a
+    // row of the full-attention tail or a contextual key needs them
+    int it0 = 0;
+    if (SEMI && si.ctx_eff <= 0 && min(q_end - 1, si.cap) < si.tail0) it0 = max(min(q0, si.cap) - si.win, 0) / BN;
+    int it = (has_skip && it0 >= skip_a) ? max(it0, skip_b) : it0;
     if (it < nkv) issue_tile(it, std::integral_constant<int, 0>{});
 
     // ---- Q fragments (B operand): lane holds row qw0 + l32 ----
@@ -251,7 +264,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         if (MASKED) {
           const int j = k0 + jl;
           // branch-free keep(m, j) & (j < n)
-          const bool kp = ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
+          const bool kp = SEMI ? ((m == j) | ((j < idm) & ((idm - j <= si.win) | tail_row)) | (j < si.ctx_eff)) & (j < si.n)
+                               : ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
           pe = kp ? pe : 0.f;
         }
         pv[r] = pe;
@@ -409,14 +423,18 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       const int k0 = it * BN;
       const int k1 = k0 + BN;
       // wave-level classification of this (32 query rows) x (64 keys) block
-      const bool any_kept = wave_has_rows && ((k0 <= m_hi && k1 > m_lo) /* diagonal crosses */ ||
-                                              (k0 < si.cap && k0 <= m_hi) /* causal history */ ||
-                                              (k0 < si.ctx_eff));
+      bool any_kept = wave_has_rows && ((k0 <= m_hi && k1 > m_lo) /* diagonal crosses */ ||
+                                        (k0 < si.cap && k0 <= m_hi) /* causal history */ ||
+                                        (k0 < si.ctx_eff));
+      if (SEMI)  // history keys count only inside some row's window
+        any_kept = wave_has_rows && ((k0 <= m_hi && k1 > m_lo) || (k0 < si.ctx_eff) ||
+                                     (k0 < idhi_w && (wave_has_tail || k1 > idlo_w - si.win)));
       if (!any_kept) {
         if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, BUF ^ 1>{});  // this wave still copies its share
         return;
       }
-      const bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
+      bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
+      if (SEMI) full = full && (idlo_w >= si.tail0 || k0 >= idhi_w - si.win);  // inside every row's window
       if (full) tile_body(std::false_type{}, buf_tag, k0, nxt, std::false_type{});
       else tile_body(std::true_type{}, buf_tag, k0, nxt, std::false_type{});
     };
@@ -425,7 +443,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     // (64 t + 63 <= m_lo and 64 t + 64 <= cap), inside the first contiguous run of the walk, and
     // followed by a tile that exists and is whole.  Taken in pairs (stage 0, stage 1).
     int fast_pairs = 0;
-    if (wave_has_rows && it == 0) {
+    if (!SEMI && wave_has_rows && it == 0) {
       const int run_end = has_skip ? skip_a : nkv;
       int fast_end = min(min((m_lo + 1) / BN, cap0 / BN), min(run_end - 1, si.n / BN - 1));
       fast_pairs = max(fast_end, 0) / 2;

@@ -75,13 +75,13 @@ _SCHEMA = (
 _FP8_SCHEMA = (
     "hstu_jagged_attention_fp8_fwd(int N, float alpha, Tensor q_fp8, Tensor k_fp8, Tensor v, "
     "Tensor q_scale, Tensor k_scale, Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, "
-    "int contextual_seq_len, Tensor? rab=None) -> (Tensor, Tensor)"
+    "int contextual_seq_len, Tensor? rab=None, int max_attn_len=0, int full_attn_size=0) -> (Tensor, Tensor)"
 )
 _QUANT_SCHEMA = "hstu_quantize_e4m3_per_head(Tensor x) -> (Tensor, Tensor)"
 _BWD_SCHEMA = (
     "hstu_jagged_attention_bwd(Tensor dout, int N, float alpha, Tensor q, Tensor k, Tensor v, "
     "Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, int contextual_seq_len, "
-    "Tensor? rab=None) -> (Tensor, Tensor, Tensor)"
+    "Tensor? rab=None, int max_attn_len=0, int full_attn_size=0) -> (Tensor, Tensor, Tensor)"
 )
 
 _LIBRARY = torch.library.Library("recir", "FRAGMENT")
@@ -166,8 +166,14 @@ def _raise_status(entry, rc):
     raise RuntimeError(f"{entry} launch failed (hipError {rc}): {msg}")
 
 
+def _check_window(max_attn_len, full_attn_size):
+    if max_attn_len < 0 or full_attn_size < 0:
+        raise ValueError("max_attn_len and full_attn_size must be non-negative")
+
+
 def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale, N, alpha,
-            contextual_seq_len, dtype_code) -> torch.Tensor:
+            contextual_seq_len, dtype_code, max_attn_len=0, full_attn_size=0) -> torch.Tensor:
+    _check_window(max_attn_len, full_attn_size)
     L = _lib.load()
     dev = q.device
     B, off, nt, sc, rb, flags = _prepare("hstu_jagged_attention_fwd", q, k, v, seq_offsets, num_targets,
@@ -184,8 +190,8 @@ def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale
     with torch.cuda.device(dev):
         rc = L.recir_hstu_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(off), _ptr(nt), _ptr(rb),
                                    _ptr(sc), _ptr(q_scale), _ptr(k_scale), T, B, H, Dqk, Dv, int(N),
-                                   int(contextual_seq_len), float(alpha), dtype_code, flags,
-                                   _ptr(ws), ws.numel(), stream)
+                                   int(contextual_seq_len), int(max_attn_len), int(full_attn_size),
+                                   float(alpha), dtype_code, flags, _ptr(ws), ws.numel(), stream)
     if rc != 0:
         _raise_status("recir_hstu_attn_fwd", rc)
     return out
@@ -204,7 +210,8 @@ def _dtype_code(q, k, v):
 
 
 def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
-                rab=None):
+                rab=None, max_attn_len=0, full_attn_size=0):
+    _check_window(max_attn_len, full_attn_size)
     L = _lib.load()
     dev = q.device
     code = _dtype_code(q, k, v)
@@ -227,8 +234,8 @@ def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, c
     with torch.cuda.device(dev):
         rc = L.recir_hstu_attn_bwd(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv),
                                    _ptr(off), _ptr(nt), _ptr(rb), _ptr(sc), T, B, H, Dqk, Dv, int(N),
-                                   int(contextual_seq_len), float(alpha), code, flags, _ptr(ws),
-                                   ws.numel(), stream)
+                                   int(contextual_seq_len), int(max_attn_len), int(full_attn_size),
+                                   float(alpha), code, flags, _ptr(ws), ws.numel(), stream)
     if rc != 0:
         _raise_status("recir_hstu_attn_bwd", rc)
     return dq, dk, dv
@@ -237,21 +244,19 @@ def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, c
 def _fwd_device(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
                 max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads=0, rab=None):
     # same rejections as the reference fallback (kjt_split_per_feature.cpp:616-622) plus the
-    # features outside the causal + target mask
+    # non-causal mask types
     if num_softmax_heads != 0:
         raise ValueError("softmax attention heads are unsupported")
     if invalid_attn_mask_type != "lower_triangular":
         raise ValueError("only the causal mask ('lower_triangular') is supported")
-    if max_attn_len != 0 or full_attn_size != 0:
-        raise ValueError("max_attn_len and full_attn_size (semi-local attention) are unsupported")
     code = _dtype_code(q, k, v)
     out = _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, None, None, N, alpha,
-                  contextual_seq_len, code)
+                  contextual_seq_len, code, max_attn_len, full_attn_size)
     return out, torch.zeros((1,), dtype=torch.float32, device=q.device)
 
 
 def _fp8_fwd_device(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, num_targets,
-                    attn_scale, contextual_seq_len, rab=None):
+                    attn_scale, contextual_seq_len, rab=None, max_attn_len=0, full_attn_size=0):
     ok = (torch.float8_e4m3fn, torch.uint8)
     if q_fp8.dtype not in ok or k_fp8.dtype not in ok:
         raise ValueError("q_fp8 and k_fp8 must be float8_e4m3fn (or its uint8 bytes)")
@@ -264,7 +269,8 @@ def _fp8_fwd_device(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, nu
     qs = q_scale.to(device=v.device, dtype=torch.float32).contiguous()
     ks = k_scale.to(device=v.device, dtype=torch.float32).contiguous()
     out = _launch(q_fp8.view(torch.uint8), k_fp8.view(torch.uint8), v, seq_offsets, num_targets,
-                  attn_scale, rab, qs, ks, N, alpha, contextual_seq_len, _lib.DTYPE_FP8_E4M3)
+                  attn_scale, rab, qs, ks, N, alpha, contextual_seq_len, _lib.DTYPE_FP8_E4M3,
+                  max_attn_len, full_attn_size)
     return out, torch.zeros((1,), dtype=torch.float32, device=v.device)
 
 
@@ -314,7 +320,7 @@ def _fwd_fake(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_target
 
 @torch.library.register_fake("recir::hstu_jagged_attention_fp8_fwd")
 def _fp8_fwd_fake(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, num_targets, attn_scale,
-                  contextual_seq_len, rab=None):
+                  contextual_seq_len, rab=None, max_attn_len=0, full_attn_size=0):
     _check_common(q_fp8, k_fp8, v, seq_offsets, num_targets, N)
     return v.new_empty((q_fp8.shape[0], q_fp8.shape[1], v.shape[2])), v.new_empty((1,), dtype=torch.float32)
 
@@ -325,23 +331,25 @@ def _quant_fake(x):
 
 
 @torch.library.register_fake("recir::hstu_jagged_attention_bwd")
-def _bwd_fake(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab=None):
+def _bwd_fake(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab=None,
+              max_attn_len=0, full_attn_size=0):
     _check_common(q, k, v, seq_offsets, num_targets, N)
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 def _setup_context(ctx, inputs, output):
-    (N, alpha, q, k, v, seq_offsets, _mask_type, num_targets, attn_scale, _max_attn_len,
-     contextual_seq_len, _full_attn_size, _num_softmax_heads, rab) = inputs
+    (N, alpha, q, k, v, seq_offsets, _mask_type, num_targets, attn_scale, max_attn_len,
+     contextual_seq_len, full_attn_size, _num_softmax_heads, rab) = inputs
     ctx.save_for_backward(q, k, v, seq_offsets, num_targets, attn_scale, rab)
-    ctx.hstu_args = (int(N), float(alpha), int(contextual_seq_len))
+    ctx.hstu_args = (int(N), float(alpha), int(contextual_seq_len), int(max_attn_len), int(full_attn_size))
 
 
 def _autograd_backward(ctx, grad_out, _grad_aux):
     q, k, v, seq_offsets, num_targets, attn_scale, rab = ctx.saved_tensors
-    N, alpha, contextual_seq_len = ctx.hstu_args
+    N, alpha, contextual_seq_len, max_attn_len, full_attn_size = ctx.hstu_args
     dq, dk, dv = torch.ops.recir.hstu_jagged_attention_bwd(
-        grad_out, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab)
+        grad_out, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab,
+        max_attn_len, full_attn_size)
     # one gradient slot per forward argument; attn_scale and rab receive none
     return (None, None, dq, dk, dv, None, None, None, None, None, None, None, None, None)
 
@@ -357,12 +365,17 @@ hstu_jagged_attention_bwd = torch.ops.recir.hstu_jagged_attention_bwd
 
 def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len: int,
                           alpha: Optional[float] = None, attn_scale=None,
-                          contextual_seq_len: int = 0, rab=None) -> torch.Tensor:
+                          contextual_seq_len: int = 0, rab=None, max_attn_len: int = 0,
+                          full_attn_size: int = 0) -> torch.Tensor:
     """Packed HSTU attention with the defaults of the accelerator entry point it replaces
     (recir/ops/pallas/jagged_hstu_attention.py:1550-1555, recir/ops/helion/jagged_hstu_attention.py:
     798-804): ``num_targets=None`` means no targets, ``alpha=None`` means ``1/sqrt(Dqk)``,
     ``attn_scale=None`` means ``1/max_seq_len``.  Returns ``out [T, H, Dv]`` with rows at and
     after ``seq_offsets[-1]`` zero.  ``attn_scale`` may be a float, a 0-d tensor or a ``[T]`` tensor.
+    ``max_attn_len > 0`` selects the semi-local mask of the reference operator
+    (recir/ops/kjt_split_per_feature.cpp:654-668; the reference's accelerator kernels fix it to 256 /
+    256, recir/ops/helion/jagged_hstu_attention.py:95-147): history keys within ``max_attn_len``
+    positions, and full causal attention for the rows from ``full_attn_size`` before the targets on.
     """
     _check_common(q, k, v, seq_offsets, num_targets, max_seq_len)
     if alpha is None:
@@ -370,14 +383,15 @@ def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len
     if attn_scale is not None and not isinstance(attn_scale, torch.Tensor):
         attn_scale = torch.tensor(float(attn_scale), dtype=torch.float32, device=q.device)
     out, _ = hstu_jagged_attention_fwd(int(max_seq_len), float(alpha), q, k, v, seq_offsets,
-                                       "lower_triangular", num_targets, attn_scale, 0,
-                                       int(contextual_seq_len), 0, 0, rab)
+                                       "lower_triangular", num_targets, attn_scale, int(max_attn_len),
+                                       int(contextual_seq_len), int(full_attn_size), 0, rab)
     return out
 
 
 def jagged_hstu_attention_backward(dout, q, k, v, seq_offsets, num_targets=None, attn_scale=None, *,
                                    max_seq_len: int, alpha: Optional[float] = None,
-                                   contextual_seq_len: int = 0, rab=None):
+                                   contextual_seq_len: int = 0, rab=None, max_attn_len: int = 0,
+                                   full_attn_size: int = 0):
     """``(dq, dk, dv)`` of ``jagged_hstu_attention`` for the upstream gradient ``dout [T, H, Dv]``;
     argument order and defaults of ``pallas_jagged_hstu_attention_backward``
     (recir/ops/pallas/jagged_hstu_attention.py:1343-1358; called that way by its own test,
@@ -390,7 +404,8 @@ def jagged_hstu_attention_backward(dout, q, k, v, seq_offsets, num_targets=None,
     if attn_scale is not None and not isinstance(attn_scale, torch.Tensor):
         attn_scale = torch.tensor(float(attn_scale), dtype=torch.float32, device=q.device)
     return hstu_jagged_attention_bwd(dout, int(max_seq_len), float(alpha), q, k, v, seq_offsets,
-                                     num_targets, attn_scale, int(contextual_seq_len), rab)
+                                     num_targets, attn_scale, int(contextual_seq_len), rab,
+                                     int(max_attn_len), int(full_attn_size))
 
 
 def quantize_e4m3_per_head(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -403,7 +418,8 @@ def quantize_e4m3_per_head(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]
 
 def jagged_hstu_attention_fp8(q, k, v, seq_offsets, num_targets=None, *, max_seq_len: int,
                               alpha: Optional[float] = None, attn_scale=None,
-                              contextual_seq_len: int = 0, rab=None) -> torch.Tensor:
+                              contextual_seq_len: int = 0, rab=None, max_attn_len: int = 0,
+                              full_attn_size: int = 0) -> torch.Tensor:
     """Inference variant: bf16 q and k are quantised per head to e4m3 on the device, the scores are
     contracted in fp8 and dequantised with ``q_scale[h] * k_scale[h]``; v, P.V and out stay bf16."""
     _check_common(q, k, v, seq_offsets, num_targets, max_seq_len)
@@ -415,7 +431,7 @@ def jagged_hstu_attention_fp8(q, k, v, seq_offsets, num_targets=None, *, max_seq
     k8, ks = quantize_e4m3_per_head(k)
     out, _ = torch.ops.recir.hstu_jagged_attention_fp8_fwd(
         int(max_seq_len), float(alpha), q8, k8, v, qs, ks, seq_offsets, num_targets, attn_scale,
-        int(contextual_seq_len), rab)
+        int(contextual_seq_len), rab, int(max_attn_len), int(full_attn_size))
     return out
 
 

@@ -1,4 +1,5 @@
-"""Synthetic inputs for the five benchmark configurations of the HSTU attention path.
+"""Synthetic inputs for the benchmark configurations of the HSTU attention path (1-5 from the
+baseline; 6 = configuration 2 with the reference's semi-local mask, 256 local + 256 full tail).
 
 Sequence lengths come from ``numpy.random.Generator(PCG64(seed))``; q, k, v (and the relative
 attention bias) from ``torch.Generator().manual_seed(seed)`` on the CPU in the order q, k, v, rab.
@@ -28,6 +29,8 @@ class Workload:
     contextual_seq_len: int = 0
     rab: Optional[torch.Tensor] = None  # [H, 2*max_seq_len-1] float32
     lengths: np.ndarray = field(default=None)  # [B] full sequence lengths (history + targets)
+    max_attn_len: int = 0    # > 0: semi-local window over the history
+    full_attn_size: int = 0  # > 0 (with max_attn_len > 0): the last rows keep full causal attention
 
     @property
     def T(self) -> int:
@@ -42,12 +45,31 @@ class Workload:
         return int(self.q.shape[1])
 
     def pairs(self) -> int:
-        """Unmasked (query, key) pairs: h(h+1)/2 + t(h+1) + c(c-1)/2 per sequence."""
+        """Unmasked (query, key) pairs.  Causal mask: h(h+1)/2 + t(h+1) + c(c-1)/2 per sequence; in
+        general, per query row: the diagonal, the visible history keys (all keys below the row's
+        target-clamped position, or the last ``max_attn_len`` of them unless the row is in the
+        full-attention tail) and the contextual keys not counted yet."""
         total = 0
         c = self.contextual_seq_len
+        A, F = self.max_attn_len, self.full_attn_size
         for n, t in zip(self.lengths.tolist(), self.num_targets.tolist()):
-            h = n - t
-            total += h * (h + 1) // 2 + t * (h + 1) + (c * (c - 1) // 2 if c > 0 else 0)
+            if n <= 0:
+                continue
+            cap = min(max(n - t, -1), n)
+            m = np.arange(n, dtype=np.int64)
+            idm = np.minimum(m, cap)
+            pos = np.maximum(idm, 0)
+            if A > 0:
+                tail = (idm >= cap - F) if F > 0 else np.zeros(n, dtype=bool)
+                lo = np.where(tail, 0, np.maximum(pos - A, 0))
+            else:
+                lo = np.zeros(n, dtype=np.int64)
+            hist = pos - lo
+            total += int(n + hist.sum())
+            ce = min(c, n) if c > 0 else 0
+            if ce > 0:
+                in_ctx = np.maximum(np.minimum(pos, ce) - np.minimum(lo, ce), 0) + (m < ce)
+                total += int((ce - in_ctx).sum())
         return total
 
     def flops(self) -> int:
@@ -71,7 +93,7 @@ def history_lengths(config: int, seed: int = 0) -> np.ndarray:
     rng = np.random.Generator(np.random.PCG64(seed))
     if config == 1:
         return np.full((4,), 16, dtype=np.int64)
-    if config in (2, 3, 5):
+    if config in (2, 3, 5, 6):
         return rng.integers(256, 1985, size=32).astype(np.int64)
     if config == 4:
         return np.clip(rng.zipf(1.2, size=8), 128, 8064).astype(np.int64)
@@ -85,11 +107,13 @@ _SPEC = {
     3: (64, 2048, 4, 128, "bf16", 1.0 / 128),
     4: (128, 8192, 4, 128, "bf16", 1.0 / 128),
     5: (64, 2048, 4, 128, "fp8", 1.0 / 128),
+    6: (64, 2048, 4, 128, "bf16", 1.0 / 128),  # config 2 with the semi-local mask (256 local, 256 full tail)
 }
 
 
 def make_jagged(lengths, num_targets, H, Dqk, Dv, *, max_seq_len, alpha, dtype="fp32", seed=0,
-                contextual_seq_len=0, with_rab=False, rab_std=0.02, tail_rows=0, name="custom"):
+                contextual_seq_len=0, with_rab=False, rab_std=0.02, tail_rows=0, name="custom",
+                max_attn_len=0, full_attn_size=0):
     """Build a workload from explicit full lengths (history + targets) and target counts."""
     lengths = np.asarray(lengths, dtype=np.int64)
     T = int(lengths.sum()) + int(tail_rows)
@@ -108,7 +132,8 @@ def make_jagged(lengths, num_targets, H, Dqk, Dv, *, max_seq_len, alpha, dtype="
     return Workload(name=name, q=q, k=k, v=v, seq_offsets=torch.from_numpy(off),
                     num_targets=torch.as_tensor(np.asarray(num_targets, dtype=np.int64)),
                     max_seq_len=int(max_seq_len), alpha=float(alpha), dtype=dtype,
-                    contextual_seq_len=int(contextual_seq_len), rab=rab, lengths=lengths)
+                    contextual_seq_len=int(contextual_seq_len), rab=rab, lengths=lengths,
+                    max_attn_len=int(max_attn_len), full_attn_size=int(full_attn_size))
 
 
 def make_config(config: int, seed: int = 0) -> Workload:
@@ -117,4 +142,5 @@ def make_config(config: int, seed: int = 0) -> Workload:
     lengths = hist + t
     return make_jagged(lengths, np.full_like(hist, t), H, D, D, max_seq_len=N, alpha=alpha,
                        dtype=dtype, seed=seed, contextual_seq_len=8 if config == 3 else 0,
-                       with_rab=(config == 3), name=f"config{config}")
+                       with_rab=(config == 3), name=f"config{config}",
+                       max_attn_len=256 if config == 6 else 0, full_attn_size=256 if config == 6 else 0)

@@ -13,12 +13,14 @@ SMALL_CASES = {}
 
 
 def _add(name, lengths, targets, N, *, H=2, Dqk=8, Dv=6, alpha=None, attn_scale=0.17, ctx=0,
-         per_token_scale=False, seed=0, tail_rows=0, no_targets=False, bf16_inputs=False):
+         per_token_scale=False, seed=0, tail_rows=0, no_targets=False, bf16_inputs=False,
+         max_attn_len=0, full_attn_size=0):
     SMALL_CASES[name] = dict(lengths=list(lengths), targets=list(targets), N=N, H=H, Dqk=Dqk, Dv=Dv,
                              alpha=(1.0 / math.sqrt(Dqk)) if alpha is None else alpha,
                              attn_scale=attn_scale, ctx=ctx, per_token_scale=per_token_scale,
                              seed=seed, tail_rows=tail_rows, no_targets=no_targets,
-                             bf16_inputs=bf16_inputs)
+                             bf16_inputs=bf16_inputs, max_attn_len=max_attn_len,
+                             full_attn_size=full_attn_size)
 
 
 _add("ref_nonuniform_causal", [7, 3, 9], [0, 0, 0], 9)
@@ -42,6 +44,18 @@ _add("d128_mixed", [130, 64, 257, 1, 0, 200], [3, 64, 70, 1, 0, 0], 300, H=2, Dq
      alpha=1.0 / 128, attn_scale=None, tail_rows=3, bf16_inputs=True)
 _add("d128_ctx_refrule", [150, 70, 33], [20, 70, 0], 256, H=1, Dqk=128, Dv=128, alpha=1.0 / 128,
      attn_scale=0.01, ctx=4, bf16_inputs=True, seed=3)
+# semi-local mask of the reference operator (kjt_split_per_feature.cpp:654-668): window only, window
+# plus full-attention tail, a tail longer than the history, targets, the contextual switch, and
+# head-dim-128 shapes whose windows cut through key tiles
+_add("sl_window_only", [12, 3, 9, 20], [2, 0, 1, 5], 20, max_attn_len=3, seed=40)
+_add("sl_window_and_tail", [12, 3, 9, 20], [2, 0, 1, 5], 20, max_attn_len=3, full_attn_size=4, seed=41)
+_add("sl_tail_exceeds_history", [7, 3, 9], [2, 3, 0], 9, max_attn_len=2, full_attn_size=50, seed=42)
+_add("sl_ctx_refrule", [10, 6, 1], [3, 6, 0], 10, max_attn_len=2, full_attn_size=2, ctx=1, seed=43)
+_add("sl_full_size_without_window", [7, 3, 9], [1, 0, 2], 9, max_attn_len=0, full_attn_size=3, seed=44)
+_add("d128_semilocal", [300, 130, 64, 257, 1], [10, 0, 64, 30, 0], 320, H=2, Dqk=128, Dv=128, alpha=1.0 / 128,
+     attn_scale=None, tail_rows=2, bf16_inputs=True, max_attn_len=70, full_attn_size=40, seed=45)
+_add("d128_semilocal_window_only", [260, 200], [0, 33], 300, H=1, Dqk=128, Dv=128, alpha=1.0 / 128,
+     attn_scale=0.02, bf16_inputs=True, max_attn_len=64, seed=46)
 
 
 def build_inputs(case):
@@ -53,7 +67,8 @@ def build_inputs(case):
     wl = make_jagged(case["lengths"], case["targets"], case["H"], case["Dqk"], case["Dv"],
                      max_seq_len=case["N"], alpha=case["alpha"],
                      dtype="bf16" if case["bf16_inputs"] else "fp32", seed=case["seed"],
-                     contextual_seq_len=case["ctx"], tail_rows=case["tail_rows"])
+                     contextual_seq_len=case["ctx"], tail_rows=case["tail_rows"],
+                     max_attn_len=case["max_attn_len"], full_attn_size=case["full_attn_size"])
     if case["per_token_scale"]:
         g = torch.Generator().manual_seed(1000 + case["seed"])
         scale = torch.rand(wl.T, generator=g) * 0.5 + 0.05

@@ -37,7 +37,8 @@ SAMPLED_ROWS = 64
 def run_ref(wl, scale, nt):
     return hstu_oracle.ref_attn_fwd(wl.q, wl.k, wl.v, wl.seq_offsets, nt, max_seq_len=wl.max_seq_len,
                                     alpha=wl.alpha, attn_scale=scale,
-                                    contextual_seq_len=wl.contextual_seq_len)
+                                    contextual_seq_len=wl.contextual_seq_len,
+                                    max_attn_len=wl.max_attn_len, full_attn_size=wl.full_attn_size)
 
 
 def run_ref_bwd(wl, scale, nt, dout):
@@ -45,7 +46,8 @@ def run_ref_bwd(wl, scale, nt, dout):
     q, k, v = (t.detach().clone().requires_grad_(True) for t in (wl.q, wl.k, wl.v))
     out = hstu_oracle.ref_attn_fwd(q, k, v, wl.seq_offsets, nt, max_seq_len=wl.max_seq_len,
                                    alpha=wl.alpha, attn_scale=scale,
-                                   contextual_seq_len=wl.contextual_seq_len)
+                                   contextual_seq_len=wl.contextual_seq_len,
+                                   max_attn_len=wl.max_attn_len, full_attn_size=wl.full_attn_size)
     out.backward(dout[: out.shape[0]])
     return q.grad, k.grad, v.grad
 

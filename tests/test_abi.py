@@ -37,7 +37,7 @@ def test_header_symbols_are_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.recir_hstu_abi_version() == 2
+    assert lib.recir_hstu_abi_version() == 3
 
 
 def test_workspace_size_is_host_arithmetic(lib):
@@ -58,12 +58,13 @@ def test_workspace_size_is_host_arithmetic(lib):
     (dict(q=None), "non-null"),
     (dict(off=None), "seq_offsets"),
     (dict(dtype=2), "q_scale"),
+    (dict(A=-1), "max_attn_len and full_attn_size"),
 ])
 def test_invalid_arguments_are_rejected_before_launch(lib, kw, needle):
-    a = dict(q=8, k=8, v=8, out=8, off=8, T=4, B=1, H=1, Dqk=8, Dv=8, N=4, ctx=0, dtype=1)
+    a = dict(q=8, k=8, v=8, out=8, off=8, T=4, B=1, H=1, Dqk=8, Dv=8, N=4, ctx=0, dtype=1, A=0, F=0)
     a.update(kw)
     rc = lib.recir_hstu_attn_fwd(a["q"], a["k"], a["v"], a["out"], a["off"], None, None, None, None, None,
-                                 a["T"], a["B"], a["H"], a["Dqk"], a["Dv"], a["N"], a["ctx"], 1.0,
+                                 a["T"], a["B"], a["H"], a["Dqk"], a["Dv"], a["N"], a["ctx"], a["A"], a["F"], 1.0,
                                  a["dtype"], 0, None, 0, None)
     assert rc < 0
     assert needle in lib.recir_hstu_last_error().decode()
@@ -73,16 +74,17 @@ def test_invalid_arguments_are_rejected_before_launch(lib, kw, needle):
     (dict(T=-1), "negative size"),
     (dict(H=0), "must be positive"),
     (dict(N=0), "max_seq_len"),
+    (dict(F=-1), "max_attn_len and full_attn_size"),
     (dict(dtype=2), "bf16 and fp32"),
     (dict(dq=None), "non-null"),
     (dict(off=None), "seq_offsets"),
 ])
 def test_backward_invalid_arguments_are_rejected_before_launch(lib, kw, needle):
-    a = dict(dout=8, q=8, k=8, v=8, dq=8, dk=8, dv=8, off=8, T=4, B=1, H=1, Dqk=8, Dv=8, N=4, ctx=0, dtype=1)
+    a = dict(dout=8, q=8, k=8, v=8, dq=8, dk=8, dv=8, off=8, T=4, B=1, H=1, Dqk=8, Dv=8, N=4, ctx=0, dtype=1, A=0, F=0)
     a.update(kw)
     rc = lib.recir_hstu_attn_bwd(a["dout"], a["q"], a["k"], a["v"], a["dq"], a["dk"], a["dv"], a["off"], None,
-                                 None, None, a["T"], a["B"], a["H"], a["Dqk"], a["Dv"], a["N"], a["ctx"], 1.0,
-                                 a["dtype"], 0, None, 0, None)
+                                 None, None, a["T"], a["B"], a["H"], a["Dqk"], a["Dv"], a["N"], a["ctx"], a["A"], a["F"],
+                                 1.0, a["dtype"], 0, None, 0, None)
     assert rc < 0
     assert needle in lib.recir_hstu_last_error().decode()
 
@@ -109,7 +111,7 @@ def test_backward_fake_kernel_and_autograd_wiring():
 
 def test_empty_input_is_ok_without_launch(lib):
     rc = lib.recir_hstu_attn_fwd(None, None, None, None, None, None, None, None, None, None,
-                                 0, 0, 2, 8, 8, 4, 0, 1.0, 1, 0, None, 0, None)
+                                 0, 0, 2, 8, 8, 4, 0, 0, 0, 1.0, 1, 0, None, 0, None)
     assert rc == 0
 
 

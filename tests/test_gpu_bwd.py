@@ -45,7 +45,8 @@ def run_hip_bwd(wl, dout, *, attn_scale=None, num_targets="default", rab=None, c
     grads = recir_amd.jagged_hstu_attention_backward(
         dout.to(q.device, q.dtype), q, k, v, off, nt, sc, max_seq_len=wl.max_seq_len, alpha=wl.alpha,
         contextual_seq_len=wl.contextual_seq_len if ctx is None else ctx,
-        rab=None if rab is None else rab.cuda())
+        rab=None if rab is None else rab.cuda(), max_attn_len=wl.max_attn_len,
+        full_attn_size=wl.full_attn_size)
     torch.cuda.synchronize()
     return grads
 
@@ -69,7 +70,8 @@ def test_small_cases_match_backward_oracle_and_golden(oracle, name):
     want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
                            None if nt is None else nt.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
                            attn_scale=_scale_np(scale), contextual_seq_len=case["ctx"],
-                           ctx_mode=oracle.CTX_REFCPP)
+                           ctx_mode=oracle.CTX_REFCPP, max_attn_len=case["max_attn_len"],
+                           full_attn_size=case["full_attn_size"])
     end = int(wl.seq_offsets[-1])
     with ops.reference_contextual_rule():
         got = run_hip_bwd(wl, dout, attn_scale=scale, num_targets=ntd, dtype="fp32")
@@ -185,3 +187,25 @@ def test_tiled_backward_agrees_with_generic_at_full_size():
     assert _lib.last_kernel() == "bwd_generic_bf16"
     end = int(wl.seq_offsets[-1])
     assert_grads_close(got, [r.float().cpu().numpy() for r in ref], end, BF16_REL, "config2")
+
+
+@pytest.mark.parametrize("A,F,ctx", [(64, 0, 0), (100, 37, 0), (33, 200, 0), (128, 64, 5)])
+def test_semilocal_backward_matches_oracle(oracle, A, F, ctx):
+    from recir_amd import _lib, ops
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([1, 63, 64, 65, 127, 129, 0, 300, 517, 90], [0, 3, 64, 1, 100, 0, 0, 60, 130, 90], 2, 128, 128,
+                     max_seq_len=520, alpha=1.0 / 128, dtype="bf16", seed=60 + A, contextual_seq_len=ctx,
+                     tail_rows=3, max_attn_len=A, full_attn_size=F)
+    g = torch.Generator().manual_seed(4)
+    dout = torch.randn(wl.T, wl.H, 128, generator=g).to(torch.bfloat16).float()
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                           contextual_seq_len=ctx, max_attn_len=A, full_attn_size=F)
+    end = int(wl.seq_offsets[-1])
+    got = run_hip_bwd(wl, dout)
+    assert _lib.last_kernel() == "bwd_tiled_d128_bf16"
+    assert_grads_close(got, want, end, BF16_REL, f"A{A} F{F}")
+    with ops.force_kernel(ops.KERNEL_GENERIC):
+        gotg = run_hip_bwd(wl, dout)
+    assert_grads_close(gotg, want, end, BF16_REL, f"generic A{A} F{F}")

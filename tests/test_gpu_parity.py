@@ -381,3 +381,48 @@ def test_w64_kernel_full_size(oracle, config):
     ref = _fp8_reference(oracle, wl) if config == 5 else run_oracle(oracle, wl)
     assert_bf16_close(out, ref, f"w64 config{config}")
     assert_same_zero_structure(out, ref, int(wl.seq_offsets[-1]))
+
+
+def test_semilocal_full_size_matches_oracle(oracle):
+    """Configuration 2 with the reference's semi-local shape (256 local + 256 full tail): the tiled
+    kernel (which skips key tiles below the window) against the oracle."""
+    from recir_amd import _lib
+    from recir_amd.workloads import make_config
+
+    wl = make_config(6)
+    out = run_hip(wl)
+    assert _lib.last_kernel() == "tiled_d128_bf16"
+    ref = run_oracle(oracle, wl)
+    st = assert_bf16_close(out, ref, "config6")
+    print(f"config6: {st}")
+
+
+@pytest.mark.parametrize("A,F,ctx", [(64, 0, 0), (100, 37, 0), (33, 200, 0), (128, 64, 5), (1, 1, 0)])
+def test_semilocal_windows_across_tiles(oracle, A, F, ctx):
+    from recir_amd import ops
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([1, 63, 64, 65, 127, 129, 0, 300, 517, 90], [0, 3, 64, 1, 100, 0, 0, 60, 130, 90], 2, 128, 128,
+                     max_seq_len=520, alpha=1.0 / 128, dtype="bf16", seed=50 + A, contextual_seq_len=ctx,
+                     tail_rows=3, max_attn_len=A, full_attn_size=F)
+    ref = run_oracle(oracle, wl)
+    out = run_hip(wl)
+    assert_bf16_close(out, ref, f"A{A} F{F}")
+    assert not out[int(wl.seq_offsets[-1]):].float().cpu().numpy().any()
+    with ops.force_kernel(ops.KERNEL_GENERIC):
+        outg = run_hip(wl)
+    assert_bf16_close(outg, ref, f"generic A{A} F{F}")
+    # fp8 q/k variant shares the tile walk
+    out8 = run_hip(wl, fp8=True)
+    st = error_stats(out8, ref)
+    assert st["max_abs"] <= FP8_MAX_ABS, st
+
+
+def test_semilocal_is_rejected_by_the_tilings_without_it():
+    from recir_amd import ops
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([200], [10], 1, 128, 128, max_seq_len=256, alpha=1.0 / 128, dtype="bf16", max_attn_len=8)
+    for variant in (ops.KERNEL_TILED, ops.KERNEL_TILED_W64):
+        with ops.force_kernel(variant), pytest.raises(ValueError, match="semi-local"):
+            run_hip(wl)

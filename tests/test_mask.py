@@ -115,3 +115,68 @@ def test_workload_flop_model_matches_brute_force(oracle):
     wl4 = make_config(4)
     assert (wl4.lengths - 128).tolist() == [158, 128, 4705, 8064, 690, 8064, 128, 128]
     assert wl4.T == 23089
+
+
+def test_semilocal_mask_forms_agree_exhaustively(oracle):
+    """The "history key, near or full-tail row" form against the reference's clamped-id arithmetic
+    (kjt_split_per_feature.cpp:639-674) for every (n, t, A, F, ctx, m, j) with n <= 18."""
+    L = oracle.lib()
+    for n in range(0, 19):
+        for t in list(range(0, n + 1)) + [n + 2]:
+            for A in (0, 1, 2, 3, 6, 40):
+                for F in (0, 1, 3, 7, 40):
+                    for ctx, mode in ((0, 0), (2, 0), (1, 1)):
+                        for m in range(n):
+                            for j in range(n):
+                                a = L.hstu_oracle_keep_sl(m, j, n, t, ctx, mode, A, F)
+                                b = L.hstu_oracle_keep_sl_clamp_id(m, j, n, t, ctx, mode, A, F)
+                                assert a == b, (n, t, A, F, ctx, mode, m, j)
+
+
+def test_semilocal_mask_matches_the_accelerator_kernels_form(oracle):
+    """Third form, the one the reference's accelerator kernels use for the 256/256 shape
+    (helion/jagged_hstu_attention.py:124-147): local | full | diagonal on the raw query index,
+    valid when full_attn_size > 0 and targets do not exceed the length."""
+    for n in (1, 5, 13, 30):
+        for t in (0, 1, n // 3, n):
+            hist_end = n - t
+            for A in (1, 4, 9):
+                for F in (1, 3, 12, 64):
+                    full_start = hist_end - F
+                    for m in range(n):
+                        for j in range(n):
+                            hk = j < hist_end
+                            local = (m >= j) and (m - j <= A) and (m < full_start) and hk
+                            full = (m >= j) and (m >= full_start) and hk
+                            want = local or full or (m == j)
+                            assert oracle.keep_sl(m, j, n, t, 0, 0, A, F) == want, (n, t, A, F, m, j)
+
+
+def test_semilocal_reduces_to_causal_and_counts_rows(oracle):
+    n, t = 23, 5
+    cap = n - t
+    for m in range(n):
+        for j in range(n):
+            # no window: full_attn_size alone changes nothing; a window at least as long as the history is causal
+            assert oracle.keep_sl(m, j, n, t, 0, 0, 0, 7) == oracle.keep(m, j, n, t)
+            assert oracle.keep_sl(m, j, n, t, 0, 0, n, 0) == oracle.keep(m, j, n, t)
+    A, F = 4, 6
+    for m in range(n):
+        cnt = sum(oracle.keep_sl(m, j, n, t, 0, 0, A, F) for j in range(n))
+        idm = min(m, cap)
+        assert cnt == 1 + (idm if idm >= cap - F else min(idm, A))
+
+
+def test_workload_pair_count_matches_brute_force_with_windows(oracle):
+    from recir_amd.workloads import make_jagged
+
+    rng = np.random.default_rng(3)
+    for _ in range(60):
+        B = int(rng.integers(1, 5))
+        lengths = rng.integers(0, 28, size=B)
+        targets = [int(rng.integers(0, l + 3)) for l in lengths]
+        A, F, c = int(rng.choice([0, 1, 3, 7, 40])), int(rng.choice([0, 1, 4, 50])), int(rng.choice([0, 1, 3, 9]))
+        wl = make_jagged(lengths, targets, 1, 4, 4, max_seq_len=40, alpha=1.0, contextual_seq_len=c,
+                         max_attn_len=A, full_attn_size=F)
+        want = sum(oracle.count_pairs_sl(int(n), int(t), c, 0, A, F) for n, t in zip(lengths, targets))
+        assert wl.pairs() == want

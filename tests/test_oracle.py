@@ -26,7 +26,8 @@ def _run_case(oracle, case, ctx_mode=None, **kw):
     out = oracle.attn_fwd(wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
                           None if nt is None else nt.numpy(), max_seq_len=wl.max_seq_len,
                           alpha=wl.alpha, attn_scale=sc, contextual_seq_len=case["ctx"],
-                          ctx_mode=mode, **kw)
+                          ctx_mode=mode, max_attn_len=case["max_attn_len"],
+                          full_attn_size=case["full_attn_size"], **kw)
     return wl, out
 
 

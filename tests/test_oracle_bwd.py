@@ -31,7 +31,8 @@ def _oracle_bwd(oracle, case, ctx_mode=None, **kw):
     mode = oracle.CTX_REFCPP if ctx_mode is None else ctx_mode
     grads = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
                             None if nt is None else nt.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
-                            attn_scale=_scale_arg(scale), contextual_seq_len=case["ctx"], ctx_mode=mode, **kw)
+                            attn_scale=_scale_arg(scale), contextual_seq_len=case["ctx"], ctx_mode=mode,
+                            max_attn_len=case["max_attn_len"], full_attn_size=case["full_attn_size"], **kw)
     return wl, dout, grads
 
 
@@ -47,7 +48,8 @@ def test_backward_oracle_matches_reference_autograd_golden(oracle, name):
         assert not g[end:].any()  # tail rows get no gradient
 
 
-@pytest.mark.parametrize("name", ["per_token_scale", "d128_mixed", "d128_ctx_refrule"])
+@pytest.mark.parametrize("name", ["per_token_scale", "d128_mixed", "d128_ctx_refrule", "d128_semilocal",
+                                  "sl_window_and_tail"])
 def test_live_reference_autograd_when_built(oracle, name):
     if not oracle.ref_available():
         pytest.skip("oracle/_ref not built")
@@ -56,7 +58,8 @@ def test_live_reference_autograd_when_built(oracle, name):
     dout = upstream_gradient(case, wl)
     q, k, v = (t.clone().requires_grad_(True) for t in (wl.q, wl.k, wl.v))
     out = oracle.ref_attn_fwd(q, k, v, wl.seq_offsets, nt, max_seq_len=wl.max_seq_len, alpha=wl.alpha,
-                              attn_scale=scale, contextual_seq_len=case["ctx"])
+                              attn_scale=scale, contextual_seq_len=case["ctx"],
+                              max_attn_len=case["max_attn_len"], full_attn_size=case["full_attn_size"])
     out.backward(dout[: out.shape[0]])
     _, _, grads = _oracle_bwd(oracle, case)
     for g, want in zip(grads, (q.grad, k.grad, v.grad)):
