@@ -20,6 +20,16 @@ from .ops import (  # noqa: F401
     KERNEL_TILED_W64,
 )
 
+from .jagged import (  # noqa: F401,E402
+    concat_2D_jagged_fwd,
+    concat_2d_jagged,
+    dense_to_jagged,
+    jagged_to_padded_dense,
+    register_jagged_swaps,
+    split_2D_jagged_fwd,
+    split_2d_jagged,
+)
+
 __all__ = [
     "hstu_jagged_attention_fwd",
     "hstu_jagged_attention_bwd",

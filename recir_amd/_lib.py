@@ -31,6 +31,13 @@ EXPORTS = (
     "recir_hstu_abi_version",
     "recir_hstu_last_kernel",
 )
+# every symbol include/recir_jagged.h declares
+JAGGED_EXPORTS = (
+    "recir_jagged_to_padded_dense",
+    "recir_dense_to_jagged",
+    "recir_concat_2d_jagged",
+    "recir_split_2d_jagged",
+)
 
 _lib = None
 
@@ -63,6 +70,13 @@ def load() -> ctypes.CDLL:
     L.recir_hstu_quantize_e4m3_per_head.restype = ctypes.c_int
     L.recir_hstu_calibration_copy.argtypes = [vp, vp, sz, vp]
     L.recir_hstu_calibration_copy.restype = ctypes.c_int
+    i64 = ctypes.c_int64
+    L.recir_jagged_to_padded_dense.argtypes = [vp, vp, vp, i64, i32, i32, i64, i32, ctypes.c_uint64, u32, vp]
+    L.recir_dense_to_jagged.argtypes = [vp, vp, vp, i64, i32, i32, i64, u32, vp]
+    L.recir_concat_2d_jagged.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i64, i64, i64, i32, i32, u32, vp]
+    L.recir_split_2d_jagged.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i64, i64, i64, i32, u32, vp]
+    for name in JAGGED_EXPORTS:
+        getattr(L, name).restype = ctypes.c_int
     L.recir_hstu_last_error.argtypes = []
     L.recir_hstu_last_error.restype = ctypes.c_char_p
     L.recir_hstu_last_kernel.argtypes = []

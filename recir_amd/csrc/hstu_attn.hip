@@ -21,6 +21,7 @@
 #include <cstring>
 
 #include "recir_hstu.h"
+#include "recir_jagged.h"
 
 #include "hstu_common.h"
 #include "hstu_plan.h"
@@ -29,6 +30,7 @@
 #include "hstu_tiled_d128_w64.h"
 #include "hstu_bwd_generic.h"
 #include "hstu_bwd_d128.h"
+#include "jagged_rows.h"
 
 using namespace recir_hstu;
 
@@ -540,6 +542,133 @@ int recir_hstu_quantize_e4m3_per_head(const void* x_bf16, void* codes_u8, float*
     if (int rc = launch_status("hstu_quant_encode")) return rc;
   }
   return RECIR_HSTU_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------------
+// Jagged neighbours (row gathers)
+// ---------------------------------------------------------------------------------------------
+namespace {
+
+// largest chunk (16, 4, 2, 1 bytes) that divides the row size and keeps every pointer aligned
+int chunk_bytes(int64_t row_bytes, std::initializer_list<const void*> ptrs) {
+  size_t bits = (size_t)row_bytes;
+  for (const void* q : ptrs) bits |= (size_t)q;
+  if ((bits & 15) == 0) return 16;
+  if ((bits & 3) == 0) return 4;
+  if ((bits & 1) == 0) return 2;
+  return 1;
+}
+
+unsigned row_grid(long long chunks) {
+  const long long blocks = (chunks + 255) / 256;
+  return (unsigned)(blocks < 1 ? 1 : (blocks > 16384 ? 16384 : blocks));
+}
+
+int check_rows(int64_t row_bytes, int32_t B) {
+  if (row_bytes <= 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "row_bytes must be positive, got %lld", (long long)row_bytes);
+  if (B < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "negative batch size %d", B);
+  return 0;
+}
+
+#define RECIR_DISPATCH_CHUNK(cb, KERNEL, grid, stream, params, cpr)                               \
+  do {                                                                                            \
+    if (cb == 16) hipLaunchKernelGGL((KERNEL<uint4>), dim3(grid), dim3(256), 0, stream, params, cpr);          \
+    else if (cb == 4) hipLaunchKernelGGL((KERNEL<unsigned>), dim3(grid), dim3(256), 0, stream, params, cpr);   \
+    else if (cb == 2) hipLaunchKernelGGL((KERNEL<unsigned short>), dim3(grid), dim3(256), 0, stream, params, cpr); \
+    else hipLaunchKernelGGL((KERNEL<unsigned char>), dim3(grid), dim3(256), 0, stream, params, cpr);           \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int recir_jagged_to_padded_dense(const void* values, void* out, const void* offsets,
+                                 int64_t total_rows, int32_t B, int32_t max_len, int64_t row_bytes,
+                                 int32_t elem_bytes, uint64_t pad_bits, uint32_t flags,
+                                 void* hip_stream) {
+  using namespace recir_jagged;
+  if (int rc = check_rows(row_bytes, B)) return rc;
+  if (max_len < 0 || total_rows < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "negative size");
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "padding element of %d bytes (1, 2, 4 or 8 supported)", elem_bytes);
+  if (row_bytes % elem_bytes) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "row_bytes is not a multiple of elem_bytes");
+  if (B == 0 || max_len == 0) return RECIR_HSTU_OK;
+  if (!out || !offsets || (total_rows > 0 && !values)) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "null pointer");
+  const int cb = chunk_bytes(row_bytes, {values, out});
+  PadParams p{(const char*)values, (char*)out, {offsets, 0, (int)(flags & RECIR_HSTU_FLAG_OFFSETS_I32)},
+              total_rows, B, max_len, pad_bits, elem_bytes};
+  const long long cpr = row_bytes / cb;
+  RECIR_DISPATCH_CHUNK(cb, jagged_to_padded_dense_kernel, row_grid((long long)B * max_len * cpr), (hipStream_t)hip_stream, p, cpr);
+  return launch_status("jagged_to_padded_dense_kernel");
+}
+
+int recir_dense_to_jagged(const void* dense, void* out, const void* offsets, int64_t total_L,
+                          int32_t B, int32_t N, int64_t row_bytes, uint32_t flags, void* hip_stream) {
+  using namespace recir_jagged;
+  if (int rc = check_rows(row_bytes, B)) return rc;
+  if (N < 0 || total_L < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "negative size");
+  if (total_L == 0) return RECIR_HSTU_OK;
+  if (!out) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "null pointer");
+  if (B == 0 || N == 0) {  // nothing to gather from: zeros
+    if (row_bytes & 1) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "odd row size with an empty dense input");
+    hipLaunchKernelGGL(hstu_fill_zero, dim3(1024), dim3(256), 0, (hipStream_t)hip_stream, (unsigned short*)out,
+                       (size_t)(total_L * row_bytes) / 2);
+    return launch_status("hstu_fill_zero");
+  }
+  if (!dense || !offsets) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "null pointer");
+  const int cb = chunk_bytes(row_bytes, {dense, out});
+  UnpadParams p{(const char*)dense, (char*)out, {offsets, 0, (int)(flags & RECIR_HSTU_FLAG_OFFSETS_I32)}, total_L, B, N};
+  const long long cpr = row_bytes / cb;
+  RECIR_DISPATCH_CHUNK(cb, dense_to_jagged_kernel, row_grid(total_L * cpr), (hipStream_t)hip_stream, p, cpr);
+  return launch_status("dense_to_jagged_kernel");
+}
+
+int recir_concat_2d_jagged(const void* values_a, const void* values_b, void* out,
+                           const void* offsets_a, const void* offsets_b, int32_t B,
+                           int32_t dense_len_a, int32_t dense_len_b, int64_t rows_a, int64_t rows_b,
+                           int64_t row_bytes, int32_t is_replace, int32_t n_prefix_from_right,
+                           uint32_t flags, void* hip_stream) {
+  using namespace recir_jagged;
+  if (int rc = check_rows(row_bytes, B)) return rc;
+  // same argument rules as the reference (kjt_split_per_feature.cpp:108-121)
+  if (!offsets_a && !offsets_b) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "at least one input must be jagged");
+  if (n_prefix_from_right < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "n_prefix_from_right must be non-negative, got %d", n_prefix_from_right);
+  if (is_replace && n_prefix_from_right != 0)
+    return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "n_prefix_from_right is not supported when is_replace is true");
+  if (n_prefix_from_right != 0 && (!offsets_a || !offsets_b))
+    return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "n_prefix_from_right is only supported for two jagged inputs");
+  if (rows_a < 0 || rows_b < 0 || dense_len_a < 0 || dense_len_b < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "negative size");
+  const long long out_rows = is_replace ? rows_a : rows_a + rows_b;
+  if (out_rows == 0 || B == 0) return RECIR_HSTU_OK;
+  if (!out || (rows_a > 0 && !values_a) || (rows_b > 0 && !values_b)) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "null pointer");
+  const int i32 = (int)(flags & RECIR_HSTU_FLAG_OFFSETS_I32);
+  const int cb = chunk_bytes(row_bytes, {values_a, values_b, out});
+  ConcatParams p{(const char*)values_a, (const char*)values_b, (char*)out, {offsets_a, dense_len_a, i32},
+                 {offsets_b, dense_len_b, i32}, rows_a, rows_b, out_rows, B, is_replace, n_prefix_from_right};
+  const long long cpr = row_bytes / cb;
+  RECIR_DISPATCH_CHUNK(cb, concat_2d_jagged_kernel, row_grid(out_rows * cpr), (hipStream_t)hip_stream, p, cpr);
+  return launch_status("concat_2d_jagged_kernel");
+}
+
+int recir_split_2d_jagged(const void* values, void* out_a, void* out_b, const void* offsets_a,
+                          const void* offsets_b, int32_t B, int32_t dense_len_a, int32_t dense_len_b,
+                          int64_t rows_a, int64_t rows_b, int64_t row_bytes,
+                          int32_t n_prefix_to_right, uint32_t flags, void* hip_stream) {
+  using namespace recir_jagged;
+  if (int rc = check_rows(row_bytes, B)) return rc;
+  if (n_prefix_to_right < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "n_prefix_to_right must be non-negative, got %d", n_prefix_to_right);
+  if (rows_a < 0 || rows_b < 0 || dense_len_a < 0 || dense_len_b < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "negative size");
+  if (rows_a + rows_b == 0 || B == 0) return RECIR_HSTU_OK;
+  if (!values || (rows_a > 0 && !out_a) || (rows_b > 0 && !out_b)) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "null pointer");
+  const int i32 = (int)(flags & RECIR_HSTU_FLAG_OFFSETS_I32);
+  const int cb = chunk_bytes(row_bytes, {values, out_a, out_b});
+  SplitParams p{(const char*)values, (char*)out_a, (char*)out_b, {offsets_a, dense_len_a, i32},
+                {offsets_b, dense_len_b, i32}, rows_a, rows_b, rows_a + rows_b, B, n_prefix_to_right};
+  const long long cpr = row_bytes / cb;
+  RECIR_DISPATCH_CHUNK(cb, split_2d_jagged_kernel, row_grid((rows_a + rows_b) * cpr), (hipStream_t)hip_stream, p, cpr);
+  return launch_status("split_2d_jagged_kernel");
 }
 
 }  // extern "C"

@@ -36,6 +36,22 @@ def test_header_symbols_are_exported(lib):
         assert hasattr(lib, name), name
 
 
+def test_jagged_header_symbols_are_exported(lib):
+    from recir_amd import _lib
+
+    text = open(os.path.join(ROOT, "include", "recir_jagged.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    declared = sorted(set(re.findall(r"\b(recir_[a-z0-9_]+)\s*\(", text)))
+    assert declared == sorted(_lib.JAGGED_EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    # argument rules are checked before any launch (no GPU needed)
+    assert lib.recir_concat_2d_jagged(8, 8, 8, None, None, 1, 1, 1, 1, 1, 16, 0, 0, 0, None) < 0
+    assert "at least one input must be jagged" in lib.recir_hstu_last_error().decode()
+    assert lib.recir_jagged_to_padded_dense(8, 8, 8, 4, 1, 4, 0, 2, 0, 0, None) < 0
+    assert "row_bytes" in lib.recir_hstu_last_error().decode()
+
+
 def test_abi_version(lib):
     assert lib.recir_hstu_abi_version() == 3
 
