@@ -170,6 +170,49 @@ def bench_backward(args, wl, L, dev):
     }))
 
 
+def bench_jagged(args, wl, dev):
+    """HBM-bound neighbours of the path on the workload's own rows ([T, H * D] bf16): algorithmic bytes
+    (rows read + rows written) over the kernel time from HIP events, against 8 TB/s."""
+    import torch
+
+    import recir_amd
+
+    x = wl.q.to(dev, torch.bfloat16).reshape(wl.T, -1)
+    off = wl.seq_offsets.to(dev)
+    row = x.shape[1] * 2
+    dense = recir_amd.jagged_to_padded_dense(x, [off], [wl.max_seq_len], 0.0)
+    half = (off // 2)
+    a_off, b_off = half, off - half
+    a = x[: int(a_off[-1])].contiguous()
+    b = x[: int(b_off[-1])].contiguous()
+    cat = recir_amd.concat_2d_jagged(a, a_off, b, b_off)
+    ops_ = {
+        "jagged_to_padded_dense": (lambda: recir_amd.jagged_to_padded_dense(x, [off], [wl.max_seq_len], 0.0),
+                                   wl.T * row + wl.B * wl.max_seq_len * row),
+        "dense_to_jagged": (lambda: recir_amd.dense_to_jagged(dense, [off], wl.T), 2 * wl.T * row),
+        "concat_2d_jagged": (lambda: recir_amd.concat_2d_jagged(a, a_off, b, b_off), 2 * cat.shape[0] * row),
+        "split_2d_jagged": (lambda: recir_amd.split_2d_jagged(cat, a_off, b_off, a.shape[0], b.shape[0]),
+                            2 * cat.shape[0] * row),
+    }
+    res = {}
+    for name, (fn, nbytes) in ops_.items():
+        for _ in range(args.warmup):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        res[name] = {"ms_per_call": ms, "algorithmic_bytes": nbytes, "achieved_GBs": nbytes / (ms * 1e-3) / 1e9,
+                     "frac_of_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+    print(json.dumps({"metric": "jagged row-gather operators, algorithmic GB/s (includes allocation of the output)",
+                      "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": "u8",
+                      "data": "synthetic", "config": {"workload": describe(wl, args.config), "row_bytes": row},
+                      "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBS, "unit": "GB/s"}, "ops": res}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -181,6 +224,9 @@ def main():
     ap.add_argument("--backward", action="store_true",
                     help="measure the backward entry point (dq, dk, dv) instead of the forward; "
                          "prints its own JSON line (not the headline metric)")
+    ap.add_argument("--jagged", action="store_true",
+                    help="measure the jagged row-gather operators on the workload's [T, H*D] rows "
+                         "against the HBM roofline; prints its own JSON line")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="BYTES",
                     help="only launch the library's plain copy kernel on BYTES bytes a few times "
                          "(for scaling FETCH_SIZE / WRITE_SIZE counter readings) and exit")
@@ -212,6 +258,8 @@ def main():
     wl = make_config(args.config)
     if args.backward:
         return bench_backward(args, wl, L, dev)
+    if args.jagged:
+        return bench_jagged(args, wl, dev)
     fp8 = wl.dtype == "fp8"
     dt = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
     q, k, v = wl.q.to(dev, dt), wl.k.to(dev, dt), wl.v.to(dev, dt)

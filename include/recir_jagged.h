@@ -64,6 +64,31 @@ int recir_split_2d_jagged(const void* values, void* out_a, void* out_b, const vo
                           int64_t rows_a, int64_t rows_b, int64_t row_bytes,
                           int32_t n_prefix_to_right, uint32_t flags, void* hip_stream);
 
+/*
+ * out[r] = seq[r] + (pos_emb[pos(r)] + ts_emb[bucket(r)]) for every packed token r, plus the position
+ * rows and timestamp buckets used, each sorted ascending (stable) with its permutation.
+ * Replaces: facebook::recir::addTimestampPositionEmbeddings
+ * (recir/ops/kjt_split_per_feature.cpp:307-428; index rules :371-394).
+ * seq, out [L, D] bf16 or fp32 (seq_dtype: RECIR_HSTU_DTYPE_BF16 / _FP32); pos_emb [P, D] and ts_emb
+ * [TS >= 2049, D] share table_dtype; timestamps [B, Tmax] int64 (timestamps_float = 0) or float32;
+ * seq_lengths [B], num_targets [B] or NULL, seq_offsets [B + 1]: int64, or int32 with
+ * RECIR_HSTU_FLAG_OFFSETS_I32; sorted_pos, pos_order, sorted_ts, ts_order [L] int32.
+ * time_bucket_log: 0 = sqrt, 1 = log (the float log of the device; a value within one ulp of an
+ * integer can land in the neighbouring bucket of the host's).
+ * Data-dependent argument errors of the reference (lengths outside the timestamp range, more targets
+ * than tokens) are not raised: indices are clamped instead.
+ */
+int recir_add_timestamp_position_embeddings(
+    const void* seq, void* out, const void* seq_offsets, const void* pos_emb, const void* ts_emb,
+    const void* timestamps, const void* seq_lengths, const void* num_targets, int32_t* sorted_pos,
+    int32_t* pos_order, int32_t* sorted_ts, int32_t* ts_order, int64_t L, int32_t B, int32_t D,
+    int32_t P, int32_t TS, int32_t Tmax, int32_t max_contextual_seq_len, int32_t interleave_targets,
+    int32_t time_bucket_log, int32_t seq_dtype, int32_t table_dtype, int32_t timestamps_float,
+    uint32_t flags, void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* Scratch size the call above needs for L tokens. */
+size_t recir_add_timestamp_position_embeddings_workspace_bytes(int64_t L);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,14 @@ Plain numpy / Python loops over samples, each function following the reference l
                            [b[:n_prefix], a, b[n_prefix:]]; replace mode [a[:len_a-len_b], b]; a
                            dense side is [B, S, D])
   split_2d_jagged          recir/ops/kjt_split_per_feature.cpp:430-489
+  add_ts_pos_emb           recir/ops/kjt_split_per_feature.cpp:307-428 (position rule :371-382,
+                           time buckets :384-392, sums in the tensors' own types :396-401, the two
+                           sorted index lists :413-427); float32 arithmetic via numpy, bf16 via
+                           explicit round-to-nearest-even
+
+add_ts_pos_emb is pinned by the reference's known-answer test (KjtSplitPerFeatureTest.cpp:141-175)
+and by the compiled reference operator on random inputs (values bit-exact for sqrt buckets; log
+buckets compared away from integer boundaries, where one ulp of the logarithm decides).
 
 Pins (tests/test_jagged_oracle.py): the reference's own known-answer tests
 (recir/ops/tests/KjtSplitPerFeatureTest.cpp:50-91, :177-189), the reference's compiled C++ operators
@@ -105,3 +113,54 @@ def split_2d_jagged(values, offsets_a, offsets_b, dense_size_a=0, dense_size_b=0
     if dense_size_b:
         bb = bb.reshape((B, dense_size_b) + values.shape[1:])
     return a, bb
+
+
+def _round_bf16(x):
+    """float32 array rounded to the nearest bfloat16 (ties to even), returned as float32."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def add_ts_pos_emb(seq, offsets, pos_emb, ts_emb, timestamps, seq_lengths, num_targets=None,
+                   max_contextual_seq_len=0, interleave_targets=False, time_bucket_fn="sqrt",
+                   seq_bf16=False, tab_bf16=False):
+    """Returns (out [L, D] float32 holding values of the sequence type, position rows [L], buckets [L],
+    and the pre-bucket float values [L] so that a test can tell how close a bucket boundary is)."""
+    seq = np.asarray(seq, dtype=np.float32)
+    pos_emb, ts_emb = np.asarray(pos_emb, dtype=np.float32), np.asarray(ts_emb, dtype=np.float32)
+    offsets = np.asarray(offsets, dtype=np.int64)
+    timestamps = np.asarray(timestamps)
+    B = len(seq_lengths)
+    out = np.array(seq, copy=True)
+    pos_idx = np.zeros(seq.shape[0], dtype=np.int64)
+    ts_idx = np.zeros(seq.shape[0], dtype=np.int64)
+    pre = np.zeros(seq.shape[0], dtype=np.float32)
+    P = pos_emb.shape[0]
+    for b in range(B):
+        s, e = int(offsets[b]), int(offsets[b + 1])
+        n = e - s
+        length = int(seq_lengths[b])
+        high = length
+        if num_targets is not None:
+            high -= int(num_targets[b]) * (2 if interleave_targets else 1)
+        i = np.arange(n, dtype=np.int64)
+        pi = high - np.minimum(i, high) + max_contextual_seq_len
+        pi = np.minimum(pi, P - 1)
+        pi = np.where(i < max_contextual_seq_len, i, pi)
+        row = timestamps[b]
+        delta = (row[length - 1] - row[:n]).astype(np.float32)
+        delta = np.maximum(delta, np.float32(1e-6)) / np.float32(60.0)
+        x = np.log(delta) if time_bucket_fn == "log" else np.sqrt(delta)
+        x = x.astype(np.float32)
+        ti = np.clip(np.trunc(x).astype(np.int64), 0, 2048)
+        add = pos_emb[pi] + ts_emb[ti]
+        if tab_bf16:
+            add = _round_bf16(add)
+        if seq_bf16:
+            add = _round_bf16(add)
+            out[s:e] = _round_bf16(seq[s:e] + add)
+        else:
+            out[s:e] = seq[s:e] + add
+        pos_idx[s:e], ts_idx[s:e], pre[s:e] = pi, ti, x
+    return out, pos_idx, ts_idx, pre

@@ -21,6 +21,7 @@ from .ops import (  # noqa: F401
 )
 
 from .jagged import (  # noqa: F401,E402
+    add_ts_pos_emb_fwd,
     concat_2D_jagged_fwd,
     concat_2d_jagged,
     dense_to_jagged,

@@ -37,6 +37,8 @@ JAGGED_EXPORTS = (
     "recir_dense_to_jagged",
     "recir_concat_2d_jagged",
     "recir_split_2d_jagged",
+    "recir_add_timestamp_position_embeddings",
+    "recir_add_timestamp_position_embeddings_workspace_bytes",
 )
 
 _lib = None
@@ -75,8 +77,11 @@ def load() -> ctypes.CDLL:
     L.recir_dense_to_jagged.argtypes = [vp, vp, vp, i64, i32, i32, i64, u32, vp]
     L.recir_concat_2d_jagged.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i64, i64, i64, i32, i32, u32, vp]
     L.recir_split_2d_jagged.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i64, i64, i64, i32, u32, vp]
+    L.recir_add_timestamp_position_embeddings.argtypes = [vp] * 12 + [i64] + [i32] * 11 + [u32, vp, sz, vp]
+    L.recir_add_timestamp_position_embeddings_workspace_bytes.argtypes = [i64]
     for name in JAGGED_EXPORTS:
         getattr(L, name).restype = ctypes.c_int
+    L.recir_add_timestamp_position_embeddings_workspace_bytes.restype = sz
     L.recir_hstu_last_error.argtypes = []
     L.recir_hstu_last_error.restype = ctypes.c_char_p
     L.recir_hstu_last_kernel.argtypes = []

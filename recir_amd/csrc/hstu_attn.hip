@@ -31,6 +31,9 @@
 #include "hstu_bwd_generic.h"
 #include "hstu_bwd_d128.h"
 #include "jagged_rows.h"
+#include "ts_pos_embeddings.h"
+
+#include <rocprim/rocprim.hpp>
 
 using namespace recir_hstu;
 
@@ -669,6 +672,78 @@ int recir_split_2d_jagged(const void* values, void* out_a, void* out_b, const vo
   const long long cpr = row_bytes / cb;
   RECIR_DISPATCH_CHUNK(cb, split_2d_jagged_kernel, row_grid((rows_a + rows_b) * cpr), (hipStream_t)hip_stream, p, cpr);
   return launch_status("split_2d_jagged_kernel");
+}
+
+}  // extern "C"
+
+namespace {
+size_t sort_temp_bytes(int64_t L) {
+  size_t bytes = 0;
+  (void)rocprim::radix_sort_pairs(nullptr, bytes, (const int*)nullptr, (int*)nullptr, (const int*)nullptr, (int*)nullptr,
+                                  (size_t)(L > 0 ? L : 1), 0, 12);
+  return bytes;
+}
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+}  // namespace
+
+extern "C" {
+
+size_t recir_add_timestamp_position_embeddings_workspace_bytes(int64_t L) {
+  if (L < 0) return 0;
+  // unsorted position rows, unsorted buckets, identity permutation, sort scratch
+  return 3 * align256((size_t)L * 4) + align256(sort_temp_bytes(L));
+}
+
+int recir_add_timestamp_position_embeddings(
+    const void* seq, void* out, const void* seq_offsets, const void* pos_emb, const void* ts_emb,
+    const void* timestamps, const void* seq_lengths, const void* num_targets, int32_t* sorted_pos,
+    int32_t* pos_order, int32_t* sorted_ts, int32_t* ts_order, int64_t L, int32_t B, int32_t D,
+    int32_t P, int32_t TS, int32_t Tmax, int32_t max_contextual_seq_len, int32_t interleave_targets,
+    int32_t time_bucket_log, int32_t seq_dtype, int32_t table_dtype, int32_t timestamps_float,
+    uint32_t flags, void* workspace, size_t workspace_bytes, void* hip_stream) {
+  using namespace recir_jagged;
+  hipStream_t stream = (hipStream_t)hip_stream;
+  if (L < 0 || B < 0 || D <= 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "bad sizes: L=%lld B=%d D=%d", (long long)L, B, D);
+  if (L > 0x7fffffffll) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "more than 2^31 - 1 tokens");
+  // same shape rules as the reference (kjt_split_per_feature.cpp:320-347)
+  if (TS < 2049) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "timestamp embeddings must contain 2049 buckets, got %d", TS);
+  if (P <= 0 || Tmax <= 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "position table and timestamps must be non-empty");
+  if (max_contextual_seq_len < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "max_contextual_seq_len must be >= 0");
+  for (int dt : {seq_dtype, table_dtype})
+    if (dt != RECIR_HSTU_DTYPE_BF16 && dt != RECIR_HSTU_DTYPE_FP32)
+      return fail(RECIR_HSTU_ERR_UNSUPPORTED, "embeddings must be bf16 or fp32, got dtype %d", dt);
+  if (L == 0) return RECIR_HSTU_OK;
+  if (B == 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "tokens without sequences");
+  if (!seq || !out || !seq_offsets || !pos_emb || !ts_emb || !timestamps || !seq_lengths || !sorted_pos || !pos_order ||
+      !sorted_ts || !ts_order)
+    return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "null pointer");
+  const size_t need = recir_add_timestamp_position_embeddings_workspace_bytes(L);
+  if (!workspace || workspace_bytes < need || ((size_t)workspace & 255))
+    return fail(RECIR_HSTU_ERR_WORKSPACE, "workspace of %zu bytes (256-byte aligned) required, got %zu at %p", need,
+                workspace_bytes, workspace);
+  const size_t seg = align256((size_t)L * 4);
+  TsPosParams p;
+  memset(&p, 0, sizeof(p));
+  p.seq = seq; p.out = out; p.offsets = seq_offsets; p.pos_emb = pos_emb; p.ts_emb = ts_emb;
+  p.timestamps = timestamps; p.seq_lengths = seq_lengths; p.num_targets = num_targets;
+  p.pos_idx = (int*)workspace; p.ts_idx = (int*)((char*)workspace + seg); p.iota = (int*)((char*)workspace + 2 * seg);
+  p.L = L; p.B = B; p.D = D; p.P = P; p.TS = TS; p.Tmax = Tmax; p.max_ctx = max_contextual_seq_len;
+  p.interleave = interleave_targets != 0; p.use_log = time_bucket_log != 0;
+  p.seq_bf16 = seq_dtype == RECIR_HSTU_DTYPE_BF16; p.tab_bf16 = table_dtype == RECIR_HSTU_DTYPE_BF16;
+  p.ts_is_float = timestamps_float != 0; p.i32 = (int)(flags & RECIR_HSTU_FLAG_OFFSETS_I32);
+  const long long chunks = L * ((D + 7) / 8);
+  hipLaunchKernelGGL(ts_pos_embeddings_kernel, dim3(row_grid(chunks)), dim3(256), 0, stream, p);
+  if (int rc = launch_status("ts_pos_embeddings_kernel")) return rc;
+  void* temp = (char*)workspace + 3 * seg;
+  size_t temp_bytes = sort_temp_bytes(L);
+  // position rows fit 31 bits, buckets 12 (0..2048)
+  hipError_t e = rocprim::radix_sort_pairs(temp, temp_bytes, (const int*)p.pos_idx, (int*)sorted_pos, (const int*)p.iota,
+                                           (int*)pos_order, (size_t)L, 0, 31, stream);
+  if (e != hipSuccess) return fail((int)e, "sort of the position rows: %s", hipGetErrorString(e));
+  e = rocprim::radix_sort_pairs(temp, temp_bytes, (const int*)p.ts_idx, (int*)sorted_ts, (const int*)p.iota, (int*)ts_order,
+                                (size_t)L, 0, 12, stream);
+  if (e != hipSuccess) return fail((int)e, "sort of the timestamp buckets: %s", hipGetErrorString(e));
+  return RECIR_HSTU_OK;
 }
 
 }  // extern "C"

@@ -30,6 +30,8 @@ _SCHEMAS = {
     "split_2d_jagged": "split_2d_jagged(Tensor values, Tensor offsets_left, Tensor offsets_right, SymInt seq_len_a, SymInt seq_len_b) -> (Tensor, Tensor)",
     "concat_2D_jagged_fwd": "concat_2D_jagged_fwd(int max_seq_len, Tensor values_a, Tensor values_b, Tensor? offsets_a, Tensor? offsets_b, bool is_replace, int n_prefix_from_right) -> Tensor",
     "split_2D_jagged_fwd": "split_2D_jagged_fwd(Tensor values, int max_seq_len, Tensor offsets_a, Tensor offsets_b, int seq_len_a, int seq_len_b, bool is_dense_a, bool is_dense_b, int dense_size, int n_prefix_to_right, int B) -> (Tensor, Tensor)",
+    # hammer::add_ts_pos_emb_fwd_op, recir/ops/kjt_split_per_feature.cpp:776-779
+    "add_ts_pos_emb_fwd": "add_ts_pos_emb_fwd(Tensor seq_embeddings, Tensor seq_offsets, Tensor pos_embeddings, Tensor ts_embeddings, Tensor timestamps, Tensor seq_lengths, Tensor? num_targets, int max_seq_len, int max_contextual_seq_len, bool interleave_targets, str time_bucket_fn) -> (Tensor, Tensor, Tensor, Tensor, Tensor)",
 }
 _defined_here = set()
 
@@ -260,7 +262,68 @@ def _split_2D_jagged_fwd_device(values, max_seq_len, offsets_a, offsets_b, seq_l
     return a, b
 
 
+def _add_ts_pos_emb_fwd_device(seq_embeddings, seq_offsets, pos_embeddings, ts_embeddings, timestamps, seq_lengths,
+                               num_targets, max_seq_len, max_contextual_seq_len, interleave_targets, time_bucket_fn):
+    """Argument checks and messages of the reference (recir/ops/kjt_split_per_feature.cpp:320-347)."""
+    _need_cuda("add_ts_pos_emb_fwd", seq_embeddings)
+    L = _lib.load()
+    if seq_embeddings.dim() != 2:
+        raise ValueError("sequence embeddings must be two-dimensional")
+    if pos_embeddings.dim() != 2 or ts_embeddings.dim() != 2:
+        raise ValueError("position and timestamp embeddings must be two-dimensional")
+    if timestamps.dim() != 2:
+        raise ValueError("timestamps must be two-dimensional")
+    if seq_lengths.dim() != 1:
+        raise ValueError("sequence lengths must be one-dimensional")
+    D = seq_embeddings.shape[1]
+    if pos_embeddings.shape[1] != D or ts_embeddings.shape[1] != D:
+        raise ValueError("all embeddings must have the same dimension")
+    if ts_embeddings.shape[0] < 2049:
+        raise ValueError("timestamp embeddings must contain 2049 buckets")
+    B = seq_lengths.numel()
+    if seq_offsets.numel() != B + 1:
+        raise ValueError("sequence offsets size must match the batch size")
+    if timestamps.shape[0] != B:
+        raise ValueError("timestamps size must match the batch size")
+    if num_targets is not None and num_targets.numel() != B:
+        raise ValueError("num_targets size must match the batch size")
+    if time_bucket_fn not in ("log", "sqrt"):
+        raise ValueError("time_bucket_fn must be 'log' or 'sqrt'")
+    codes = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_FP32}
+    if seq_embeddings.dtype not in codes or pos_embeddings.dtype not in codes or ts_embeddings.dtype != pos_embeddings.dtype:
+        raise ValueError("embeddings must be bfloat16 or float32, and both tables of one dtype")
+    if timestamps.dtype == torch.float32:
+        ts_float = 1
+    elif timestamps.dtype == torch.int64:
+        ts_float = 0
+    else:
+        raise ValueError(f"timestamps must be int64 or float32, got {timestamps.dtype}")
+    off, flags = _offsets(seq_offsets)
+    lens = seq_lengths.to(off.dtype).contiguous()
+    nt = None if num_targets is None else num_targets.to(off.dtype).contiguous()
+    seq = seq_embeddings.contiguous()
+    pos, ts_tab, stamps = pos_embeddings.contiguous(), ts_embeddings.contiguous(), timestamps.contiguous()
+    rows = seq.shape[0]
+    dev = seq.device
+    out = torch.empty_like(seq)
+    idx = [torch.empty((rows,), dtype=torch.int32, device=dev) for _ in range(4)]
+    if rows > 0:
+        ws_bytes = L.recir_add_timestamp_position_embeddings_workspace_bytes(rows)
+        ws = torch.empty((ws_bytes + 256,), dtype=torch.uint8, device=dev)
+        base = (ws.data_ptr() + 255) // 256 * 256
+        with torch.cuda.device(dev):
+            rc = L.recir_add_timestamp_position_embeddings(
+                seq.data_ptr(), out.data_ptr(), off.data_ptr(), pos.data_ptr(), ts_tab.data_ptr(), stamps.data_ptr(),
+                lens.data_ptr(), None if nt is None else nt.data_ptr(), idx[0].data_ptr(), idx[1].data_ptr(),
+                idx[2].data_ptr(), idx[3].data_ptr(), rows, B, D, pos.shape[0], ts_tab.shape[0], stamps.shape[1],
+                int(max_contextual_seq_len), int(bool(interleave_targets)), int(time_bucket_fn == "log"),
+                codes[seq.dtype], codes[pos.dtype], ts_float, flags, base, ws_bytes, _stream(dev))
+        _status("recir_add_timestamp_position_embeddings", rc)
+    return out, idx[0], idx[1], idx[2], idx[3]
+
+
 _IMPLS = {
+    "add_ts_pos_emb_fwd": _add_ts_pos_emb_fwd_device,
     "jagged_to_padded_dense": _jagged_to_padded_dense_device,
     "dense_to_jagged": _dense_to_jagged_device,
     "concat_2d_jagged": _concat_2d_jagged_device,
@@ -368,6 +431,16 @@ if "split_2D_jagged_fwd" in _defined_here:
         return a, b
 
 
+if "add_ts_pos_emb_fwd" in _defined_here:
+    @torch.library.register_fake("recir::add_ts_pos_emb_fwd")
+    def _add_ts_pos_fake(seq_embeddings, seq_offsets, pos_embeddings, ts_embeddings, timestamps, seq_lengths, num_targets,
+                         max_seq_len, max_contextual_seq_len, interleave_targets, time_bucket_fn):
+        n = seq_embeddings.shape[0]
+        i32 = [seq_embeddings.new_empty((n,), dtype=torch.int32) for _ in range(4)]
+        return (torch.empty_like(seq_embeddings), *i32)
+
+
+add_ts_pos_emb_fwd = torch.ops.recir.add_ts_pos_emb_fwd
 jagged_to_padded_dense = torch.ops.recir.jagged_to_padded_dense
 dense_to_jagged = torch.ops.recir.dense_to_jagged
 concat_2d_jagged = torch.ops.recir.concat_2d_jagged
@@ -381,7 +454,8 @@ def register_jagged_swaps(registry) -> int:
     (same positional arguments; recir/lowering/op_swap.py:78-97 rewrites only the node target)."""
     added = 0
     pairs = (("generative_recommenders", "concat_2D_jagged_fwd_op", concat_2D_jagged_fwd),
-             ("generative_recommenders", "split_2D_jagged_fwd_op", split_2D_jagged_fwd))
+             ("generative_recommenders", "split_2D_jagged_fwd_op", split_2D_jagged_fwd),
+             ("hammer", "add_ts_pos_emb_fwd_op", add_ts_pos_emb_fwd))
     for ns, name, repl in pairs:
         try:
             packet = getattr(getattr(torch.ops, ns), name)

