@@ -26,7 +26,10 @@
 // r stored at chunk c ^ f(r & 7) with f(r) = ((r & 3) << 1) | (r >> 2).  Eight consecutive rows then
 // put one logical chunk on all banks (ds_read_b128 fragments), and four consecutive rows put one
 // logical 32-byte slot on all banks (ds_read_b64_tr_b16 fragments), so both read patterns of a
-// tile are free of bank conflicts.  Tiles travel HBM -> LDS with global_load_lds_dwordx4 (64 lanes
+// tile are free of bank conflicts on 32 banks.  (gfx950's LDS has 64: both patterns then run at half
+// of its 256 bytes per clock.  The 16-row variant c ^ (((r & 3) << 2) | ((r >> 2) & 3)) removes that,
+// but measured no faster and costs address registers, so the 8-row form stays.)
+// Tiles travel HBM -> LDS with global_load_lds_dwordx4 (64 lanes
 // x 16 bytes land on consecutive LDS addresses; the swizzle is applied to the address each lane
 // fetches), two stages, one barrier per tile.
 #pragma once
@@ -102,8 +105,7 @@ __device__ __forceinline__ void bwd_issue_rows(const char* gbase, unsigned row_b
     const int j = 4 * wave + ps;
     const int row = min(4 * j + c.ld_row, last);
     const unsigned chunk = (ps & 1) ? c.ld_swz_o : c.ld_swz_e;
-    const char* src = gbase + (size_t)row * row_bytes + chunk * 16u;
-    __builtin_amdgcn_global_load_lds((const unsigned*)src, (lds_void*)&tile[j * 512], 16, 0, 0);
+    copy16(gbase, (unsigned)row * row_bytes + chunk * 16u, (unsigned)(size_t)&tile[j * 512]);
   }
 }
 

@@ -17,9 +17,12 @@
 // tile i run and must have landed (vmcnt) before the barrier that ends tile i.
 //
 // LDS layouts (both tiles are [BN rows][256 bytes], swizzled in place of padding):
-//   K  16-byte chunk c of row r sits at chunk c ^ (r & 7)         (ds_read_b128 of 8 rows: all banks)
-//   V  32-byte slot  s of row r sits at slot  s ^ (r & 3)         (transposing read of 4 rows x 32 B:
-//                                                                  all banks)
+//   K  16-byte chunk c of row r sits at chunk c ^ (r & 7)
+//   V  32-byte slot  s of row r sits at slot  s ^ (r & 3)
+// These are free of bank conflicts for 32 banks.  gfx950's LDS has 64 (256 bytes per clock), where
+// they run at half rate; the conflict-free forms (K: c ^ (r & 15), V: s ^ 2 (r & 3), HSTU_DL_SWZ64)
+// halve the LDS busy time but need six more address registers, and the kernel, which is bound by
+// VALU issue and not by LDS bandwidth, is slower with them.
 // A global_load_lds instruction writes 64 lanes x 16 bytes to consecutive LDS addresses, so the
 // swizzle is applied to the global address each lane fetches.
 #pragma once
@@ -43,6 +46,51 @@ typedef __attribute__((ext_vector_type(8))) int i32x8;
 // contraction stay bf16.  The K tile is then [BN rows][128 bytes], chunk c of row r at c ^ (r & 7).
 // SEMI: the semi-local mask (max_attn_len > 0) -- window test in the partial tiles, key tiles below
 // every row's window not walked; the causal instantiation carries none of it.
+#ifndef HSTU_DL_ASM_COPY
+#define HSTU_DL_ASM_COPY 1
+#endif
+// One global -> LDS copy instruction: 64 lanes x 16 bytes from base + per-lane offset to 1 KB of
+// consecutive LDS.  Written as assembly so that the compiler does not treat it as an access that
+// may touch both memories: with the builtin every later wait for an LDS read becomes a wait for
+// all of them (and for nothing less), which exposes a full LDS round trip several times per tile.
+// Ordering against LDS reads is the caller's (vmcnt wait + barrier).
+__device__ __forceinline__ void copy16(const void* base, unsigned lane_off, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_addr), "v"(lane_off), "s"(base) : "memory");
+}
+// LDS swizzle of the bf16 K and V tiles: 1 = free of bank conflicts on the 64-bank LDS
+// (K chunk ^ (row & 15), V slot ^ 2 (row & 3)); 0 = the 32-bank forms (K chunk ^ (row & 7), V slot ^
+// (row & 3)), which run the LDS reads at half rate but need six address registers fewer.
+#ifndef HSTU_DL_SWZ64
+#define HSTU_DL_SWZ64 0
+#endif
+constexpr int KSWZ = HSTU_DL_SWZ64 ? 15 : 7;
+constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
+#ifndef HSTU_DL_SLOTS
+#define HSTU_DL_SLOTS 1
+#endif
+#ifndef HSTU_DL_PDK
+#define HSTU_DL_PDK 16  // K fragments (slots 0..15) are requested this many slots ahead
+#endif
+#ifndef HSTU_DL_PDV
+#define HSTU_DL_PDV 10  // V fragments (slots 16..31) likewise
+#endif
+#ifndef HSTU_DL_ABL
+#define HSTU_DL_ABL 0  // debug builds: 1 no SiLU, 2 no LDS fragment reads, 32 no V reads, 4 no copies, 16 no barrier
+#endif
+#if HSTU_DL_ABL & 16
+#define HSTU_DL_TILE_SYNC() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
+#elif HSTU_DL_ABL & 8
+#define HSTU_DL_TILE_SYNC() __syncthreads()
+#else
+#define HSTU_DL_TILE_SYNC() do { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); __syncthreads(); } while (0)
+#endif
+#ifndef HSTU_DL_C0
+#define HSTU_DL_C0 0     // slot of the first copy instruction of the next tile
+#define HSTU_DL_CSTEP 1  // slots between copy instructions
+#endif
+#ifndef HSTU_DL_U0
+#define HSTU_DL_U0 9  // slot of the first SiLU unit
+#endif
 template <bool HAS_RAB, bool FP8, bool SEMI>
 __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
   // The two pipeline stages are separate objects and every access names its stage at compile time:
@@ -68,21 +116,26 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
   zero_tail_rows<256>(p, (size_t)p.H * HD * 2);
 
   // ---- per-lane constants of the LDS access patterns ----
-  // K fragment (ds_read_b128): row 32 kvb + l32, chunk (2 kk + half) ^ (l32 & 7); kk and kk + 4 differ
-  // by 128 bytes, kk & 3 enters as an XOR of address bits 5..6
-  const unsigned ks_rd = (unsigned)l32 * (HD * 2) + (unsigned)((half ^ (l32 & 7)) * 16);
+  // K fragment (ds_read_b128): row 32 kvb + l32, chunk (2 kk + half) ^ (l32 & 15); kk enters as an
+  // XOR of address bits 5..7
+  const unsigned ks_rd = (unsigned)l32 * (HD * 2) + (unsigned)((half ^ (l32 & KSWZ)) * 16);
   // V^T fragment (two ds_read_b64_tr_b16): source lane s = lane & 15 of a 16-lane group supplies the
   // 8 bytes at row 4 half + (s >> 2) (+ 16 s2 + 8 rd), d = 32 db + 16 dgrp + 4 (s & 3) .. +3
   const int tr_s = lane & 15, tr_r = tr_s >> 2, tr_c = tr_s & 3, tr_dgrp = (lane >> 4) & 1;
+#if HSTU_DL_SWZ64
+  const unsigned vt_rd = (unsigned)(4 * half + tr_r) * (HD * 2) + (unsigned)tr_r * 64u + (unsigned)tr_dgrp * 32u + (unsigned)tr_c * 8u;
+#else
   const unsigned vt_base = (unsigned)(4 * half + tr_r) * (HD * 2) + (unsigned)((tr_dgrp ^ (tr_r & 1)) * 32) + (unsigned)tr_c * 8u;
   const unsigned vt_rd_e = vt_base + (unsigned)((tr_r >> 1) * 64);  // even db: slot bit 1 flipped upwards
   const unsigned vt_rd_o = vt_base - (unsigned)((tr_r >> 1) * 64);  // odd db: downwards
+#endif
   // global -> LDS copies: instruction j of a tile (16 per matrix, wave w issues j = 4 w + ps) fills rows
   // 4 j .. 4 j + 3; lane i lands at row 4 j + (i >> 4), physical chunk i & 15
   const int ld_row = lane >> 4, ld_chunk = lane & 15;
-  // fp8 K: fragment = 32 bytes at row 32 kvb + l32, chunks (4 st + 2 half + {0, 1}) ^ (l32 & 7); a copy
+  // fp8 K: fragment = 32 bytes at row 32 kvb + l32, chunks (4 st + 2 half + {0, 1}) ^ ((l32 >> 1) & 7)
+  // (rows of 128 bytes: two rows per pass over the banks); a copy
   // instruction fills 8 rows of 128 bytes, lane i lands at row 8 j + (i >> 3), physical chunk i & 7
-  const unsigned k8_rd = (unsigned)l32 * 128u + (unsigned)(((2 * half) ^ (l32 & 7)) * 16);
+  const unsigned k8_rd = (unsigned)l32 * 128u + (unsigned)(((2 * half) ^ ((l32 >> 1) & 7)) * 16);
   const int ld8_row = lane >> 3, ld8_chunk = lane & 7;
 
 #ifdef HSTU_TRACE
@@ -113,10 +166,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     const float* __restrict__ rabg = HAS_RAB ? p.rab + (size_t)h * rab_w : nullptr;
 
     // logical 16-byte chunk each lane fetches so that the swizzled layout comes out
-    const unsigned k_off_e = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ ld_row) * 16);        // rows 8a + 0..3
-    const unsigned k_off_o = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ (4 + ld_row)) * 16);  // rows 8a + 4..7
-    const unsigned v_off = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ (2 * ld_row)) * 16);
-    const unsigned k8_off = (unsigned)ld8_row * krow_bytes + (unsigned)((ld8_chunk ^ ld8_row) * 16);
+    const unsigned k_off = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ ld_row) * 16);  // rows 16 a + 0..3; ^ 64 ps for rows 16 a + 4 ps + 0..3
+    const unsigned v_off = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ (VSWZ * ld_row)) * 16);
+    const unsigned k8_off = (unsigned)ld8_row * krow_bytes + (unsigned)((ld8_chunk ^ (ld8_row >> 1)) * 16);  // rows 16 a + 0..7; ^ 64 for rows 16 a + 8..15
 
     const int qw0 = q0 + wave * 32;
     const int m = qw0 + l32;
@@ -141,7 +193,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 
     // Copies of one tile: 4 + 4 instructions per wave.  Rows at or past the end of the sequence
     // (last, partial tile only) re-read the sequence's last row; the mask zeroes their contribution.
-    auto issue_tile_as = [&](int it, auto buf_tag, auto whole_tag) __attribute__((always_inline)) {
+    // part 2 ps (+ 1) = the K (V) instruction of rows 16 wave + 4 ps .. + 3; part 8 = fp8 K and the bias band
+    auto issue_part = [&](int it, auto buf_tag, auto whole_tag, int part) __attribute__((always_inline)) {
       constexpr int BUF = decltype(buf_tag)::value;
       constexpr bool KNOWN_WHOLE = decltype(whole_tag)::value;  // caller guarantees k0 + BN <= n
       unsigned short* Kd = BUF ? Ks1 : Ks0;
@@ -152,36 +205,47 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       const char* vt = vgb + (size_t)k0 * row_bytes;
       const bool whole = KNOWN_WHOLE || k0 + BN <= si.n;
       const int last = si.n - 1 - k0;
-#pragma unroll
-      for (int ps = 0; ps < 4; ++ps) {
+      if (part < 8) {
+        const int ps = part >> 1;
+        const bool is_v = part & 1;
         const int r0 = 4 * (4 * wave + ps);  // first row this instruction fills
-        unsigned ko = (ps & 1) ? k_off_o : k_off_e;
+        unsigned ko = k_off ^ (unsigned)(64 * (ps & (KSWZ >> 2)));
         unsigned vo = v_off;
         const char* kr = kt + (size_t)r0 * krow_bytes;
         const char* vr = vt + (size_t)r0 * row_bytes;
         if (!whole) {
           asm volatile("" ::: "memory");  // keep the clamping arithmetic off the steady-state path
           const int row = min(r0 + ld_row, last);
-          ko = (unsigned)row * krow_bytes + (unsigned)((ld_chunk ^ ((r0 + ld_row) & 7)) * 16);
-          vo = (unsigned)row * row_bytes + (unsigned)((ld_chunk ^ (2 * ld_row)) * 16);
+          ko = (unsigned)row * krow_bytes + (unsigned)((ld_chunk ^ ((r0 + ld_row) & KSWZ)) * 16);
+          vo = (unsigned)row * row_bytes + (unsigned)((ld_chunk ^ (VSWZ * ld_row)) * 16);
           kr = kt;
           vr = vt;
         }
-        if (!FP8) __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)&Kd[r0 * HD], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const unsigned*)(vr + vo), (lds_void*)&Vd[r0 * HD], 16, 0, 0);
+#if HSTU_DL_ASM_COPY
+        if (!is_v) { if (!FP8) copy16(kr, ko, (unsigned)(size_t)&Kd[r0 * HD]); }
+        else copy16(vr, vo, (unsigned)(size_t)&Vd[r0 * HD]);
+#else
+        if (!is_v) { if (!FP8) __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)&Kd[r0 * HD], 16, 0, 0); }
+        else __builtin_amdgcn_global_load_lds((const unsigned*)(vr + vo), (lds_void*)&Vd[r0 * HD], 16, 0, 0);
+#endif
+        return;
       }
       if (FP8) {
 #pragma unroll
         for (int ps = 0; ps < 2; ++ps) {
           const int r0 = 8 * (2 * wave + ps);
-          unsigned ko = k8_off;
+          unsigned ko = k8_off ^ (unsigned)(64 * (ps & 1));
           const char* kr = kt + (size_t)r0 * krow_bytes;
           if (!whole) {
             asm volatile("" ::: "memory");
-            ko = (unsigned)min(r0 + ld8_row, last) * krow_bytes + (unsigned)((ld8_chunk ^ ld8_row) * 16);
+            ko = (unsigned)min(r0 + ld8_row, last) * krow_bytes + (unsigned)((ld8_chunk ^ (((r0 + ld8_row) >> 1) & 7)) * 16);
             kr = kt;
           }
+#if HSTU_DL_ASM_COPY
+          copy16(kr, ko, (unsigned)(size_t)((char*)Kd + r0 * 128));
+#else
           __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)((char*)Kd + r0 * 128), 16, 0, 0);
+#endif
         }
       }
       if (HAS_RAB) {
@@ -191,6 +255,10 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
         if (tid < BM + BN - 1) rabd[tid] = rabg[idx] * kLog2e;
       }
+    };
+    auto issue_tile_as = [&](int it, auto buf_tag, auto whole_tag) __attribute__((always_inline)) {
+#pragma unroll
+      for (int part = 0; part <= 8; ++part) issue_part(it, buf_tag, whole_tag, part);
     };
     auto issue_tile = [&](int it, auto buf_tag) __attribute__((always_inline)) {
       issue_tile_as(it, buf_tag, std::false_type{});
@@ -295,15 +363,113 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       const std::integral_constant<int, BUF ^ 1> other{};
       const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       auto k_frag = [&](int kvb, int kk) __attribute__((always_inline)) {
+#if HSTU_DL_SWZ64
+        return *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)(kk * 32)));
+#else
         return *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)((kk & 3) * 32)) + (kk >> 2) * 128);
+#endif
       };
       auto v_frag = [&](int db, int s2) __attribute__((always_inline)) {
+#if HSTU_DL_SWZ64
+        const char* a = vb + (vt_rd ^ (unsigned)(db * 64)) + s2 * 16 * HD * 2;
+#else
         const char* a = vb + ((db & 1) ? vt_rd_o : vt_rd_e) + db * 64 + s2 * 16 * HD * 2;
+#endif
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)a);
         const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a + 8 * HD * 2));
         const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         return __builtin_bit_cast(bf16x8, both);
       };
+#if HSTU_DL_SLOTS
+      if constexpr (!FP8 && !HAS_RAB && (FAST || HSTU_DL_SLOTS > 1)) {  // (mask and bias state leave this schedule too few registers)
+        // Hand-placed schedule, one MFMA per slot with a scheduling fence after each:
+        //   slots  0..7   S0 = K[0:32] Q^T            slots  8..15  S1 = K[32:64] Q^T
+        //   slots 16..31  O^T[db] += V^T[db, s2] P^T[s2], key step s2 = (slot - 16) / 4, db = slot & 3
+        // SiLU of the 32 scores a lane holds runs as 16 units of two scores (one packed word), one
+        // unit per slot from slot 9 on, so that every packed word is ready four slots before the
+        // MFMA that consumes it; the LDS fragment of slot s + PD is requested in slot s.
+        f32x16 sblk[2];
+        unsigned pw[2][8];
+        bf16x8 F[32];
+        // slot in which the LDS fragment of slot s is requested (-1: before slot 0).  The registers
+        // that hold scores and packed P are free when a tile starts, so every K fragment can be in
+        // flight at once; V fragments follow as K fragments are consumed.
+        // (the bodies that carry mask or clamping state have fewer registers to spare: distance 6)
+        constexpr int PDK = FAST ? HSTU_DL_PDK : 6, PDV = FAST ? HSTU_DL_PDV : 6;
+        auto frag_req = [](int s) constexpr { return s < PDK ? -1 : (s < 16 ? s - PDK : max(s - PDV, 0)); };
+        auto slot_frag = [&](int s) __attribute__((always_inline)) {
+          // stand-ins differ per 32-key block so that the two score blocks stay distinct computations
+#if HSTU_DL_ABL & 2
+          return qf[(s + (s >> 3)) & 7];
+#elif HSTU_DL_ABL & 32
+          return s < 16 ? k_frag(s >> 3, s & 7) : qf[s & 7];
+#elif HSTU_DL_ABL & 64
+          return s < 16 ? qf[(s + (s >> 3)) & 7] : v_frag((s - 16) & 3, (s - 16) >> 2);
+#else
+          return s < 16 ? k_frag(s >> 3, s & 7) : v_frag((s - 16) & 3, (s - 16) >> 2);
+#endif
+        };
+        auto silu_unit = [&](int u) __attribute__((always_inline)) {
+          constexpr bool MASKED = decltype(masked_tag)::value;
+          const int blk = u >> 3, e = u & 7;
+          float pe[2];
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int r = 2 * e + t;
+            const int jl = blk * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            float sv = sblk[blk][r];
+            if (HAS_RAB) sv += rabt[(m - q0) - jl + (BN - 1)];
+            const float ex = __builtin_amdgcn_exp2f(-sv);
+            float pv = sv * __builtin_amdgcn_rcpf(1.0f + ex);
+            if (MASKED) {
+              const int j = k0 + jl;
+              const bool kp = SEMI ? ((m == j) | ((j < idm) & ((idm - j <= si.win) | tail_row)) | (j < si.ctx_eff)) & (j < si.n)
+                                   : ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
+              pv = kp ? pv : 0.f;
+            }
+            pe[t] = pv;
+          }
+          pw[blk][e] = pack_bf16x2(pe[0], pe[1]);
+#if HSTU_DL_ABL & 1
+          pw[blk][e] = __float_as_uint(sblk[blk][2 * e]) ^ __float_as_uint(sblk[blk][2 * e + 1]);
+#endif
+        };
+#pragma unroll
+        for (int s = 0; s < 32; ++s)
+          if (frag_req(s) < 0) F[s] = slot_frag(s);
+        // the copies of the next tile go out one per slot: a burst of eight would hold this wave's
+        // MFMAs back for as long as the address unit takes to accept them
+        const bool copy_next = FAST || nxt < nkv;
+        auto issue_slot = [&](int part) __attribute__((always_inline)) {
+          if (HSTU_DL_ABL & 4) return;
+          if constexpr (FAST) issue_part(nxt, other, std::true_type{}, part);
+          else if (copy_next) issue_part(nxt, other, std::false_type{}, part);
+        };
+        if (HAS_RAB) issue_slot(8);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < 32; ++s) {
+          if (s == 8) HSTU_STAMP(1);
+          if (s == 16) HSTU_STAMP(2);
+          if (s == 24) HSTU_STAMP(3);
+#pragma unroll
+          for (int t = s + 1; t < 32; ++t)
+            if (frag_req(t) == s) F[t] = slot_frag(t);
+          if (s < 16) {
+            sblk[s >> 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], qf[s & 7], (s & 7) == 0 ? zero : sblk[s >> 3], 0, 0, 0);
+          } else {
+            const int s2 = (s - 16) >> 2, db = s & 3;
+            const u32x4 w = {pw[s2 >> 1][4 * (s2 & 1) + 0], pw[s2 >> 1][4 * (s2 & 1) + 1], pw[s2 >> 1][4 * (s2 & 1) + 2],
+                             pw[s2 >> 1][4 * (s2 & 1) + 3]};
+            acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], __builtin_bit_cast(bf16x8, w), acc[db], 0, 0, 0);
+          }
+          if (s >= HSTU_DL_C0 && s < HSTU_DL_C0 + 8 * HSTU_DL_CSTEP && (s - HSTU_DL_C0) % HSTU_DL_CSTEP == 0) issue_slot((s - HSTU_DL_C0) / HSTU_DL_CSTEP);
+          if (s >= HSTU_DL_U0 && s < HSTU_DL_U0 + 16) silu_unit(s - HSTU_DL_U0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        return;
+      }
+#endif
       f32x16 s0, s1;
       bf16x8 pb0, pb1, pb2, pb3;
       // The 32 MFMAs of the block run as eight groups of four.  The LDS fragments of group g + 1 are
@@ -443,11 +609,13 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     // (64 t + 63 <= m_lo and 64 t + 64 <= cap), inside the first contiguous run of the walk, and
     // followed by a tile that exists and is whole.  Taken in pairs (stage 0, stage 1).
     int fast_pairs = 0;
+#ifndef HSTU_TRACE
     if (!SEMI && wave_has_rows && it == 0) {
       const int run_end = has_skip ? skip_a : nkv;
       int fast_end = min(min((m_lo + 1) / BN, cap0 / BN), min(run_end - 1, si.n / BN - 1));
       fast_pairs = max(fast_end, 0) / 2;
     }
+#endif
 
     HSTU_ITEM_STAMP(1);
     if (it < nkv) {
@@ -456,11 +624,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       HSTU_ITEM_STAMP(2);
       for (int pi = 0; pi < fast_pairs; ++pi) {
         tile_body(std::false_type{}, std::integral_constant<int, 0>{}, it * BN, it + 1, std::true_type{});
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        HSTU_DL_TILE_SYNC();
         tile_body(std::false_type{}, std::integral_constant<int, 1>{}, (it + 1) * BN, it + 2, std::true_type{});
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        HSTU_DL_TILE_SYNC();
         it += 2;
       }
       // two tiles per trip so that the stage index is a compile-time constant
