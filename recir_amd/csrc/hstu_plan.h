@@ -18,7 +18,10 @@
 
 namespace recir_hstu {
 
-constexpr int PLAN_THREADS = 1024;
+#ifndef HSTU_PLAN_THREADS
+#define HSTU_PLAN_THREADS 1024
+#endif
+constexpr int PLAN_THREADS = HSTU_PLAN_THREADS;
 constexpr int PLAN_MAX_B = 1024;      // fast path: sequences ...
 constexpr int PLAN_MAX_PAIRS = 4096;  // ... (sequence, head) pairs ...
 constexpr int PLAN_MAX_TILES = 256;   // ... and query tiles per sequence that fit the LDS tables

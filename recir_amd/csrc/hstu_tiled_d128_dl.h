@@ -65,6 +65,9 @@ __device__ __forceinline__ void copy16(const void* base, unsigned lane_off, unsi
 #endif
 constexpr int KSWZ = HSTU_DL_SWZ64 ? 15 : 7;
 constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
+#ifndef HSTU_DL_PRIO
+#define HSTU_DL_PRIO 1  // wave priority while an MFMA is waiting to issue (0: leave it alone)
+#endif
 #ifndef HSTU_DL_SLOTS
 #define HSTU_DL_SLOTS 1
 #endif
@@ -455,6 +458,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 #pragma unroll
           for (int t = s + 1; t < 32; ++t)
             if (frag_req(t) == s) F[t] = slot_frag(t);
+#if HSTU_DL_PRIO
+          __builtin_amdgcn_s_setprio(HSTU_DL_PRIO);
+#endif
           if (s < 16) {
             sblk[s >> 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], qf[s & 7], (s & 7) == 0 ? zero : sblk[s >> 3], 0, 0, 0);
           } else {
@@ -463,6 +469,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
                              pw[s2 >> 1][4 * (s2 & 1) + 3]};
             acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], __builtin_bit_cast(bf16x8, w), acc[db], 0, 0, 0);
           }
+#if HSTU_DL_PRIO
+          __builtin_amdgcn_s_setprio(0);
+#endif
           if (s >= HSTU_DL_C0 && s < HSTU_DL_C0 + 8 * HSTU_DL_CSTEP && (s - HSTU_DL_C0) % HSTU_DL_CSTEP == 0) issue_slot((s - HSTU_DL_C0) / HSTU_DL_CSTEP);
           if (s >= HSTU_DL_U0 && s < HSTU_DL_U0 + 16) silu_unit(s - HSTU_DL_U0);
           __builtin_amdgcn_sched_barrier(0);
