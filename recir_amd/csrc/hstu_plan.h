@@ -116,23 +116,24 @@ __global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int b
     above[x][t] = tiles_above(x, t);
   }
   __syncthreads();
-  // one thread per (rank, tile); the heads of a sequence share everything but the list
-  for (int i = tid; i < B * tmax; i += PLAN_THREADS) {
-    const int r = i / tmax, t = i - r * tmax;
+  // one thread per (rank, tile, head)
+  const int per_rank = tmax * H;
+  for (int i = tid; i < B * per_rank; i += PLAN_THREADS) {
+    const int r = i / per_rank, rem = i - r * per_rank;
+    const int t = rem / H, h = rem - t * H;
     const int my_nt = nt_by_rank[r];
     if (t >= my_nt) continue;
     const int b = seq_of_rank[r];
     SeqInfo si;
     si.s = seq_s[b]; si.n = seq_n[b]; si.cap = seq_cap[b]; si.ctx_eff = seq_ctx[b];
-    for (int h = 0; h < H; ++h) {
-      const int pr = r * H + h;
-      const int x = snake_xcd(pr), k = snake_slot(pr);
-      int pos = t < ttab ? above[x][t] : tiles_above(x, t);
-      for (int k2 = 0; k2 < k; ++k2) pos += xnt[x][k2] > t;
-      WorkItem w;
-      fill_item(w, si, bm, t, my_nt, mode, h, b);
-      p.ws_items[(size_t)x * p.items_cap + pos] = w;
-    }
+    const int pr = r * H + h;
+    const int x = snake_xcd(pr), k = snake_slot(pr);
+    // pairs enter a list in rank order, so the k pairs ahead of this one in its list have at least
+    // as many tiles: each of them owns a tile t, and all of those come first
+    const int pos = (t < ttab ? above[x][t] : tiles_above(x, t)) + k;
+    WorkItem w;
+    fill_item(w, si, bm, t, my_nt, mode, h, b);
+    p.ws_items[(size_t)x * p.items_cap + pos] = w;
   }
   if (tid < NUM_XCD) {
     int total = 0;
