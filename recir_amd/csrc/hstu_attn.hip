@@ -467,13 +467,15 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     bq.f.items_cap = bk.f.items_cap = (int)items;
     bq.f.grid_slots = bk.f.grid_slots = (int)slots;
     if (!(flags & RECIR_HSTU_FLAG_REUSE_PLAN)) {
-      for (int rev = 0; rev < 2; ++rev) {
-        const Params& pp = rev ? bk.f : bq.f;
-        if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS)
-          hipLaunchKernelGGL(hstu_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, pp, BWD_BM, rev ? PLAN_REVERSE : PLAN_SHIFT_ODD);
-        else
+      if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS) {
+        hipLaunchKernelGGL(hstu_plan_pair_kernel, dim3(2), dim3(PLAN_THREADS), 0, stream, bq.f, PLAN_SHIFT_ODD, bk.f, PLAN_REVERSE, BWD_BM);
+        if (int rc = launch_status("hstu_plan_pair_kernel")) return rc;
+      } else {
+        for (int rev = 0; rev < 2; ++rev) {
+          const Params& pp = rev ? bk.f : bq.f;
           hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, pp, BWD_BM, rev ? PLAN_REVERSE : PLAN_SHIFT_ODD);
-        if (int rc = launch_status("hstu_plan_kernel")) return rc;
+          if (int rc = launch_status("hstu_plan_kernel")) return rc;
+        }
       }
     }
     const dim3 grid((unsigned)(slots * NUM_XCD));

@@ -61,7 +61,7 @@ __device__ __forceinline__ void fill_item(WorkItem& w, const SeqInfo& si, int bm
 }
 
 // Fast path: everything in LDS, one block.
-__global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int bm, int mode) {
+__device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode) {
   __shared__ int nt[PLAN_MAX_B];          // query tiles of sequence b
   __shared__ int seq_of_rank[PLAN_MAX_B];
   __shared__ int nt_by_rank[PLAN_MAX_B];
@@ -140,6 +140,17 @@ __global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int b
     for (int k = 0; k < per_list; ++k) total += xnt[tid][k];
     p.ws_counts[tid] = total;
   }
+}
+
+__global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_kernel(Params p, int bm, int mode) {
+  plan_one_block(p, bm, mode);
+}
+
+// Two lists over the same sequences in one launch (the backward's query-tile and key-tile lists):
+// block 0 builds the first, block 1 the second.
+__global__ __launch_bounds__(PLAN_THREADS) void hstu_plan_pair_kernel(Params pa, int mode_a, Params pb, int mode_b, int bm) {
+  if (blockIdx.x == 0) plan_one_block(pa, bm, mode_a);
+  else plan_one_block(pb, bm, mode_b);
 }
 
 // General path for batches beyond the LDS tables: no ranking, pairs dealt in input order, list
