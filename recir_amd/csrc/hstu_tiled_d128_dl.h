@@ -65,6 +65,9 @@ __device__ __forceinline__ void copy16(const void* base, unsigned lane_off, unsi
 #endif
 constexpr int KSWZ = HSTU_DL_SWZ64 ? 15 : 7;
 constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
+#ifndef HSTU_DL_PVORDER
+#define HSTU_DL_PVORDER 0
+#endif
 #ifndef HSTU_DL_PRIO
 #define HSTU_DL_PRIO 1  // wave priority while an MFMA is waiting to issue (0: leave it alone)
 #endif
@@ -400,6 +403,14 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         // (the bodies that carry mask or clamping state have fewer registers to spare: distance 6)
         constexpr int PDK = FAST ? HSTU_DL_PDK : 6, PDV = FAST ? HSTU_DL_PDV : 6;
         auto frag_req = [](int s) constexpr { return s < PDK ? -1 : (s < 16 ? s - PDK : max(s - PDV, 0)); };
+        // slot 16 + j of the second contraction: accumulator db, key step s2
+#if HSTU_DL_PVORDER == 1   // two consecutive MFMAs per accumulator
+        auto pv_db = [](int s) constexpr { return ((s - 16) >> 1) & 3; };
+        auto pv_s2 = [](int s) constexpr { return 2 * ((s - 16) >> 3) + ((s - 16) & 1); };
+#else                      // the four accumulators in turn
+        auto pv_db = [](int s) constexpr { return (s - 16) & 3; };
+        auto pv_s2 = [](int s) constexpr { return (s - 16) >> 2; };
+#endif
         auto slot_frag = [&](int s) __attribute__((always_inline)) {
           // stand-ins differ per 32-key block so that the two score blocks stay distinct computations
 #if HSTU_DL_ABL & 2
@@ -409,7 +420,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 #elif HSTU_DL_ABL & 64
           return s < 16 ? qf[(s + (s >> 3)) & 7] : v_frag((s - 16) & 3, (s - 16) >> 2);
 #else
-          return s < 16 ? k_frag(s >> 3, s & 7) : v_frag((s - 16) & 3, (s - 16) >> 2);
+          return s < 16 ? k_frag(s >> 3, s & 7) : v_frag(pv_db(s), pv_s2(s));
 #endif
         };
         auto silu_unit = [&](int u) __attribute__((always_inline)) {
@@ -464,7 +475,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           if (s < 16) {
             sblk[s >> 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], qf[s & 7], (s & 7) == 0 ? zero : sblk[s >> 3], 0, 0, 0);
           } else {
-            const int s2 = (s - 16) >> 2, db = s & 3;
+            const int s2 = pv_s2(s), db = pv_db(s);
             const u32x4 w = {pw[s2 >> 1][4 * (s2 & 1) + 0], pw[s2 >> 1][4 * (s2 & 1) + 1], pw[s2 >> 1][4 * (s2 & 1) + 2],
                              pw[s2 >> 1][4 * (s2 & 1) + 3]};
             acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], __builtin_bit_cast(bf16x8, w), acc[db], 0, 0, 0);
