@@ -417,6 +417,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           return qf[(s + (s >> 3)) & 7];
 #elif HSTU_DL_ABL & 32
           return s < 16 ? k_frag(s >> 3, s & 7) : qf[s & 7];
+#elif HSTU_DL_ABL & 256  // timing study: the first K fragments of a tile do not come from LDS
+          return s < (HSTU_DL_ABL >> 12) ? qf[(s + 1) & 7] : (s < 16 ? k_frag(s >> 3, s & 7) : v_frag(pv_db(s), pv_s2(s)));
 #elif HSTU_DL_ABL & 64
           return s < 16 ? qf[(s + (s >> 3)) & 7] : v_frag((s - 16) & 3, (s - 16) >> 2);
 #else
