@@ -13,6 +13,9 @@ from .ops import (  # noqa: F401
     jagged_hstu_attention_fp8,
     quantize_e4m3_per_head,
     register_swaps,
+    hstu_attention_matcher,
+    attention_via_fp8,
+    fp8_attention_region,
     KERNEL_AUTO,
     KERNEL_GENERIC,
     KERNEL_TILED,
@@ -39,4 +42,7 @@ __all__ = [
     "jagged_hstu_attention_fp8",
     "quantize_e4m3_per_head",
     "register_swaps",
+    "hstu_attention_matcher",
+    "attention_via_fp8",
+    "fp8_attention_region",
 ]

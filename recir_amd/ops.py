@@ -435,6 +435,73 @@ def jagged_hstu_attention_fp8(q, k, v, seq_offsets, num_targets=None, *, max_seq
     return out
 
 
+def hstu_attention_matcher(node) -> bool:
+    """``OpMatcher`` of RecIR's training-to-inference swap
+    (recir/region_transforms/inference_swap.py:73-77): true for a graph node that calls the HSTU
+    attention operator, under this package's name or the reference's."""
+    if node.op != "call_function":
+        return False
+    targets = [hstu_jagged_attention_fwd, hstu_jagged_attention_fwd.default]
+    try:
+        src = torch.ops.hammer.triton_ragged_attention_fwd
+        targets += [src, src.default]
+    except (AttributeError, RuntimeError):
+        pass
+    return any(node.target is t for t in targets)
+
+
+def attention_via_fp8(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
+                      max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads=0, rab=None):
+    """The attention operator's positional signature, computed with q and k quantised per head to
+    fp8 e4m3 (v, the accumulation and the output stay as they are).  Module level on purpose: it
+    becomes a ``call_function`` target of the inference graph, and a saved GraphModule names its
+    targets by qualified name (recir/region_transforms/inference_swap.py:89-104)."""
+    if num_softmax_heads != 0:
+        raise ValueError("softmax attention heads are unsupported")
+    if invalid_attn_mask_type != "lower_triangular":
+        raise ValueError("only the causal mask ('lower_triangular') is supported")
+    q8, qs = quantize_e4m3_per_head(q)
+    k8, ks = quantize_e4m3_per_head(k)
+    return torch.ops.recir.hstu_jagged_attention_fp8_fwd(
+        int(N), float(alpha), q8, k8, v, qs, ks, seq_offsets, num_targets, attn_scale,
+        int(contextual_seq_len), rab, int(max_attn_len), int(full_attn_size))
+
+
+class Fp8AttentionRegion:
+    """Callable the factory below returns.  It is spliced into the host graph as a ``call_function``
+    target (recir/region_transforms/core.py:358-362), which needs a ``__name__``; it holds a copy of
+    the region in which every attention node runs ``attention_via_fp8``.  It pickles by value (the
+    class and the rewritten region are importable); a host graph that names it as a target can be
+    run, not re-loaded from a file in another process."""
+
+    def __init__(self, gm):
+        self.gm = gm
+        self.__name__ = "fp8_attention_region"
+        self.__qualname__ = "fp8_attention_region"
+
+    def __call__(self, *inputs):
+        return self.gm(*inputs)
+
+
+def fp8_attention_region(region_gm):
+    """``RegionFactory`` of the same swap: given the sub-GraphModule extracted around the matched
+    node(s), returns the callable that replaces it.  It takes the region's external inputs
+    positionally and returns the region's outputs, whatever else (getitem, casts) the region holds."""
+    import copy
+
+    gm = copy.deepcopy(region_gm)
+    hits = 0
+    for node in gm.graph.nodes:
+        if hstu_attention_matcher(node):
+            node.target = attention_via_fp8
+            hits += 1
+    if hits == 0:
+        raise ValueError("the region holds no HSTU attention node")
+    gm.graph.lint()
+    gm.recompile()
+    return Fp8AttentionRegion(gm)
+
+
 def register_swaps(registry) -> int:
     """Fill a RecIR ``OpSwapRegistry`` (recir/lowering/op_swap.py:16-75) with every source operator
     present in this process that the HIP operator can replace argument-for-argument.  Returns the

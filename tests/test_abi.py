@@ -236,3 +236,64 @@ def test_register_swaps_fills_a_registry():
     reg = Registry()
     n = recir_amd.register_swaps(reg)
     assert n == len(reg.map)  # 0 unless the reference's hammer op is loaded in this process
+
+
+def _attention_graph():
+    """A traced graph with one attention node, a getitem and a cast after it, plus the region a
+    single-node match extracts from it (placeholders for the node's tensor inputs, constants inside),
+    as recir/region_transforms/core.py builds it for inference_swap.py:293-307."""
+    import torch.fx as fx
+
+    import recir_amd
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    op = recir_amd.hstu_jagged_attention_fwd.default
+
+    def f(q, k, v, off, nt):
+        out, _aux = op(16, 0.25, q, k, v, off, "lower_triangular", nt, None, 0, 0, 0)
+        return out.float() * 2.0
+
+    q, k, v = (torch.empty(12, 2, 128, dtype=torch.bfloat16) for _ in range(3))
+    gm = make_fx(f, tracing_mode="fake")(q, k, v, torch.empty(3, dtype=torch.int64), torch.empty(2, dtype=torch.int64))
+    matched = [n for n in gm.graph.nodes if recir_amd.hstu_attention_matcher(n)]
+    assert len(matched) == 1
+    node = matched[0]
+    region = fx.Graph()
+    env = {}
+    for a in node.args:
+        if isinstance(a, fx.Node):
+            env[a] = region.placeholder(a.name)
+    new = region.node_copy(node, lambda n: env[n])
+    region.output(new)
+    return gm, node, fx.GraphModule(torch.nn.Module(), region)
+
+
+def test_fp8_region_factory_rewrites_the_matched_region():
+    """Matcher and factory of the training-to-inference swap: the factory's callable keeps the
+    region's inputs and constants, runs the fp8 entry point in place of the attention node, can be
+    pickled (its target is a module-level function), and has no CPU path."""
+    import pickle
+
+    import recir_amd
+
+    gm, node, region_gm = _attention_graph()
+    assert not any(recir_amd.hstu_attention_matcher(n) for n in gm.graph.nodes if n is not node)
+    run = recir_amd.fp8_attention_region(region_gm)
+    assert run.__name__ == "fp8_attention_region"  # usable as a call_function target
+    calls = [n for n in run.gm.graph.nodes if n.op == "call_function"]
+    assert len(calls) == 1 and calls[0].target is recir_amd.attention_via_fp8
+    assert calls[0].args[0] == 16 and calls[0].args[1] == 0.25 and calls[0].args[6] == "lower_triangular"
+    assert [n.op for n in run.gm.graph.nodes].count("placeholder") == 5
+    # the region handed in is left as it was
+    assert any(recir_amd.hstu_attention_matcher(n) for n in region_gm.graph.nodes)
+    assert b"attention_via_fp8" in pickle.dumps(run)
+    q = torch.zeros(12, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises((NotImplementedError, RuntimeError), match="no CPU implementation"):
+        run(q, q, q, torch.tensor([0, 5, 12]), torch.tensor([1, 2]))
+    with pytest.raises(ValueError, match="no HSTU attention node"):
+        import torch.fx as fx
+
+        g = fx.Graph()
+        x = g.placeholder("x")
+        g.output(x)
+        recir_amd.fp8_attention_region(fx.GraphModule(torch.nn.Module(), g))

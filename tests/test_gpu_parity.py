@@ -368,6 +368,51 @@ def test_config5_fp8_matches_oracle(oracle):
     assert_same_zero_structure(out, run_oracle(oracle, wl), int(wl.seq_offsets[-1]))
 
 
+def test_fp8_region_swap_in_a_traced_graph(oracle):
+    """The training-to-inference hook end to end: trace a function that calls the bf16 operator,
+    cut out the matched node as a region, let the factory build its replacement, splice it back and
+    run both graphs.  The swapped graph must equal the fp8 entry point bit for bit and stay within
+    the fp8 tolerance of the fp32 oracle."""
+    import torch.fx as fx
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    import recir_amd
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([200, 70, 0, 131], [16, 70, 0, 3], 2, 128, 128, max_seq_len=256, alpha=1.0 / 128,
+                     dtype="bf16", seed=31, tail_rows=3)
+    q, k, v, off, nt = to_device(wl)
+    op = recir_amd.hstu_jagged_attention_fwd.default
+
+    def f(q, k, v, off, nt):
+        out, _aux = op(wl.max_seq_len, wl.alpha, q, k, v, off, "lower_triangular", nt, None, 0, 0, 0)
+        return out.float() * 2.0
+
+    gm = make_fx(f, tracing_mode="fake")(q, k, v, off, nt)
+    node = next(n for n in gm.graph.nodes if recir_amd.hstu_attention_matcher(n))
+    region = fx.Graph()
+    env = {a: region.placeholder(a.name) for a in node.args if isinstance(a, fx.Node)}
+    region.output(region.node_copy(node, lambda n: env[n]))
+    run = recir_amd.fp8_attention_region(fx.GraphModule(torch.nn.Module(), region))
+    ref_bf16 = gm(q, k, v, off, nt)
+    assert _lib.last_kernel() == "tiled_d128_bf16"
+    with gm.graph.inserting_before(node):
+        repl = gm.graph.call_function(run, tuple(a for a in node.args if isinstance(a, fx.Node)))
+    node.replace_all_uses_with(repl)
+    gm.graph.erase_node(node)
+    gm.recompile()
+    got = gm(q, k, v, off, nt)
+    torch.cuda.synchronize()
+    assert _lib.last_kernel() == "tiled_d128_fp8qk"
+    direct = recir_amd.jagged_hstu_attention_fp8(q, k, v, off, nt, max_seq_len=wl.max_seq_len, alpha=wl.alpha)
+    assert torch.equal(got, direct.float() * 2.0)
+    want = 2.0 * run_oracle(oracle, wl)
+    st = error_stats(got, want)
+    assert st["max_abs"] <= 2 * FP8_MAX_ABS and st["rel_fro"] <= 5e-2, st
+    assert error_stats(ref_bf16, want)["rel_fro"] <= 2e-2
+
+
 @pytest.mark.parametrize("config", [2, 3, 4, 5])
 def test_w64_kernel_full_size(oracle, config):
     """The 64-rows-per-wave kernel on the full-size configurations, against the oracle."""
