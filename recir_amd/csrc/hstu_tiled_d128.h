@@ -34,8 +34,8 @@ __device__ __forceinline__ int vt_swz(int d) { return (d ^ (d >> 3)) & 7; }
 
 // One thread's share of a staged K/V tile (kept as named members, not arrays, so that it lives in
 // registers whatever the control flow around it looks like).
-#ifdef HSTU_TRACE
-// Debug build only: per-wave phase timestamps of one workgroup (see _work tooling).
+#if defined(HSTU_TRACE) && !defined(HSTU_TRACE_ITEMS_ONLY)
+// Debug build only: per-wave phase timestamps of one workgroup.
 __device__ unsigned long long g_trace[4 * 64 * 8];
 __device__ int g_trace_block = 0;
 #define HSTU_STAMP(slot)                                                                  \
@@ -46,6 +46,10 @@ __device__ int g_trace_block = 0;
     __builtin_amdgcn_sched_barrier(0);                                                    \
   } while (0)
 #else
+#ifdef HSTU_TRACE
+__device__ unsigned long long g_trace[4 * 64 * 8];
+__device__ int g_trace_block = 0;
+#endif
 #define HSTU_STAMP(slot) do { } while (0)
 #endif
 #ifdef HSTU_TRACE

@@ -65,9 +65,6 @@ __device__ __forceinline__ void copy16(const void* base, unsigned lane_off, unsi
 #endif
 constexpr int KSWZ = HSTU_DL_SWZ64 ? 15 : 7;
 constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
-#ifndef HSTU_DL_PVORDER
-#define HSTU_DL_PVORDER 0
-#endif
 #ifndef HSTU_DL_PRIO
 #define HSTU_DL_PRIO 1  // wave priority while an MFMA is waiting to issue (0: leave it alone)
 #endif
@@ -404,21 +401,14 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         constexpr int PDK = FAST ? HSTU_DL_PDK : 6, PDV = FAST ? HSTU_DL_PDV : 6;
         auto frag_req = [](int s) constexpr { return s < PDK ? -1 : (s < 16 ? s - PDK : max(s - PDV, 0)); };
         // slot 16 + j of the second contraction: accumulator db, key step s2
-#if HSTU_DL_PVORDER == 1   // two consecutive MFMAs per accumulator
-        auto pv_db = [](int s) constexpr { return ((s - 16) >> 1) & 3; };
-        auto pv_s2 = [](int s) constexpr { return 2 * ((s - 16) >> 3) + ((s - 16) & 1); };
-#else                      // the four accumulators in turn
         auto pv_db = [](int s) constexpr { return (s - 16) & 3; };
         auto pv_s2 = [](int s) constexpr { return (s - 16) >> 2; };
-#endif
         auto slot_frag = [&](int s) __attribute__((always_inline)) {
           // stand-ins differ per 32-key block so that the two score blocks stay distinct computations
 #if HSTU_DL_ABL & 2
           return qf[(s + (s >> 3)) & 7];
 #elif HSTU_DL_ABL & 32
           return s < 16 ? k_frag(s >> 3, s & 7) : qf[s & 7];
-#elif HSTU_DL_ABL & 256  // timing study: the first K fragments of a tile do not come from LDS
-          return s < (HSTU_DL_ABL >> 12) ? qf[(s + 1) & 7] : (s < 16 ? k_frag(s >> 3, s & 7) : v_frag(pv_db(s), pv_s2(s)));
 #elif HSTU_DL_ABL & 64
           return s < 16 ? qf[(s + (s >> 3)) & 7] : v_frag((s - 16) & 3, (s - 16) >> 2);
 #else
@@ -631,7 +621,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     // (64 t + 63 <= m_lo and 64 t + 64 <= cap), inside the first contiguous run of the walk, and
     // followed by a tile that exists and is whole.  Taken in pairs (stage 0, stage 1).
     int fast_pairs = 0;
-#ifndef HSTU_TRACE
+#if !defined(HSTU_TRACE) || defined(HSTU_TRACE_ITEMS_ONLY)
     if (!SEMI && wave_has_rows && it == 0) {
       const int run_end = has_skip ? skip_a : nkv;
       int fast_end = min(min((m_lo + 1) / BN, cap0 / BN), min(run_end - 1, si.n / BN - 1));
@@ -640,10 +630,16 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 #endif
 
     HSTU_ITEM_STAMP(1);
+#ifdef HSTU_TRACE
+    long long trace_c2 = clock64();
+#endif
     if (it < nkv) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       HSTU_ITEM_STAMP(2);
+#ifdef HSTU_TRACE
+      trace_c2 = clock64();
+#endif
       for (int pi = 0; pi < fast_pairs; ++pi) {
         tile_body(std::false_type{}, std::integral_constant<int, 0>{}, it * BN, it + 1, std::true_type{});
         HSTU_DL_TILE_SYNC();
@@ -685,6 +681,11 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     }
 
     HSTU_ITEM_STAMP(3);
+#ifdef HSTU_TRACE
+    // shader cycles of the tile loop (with the wall-clock stamps 2 and 3: the clock it ran at)
+    if (lane == 0 && blockIdx.x < 4096 && slot == (int)(blockIdx.x / NUM_XCD) && it0 >= 0)
+      g_item_trace[(blockIdx.x * 4 + wave) * 8 + 1] = (unsigned long long)(clock64() - trace_c2);
+#endif
     // ---- epilogue: O^T accumulators -> out[s + m, h, :] ----
     if (m < q_end) {
       float oscale = 1.0f / (float)p.N;
