@@ -577,12 +577,30 @@ int check_rows(int64_t row_bytes, int32_t B) {
   return 0;
 }
 
-#define RECIR_DISPATCH_CHUNK(cb, KERNEL, grid, stream, params, cpr)                               \
+// lanes per row group (log2): the smallest power of two that covers the chunks of a row, at most 64
+static int group_log2(long long cpr) {
+  int lg = 0;
+  while (lg < 6 && (1ll << lg) < cpr) ++lg;
+  return lg;
+}
+// blocks of four waves, one block of rows (JAG_ITERS iterations of 64 >> lg rows, at most 64 rows) per wave
+static unsigned gather_grid(long long rows, int lg) {
+  const long long rpi = 64 >> lg;
+  const long long per_wave = rpi * JAG_ITERS < 64 ? rpi * JAG_ITERS : 64;
+  long long blocks = ((rows + per_wave - 1) / per_wave + 3) / 4;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 65536) blocks = 65536;
+  return (unsigned)blocks;
+}
+
+#define RECIR_DISPATCH_CHUNK(cb, KERNEL, rows, stream, params, cpr)                                \
   do {                                                                                            \
-    if (cb == 16) hipLaunchKernelGGL((KERNEL<uint4>), dim3(grid), dim3(256), 0, stream, params, cpr);          \
-    else if (cb == 4) hipLaunchKernelGGL((KERNEL<unsigned>), dim3(grid), dim3(256), 0, stream, params, cpr);   \
-    else if (cb == 2) hipLaunchKernelGGL((KERNEL<unsigned short>), dim3(grid), dim3(256), 0, stream, params, cpr); \
-    else hipLaunchKernelGGL((KERNEL<unsigned char>), dim3(grid), dim3(256), 0, stream, params, cpr);           \
+    const int lg_ = group_log2(cpr);                                                              \
+    const unsigned grid_ = gather_grid(rows, lg_);                                                \
+    if (cb == 16) hipLaunchKernelGGL((KERNEL<uint4>), dim3(grid_), dim3(256), 0, stream, params, cpr, lg_);          \
+    else if (cb == 4) hipLaunchKernelGGL((KERNEL<unsigned>), dim3(grid_), dim3(256), 0, stream, params, cpr, lg_);   \
+    else if (cb == 2) hipLaunchKernelGGL((KERNEL<unsigned short>), dim3(grid_), dim3(256), 0, stream, params, cpr, lg_); \
+    else hipLaunchKernelGGL((KERNEL<unsigned char>), dim3(grid_), dim3(256), 0, stream, params, cpr, lg_);           \
   } while (0)
 
 }  // namespace
@@ -605,7 +623,7 @@ int recir_jagged_to_padded_dense(const void* values, void* out, const void* offs
   PadParams p{(const char*)values, (char*)out, {offsets, 0, (int)(flags & RECIR_HSTU_FLAG_OFFSETS_I32)},
               total_rows, B, max_len, pad_bits, elem_bytes};
   const long long cpr = row_bytes / cb;
-  RECIR_DISPATCH_CHUNK(cb, jagged_to_padded_dense_kernel, row_grid((long long)B * max_len * cpr), (hipStream_t)hip_stream, p, cpr);
+  RECIR_DISPATCH_CHUNK(cb, jagged_to_padded_dense_kernel, (long long)B * max_len, (hipStream_t)hip_stream, p, cpr);
   return launch_status("jagged_to_padded_dense_kernel");
 }
 
@@ -626,7 +644,7 @@ int recir_dense_to_jagged(const void* dense, void* out, const void* offsets, int
   const int cb = chunk_bytes(row_bytes, {dense, out});
   UnpadParams p{(const char*)dense, (char*)out, {offsets, 0, (int)(flags & RECIR_HSTU_FLAG_OFFSETS_I32)}, total_L, B, N};
   const long long cpr = row_bytes / cb;
-  RECIR_DISPATCH_CHUNK(cb, dense_to_jagged_kernel, row_grid(total_L * cpr), (hipStream_t)hip_stream, p, cpr);
+  RECIR_DISPATCH_CHUNK(cb, dense_to_jagged_kernel, total_L, (hipStream_t)hip_stream, p, cpr);
   return launch_status("dense_to_jagged_kernel");
 }
 
@@ -653,7 +671,7 @@ int recir_concat_2d_jagged(const void* values_a, const void* values_b, void* out
   ConcatParams p{(const char*)values_a, (const char*)values_b, (char*)out, {offsets_a, dense_len_a, i32},
                  {offsets_b, dense_len_b, i32}, rows_a, rows_b, out_rows, B, is_replace, n_prefix_from_right};
   const long long cpr = row_bytes / cb;
-  RECIR_DISPATCH_CHUNK(cb, concat_2d_jagged_kernel, row_grid(out_rows * cpr), (hipStream_t)hip_stream, p, cpr);
+  RECIR_DISPATCH_CHUNK(cb, concat_2d_jagged_kernel, out_rows, (hipStream_t)hip_stream, p, cpr);
   return launch_status("concat_2d_jagged_kernel");
 }
 
@@ -672,7 +690,7 @@ int recir_split_2d_jagged(const void* values, void* out_a, void* out_b, const vo
   SplitParams p{(const char*)values, (char*)out_a, (char*)out_b, {offsets_a, dense_len_a, i32},
                 {offsets_b, dense_len_b, i32}, rows_a, rows_b, rows_a + rows_b, B, n_prefix_to_right};
   const long long cpr = row_bytes / cb;
-  RECIR_DISPATCH_CHUNK(cb, split_2d_jagged_kernel, row_grid((rows_a + rows_b) * cpr), (hipStream_t)hip_stream, p, cpr);
+  RECIR_DISPATCH_CHUNK(cb, split_2d_jagged_kernel, rows_a + rows_b, (hipStream_t)hip_stream, p, cpr);
   return launch_status("split_2d_jagged_kernel");
 }
 
