@@ -194,6 +194,20 @@ def bench_jagged(args, wl, dev):
         "split_2d_jagged": (lambda: recir_amd.split_2d_jagged(cat, a_off, b_off, a.shape[0], b.shape[0]),
                             2 * cat.shape[0] * row),
     }
+    # position / timestamp embedding add on [T, 512] bf16 rows: rows read and written plus the four
+    # index lists (the table rows stay in cache)
+    D = 512
+    g = torch.Generator().manual_seed(0)
+    seq = torch.randn(wl.T, D, generator=g).to(torch.bfloat16).to(dev)
+    pos_tab = torch.randn(wl.max_seq_len + 64, D, generator=g).to(torch.bfloat16).to(dev)
+    ts_tab = torch.randn(2049, D, generator=g).to(torch.bfloat16).to(dev)
+    stamps = torch.sort(torch.randint(0, 40_000_000, (wl.B, wl.max_seq_len), generator=g), dim=1).values.to(dev)
+    lengths = off[1:] - off[:-1]
+    ntg = wl.num_targets.to(dev)
+    ops_["add_ts_pos_emb_fwd"] = (
+        lambda: recir_amd.add_ts_pos_emb_fwd(seq, off, pos_tab, ts_tab, stamps, lengths, ntg, wl.max_seq_len, 0,
+                                             False, "sqrt"),
+        2 * wl.T * D * 2 + 4 * wl.T * 4)
     res = {}
     for name, (fn, nbytes) in ops_.items():
         for _ in range(args.warmup):
@@ -207,7 +221,7 @@ def bench_jagged(args, wl, dev):
         ms = e0.elapsed_time(e1) / args.steps
         res[name] = {"ms_per_call": ms, "algorithmic_bytes": nbytes, "achieved_GBs": nbytes / (ms * 1e-3) / 1e9,
                      "frac_of_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
-    print(json.dumps({"metric": "jagged row-gather operators, algorithmic GB/s (includes allocation of the output)",
+    print(json.dumps({"metric": "jagged row-gather operators and embedding add, algorithmic GB/s (includes allocation of the outputs)",
                       "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": "u8",
                       "data": "synthetic", "config": {"workload": describe(wl, args.config), "row_bytes": row},
                       "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBS, "unit": "GB/s"}, "ops": res}))

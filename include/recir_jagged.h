@@ -86,8 +86,9 @@ int recir_add_timestamp_position_embeddings(
     int32_t time_bucket_log, int32_t seq_dtype, int32_t table_dtype, int32_t timestamps_float,
     uint32_t flags, void* workspace, size_t workspace_bytes, void* hip_stream);
 
-/* Scratch size the call above needs for L tokens. */
-size_t recir_add_timestamp_position_embeddings_workspace_bytes(int64_t L);
+/* Scratch size the call above needs for L tokens, a position table of P rows and a timestamp table
+ * of TS rows (256-byte aligned scratch). */
+size_t recir_add_timestamp_position_embeddings_workspace_bytes(int64_t L, int32_t P, int32_t TS);
 
 #ifdef __cplusplus
 }

@@ -78,7 +78,7 @@ def load() -> ctypes.CDLL:
     L.recir_concat_2d_jagged.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i64, i64, i64, i32, i32, u32, vp]
     L.recir_split_2d_jagged.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i64, i64, i64, i32, u32, vp]
     L.recir_add_timestamp_position_embeddings.argtypes = [vp] * 12 + [i64] + [i32] * 11 + [u32, vp, sz, vp]
-    L.recir_add_timestamp_position_embeddings_workspace_bytes.argtypes = [i64]
+    L.recir_add_timestamp_position_embeddings_workspace_bytes.argtypes = [i64, i32, i32]
     for name in JAGGED_EXPORTS:
         getattr(L, name).restype = ctypes.c_int
     L.recir_add_timestamp_position_embeddings_workspace_bytes.restype = sz

@@ -32,6 +32,7 @@
 #include "hstu_bwd_d128.h"
 #include "jagged_rows.h"
 #include "ts_pos_embeddings.h"
+#include "counting_sort.h"
 
 #include <rocprim/rocprim.hpp>
 
@@ -708,10 +709,34 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 extern "C" {
 
-size_t recir_add_timestamp_position_embeddings_workspace_bytes(int64_t L) {
-  if (L < 0) return 0;
-  // unsorted position rows, unsorted buckets, identity permutation, sort scratch
-  return 3 * align256((size_t)L * 4) + align256(sort_temp_bytes(L));
+// chunks (one per wave) and tokens per chunk of the counting sort
+static void csort_chunks(int64_t L, int& NW, int& CW) {
+#ifndef CSORT_CHUNK
+#define CSORT_CHUNK 512
+#endif
+  long long nw = (L + CSORT_CHUNK - 1) / CSORT_CHUNK;
+  nw = nw < 1 ? 1 : (nw > recir_jagged::CSORT_MAX_CHUNKS ? recir_jagged::CSORT_MAX_CHUNKS : nw);
+  long long cw = ((L + nw - 1) / nw + 63) / 64 * 64;
+  if (cw < 64) cw = 64;
+  CW = (int)cw;
+  NW = (int)((L + cw - 1) / cw);
+  if (NW < 1) NW = 1;
+}
+static int bucket_keys(int32_t TS) { return TS < 2049 ? TS : 2049; }
+
+size_t recir_add_timestamp_position_embeddings_workspace_bytes(int64_t L, int32_t P, int32_t TS) {
+  if (L < 0 || P < 0 || TS < 0) return 0;
+  // unsorted position rows, unsorted buckets, identity permutation, sort scratch (the larger of the
+  // counting sort's tables and the general sort's)
+  size_t scratch = sort_temp_bytes(L);
+  if (P <= recir_jagged::CSORT_MAX_K) {
+    int NW, CW;
+    csort_chunks(L, NW, CW);
+    const size_t keys = (size_t)P + (size_t)bucket_keys(TS);
+    const size_t tables = align256((size_t)NW * keys * 4) + align256(keys * 4) + 512;
+    if (tables > scratch) scratch = tables;
+  }
+  return 3 * align256((size_t)L * 4) + align256(scratch);
 }
 
 int recir_add_timestamp_position_embeddings(
@@ -737,7 +762,7 @@ int recir_add_timestamp_position_embeddings(
   if (!seq || !out || !seq_offsets || !pos_emb || !ts_emb || !timestamps || !seq_lengths || !sorted_pos || !pos_order ||
       !sorted_ts || !ts_order)
     return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "null pointer");
-  const size_t need = recir_add_timestamp_position_embeddings_workspace_bytes(L);
+  const size_t need = recir_add_timestamp_position_embeddings_workspace_bytes(L, P, TS);
   if (!workspace || workspace_bytes < need || ((size_t)workspace & 255))
     return fail(RECIR_HSTU_ERR_WORKSPACE, "workspace of %zu bytes (256-byte aligned) required, got %zu at %p", need,
                 workspace_bytes, workspace);
@@ -751,10 +776,59 @@ int recir_add_timestamp_position_embeddings(
   p.interleave = interleave_targets != 0; p.use_log = time_bucket_log != 0;
   p.seq_bf16 = seq_dtype == RECIR_HSTU_DTYPE_BF16; p.tab_bf16 = table_dtype == RECIR_HSTU_DTYPE_BF16;
   p.ts_is_float = timestamps_float != 0; p.i32 = (int)(flags & RECIR_HSTU_FLAG_OFFSETS_I32);
-  const long long chunks = L * ((D + 7) / 8);
-  hipLaunchKernelGGL(ts_pos_embeddings_kernel, dim3(row_grid(chunks)), dim3(256), 0, stream, p);
+  {
+    // elements per lane and access: 8 (both types two bytes wide) or 4 when the row length and the
+    // alignment of all four tensors allow 16-byte accesses, else 1
+    const bool aligned = ((((size_t)seq | (size_t)out | (size_t)pos_emb | (size_t)ts_emb) & 15) == 0);
+    const int wide = (p.seq_bf16 && p.tab_bf16) ? 8 : 4;
+    const int E = (aligned && D % wide == 0) ? wide : 1;
+    const int lg = group_log2(D / E);
+    const long long rpi = 64 >> lg;
+    const long long per_wave = rpi * 8 < 64 ? rpi * 8 : 64;
+    long long blocks = ((L + per_wave - 1) / per_wave + 3) / 4;
+    if (blocks > 65536) blocks = 65536;
+    const dim3 grid((unsigned)blocks), block(256);
+#define RECIR_TS_POS_LAUNCH(EE)                                                                              \
+    do {                                                                                                     \
+      if (p.seq_bf16 && p.tab_bf16) hipLaunchKernelGGL((ts_pos_embeddings_kernel<EE, true, true>), grid, block, 0, stream, p, lg);   \
+      else if (p.seq_bf16) hipLaunchKernelGGL((ts_pos_embeddings_kernel<EE, true, false>), grid, block, 0, stream, p, lg);           \
+      else if (p.tab_bf16) hipLaunchKernelGGL((ts_pos_embeddings_kernel<EE, false, true>), grid, block, 0, stream, p, lg);           \
+      else hipLaunchKernelGGL((ts_pos_embeddings_kernel<EE, false, false>), grid, block, 0, stream, p, lg);                         \
+    } while (0)
+    if (E == 8) RECIR_TS_POS_LAUNCH(8);
+    else if (E == 4) RECIR_TS_POS_LAUNCH(4);
+    else RECIR_TS_POS_LAUNCH(1);
+#undef RECIR_TS_POS_LAUNCH
+  }
   if (int rc = launch_status("ts_pos_embeddings_kernel")) return rc;
   void* temp = (char*)workspace + 3 * seg;
+  if (P <= CSORT_MAX_K) {
+    // both lists in three launches (stable counting sort: position rows < P, buckets <= 2048)
+    CsortParams c;
+    memset(&c, 0, sizeof(c));
+    csort_chunks(L, c.NW, c.CW);
+    c.L = L;
+    const int kp = P, kt = bucket_keys(TS);
+    c.kmax = kp > kt ? kp : kt;
+    char* t = (char*)temp;
+    int* counts = (int*)t;
+    t += align256((size_t)c.NW * ((size_t)kp + kt) * 4);
+    int* starts = (int*)t;
+    auto bits_of = [](int k) { int b = 0; while ((1 << b) < k) ++b; return b; };
+    c.list[0] = {p.pos_idx, sorted_pos, pos_order, counts, starts, kp, bits_of(kp)};
+    c.list[1] = {p.ts_idx, sorted_ts, ts_order, counts + (size_t)c.NW * kp, starts + kp, kt, bits_of(kt)};
+    // LDS: one histogram per wave, and in the scatter kernel one more table for the block
+    int wpb = 65536 / (c.kmax * 4) - 1;
+    wpb = wpb < 1 ? 1 : (wpb > 4 ? 4 : wpb);
+    const dim3 grid((unsigned)((c.NW + wpb - 1) / wpb), 2), block((unsigned)(wpb * 64));
+    hipLaunchKernelGGL(csort_count, grid, block, (size_t)wpb * c.kmax * 4, stream, c);
+    if (int rc = launch_status("csort_count")) return rc;
+    hipLaunchKernelGGL(csort_scan, dim3((unsigned)((c.kmax + 255) / 256), 2), dim3(256), 0, stream, c);
+    if (int rc = launch_status("csort_scan")) return rc;
+    hipLaunchKernelGGL(csort_scatter, grid, block, (size_t)(wpb + 1) * c.kmax * 4, stream, c);
+    if (int rc = launch_status("csort_scatter")) return rc;
+    return RECIR_HSTU_OK;
+  }
   size_t temp_bytes = sort_temp_bytes(L);
   // position rows fit 31 bits, buckets 12 (0..2048)
   hipError_t e = rocprim::radix_sort_pairs(temp, temp_bytes, (const int*)p.pos_idx, (int*)sorted_pos, (const int*)p.iota,

@@ -308,7 +308,7 @@ def _add_ts_pos_emb_fwd_device(seq_embeddings, seq_offsets, pos_embeddings, ts_e
     out = torch.empty_like(seq)
     idx = [torch.empty((rows,), dtype=torch.int32, device=dev) for _ in range(4)]
     if rows > 0:
-        ws_bytes = L.recir_add_timestamp_position_embeddings_workspace_bytes(rows)
+        ws_bytes = L.recir_add_timestamp_position_embeddings_workspace_bytes(rows, pos.shape[0], ts_tab.shape[0])
         ws = torch.empty((ws_bytes + 256,), dtype=torch.uint8, device=dev)
         base = (ws.data_ptr() + 255) // 256 * 256
         with torch.cuda.device(dev):

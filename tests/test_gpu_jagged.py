@@ -211,3 +211,33 @@ def test_add_ts_pos_emb(fn, seq_dt, tab_dt, ts_dt):
         if fn == "sqrt":
             assert safe.all() or True
             np.testing.assert_array_equal(got_ti, ti)  # sqrt is correctly rounded on both sides
+
+
+@pytest.mark.parametrize("P,D", [(4000, 8), (9000, 8), (64, 24)])
+def test_add_ts_pos_emb_sorted_lists_across_chunks(P, D):
+    """Sequences long enough for the index lists to span several chunks of the counting sort
+    (P <= 8192) and the general sort (P = 9000): sorted keys and permutations equal numpy's stable
+    argsort, rows equal the restatement; D = 24 fp32 takes the 16-byte path, D = 8 bf16 too."""
+    import recir_amd
+
+    rng = np.random.default_rng(5)
+    lengths = np.array([700, 1500, 33, 0, 900, 2047])
+    targets = np.array([10, 200, 33, 0, 0, 64])
+    off = _offsets(lengths)
+    Tmax = 2048
+    seq_dt = torch.float32 if D == 24 else torch.bfloat16
+    seq = torch.tensor(rng.standard_normal((int(off[-1]), D)).astype(np.float32)).to(seq_dt)
+    pos = torch.tensor(rng.standard_normal((P, D)).astype(np.float32)).to(seq_dt)
+    tab = torch.tensor(rng.standard_normal((2049, D)).astype(np.float32)).to(seq_dt)
+    stamps = np.sort(rng.integers(0, 400_000_000, size=(len(lengths), Tmax)), axis=1)
+    got = recir_amd.add_ts_pos_emb_fwd(seq.to(DEV), torch.tensor(off, device=DEV), pos.to(DEV), tab.to(DEV),
+                                       torch.tensor(stamps, device=DEV), torch.tensor(lengths, device=DEV),
+                                       torch.tensor(targets, device=DEV), 2048, 2, False, "sqrt")
+    bf = seq_dt == torch.bfloat16
+    out, pi, ti, _pre = jo.add_ts_pos_emb(seq.float().numpy(), off, pos.float().numpy(), tab.float().numpy(), stamps,
+                                          lengths, targets, 2, False, "sqrt", seq_bf16=bf, tab_bf16=bf)
+    np.testing.assert_array_equal(got[1].cpu().numpy(), np.sort(pi))
+    np.testing.assert_array_equal(got[2].cpu().numpy(), np.argsort(pi, kind="stable"))
+    np.testing.assert_array_equal(got[3].cpu().numpy(), np.sort(ti))
+    np.testing.assert_array_equal(got[4].cpu().numpy(), np.argsort(ti, kind="stable"))
+    np.testing.assert_array_equal(got[0].float().cpu().numpy(), out)
