@@ -44,38 +44,104 @@ namespace {
 // Per-head e4m3 quantiser: amax per head (bf16 magnitudes compare as integers), scale = amax / 448,
 // codes = e4m3(clamp(x / scale)).  Eight elements (16 bytes) per thread; D is a multiple of 8.
 // ---------------------------------------------------------------------------------------------
+// head of 16-byte chunk i of a [T, H, D] bf16 tensor (D8 = D / 8 chunks per row).  The general
+// form is two 64-bit divisions per chunk, which costs more than moving the chunk: shifts and masks
+// when D8 and H are powers of two (d8_shift, h_mask >= 0), 32-bit arithmetic when the index fits.
+__device__ __forceinline__ int quant_head(size_t i, int D8, int H, int d8_shift, int h_mask) {
+  if (d8_shift >= 0) {
+    const size_t row = i >> d8_shift;
+    return h_mask >= 0 ? (int)(row & (size_t)h_mask) : (int)(row % (size_t)H);
+  }
+  if (i <= 0xffffffffull) return (int)(((unsigned)i / (unsigned)D8) % (unsigned)H);
+  return (int)((i / (size_t)D8) % (size_t)H);
+}
+
 __global__ void hstu_quant_clear(unsigned* amax_bits, int H) {
   for (int h = threadIdx.x; h < H; h += blockDim.x) amax_bits[h] = 0u;
 }
 
-__global__ __launch_bounds__(256) void hstu_quant_amax(const u32x4* x, unsigned* amax_bits, size_t n8, int H, int D8) {
+// Per-head maximum magnitude.  The maxima of a block are gathered in LDS (integer max on the bf16
+// magnitude bits) and only then merged into the H global words: one global atomic per element chunk
+// would queue millions of them on H addresses.
+constexpr int QUANT_LDS_HEADS = 4096;
+#ifndef QUANT_AMAX_BLOCKS
+#define QUANT_AMAX_BLOCKS 1024
+#endif
+__global__ __launch_bounds__(256) void hstu_quant_amax(const u32x4* x, unsigned* amax_bits, unsigned* partial, size_t n8, int H, int D8, int d8_shift, int h_mask) {
+  __shared__ unsigned lmax[QUANT_LDS_HEADS];
+  const bool in_lds = H <= QUANT_LDS_HEADS;
+  if (in_lds) {
+    for (int h = threadIdx.x; h < H; h += blockDim.x) lmax[h] = 0u;
+    __syncthreads();
+  }
   const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
-    const u32x4 v = x[i];
-    unsigned mx = 0;
+  // When the grid stride is a multiple of the chunks of one token (D8 * H), a thread meets the same
+  // head in every iteration: it keeps one running maximum and merges it once.
+  const bool fixed_head = stride % ((size_t)D8 * H) == 0;
+  constexpr int U = 4;  // loads in flight per thread
+  const size_t first = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  unsigned run = 0;
+  for (size_t i0 = first; i0 < n8; i0 += stride * U) {
+    u32x4 v[U];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      mx = max(mx, (v[j] << 16) & 0x7fffffffu);
-      mx = max(mx, v[j] & 0x7fff0000u);
+    for (int u = 0; u < U; ++u) {
+      const size_t i = i0 + u * stride;
+      v[u] = i < n8 ? x[i] : u32x4{0u, 0u, 0u, 0u};
     }
-    const int h = (int)((i / D8) % H);
-    // wave-level reduction when the whole wave sits in one head (D8 >= 64 is not required for correctness)
-    atomicMax(&amax_bits[h], mx);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const size_t i = i0 + u * stride;
+      unsigned mx = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        mx = max(mx, (v[u][j] << 16) & 0x7fffffffu);
+        mx = max(mx, v[u][j] & 0x7fff0000u);
+      }
+      if (fixed_head) {
+        run = max(run, mx);
+      } else if (i < n8) {
+        const int h = quant_head(i, D8, H, d8_shift, h_mask);
+        if (in_lds) atomicMax(&lmax[h], mx);
+        else atomicMax(&amax_bits[h], mx);
+      }
+    }
+  }
+  if (fixed_head && first < n8) {
+    const int h = quant_head(first, D8, H, d8_shift, h_mask);
+    if (in_lds) atomicMax(&lmax[h], run);
+    else atomicMax(&amax_bits[h], run);
+  }
+  if (in_lds) {
+    __syncthreads();
+    // with a scratch table every block leaves its maxima for the finalising kernel; otherwise H
+    // global atomics per block (a thousand blocks on H addresses: about 12 us of queueing)
+    for (int h = threadIdx.x; h < H; h += blockDim.x) {
+      if (partial) partial[(size_t)blockIdx.x * H + h] = lmax[h];
+      else if (lmax[h]) atomicMax(&amax_bits[h], lmax[h]);
+    }
   }
 }
 
-__global__ void hstu_quant_finalize(float* scale, int H) {
+__global__ __launch_bounds__(1024) void hstu_quant_finalize(float* scale, const unsigned* partial, int blocks, int H) {
+  __shared__ unsigned red[QUANT_LDS_HEADS];
+  if (partial) {  // H <= QUANT_LDS_HEADS on this path
+    for (int h = threadIdx.x; h < H; h += blockDim.x) red[h] = 0u;
+    __syncthreads();
+    const int n = blocks * H;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) atomicMax(&red[i % H], partial[i]);
+    __syncthreads();
+  }
   for (int h = threadIdx.x; h < H; h += blockDim.x) {
-    const float amax = __uint_as_float(((unsigned*)scale)[h]);
-    scale[h] = fmaxf(amax, 1e-12f) / 448.0f;
+    const unsigned bits = partial ? red[h] : ((unsigned*)scale)[h];
+    scale[h] = fmaxf(__uint_as_float(bits), 1e-12f) / 448.0f;
   }
 }
 
-__global__ __launch_bounds__(256) void hstu_quant_encode(const u32x4* x, u32x2* codes, const float* scale, size_t n8, int H, int D8) {
+__global__ __launch_bounds__(256) void hstu_quant_encode(const u32x4* x, u32x2* codes, const float* scale, size_t n8, int H, int D8, int d8_shift, int h_mask) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
     const u32x4 v = x[i];
-    const float sc = scale[(i / D8) % H];
+    const float sc = scale[quant_head(i, D8, H, d8_shift, h_mask)];
     float y[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -535,16 +601,27 @@ int recir_hstu_quantize_e4m3_per_head(const void* x_bf16, void* codes_u8, float*
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "x must be 16-byte and codes 8-byte aligned");
   const size_t n8 = (size_t)T * H * (D / 8);
   const unsigned blocks = (unsigned)((n8 + 255) / 256 < 4096 ? (n8 + 255) / 256 : 4096);
-  hipLaunchKernelGGL(hstu_quant_clear, dim3(1), dim3(256), 0, stream, (unsigned*)scale, H);
-  if (int rc = launch_status("hstu_quant_clear")) return rc;
+  const unsigned amax_blocks = blocks < QUANT_AMAX_BLOCKS ? blocks : QUANT_AMAX_BLOCKS;  // each block ends with H global atomics on H addresses
+  const int D8 = D / 8;
+  int d8_shift = -1, h_mask = -1;
+  if ((D8 & (D8 - 1)) == 0) { d8_shift = 0; while ((1 << d8_shift) < D8) ++d8_shift; }
+  if ((H & (H - 1)) == 0) h_mask = H - 1;
+  // the codes buffer doubles as the table of per-block maxima (it is written only afterwards)
+  unsigned* partial = nullptr;
+  if (H <= QUANT_LDS_HEADS && n8 > 0 && (size_t)T * H * D >= (size_t)amax_blocks * H * 4 && (((size_t)codes_u8) & 3) == 0)
+    partial = (unsigned*)codes_u8;
+  if (!partial) {
+    hipLaunchKernelGGL(hstu_quant_clear, dim3(1), dim3(256), 0, stream, (unsigned*)scale, H);
+    if (int rc = launch_status("hstu_quant_clear")) return rc;
+  }
   if (n8 > 0) {
-    hipLaunchKernelGGL(hstu_quant_amax, dim3(blocks), dim3(256), 0, stream, (const u32x4*)x_bf16, (unsigned*)scale, n8, H, D / 8);
+    hipLaunchKernelGGL(hstu_quant_amax, dim3(amax_blocks), dim3(256), 0, stream, (const u32x4*)x_bf16, (unsigned*)scale, partial, n8, H, D / 8, d8_shift, h_mask);
     if (int rc = launch_status("hstu_quant_amax")) return rc;
   }
-  hipLaunchKernelGGL(hstu_quant_finalize, dim3(1), dim3(256), 0, stream, scale, H);
+  hipLaunchKernelGGL(hstu_quant_finalize, dim3(1), dim3(1024), 0, stream, scale, (const unsigned*)partial, (int)amax_blocks, H);
   if (int rc = launch_status("hstu_quant_finalize")) return rc;
   if (n8 > 0) {
-    hipLaunchKernelGGL(hstu_quant_encode, dim3(blocks), dim3(256), 0, stream, (const u32x4*)x_bf16, (u32x2*)codes_u8, scale, n8, H, D / 8);
+    hipLaunchKernelGGL(hstu_quant_encode, dim3(blocks), dim3(256), 0, stream, (const u32x4*)x_bf16, (u32x2*)codes_u8, scale, n8, H, D / 8, d8_shift, h_mask);
     if (int rc = launch_status("hstu_quant_encode")) return rc;
   }
   return RECIR_HSTU_OK;
