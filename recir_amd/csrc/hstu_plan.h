@@ -37,6 +37,11 @@ __device__ __forceinline__ int snake_slot(int pr) {
 
 constexpr int PLAN_REVERSE = 1;     // item at the position of tile t carries tile nt - 1 - t
 constexpr int PLAN_SHIFT_ODD = 2;   // see tile_rows
+constexpr int PLAN_NO_SPREAD = 4;   // always deal whole (sequence, head) pairs
+#ifndef HSTU_PLAN_SPREAD_AT
+#define HSTU_PLAN_SPREAD_AT 1.05f
+#endif
+constexpr float PLAN_SPREAD_AT = HSTU_PLAN_SPREAD_AT;  // heaviest list / mean list beyond which tiles are dealt
 
 // Rows [q0, q_end) of tile t of a sequence of n rows cut into tiles of bm rows.  Plain cut:
 // [t bm, t bm + bm).  With PLAN_SHIFT_ODD and an odd number of half tiles, tile 0 holds the first
@@ -67,7 +72,8 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
   __shared__ int nt_by_rank[PLAN_MAX_B];
   __shared__ int xnt[NUM_XCD][PLAN_MAX_PAIRS / NUM_XCD + 2];  // tiles of the k-th pair of list x
   __shared__ int above[NUM_XCD][PLAN_MAX_TILES + 1];          // tiles of list x with index > t
-  __shared__ int tmax_s;
+  __shared__ int tmax_s, spread_s, items_s;
+  __shared__ float list_work[NUM_XCD];
   __shared__ int seq_s[PLAN_MAX_B], seq_n[PLAN_MAX_B], seq_cap[PLAN_MAX_B], seq_ctx[PLAN_MAX_B];
   const int tid = threadIdx.x;
   const int B = p.B, H = p.H;
@@ -105,6 +111,58 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
   }
   __syncthreads();
   const int tmax = tmax_s;
+  // Work of a pair with v tiles ~ v (v + 1) / 2 (tile t meets t + 1 key tiles).  When dealing whole
+  // pairs leaves the lists unequal (few pairs, or one sequence far longer than the rest), tiles are
+  // dealt instead: see below.
+  if (tid < NUM_XCD) {
+    float w = 0.f;
+    for (int k = 0; k < per_list; ++k) { const float v = (float)xnt[tid][k]; w += v * (v + 1.f); }
+    list_work[tid] = w;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float mx = 0.f, sum = 0.f;
+    for (int x = 0; x < NUM_XCD; ++x) { mx = fmaxf(mx, list_work[x]); sum += list_work[x]; }
+    int n_items = 0;
+    for (int r = 0; r < B; ++r) n_items += nt_by_rank[r];
+    items_s = n_items * H;
+    spread_s = (mode & PLAN_NO_SPREAD) ? 0 : (mx * NUM_XCD > sum * PLAN_SPREAD_AT);
+  }
+  __syncthreads();
+  if (spread_s) {
+    // All tiles of all pairs in one order, tile index descending and pair rank ascending inside one
+    // index, dealt to the lists in the same boustrophedon order: every list is still heaviest
+    // first, the list sums differ by at most one tile's work, and a pair's K and V rows are read
+    // through several L2s, which costs little when few pairs carry the work.
+    const int ttab = min(tmax, PLAN_MAX_TILES) + 1;
+    auto all_above = [&](int t) {
+      int a = 0;
+      for (int r = 0; r < B; ++r) a += max(0, nt_by_rank[r] - 1 - t);
+      return a * H;
+    };
+    for (int t = tid; t < ttab; t += PLAN_THREADS) above[0][t] = all_above(t);
+    __syncthreads();
+    const int per_rank = tmax * H;
+    for (int i = tid; i < B * per_rank; i += PLAN_THREADS) {
+      const int r = i / per_rank, rem = i - r * per_rank;
+      const int t = rem / H, h = rem - t * H;
+      const int my_nt = nt_by_rank[r];
+      if (t >= my_nt) continue;
+      const int b = seq_of_rank[r];
+      SeqInfo si;
+      si.s = seq_s[b]; si.n = seq_n[b]; si.cap = seq_cap[b]; si.ctx_eff = seq_ctx[b];
+      // the r ranks ahead have at least as many tiles, so each of their pairs owns a tile t
+      const int g = (t < ttab ? above[0][t] : all_above(t)) + r * H + h;
+      WorkItem w;
+      fill_item(w, si, bm, t, my_nt, mode, h, b);
+      p.ws_items[(size_t)snake_xcd(g) * p.items_cap + snake_slot(g)] = w;
+    }
+    if (tid < NUM_XCD) {
+      const int n_items = items_s, part = n_items % (2 * NUM_XCD);
+      p.ws_counts[tid] = 2 * (n_items / (2 * NUM_XCD)) + (tid < part ? 1 : 0) + (tid >= 2 * NUM_XCD - part ? 1 : 0);
+    }
+    return;
+  }
   auto tiles_above = [&](int x, int t) {
     int a = 0;
     for (int k = 0; k < per_list; ++k) a += max(0, xnt[x][k] - 1 - t);

@@ -171,6 +171,23 @@ def test_tiled_backward_matches_oracle_on_ragged_tiles(oracle, ctx):
     assert_grads_close(got, want, int(wl.seq_offsets[-1]), BF16_REL, f"ragged ctx{ctx}")
 
 
+@pytest.mark.parametrize("lengths", [[900] + [70] * 20, [260] * 16], ids=["one_long", "even"])
+def test_tiled_backward_with_tiles_and_pairs_dealt(oracle, lengths):
+    """The work lists of both backward kernels when single tiles are dealt to the XCDs (one sequence
+    far longer than the rest) and when whole (sequence, head) pairs are."""
+    from recir_amd import _lib
+
+    wl = _mid_workload(77, lengths, [2] * len(lengths), 0)
+    g = torch.Generator().manual_seed(10)
+    dout = torch.randn(wl.T, wl.H, 128, generator=g).to(torch.bfloat16).float()
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                           attn_scale=np.float32(0.02), contextual_seq_len=0)
+    got = run_hip_bwd(wl, dout, attn_scale=torch.tensor(0.02))
+    assert _lib.last_kernel() == "bwd_tiled_d128_bf16"
+    assert_grads_close(got, want, int(wl.seq_offsets[-1]), BF16_REL, f"lengths {lengths[:2]}")
+
+
 def test_tiled_backward_agrees_with_generic_at_full_size():
     """Config 2 (B=32, up to 2048 tokens per sequence): the tiled MFMA kernels against the generic
     fp32-arithmetic kernels on the same bf16 tensors."""

@@ -262,6 +262,17 @@ def test_many_short_sequences_use_the_general_work_list(oracle):
     assert_bf16_close(out, run_oracle(oracle, wl), "B=1300")
 
 
+@pytest.mark.parametrize("lengths", [[1500] + [70] * 30, [300] * 16, [700]], ids=["one_long", "even", "single"])
+def test_work_list_dealing_by_tiles_and_by_pairs(oracle, lengths):
+    """One sequence far longer than the rest, or fewer (sequence, head) pairs than XCDs, makes the
+    work-list builder deal single tiles to the XCD lists; an even batch deals whole pairs."""
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged(lengths, [3] * len(lengths), 2, 128, 128, max_seq_len=max(lengths), alpha=1 / 128,
+                     dtype="bf16", seed=21)
+    assert_bf16_close(run_hip(wl), run_oracle(oracle, wl), f"lengths {lengths[:2]}...")
+
+
 def test_sequences_longer_than_max_seq_len_do_not_break_the_work_list(oracle):
     """Out of contract (n > max_seq_len), but the launch must stay in bounds: the work lists are
     then longer than the grid assumes and the workgroups loop over them."""
