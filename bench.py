@@ -118,8 +118,8 @@ def bench_backward(args, wl, L, dev):
 
     from recir_amd import _lib
 
-    if wl.dtype not in ("bf16", "fp32") or wl.rab is not None:
-        print("--backward supports the bf16/fp32 configurations without a score bias", file=sys.stderr)
+    if wl.dtype not in ("bf16", "fp32"):
+        print("--backward supports the bf16/fp32 configurations", file=sys.stderr)
         sys.exit(2)
     dt = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
     q, k, v = wl.q.to(dev, dt), wl.k.to(dev, dt), wl.v.to(dev, dt)
@@ -127,6 +127,7 @@ def bench_backward(args, wl, L, dev):
     dout = torch.randn(wl.T, wl.H, v.shape[2], generator=g).to(dev, dt)
     off, nt = wl.seq_offsets.to(dev), wl.num_targets.to(dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    rab = None if wl.rab is None else wl.rab.to(dev)
     T, H, Dqk = q.shape
     Dv = v.shape[2]
     code = _lib.DTYPE_FP32 if wl.dtype == "fp32" else _lib.DTYPE_BF16
@@ -136,7 +137,8 @@ def bench_backward(args, wl, L, dev):
 
     def call(flags=0):
         rc = L.recir_hstu_attn_bwd(dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), dq.data_ptr(),
-                                   dk.data_ptr(), dv.data_ptr(), off.data_ptr(), nt.data_ptr(), None, None,
+                                   dk.data_ptr(), dv.data_ptr(), off.data_ptr(), nt.data_ptr(),
+                                   None if rab is None else rab.data_ptr(), None,
                                    T, wl.B, H, Dqk, Dv, wl.max_seq_len, wl.contextual_seq_len, wl.max_attn_len,
                                    wl.full_attn_size, wl.alpha, code, flags0 | flags, ws.data_ptr(), ws.numel(), ctypes.c_void_p(stream.cuda_stream))
         if rc != 0:

@@ -291,6 +291,21 @@ int launch_status(const char* what) {
 size_t max_items(int T, int B, int H) { return ((size_t)((T + BM - 1) / BM) + (size_t)B) * (size_t)H; }
 constexpr size_t WS_HEADER = 64;
 
+template <bool SEMI, bool HAS_RAB>
+void launch_bwd_tiled_as(dim3 grid, hipStream_t stream, const BwdParams& bk, const BwdParams& bq) {
+  hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB>), grid, dim3(256), 0, stream, bk);
+  hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, HAS_RAB>), grid, dim3(256), 0, stream, bq);
+}
+void launch_bwd_tiled(bool semi, bool has_rab, dim3 grid, hipStream_t stream, const BwdParams& bk, const BwdParams& bq) {
+  if (semi) {
+    if (has_rab) launch_bwd_tiled_as<true, true>(grid, stream, bk, bq);
+    else launch_bwd_tiled_as<true, false>(grid, stream, bk, bq);
+  } else {
+    if (has_rab) launch_bwd_tiled_as<false, true>(grid, stream, bk, bq);
+    else launch_bwd_tiled_as<false, false>(grid, stream, bk, bq);
+  }
+}
+
 template <bool FP8>
 void launch_dl(bool has_rab, bool semi, dim3 grid, hipStream_t stream, const Params& p) {
   if (semi) {
@@ -507,12 +522,12 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "head dims above %d are not supported (Dqk=%d Dv=%d)", BWD_GENERIC_MAX_D, Dqk, Dv);
   if ((unsigned)H > 65535u) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "more than 65535 heads");
   const unsigned variant = (flags & RECIR_HSTU_FLAG_KERNEL_MASK) >> RECIR_HSTU_FLAG_KERNEL_SHIFT;
-  // the tiled kernels cover bf16, head dim 128, a scalar output scale and no score bias
-  const bool tiled_ok = bf16 && Dqk == HD && Dv == HD && !rab && !(flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) &&
+  // the tiled kernels cover bf16, head dim 128 and a scalar output scale
+  const bool tiled_ok = bf16 && Dqk == HD && Dv == HD && !(flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) &&
                         (((size_t)dout | (size_t)q | (size_t)k | (size_t)v | (size_t)dq | (size_t)dk | (size_t)dv) & 15) == 0;
   if (variant >= 2 && !tiled_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "tiled backward needs bf16, Dqk = Dv = 128, 16-byte aligned tensors, "
-                "a scalar attn_scale and no rab");
+                "and a scalar attn_scale");
   if (tiled_ok && variant != 1) {
     const size_t half_ws = (recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype) + 255) & ~(size_t)255;
     if (!workspace || workspace_bytes < 2 * half_ws || ((size_t)workspace & 15))
@@ -546,13 +561,9 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
       }
     }
     const dim3 grid((unsigned)(slots * NUM_XCD));
-    if (semi) hipLaunchKernelGGL(hstu_bwd_dkv_d128<true>, grid, dim3(256), 0, stream, bk);
-    else hipLaunchKernelGGL(hstu_bwd_dkv_d128<false>, grid, dim3(256), 0, stream, bk);
-    if (int rc = launch_status("hstu_bwd_dkv_d128")) return rc;
-    if (semi) hipLaunchKernelGGL(hstu_bwd_dq_d128<true>, grid, dim3(256), 0, stream, bq);
-    else hipLaunchKernelGGL(hstu_bwd_dq_d128<false>, grid, dim3(256), 0, stream, bq);
-    if (int rc = launch_status("hstu_bwd_dq_d128")) return rc;
-    g_last_kernel = "bwd_tiled_d128_bf16";
+    launch_bwd_tiled(semi, rab != nullptr, grid, stream, bk, bq);
+    if (int rc = launch_status("hstu_bwd_d128")) return rc;
+    g_last_kernel = rab ? "bwd_tiled_d128_bf16_rab" : "bwd_tiled_d128_bf16";
     return RECIR_HSTU_OK;
   }
   const dim3 grid((unsigned)T, (unsigned)H);

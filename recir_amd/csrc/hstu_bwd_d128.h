@@ -1,5 +1,5 @@
 // Tiled MFMA kernels of the HSTU attention backward, head dim 128 (qk and v), bf16 tensors,
-// scalar output scale, no score bias.
+// scalar output scale, optional relative score bias (read only: it gets no gradient).
 //
 // Two kernels, as in the reference (recir/ops/pallas/jagged_hstu_attention.py:724-1339 and
 // recir/ops/helion/jagged_hstu_attention.py:356-570): every gradient row has one writer.
@@ -100,6 +100,11 @@ __device__ __forceinline__ bf16x8 bwd_tr_frag(const char* tile, const BwdLanes& 
 // row `last`; what they contribute is masked by the caller.
 __device__ __forceinline__ void bwd_issue_rows(const char* gbase, unsigned row_bytes, int last, unsigned short* tile,
                                                const BwdLanes& c, int wave) {
+  // the base is the same for every lane; say so where the compiler cannot prove it (the copy takes
+  // it in scalar registers)
+  const size_t gb = (size_t)gbase;
+  gbase = (const char*)(((size_t)(unsigned)__builtin_amdgcn_readfirstlane((int)(gb >> 32)) << 32) |
+                        (size_t)(unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)gb));
 #pragma unroll
   for (int ps = 0; ps < 4; ++ps) {
     const int j = 4 * wave + ps;
@@ -134,11 +139,25 @@ __device__ __forceinline__ float bwd_output_scale(const Params& p) {
   return p.attn_scale ? p.attn_scale[0] : 1.0f / (float)p.N;
 }
 
+// Score-bias entries of one 32 x 32 block for this lane: element r sits at index
+// base + step (8 (r / 4) + r % 4) of the head's row of rab (index = query - key + N - 1, clamped to
+// the row as in the forward), step = -1 when the block's elements run over keys, +1 over queries.
+// The table is small (H (2N - 1) floats) and stays in the caches; the loads are issued before the
+// products of the block and consumed after them.
+__device__ __forceinline__ void bwd_bias_block(const float* __restrict__ rab_row, int rab_w, int base, int step, float (&b)[16]) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int idx = base + step * (8 * (r >> 2) + (r & 3));
+    b[r] = rab_row[min(max(idx, 0), rab_w - 1)];
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // dQ
 // ---------------------------------------------------------------------------------------------
 // SEMI: semi-local mask (max_attn_len > 0), as in the forward kernel.
-template <bool SEMI>
+// HAS_RAB: scores carry the relative bias rab[h, query - key + N - 1] (no gradient flows to it).
+template <bool SEMI, bool HAS_RAB>
 __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp) {
   const Params& p = bp.f;
   __shared__ __attribute__((aligned(1024))) unsigned short Ks0[BWD_BN * HD];
@@ -170,6 +189,8 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     const unsigned row_bytes = (unsigned)p.H * HD * 2u;
     const char* __restrict__ kgb = (const char*)p.k + ((size_t)si.s * p.H + h) * (HD * 2);
     const char* __restrict__ vgb = (const char*)p.v + ((size_t)si.s * p.H + h) * (HD * 2);
+    const int rab_w = 2 * p.N - 1;
+    const float* __restrict__ rab_row = HAS_RAB ? p.rab + (size_t)h * rab_w : nullptr;
 
     const int qw0 = q0 + wave * 32;
     const int m = qw0 + l32;
@@ -229,6 +250,14 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
 #pragma unroll
       for (int kvb = 0; kvb < 2; ++kvb) {
         f32x16 st = zero, dpt = zero;
+        if (HAS_RAB) {
+          // the bias enters as the initial value of the score accumulator: no register lives across
+          // the products for it (this kernel runs at its register limit)
+          float bias[16];
+          bwd_bias_block(rab_row, rab_w, m - (k0 + kvb * 32 + 4 * half) + p.N - 1, -1, bias);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) st[r] = bias[r] * kLog2e;
+        }
         // phases are fenced so that the fragment reads of one are not hoisted over the previous one
         // (keeps the live registers within the two-waves-per-SIMD budget)
         __builtin_amdgcn_sched_barrier(0);
@@ -328,7 +357,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
 // ---------------------------------------------------------------------------------------------
 // dK, dV
 // ---------------------------------------------------------------------------------------------
-template <bool SEMI>
+template <bool SEMI, bool HAS_RAB>
 __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
   const Params& p = bp.f;
   __shared__ __attribute__((aligned(1024))) unsigned short Qs0[BWD_BN * HD];
@@ -360,6 +389,8 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     const unsigned row_bytes = (unsigned)p.H * HD * 2u;
     const char* __restrict__ qgb = (const char*)p.q + ((size_t)si.s * p.H + h) * (HD * 2);
     const char* __restrict__ ggb = (const char*)bp.dout + ((size_t)si.s * p.H + h) * (HD * 2);
+    const int rab_w = 2 * p.N - 1;
+    const float* __restrict__ rab_row = HAS_RAB ? p.rab + (size_t)h * rab_w : nullptr;
 
     const int jw0 = j0 + wave * 32;
     const int j = jw0 + l32;  // this lane's key row
@@ -407,6 +438,8 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
 #pragma unroll
       for (int qb32 = 0; qb32 < 2; ++qb32) {
         f32x16 s = zero, dp = zero;
+        float bias[16];
+        if (HAS_RAB) bwd_bias_block(rab_row, rab_w, m0 + qb32 * 32 + 4 * half - j + p.N - 1, 1, bias);
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
           s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(qb, lc, qb32, kk), kf[kk], s, 0, 0, 0);
@@ -416,7 +449,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
         float pv[16], ds[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float u = s[r];
+          const float u = HAS_RAB ? fmaf(bias[r], kLog2e, s[r]) : s[r];
           const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
           const float sv = u * kLn2;
           float pe = sv * sig;

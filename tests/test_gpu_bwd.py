@@ -171,6 +171,57 @@ def test_tiled_backward_matches_oracle_on_ragged_tiles(oracle, ctx):
     assert_grads_close(got, want, int(wl.seq_offsets[-1]), BF16_REL, f"ragged ctx{ctx}")
 
 
+@pytest.mark.parametrize("A,F,ctx", [(0, 0, 0), (0, 0, 70), (100, 37, 5)])
+def test_tiled_backward_with_score_bias(oracle, A, F, ctx):
+    """Relative bias rab[h, query - key + N - 1] inside the tiled kernels (plain and semi-local mask),
+    a bias large enough that dropping it, or reading it at a shifted index, fails the tolerance."""
+    from recir_amd import _lib, ops
+    from recir_amd.workloads import make_jagged
+
+    lengths = [1, 63, 64, 65, 127, 128, 129, 0, 191, 257, 330, 90]
+    targets = [0, 3, 64, 1, 100, 0, 129, 0, 60, 2, 200, 90]
+    wl = make_jagged(lengths, targets, 2, 128, 128, max_seq_len=max(lengths), alpha=1.0 / 128, dtype="bf16",
+                     seed=41 + ctx, contextual_seq_len=ctx, tail_rows=5, max_attn_len=A, full_attn_size=F)
+    g = torch.Generator().manual_seed(12)
+    dout = torch.randn(wl.T, wl.H, 128, generator=g).to(torch.bfloat16).float()
+    rab = torch.randn(wl.H, 2 * wl.max_seq_len - 1, generator=g)
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha, rab=rab.numpy(),
+                           contextual_seq_len=ctx, max_attn_len=A, full_attn_size=F)
+    end = int(wl.seq_offsets[-1])
+    got = run_hip_bwd(wl, dout, rab=rab)
+    assert _lib.last_kernel() == "bwd_tiled_d128_bf16_rab"
+    assert_grads_close(got, want, end, BF16_REL, f"rab A{A} F{F} ctx{ctx}")
+    no_bias = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                              wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                              contextual_seq_len=ctx, max_attn_len=A, full_attn_size=F)
+    assert error_stats(got[0], no_bias[0])["rel_fro"] > 10 * BF16_REL  # the bias matters at this size
+    shifted = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                              wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                              rab=torch.roll(rab, 1, dims=1).numpy(), contextual_seq_len=ctx, max_attn_len=A,
+                              full_attn_size=F)
+    assert error_stats(got[0], shifted[0])["rel_fro"] > 10 * BF16_REL  # and so does its index
+    with ops.force_kernel(ops.KERNEL_GENERIC):
+        gotg = run_hip_bwd(wl, dout, rab=rab)
+    assert_grads_close(gotg, want, end, BF16_REL, "generic rab")
+
+
+def test_config3_backward_tiled_agrees_with_generic():
+    """Config 3 (bias + contextual prefix) at full size: tiled against generic kernels."""
+    from recir_amd import _lib, ops
+    from recir_amd.workloads import make_config
+
+    wl = make_config(3)
+    g = torch.Generator().manual_seed(5)
+    dout = torch.randn(wl.T, wl.H, 128, generator=g)
+    got = run_hip_bwd(wl, dout, rab=wl.rab)
+    assert _lib.last_kernel() == "bwd_tiled_d128_bf16_rab"
+    with ops.force_kernel(ops.KERNEL_GENERIC):
+        ref = run_hip_bwd(wl, dout, rab=wl.rab)
+    assert _lib.last_kernel() == "bwd_generic_bf16"
+    assert_grads_close(got, [r.float().cpu().numpy() for r in ref], int(wl.seq_offsets[-1]), BF16_REL, "config3")
+
+
 @pytest.mark.parametrize("lengths", [[900] + [70] * 20, [260] * 16], ids=["one_long", "even"])
 def test_tiled_backward_with_tiles_and_pairs_dealt(oracle, lengths):
     """The work lists of both backward kernels when single tiles are dealt to the XCDs (one sequence
