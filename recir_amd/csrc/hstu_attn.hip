@@ -293,8 +293,13 @@ constexpr size_t WS_HEADER = 64;
 
 template <bool SEMI, bool HAS_RAB>
 void launch_bwd_tiled_as(dim3 grid, hipStream_t stream, const BwdParams& bk, const BwdParams& bq) {
-  hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB>), grid, dim3(256), 0, stream, bk);
-  hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, HAS_RAB>), grid, dim3(256), 0, stream, bq);
+  if (bk.f.attn_scale && (bk.f.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN)) {
+    hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB, true>), grid, dim3(256), 0, stream, bk);
+    hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, HAS_RAB, true>), grid, dim3(256), 0, stream, bq);
+  } else {
+    hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB, false>), grid, dim3(256), 0, stream, bk);
+    hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, HAS_RAB, false>), grid, dim3(256), 0, stream, bq);
+  }
 }
 void launch_bwd_tiled(bool semi, bool has_rab, dim3 grid, hipStream_t stream, const BwdParams& bk, const BwdParams& bq) {
   if (semi) {
@@ -522,12 +527,11 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "head dims above %d are not supported (Dqk=%d Dv=%d)", BWD_GENERIC_MAX_D, Dqk, Dv);
   if ((unsigned)H > 65535u) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "more than 65535 heads");
   const unsigned variant = (flags & RECIR_HSTU_FLAG_KERNEL_MASK) >> RECIR_HSTU_FLAG_KERNEL_SHIFT;
-  // the tiled kernels cover bf16, head dim 128 and a scalar output scale
-  const bool tiled_ok = bf16 && Dqk == HD && Dv == HD && !(flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) &&
+  // the tiled kernels cover bf16 at head dim 128
+  const bool tiled_ok = bf16 && Dqk == HD && Dv == HD &&
                         (((size_t)dout | (size_t)q | (size_t)k | (size_t)v | (size_t)dq | (size_t)dk | (size_t)dv) & 15) == 0;
   if (variant >= 2 && !tiled_ok)
-    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "tiled backward needs bf16, Dqk = Dv = 128, 16-byte aligned tensors, "
-                "and a scalar attn_scale");
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "tiled backward needs bf16, Dqk = Dv = 128 and 16-byte aligned tensors");
   if (tiled_ok && variant != 1) {
     const size_t half_ws = (recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype) + 255) & ~(size_t)255;
     if (!workspace || workspace_bytes < 2 * half_ws || ((size_t)workspace & 15))

@@ -1,5 +1,5 @@
 // Tiled MFMA kernels of the HSTU attention backward, head dim 128 (qk and v), bf16 tensors,
-// scalar output scale, optional relative score bias (read only: it gets no gradient).
+// scalar or per-token output scale, optional relative score bias (read only: neither gets a gradient).
 //
 // Two kernels, as in the reference (recir/ops/pallas/jagged_hstu_attention.py:724-1339 and
 // recir/ops/helion/jagged_hstu_attention.py:356-570): every gradient row has one writer.
@@ -98,12 +98,13 @@ __device__ __forceinline__ bf16x8 bwd_tr_frag(const char* tile, const BwdLanes& 
 // This wave's share (4 of 16 instructions) of the copy of rows [r_first, r_first + 64) of a
 // [rows, H, 128] bf16 matrix into a staged tile.  Rows past `last` (relative to r_first) re-read
 // row `last`; what they contribute is masked by the caller.
+template <bool PIN_BASE>
 __device__ __forceinline__ void bwd_issue_rows(const char* gbase, unsigned row_bytes, int last, unsigned short* tile,
                                                const BwdLanes& c, int wave) {
-  // the base is the same for every lane; say so where the compiler cannot prove it (the copy takes
-  // it in scalar registers)
+  // the base is the same for every lane; PIN_BASE says so where the compiler cannot prove it (the
+  // copy takes it in scalar registers)
   const size_t gb = (size_t)gbase;
-  gbase = (const char*)(((size_t)(unsigned)__builtin_amdgcn_readfirstlane((int)(gb >> 32)) << 32) |
+  if (PIN_BASE) gbase = (const char*)(((size_t)(unsigned)__builtin_amdgcn_readfirstlane((int)(gb >> 32)) << 32) |
                         (size_t)(unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)gb));
 #pragma unroll
   for (int ps = 0; ps < 4; ++ps) {
@@ -157,7 +158,8 @@ __device__ __forceinline__ void bwd_bias_block(const float* __restrict__ rab_row
 // ---------------------------------------------------------------------------------------------
 // SEMI: semi-local mask (max_attn_len > 0), as in the forward kernel.
 // HAS_RAB: scores carry the relative bias rab[h, query - key + N - 1] (no gradient flows to it).
-template <bool SEMI, bool HAS_RAB>
+// PER_TOKEN: the output scale is a [T] vector; P and dS of query row m carry attn_scale[m].
+template <bool SEMI, bool HAS_RAB, bool PER_TOKEN>
 __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp) {
   const Params& p = bp.f;
   __shared__ __attribute__((aligned(1024))) unsigned short Ks0[BWD_BN * HD];
@@ -216,8 +218,8 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       constexpr int BUF = decltype(buf_tag)::value;
       const int k0 = it * BWD_BN;
       const int last = si.n - 1 - k0;
-      bwd_issue_rows(kgb + (size_t)k0 * row_bytes, row_bytes, last, BUF ? Ks1 : Ks0, lc, wave);
-      bwd_issue_rows(vgb + (size_t)k0 * row_bytes, row_bytes, last, BUF ? Vs1 : Vs0, lc, wave);
+      bwd_issue_rows<HAS_RAB>(kgb + (size_t)k0 * row_bytes, row_bytes, last, BUF ? Ks1 : Ks0, lc, wave);
+      bwd_issue_rows<HAS_RAB>(vgb + (size_t)k0 * row_bytes, row_bytes, last, BUF ? Vs1 : Vs0, lc, wave);
     };
 
     int it0 = 0;  // semi-local: key tiles below the first row's window are not walked
@@ -227,7 +229,11 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
 
     bf16x8 qf[8], gf[8];
     bwd_load_row_frags(p.q, (size_t)si.s + m, p.H, h, half, m < q_end, true, p.alpha * kLog2e, qf);
-    bwd_load_row_frags(bp.dout, (size_t)si.s + m, p.H, h, half, m < q_end, false, 1.0f, gf);
+    // a per-token output scale multiplies row m of P, hence row m of dS: fold it into this lane's
+    // dO row
+    constexpr bool per_token = PER_TOKEN;
+    const float row_scale = per_token ? p.attn_scale[si.s + min(m, si.n - 1)] : 1.0f;
+    bwd_load_row_frags(bp.dout, (size_t)si.s + m, p.H, h, half, m < q_end, per_token, row_scale, gf);
 
     f32x16 acc[4];
 #pragma unroll
@@ -337,7 +343,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
 
     // dQ^T accumulators -> dq[s + m, h, :]; element 4 rq + i of block db is column 32 db + 8 rq + 4 half + i
     if (m < q_end) {
-      const float oscale = p.alpha * bwd_output_scale(p);
+      const float oscale = per_token ? p.alpha : p.alpha * bwd_output_scale(p);
       unsigned short* orow = (unsigned short*)bp.dq + ((size_t)(si.s + m) * p.H + h) * HD;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
@@ -357,7 +363,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
 // ---------------------------------------------------------------------------------------------
 // dK, dV
 // ---------------------------------------------------------------------------------------------
-template <bool SEMI, bool HAS_RAB>
+template <bool SEMI, bool HAS_RAB, bool PER_TOKEN>
 __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
   const Params& p = bp.f;
   __shared__ __attribute__((aligned(1024))) unsigned short Qs0[BWD_BN * HD];
@@ -412,8 +418,8 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       constexpr int BUF = decltype(buf_tag)::value;
       const int m0 = it * BWD_BN;
       const int last = si.n - 1 - m0;
-      bwd_issue_rows(qgb + (size_t)m0 * row_bytes, row_bytes, last, BUF ? Qs1 : Qs0, lc, wave);
-      bwd_issue_rows(ggb + (size_t)m0 * row_bytes, row_bytes, last, BUF ? Gs1 : Gs0, lc, wave);
+      bwd_issue_rows<HAS_RAB>(qgb + (size_t)m0 * row_bytes, row_bytes, last, BUF ? Qs1 : Qs0, lc, wave);
+      bwd_issue_rows<HAS_RAB>(ggb + (size_t)m0 * row_bytes, row_bytes, last, BUF ? Gs1 : Gs0, lc, wave);
     };
 
     int it = t_first;
@@ -440,6 +446,12 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
         f32x16 s = zero, dp = zero;
         float bias[16];
         if (HAS_RAB) bwd_bias_block(rab_row, rab_w, m0 + qb32 * 32 + 4 * half - j + p.N - 1, 1, bias);
+        float ts[16];
+        if (PER_TOKEN) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            ts[r] = p.attn_scale[si.s + min(m0 + qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3), si.n - 1)];
+        }
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
           s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(qb, lc, qb32, kk), kf[kk], s, 0, 0, 0);
@@ -454,6 +466,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
           const float sv = u * kLn2;
           float pe = sv * sig;
           float g = dp[r] * (sig * (1.0f + sv * (1.0f - sig)));
+          if (PER_TOKEN) { pe *= ts[r]; g *= ts[r]; }
           if (MASKED) {
             const int m = m0 + qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
             const int idm = min(m, si.cap);
@@ -526,7 +539,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     }
 
     if (j < si.n) {
-      const float vscale = bwd_output_scale(p);
+      const float vscale = PER_TOKEN ? 1.0f : bwd_output_scale(p);
       const float kscale = p.alpha * vscale;
       unsigned short* krow = (unsigned short*)bp.dk + ((size_t)(si.s + j) * p.H + h) * HD;
       unsigned short* vrow = (unsigned short*)bp.dv + ((size_t)(si.s + j) * p.H + h) * HD;

@@ -206,6 +206,32 @@ def test_tiled_backward_with_score_bias(oracle, A, F, ctx):
     assert_grads_close(gotg, want, end, BF16_REL, "generic rab")
 
 
+@pytest.mark.parametrize("with_rab", [False, True])
+def test_tiled_backward_with_per_token_scale(oracle, with_rab):
+    """attn_scale as a [T] vector (row m of P carries attn_scale[m]) inside the tiled kernels; the
+    vector varies by 4x across tokens so that using one value for all rows fails."""
+    from recir_amd import _lib
+
+    lengths = [1, 63, 64, 65, 127, 128, 129, 0, 191, 257, 330, 90]
+    targets = [0, 3, 64, 1, 100, 0, 129, 0, 60, 2, 200, 90]
+    wl = _mid_workload(57, lengths, targets, 3)
+    g = torch.Generator().manual_seed(13)
+    dout = torch.randn(wl.T, wl.H, 128, generator=g).to(torch.bfloat16).float()
+    scale = (0.5 + 1.5 * torch.rand(wl.T, generator=g)) / 300
+    rab = torch.randn(wl.H, 2 * wl.max_seq_len - 1, generator=g) if with_rab else None
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                           attn_scale=scale.numpy(), rab=None if rab is None else rab.numpy(), contextual_seq_len=3)
+    got = run_hip_bwd(wl, dout, attn_scale=scale, rab=rab)
+    assert _lib.last_kernel() == ("bwd_tiled_d128_bf16_rab" if with_rab else "bwd_tiled_d128_bf16")
+    assert_grads_close(got, want, int(wl.seq_offsets[-1]), BF16_REL, "per-token scale")
+    flat = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                           attn_scale=np.float32(scale.mean().item()), rab=None if rab is None else rab.numpy(),
+                           contextual_seq_len=3)
+    assert error_stats(got[1], flat[1])["rel_fro"] > 5 * BF16_REL
+
+
 def test_config3_backward_tiled_agrees_with_generic():
     """Config 3 (bias + contextual prefix) at full size: tiled against generic kernels."""
     from recir_amd import _lib, ops
