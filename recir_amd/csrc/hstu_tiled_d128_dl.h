@@ -68,6 +68,12 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
 #ifndef HSTU_DL_PRIO
 #define HSTU_DL_PRIO 1  // wave priority while an MFMA is waiting to issue (0: leave it alone)
 #endif
+#ifndef HSTU_DL_RAB_SLOTS
+#define HSTU_DL_RAB_SLOTS 1  // the bias instantiations use the hand-placed slot schedule too
+#endif
+#ifndef HSTU_DL_B1
+#define HSTU_DL_B1 5  // slot in which the bias of the second score block is read (first used in slot 8)
+#endif
 #ifndef HSTU_DL_SLOTS
 #define HSTU_DL_SLOTS 1
 #endif
@@ -96,6 +102,7 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
 #endif
 template <bool HAS_RAB, bool FP8, bool SEMI>
 __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
+  constexpr bool ASM_COPY = HSTU_DL_ASM_COPY != 0;
   // The two pipeline stages are separate objects and every access names its stage at compile time:
   // the compiler then knows that an LDS read of one stage cannot alias the global -> LDS copies in
   // flight into the other, and does not wait for them.
@@ -224,13 +231,13 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           kr = kt;
           vr = vt;
         }
-#if HSTU_DL_ASM_COPY
-        if (!is_v) { if (!FP8) copy16(kr, ko, (unsigned)(size_t)&Kd[r0 * HD]); }
-        else copy16(vr, vo, (unsigned)(size_t)&Vd[r0 * HD]);
-#else
-        if (!is_v) { if (!FP8) __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)&Kd[r0 * HD], 16, 0, 0); }
-        else __builtin_amdgcn_global_load_lds((const unsigned*)(vr + vo), (lds_void*)&Vd[r0 * HD], 16, 0, 0);
-#endif
+        if constexpr (ASM_COPY) {
+          if (!is_v) { if (!FP8) copy16(kr, ko, (unsigned)(size_t)&Kd[r0 * HD]); }
+          else copy16(vr, vo, (unsigned)(size_t)&Vd[r0 * HD]);
+        } else {
+          if (!is_v) { if (!FP8) __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)&Kd[r0 * HD], 16, 0, 0); }
+          else __builtin_amdgcn_global_load_lds((const unsigned*)(vr + vo), (lds_void*)&Vd[r0 * HD], 16, 0, 0);
+        }
         return;
       }
       if (FP8) {
@@ -244,20 +251,25 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
             ko = (unsigned)min(r0 + ld8_row, last) * krow_bytes + (unsigned)((ld8_chunk ^ (((r0 + ld8_row) >> 1) & 7)) * 16);
             kr = kt;
           }
-#if HSTU_DL_ASM_COPY
-          copy16(kr, ko, (unsigned)(size_t)((char*)Kd + r0 * 128));
-#else
-          __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)((char*)Kd + r0 * 128), 16, 0, 0);
-#endif
+          if constexpr (ASM_COPY) copy16(kr, ko, (unsigned)(size_t)((char*)Kd + r0 * 128));
+          else __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)((char*)Kd + r0 * 128), 16, 0, 0);
         }
       }
-      if (HAS_RAB) {
-        // band of bias entries this (q tile, kv tile) can touch: index (m - j) + N - 1, staged
-        // pre-multiplied by log2(e); plain stores, ordered by the barrier that publishes the tile
-        int idx = q0 - k0 - (BN - 1) + p.N - 1 + tid;
-        idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
-        if (tid < BM + BN - 1) rabd[tid] = rabg[idx] * kLog2e;
-      }
+    };
+    // Band of bias entries a (query tile, key tile) pair can touch: index (m - j) + N - 1, staged
+    // pre-multiplied by log2(e) with plain stores, ordered by the barrier that publishes the tile.
+    // In two steps, so that the load's round trip passes under a tile's arithmetic: the load goes
+    // out before the tile's copies (the wait for it would otherwise wait for them too), the store
+    // follows at the end of the tile.
+    auto band_load = [&](int it) __attribute__((always_inline)) {
+      int idx = q0 - it * BN - (BN - 1) + p.N - 1 + tid;
+      idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
+      return rabg[idx];  // scaled in band_store: nothing may use the value before the tile's arithmetic is over
+    };
+    auto band_store = [&](auto buf_tag, float val) __attribute__((always_inline)) {
+      constexpr int BUF = decltype(buf_tag)::value;
+      asm volatile("" : "+v"(val));  // first use of the loaded value: the wait for it stays here
+      if (tid < BM + BN - 1) (BUF ? rabs1 : rabs0)[tid] = val * kLog2e;
     };
     auto issue_tile_as = [&](int it, auto buf_tag, auto whole_tag) __attribute__((always_inline)) {
 #pragma unroll
@@ -266,6 +278,13 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     auto issue_tile = [&](int it, auto buf_tag) __attribute__((always_inline)) {
       issue_tile_as(it, buf_tag, std::false_type{});
     };
+    // copies and band where nothing is there to overlap with (tiles this wave skips)
+    auto issue_tile_and_band = [&](int it, auto buf_tag) __attribute__((always_inline)) {
+      float band = 0.f;
+      if (HAS_RAB) band = band_load(it);
+      issue_tile(it, buf_tag);
+      if (HAS_RAB) band_store(buf_tag, band);
+    };
 
     // first tile in flight before anything else is waited for
     // semi-local: key tiles below the window of the workgroup's first row are not walked unless a
@@ -273,6 +292,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     int it0 = 0;
     if (SEMI && si.ctx_eff <= 0 && min(q_end - 1, si.cap) < si.tail0) it0 = max(min(q0, si.cap) - si.win, 0) / BN;
     int it = (has_skip && it0 >= skip_a) ? max(it0, skip_b) : it0;
+    float band_first = 0.f;  // stored once the Q rows are in, just before the first barrier
+    if (HAS_RAB && it < nkv) band_first = band_load(it);
     if (it < nkv) issue_tile(it, std::integral_constant<int, 0>{});
 
     // ---- Q fragments (B operand): lane holds row qw0 + l32 ----
@@ -384,7 +405,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         return __builtin_bit_cast(bf16x8, both);
       };
 #if HSTU_DL_SLOTS
-      if constexpr (!FP8 && !HAS_RAB && (FAST || HSTU_DL_SLOTS > 1)) {  // (mask and bias state leave this schedule too few registers)
+      if constexpr (!FP8 && (!HAS_RAB || HSTU_DL_RAB_SLOTS) && (FAST || HSTU_DL_SLOTS > 1)) {  // (mask state leaves this schedule too few registers)
         // Hand-placed schedule, one MFMA per slot with a scheduling fence after each:
         //   slots  0..7   S0 = K[0:32] Q^T            slots  8..15  S1 = K[32:64] Q^T
         //   slots 16..31  O^T[db] += V^T[db, s2] P^T[s2], key step s2 = (slot - 16) / 4, db = slot & 3
@@ -423,8 +444,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           for (int t = 0; t < 2; ++t) {
             const int r = 2 * e + t;
             const int jl = blk * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            float sv = sblk[blk][r];
-            if (HAS_RAB) sv += rabt[(m - q0) - jl + (BN - 1)];
+            const float sv = sblk[blk][r];  // the bias is already in there, see bias_block
             const float ex = __builtin_amdgcn_exp2f(-sv);
             float pv = sv * __builtin_amdgcn_rcpf(1.0f + ex);
             if (MASKED) {
@@ -440,6 +460,16 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           pw[blk][e] = __float_as_uint(sblk[blk][2 * e]) ^ __float_as_uint(sblk[blk][2 * e + 1]);
 #endif
         };
+        // The bias enters as the initial value of the score accumulators (no addition in the SiLU
+        // units, no register of its own): block 0 is read with the fragments that open the tile,
+        // block 1 three slots before its first MFMA (any earlier and it competes with the K
+        // fragments in flight).
+        auto bias_block = [&](int blk) __attribute__((always_inline)) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            sblk[blk][r] = rabt[(m - q0) - (blk * 32 + 8 * (r >> 2) + 4 * half + (r & 3)) + (BN - 1)];
+        };
+        if (HAS_RAB) bias_block(0);
 #pragma unroll
         for (int s = 0; s < 32; ++s)
           if (frag_req(s) < 0) F[s] = slot_frag(s);
@@ -451,7 +481,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           if constexpr (FAST) issue_part(nxt, other, std::true_type{}, part);
           else if (copy_next) issue_part(nxt, other, std::false_type{}, part);
         };
-        if (HAS_RAB) issue_slot(8);
+        // bias band of the next tile: loaded here, stored to LDS in the last slot
+        float band_next = 0.f;
+        if (HAS_RAB && copy_next) band_next = band_load(nxt);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 32; ++s) {
@@ -461,11 +493,12 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 #pragma unroll
           for (int t = s + 1; t < 32; ++t)
             if (frag_req(t) == s) F[t] = slot_frag(t);
+          if (HAS_RAB && s == HSTU_DL_B1) bias_block(1);
 #if HSTU_DL_PRIO
           __builtin_amdgcn_s_setprio(HSTU_DL_PRIO);
 #endif
           if (s < 16) {
-            sblk[s >> 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], qf[s & 7], (s & 7) == 0 ? zero : sblk[s >> 3], 0, 0, 0);
+            sblk[s >> 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], qf[s & 7], (!HAS_RAB && (s & 7) == 0) ? zero : sblk[s >> 3], 0, 0, 0);
           } else {
             const int s2 = pv_s2(s), db = pv_db(s);
             const u32x4 w = {pw[s2 >> 1][4 * (s2 & 1) + 0], pw[s2 >> 1][4 * (s2 & 1) + 1], pw[s2 >> 1][4 * (s2 & 1) + 2],
@@ -477,6 +510,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 #endif
           if (s >= HSTU_DL_C0 && s < HSTU_DL_C0 + 8 * HSTU_DL_CSTEP && (s - HSTU_DL_C0) % HSTU_DL_CSTEP == 0) issue_slot((s - HSTU_DL_C0) / HSTU_DL_CSTEP);
           if (s >= HSTU_DL_U0 && s < HSTU_DL_U0 + 16) silu_unit(s - HSTU_DL_U0);
+          if (HAS_RAB && s == 31 && copy_next) band_store(other, band_next);
           __builtin_amdgcn_sched_barrier(0);
         }
         return;
@@ -484,6 +518,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 #endif
       f32x16 s0, s1;
       bf16x8 pb0, pb1, pb2, pb3;
+      float band_nxt = 0.f;
+      if (HAS_RAB && (FAST || nxt < nkv)) band_nxt = band_load(nxt);
       // The 32 MFMAs of the block run as eight groups of four.  The LDS fragments of group g + 1 are
       // fetched while group g computes (two alternating sets of four registers-quads), so that no
       // MFMA waits for an LDS round trip; only the reads that open the tile are exposed.
@@ -594,6 +630,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       mfma_group(6, fa);
       __builtin_amdgcn_sched_barrier(0);
       mfma_group(7, fb);
+      if (HAS_RAB && (FAST || nxt < nkv)) band_store(other, band_nxt);
     };
 
     auto compute_tile = [&](int it, auto buf_tag, int nxt) __attribute__((always_inline)) {
@@ -608,7 +645,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         any_kept = wave_has_rows && ((k0 <= m_hi && k1 > m_lo) || (k0 < si.ctx_eff) ||
                                      (k0 < idhi_w && (wave_has_tail || k1 > idlo_w - si.win)));
       if (!any_kept) {
-        if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, BUF ^ 1>{});  // this wave still copies its share
+        if (nxt < nkv) issue_tile_and_band(nxt, std::integral_constant<int, BUF ^ 1>{});  // this wave still copies its share
         return;
       }
       bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
@@ -634,6 +671,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     long long trace_c2 = clock64();
 #endif
     if (it < nkv) {
+      if (HAS_RAB) band_store(std::integral_constant<int, 0>{}, band_first);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       HSTU_ITEM_STAMP(2);
