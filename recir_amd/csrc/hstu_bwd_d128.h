@@ -203,6 +203,10 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     const bool tail_row = idm >= si.tail0;
     const int idlo_w = min(m_lo, si.cap), idhi_w = min(m_hi, si.cap);
     const bool wave_has_tail = idhi_w >= si.tail0;
+    // causal mask of this lane's row as bounds on the key index (key k0 + 4 half + c, c a
+    // compile-time constant per element): kept iff j < max(min(idm, n), min(ctx_eff, n)) or j == m
+    const int mk_eq = (m < si.n ? m : -0x40000000) - 4 * half;
+    const int mk_top = max(min(idm, si.n), min(si.ctx_eff, si.n)) - 4 * half;
 
     // key tiles [0, nkv) minus the run [skip_a, skip_b) that holds only target keys off this query
     // tile's diagonal (and no contextual key): the tiles the forward walks
@@ -285,9 +289,10 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
           const float sv = u * kLn2;
           float g = dpt[r] * (sig * (1.0f + sv * (1.0f - sig)));
           if (MASKED) {
-            const int j = k0 + kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            const int c = kvb * 32 + 8 * (r >> 2) + (r & 3);
+            const int j = k0 + 4 * half + c;
             const bool kp = SEMI ? ((m == j) | ((j < idm) & ((idm - j <= si.win) | tail_row)) | (j < si.ctx_eff)) & (j < si.n)
-                                 : ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
+                                 : ((c < mk_top - k0) | (c == mk_eq - k0));
             g = kp ? g : 0.f;
           }
           ds[r] = g;
@@ -403,6 +408,12 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     const int j_lo = jw0;
     const int j_hi = min(jw0 + 31, si.n - 1);
     const bool wave_has_rows = j_lo < si.n;
+    // causal mask of this lane's key as bounds on the query index (row m0 + 4 half + c): a contextual
+    // key is seen by every row, a history key by the rows from its own on, a target key by its own
+    // row only; rows end at n
+    const int mk_from = (j < si.ctx_eff ? 0 : (j < si.cap ? j : 0x40000000)) - 4 * half;
+    const int mk_own = j - 4 * half;
+    const int mk_end = si.n - 4 * half;
 
     // Query tiles that see a key of [j0, j0 + 128): from the diagonal (from 0 when the tile holds a
     // contextual key) to the end of the sequence when the tile holds a history key, else through
@@ -468,10 +479,11 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
           float g = dp[r] * (sig * (1.0f + sv * (1.0f - sig)));
           if (PER_TOKEN) { pe *= ts[r]; g *= ts[r]; }
           if (MASKED) {
-            const int m = m0 + qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            const int c = qb32 * 32 + 8 * (r >> 2) + (r & 3);
+            const int m = m0 + 4 * half + c;
             const int idm = min(m, si.cap);
             const bool kp = SEMI ? ((m == j) | ((j < idm) & ((idm - j <= si.win) | (idm >= si.tail0))) | (j < si.ctx_eff)) & (m < si.n)
-                                 : ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (m < si.n);
+                                 : ((c >= mk_from - m0) | (c == mk_own - m0)) & (c < mk_end - m0);
             pe = kp ? pe : 0.f;
             g = kp ? g : 0.f;
           }

@@ -190,6 +190,21 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     const bool tail_row = idm >= si.tail0;
     const int idlo_w = min(m_lo, si.cap), idhi_w = min(m_hi, si.cap);
     const bool wave_has_tail = idhi_w >= si.tail0;
+    // Causal mask of this lane's row as bounds on the key index: key j is kept iff
+    //   j < max(min(idm, n), min(ctx_eff, n))  or  j == m (and m < n).
+    // Element r of a score block is key k0 + 4 half + c with a compile-time c, so the bounds are
+    // kept relative to 4 half and, per tile, to k0: two comparisons against constants per element
+    // instead of the predicate's five.  (The semi-local predicate in the same form needs four and
+    // measured slower than the direct one.)
+    const int mk_eq = (m < si.n ? m : -0x40000000) - 4 * half;
+    const int mk_top = max(min(idm, si.n), min(si.ctx_eff, si.n)) - 4 * half;
+    auto kept = [&](int k0, int c) __attribute__((always_inline)) {
+      if (SEMI) {
+        const int j = k0 + 4 * half + c;
+        return (bool)(((m == j) | ((j < idm) & ((idm - j <= si.win) | tail_row)) | (j < si.ctx_eff)) & (j < si.n));
+      }
+      return (bool)((c < mk_top - k0) | (c == mk_eq - k0));
+    };
 
     // key tiles [0, nkv) minus the run [skip_a, skip_b) that holds only target keys off this query
     // tile's diagonal (and no contextual key)
@@ -353,13 +368,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         if (HAS_RAB) s += rabt[(m - q0) - jl + (BN - 1)];
         const float ex = __builtin_amdgcn_exp2f(-s);
         float pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
-        if (MASKED) {
-          const int j = k0 + jl;
-          // branch-free keep(m, j) & (j < n)
-          const bool kp = SEMI ? ((m == j) | ((j < idm) & ((idm - j <= si.win) | tail_row)) | (j < si.ctx_eff)) & (j < si.n)
-                               : ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
-          pe = kp ? pe : 0.f;
-        }
+        if (MASKED) pe = kept(k0, kvb * 32 + 8 * (r >> 2) + (r & 3)) ? pe : 0.f;
         pv[r] = pe;
       }
       u32x4 w0, w1;
@@ -447,12 +456,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
             const float sv = sblk[blk][r];  // the bias is already in there, see bias_block
             const float ex = __builtin_amdgcn_exp2f(-sv);
             float pv = sv * __builtin_amdgcn_rcpf(1.0f + ex);
-            if (MASKED) {
-              const int j = k0 + jl;
-              const bool kp = SEMI ? ((m == j) | ((j < idm) & ((idm - j <= si.win) | tail_row)) | (j < si.ctx_eff)) & (j < si.n)
-                                   : ((m == j) | ((m >= j) & (j < si.cap)) | (j < si.ctx_eff)) & (j < si.n);
-              pv = kp ? pv : 0.f;
-            }
+            if (MASKED) pv = kept(k0, blk * 32 + 8 * (r >> 2) + (r & 3)) ? pv : 0.f;
             pe[t] = pv;
           }
           pw[blk][e] = pack_bf16x2(pe[0], pe[1]);
