@@ -303,3 +303,58 @@ def test_semilocal_backward_matches_oracle(oracle, A, F, ctx):
     with ops.force_kernel(ops.KERNEL_GENERIC):
         gotg = run_hip_bwd(wl, dout)
     assert_grads_close(gotg, want, end, BF16_REL, f"generic A{A} F{F}")
+
+
+def _random_case(seed):
+    """A seeded draw over everything the tiled kernels branch on: batch shape, lengths around tile
+    boundaries, target counts, contextual prefix, semi-local window, bias, kind of output scale."""
+    from recir_amd.workloads import make_jagged
+
+    rng = np.random.default_rng(1000 + seed)
+    B = int(rng.integers(1, 7))
+    edges = np.array([0, 1, 31, 32, 33, 63, 64, 65, 127, 128, 129, 191, 192, 255, 256, 257])
+    lengths = [int(rng.choice(edges)) if rng.random() < 0.5 else int(rng.integers(0, 420)) for _ in range(B)]
+    targets = [int(rng.integers(0, n + 1)) if rng.random() < 0.6 else 0 for n in lengths]
+    H = int(rng.integers(1, 4))
+    ctx = int(rng.choice([0, 0, 3, 70]))
+    A = int(rng.choice([0, 0, 33, 128]))
+    F = int(rng.choice([0, 40])) if A else 0
+    with_rab = bool(rng.random() < 0.4)
+    scale_kind = str(rng.choice(["default", "scalar", "per_token"]))
+    N = max(max(lengths), 1) + int(rng.integers(0, 9))
+    wl = make_jagged(lengths, targets, H, 128, 128, max_seq_len=N, alpha=1.0 / 128, dtype="bf16", seed=seed,
+                     contextual_seq_len=ctx, tail_rows=int(rng.integers(0, 4)), max_attn_len=A, full_attn_size=F,
+                     with_rab=with_rab, rab_std=0.5)
+    g = torch.Generator().manual_seed(seed)
+    scale = None
+    if scale_kind == "scalar":
+        scale = torch.tensor(0.01)
+    elif scale_kind == "per_token":
+        scale = (0.5 + torch.rand(wl.T, generator=g)) / 100
+    dout = torch.randn(wl.T, wl.H, 128, generator=g).to(torch.bfloat16).float()
+    return wl, scale, dout
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_randomized_cases_forward_and_backward(oracle, seed):
+    """Forward and backward of the tiled kernels against the oracle on seeded random cases."""
+    from recir_amd import _lib
+    from tests.parity_util import assert_bf16_close, run_hip, run_oracle
+
+    wl, scale, dout = _random_case(seed)
+    what = (f"seed {seed}: lengths {wl.lengths.tolist()} targets {wl.num_targets.tolist()} H {wl.H} ctx "
+            f"{wl.contextual_seq_len} A {wl.max_attn_len} F {wl.full_attn_size} rab {wl.rab is not None}")
+    out = run_hip(wl, attn_scale=scale)
+    if wl.T:
+        assert _lib.last_kernel().startswith("tiled_d128"), what
+    assert_bf16_close(out, run_oracle(oracle, wl, attn_scale=scale), what)
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                           attn_scale=_scale_np(scale), rab=None if wl.rab is None else wl.rab.numpy(),
+                           contextual_seq_len=wl.contextual_seq_len, max_attn_len=wl.max_attn_len,
+                           full_attn_size=wl.full_attn_size)
+    got = run_hip_bwd(wl, dout, attn_scale=scale, rab=wl.rab)
+    if wl.T:
+        assert _lib.last_kernel().startswith("bwd_tiled_d128"), what
+    if np.abs(want[0]).max() > 0:
+        assert_grads_close(got, want, int(wl.seq_offsets[-1]), BF16_REL, what)
