@@ -369,6 +369,32 @@ def test_fp8_small_case(oracle, with_rab):
     assert not out[int(wl.seq_offsets[-1]):].any()
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_fp8_randomized_cases(oracle, seed):
+    """The fp8 q/k kernel on seeded random cases (tile-boundary lengths, targets, prefix, window,
+    bias), against the oracle on the same quantised operands."""
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    rng = np.random.default_rng(2000 + seed)
+    B = int(rng.integers(1, 6))
+    edges = np.array([0, 1, 31, 32, 33, 63, 64, 65, 127, 128, 129, 191, 192, 255, 256, 257])
+    lengths = [int(rng.choice(edges)) if rng.random() < 0.5 else int(rng.integers(0, 420)) for _ in range(B)]
+    targets = [int(rng.integers(0, n + 1)) if rng.random() < 0.6 else 0 for n in lengths]
+    A = int(rng.choice([0, 0, 33, 128]))
+    wl = make_jagged(lengths, targets, int(rng.integers(1, 4)), 128, 128, max_seq_len=max(max(lengths), 1) + 3,
+                     alpha=1.0 / 128, dtype="fp8", seed=seed, contextual_seq_len=int(rng.choice([0, 0, 3, 70])),
+                     tail_rows=int(rng.integers(0, 4)), max_attn_len=A, full_attn_size=int(rng.choice([0, 40])) if A else 0,
+                     with_rab=bool(rng.random() < 0.4), rab_std=0.3)
+    what = (f"seed {seed}: lengths {lengths} targets {targets} H {wl.H} ctx {wl.contextual_seq_len} "
+            f"A {wl.max_attn_len} F {wl.full_attn_size} rab {wl.rab is not None}")
+    out = run_hip(wl, fp8=True)
+    if wl.T:
+        assert _lib.last_kernel().startswith("tiled_d128_fp8qk"), what
+    assert_bf16_close(out, _fp8_reference(oracle, wl), what)
+    assert not out[int(wl.seq_offsets[-1]):].any(), what
+
+
 def test_config5_fp8_matches_oracle(oracle):
     from recir_amd.workloads import make_config
 
