@@ -13,6 +13,7 @@ from .ops import (  # noqa: F401
     jagged_hstu_attention_fp8,
     quantize_e4m3_per_head,
     register_swaps,
+    set_plan_cache,
     hstu_attention_matcher,
     attention_via_fp8,
     fp8_attention_region,
@@ -42,6 +43,7 @@ __all__ = [
     "jagged_hstu_attention_fp8",
     "quantize_e4m3_per_head",
     "register_swaps",
+    "set_plan_cache",
     "hstu_attention_matcher",
     "attention_via_fp8",
     "fp8_attention_region",

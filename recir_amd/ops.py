@@ -14,6 +14,7 @@ There is deliberately no CPU or eager implementation: a CPU tensor, or a missing
 """
 from __future__ import annotations
 
+import collections
 import math
 from typing import Optional, Tuple
 
@@ -171,6 +172,47 @@ def _check_window(max_attn_len, full_attn_size):
         raise ValueError("max_attn_len and full_attn_size must be non-negative")
 
 
+# Work lists depend only on the sequence layout, which the layers of one model step share
+# (cf. RECIR_HSTU_FLAG_REUSE_PLAN): keep the workspace of the last few layouts and let later calls
+# with the very same offset tensors skip the list construction.  An entry holds the tensors it was
+# built from, so their identity cannot be recycled while it lives, and it is valid only while their
+# version counters stand where they stood; a layout changed behind torch's back (a foreign kernel
+# writing into the offsets) is not seen -- switch the cache off for such callers.
+_PLAN_CACHE_ENTRIES = 8
+_plan_cache = collections.OrderedDict()
+_plan_cache_enabled = True
+plan_cache_stats = {"hits": 0, "misses": 0}
+
+
+def set_plan_cache(enabled: bool) -> None:
+    """Enable or disable the reuse of work lists between calls that pass the same offset tensors."""
+    global _plan_cache_enabled
+    _plan_cache_enabled = bool(enabled)
+    _plan_cache.clear()
+
+
+def _workspace(kind, seq_offsets, num_targets, layout, ws_bytes, dev, stream):
+    """Workspace for one launch and the flag to pass with it: a cached one whose lists are valid
+    (flag = reuse), or a new one (flag = 0) that is remembered for the next call."""
+    size = max(int(ws_bytes), 16)
+    # under stream capture a launch is recorded, not run: lists "built" there do not exist yet
+    if not _plan_cache_enabled or torch.cuda.is_current_stream_capturing():
+        return torch.empty((size,), dtype=torch.uint8, device=dev), 0, None
+    key = (kind, id(seq_offsets), seq_offsets._version, id(num_targets),
+           None if num_targets is None else num_targets._version, layout, dev.index, stream, size)
+    hit = _plan_cache.get(key)
+    if hit is not None and hit[0] is seq_offsets and hit[1] is num_targets:
+        _plan_cache.move_to_end(key)
+        plan_cache_stats["hits"] += 1
+        return hit[2], _lib.FLAG_REUSE_PLAN, key
+    plan_cache_stats["misses"] += 1
+    ws = torch.empty((size,), dtype=torch.uint8, device=dev)
+    _plan_cache[key] = (seq_offsets, num_targets, ws)
+    while len(_plan_cache) > _PLAN_CACHE_ENTRIES:
+        _plan_cache.popitem(last=False)
+    return ws, 0, key
+
+
 def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale, N, alpha,
             contextual_seq_len, dtype_code, max_attn_len=0, full_attn_size=0) -> torch.Tensor:
     _check_window(max_attn_len, full_attn_size)
@@ -185,14 +227,18 @@ def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale
     if T == 0:
         return out
     ws_bytes = L.recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype_code)
-    ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
+    # what the lists depend on besides the offset tensors themselves
+    layout = (T, B, H, Dqk, Dv, dtype_code, int(N), int(contextual_seq_len), int(max_attn_len), int(full_attn_size), flags)
+    ws, reuse, key = _workspace("fwd", seq_offsets, num_targets, layout, ws_bytes, dev, stream)
     with torch.cuda.device(dev):
         rc = L.recir_hstu_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(off), _ptr(nt), _ptr(rb),
                                    _ptr(sc), _ptr(q_scale), _ptr(k_scale), T, B, H, Dqk, Dv, int(N),
                                    int(contextual_seq_len), int(max_attn_len), int(full_attn_size),
-                                   float(alpha), dtype_code, flags, _ptr(ws), ws.numel(), stream)
+                                   float(alpha), dtype_code, flags | reuse, _ptr(ws), ws.numel(), stream)
     if rc != 0:
+        if key is not None:
+            _plan_cache.pop(key, None)
         _raise_status("recir_hstu_attn_fwd", rc)
     return out
 
@@ -229,14 +275,17 @@ def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, c
     if T == 0:
         return dq, dk, dv
     ws_bytes = L.recir_hstu_attn_bwd_workspace_bytes(T, B, H, Dqk, Dv, code)
-    ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
+    layout = (T, B, H, Dqk, Dv, code, int(N), int(contextual_seq_len), int(max_attn_len), int(full_attn_size), flags)
+    ws, reuse, key = _workspace("bwd", seq_offsets, num_targets, layout, ws_bytes, dev, stream)
     with torch.cuda.device(dev):
         rc = L.recir_hstu_attn_bwd(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv),
                                    _ptr(off), _ptr(nt), _ptr(rb), _ptr(sc), T, B, H, Dqk, Dv, int(N),
                                    int(contextual_seq_len), int(max_attn_len), int(full_attn_size),
-                                   float(alpha), code, flags, _ptr(ws), ws.numel(), stream)
+                                   float(alpha), code, flags | reuse, _ptr(ws), ws.numel(), stream)
     if rc != 0:
+        if key is not None:
+            _plan_cache.pop(key, None)
         _raise_status("recir_hstu_attn_bwd", rc)
     return dq, dk, dv
 

@@ -286,6 +286,48 @@ def test_sequences_longer_than_max_seq_len_do_not_break_the_work_list(oracle):
     assert_bf16_close(out, run_oracle(oracle, wl), "n > N")
 
 
+def test_work_lists_are_reused_for_the_same_offset_tensors_and_rebuilt_when_they_change(oracle):
+    """The operator keeps the work lists of a layout and reuses them while the caller passes the
+    very same offset tensors unchanged (the layers of one step); an in-place change of the offsets
+    (version counter) or other tensors build new lists."""
+    import recir_amd
+    from recir_amd import ops
+    from recir_amd.workloads import make_jagged
+
+    recir_amd.set_plan_cache(True)  # also empties it
+    wl = make_jagged([300, 129, 64, 1, 0, 517], [40, 129, 0, 0, 0, 6], 2, 128, 128, max_seq_len=600,
+                     alpha=1.0 / 128, dtype="bf16", seed=31)
+    q, k, v, off, nt = to_device(wl)
+    kw = dict(max_seq_len=wl.max_seq_len, alpha=wl.alpha)
+    before = dict(ops.plan_cache_stats)
+    a = recir_amd.jagged_hstu_attention(q, k, v, off, nt, **kw)
+    b = recir_amd.jagged_hstu_attention(q, k, v, off, nt, **kw)      # same tensors: lists reused
+    c = recir_amd.jagged_hstu_attention(v, q, k, off, nt, **kw)      # another layer's q, k, v
+    assert ops.plan_cache_stats["misses"] - before["misses"] == 1
+    assert ops.plan_cache_stats["hits"] - before["hits"] == 2
+    assert torch.equal(a, b)
+    assert_bf16_close(a, run_oracle(oracle, wl), "first call")
+    assert_bf16_close(c, oracle.attn_fwd(wl.v.numpy(), wl.q.numpy(), wl.k.numpy(), wl.seq_offsets.numpy(),
+                                         wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha), "reused")
+    # the same tensor objects with another layout written into them
+    wl2 = make_jagged([100, 400, 3, 250, 200, 58], [0, 10, 3, 0, 100, 1], 2, 128, 128, max_seq_len=600,
+                      alpha=1.0 / 128, dtype="bf16", seed=31)
+    assert wl2.T == wl.T
+    off.copy_(wl2.seq_offsets.to(off.device))
+    nt.copy_(wl2.num_targets.to(nt.device))
+    d = recir_amd.jagged_hstu_attention(q, k, v, off, nt, **kw)
+    assert ops.plan_cache_stats["misses"] - before["misses"] == 2
+    assert_bf16_close(d, oracle.attn_fwd(wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl2.seq_offsets.numpy(),
+                                         wl2.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha),
+                      "after an in-place change of the offsets")
+    # switched off: every call builds its lists
+    recir_amd.set_plan_cache(False)
+    e = recir_amd.jagged_hstu_attention(q, k, v, off, nt, **kw)
+    assert torch.equal(d, e)
+    assert ops.plan_cache_stats["misses"] - before["misses"] == 2 and ops.plan_cache_stats["hits"] - before["hits"] == 2
+    recir_amd.set_plan_cache(True)
+
+
 def test_rab_zero_is_identical_to_no_rab():
     from recir_amd.workloads import make_jagged
 
