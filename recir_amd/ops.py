@@ -198,8 +198,11 @@ def _workspace(kind, seq_offsets, num_targets, layout, ws_bytes, dev, stream):
     # under stream capture a launch is recorded, not run: lists "built" there do not exist yet
     if not _plan_cache_enabled or torch.cuda.is_current_stream_capturing():
         return torch.empty((size,), dtype=torch.uint8, device=dev), 0, None
-    key = (kind, id(seq_offsets), seq_offsets._version, id(num_targets),
-           None if num_targets is None else num_targets._version, layout, dev.index, stream, size)
+    try:
+        versions = (seq_offsets._version, None if num_targets is None else num_targets._version)
+    except RuntimeError:  # inference tensors carry no version counter: nothing to validate an entry with
+        return torch.empty((size,), dtype=torch.uint8, device=dev), 0, None
+    key = (kind, id(seq_offsets), id(num_targets), versions, layout, dev.index, stream, size)
     hit = _plan_cache.get(key)
     if hit is not None and hit[0] is seq_offsets and hit[1] is num_targets:
         _plan_cache.move_to_end(key)

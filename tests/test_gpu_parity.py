@@ -320,6 +320,13 @@ def test_work_lists_are_reused_for_the_same_offset_tensors_and_rebuilt_when_they
     assert_bf16_close(d, oracle.attn_fwd(wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl2.seq_offsets.numpy(),
                                          wl2.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha),
                       "after an in-place change of the offsets")
+    # tensors made under inference mode have no version counter: never cached, still right
+    with torch.inference_mode():
+        off_i, nt_i = off.clone(), nt.clone()
+        f1 = recir_amd.jagged_hstu_attention(q, k, v, off_i, nt_i, **kw)
+        f2 = recir_amd.jagged_hstu_attention(q, k, v, off_i, nt_i, **kw)
+    assert torch.equal(f1, d) and torch.equal(f2, d)
+    assert ops.plan_cache_stats["misses"] - before["misses"] == 2 and ops.plan_cache_stats["hits"] - before["hits"] == 2
     # switched off: every call builds its lists
     recir_amd.set_plan_cache(False)
     e = recir_amd.jagged_hstu_attention(q, k, v, off, nt, **kw)
