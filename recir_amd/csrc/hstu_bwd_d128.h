@@ -140,17 +140,23 @@ __device__ __forceinline__ float bwd_output_scale(const Params& p) {
   return p.attn_scale ? p.attn_scale[0] : 1.0f / (float)p.N;
 }
 
-// Score-bias entries of one 32 x 32 block for this lane: element r sits at index
-// base + step (8 (r / 4) + r % 4) of the head's row of rab (index = query - key + N - 1, clamped to
-// the row as in the forward), step = -1 when the block's elements run over keys, +1 over queries.
-// The table is small (H (2N - 1) floats) and stays in the caches; the loads are issued before the
-// products of the block and consumed after them.
-__device__ __forceinline__ void bwd_bias_block(const float* __restrict__ rab_row, int rab_w, int base, int step, float (&b)[16]) {
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int idx = base + step * (8 * (r >> 2) + (r & 3));
-    b[r] = rab_row[min(max(idx, 0), rab_w - 1)];
-  }
+// Score bias in the tiled kernels.  The copies of a tile are assembly the compiler cannot count, so
+// every wait it inserts for a load of its own waits for the copies in flight as well: bias values
+// fetched from global memory inside a tile body would expose a copy round trip per tile.  Instead
+// the 191 entries rab[h, m - j + N - 1] one (128-row, 64-row) tile pair can touch are staged in LDS,
+// two stages like the tiles: the load goes out before the tile's copies, the store (scaled by
+// log2(e), index clamped to the row) follows at the end of the tile, where everything is waited for
+// anyway; the scores start at the bias (LDS reads straight into the accumulator).
+constexpr int BWD_BAND = BWD_BM + BWD_BN;  // 191 used
+__device__ __forceinline__ float bwd_band_load(const float* __restrict__ rab_row, int rab_w, int first_idx, int tid) {
+  return rab_row[min(max(first_idx + tid, 0), rab_w - 1)];
+}
+// REVERSED: entry 190 - i holds index first + i, for the kernel whose elements run over keys (the
+// index falls with the key): a lane's elements then sit at ascending addresses.
+template <bool REVERSED>
+__device__ __forceinline__ void bwd_band_store(float* band, float val, int tid) {
+  asm volatile("" : "+v"(val));  // first use of the loaded value: the wait for it stays here
+  if (tid < BWD_BAND - 1) band[REVERSED ? (BWD_BAND - 2) - tid : tid] = val * kLog2e;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -166,6 +172,8 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
   __shared__ __attribute__((aligned(1024))) unsigned short Ks1[BWD_BN * HD];
   __shared__ __attribute__((aligned(1024))) unsigned short Vs0[BWD_BN * HD];
   __shared__ __attribute__((aligned(1024))) unsigned short Vs1[BWD_BN * HD];
+  __shared__ float band0[HAS_RAB ? BWD_BAND : 1];
+  __shared__ float band1[HAS_RAB ? BWD_BAND : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -226,9 +234,21 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       bwd_issue_rows<HAS_RAB>(vgb + (size_t)k0 * row_bytes, row_bytes, last, BUF ? Vs1 : Vs0, lc, wave);
     };
 
+    // The band is staged reversed: the entry for this lane's row and the key at offset 4 half + c of
+    // a tile is at byte 4 (127 - (m - q0) + 4 half + c) of the stage, ascending with c.  The lane
+    // part is made opaque to the compiler, which otherwise forms an address register per pair of
+    // elements and spills them.
+    unsigned band_lane = 4u * (unsigned)(127 - (m - q0) + 4 * half);
+    asm volatile("" : "+v"(band_lane));
+    // bias band of key tile t: entry i is rab index q0 - 64 t - 63 + N - 1 + i
+    auto band_of = [&](int t) __attribute__((always_inline)) {
+      return bwd_band_load(rab_row, rab_w, q0 - t * BWD_BN - (BWD_BN - 1) + p.N - 1, tid);
+    };
     int it0 = 0;  // semi-local: key tiles below the first row's window are not walked
     if (SEMI && si.ctx_eff <= 0 && min(q_end - 1, si.cap) < si.tail0) it0 = max(min(q0, si.cap) - si.win, 0) / BWD_BN;
     int it = (has_skip && it0 >= skip_a) ? max(it0, skip_b) : it0;
+    float band_first = 0.f;
+    if (HAS_RAB && it < nkv) band_first = band_of(it);
     if (it < nkv) issue_tile(it, std::integral_constant<int, 0>{});
 
     bf16x8 qf[8], gf[8];
@@ -256,18 +276,11 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       constexpr int BUF = decltype(buf_tag)::value;
       const char* kb = (const char*)(BUF ? Ks1 : Ks0);
       const char* vb = (const char*)(BUF ? Vs1 : Vs0);
+      const unsigned band_addr = (unsigned)(size_t)(BUF ? band1 : band0) + band_lane;  // LDS byte address
       const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kvb = 0; kvb < 2; ++kvb) {
         f32x16 st = zero, dpt = zero;
-        if (HAS_RAB) {
-          // the bias enters as the initial value of the score accumulator: no register lives across
-          // the products for it (this kernel runs at its register limit)
-          float bias[16];
-          bwd_bias_block(rab_row, rab_w, m - (k0 + kvb * 32 + 4 * half) + p.N - 1, -1, bias);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) st[r] = bias[r] * kLog2e;
-        }
         // phases are fenced so that the fragment reads of one are not hoisted over the previous one
         // (keeps the live registers within the two-waves-per-SIMD budget)
         __builtin_amdgcn_sched_barrier(0);
@@ -284,7 +297,9 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
         float ds[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float u = st[r];
+          // (the bias is added here, not taken as the accumulator's start: by now the fragment
+          // registers of the products are free, before them the kernel is at its register limit)
+          const float u = HAS_RAB ? st[r] + *(lds_cfloat*)(band_addr + 4u * (unsigned)(kvb * 32 + 8 * (r >> 2) + (r & 3))) : st[r];
           const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
           const float sv = u * kLn2;
           float g = dpt[r] * (sig * (1.0f + sv * (1.0f - sig)));
@@ -330,19 +345,25 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     };
 
     // two tiles per trip so that the stage index is a compile-time constant
+    if (HAS_RAB && it < nkv) bwd_band_store<true>(band0, band_first, tid);
     while (it < nkv) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile `it` have landed
       __syncthreads();                                   // everybody's; the other stage is free again
       int nxt = next_tile(it);
+      float band_nxt = 0.f;
+      if (HAS_RAB && nxt < nkv) band_nxt = band_of(nxt);
       if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, 1>{});
       compute_tile(it, std::integral_constant<int, 0>{});
+      if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band1, band_nxt, tid);
       it = nxt;
       if (it >= nkv) break;
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       nxt = next_tile(it);
+      if (HAS_RAB && nxt < nkv) band_nxt = band_of(nxt);
       if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, 0>{});
       compute_tile(it, std::integral_constant<int, 1>{});
+      if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band0, band_nxt, tid);
       it = nxt;
     }
 
@@ -375,6 +396,8 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
   __shared__ __attribute__((aligned(1024))) unsigned short Qs1[BWD_BN * HD];
   __shared__ __attribute__((aligned(1024))) unsigned short Gs0[BWD_BN * HD];
   __shared__ __attribute__((aligned(1024))) unsigned short Gs1[BWD_BN * HD];
+  __shared__ float band0[HAS_RAB ? BWD_BAND : 1];
+  __shared__ float band1[HAS_RAB ? BWD_BAND : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -433,7 +456,13 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       bwd_issue_rows<HAS_RAB>(ggb + (size_t)m0 * row_bytes, row_bytes, last, BUF ? Gs1 : Gs0, lc, wave);
     };
 
+    // bias band of query tile t: entry i is rab index 64 t - j0 - 127 + N - 1 + i
+    auto band_of = [&](int t) __attribute__((always_inline)) {
+      return bwd_band_load(rab_row, rab_w, t * BWD_BN - j0 - (BWD_BM - 1) + p.N - 1, tid);
+    };
     int it = t_first;
+    float band_first = 0.f;
+    if (HAS_RAB && it < nq) band_first = band_of(it);
     if (it < nq) issue_tile(it, std::integral_constant<int, 0>{});
 
     bf16x8 kf[8], vf[8];
@@ -451,12 +480,16 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       constexpr int BUF = decltype(buf_tag)::value;
       const char* qb = (const char*)(BUF ? Qs1 : Qs0);
       const char* gb = (const char*)(BUF ? Gs1 : Gs0);
+      const float* bandt = BUF ? band1 : band0;
       const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int qb32 = 0; qb32 < 2; ++qb32) {
         f32x16 s = zero, dp = zero;
-        float bias[16];
-        if (HAS_RAB) bwd_bias_block(rab_row, rab_w, m0 + qb32 * 32 + 4 * half - j + p.N - 1, 1, bias);
+        if (HAS_RAB) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            s[r] = bandt[(qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3)) - (j - j0) + (BWD_BM - 1)];
+        }
         float ts[16];
         if (PER_TOKEN) {
 #pragma unroll
@@ -472,7 +505,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
         float pv[16], ds[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float u = HAS_RAB ? fmaf(bias[r], kLog2e, s[r]) : s[r];
+          const float u = s[r];
           const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
           const float sv = u * kLn2;
           float pe = sv * sig;
@@ -534,19 +567,25 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       else tile_body(std::true_type{}, buf_tag, m0);
     };
 
+    if (HAS_RAB && it < nq) bwd_band_store<false>(band0, band_first, tid);
     while (it < nq) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       int nxt = it + 1;
+      float band_nxt = 0.f;
+      if (HAS_RAB && nxt < nq) band_nxt = band_of(nxt);
       if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 1>{});
       compute_tile(it, std::integral_constant<int, 0>{});
+      if (HAS_RAB && nxt < nq) bwd_band_store<false>(band1, band_nxt, tid);
       it = nxt;
       if (it >= nq) break;
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       nxt = it + 1;
+      if (HAS_RAB && nxt < nq) band_nxt = band_of(nxt);
       if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 0>{});
       compute_tile(it, std::integral_constant<int, 1>{});
+      if (HAS_RAB && nxt < nq) bwd_band_store<false>(band0, band_nxt, tid);
       it = nxt;
     }
 

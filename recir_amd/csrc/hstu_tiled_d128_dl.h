@@ -36,6 +36,7 @@ namespace recir_hstu {
 typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(8))) short i16x8;
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) const float lds_cfloat;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 typedef __attribute__((ext_vector_type(8))) int i32x8;
@@ -70,6 +71,9 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
 #endif
 #ifndef HSTU_DL_RAB_SLOTS
 #define HSTU_DL_RAB_SLOTS 1  // the bias instantiations use the hand-placed slot schedule too
+#endif
+#ifndef HSTU_DL_PDK_RAB
+#define HSTU_DL_PDK_RAB 12  // K fragments in flight when a tile opens, bias instantiations (the bias block needs registers too)
 #endif
 #ifndef HSTU_DL_B1
 #define HSTU_DL_B1 5  // slot in which the bias of the second score block is read (first used in slot 8)
@@ -190,6 +194,12 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     const bool tail_row = idm >= si.tail0;
     const int idlo_w = min(m_lo, si.cap), idhi_w = min(m_hi, si.cap);
     const bool wave_has_tail = idhi_w >= si.tail0;
+    // The staged bias band is stored reversed (entry 190 - i holds rab index first + i), so that the
+    // elements a lane holds, keys k0 + 4 half + c with ascending c, sit at ascending addresses:
+    // byte 4 (127 - (m - q0) + 4 half + c) of the stage.  The lane part is made opaque to the compiler,
+    // which otherwise forms an address register per pair of elements.
+    unsigned rab_lane = 4u * (unsigned)(127 - (m - q0) + 4 * half);
+    if (HAS_RAB) asm volatile("" : "+v"(rab_lane));
     // Causal mask of this lane's row as bounds on the key index: key j is kept iff
     //   j < max(min(idm, n), min(ctx_eff, n))  or  j == m (and m < n).
     // Element r of a score block is key k0 + 4 half + c with a compile-time c, so the bounds are
@@ -218,13 +228,12 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 
     // Copies of one tile: 4 + 4 instructions per wave.  Rows at or past the end of the sequence
     // (last, partial tile only) re-read the sequence's last row; the mask zeroes their contribution.
-    // part 2 ps (+ 1) = the K (V) instruction of rows 16 wave + 4 ps .. + 3; part 8 = fp8 K and the bias band
+    // part 2 ps (+ 1) = the K (V) instruction of rows 16 wave + 4 ps .. + 3; part 8 = fp8 K
     auto issue_part = [&](int it, auto buf_tag, auto whole_tag, int part) __attribute__((always_inline)) {
       constexpr int BUF = decltype(buf_tag)::value;
       constexpr bool KNOWN_WHOLE = decltype(whole_tag)::value;  // caller guarantees k0 + BN <= n
       unsigned short* Kd = BUF ? Ks1 : Ks0;
       unsigned short* Vd = BUF ? Vs1 : Vs0;
-      float* rabd = BUF ? rabs1 : rabs0;
       const int k0 = it * BN;
       const char* kt = kgb + (size_t)k0 * krow_bytes;
       const char* vt = vgb + (size_t)k0 * row_bytes;
@@ -284,7 +293,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     auto band_store = [&](auto buf_tag, float val) __attribute__((always_inline)) {
       constexpr int BUF = decltype(buf_tag)::value;
       asm volatile("" : "+v"(val));  // first use of the loaded value: the wait for it stays here
-      if (tid < BM + BN - 1) (BUF ? rabs1 : rabs0)[tid] = val * kLog2e;
+      if (tid < BM + BN - 1) (BUF ? rabs1 : rabs0)[(BM + BN - 2) - tid] = val * kLog2e;
     };
     auto issue_tile_as = [&](int it, auto buf_tag, auto whole_tag) __attribute__((always_inline)) {
 #pragma unroll
@@ -356,7 +365,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 
     // silu + mask + bf16 packing of one 32 x 32 score block (accumulator layout) into two B operands
-    auto silu_pack = [&](auto masked_tag, const f32x16& sv, int k0, int kvb, const float* rabt, bf16x8& o0,
+    auto silu_pack = [&](auto masked_tag, const f32x16& sv, int k0, int kvb, unsigned rab_addr, bf16x8& o0,
                          bf16x8& o1) __attribute__((always_inline)) {
       constexpr bool MASKED = decltype(masked_tag)::value;
       f32x16 pv;
@@ -365,7 +374,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
         float s = sv[r];
         if (FP8) s *= s_mul;
-        if (HAS_RAB) s += rabt[(m - q0) - jl + (BN - 1)];
+        if (HAS_RAB) s += *(lds_cfloat*)(rab_addr + 4u * (unsigned)(kvb * 32 + 8 * (r >> 2) + (r & 3)));
         const float ex = __builtin_amdgcn_exp2f(-s);
         float pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
         if (MASKED) pe = kept(k0, kvb * 32 + 8 * (r >> 2) + (r & 3)) ? pe : 0.f;
@@ -392,7 +401,10 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       constexpr bool FAST = decltype(fast_tag)::value;  // the next tile exists and is whole
       const char* kb = (const char*)(BUF ? Ks1 : Ks0);
       const char* vb = (const char*)(BUF ? Vs1 : Vs0);
-      const float* rabt = BUF ? rabs1 : rabs0;
+      // LDS byte address of this lane's part of the tile's bias band; opaque per tile, so that the
+      // element addresses stay this register plus a constant instead of becoming 64 hoisted registers
+      unsigned rab_addr = (unsigned)(size_t)(BUF ? rabs1 : rabs0) + rab_lane;
+      if (HAS_RAB) asm volatile("" : "+v"(rab_addr));
       const std::integral_constant<int, BUF ^ 1> other{};
       const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       auto k_frag = [&](int kvb, int kk) __attribute__((always_inline)) {
@@ -428,7 +440,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         // that hold scores and packed P are free when a tile starts, so every K fragment can be in
         // flight at once; V fragments follow as K fragments are consumed.
         // (the bodies that carry mask or clamping state have fewer registers to spare: distance 6)
-        constexpr int PDK = FAST ? HSTU_DL_PDK : 6, PDV = FAST ? HSTU_DL_PDV : 6;
+        constexpr int PDK = FAST ? (HAS_RAB ? HSTU_DL_PDK_RAB : HSTU_DL_PDK) : 6, PDV = FAST ? HSTU_DL_PDV : 6;
         auto frag_req = [](int s) constexpr { return s < PDK ? -1 : (s < 16 ? s - PDK : max(s - PDV, 0)); };
         // slot 16 + j of the second contraction: accumulator db, key step s2
         auto pv_db = [](int s) constexpr { return (s - 16) & 3; };
@@ -471,7 +483,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         auto bias_block = [&](int blk) __attribute__((always_inline)) {
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            sblk[blk][r] = rabt[(m - q0) - (blk * 32 + 8 * (r >> 2) + 4 * half + (r & 3)) + (BN - 1)];
+            sblk[blk][r] = *(lds_cfloat*)(rab_addr + 4u * (unsigned)(blk * 32 + 8 * (r >> 2) + (r & 3)));
         };
         if (HAS_RAB) bias_block(0);
 #pragma unroll
@@ -573,7 +585,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         load_group(4, fa);
         s1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kb0, q8[0], zero, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
         s1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kb1, q8[1], s1, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
-        silu_pack(masked_tag, s0, k0, 0, rabt, pb0, pb1);
+        silu_pack(masked_tag, s0, k0, 0, rab_addr, pb0, pb1);
       } else {
       load_group(0, fa);
       if constexpr (FAST) issue_tile_as(nxt, other, std::true_type{}); else if (nxt < nkv) issue_tile(nxt, other);
@@ -587,7 +599,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       // groups 2 and 3 with silu(S0)
       load_group(3, fb);
       mfma_group(2, fa);
-      silu_pack(masked_tag, s0, k0, 0, rabt, pb0, pb1);
+      silu_pack(masked_tag, s0, k0, 0, rab_addr, pb0, pb1);
       load_group(4, fa);
       mfma_group(3, fb);
       // MFMAs issue in pairs: the second of a back-to-back pair costs less issue time than a lone one
@@ -611,7 +623,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       // groups 4 and 5 with silu(S1)
       load_group(5, fb);
       mfma_group(4, fa);
-      silu_pack(masked_tag, s1, k0, 1, rabt, pb2, pb3);
+      silu_pack(masked_tag, s1, k0, 1, rab_addr, pb2, pb3);
       load_group(6, fa);
       mfma_group(5, fb);
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
