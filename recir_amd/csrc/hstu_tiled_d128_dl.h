@@ -76,6 +76,9 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
 #define HSTU_DL_RAB_SLOTS 2  // bias instantiations: 1 = slot schedule where the unbiased kernel has it, 2 = in every bf16 tile
                              // body (the other body adds the bias in the SiLU arithmetic; measured 2-3 % slower)
 #endif
+#ifndef HSTU_DL_PD_SLOW
+#define HSTU_DL_PD_SLOW 6  // fragment prefetch distance of the bodies that carry mask or clamping state
+#endif
 #ifndef HSTU_DL_PDK_RAB
 #define HSTU_DL_PDK_RAB 12  // K fragments in flight when a tile opens, bias instantiations (the bias block needs registers too)
 #endif
@@ -444,7 +447,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         // that hold scores and packed P are free when a tile starts, so every K fragment can be in
         // flight at once; V fragments follow as K fragments are consumed.
         // (the bodies that carry mask or clamping state have fewer registers to spare: distance 6)
-        constexpr int PDK = FAST ? (HAS_RAB ? HSTU_DL_PDK_RAB : HSTU_DL_PDK) : 6, PDV = FAST ? HSTU_DL_PDV : 6;
+        constexpr int PDK = FAST ? (HAS_RAB ? HSTU_DL_PDK_RAB : HSTU_DL_PDK) : HSTU_DL_PD_SLOW, PDV = FAST ? HSTU_DL_PDV : HSTU_DL_PD_SLOW;
         auto frag_req = [](int s) constexpr { return s < PDK ? -1 : (s < 16 ? s - PDK : max(s - PDV, 0)); };
         // slot 16 + j of the second contraction: accumulator db, key step s2
         auto pv_db = [](int s) constexpr { return (s - 16) & 3; };
