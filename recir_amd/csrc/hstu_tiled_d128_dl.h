@@ -80,7 +80,7 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
 #define HSTU_DL_PD_SLOW 6  // fragment prefetch distance of the bodies that carry mask or clamping state
 #endif
 #ifndef HSTU_DL_PDK_RAB
-#define HSTU_DL_PDK_RAB 12  // K fragments in flight when a tile opens, bias instantiations (the bias block needs registers too)
+#define HSTU_DL_PDK_RAB 6  // K fragments in flight when a tile opens, bias instantiations (the bias block needs registers too)
 #endif
 #ifndef HSTU_DL_B1
 #define HSTU_DL_B1 5  // slot in which the bias of the second score block is read (first used in slot 8)
@@ -89,7 +89,7 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
 #define HSTU_DL_SLOTS 1
 #endif
 #ifndef HSTU_DL_PDK
-#define HSTU_DL_PDK 16  // K fragments (slots 0..15) are requested this many slots ahead
+#define HSTU_DL_PDK 6  // K fragments (slots 0..15) are requested this many slots ahead
 #endif
 #ifndef HSTU_DL_PDV
 #define HSTU_DL_PDV 10  // V fragments (slots 16..31) likewise
@@ -443,10 +443,10 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         f32x16 sblk[2];
         unsigned pw[2][8];
         bf16x8 F[32];
-        // slot in which the LDS fragment of slot s is requested (-1: before slot 0).  The registers
-        // that hold scores and packed P are free when a tile starts, so every K fragment can be in
-        // flight at once; V fragments follow as K fragments are consumed.
-        // (the bodies that carry mask or clamping state have fewer registers to spare: distance 6)
+        // slot in which the LDS fragment of slot s is requested (-1: before slot 0).  Six K fragments
+        // open a tile; all sixteen would fit the registers that scores and packed P leave free at
+        // that point, but measured 1-3 % slower (configurations 2 and 4).  V fragments run ten slots
+        // ahead.  (The bodies that carry mask or clamping state: distance 6 for both.)
         constexpr int PDK = FAST ? (HAS_RAB ? HSTU_DL_PDK_RAB : HSTU_DL_PDK) : HSTU_DL_PD_SLOW, PDV = FAST ? HSTU_DL_PDV : HSTU_DL_PD_SLOW;
         auto frag_req = [](int s) constexpr { return s < PDK ? -1 : (s < 16 ? s - PDK : max(s - PDV, 0)); };
         // slot 16 + j of the second contraction: accumulator db, key step s2
