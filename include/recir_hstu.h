@@ -92,6 +92,28 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
                         int32_t full_attn_size, float alpha, int32_t dtype, uint32_t flags,
                         void* workspace, size_t workspace_bytes, void* hip_stream);
 
+/*
+ * recir_hstu_attn_fwd for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  Same arguments and results as recir_hstu_attn_fwd without the workspace: the work
+ * lists live in a device array of RECIR_HSTU_NOALLOC_SCRATCH_BYTES bytes that is part of the
+ * library image (each GPU the library runs on holds its own copy until the process ends).  The
+ * call allocates and frees nothing.  Sizes whose work lists do not fit
+ * (recir_hstu_attn_fwd_workspace_bytes(...) > RECIR_HSTU_NOALLOC_SCRATCH_BYTES) are rejected with
+ * RECIR_HSTU_ERR_WORKSPACE; RECIR_HSTU_FLAG_REUSE_PLAN is rejected (the array is shared by every
+ * call on the GPU, so a later call cannot know whose lists it holds).  The device of `hip_stream`
+ * must be the current device.  All calls on one GPU share that GPU's array: calls that can overlap
+ * on the device (different streams) race and must be ordered by the caller.
+ */
+#define RECIR_HSTU_NOALLOC_SCRATCH_BYTES (4u << 20)
+int recir_hstu_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* out,
+                                const void* seq_offsets, const void* num_targets, const float* rab,
+                                const float* attn_scale, const float* q_scale, const float* k_scale,
+                                int32_t T, int32_t B, int32_t H, int32_t Dqk, int32_t Dv,
+                                int32_t max_seq_len, int32_t contextual_seq_len,
+                                int32_t max_attn_len, int32_t full_attn_size, float alpha,
+                                int32_t dtype, uint32_t flags, void* hip_stream);
+
 /* Scratch size recir_hstu_attn_fwd needs for these sizes (upper bound over all kernel variants). */
 size_t recir_hstu_attn_fwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk,
                                            int32_t Dv, int32_t dtype);

@@ -18,10 +18,12 @@ FLAG_CTX_REFERENCE = 0x2
 FLAG_SCALE_PER_TOKEN = 0x4
 FLAG_REUSE_PLAN = 0x8
 FLAG_KERNEL_SHIFT = 8
+NOALLOC_SCRATCH_BYTES = 4 << 20
 
 # every symbol include/recir_hstu.h declares
 EXPORTS = (
     "recir_hstu_attn_fwd",
+    "recir_hstu_attn_fwd_noalloc",
     "recir_hstu_attn_fwd_workspace_bytes",
     "recir_hstu_attn_bwd",
     "recir_hstu_attn_bwd_workspace_bytes",
@@ -62,6 +64,8 @@ def load() -> ctypes.CDLL:
     L.recir_hstu_attn_fwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                       i32, i32, i32, i32, i32, i32, i32, i32, i32, f32, i32, u32, vp, sz, vp]
     L.recir_hstu_attn_fwd.restype = ctypes.c_int
+    L.recir_hstu_attn_fwd_noalloc.argtypes = L.recir_hstu_attn_fwd.argtypes[:22] + [vp]
+    L.recir_hstu_attn_fwd_noalloc.restype = ctypes.c_int
     L.recir_hstu_attn_fwd_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     L.recir_hstu_attn_fwd_workspace_bytes.restype = sz
     L.recir_hstu_attn_bwd.argtypes = [vp] * 11 + [i32] * 9 + [f32, i32, u32, vp, sz, vp]

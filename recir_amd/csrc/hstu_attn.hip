@@ -16,9 +16,11 @@
 //   hstu_amax_per_head / hstu_quant_e4m3_per_head   per-head fp8 quantiser
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "recir_hstu.h"
 #include "recir_jagged.h"
@@ -467,6 +469,73 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
   if (int rc = launch_status("hstu_fwd_generic")) return rc;
   g_last_kernel = dtype == RECIR_HSTU_DTYPE_BF16 ? "generic_bf16" : "generic_fp32";
   return RECIR_HSTU_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------------
+// Forward entry point that allocates nothing: the work lists live in a device array of the
+// library image instead of a caller-provided workspace.
+// ---------------------------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[RECIR_HSTU_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+// Device address of `scratch` on each GPU.  In host code the array's name is only a handle for the
+// runtime; the address a kernel can use comes from hipGetSymbolAddress, once per device, with that
+// device current (every GPU holds its own copy of the array at its own address).
+std::atomic<void*> g_scratch_ptr[NOALLOC_MAX_DEVICES];
+std::mutex g_scratch_mutex;
+
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail((int)e, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "device index %d outside the %d the library keeps scratch addresses for", dev,
+                NOALLOC_MAX_DEVICES);
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!ptr) {
+      e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !ptr)
+        return fail(e != hipSuccess ? (int)e : RECIR_HSTU_ERR_WORKSPACE, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                    hipGetErrorString(e));
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return 0;
+}
+}  // namespace
+
+extern "C" {
+
+int recir_hstu_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* out,
+                                const void* seq_offsets, const void* num_targets, const float* rab,
+                                const float* attn_scale, const float* q_scale, const float* k_scale,
+                                int32_t T, int32_t B, int32_t H, int32_t Dqk, int32_t Dv,
+                                int32_t max_seq_len, int32_t contextual_seq_len,
+                                int32_t max_attn_len, int32_t full_attn_size, float alpha,
+                                int32_t dtype, uint32_t flags, void* hip_stream) {
+  if (flags & RECIR_HSTU_FLAG_REUSE_PLAN)
+    return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT,
+                "RECIR_HSTU_FLAG_REUSE_PLAN is not available without a caller-owned workspace: the built-in scratch is "
+                "shared by every call on the GPU");
+  const size_t need = recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype);
+  if (need > (size_t)RECIR_HSTU_NOALLOC_SCRATCH_BYTES)
+    return fail(RECIR_HSTU_ERR_WORKSPACE,
+                "work lists of %zu bytes (T=%d B=%d H=%d) exceed the built-in scratch of %zu bytes; use recir_hstu_attn_fwd "
+                "with a workspace", need, T, B, H, (size_t)RECIR_HSTU_NOALLOC_SCRATCH_BYTES);
+  void* ptr = nullptr;
+  if (int rc = scratch_of_current_device(&ptr)) return rc;
+  // The plan kernel writes every list length and every item the attention kernel reads, so
+  // nothing left in the array by an earlier call is seen: no clearing needed.
+  return recir_hstu_attn_fwd(q, k, v, out, seq_offsets, num_targets, rab, attn_scale, q_scale, k_scale, T, B, H, Dqk, Dv,
+                             max_seq_len, contextual_seq_len, max_attn_len, full_attn_size, alpha, dtype, flags, ptr,
+                             (size_t)RECIR_HSTU_NOALLOC_SCRATCH_BYTES, hip_stream);
 }
 
 size_t recir_hstu_attn_bwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk, int32_t Dv,
