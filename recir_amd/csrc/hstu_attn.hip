@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -29,7 +30,6 @@
 #include "hstu_plan.h"
 #include "hstu_tiled_d128.h"
 #include "hstu_tiled_d128_dl.h"
-#include "hstu_tiled_d128_w64.h"
 #include "hstu_bwd_generic.h"
 #include "hstu_bwd_d128.h"
 #include "jagged_rows.h"
@@ -389,11 +389,18 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
   const bool tiled_ok = (dtype == RECIR_HSTU_DTYPE_BF16 || fp8) && Dqk == HD && Dv == HD &&
                         (((size_t)q | (size_t)k | (size_t)v | (size_t)out) & 15) == 0;
   bool use_tiled = tiled_ok;
+  // The tiled kernels keep a bias divided by the score multiplier in their accumulators: not
+  // possible with alpha = 0 (the scores are then the bias alone), which the generic kernel handles.
+  const bool bias_needs_generic = rab && !std::isnormal(1.0f / alpha);
+  if (bias_needs_generic && !fp8) use_tiled = false;
+  if (bias_needs_generic && (fp8 || variant >= 2))
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "a bias with alpha = %g runs on the generic kernel only", (double)alpha);
   if (variant == 1 && !fp8) use_tiled = false;
   if (fp8 && variant == 2) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "fp8 q/k runs on the direct-to-LDS tiled kernel only");
   if (variant >= 2 && !tiled_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "tiled kernel needs bf16, Dqk = Dv = 128 and 16-byte aligned tensors");
-  if (semi && (variant == 2 || variant == 4))
+  if (variant > 3) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "unknown kernel selector %u", variant);
+  if (semi && variant == 2)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "the semi-local mask runs on the direct-to-LDS tiled kernel or the generic one");
 
   if (use_tiled) {
@@ -405,9 +412,7 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     p.ws_counts = (int*)workspace;
     p.ws_items = (WorkItem*)((char*)workspace + WS_HEADER);
     p.items_cap = (int)items;
-    // query rows per workgroup: 256 for the 64-rows-per-wave kernel, else 128
-    const bool w64 = variant == 4;
-    const int bm = w64 ? BM2 : BM;
+    const int bm = BM;
     // only the direct-to-LDS kernel reads the row bound of an item
     const int plan_mode = (variant == 0 || variant == 3) ? PLAN_SHIFT_ODD : 0;
     // slots per XCD the launch covers: an even share of the items plus the imbalance the dealing of
@@ -428,19 +433,6 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
       if (int rc = launch_status("hstu_plan_kernel")) return rc;
     }
     const dim3 grid((unsigned)(slots * NUM_XCD));
-    if (w64) {
-      if (dtype == RECIR_HSTU_DTYPE_FP8_E4M3) {
-        if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_w64<true, true>), grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((hstu_fwd_tiled_d128_w64<false, true>), grid, dim3(256), 0, stream, p);
-        g_last_kernel = rab ? "tiled_d128_w64_fp8qk_rab" : "tiled_d128_w64_fp8qk";
-      } else {
-        if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128_w64<true, false>), grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((hstu_fwd_tiled_d128_w64<false, false>), grid, dim3(256), 0, stream, p);
-        g_last_kernel = rab ? "tiled_d128_w64_bf16_rab" : "tiled_d128_w64_bf16";
-      }
-      if (int rc = launch_status("hstu_fwd_tiled_d128_w64")) return rc;
-      return RECIR_HSTU_OK;
-    }
     if (variant == 2) {  // register-staged tiles (kept for comparison and tiling-invariance tests)
       if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128<true>), grid, dim3(256), 0, stream, p);
       else hipLaunchKernelGGL((hstu_fwd_tiled_d128<false>), grid, dim3(256), 0, stream, p);
@@ -653,17 +645,6 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   g_last_kernel = bf16 ? "bwd_generic_bf16" : "bwd_generic_fp32";
   return RECIR_HSTU_OK;
 }
-
-#ifdef HSTU_TRACE
-// Debug build only (never part of the shipped library): select the traced workgroup / read stamps.
-int recir_hstu_debug_item_trace(void* host_dst) {
-  return (int)hipMemcpyFromSymbol(host_dst, HIP_SYMBOL(recir_hstu::g_item_trace), sizeof(recir_hstu::g_item_trace));
-}
-int recir_hstu_debug_trace(int block, void* host_dst) {
-  if (host_dst) return (int)hipMemcpyFromSymbol(host_dst, HIP_SYMBOL(recir_hstu::g_trace), sizeof(recir_hstu::g_trace));
-  return (int)hipMemcpyToSymbol(HIP_SYMBOL(recir_hstu::g_trace_block), &block, sizeof(int));
-}
-#endif
 
 int recir_hstu_calibration_copy(void* dst, const void* src, size_t bytes, void* hip_stream) {
   if (!dst || !src || (bytes & 15) || (((size_t)dst | (size_t)src) & 15))

@@ -34,41 +34,7 @@ __device__ __forceinline__ int vt_swz(int d) { return (d ^ (d >> 3)) & 7; }
 
 // One thread's share of a staged K/V tile (kept as named members, not arrays, so that it lives in
 // registers whatever the control flow around it looks like).
-#if defined(HSTU_TRACE) && !defined(HSTU_TRACE_ITEMS_ONLY)
-// Debug build only: per-wave phase timestamps of one workgroup.
-__device__ unsigned long long g_trace[4 * 64 * 8];
-__device__ int g_trace_block = 0;
-#define HSTU_STAMP(slot)                                                                  \
-  do {                                                                                    \
-    __builtin_amdgcn_sched_barrier(0);                                                    \
-    if (trace_on && lane == 0 && trace_it < 64)                                           \
-      g_trace[(wave * 64 + trace_it) * 8 + (slot)] = __builtin_readcyclecounter();        \
-    __builtin_amdgcn_sched_barrier(0);                                                    \
-  } while (0)
-#else
-#ifdef HSTU_TRACE
-__device__ unsigned long long g_trace[4 * 64 * 8];
-__device__ int g_trace_block = 0;
-#endif
-#define HSTU_STAMP(slot) do { } while (0)
-#endif
-#ifdef HSTU_TRACE
-// Debug build only: wall-clock stamps (100 MHz) of the phases of every workgroup's first item.
-__device__ unsigned long long g_item_trace[4096 * 4 * 8];
-#define HSTU_ITEM_STAMP(k)                                                                      \
-  do {                                                                                         \
-    __builtin_amdgcn_sched_barrier(0);                                                         \
-    if (lane == 0 && blockIdx.x < 4096 && slot == (int)(blockIdx.x / NUM_XCD))                 \
-      g_item_trace[(blockIdx.x * 4 + wave) * 8 + (k)] = wall_clock64();                        \
-    __builtin_amdgcn_sched_barrier(0);                                                         \
-  } while (0)
-#else
-#define HSTU_ITEM_STAMP(k) do { } while (0)
-#endif
 
-#ifndef HSTU_EXP
-#define HSTU_EXP 0  // debug builds only: bit mask that removes pieces of the kernel for timing studies
-#endif
 
 struct TileRegs {
   u32x4 k0, k1, k2, k3;
@@ -81,10 +47,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
   __shared__ __attribute__((aligned(16))) unsigned short Ks[2][BN * HD];
   __shared__ __attribute__((aligned(16))) unsigned short Vts[2][HD * BN];
   __shared__ float rabs[2][HAS_RAB ? (BM + BN) : 1];
-#if HSTU_EXP & 64
-  __shared__ char occupancy_pad[40000];  // debug builds only: forces one workgroup per CU
-  if (p.T < 0) occupancy_pad[threadIdx.x] = 1;
-#endif
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -113,27 +75,24 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
   const float* __restrict__ rabg = HAS_RAB ? p.rab + (size_t)h * rab_w : nullptr;
 
   // ---- Q fragments (B operand): lane holds row qw0 + l32, d = 16 kk + 8 half .. +7 ----
-  // q is pre-multiplied by alpha * log2(e) (rounded back to bf16), so the score accumulator holds
-  // u = x * log2(e) directly, sigmoid needs exp2(-u) with no multiply, and u * sigmoid(x) is
-  // accumulated; the constant 1 / log2(e) goes into the output scale.
+  // q enters the products as stored (no rescaling, hence no rounding of its own): the score
+  // accumulator holds S' = q . k, S' sigmoid(alpha S') is accumulated and alpha goes into the output scale.
   const int qw0 = q0 + wave * 32;
   const int m = qw0 + l32;
   bf16x8 qf[8];
   {
     const bool valid = m < si.n;
     const unsigned short* qrow = (const unsigned short*)p.q + ((size_t)(si.s + (valid ? m : 0)) * p.H + h) * HD;
-    const float qmul = p.alpha * kLog2e;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
       const u32x4 zero4 = {0u, 0u, 0u, 0u};
       const u32x4 t = valid ? *(const u32x4*)(qrow + kk * 16 + half * 8) : zero4;
-      u32x4 sc;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        sc[i] = pack_bf16x2(__uint_as_float(t[i] << 16) * qmul, __uint_as_float(t[i] & 0xffff0000u) * qmul);
-      qf[kk] = __builtin_bit_cast(bf16x8, sc);
+      qf[kk] = __builtin_bit_cast(bf16x8, t);
     }
   }
+  // accumulator value S' = q . k (+ bias / alpha); sigmoid(alpha S') = 1 / (1 + exp2(neg_c S'))
+  const float neg_c = -(p.alpha * kLog2e);
+  const float bias_mul = HAS_RAB ? 1.0f / p.alpha : 0.f;
 
   f32x16 acc[4];
 #pragma unroll
@@ -155,10 +114,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
   const int skip_b = q0 / BN;
   const bool has_skip = skip_a < skip_b;
 
-#ifdef HSTU_TRACE
-  const bool trace_on = (int)blockIdx.x == g_trace_block;
-  int trace_it = 0;
-#endif
   // staging roles of this thread
   const int k_chunk = tid & 15, k_row0 = tid >> 4;        // K: rows k_row0 + 16 ps, 16-byte chunk
   const int v_g = tid >> 4, v_e = tid & 15;               // V: rows 4 v_g .. +3, d = 8 v_e .. +7
@@ -204,7 +159,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
       // band of bias entries this (q tile, kv tile) can touch: index (m - j) + N - 1
       int idx = q0 - k0 - (BN - 1) + p.N - 1 + tid;
       idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
-      tr.rab = (tid < BM + BN - 1) ? rabg[idx] * kLog2e : 0.f;
+      tr.rab = (tid < BM + BN - 1) ? rabg[idx] * bias_mul : 0.f;
     }
   };
 
@@ -258,14 +213,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
     for (int r = 0; r < 16; ++r) {
       const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
       float s = sv[r];
-      if (HAS_RAB) s += rabs[buf][(m - q0) - jl + (BN - 1)];  // bias staged pre-multiplied by log2(e)
-      float pe;
-      if (HSTU_EXP & 1) {
-        pe = s;
-      } else {
-        const float ex = __builtin_amdgcn_exp2f(-s);
-        pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
-      }
+      if (HAS_RAB) s += rabs[buf][(m - q0) - jl + (BN - 1)];  // bias staged divided by alpha
+      const float ex = __builtin_amdgcn_exp2f(s * neg_c);
+      float pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
       if (MASKED) {
         const int j = k0 + jl;
         // branch-free keep(m, j) & (j < n)
@@ -306,13 +256,12 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
     bf16x8 pb0, pb1, pb2, pb3;
     // stage 0
 #pragma unroll
-    for (int kk = 0; kk < ((HSTU_EXP & 8) ? 1 : 8); ++kk)
+    for (int kk = 0; kk < 8; ++kk)
       s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(0, kk), qf[kk], kk == 0 ? zero : s0, 0, 0, 0);
-    HSTU_STAMP(1);
     __builtin_amdgcn_sched_barrier(0);
     // stage A
 #pragma unroll
-    for (int kk = 0; kk < ((HSTU_EXP & 8) ? 1 : 8); ++kk)
+    for (int kk = 0; kk < 8; ++kk)
       s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(1, kk), qf[kk], kk == 0 ? zero : s1, 0, 0, 0);
     silu_pack(masked_tag, s0, k0, 0, buf, pb0, pb1);
     // MFMAs issue in pairs: the second of a back-to-back pair costs less issue time than a
@@ -323,11 +272,10 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
       __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // 10 VALU
       __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);   // 8 transcendental
     }
-    HSTU_STAMP(2);
     __builtin_amdgcn_sched_barrier(0);
     // stage B
 #pragma unroll
-    for (int db = 0; db < ((HSTU_EXP & 4) ? 1 : 4); ++db) {
+    for (int db = 0; db < 4; ++db) {
       acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 0), pb0, acc[db], 0, 0, 0);
       acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 1), pb1, acc[db], 0, 0, 0);
     }
@@ -338,11 +286,10 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
       __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
       __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);
     }
-    HSTU_STAMP(3);
     __builtin_amdgcn_sched_barrier(0);
     // stage C
 #pragma unroll
-    for (int db = 0; db < ((HSTU_EXP & 4) ? 1 : 4); ++db) {
+    for (int db = 0; db < 4; ++db) {
       acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 2), pb2, acc[db], 0, 0, 0);
       acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(db, 3), pb3, acc[db], 0, 0, 0);
     }
@@ -373,22 +320,14 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
     int nxt = next_tile(it);
     if (nxt < nkv) load_tile(nxt, tr);
     while (true) {
-      HSTU_STAMP(0);
       compute_tile(it, buf);
-      HSTU_STAMP(4);
       if (nxt >= nkv) break;
-      if (!(HSTU_EXP & 2)) store_tile(buf ^ 1, tr);
-      HSTU_STAMP(5);
-      if (!(HSTU_EXP & 16)) __syncthreads();
-      HSTU_STAMP(6);
+      store_tile(buf ^ 1, tr);
+      __syncthreads();
       it = nxt;
       buf ^= 1;
       nxt = next_tile(it);
-      if (!(HSTU_EXP & (2 | 32)) && nxt < nkv) load_tile(nxt, tr);
-      HSTU_STAMP(7);
-#ifdef HSTU_TRACE
-      ++trace_it;
-#endif
+      if (nxt < nkv) load_tile(nxt, tr);
     }
   }
 
@@ -397,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
     float oscale = 1.0f / (float)p.N;
     if (p.attn_scale)
       oscale = (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) ? p.attn_scale[si.s + m] : p.attn_scale[0];
-    oscale *= 1.0f / kLog2e;
+    oscale *= p.alpha;
     unsigned short* orow = (unsigned short*)p.out + ((size_t)(si.s + m) * p.H + h) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {

@@ -10,8 +10,10 @@
 //                 layout of the next contraction
 //   O^T[d, q]  += V^T[d, kv] . P^T[kv, q]     A = V^T, read from the row-major V tile with
 //                 ds_read_b64_tr_b16 (each 16-lane group transposes a 4 x 16 block)
-// q is pre-multiplied by alpha * log2(e), so sigmoid needs exp2(-u) only and the constant factors
-// (1 / log2(e), the 1/N scale) are applied once to the fp32 output accumulator.
+// The score accumulators hold the raw products S' = q . k (+ bias / alpha): q is not rescaled, so no
+// rounding beyond the operands' own enters a score.  With c = alpha * log2(e), sigmoid(alpha S') =
+// 1 / (1 + exp2(-c S')) and P' = S' sigmoid(alpha S') is what is rounded to bf16; the remaining factor
+// (alpha and the 1/N scale) is applied once to the fp32 output accumulator.
 //
 // Pipeline: two LDS stages.  The global_load_lds of tile i+1 are issued while the first MFMAs of
 // tile i run and must have landed (vmcnt) before the barrier that ends tile i.
@@ -94,16 +96,7 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
 #ifndef HSTU_DL_PDV
 #define HSTU_DL_PDV 10  // V fragments (slots 16..31) likewise
 #endif
-#ifndef HSTU_DL_ABL
-#define HSTU_DL_ABL 0  // debug builds: 1 no SiLU, 2 no LDS fragment reads, 32 no V reads, 4 no copies, 16 no barrier
-#endif
-#if HSTU_DL_ABL & 16
-#define HSTU_DL_TILE_SYNC() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
-#elif HSTU_DL_ABL & 8
-#define HSTU_DL_TILE_SYNC() __syncthreads()
-#else
 #define HSTU_DL_TILE_SYNC() do { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); __syncthreads(); } while (0)
-#endif
 #ifndef HSTU_DL_C0
 #define HSTU_DL_C0 0     // slot of the first copy instruction of the next tile
 #define HSTU_DL_CSTEP 1  // slots between copy instructions
@@ -123,10 +116,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
   __shared__ __attribute__((aligned(1024))) unsigned short Vs1[BN * HD];
   __shared__ float rabs0[HAS_RAB ? (BM + BN) : 1];
   __shared__ float rabs1[HAS_RAB ? (BM + BN) : 1];
-#if HSTU_EXP & 64
-  __shared__ char occupancy_pad[40000];  // debug builds only: forces one workgroup per CU
-  if (p.T < 0) occupancy_pad[threadIdx.x] = 1;
-#endif
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -159,17 +148,12 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
   const unsigned k8_rd = (unsigned)l32 * 128u + (unsigned)(((2 * half) ^ ((l32 >> 1) & 7)) * 16);
   const int ld8_row = lane >> 3, ld8_chunk = lane & 7;
 
-#ifdef HSTU_TRACE
-  const bool trace_on = (int)blockIdx.x == g_trace_block;
-  int trace_it = 0;
-#endif
   // Work list of the XCD this workgroup runs on.  Normally one item per workgroup; the stride loop
   // only matters when a list is longer than the launch assumed (sequences above max_seq_len).
   const int xcd = blockIdx.x % NUM_XCD;
   const int list_len = p.ws_counts[xcd];
   const WorkItem* __restrict__ list = p.ws_items + (size_t)xcd * p.items_cap;
   for (int slot = blockIdx.x / NUM_XCD; slot < list_len; slot += p.grid_slots) {
-    HSTU_ITEM_STAMP(0);
     const WorkItem wi = list[slot];
     SeqInfo si;
     si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
@@ -185,6 +169,13 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     const char* __restrict__ vgb = (const char*)p.v + ((size_t)si.s * p.H + h) * (HD * 2);
     const int rab_w = 2 * p.N - 1;
     const float* __restrict__ rabg = HAS_RAB ? p.rab + (size_t)h * rab_w : nullptr;
+    // score_c: the factor between an accumulator value S' and the argument of exp2,
+    //   alpha log2(e) (fp8: alpha q_scale[h] k_scale[h] log2(e)); bias_mul: what the bias is staged with
+    //   (log2(e) / score_c); the output carries score_c / log2(e) on top of the scale
+    float score_c = p.alpha * kLog2e;
+    if (FP8) score_c *= p.q_scale[h] * p.k_scale[h];
+    const float neg_c = -score_c;
+    const float bias_mul = HAS_RAB ? kLog2e / score_c : 0.f;
 
     // logical 16-byte chunk each lane fetches so that the swizzled layout comes out
     const unsigned k_off = (unsigned)ld_row * row_bytes + (unsigned)((ld_chunk ^ ld_row) * 16);  // rows 16 a + 0..3; ^ 64 ps for rows 16 a + 4 ps + 0..3
@@ -288,7 +279,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       }
     };
     // Band of bias entries a (query tile, key tile) pair can touch: index (m - j) + N - 1, staged
-    // pre-multiplied by log2(e) with plain stores, ordered by the barrier that publishes the tile.
+    // divided by the score multiplier (alpha; fp8: alpha q_scale k_scale) with plain stores, ordered by the barrier that publishes the tile.
     // In two steps, so that the load's round trip passes under a tile's arithmetic: the load goes
     // out before the tile's copies (the wait for it would otherwise wait for them too), the store
     // follows at the end of the tile.
@@ -300,7 +291,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     auto band_store = [&](auto buf_tag, float val) __attribute__((always_inline)) {
       constexpr int BUF = decltype(buf_tag)::value;
       asm volatile("" : "+v"(val));  // first use of the loaded value: the wait for it stays here
-      if (tid < BM + BN - 1) (BUF ? rabs1 : rabs0)[(BM + BN - 2) - tid] = val * kLog2e;
+      if (tid < BM + BN - 1) (BUF ? rabs1 : rabs0)[(BM + BN - 2) - tid] = val * bias_mul;
     };
     auto issue_tile_as = [&](int it, auto buf_tag, auto whole_tag) __attribute__((always_inline)) {
 #pragma unroll
@@ -328,15 +319,12 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     if (it < nkv) issue_tile(it, std::integral_constant<int, 0>{});
 
     // ---- Q fragments (B operand): lane holds row qw0 + l32 ----
-    // bf16: d = 16 kk + 8 half .. +7, pre-multiplied by alpha * log2(e) and rounded back to bf16
-    // fp8 : d = 64 st + 32 half .. +31 (raw bytes); the factor goes onto the fp32 scores instead
+    // bf16: d = 16 kk + 8 half .. +7, as stored;  fp8: d = 64 st + 32 half .. +31 (raw bytes)
     bf16x8 qf[FP8 ? 1 : 8];
     i32x8 q8[FP8 ? 2 : 1];
-    float s_mul = 1.0f;  // fp8: alpha * q_scale[h] * k_scale[h] * log2(e)
     {
       const bool valid = m < q_end;
       if constexpr (FP8) {
-        s_mul = p.alpha * p.q_scale[h] * p.k_scale[h] * kLog2e;
         const char* qrow = (const char*)p.q + ((size_t)(si.s + (valid ? m : 0)) * p.H + h) * HD;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
@@ -347,20 +335,11 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         }
       } else {
         const unsigned short* qrow = (const unsigned short*)p.q + ((size_t)(si.s + (valid ? m : 0)) * p.H + h) * HD;
-        const float qmul = p.alpha * kLog2e;
-        u32x4 t[8];
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
           const u32x4 zero4 = {0u, 0u, 0u, 0u};
-          t[kk] = valid ? *(const u32x4*)(qrow + kk * 16 + half * 8) : zero4;
-        }
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          u32x4 sc;
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            sc[i] = pack_bf16x2(__uint_as_float(t[kk][i] << 16) * qmul, __uint_as_float(t[kk][i] & 0xffff0000u) * qmul);
-          qf[kk] = __builtin_bit_cast(bf16x8, sc);
+          const u32x4 t = valid ? *(const u32x4*)(qrow + kk * 16 + half * 8) : zero4;
+          qf[kk] = __builtin_bit_cast(bf16x8, t);
         }
       }
     }
@@ -380,9 +359,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       for (int r = 0; r < 16; ++r) {
         const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
         float s = sv[r];
-        if (FP8) s *= s_mul;
         if (HAS_RAB) s += *(lds_cfloat*)(rab_addr + 4u * (unsigned)(kvb * 32 + 8 * (r >> 2) + (r & 3)));
-        const float ex = __builtin_amdgcn_exp2f(-s);
+        const float ex = __builtin_amdgcn_exp2f(s * neg_c);
         float pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
         if (MASKED) pe = kept(k0, kvb * 32 + 8 * (r >> 2) + (r & 3)) ? pe : 0.f;
         pv[r] = pe;
@@ -454,15 +432,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         auto pv_s2 = [](int s) constexpr { return (s - 16) >> 2; };
         auto slot_frag = [&](int s) __attribute__((always_inline)) {
           // stand-ins differ per 32-key block so that the two score blocks stay distinct computations
-#if HSTU_DL_ABL & 2
-          return qf[(s + (s >> 3)) & 7];
-#elif HSTU_DL_ABL & 32
-          return s < 16 ? k_frag(s >> 3, s & 7) : qf[s & 7];
-#elif HSTU_DL_ABL & 64
-          return s < 16 ? qf[(s + (s >> 3)) & 7] : v_frag((s - 16) & 3, (s - 16) >> 2);
-#else
           return s < 16 ? k_frag(s >> 3, s & 7) : v_frag(pv_db(s), pv_s2(s));
-#endif
         };
         auto silu_unit = [&](int u) __attribute__((always_inline)) {
           constexpr bool MASKED = decltype(masked_tag)::value;
@@ -473,15 +443,12 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
             const int r = 2 * e + t;
             const int jl = blk * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
             const float sv = sblk[blk][r];  // the bias is already in there, see bias_block
-            const float ex = __builtin_amdgcn_exp2f(-sv);
+            const float ex = __builtin_amdgcn_exp2f(sv * neg_c);
             float pv = sv * __builtin_amdgcn_rcpf(1.0f + ex);
             if (MASKED) pv = kept(k0, blk * 32 + 8 * (r >> 2) + (r & 3)) ? pv : 0.f;
             pe[t] = pv;
           }
           pw[blk][e] = pack_bf16x2(pe[0], pe[1]);
-#if HSTU_DL_ABL & 1
-          pw[blk][e] = __float_as_uint(sblk[blk][2 * e]) ^ __float_as_uint(sblk[blk][2 * e + 1]);
-#endif
         };
         // The bias enters as the initial value of the score accumulators (no addition in the SiLU
         // units, no register of its own): block 0 is read with the fragments that open the tile,
@@ -500,7 +467,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         // MFMAs back for as long as the address unit takes to accept them
         const bool copy_next = FAST || nxt < nkv;
         auto issue_slot = [&](int part) __attribute__((always_inline)) {
-          if (HSTU_DL_ABL & 4) return;
           if constexpr (FAST) issue_part(nxt, other, std::true_type{}, part);
           else if (copy_next) issue_part(nxt, other, std::false_type{}, part);
         };
@@ -510,9 +476,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 32; ++s) {
-          if (s == 8) HSTU_STAMP(1);
-          if (s == 16) HSTU_STAMP(2);
-          if (s == 24) HSTU_STAMP(3);
 #pragma unroll
           for (int t = s + 1; t < 32; ++t)
             if (frag_req(t) == s) F[t] = slot_frag(t);
@@ -587,7 +550,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         const i32x8 kb0 = k8_frag(1, 0), kb1 = k8_frag(1, 1);
         s0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ka0, q8[0], zero, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
         s0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ka1, q8[1], s0, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
-        HSTU_STAMP(1);
         __builtin_amdgcn_sched_barrier(0);
         load_group(4, fa);
         s1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kb0, q8[0], zero, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
@@ -601,7 +563,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       __builtin_amdgcn_sched_barrier(0);
       load_group(2, fa);
       mfma_group(1, fb);
-      HSTU_STAMP(1);
       __builtin_amdgcn_sched_barrier(0);
       // groups 2 and 3 with silu(S0)
       load_group(3, fb);
@@ -625,7 +586,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);
       }
       }
-      HSTU_STAMP(2);
       __builtin_amdgcn_sched_barrier(0);
       // groups 4 and 5 with silu(S1)
       load_group(5, fb);
@@ -647,7 +607,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
         __builtin_amdgcn_sched_group_barrier(0x400, 8, 0);
       }
-      HSTU_STAMP(3);
       __builtin_amdgcn_sched_barrier(0);
       load_group(7, fb);
       mfma_group(6, fa);
@@ -681,26 +640,16 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     // (64 t + 63 <= m_lo and 64 t + 64 <= cap), inside the first contiguous run of the walk, and
     // followed by a tile that exists and is whole.  Taken in pairs (stage 0, stage 1).
     int fast_pairs = 0;
-#if !defined(HSTU_TRACE) || defined(HSTU_TRACE_ITEMS_ONLY)
     if (!SEMI && wave_has_rows && it == 0) {
       const int run_end = has_skip ? skip_a : nkv;
       int fast_end = min(min((m_lo + 1) / BN, cap0 / BN), min(run_end - 1, si.n / BN - 1));
       fast_pairs = max(fast_end, 0) / 2;
     }
-#endif
 
-    HSTU_ITEM_STAMP(1);
-#ifdef HSTU_TRACE
-    long long trace_c2 = clock64();
-#endif
     if (it < nkv) {
       if (HAS_RAB) band_store(std::integral_constant<int, 0>{}, band_first);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      HSTU_ITEM_STAMP(2);
-#ifdef HSTU_TRACE
-      trace_c2 = clock64();
-#endif
       for (int pi = 0; pi < fast_pairs; ++pi) {
         tile_body(std::false_type{}, std::integral_constant<int, 0>{}, it * BN, it + 1, std::true_type{});
         HSTU_DL_TILE_SYNC();
@@ -711,48 +660,26 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       // two tiles per trip so that the stage index is a compile-time constant
       while (true) {
         int nxt = next_tile(it);
-        HSTU_STAMP(0);
         compute_tile(it, std::integral_constant<int, 0>{}, nxt);
-        HSTU_STAMP(4);
         if (nxt >= nkv) break;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile nxt have landed
-        HSTU_STAMP(5);
         __syncthreads();                                   // ... and everybody's; tile it is no longer read
-        HSTU_STAMP(6);
-        HSTU_STAMP(7);
-#ifdef HSTU_TRACE
-        ++trace_it;
-#endif
         it = nxt;
         nxt = next_tile(it);
-        HSTU_STAMP(0);
         compute_tile(it, std::integral_constant<int, 1>{}, nxt);
-        HSTU_STAMP(4);
         if (nxt >= nkv) break;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        HSTU_STAMP(5);
         __syncthreads();
-        HSTU_STAMP(6);
-        HSTU_STAMP(7);
-#ifdef HSTU_TRACE
-        ++trace_it;
-#endif
         it = nxt;
       }
     }
 
-    HSTU_ITEM_STAMP(3);
-#ifdef HSTU_TRACE
-    // shader cycles of the tile loop (with the wall-clock stamps 2 and 3: the clock it ran at)
-    if (lane == 0 && blockIdx.x < 4096 && slot == (int)(blockIdx.x / NUM_XCD) && it0 >= 0)
-      g_item_trace[(blockIdx.x * 4 + wave) * 8 + 1] = (unsigned long long)(clock64() - trace_c2);
-#endif
     // ---- epilogue: O^T accumulators -> out[s + m, h, :] ----
     if (m < q_end) {
       float oscale = 1.0f / (float)p.N;
       if (p.attn_scale)
         oscale = (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) ? p.attn_scale[si.s + m] : p.attn_scale[0];
-      oscale *= 1.0f / kLog2e;
+      oscale *= score_c * (1.0f / kLog2e);
       unsigned short* orow = (unsigned short*)p.out + ((size_t)(si.s + m) * p.H + h) * HD;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
@@ -765,18 +692,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         }
       }
     }
-    HSTU_ITEM_STAMP(4);
     __syncthreads();  // LDS buffers are reused by the next item
-    HSTU_ITEM_STAMP(5);
-#ifdef HSTU_TRACE
-    if (lane == 0 && blockIdx.x < 4096 && slot == (int)(blockIdx.x / NUM_XCD)) {
-      unsigned hwid, xcc;
-      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
-      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-      g_item_trace[(blockIdx.x * 4 + wave) * 8 + 6] = ((unsigned long long)xcc << 32) | hwid;
-      g_item_trace[(blockIdx.x * 4 + wave) * 8 + 7] = (unsigned long long)nkv;
-    }
-#endif
   }  // work items
 }
 
