@@ -59,21 +59,49 @@ def run_oracle(oracle, wl, *, attn_scale=None, num_targets="default", rab="defau
 
 
 def error_stats(out, ref):
+    """Error of ``out`` against ``ref`` over the whole tensor and per row.  A row is one (token, head)
+    vector of the last dimension: ``worst_row_rel`` is the largest ``max|err row| / (max|ref row| +
+    floor)`` with ``floor`` the smallest non-zero row maximum of the reference, so that a short-prefix
+    row of magnitude 1e-4 counts as much as a row of magnitude 1e-2."""
     out = out.detach().float().cpu().numpy().astype(np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     err = np.abs(out - ref)
     ref_max = max(np.abs(ref).max(), 1e-30) if ref.size else 1.0
     fro = np.sqrt((err ** 2).sum() / max((ref ** 2).sum(), 1e-30)) if ref.size else 0.0
+    worst_row_rel, row_floor = 0.0, 0.0
+    if ref.size and ref.ndim >= 2:
+        d = ref.shape[-1]
+        row_ref = np.abs(ref).reshape(-1, d).max(axis=1)
+        row_err = err.reshape(-1, d).max(axis=1)
+        nz = row_ref[row_ref > 0]
+        row_floor = float(nz.min()) if nz.size else 0.0
+        denom = row_ref + row_floor
+        ok = denom > 0
+        worst_row_rel = float((row_err[ok] / denom[ok]).max()) if ok.any() else 0.0
+        if (~ok).any() and row_err[~ok].max() > 0:  # reference rows that are all zero must come out zero
+            worst_row_rel = float("inf")
     return dict(max_abs=float(err.max()) if err.size else 0.0,
                 rel_to_max=float(err.max() / ref_max) if err.size else 0.0, rel_fro=float(fro),
-                ref_max=float(ref_max))
+                worst_row_rel=worst_row_rel, row_floor=row_floor, ref_max=float(ref_max))
+
+
+def report(what, st):
+    """One line per comparison, picked up from a ``pytest -s`` log for the error table."""
+    print(f"[parity] {what}: max_abs={st['max_abs']:.3e} rel_to_max={st['rel_to_max']:.3e} "
+          f"rel_fro={st['rel_fro']:.3e} worst_row_rel={st['worst_row_rel']:.3e} ref_max={st['ref_max']:.3e}",
+          flush=True)
 
 
 def assert_bf16_close(out, ref, what=""):
+    """bf16 tolerance against the fp32 oracle: max-abs 1e-2, 2e-2 relative to the largest reference
+    magnitude and of the Frobenius norm, and 2e-2 relative per row (the absolute bound alone says
+    nothing where the outputs themselves are below 1e-2, as at the benchmark sizes)."""
     st = error_stats(out, ref)
+    report(what, st)
     assert st["max_abs"] <= BF16_MAX_ABS, (what, st)
     assert st["rel_to_max"] <= BF16_REL, (what, st)
     assert st["rel_fro"] <= BF16_REL, (what, st)
+    assert st["worst_row_rel"] <= BF16_REL, (what, st)
     return st
 
 

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from tests.golden.cases import SMALL_CASES, build_inputs
-from tests.parity_util import (FP8_MAX_ABS, FP32_ATOL, FP32_RTOL, assert_bf16_close, assert_same_zero_structure,
+from tests.parity_util import (BF16_REL, FP8_MAX_ABS, FP32_ATOL, FP32_RTOL, assert_bf16_close, assert_same_zero_structure,
                                error_stats, run_hip, run_oracle, to_device)
 
 pytestmark = pytest.mark.gpu
@@ -104,13 +104,6 @@ def test_tiled_and_generic_kernels_agree(oracle, config):
         assert error_stats(a2, a.float().cpu().numpy())["rel_to_max"] <= 2 ** -7
     else:
         assert torch.equal(a, a2)  # same arithmetic in the same order: only the staging differs
-    with ops.force_kernel(ops.KERNEL_TILED_W64):
-        a3 = run_hip(wl)
-        assert "w64" in _lib.last_kernel()
-    if config == 3:  # the bias is added with one fused multiply-add there: last-bit differences
-        assert error_stats(a3, a.float().cpu().numpy())["rel_to_max"] <= 2 ** -7
-    else:
-        assert torch.equal(a, a3)  # 64 rows per wave: same per-row arithmetic again
     with ops.force_kernel(ops.KERNEL_GENERIC):
         b = run_hip(wl)
         assert _lib.last_kernel() == "generic_bf16"
@@ -122,7 +115,7 @@ def test_tiled_and_generic_kernels_agree(oracle, config):
     np.testing.assert_array_equal(za, zb)
 
 
-@pytest.mark.parametrize("kernel", ["tiled", "tiled_regstage", "tiled_w64", "generic"])
+@pytest.mark.parametrize("kernel", ["tiled", "tiled_regstage", "generic"])
 @pytest.mark.parametrize("ctx", [0, 5, 200])
 def test_mask_is_bit_exact(oracle, kernel, ctx):
     """Positive constant scores and one-hot values make out[m, c] non-zero exactly when row m keeps a
@@ -141,7 +134,7 @@ def test_mask_is_bit_exact(oracle, kernel, ctx):
     for b, n in enumerate(lengths):
         for j in range(n):
             wl.v[off[b] + j, 0, j % 128] = 1.0
-    variant = {"tiled": ops.KERNEL_TILED_DIRECT, "tiled_regstage": ops.KERNEL_TILED, "tiled_w64": ops.KERNEL_TILED_W64, "generic": ops.KERNEL_GENERIC}[kernel]
+    variant = {"tiled": ops.KERNEL_TILED_DIRECT, "tiled_regstage": ops.KERNEL_TILED, "generic": ops.KERNEL_GENERIC}[kernel]
     with ops.force_kernel(variant):
         out = run_hip(wl).float().cpu().numpy()
     want = np.zeros((wl.T, 128), dtype=bool)
@@ -250,6 +243,33 @@ def test_generic_kernel_head_dims(oracle, shape):
     assert st["rel_to_max"] <= 3e-2, st  # v is also rounded to bf16 here
 
 
+@pytest.mark.parametrize("D,dtype", [(128, "bf16"), (8, "fp32")])
+def test_alpha_default_is_inverse_sqrt_of_head_dim(oracle, D, dtype):
+    """``alpha=None`` means ``1/sqrt(Dqk)`` (recir/ops/pallas/jagged_hstu_attention.py:1550-1555),
+    on the tiled kernel (head dim 128) and on the generic one (head dim 8)."""
+    import math
+
+    import recir_amd
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([150, 3, 70], [20, 0, 70], 2, D, D, max_seq_len=160, alpha=1.0 / math.sqrt(D), dtype=dtype, seed=21,
+                     tail_rows=3)
+    q, k, v, off, nt = to_device(wl)
+    out = recir_amd.jagged_hstu_attention(q, k, v, off, nt, max_seq_len=wl.max_seq_len)  # alpha, attn_scale left out
+    torch.cuda.synchronize()
+    assert _lib.last_kernel().startswith("tiled_d128" if D == 128 else "generic")
+    ref = run_oracle(oracle, wl)  # the oracle gets 1/sqrt(D) explicitly
+    if dtype == "bf16":
+        assert_bf16_close(out, ref, f"alpha=None D={D}")
+    else:
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=FP32_RTOL, atol=FP32_ATOL)
+    # and it is not what another alpha would give (the scores here are O(1), so alpha matters)
+    other = run_oracle(oracle, make_jagged([150, 3, 70], [20, 0, 70], 2, D, D, max_seq_len=160, alpha=1.0 / D, dtype=dtype,
+                                           seed=21, tail_rows=3))
+    assert np.abs(other - ref).max() > 10 * (BF16_REL if dtype == "bf16" else FP32_RTOL) * np.abs(ref).max()
+
+
 def test_many_short_sequences_use_the_general_work_list(oracle):
     """More sequences than the single-block work-list builder tabulates (1024)."""
     from recir_amd import _lib
@@ -332,7 +352,15 @@ def test_work_lists_are_reused_for_the_same_offset_tensors_and_rebuilt_when_they
     e = recir_amd.jagged_hstu_attention(q, k, v, off, nt, **kw)
     assert torch.equal(d, e)
     assert ops.plan_cache_stats["misses"] - before["misses"] == 2 and ops.plan_cache_stats["hits"] - before["hits"] == 2
-    recir_amd.set_plan_cache(True)
+    # a step scope: reuse inside, nothing kept afterwards; offsets that arrive on the host are moved
+    # to the device and still reused (the entry is keyed on the caller's tensors)
+    off_h, nt_h = off.cpu(), nt.cpu()
+    with recir_amd.plan_cache_scope():
+        g1 = recir_amd.jagged_hstu_attention(q, k, v, off_h, nt_h, **kw)
+        g2 = recir_amd.jagged_hstu_attention(q, k, v, off_h, nt_h, **kw)
+    assert torch.equal(g1, d) and torch.equal(g2, d)
+    assert ops.plan_cache_stats["misses"] - before["misses"] == 3 and ops.plan_cache_stats["hits"] - before["hits"] == 3
+    assert not ops._plan_cache and not ops._plan_cache_enabled  # off again, as before the scope
 
 
 def test_rab_zero_is_identical_to_no_rab():
@@ -502,21 +530,6 @@ def test_fp8_region_swap_in_a_traced_graph(oracle):
     assert error_stats(ref_bf16, want)["rel_fro"] <= 2e-2
 
 
-@pytest.mark.parametrize("config", [2, 3, 4, 5])
-def test_w64_kernel_full_size(oracle, config):
-    """The 64-rows-per-wave kernel on the full-size configurations, against the oracle."""
-    from recir_amd import _lib, ops
-    from recir_amd.workloads import make_config
-
-    wl = make_config(config)
-    with ops.force_kernel(ops.KERNEL_TILED_W64):
-        out = run_hip(wl, fp8=(config == 5))
-    assert "w64" in _lib.last_kernel()
-    ref = _fp8_reference(oracle, wl) if config == 5 else run_oracle(oracle, wl)
-    assert_bf16_close(out, ref, f"w64 config{config}")
-    assert_same_zero_structure(out, ref, int(wl.seq_offsets[-1]))
-
-
 def test_semilocal_full_size_matches_oracle(oracle):
     """Configuration 2 with the reference's semi-local shape (256 local + 256 full tail): the tiled
     kernel (which skips key tiles below the window) against the oracle."""
@@ -557,6 +570,6 @@ def test_semilocal_is_rejected_by_the_tilings_without_it():
     from recir_amd.workloads import make_jagged
 
     wl = make_jagged([200], [10], 1, 128, 128, max_seq_len=256, alpha=1.0 / 128, dtype="bf16", max_attn_len=8)
-    for variant in (ops.KERNEL_TILED, ops.KERNEL_TILED_W64):
+    for variant in (ops.KERNEL_TILED,):
         with ops.force_kernel(variant), pytest.raises(ValueError, match="semi-local"):
             run_hip(wl)
