@@ -8,11 +8,13 @@ and a keyword front end with the defaults of the packed accelerator kernel it re
 from .ops import (  # noqa: F401
     hstu_jagged_attention_fwd,
     hstu_jagged_attention_bwd,
+    triton_ragged_attention_fwd,
     jagged_hstu_attention,
     jagged_hstu_attention_backward,
     jagged_hstu_attention_fp8,
     quantize_e4m3_per_head,
     register_swaps,
+    plan_cache_scope,
     set_plan_cache,
     hstu_attention_matcher,
     attention_via_fp8,
@@ -21,7 +23,6 @@ from .ops import (  # noqa: F401
     KERNEL_GENERIC,
     KERNEL_TILED,
     KERNEL_TILED_DIRECT,
-    KERNEL_TILED_W64,
 )
 
 from .jagged import (  # noqa: F401,E402
@@ -38,11 +39,13 @@ from .jagged import (  # noqa: F401,E402
 __all__ = [
     "hstu_jagged_attention_fwd",
     "hstu_jagged_attention_bwd",
+    "triton_ragged_attention_fwd",
     "jagged_hstu_attention",
     "jagged_hstu_attention_backward",
     "jagged_hstu_attention_fp8",
     "quantize_e4m3_per_head",
     "register_swaps",
+    "plan_cache_scope",
     "set_plan_cache",
     "hstu_attention_matcher",
     "attention_via_fp8",

@@ -5,7 +5,9 @@ import ctypes
 import os
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_PKG, "librecir_hstu.so")
+# RECIR_HSTU_LIB names another build of the same library (deployments that keep the binary
+# elsewhere, A/B measurements of two builds); there is still no fallback if it is missing
+LIB_PATH = os.environ.get("RECIR_HSTU_LIB") or os.path.join(_PKG, "librecir_hstu.so")
 
 ABI_VERSION = 3
 

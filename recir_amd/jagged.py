@@ -61,12 +61,25 @@ def _no_cpu(*args, **kwargs):
                        "backed only by the gfx950 HIP library (librecir_hstu.so); move the tensors to the GPU")
 
 
-def _offsets(off: torch.Tensor, like: Optional[torch.Tensor] = None):
+def _offsets(off: torch.Tensor, like: Optional[torch.Tensor] = None, dev=None):
+    """Offsets as the kernels read them: int32 or int64, contiguous, on the device of the values
+    (index tensors may arrive on any device, as with the reference operators, and are moved: a host
+    pointer must never reach a kernel)."""
     if off.dtype not in (torch.int32, torch.int64):
         raise ValueError(f"offsets must be int32 or int64, got {off.dtype}")
     if like is not None and off.dtype != like.dtype:
         off = off.to(like.dtype)
+    if dev is not None:
+        off = off.to(dev)
     return off.contiguous(), (_lib.FLAG_OFFSETS_I32 if off.dtype == torch.int32 else 0)
+
+
+def _same_device(dev, **tensors):
+    """Value tensors must share one device (recir/ops/kjt_split_per_feature.cpp:112-114 checks the
+    same); raised before anything is launched."""
+    for name, t in tensors.items():
+        if t is not None and t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, the values on {dev}")
 
 
 def _row_bytes(t: torch.Tensor, lead_dims: int) -> int:
@@ -107,7 +120,7 @@ def _jagged_to_padded_dense_device(values, offsets: List[torch.Tensor], max_leng
     L = _lib.load()
     if len(offsets) != 1 or len(max_lengths) != 1:
         raise ValueError("one jagged dimension is supported (one offsets tensor, one max length)")
-    off, flags = _offsets(offsets[0])
+    off, flags = _offsets(offsets[0], dev=values.device)
     B, max_len = off.shape[0] - 1, int(max_lengths[0])
     values = values.contiguous()
     out = values.new_empty((B, max_len) + tuple(values.shape[1:]))
@@ -127,7 +140,7 @@ def _jagged_to_padded_dense_device(values, offsets: List[torch.Tensor], max_leng
 def _dense_to_jagged_device(dense, offsets: List[torch.Tensor], total_L: Optional[int] = None):
     _need_cuda("dense_to_jagged", dense)
     L = _lib.load()
-    off, flags = _offsets(offsets[0])
+    off, flags = _offsets(offsets[0], dev=dense.device)
     if total_L is None:
         total_L = int(off[-1].item())  # the reference reads it from the device as well
     dense = dense.contiguous()
@@ -145,6 +158,7 @@ def _dense_to_jagged_device(dense, offsets: List[torch.Tensor], total_L: Optiona
 def _concat_impl(values_a, values_b, offsets_a, offsets_b, is_replace: bool, n_prefix: int):
     _need_cuda("concat_2d_jagged", values_a)
     L = _lib.load()
+    _same_device(values_a.device, values_b=values_b)
     if offsets_a is None and offsets_b is None:
         raise ValueError("at least one input must be jagged")
     if values_a.dtype != values_b.dtype:
@@ -156,9 +170,9 @@ def _concat_impl(values_a, values_b, offsets_a, offsets_b, is_replace: bool, n_p
     oa = ob = None
     dense_a = dense_b = 0
     if offsets_a is not None:
-        oa, flags = _offsets(offsets_a)
+        oa, flags = _offsets(offsets_a, dev=values_a.device)
     if offsets_b is not None:
-        ob, flags = _offsets(offsets_b, oa)
+        ob, flags = _offsets(offsets_b, oa, dev=values_a.device)
         if oa is not None and oa.dtype != ob.dtype:
             oa = oa.to(ob.dtype)
     if oa is None:
@@ -210,9 +224,9 @@ def _split_impl(values, offsets_a, offsets_b, rows_a: int, rows_b: int, dense_a:
     oa = ob = None
     flags = 0
     if not dense_a:
-        oa, flags = _offsets(offsets_a)
+        oa, flags = _offsets(offsets_a, dev=values.device)
     if not dense_b:
-        ob, flags = _offsets(offsets_b, oa)
+        ob, flags = _offsets(offsets_b, oa, dev=values.device)
         if oa is not None and oa.dtype != ob.dtype:
             oa = oa.to(ob.dtype)
     if B is None:
@@ -298,9 +312,11 @@ def _add_ts_pos_emb_fwd_device(seq_embeddings, seq_offsets, pos_embeddings, ts_e
         ts_float = 0
     else:
         raise ValueError(f"timestamps must be int64 or float32, got {timestamps.dtype}")
-    off, flags = _offsets(seq_offsets)
-    lens = seq_lengths.to(off.dtype).contiguous()
-    nt = None if num_targets is None else num_targets.to(off.dtype).contiguous()
+    dev = seq_embeddings.device
+    _same_device(dev, pos_embeddings=pos_embeddings, ts_embeddings=ts_embeddings, timestamps=timestamps)
+    off, flags = _offsets(seq_offsets, dev=dev)
+    lens = seq_lengths.to(device=dev, dtype=off.dtype).contiguous()
+    nt = None if num_targets is None else num_targets.to(device=dev, dtype=off.dtype).contiguous()
     seq = seq_embeddings.contiguous()
     pos, ts_tab, stamps = pos_embeddings.contiguous(), ts_embeddings.contiguous(), timestamps.contiguous()
     rows = seq.shape[0]

@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import collections
 import math
+import threading
 from typing import Optional, Tuple
 
 import torch
@@ -26,7 +27,6 @@ KERNEL_AUTO = 0
 KERNEL_GENERIC = 1
 KERNEL_TILED = 2         # tiled MFMA kernel, K/V staged through registers
 KERNEL_TILED_DIRECT = 3  # tiled MFMA kernel, K/V copied global -> LDS directly
-KERNEL_TILED_W64 = 4     # tiled MFMA kernel, 64 query rows per wave, four-stage LDS ring
 
 _forced_kernel = KERNEL_AUTO
 _ctx_reference_rule = False
@@ -85,11 +85,27 @@ _BWD_SCHEMA = (
     "Tensor? rab=None, int max_attn_len=0, int full_attn_size=0) -> (Tensor, Tensor, Tensor)"
 )
 
+# The reference's own schema (recir/ops/kjt_split_per_feature.cpp:780-783), argument for argument and
+# with the reference's contextual rule (:672-674): the operator a swapped graph node is retargeted to.
+_REF_SCHEMA = (
+    "triton_ragged_attention_fwd(int N, float alpha, Tensor q, Tensor k, Tensor v, "
+    "Tensor seq_offsets, str invalid_attn_mask_type, Tensor? num_targets, Tensor? attn_scale, "
+    "int max_attn_len, int contextual_seq_len, int full_attn_size, int num_softmax_heads=0) "
+    "-> (Tensor, Tensor)"
+)
+_REF_BWD_SCHEMA = (
+    "triton_ragged_attention_bwd(Tensor dout, int N, float alpha, Tensor q, Tensor k, Tensor v, "
+    "Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, int contextual_seq_len, "
+    "int max_attn_len=0, int full_attn_size=0) -> (Tensor, Tensor, Tensor)"
+)
+
 _LIBRARY = torch.library.Library("recir", "FRAGMENT")
 _LIBRARY.define(_SCHEMA)
 _LIBRARY.define(_FP8_SCHEMA)
 _LIBRARY.define(_QUANT_SCHEMA)
 _LIBRARY.define(_BWD_SCHEMA)
+_LIBRARY.define(_REF_SCHEMA)
+_LIBRARY.define(_REF_BWD_SCHEMA)
 
 
 def _check_common(q, k, v, seq_offsets, num_targets, max_seq_len) -> int:
@@ -110,33 +126,43 @@ def _check_common(q, k, v, seq_offsets, num_targets, max_seq_len) -> int:
     return num_sequences
 
 
-def _index_tensors(seq_offsets, num_targets):
-    """Offsets and targets as one integer width the kernels read (int64 or int32)."""
+def _index_tensors(seq_offsets, num_targets, dev=None):
+    """Offsets and targets as one integer width the kernels read (int64 or int32), on ``dev``.  The
+    reference operator accepts them on any device (it copies them to the host,
+    recir/ops/kjt_split_per_feature.cpp:623-626), so they are moved rather than rejected: a host
+    pointer must never reach a kernel."""
     if seq_offsets.dtype not in (torch.int32, torch.int64):
         raise ValueError(f"seq_offsets must be int32 or int64, got {seq_offsets.dtype}")
-    off = seq_offsets.contiguous()
+    dev = seq_offsets.device if dev is None else dev
+    off = seq_offsets.to(dev).contiguous()
     nt = None
     if num_targets is not None:
         if num_targets.dtype not in (torch.int32, torch.int64):
             raise ValueError(f"num_targets must be int32 or int64, got {num_targets.dtype}")
-        nt = num_targets.to(off.dtype).contiguous()
+        nt = num_targets.to(device=dev, dtype=off.dtype).contiguous()
     return off, nt, (_lib.FLAG_OFFSETS_I32 if off.dtype == torch.int32 else 0)
 
 
-def _prepare(opname, q, k, v, seq_offsets, num_targets, attn_scale, rab, N):
+def _check_same_device(dev, **tensors):
+    """Value tensors must live where q lives (the reference checks the same of its inputs,
+    recir/ops/kjt_split_per_feature.cpp:112-114); raised before anything is launched."""
+    for name, t in tensors.items():
+        if t is not None and t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, q on {dev}")
+
+
+def _prepare(opname, q, k, v, seq_offsets, num_targets, attn_scale, rab, N, ctx_reference=False):
     """Checks and device-side argument tensors shared by the forward and backward launches."""
     dev = q.device
     if dev.type != "cuda":
         raise RuntimeError(
             f"recir::{opname} runs on the GPU only (got a tensor on "
             f"'{dev}'); this package has no CPU path")
-    for name, t in (("k", k), ("v", v), ("seq_offsets", seq_offsets)):
-        if t.device != dev:
-            raise ValueError(f"{name} is on {t.device}, q on {dev}")
+    _check_same_device(dev, k=k, v=v)
     B = _check_common(q, k, v, seq_offsets, num_targets, N)
     T, H, _ = q.shape
-    off, nt, flags = _index_tensors(seq_offsets, num_targets)
-    if _ctx_reference_rule:
+    off, nt, flags = _index_tensors(seq_offsets, num_targets, dev)
+    if _ctx_reference_rule or ctx_reference:
         flags |= _lib.FLAG_CTX_REFERENCE
     flags |= (_forced_kernel & 0xFF) << _lib.FLAG_KERNEL_SHIFT
     sc = None
@@ -173,22 +199,48 @@ def _check_window(max_attn_len, full_attn_size):
 
 
 # Work lists depend only on the sequence layout, which the layers of one model step share
-# (cf. RECIR_HSTU_FLAG_REUSE_PLAN): keep the workspace of the last few layouts and let later calls
-# with the very same offset tensors skip the list construction.  An entry holds the tensors it was
-# built from, so their identity cannot be recycled while it lives, and it is valid only while their
-# version counters stand where they stood; a layout changed behind torch's back (a foreign kernel
-# writing into the offsets) is not seen -- switch the cache off for such callers.
+# (cf. RECIR_HSTU_FLAG_REUSE_PLAN).  On request the operator keeps the workspace of the last few
+# layouts and lets later calls with the very same offset tensors skip the list construction.  Off
+# by default: an entry is trusted on the identity, storage and version counter of the offset
+# tensors, and a write that bypasses the version counter (``t.data.copy_``, a DLPack or numpy
+# alias, a kernel torch does not know of, ``set_``) would leave stale lists in use without an error.
+# Callers that own their offsets for the length of a step turn it on for that step
+# (``with plan_cache_scope(): ...``), which also drops the entries, and the references they hold, at
+# the end of the step.
 _PLAN_CACHE_ENTRIES = 8
 _plan_cache = collections.OrderedDict()
-_plan_cache_enabled = True
+_plan_cache_enabled = False
+_plan_cache_lock = threading.Lock()
 plan_cache_stats = {"hits": 0, "misses": 0}
 
 
 def set_plan_cache(enabled: bool) -> None:
-    """Enable or disable the reuse of work lists between calls that pass the same offset tensors."""
+    """Enable or disable (the default) the reuse of work lists between calls that pass the same,
+    unchanged offset tensors.  Either way the cache is emptied."""
     global _plan_cache_enabled
-    _plan_cache_enabled = bool(enabled)
-    _plan_cache.clear()
+    with _plan_cache_lock:
+        _plan_cache_enabled = bool(enabled)
+        _plan_cache.clear()
+
+
+class plan_cache_scope:
+    """Context manager for one model step: work lists are reused by the calls inside it that pass the
+    same offset tensors (the layers of the step), and forgotten when it ends."""
+
+    def __enter__(self):
+        self._prev = _plan_cache_enabled
+        set_plan_cache(True)
+        return self
+
+    def __exit__(self, *exc):
+        set_plan_cache(self._prev)
+        return False
+
+
+def _tensor_key(t):
+    if t is None:
+        return None
+    return (id(t), t.data_ptr(), t.storage_offset(), t.dtype, tuple(t.shape), t._version)
 
 
 def _workspace(kind, seq_offsets, num_targets, layout, ws_bytes, dev, stream):
@@ -199,30 +251,30 @@ def _workspace(kind, seq_offsets, num_targets, layout, ws_bytes, dev, stream):
     if not _plan_cache_enabled or torch.cuda.is_current_stream_capturing():
         return torch.empty((size,), dtype=torch.uint8, device=dev), 0, None
     try:
-        versions = (seq_offsets._version, None if num_targets is None else num_targets._version)
+        key = (kind, _tensor_key(seq_offsets), _tensor_key(num_targets), layout, dev.index, stream, size)
     except RuntimeError:  # inference tensors carry no version counter: nothing to validate an entry with
         return torch.empty((size,), dtype=torch.uint8, device=dev), 0, None
-    key = (kind, id(seq_offsets), id(num_targets), versions, layout, dev.index, stream, size)
-    hit = _plan_cache.get(key)
-    if hit is not None and hit[0] is seq_offsets and hit[1] is num_targets:
-        _plan_cache.move_to_end(key)
-        plan_cache_stats["hits"] += 1
-        return hit[2], _lib.FLAG_REUSE_PLAN, key
-    plan_cache_stats["misses"] += 1
-    ws = torch.empty((size,), dtype=torch.uint8, device=dev)
-    _plan_cache[key] = (seq_offsets, num_targets, ws)
-    while len(_plan_cache) > _PLAN_CACHE_ENTRIES:
-        _plan_cache.popitem(last=False)
+    with _plan_cache_lock:
+        hit = _plan_cache.get(key)
+        if hit is not None and hit[0] is seq_offsets and hit[1] is num_targets:
+            _plan_cache.move_to_end(key)
+            plan_cache_stats["hits"] += 1
+            return hit[2], _lib.FLAG_REUSE_PLAN, key
+        plan_cache_stats["misses"] += 1
+        ws = torch.empty((size,), dtype=torch.uint8, device=dev)
+        _plan_cache[key] = (seq_offsets, num_targets, ws)
+        while len(_plan_cache) > _PLAN_CACHE_ENTRIES:
+            _plan_cache.popitem(last=False)
     return ws, 0, key
 
 
 def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale, N, alpha,
-            contextual_seq_len, dtype_code, max_attn_len=0, full_attn_size=0) -> torch.Tensor:
+            contextual_seq_len, dtype_code, max_attn_len=0, full_attn_size=0, ctx_reference=False) -> torch.Tensor:
     _check_window(max_attn_len, full_attn_size)
     L = _lib.load()
     dev = q.device
     B, off, nt, sc, rb, flags = _prepare("hstu_jagged_attention_fwd", q, k, v, seq_offsets, num_targets,
-                                         attn_scale, rab, N)
+                                         attn_scale, rab, N, ctx_reference)
     T, H, Dqk = q.shape
     Dv = v.shape[2]
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
@@ -241,7 +293,8 @@ def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale
                                    float(alpha), dtype_code, flags | reuse, _ptr(ws), ws.numel(), stream)
     if rc != 0:
         if key is not None:
-            _plan_cache.pop(key, None)
+            with _plan_cache_lock:
+                _plan_cache.pop(key, None)
         _raise_status("recir_hstu_attn_fwd", rc)
     return out
 
@@ -259,13 +312,13 @@ def _dtype_code(q, k, v):
 
 
 def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
-                rab=None, max_attn_len=0, full_attn_size=0):
+                rab=None, max_attn_len=0, full_attn_size=0, ctx_reference=False):
     _check_window(max_attn_len, full_attn_size)
     L = _lib.load()
     dev = q.device
     code = _dtype_code(q, k, v)
     B, off, nt, sc, rb, flags = _prepare("hstu_jagged_attention_bwd", q, k, v, seq_offsets, num_targets,
-                                         attn_scale, rab, N)
+                                         attn_scale, rab, N, ctx_reference)
     if dout.shape != v.shape:
         raise ValueError("dout must have the shape of v, [T, H, Dv]")
     if dout.device != dev:
@@ -288,13 +341,15 @@ def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, c
                                    float(alpha), code, flags | reuse, _ptr(ws), ws.numel(), stream)
     if rc != 0:
         if key is not None:
-            _plan_cache.pop(key, None)
+            with _plan_cache_lock:
+                _plan_cache.pop(key, None)
         _raise_status("recir_hstu_attn_bwd", rc)
     return dq, dk, dv
 
 
 def _fwd_device(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
-                max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads=0, rab=None):
+                max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads=0, rab=None,
+                ctx_reference=False):
     # same rejections as the reference fallback (kjt_split_per_feature.cpp:616-622) plus the
     # non-causal mask types
     if num_softmax_heads != 0:
@@ -303,8 +358,20 @@ def _fwd_device(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targ
         raise ValueError("only the causal mask ('lower_triangular') is supported")
     code = _dtype_code(q, k, v)
     out = _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, None, None, N, alpha,
-                  contextual_seq_len, code, max_attn_len, full_attn_size)
+                  contextual_seq_len, code, max_attn_len, full_attn_size, ctx_reference)
     return out, torch.zeros((1,), dtype=torch.float32, device=q.device)
+
+
+def _ref_fwd_device(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
+                    max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads=0):
+    return _fwd_device(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
+                       max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads, None, True)
+
+
+def _ref_bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
+                    max_attn_len=0, full_attn_size=0):
+    return _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
+                       None, max_attn_len, full_attn_size, True)
 
 
 def _fp8_fwd_device(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, num_targets,
@@ -356,6 +423,10 @@ _LIBRARY.impl("hstu_jagged_attention_fwd", _fwd_device, "CUDA")
 _LIBRARY.impl("hstu_jagged_attention_fp8_fwd", _fp8_fwd_device, "CUDA")
 _LIBRARY.impl("hstu_quantize_e4m3_per_head", _quant_device, "CUDA")
 _LIBRARY.impl("hstu_jagged_attention_bwd", _bwd_device, "CUDA")
+_LIBRARY.impl("triton_ragged_attention_fwd", _ref_fwd_device, "CUDA")
+_LIBRARY.impl("triton_ragged_attention_bwd", _ref_bwd_device, "CUDA")
+_LIBRARY.impl("triton_ragged_attention_fwd", _no_cpu, "CPU")
+_LIBRARY.impl("triton_ragged_attention_bwd", _no_cpu, "CPU")
 _LIBRARY.impl("hstu_jagged_attention_bwd", _no_cpu, "CPU")
 _LIBRARY.impl("hstu_jagged_attention_fwd", _no_cpu, "CPU")
 _LIBRARY.impl("hstu_jagged_attention_fp8_fwd", _no_cpu, "CPU")
@@ -368,6 +439,20 @@ def _fwd_fake(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_target
     _check_common(q, k, v, seq_offsets, num_targets, N)
     # packed layout is kept: dim 0 of the output is dim 0 of q (recir/compiler/batch_dim.py:309-318)
     return v.new_empty((q.shape[0], q.shape[1], v.shape[2])), q.new_empty((1,), dtype=torch.float32)
+
+
+@torch.library.register_fake("recir::triton_ragged_attention_fwd")
+def _ref_fwd_fake(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
+                  max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads=0):
+    _check_common(q, k, v, seq_offsets, num_targets, N)
+    return v.new_empty((q.shape[0], q.shape[1], v.shape[2])), q.new_empty((1,), dtype=torch.float32)
+
+
+@torch.library.register_fake("recir::triton_ragged_attention_bwd")
+def _ref_bwd_fake(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
+                  max_attn_len=0, full_attn_size=0):
+    _check_common(q, k, v, seq_offsets, num_targets, N)
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 @torch.library.register_fake("recir::hstu_jagged_attention_fp8_fwd")
@@ -411,8 +496,30 @@ def _autograd_backward(ctx, grad_out, _grad_aux):
 torch.library.register_autograd("recir::hstu_jagged_attention_fwd", _autograd_backward,
                                 setup_context=_setup_context)
 
+
+
+def _ref_setup_context(ctx, inputs, output):
+    (N, alpha, q, k, v, seq_offsets, _mask_type, num_targets, attn_scale, max_attn_len,
+     contextual_seq_len, full_attn_size, _num_softmax_heads) = inputs
+    ctx.save_for_backward(q, k, v, seq_offsets, num_targets, attn_scale)
+    ctx.hstu_args = (int(N), float(alpha), int(contextual_seq_len), int(max_attn_len), int(full_attn_size))
+
+
+def _ref_autograd_backward(ctx, grad_out, _grad_aux):
+    q, k, v, seq_offsets, num_targets, attn_scale = ctx.saved_tensors
+    N, alpha, contextual_seq_len, max_attn_len, full_attn_size = ctx.hstu_args
+    dq, dk, dv = torch.ops.recir.triton_ragged_attention_bwd(
+        grad_out, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
+        max_attn_len, full_attn_size)
+    return (None, None, dq, dk, dv, None, None, None, None, None, None, None, None)
+
+
+torch.library.register_autograd("recir::triton_ragged_attention_fwd", _ref_autograd_backward,
+                                setup_context=_ref_setup_context)
+
 hstu_jagged_attention_fwd = torch.ops.recir.hstu_jagged_attention_fwd
 hstu_jagged_attention_bwd = torch.ops.recir.hstu_jagged_attention_bwd
+triton_ragged_attention_fwd = torch.ops.recir.triton_ragged_attention_fwd
 
 
 def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len: int,
@@ -493,7 +600,8 @@ def hstu_attention_matcher(node) -> bool:
     attention operator, under this package's name or the reference's."""
     if node.op != "call_function":
         return False
-    targets = [hstu_jagged_attention_fwd, hstu_jagged_attention_fwd.default]
+    targets = [hstu_jagged_attention_fwd, hstu_jagged_attention_fwd.default,
+               triton_ragged_attention_fwd, triton_ragged_attention_fwd.default]
     try:
         src = torch.ops.hammer.triton_ragged_attention_fwd
         targets += [src, src.default]
@@ -557,7 +665,13 @@ def fp8_attention_region(region_gm):
 def register_swaps(registry) -> int:
     """Fill a RecIR ``OpSwapRegistry`` (recir/lowering/op_swap.py:16-75) with every source operator
     present in this process that the HIP operator can replace argument-for-argument.  Returns the
-    number of mappings added."""
+    number of mappings added.
+
+    ``hammer::triton_ragged_attention_fwd`` maps onto ``recir::triton_ragged_attention_fwd``: the same
+    schema and the same contextual rule as the operator it replaces (keys whose target-clamped id is
+    0, recir/ops/kjt_split_per_feature.cpp:672-674), so a swapped graph returns the numbers of the
+    original for every ``contextual_seq_len``.  ``recir::hstu_jagged_attention_fwd`` (prefix rule,
+    optional bias) is for direct callers."""
     added = 0
     candidates = (("hammer", "triton_ragged_attention_fwd"),)
     for ns, name in candidates:
@@ -567,7 +681,7 @@ def register_swaps(registry) -> int:
             continue
         for target in (packet, getattr(packet, "default", None)):
             if target is not None:
-                replacement = hstu_jagged_attention_fwd if target is packet else hstu_jagged_attention_fwd.default
+                replacement = triton_ragged_attention_fwd if target is packet else triton_ragged_attention_fwd.default
                 registry.register(target, replacement)
                 added += 1
     return added

@@ -140,6 +140,29 @@ def test_cpu_tensors_fail_loudly():
         recir_amd.jagged_hstu_attention(q, q, q, off, max_seq_len=4)
 
 
+def test_index_tensors_follow_the_values_and_value_tensors_on_another_device_raise():
+    """No host pointer may reach a kernel: offsets and target counts are moved to the device of q
+    (the reference accepts them anywhere, recir/ops/kjt_split_per_feature.cpp:623-626), value tensors
+    elsewhere are an error raised before any launch.  Nothing here touches a GPU."""
+    from recir_amd import jagged, ops
+
+    off = torch.tensor([0, 3, 5], dtype=torch.int64)
+    nt = torch.tensor([1, 0], dtype=torch.int32)
+    meta = torch.device("meta")
+    o, t, flags = ops._index_tensors(off, nt, meta)
+    assert o.device == meta and t.device == meta and t.dtype == torch.int64 and flags == 0
+    o, t, flags = ops._index_tensors(off.int(), None, meta)
+    assert o.device == meta and t is None and flags == ops._lib.FLAG_OFFSETS_I32
+    o, _ = jagged._offsets(off, dev=meta)
+    assert o.device == meta
+    gpu = torch.device("cuda:0")  # only a name here: nothing is allocated on it
+    with pytest.raises(ValueError, match="v is on cpu, q on cuda:0"):
+        ops._check_same_device(gpu, k=None, v=torch.zeros(1))
+    with pytest.raises(ValueError, match="timestamps is on cpu"):
+        jagged._same_device(gpu, pos_embeddings=None, timestamps=torch.zeros(1))
+    ops._check_same_device(torch.device("cpu"), k=torch.zeros(1), v=None)
+
+
 def test_shape_errors_match_reference_messages():
     # recir/ops/pallas/tests/test_jagged_hstu_attention.py:679-690 ("shape [B]") and the validator
     # at recir/ops/pallas/jagged_hstu_attention.py:1498-1515
