@@ -93,21 +93,47 @@ def cpu_baseline(wl, flops, budget_s=20.0):
 
 
 def measured_traffic(config, kernel_name):
-    """HBM bytes per launch of the attention kernel from the committed counter summary
-    (FETCH_SIZE + WRITE_SIZE, scaled by the plain-copy calibration), or None if there is none for
-    this workload and kernel."""
+    """(HBM bytes per launch, where the figure comes from) of the attention kernel, read from the
+    committed counter summary (FETCH_SIZE + WRITE_SIZE, scaled by the plain-copy calibration): hardware
+    counters need a profiler run of their own, so the figure is replayed here, not measured.
+    (None, None) if there is no summary for this workload and kernel."""
     path = os.path.join(ROOT, "profiles", f"hstu_fwd_tiled_d128_config{config}_pmc.txt")
     try:
         text = open(path).read()
     except OSError:
         return None
-    kernel = traffic = None
+    kernel = traffic = date = None
     for line in text.splitlines():
         if line.startswith("kernel_variant:"):
             kernel = line.split(":", 1)[1].strip()
         if line.startswith("traffic_bytes_per_launch:"):
             traffic = float(line.split(":", 1)[1].strip())
-    return traffic if kernel == kernel_name else None
+        if line.startswith("measured:"):
+            date = line.split(":", 1)[1].strip()
+    if kernel != kernel_name or traffic is None:
+        return None, None
+    return traffic, f"profiles/{os.path.basename(path)} (rocprofv3 --pmc run of {date or 'an earlier date'}; not measured in this run)"
+
+
+MIN_WARMUP_MS = 30.0
+
+
+def steady_state_warmup(call, stream, min_ms=MIN_WARMUP_MS):
+    """Untimed calls until at least ``min_ms`` of device time have passed on ``stream``: the GPU needs
+    about 15 ms of continuous work to settle its clocks, whatever ``--warmup`` says.  Returns the
+    device milliseconds spent."""
+    import torch
+
+    spent = 0.0
+    while spent < min_ms:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(50):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        spent += e0.elapsed_time(e1)
+    return spent
 
 
 def bench_backward(args, wl, L, dev):
@@ -144,6 +170,7 @@ def bench_backward(args, wl, L, dev):
         if rc != 0:
             raise RuntimeError(f"recir_hstu_attn_bwd failed ({rc}): {_lib.last_error()}")
 
+    warmup_ms = steady_state_warmup(call, stream)
     for _ in range(args.warmup):
         call()
     torch.cuda.synchronize()
@@ -164,7 +191,7 @@ def bench_backward(args, wl, L, dev):
     print(json.dumps({
         "metric": "HSTU jagged attention bwd (dq, dk, dv), achieved TFLOP/s on unmasked FLOPs (5 products per pair)",
         "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "warmup_ms": warmup_ms, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": wl.dtype, "data": "synthetic",
         "config": {"workload": describe(wl, args.config), "flops_per_call": flops, "kernel": _lib.last_kernel()},
         "roofline": {"bound": "mfma", "achieved": flops / (kern_ms * 1e-3) / 1e12, "peak": peak, "unit": "TFLOP/s",
@@ -314,6 +341,7 @@ def main():
     flops = wl.flops()
     abytes = wl.algorithmic_bytes()
 
+    warmup_ms = steady_state_warmup(call, stream)
     for _ in range(args.warmup):
         call()
     torch.cuda.synchronize()
@@ -351,11 +379,13 @@ def main():
 
     peak = PEAK_TFLOPS[wl.dtype]
     achieved = flops / (kern_ms * 1e-3) / 1e12
+    traffic, traffic_source = measured_traffic(args.config, kernel_name)
     result = {
         "metric": "HSTU jagged attention fwd, achieved TFLOP/s on unmasked FLOPs (ms/call in ms_per_step; % of MFMA peak in roofline.frac)",
         "value": flops / (ms_per_step * 1e-3) / 1e12,
         "unit": "TFLOP/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "warmup_ms": warmup_ms,  # device time of the untimed calls before --warmup (steady clocks)
         "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": wl.dtype, "data": "synthetic",
@@ -365,7 +395,7 @@ def main():
         "latency_ms": {"p50": lat[len(lat) // 2], "p95": lat[int(len(lat) * 0.95) - 1], "p99": lat[-1],
                        "mean": sum(lat) / len(lat)},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
-                     "frac": achieved / peak, "traffic": measured_traffic(args.config, kernel_name), "kernel_ms": kern_ms,
+                     "frac": achieved / peak, "traffic": traffic, "traffic_source": traffic_source, "kernel_ms": kern_ms,
                      "hbm_gbs_algorithmic": abytes / (kern_ms * 1e-3) / 1e9,
                      "hbm_frac_algorithmic": abytes / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBS},
     }
