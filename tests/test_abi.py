@@ -247,7 +247,10 @@ def test_swap_registry_retargets_a_traced_node():
 
 
 def test_register_swaps_fills_a_registry():
+    """Two mappings (overload packet and ``.default``) once the reference's operator is in the process,
+    none before; tests/test_swap_wiring.py runs a swapped graph."""
     import recir_amd
+    from oracle import hstu_oracle
 
     class Registry:  # same surface as recir.lowering.op_swap.OpSwapRegistry.register
         def __init__(self):
@@ -256,9 +259,14 @@ def test_register_swaps_fills_a_registry():
         def register(self, source_op, replace_op):
             self.map[source_op] = replace_op
 
+    if not hstu_oracle.ref_available():
+        reg = Registry()
+        assert recir_amd.register_swaps(reg) == 0 and not reg.map
+        return
+    src = hstu_oracle.ref_op()
     reg = Registry()
-    n = recir_amd.register_swaps(reg)
-    assert n == len(reg.map)  # 0 unless the reference's hammer op is loaded in this process
+    assert recir_amd.register_swaps(reg) == 2
+    assert reg.map == {src: recir_amd.triton_ragged_attention_fwd, src.default: recir_amd.triton_ragged_attention_fwd.default}
 
 
 def _attention_graph():
