@@ -101,7 +101,7 @@ def measured_traffic(config, kernel_name):
     try:
         text = open(path).read()
     except OSError:
-        return None
+        return None, None
     kernel = traffic = date = None
     for line in text.splitlines():
         if line.startswith("kernel_variant:"):
