@@ -154,6 +154,7 @@ def bench_backward(args, wl, L, dev):
     off, nt = wl.seq_offsets.to(dev), wl.num_targets.to(dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     rab = None if wl.rab is None else wl.rab.to(dev)
+    drab = torch.empty_like(rab) if (args.rab_grad and rab is not None) else None
     T, H, Dqk = q.shape
     Dv = v.shape[2]
     code = _lib.DTYPE_FP32 if wl.dtype == "fp32" else _lib.DTYPE_BF16
@@ -163,7 +164,7 @@ def bench_backward(args, wl, L, dev):
 
     def call(flags=0):
         rc = L.recir_hstu_attn_bwd(dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), dq.data_ptr(),
-                                   dk.data_ptr(), dv.data_ptr(), off.data_ptr(), nt.data_ptr(),
+                                   dk.data_ptr(), dv.data_ptr(), None if drab is None else drab.data_ptr(), off.data_ptr(), nt.data_ptr(),
                                    None if rab is None else rab.data_ptr(), None,
                                    T, wl.B, H, Dqk, Dv, wl.max_seq_len, wl.contextual_seq_len, wl.max_attn_len,
                                    wl.full_attn_size, wl.alpha, code, flags0 | flags, ws.data_ptr(), ws.numel(), ctypes.c_void_p(stream.cuda_stream))
@@ -193,7 +194,8 @@ def bench_backward(args, wl, L, dev):
         "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "warmup_ms": warmup_ms, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": wl.dtype, "data": "synthetic",
-        "config": {"workload": describe(wl, args.config), "flops_per_call": flops, "kernel": _lib.last_kernel()},
+        "config": {"workload": describe(wl, args.config), "flops_per_call": flops, "kernel": _lib.last_kernel(),
+                   "rab_grad": drab is not None},
         "roofline": {"bound": "mfma", "achieved": flops / (kern_ms * 1e-3) / 1e12, "peak": peak, "unit": "TFLOP/s",
                      "frac": flops / (kern_ms * 1e-3) / 1e12 / peak, "traffic": None, "kernel_ms": kern_ms},
     }))
@@ -266,6 +268,7 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", type=int, default=0, help="kernel selector (0 auto)")
+    ap.add_argument("--rab-grad", action="store_true", help="with --backward and a configuration that has a bias table: its gradient too")
     ap.add_argument("--backward", action="store_true",
                     help="measure the backward entry point (dq, dk, dv) instead of the forward; "
                          "prints its own JSON line (not the headline metric)")

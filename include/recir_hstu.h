@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define RECIR_HSTU_ABI_VERSION 3
+#define RECIR_HSTU_ABI_VERSION 4
 
 /* element types of q/k (v and out follow: bf16 for BF16 and FP8_E4M3, fp32 for FP32) */
 #define RECIR_HSTU_DTYPE_BF16 0
@@ -132,12 +132,18 @@ size_t recir_hstu_attn_fwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int3
  * q, k, v       the forward's inputs (bf16 or fp32; FP8_E4M3 is not supported)
  * dq, dk        device, [T, H, Dqk]; dv device, [T, H, Dv]; same element type as q; written in full
  *               (rows >= seq_offsets[B] zeroed, recir/ops/helion/jagged_hstu_attention.py:916-920)
- * rab           enters S as in the forward; no gradient is produced for it
+ * rab           enters S as in the forward
+ * drab          device float [H, 2*max_seq_len-1] or NULL: gradient of rab (needs rab),
+ *               drab[h, i] = sum of dS(m, j) over the kept pairs of all sequences with
+ *               m - j + max_seq_len - 1 == i.  Written in full (zeroed first); accumulated with
+ *               float atomics, so its last bits may differ from run to run, unlike dq, dk and dv.
+ *               No counterpart in the reference (which has no rab).  No gradient is produced for
+ *               attn_scale.
  * attn_scale, flags, sizes, workspace, hip_stream: as for the forward; workspace of at least
  *               recir_hstu_attn_bwd_workspace_bytes(...) bytes
  */
 int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const void* v, void* dq,
-                        void* dk, void* dv, const void* seq_offsets, const void* num_targets,
+                        void* dk, void* dv, float* drab, const void* seq_offsets, const void* num_targets,
                         const float* rab, const float* attn_scale, int32_t T, int32_t B, int32_t H,
                         int32_t Dqk, int32_t Dv, int32_t max_seq_len, int32_t contextual_seq_len,
                         int32_t max_attn_len, int32_t full_attn_size, float alpha, int32_t dtype,

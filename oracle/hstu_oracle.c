@@ -30,6 +30,9 @@
  * independent closed forms of the mask compared exhaustively, closed-form
  * special cases (single token, all-target, constant score => kept-key count),
  * and torch's own float8_e4m3fn cast for the encoder.
+ * The gradient of the bias table (hstu_oracle_attn_bwd_rab) has no counterpart in the reference
+ * either; it is pinned by torch autograd through the dense float64 restatement in
+ * tests/test_oracle_bwd.py and by finite differences of the forward oracle.
  * The backward is pinned the way the reference pins its own kernels
  * (recir/ops/helion/jagged_hstu_attention.py:260-280, autograd through the forward): against
  * torch autograd through the reference's compiled C++ forward op, against torch autograd through
@@ -231,12 +234,15 @@ int hstu_oracle_attn_fwd_sl(const float* q, const float* k, const float* v, floa
  * p_round: 1 rounds P and dS to bf16 before they are used as matmul operands (what a bf16 kernel
  *          does); 0 keeps them in double.
  */
-int hstu_oracle_attn_bwd_sl(const float* dout, const float* q, const float* k, const float* v, float* dq,
-                            float* dk, float* dv, const int64_t* seq_offsets,
-                            const int64_t* num_targets, const float* rab, int attn_scale_kind,
-                            const float* attn_scale, int64_t T, int64_t B, int64_t H, int64_t Dqk,
-                            int64_t Dv, int64_t max_seq_len, int64_t ctx, int ctx_mode, double alpha,
-                            int p_round, int64_t max_attn_len, int64_t full_attn_size) {
+/* drab (may be NULL): gradient of the bias table, [H, 2 * max_seq_len - 1] doubles, the sum of
+ * dS(m, j) over all kept pairs of all sequences with m - j + max_seq_len - 1 equal to the column
+ * (the score is alpha q.k + rab, so d score / d rab = 1).  No counterpart in the reference. */
+int hstu_oracle_attn_bwd_rab(const float* dout, const float* q, const float* k, const float* v, float* dq,
+                             float* dk, float* dv, double* drab, const int64_t* seq_offsets,
+                             const int64_t* num_targets, const float* rab, int attn_scale_kind,
+                             const float* attn_scale, int64_t T, int64_t B, int64_t H, int64_t Dqk,
+                             int64_t Dv, int64_t max_seq_len, int64_t ctx, int ctx_mode, double alpha,
+                             int p_round, int64_t max_attn_len, int64_t full_attn_size) {
   for (int64_t b = 0; b < B; ++b) {
     const int64_t s = seq_offsets[b], e = seq_offsets[b + 1];
     if (!(0 <= s && s <= e && e <= T)) return -1;
@@ -245,6 +251,7 @@ int hstu_oracle_attn_bwd_sl(const float* dout, const float* q, const float* k, c
   memset(dk, 0, sizeof(float) * (size_t)(T * H * Dqk));
   memset(dv, 0, sizeof(float) * (size_t)(T * H * Dv));
   const int64_t rab_w = 2 * max_seq_len - 1;
+  if (drab) memset(drab, 0, sizeof(double) * (size_t)(H * rab_w));
 
   /* one (sequence, head) per task: every output row is owned by exactly one task */
 #pragma omp parallel for collapse(2) schedule(dynamic, 1)
@@ -253,6 +260,7 @@ int hstu_oracle_attn_bwd_sl(const float* dout, const float* q, const float* k, c
       const int64_t s = seq_offsets[b], e = seq_offsets[b + 1], n = e - s;
       const int64_t t = num_targets ? num_targets[b] : 0;
       if (n <= 0) continue;
+      double* adrab = drab ? (double*)calloc((size_t)rab_w, sizeof(double)) : NULL;
       double* adq = (double*)calloc((size_t)(n * Dqk), sizeof(double));
       double* adk = (double*)calloc((size_t)(n * Dqk), sizeof(double));
       double* adv = (double*)calloc((size_t)(n * Dv), sizeof(double));
@@ -283,6 +291,10 @@ int hstu_oracle_attn_bwd_sl(const float* dout, const float* q, const float* k, c
             p = (double)round_to_bf16((float)p);
             ds = (double)round_to_bf16((float)ds);
           }
+          if (adrab) {
+            const int64_t idx = m - j + max_seq_len - 1;
+            if (idx >= 0 && idx < rab_w) adrab[idx] += ds;
+          }
           for (int64_t d = 0; d < Dv; ++d) adv[j * Dv + d] += p * (double)gr[d];
           for (int64_t d = 0; d < Dqk; ++d) {
             adq[m * Dqk + d] += ds * (double)kr[d];
@@ -297,12 +309,29 @@ int hstu_oracle_attn_bwd_sl(const float* dout, const float* q, const float* k, c
         }
         for (int64_t d = 0; d < Dv; ++d) dv[((s + m) * H + h) * Dv + d] = (float)adv[m * Dv + d];
       }
+      if (adrab) {
+        /* sequences of one head add into the same row: one at a time */
+#pragma omp critical(hstu_oracle_drab)
+        for (int64_t i = 0; i < rab_w; ++i) drab[h * rab_w + i] += adrab[i];
+        free(adrab);
+      }
       free(adq);
       free(adk);
       free(adv);
     }
   }
   return 0;
+}
+
+int hstu_oracle_attn_bwd_sl(const float* dout, const float* q, const float* k, const float* v, float* dq,
+                            float* dk, float* dv, const int64_t* seq_offsets,
+                            const int64_t* num_targets, const float* rab, int attn_scale_kind,
+                            const float* attn_scale, int64_t T, int64_t B, int64_t H, int64_t Dqk,
+                            int64_t Dv, int64_t max_seq_len, int64_t ctx, int ctx_mode, double alpha,
+                            int p_round, int64_t max_attn_len, int64_t full_attn_size) {
+  return hstu_oracle_attn_bwd_rab(dout, q, k, v, dq, dk, dv, NULL, seq_offsets, num_targets, rab, attn_scale_kind,
+                                  attn_scale, T, B, H, Dqk, Dv, max_seq_len, ctx, ctx_mode, alpha, p_round,
+                                  max_attn_len, full_attn_size);
 }
 
 /* Causal forms (max_attn_len = full_attn_size = 0). */

@@ -61,6 +61,8 @@ def lib() -> ctypes.CDLL:
         L.hstu_oracle_attn_fwd_sl.restype = c_int
         L.hstu_oracle_attn_bwd_sl.argtypes = L.hstu_oracle_attn_bwd.argtypes + [i64, i64]
         L.hstu_oracle_attn_bwd_sl.restype = c_int
+        L.hstu_oracle_attn_bwd_rab.argtypes = [vp] * 11 + [c_int, vp] + [i64] * 7 + [c_int, ctypes.c_double, c_int, i64, i64]
+        L.hstu_oracle_attn_bwd_rab.restype = c_int
         for name in ("hstu_oracle_keep_sl", "hstu_oracle_keep_sl_clamp_id"):
             fn = getattr(L, name)
             fn.argtypes = [i64, i64, i64, i64, i64, c_int, i64, i64]
@@ -147,11 +149,13 @@ def attn_fwd(q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn
 
 def attn_bwd(dout, q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn_scale=None,
              rab=None, contextual_seq_len=0, ctx_mode=CTX_PREFIX, round_bf16=False,
-             max_attn_len=0, full_attn_size=0):
+             max_attn_len=0, full_attn_size=0, rab_grad=False):
     """Gradients (dq, dk, dv) of ``attn_fwd`` for the upstream gradient ``dout`` [T,H,Dv]; float32 arrays.
 
     Same argument conventions as ``attn_fwd``.  ``round_bf16`` rounds P and dS to bf16 before the
-    products that consume them (what a bf16 kernel does).  No gradient is produced for ``rab``.
+    products that consume them (what a bf16 kernel does).  With ``rab_grad`` a fourth array is
+    returned, the gradient of the bias table ``[H, 2*max_seq_len-1]`` in float64 (the sum of dS over
+    the kept pairs of every diagonal; no counterpart in the reference).
     """
     dout, q, k, v = _f32(dout), _f32(q), _f32(k), _f32(v)
     T, H, Dqk = q.shape
@@ -173,13 +177,20 @@ def attn_bwd(dout, q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha
     dq = np.empty((T, H, Dqk), dtype=np.float32)
     dk = np.empty((T, H, Dqk), dtype=np.float32)
     dv = np.empty((T, H, Dv), dtype=np.float32)
-    rc = lib().hstu_oracle_attn_bwd_sl(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv),
-                                       _ptr(off), _ptr(nt), _ptr(rb), kind, _ptr(sc), T, B, H, Dqk, Dv,
-                                       int(max_seq_len), int(contextual_seq_len), int(ctx_mode),
-                                       float(alpha), 1 if round_bf16 else 0, int(max_attn_len),
-                                       int(full_attn_size))
+    drab = None
+    if rab_grad:
+        if rb is None:
+            raise ValueError("rab_grad needs rab")
+        drab = np.zeros((H, 2 * max_seq_len - 1), dtype=np.float64)
+    rc = lib().hstu_oracle_attn_bwd_rab(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv),
+                                        _ptr(drab), _ptr(off), _ptr(nt), _ptr(rb), kind, _ptr(sc), T, B, H, Dqk, Dv,
+                                        int(max_seq_len), int(contextual_seq_len), int(ctx_mode),
+                                        float(alpha), 1 if round_bf16 else 0, int(max_attn_len),
+                                        int(full_attn_size))
     if rc != 0:
         raise ValueError("invalid jagged range in seq_offsets")
+    if rab_grad:
+        return dq, dk, dv, drab
     return dq, dk, dv
 
 

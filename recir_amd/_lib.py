@@ -9,7 +9,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 # elsewhere, A/B measurements of two builds); there is still no fallback if it is missing
 LIB_PATH = os.environ.get("RECIR_HSTU_LIB") or os.path.join(_PKG, "librecir_hstu.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_BF16 = 0
 DTYPE_FP32 = 1
@@ -70,7 +70,7 @@ def load() -> ctypes.CDLL:
     L.recir_hstu_attn_fwd_noalloc.restype = ctypes.c_int
     L.recir_hstu_attn_fwd_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     L.recir_hstu_attn_fwd_workspace_bytes.restype = sz
-    L.recir_hstu_attn_bwd.argtypes = [vp] * 11 + [i32] * 9 + [f32, i32, u32, vp, sz, vp]
+    L.recir_hstu_attn_bwd.argtypes = [vp] * 12 + [i32] * 9 + [f32, i32, u32, vp, sz, vp]
     L.recir_hstu_attn_bwd.restype = ctypes.c_int
     L.recir_hstu_attn_bwd_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     L.recir_hstu_attn_bwd_workspace_bytes.restype = sz

@@ -295,13 +295,18 @@ constexpr size_t WS_HEADER = 64;
 
 template <bool SEMI, bool HAS_RAB>
 void launch_bwd_tiled_as(dim3 grid, hipStream_t stream, const BwdParams& bk, const BwdParams& bq) {
-  if (bk.f.attn_scale && (bk.f.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN)) {
-    hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB, true>), grid, dim3(256), 0, stream, bk);
-    hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, HAS_RAB, true>), grid, dim3(256), 0, stream, bq);
-  } else {
-    hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB, false>), grid, dim3(256), 0, stream, bk);
-    hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, HAS_RAB, false>), grid, dim3(256), 0, stream, bq);
+  const bool per_token = bk.f.attn_scale && (bk.f.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
+  if (per_token) hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB, true>), grid, dim3(256), 0, stream, bk);
+  else hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB, false>), grid, dim3(256), 0, stream, bk);
+  if constexpr (HAS_RAB) {
+    if (bq.drab) {  // the query-tile kernel also sums dS along the diagonals
+      if (per_token) hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, true, true, true>), grid, dim3(256), 0, stream, bq);
+      else hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, true, false, true>), grid, dim3(256), 0, stream, bq);
+      return;
+    }
   }
+  if (per_token) hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, HAS_RAB, true>), grid, dim3(256), 0, stream, bq);
+  else hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, HAS_RAB, false>), grid, dim3(256), 0, stream, bq);
 }
 void launch_bwd_tiled(bool semi, bool has_rab, dim3 grid, hipStream_t stream, const BwdParams& bk, const BwdParams& bq) {
   if (semi) {
@@ -537,7 +542,7 @@ size_t recir_hstu_attn_bwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int3
 }
 
 int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const void* v, void* dq,
-                        void* dk, void* dv, const void* seq_offsets, const void* num_targets,
+                        void* dk, void* dv, float* drab, const void* seq_offsets, const void* num_targets,
                         const float* rab, const float* attn_scale, int32_t T, int32_t B, int32_t H,
                         int32_t Dqk, int32_t Dv, int32_t max_seq_len, int32_t contextual_seq_len,
                         int32_t max_attn_len, int32_t full_attn_size, float alpha, int32_t dtype,
@@ -554,6 +559,12 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   if (dtype != RECIR_HSTU_DTYPE_BF16 && dtype != RECIR_HSTU_DTYPE_FP32)
     return fail(dtype == RECIR_HSTU_DTYPE_FP8_E4M3 ? RECIR_HSTU_ERR_UNSUPPORTED : RECIR_HSTU_ERR_INVALID_ARGUMENT,
                 "backward supports bf16 and fp32 tensors, got dtype %d", dtype);
+  if (drab && !rab) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "drab (the gradient of rab) needs rab");
+  if (drab) {  // written in full whatever follows: zeros, then the kernels add
+    const size_t n = (size_t)H * (2 * (size_t)max_seq_len - 1);
+    hipLaunchKernelGGL(hstu_fill_zero, dim3(64), dim3(256), 0, stream, (unsigned short*)drab, n * 2);
+    if (int rc = launch_status("hstu_fill_zero")) return rc;
+  }
   if (T == 0) return RECIR_HSTU_OK;
   if (!dout || !q || !k || !v || !dq || !dk || !dv)
     return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "dout, q, k, v, dq, dk, dv must be non-null");
@@ -569,7 +580,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   p.alpha = alpha; p.flags = flags;
   p.max_attn_len = max_attn_len; p.full_attn_size = full_attn_size;
   const bool semi = max_attn_len > 0;
-  bp.dout = dout; bp.dq = dq; bp.dk = dk; bp.dv = dv;
+  bp.dout = dout; bp.dq = dq; bp.dk = dk; bp.dv = dv; bp.drab = drab;
 
   const bool bf16 = dtype == RECIR_HSTU_DTYPE_BF16;
   const size_t esz = bf16 ? 2 : 4;

@@ -165,7 +165,13 @@ __device__ __forceinline__ void bwd_band_store(float* band, float val, int tid) 
 // SEMI: semi-local mask (max_attn_len > 0), as in the forward kernel.
 // HAS_RAB: scores carry the relative bias rab[h, query - key + N - 1] (no gradient flows to it).
 // PER_TOKEN: the output scale is a [T] vector; P and dS of query row m carry attn_scale[m].
-template <bool SEMI, bool HAS_RAB, bool PER_TOKEN>
+// RAB_GRAD (with HAS_RAB): also the gradient of the bias table, drab[h, m - j + N - 1] += dS(m, j).
+//   The dS of a tile are added into an LDS band with the bias band's own indexing (ds_add_f32; the
+//   elements one instruction adds lie on different diagonals up to a two-way overlap of the lane
+//   halves), and the band of a finished tile is flushed to global memory with one float atomic
+//   per diagonal while the next tile computes into the other stage.  Sums of floats in
+//   arrival order: not bitwise reproducible, unlike dq, dk and dv.
+template <bool SEMI, bool HAS_RAB, bool PER_TOKEN, bool RAB_GRAD = false>
 __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp) {
   const Params& p = bp.f;
   __shared__ __attribute__((aligned(1024))) unsigned short Ks0[BWD_BN * HD];
@@ -174,6 +180,9 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
   __shared__ __attribute__((aligned(1024))) unsigned short Vs1[BWD_BN * HD];
   __shared__ float band0[HAS_RAB ? BWD_BAND : 1];
   __shared__ float band1[HAS_RAB ? BWD_BAND : 1];
+  __shared__ float gband0[RAB_GRAD ? BWD_BAND : 1];
+  __shared__ float gband1[RAB_GRAD ? BWD_BAND : 1];
+  static_assert(!RAB_GRAD || HAS_RAB, "the bias gradient needs the bias");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -183,6 +192,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
   const BwdLanes lc = bwd_lanes(lane);
 
   zero_tail_rows_of<256>(p, bp.dq, (size_t)p.H * HD * 2);
+  if (RAB_GRAD && tid < BWD_BAND) { gband0[tid] = 0.f; gband1[tid] = 0.f; }  // published by the first tile's barrier
 
   const int xcd = blockIdx.x % NUM_XCD;
   const int list_len = p.ws_counts[xcd];
@@ -312,6 +322,12 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
           }
           ds[r] = g;
         }
+        if constexpr (RAB_GRAD) {
+          const unsigned gaddr = (unsigned)(size_t)(BUF ? gband1 : gband0) + band_lane;
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8 * (r >> 2) + (r & 3))), ds[r], 0, 0, false);
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           w0[i] = pack_bf16x2(ds[2 * i], ds[2 * i + 1]);
@@ -344,27 +360,48 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       else tile_body(std::true_type{}, buf_tag, k0);
     };
 
+    // Gradient band of a finished key tile t -> drab (entry 190 - i of the stage is rab index
+    // first + i, as in the bias band), and the stage is cleared for the tile after the next.  The
+    // global scale of P (not the per-token one, which the dO rows carry) comes in here.
+    const float drab_scale = per_token ? 1.0f : bwd_output_scale(p);
+    auto flush_gband = [&](int t, float* g) __attribute__((always_inline)) {
+      if (tid < BWD_BAND - 1) {
+        const float val = g[(BWD_BAND - 2) - tid];
+        g[(BWD_BAND - 2) - tid] = 0.f;
+        const int idx = q0 - t * BWD_BN - (BWD_BN - 1) + p.N - 1 + tid;
+        if (val != 0.f && idx >= 0 && idx < rab_w) unsafeAtomicAdd(&bp.drab[(size_t)h * rab_w + idx], val * drab_scale);
+      }
+    };
+    int prev_tile = -1;
     // two tiles per trip so that the stage index is a compile-time constant
     if (HAS_RAB && it < nkv) bwd_band_store<true>(band0, band_first, tid);
     while (it < nkv) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile `it` have landed
       __syncthreads();                                   // everybody's; the other stage is free again
+      if (RAB_GRAD && prev_tile >= 0) flush_gband(prev_tile, gband1);
       int nxt = next_tile(it);
       float band_nxt = 0.f;
       if (HAS_RAB && nxt < nkv) band_nxt = band_of(nxt);
       if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, 1>{});
       compute_tile(it, std::integral_constant<int, 0>{});
       if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band1, band_nxt, tid);
+      prev_tile = it;
       it = nxt;
-      if (it >= nkv) break;
+      if (it >= nkv) {
+        if (RAB_GRAD) { __syncthreads(); flush_gband(prev_tile, gband0); }
+        break;
+      }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      if (RAB_GRAD) flush_gband(prev_tile, gband0);
       nxt = next_tile(it);
       if (HAS_RAB && nxt < nkv) band_nxt = band_of(nxt);
       if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, 0>{});
       compute_tile(it, std::integral_constant<int, 1>{});
       if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band0, band_nxt, tid);
+      prev_tile = it;
       it = nxt;
+      if (RAB_GRAD && it >= nkv) { __syncthreads(); flush_gband(prev_tile, gband1); }
     }
 
     // dQ^T accumulators -> dq[s + m, h, :]; element 4 rq + i of block db is column 32 db + 8 rq + 4 half + i

@@ -81,6 +81,10 @@ __global__ __launch_bounds__(64) void hstu_bwd_generic_dq(BwdParams bp) {
       const float x = dot * p.alpha + score_bias(p, h, m, j);
       const float sig = 1.0f / (1.0f + __expf(-x));
       ds = dp * scale * sig * (1.0f + x * (1.0f - sig));
+      if (bp.drab) {  // d score / d rab = 1: the pair's dS goes to its diagonal's column
+        const int rab_w = 2 * p.N - 1, idx = m - j + p.N - 1;
+        if (idx >= 0 && idx < rab_w) unsafeAtomicAdd(&bp.drab[(size_t)h * rab_w + idx], ds);
+      }
     }
     __syncthreads();
     dsbuf[lane] = ds;

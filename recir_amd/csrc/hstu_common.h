@@ -176,6 +176,7 @@ struct BwdParams {
   void* dq;          // [T,H,Dqk]
   void* dk;          // [T,H,Dqk]
   void* dv;          // [T,H,Dv]
+  float* drab;       // [H, 2N-1] gradient of the bias table, zeroed by the entry point, or null
 };
 
 }  // namespace recir_hstu

@@ -39,6 +39,7 @@ typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(8))) short i16x8;
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) const float lds_cfloat;
+typedef __attribute__((address_space(3))) float lds_float;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 typedef __attribute__((ext_vector_type(8))) int i32x8;

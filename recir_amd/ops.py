@@ -99,11 +99,19 @@ _REF_BWD_SCHEMA = (
     "int max_attn_len=0, int full_attn_size=0) -> (Tensor, Tensor, Tensor)"
 )
 
+# the backward with the gradient of the bias table as a fourth output
+_BWD_RAB_SCHEMA = (
+    "hstu_jagged_attention_bwd_rab(Tensor dout, int N, float alpha, Tensor q, Tensor k, Tensor v, "
+    "Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, int contextual_seq_len, "
+    "Tensor rab, int max_attn_len=0, int full_attn_size=0) -> (Tensor, Tensor, Tensor, Tensor)"
+)
+
 _LIBRARY = torch.library.Library("recir", "FRAGMENT")
 _LIBRARY.define(_SCHEMA)
 _LIBRARY.define(_FP8_SCHEMA)
 _LIBRARY.define(_QUANT_SCHEMA)
 _LIBRARY.define(_BWD_SCHEMA)
+_LIBRARY.define(_BWD_RAB_SCHEMA)
 _LIBRARY.define(_REF_SCHEMA)
 _LIBRARY.define(_REF_BWD_SCHEMA)
 
@@ -312,7 +320,7 @@ def _dtype_code(q, k, v):
 
 
 def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
-                rab=None, max_attn_len=0, full_attn_size=0, ctx_reference=False):
+                rab=None, max_attn_len=0, full_attn_size=0, ctx_reference=False, rab_grad=False):
     _check_window(max_attn_len, full_attn_size)
     L = _lib.load()
     dev = q.device
@@ -328,14 +336,20 @@ def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, c
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     dout = dout.to(q.dtype).contiguous()
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    drab = None
+    if rab_grad:
+        if rb is None:
+            raise ValueError("the gradient of rab needs rab")
+        drab = torch.zeros((H, 2 * int(N) - 1), dtype=torch.float32, device=dev) if T == 0 else \
+            torch.empty((H, 2 * int(N) - 1), dtype=torch.float32, device=dev)
     if T == 0:
-        return dq, dk, dv
+        return (dq, dk, dv, drab) if rab_grad else (dq, dk, dv)
     ws_bytes = L.recir_hstu_attn_bwd_workspace_bytes(T, B, H, Dqk, Dv, code)
     stream = torch.cuda.current_stream(dev).cuda_stream
     layout = (T, B, H, Dqk, Dv, code, int(N), int(contextual_seq_len), int(max_attn_len), int(full_attn_size), flags)
     ws, reuse, key = _workspace("bwd", seq_offsets, num_targets, layout, ws_bytes, dev, stream)
     with torch.cuda.device(dev):
-        rc = L.recir_hstu_attn_bwd(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv),
+        rc = L.recir_hstu_attn_bwd(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(drab),
                                    _ptr(off), _ptr(nt), _ptr(rb), _ptr(sc), T, B, H, Dqk, Dv, int(N),
                                    int(contextual_seq_len), int(max_attn_len), int(full_attn_size),
                                    float(alpha), code, flags | reuse, _ptr(ws), ws.numel(), stream)
@@ -344,7 +358,13 @@ def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, c
             with _plan_cache_lock:
                 _plan_cache.pop(key, None)
         _raise_status("recir_hstu_attn_bwd", rc)
-    return dq, dk, dv
+    return (dq, dk, dv, drab) if rab_grad else (dq, dk, dv)
+
+
+def _bwd_rab_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
+                    rab, max_attn_len=0, full_attn_size=0):
+    return _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
+                       rab, max_attn_len, full_attn_size, False, True)
 
 
 def _fwd_device(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
@@ -423,6 +443,8 @@ _LIBRARY.impl("hstu_jagged_attention_fwd", _fwd_device, "CUDA")
 _LIBRARY.impl("hstu_jagged_attention_fp8_fwd", _fp8_fwd_device, "CUDA")
 _LIBRARY.impl("hstu_quantize_e4m3_per_head", _quant_device, "CUDA")
 _LIBRARY.impl("hstu_jagged_attention_bwd", _bwd_device, "CUDA")
+_LIBRARY.impl("hstu_jagged_attention_bwd_rab", _bwd_rab_device, "CUDA")
+_LIBRARY.impl("hstu_jagged_attention_bwd_rab", _no_cpu, "CPU")
 _LIBRARY.impl("triton_ragged_attention_fwd", _ref_fwd_device, "CUDA")
 _LIBRARY.impl("triton_ragged_attention_bwd", _ref_bwd_device, "CUDA")
 _LIBRARY.impl("triton_ragged_attention_fwd", _no_cpu, "CPU")
@@ -474,6 +496,13 @@ def _bwd_fake(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, con
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
+@torch.library.register_fake("recir::hstu_jagged_attention_bwd_rab")
+def _bwd_rab_fake(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab,
+                  max_attn_len=0, full_attn_size=0):
+    _check_common(q, k, v, seq_offsets, num_targets, N)
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), rab.new_empty(rab.shape, dtype=torch.float32)
+
+
 def _setup_context(ctx, inputs, output):
     (N, alpha, q, k, v, seq_offsets, _mask_type, num_targets, attn_scale, max_attn_len,
      contextual_seq_len, full_attn_size, _num_softmax_heads, rab) = inputs
@@ -484,11 +513,18 @@ def _setup_context(ctx, inputs, output):
 def _autograd_backward(ctx, grad_out, _grad_aux):
     q, k, v, seq_offsets, num_targets, attn_scale, rab = ctx.saved_tensors
     N, alpha, contextual_seq_len, max_attn_len, full_attn_size = ctx.hstu_args
-    dq, dk, dv = torch.ops.recir.hstu_jagged_attention_bwd(
-        grad_out, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab,
-        max_attn_len, full_attn_size)
-    # one gradient slot per forward argument; attn_scale and rab receive none
-    return (None, None, dq, dk, dv, None, None, None, None, None, None, None, None, None)
+    drab = None
+    if rab is not None and ctx.needs_input_grad[13]:  # a learned bias table: its gradient as well
+        dq, dk, dv, drab = torch.ops.recir.hstu_jagged_attention_bwd_rab(
+            grad_out, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab,
+            max_attn_len, full_attn_size)
+        drab = drab.to(rab.dtype)
+    else:
+        dq, dk, dv = torch.ops.recir.hstu_jagged_attention_bwd(
+            grad_out, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab,
+            max_attn_len, full_attn_size)
+    # one gradient slot per forward argument; attn_scale receives none
+    return (None, None, dq, dk, dv, None, None, None, None, None, None, None, None, drab)
 
 
 # gradients of q, k and v flow through the backward operator (the reference attaches its backward
@@ -550,18 +586,23 @@ def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len
 def jagged_hstu_attention_backward(dout, q, k, v, seq_offsets, num_targets=None, attn_scale=None, *,
                                    max_seq_len: int, alpha: Optional[float] = None,
                                    contextual_seq_len: int = 0, rab=None, max_attn_len: int = 0,
-                                   full_attn_size: int = 0):
+                                   full_attn_size: int = 0, rab_grad: bool = False):
     """``(dq, dk, dv)`` of ``jagged_hstu_attention`` for the upstream gradient ``dout [T, H, Dv]``;
     argument order and defaults of ``pallas_jagged_hstu_attention_backward``
     (recir/ops/pallas/jagged_hstu_attention.py:1343-1358; called that way by its own test,
     recir/ops/pallas/tests/test_jagged_hstu_attention.py:248-262) and of ``hstu_ragged_attention_bwd_jax_fn``
     (recir/ops/helion/jagged_hstu_attention.py:875-920).  Rows at and after ``seq_offsets[-1]`` of
-    the three gradients are zero.  No gradient is produced for ``rab`` or ``attn_scale``."""
+    the three gradients are zero.  With ``rab_grad`` the gradient of the bias table ``[H, 2N-1]``
+    (float32) is returned as a fourth tensor; no gradient is produced for ``attn_scale``."""
     _check_common(q, k, v, seq_offsets, num_targets, max_seq_len)
     if alpha is None:
         alpha = 1.0 / math.sqrt(q.shape[2])
     if attn_scale is not None and not isinstance(attn_scale, torch.Tensor):
         attn_scale = torch.tensor(float(attn_scale), dtype=torch.float32, device=q.device)
+    if rab_grad:
+        return torch.ops.recir.hstu_jagged_attention_bwd_rab(dout, int(max_seq_len), float(alpha), q, k, v, seq_offsets,
+                                                             num_targets, attn_scale, int(contextual_seq_len), rab,
+                                                             int(max_attn_len), int(full_attn_size))
     return hstu_jagged_attention_bwd(dout, int(max_seq_len), float(alpha), q, k, v, seq_offsets,
                                      num_targets, attn_scale, int(contextual_seq_len), rab,
                                      int(max_attn_len), int(full_attn_size))

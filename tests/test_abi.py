@@ -53,7 +53,7 @@ def test_jagged_header_symbols_are_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.recir_hstu_abi_version() == 3
+    assert lib.recir_hstu_abi_version() == 4
 
 
 def test_workspace_size_is_host_arithmetic(lib):
@@ -98,7 +98,7 @@ def test_invalid_arguments_are_rejected_before_launch(lib, kw, needle):
 def test_backward_invalid_arguments_are_rejected_before_launch(lib, kw, needle):
     a = dict(dout=8, q=8, k=8, v=8, dq=8, dk=8, dv=8, off=8, T=4, B=1, H=1, Dqk=8, Dv=8, N=4, ctx=0, dtype=1, A=0, F=0)
     a.update(kw)
-    rc = lib.recir_hstu_attn_bwd(a["dout"], a["q"], a["k"], a["v"], a["dq"], a["dk"], a["dv"], a["off"], None,
+    rc = lib.recir_hstu_attn_bwd(a["dout"], a["q"], a["k"], a["v"], a["dq"], a["dk"], a["dv"], None, a["off"], None,
                                  None, None, a["T"], a["B"], a["H"], a["Dqk"], a["Dv"], a["N"], a["ctx"], a["A"], a["F"],
                                  1.0, a["dtype"], 0, None, 0, None)
     assert rc < 0

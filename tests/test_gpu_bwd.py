@@ -358,3 +358,75 @@ def test_randomized_cases_forward_and_backward(oracle, seed):
         assert _lib.last_kernel().startswith("bwd_tiled_d128"), what
     if np.abs(want[0]).max() > 0:
         assert_grads_close(got, want, int(wl.seq_offsets[-1]), BF16_REL, what)
+
+
+@pytest.mark.parametrize("case", ["tiled", "tiled_semilocal_per_token", "generic_fp32", "config3"])
+def test_gradient_of_the_bias_table(oracle, case):
+    """d rab[h, m - j + N - 1] = sum of dS(m, j) (no counterpart in the reference, which has no bias;
+    the oracle's form is pinned by torch autograd through a dense restatement).  Float atomics: the
+    tolerance is that of a sum, not bitwise."""
+    import recir_amd
+    from recir_amd import _lib
+    from recir_amd.workloads import make_config, make_jagged
+
+    scale = None
+    if case == "tiled":
+        wl = make_jagged([300, 129, 64, 1, 0, 517], [40, 129, 0, 0, 0, 6], 2, 128, 128, max_seq_len=600, alpha=1 / 128,
+                         dtype="bf16", seed=51, with_rab=True, rab_std=0.5, contextual_seq_len=3, tail_rows=5)
+    elif case == "tiled_semilocal_per_token":
+        wl = make_jagged([260, 100], [30, 0], 2, 128, 128, max_seq_len=300, alpha=1 / 128, dtype="bf16", seed=52,
+                         with_rab=True, rab_std=0.5, max_attn_len=70, full_attn_size=40)
+        scale = torch.rand(wl.T, generator=torch.Generator().manual_seed(3)) * 0.01 + 0.001
+    elif case == "generic_fp32":
+        wl = make_jagged([70, 0, 5, 33], [9, 0, 5, 1], 2, 16, 24, max_seq_len=80, alpha=0.2, dtype="fp32", seed=53,
+                         with_rab=True, rab_std=0.5, contextual_seq_len=2)
+    else:
+        wl = make_config(3)
+    dout = torch.randn(wl.T, wl.H, wl.v.shape[2], generator=torch.Generator().manual_seed(7))
+    if wl.dtype == "bf16":
+        dout = dout.bfloat16().float()
+    q, k, v, off, nt = to_device(wl)
+    sc = None if scale is None else scale.cuda()
+    kw = dict(max_seq_len=wl.max_seq_len, alpha=wl.alpha, contextual_seq_len=wl.contextual_seq_len, rab=wl.rab.cuda(),
+              max_attn_len=wl.max_attn_len, full_attn_size=wl.full_attn_size)
+    dq, dk, dv, drab = recir_amd.jagged_hstu_attention_backward(dout.to(q.device, q.dtype), q, k, v, off, nt, sc,
+                                                                rab_grad=True, **kw)
+    torch.cuda.synchronize()
+    assert _lib.last_kernel().startswith("bwd_generic" if case == "generic_fp32" else "bwd_tiled_d128")
+    assert drab.shape == wl.rab.shape and drab.dtype == torch.float32
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                           attn_scale=None if scale is None else scale.numpy(), rab=wl.rab.numpy(),
+                           contextual_seq_len=wl.contextual_seq_len, max_attn_len=wl.max_attn_len,
+                           full_attn_size=wl.full_attn_size, rab_grad=True)
+    tol = 2e-4 if case == "generic_fp32" else BF16_REL
+    assert_grads_close((dq, dk, dv), want[:3], int(wl.seq_offsets[-1]), tol, case)
+    st = error_stats(drab, want[3])
+    print(f"[parity] d rab {case}: {st}", flush=True)
+    assert st["ref_max"] > 0 and st["rel_to_max"] <= tol and st["rel_fro"] <= tol, st
+    # columns no pair touches stay exactly zero, and the three other gradients are what they are without it
+    assert not drab.cpu().numpy()[np.asarray(want[3]) == 0].any()
+    dq3, dk3, dv3 = recir_amd.jagged_hstu_attention_backward(dout.to(q.device, q.dtype), q, k, v, off, nt, sc, **kw)
+    assert torch.equal(dq, dq3) and torch.equal(dk, dk3) and torch.equal(dv, dv3)
+
+
+def test_autograd_reaches_a_learned_bias_table(oracle):
+    """A bias table that requires grad gets one through the operator's autograd formula."""
+    import recir_amd
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([200, 77], [20, 0], 2, 128, 128, max_seq_len=256, alpha=1 / 128, dtype="bf16", seed=61,
+                     with_rab=True, rab_std=0.5)
+    q, k, v, off, nt = to_device(wl)
+    rab = wl.rab.cuda().requires_grad_(True)
+    q.requires_grad_(True)
+    out = recir_amd.jagged_hstu_attention(q, k, v, off, nt, max_seq_len=wl.max_seq_len, alpha=wl.alpha, rab=rab)
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(2)).bfloat16()
+    out.backward(dout.cuda())
+    torch.cuda.synchronize()
+    want = oracle.attn_bwd(dout.float().numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha, rab=wl.rab.numpy(),
+                           rab_grad=True)
+    st = error_stats(rab.grad, want[3])
+    assert rab.grad.shape == rab.shape and st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL, st
+    assert error_stats(q.grad, want[0])["rel_fro"] <= BF16_REL

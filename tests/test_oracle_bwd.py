@@ -94,15 +94,22 @@ def test_backward_oracle_matches_dense_torch_autograd(oracle, ctx, with_rab):
     v, g = (rng.standard_normal((T, H, Dv)) for _ in range(2))
     rab = rng.standard_normal((H, 2 * N - 1)) if with_rab else None
     tq, tk, tv = (torch.tensor(x.astype(np.float32).astype(np.float64), requires_grad=True) for x in (q, k, v))
-    trab = None if rab is None else torch.tensor(rab.astype(np.float32).astype(np.float64))
+    trab = None if rab is None else torch.tensor(rab.astype(np.float32).astype(np.float64), requires_grad=True)
     out = _dense_forward_f64(tq, tk, tv, lengths, targets, N, alpha, scale, trab, ctx)
     out.backward(torch.tensor(g.astype(np.float32).astype(np.float64))[: out.shape[0]])
-    dq, dk, dv = oracle.attn_bwd(g, q, k, v, off, targets, max_seq_len=N, alpha=alpha, attn_scale=np.float32(scale),
-                                 rab=rab, contextual_seq_len=ctx, ctx_mode=oracle.CTX_PREFIX)
+    res = oracle.attn_bwd(g, q, k, v, off, targets, max_seq_len=N, alpha=alpha, attn_scale=np.float32(scale),
+                          rab=rab, contextual_seq_len=ctx, ctx_mode=oracle.CTX_PREFIX, rab_grad=with_rab)
     # attn_scale travels as float32
-    for got, want in zip((dq, dk, dv), (tq.grad, tk.grad, tv.grad)):
+    for got, want in zip(res[:3], (tq.grad, tk.grad, tv.grad)):
         np.testing.assert_allclose(got, want.numpy(), rtol=1e-5, atol=1e-6)
         assert not got[off[-1]:].any()
+    if with_rab:
+        # gradient of the bias table: autograd through the dense form's gather rab[:, m - j + N - 1]
+        want = trab.grad.numpy()
+        assert np.abs(want).max() > 0.1  # the table matters in this case
+        np.testing.assert_allclose(res[3], want, rtol=1e-5, atol=1e-6)
+        longest = max(lengths)
+        assert not res[3][:, : N - longest].any() and not res[3][:, N + longest - 1:].any()  # diagonals no pair has
 
 
 def test_backward_oracle_matches_finite_differences_of_forward_oracle(oracle):
