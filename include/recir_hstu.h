@@ -164,6 +164,16 @@ int recir_hstu_quantize_e4m3_per_head(const void* x_bf16, void* codes_u8, float*
                                       int32_t H, int32_t D, void* hip_stream);
 
 /*
+ * The same for a packed tensor whose rows at and after seq_offsets[B] are padding: those rows do
+ * not enter the per-head maxima (whatever they hold: the attention kernels ignore and zero them,
+ * and so must the scales) and get zero codes.  seq_offsets: device, [B+1], int64 or int32 with
+ * RECIR_HSTU_FLAG_OFFSETS_I32; read on the device.
+ */
+int recir_hstu_quantize_e4m3_per_head_rows(const void* x_bf16, void* codes_u8, float* scale, int32_t T,
+                                           int32_t H, int32_t D, const void* seq_offsets, int32_t B,
+                                           uint32_t flags, void* hip_stream);
+
+/*
  * Measurement aid, no counterpart in the reference: a plain device-to-device copy of `bytes` bytes
  * (multiple of 16, both pointers 16-byte aligned) by one kernel.  Hardware counters that are read
  * for the attention kernel (FETCH_SIZE, WRITE_SIZE) are scaled by what they read for this copy,

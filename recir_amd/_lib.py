@@ -30,6 +30,7 @@ EXPORTS = (
     "recir_hstu_attn_bwd",
     "recir_hstu_attn_bwd_workspace_bytes",
     "recir_hstu_quantize_e4m3_per_head",
+    "recir_hstu_quantize_e4m3_per_head_rows",
     "recir_hstu_calibration_copy",
     "recir_hstu_last_error",
     "recir_hstu_abi_version",
@@ -76,6 +77,8 @@ def load() -> ctypes.CDLL:
     L.recir_hstu_attn_bwd_workspace_bytes.restype = sz
     L.recir_hstu_quantize_e4m3_per_head.argtypes = [vp, vp, vp, i32, i32, i32, vp]
     L.recir_hstu_quantize_e4m3_per_head.restype = ctypes.c_int
+    L.recir_hstu_quantize_e4m3_per_head_rows.argtypes = [vp, vp, vp, i32, i32, i32, vp, i32, u32, vp]
+    L.recir_hstu_quantize_e4m3_per_head_rows.restype = ctypes.c_int
     L.recir_hstu_calibration_copy.argtypes = [vp, vp, sz, vp]
     L.recir_hstu_calibration_copy.restype = ctypes.c_int
     i64 = ctypes.c_int64

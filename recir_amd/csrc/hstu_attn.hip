@@ -69,8 +69,21 @@ constexpr int QUANT_LDS_HEADS = 4096;
 #ifndef QUANT_AMAX_BLOCKS
 #define QUANT_AMAX_BLOCKS 1024
 #endif
-__global__ __launch_bounds__(256) void hstu_quant_amax(const u32x4* x, unsigned* amax_bits, unsigned* partial, size_t n8, int H, int D8, int d8_shift, int h_mask) {
+// Chunks of the rows a quantiser launch looks at: all T rows, or only those below the end of the
+// sequences (seq_end points at seq_offsets[B], read on the device): rows after it are padding whose
+// contents (possibly Inf or NaN) must not reach a head's scale.
+__device__ __forceinline__ size_t quant_valid_chunks(size_t n8, const void* seq_end, int i32, int T, int H, int D8) {
+  if (!seq_end) return n8;
+  const long long e = i32 ? (long long)*(const int*)seq_end : *(const long long*)seq_end;
+  const size_t rows = (size_t)(e < 0 ? 0 : (e > T ? T : e));
+  const size_t v = rows * (size_t)H * (size_t)D8;
+  return v < n8 ? v : n8;
+}
+
+__global__ __launch_bounds__(256) void hstu_quant_amax(const u32x4* x, unsigned* amax_bits, unsigned* partial, size_t n8_all, int H, int D8, int d8_shift, int h_mask,
+                                                       const void* seq_end, int i32, int T) {
   __shared__ unsigned lmax[QUANT_LDS_HEADS];
+  const size_t n8 = quant_valid_chunks(n8_all, seq_end, i32, T, H, D8);
   const bool in_lds = H <= QUANT_LDS_HEADS;
   if (in_lds) {
     for (int h = threadIdx.x; h < H; h += blockDim.x) lmax[h] = 0u;
@@ -139,9 +152,12 @@ __global__ __launch_bounds__(1024) void hstu_quant_finalize(float* scale, const 
   }
 }
 
-__global__ __launch_bounds__(256) void hstu_quant_encode(const u32x4* x, u32x2* codes, const float* scale, size_t n8, int H, int D8, int d8_shift, int h_mask) {
+__global__ __launch_bounds__(256) void hstu_quant_encode(const u32x4* x, u32x2* codes, const float* scale, size_t n8, int H, int D8, int d8_shift, int h_mask,
+                                                         const void* seq_end, int i32, int T) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const size_t valid = quant_valid_chunks(n8, seq_end, i32, T, H, D8);
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+    if (i >= valid) { codes[i] = u32x2{0u, 0u}; continue; }  // padding rows: zero codes
     const u32x4 v = x[i];
     const float sc = scale[quant_head(i, D8, H, d8_shift, h_mask)];
     float y[8];
@@ -668,7 +684,16 @@ int recir_hstu_calibration_copy(void* dst, const void* src, size_t bytes, void* 
 
 int recir_hstu_quantize_e4m3_per_head(const void* x_bf16, void* codes_u8, float* scale, int32_t T,
                                       int32_t H, int32_t D, void* hip_stream) {
+  return recir_hstu_quantize_e4m3_per_head_rows(x_bf16, codes_u8, scale, T, H, D, nullptr, 0, 0, hip_stream);
+}
+
+int recir_hstu_quantize_e4m3_per_head_rows(const void* x_bf16, void* codes_u8, float* scale, int32_t T,
+                                           int32_t H, int32_t D, const void* seq_offsets, int32_t B,
+                                           uint32_t flags, void* hip_stream) {
   hipStream_t stream = (hipStream_t)hip_stream;
+  if (B < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "negative batch size %d", B);
+  const int i32 = (flags & RECIR_HSTU_FLAG_OFFSETS_I32) ? 1 : 0;
+  const void* seq_end = seq_offsets ? (const void*)((const char*)seq_offsets + (size_t)B * (i32 ? 4 : 8)) : nullptr;
   if (T < 0 || H <= 0 || D <= 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "bad sizes: T=%d H=%d D=%d", T, H, D);
   if (!scale) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "scale must be non-null");
   if (D % 8 != 0) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "D must be a multiple of 8, got %d", D);
@@ -691,13 +716,13 @@ int recir_hstu_quantize_e4m3_per_head(const void* x_bf16, void* codes_u8, float*
     if (int rc = launch_status("hstu_quant_clear")) return rc;
   }
   if (n8 > 0) {
-    hipLaunchKernelGGL(hstu_quant_amax, dim3(amax_blocks), dim3(256), 0, stream, (const u32x4*)x_bf16, (unsigned*)scale, partial, n8, H, D / 8, d8_shift, h_mask);
+    hipLaunchKernelGGL(hstu_quant_amax, dim3(amax_blocks), dim3(256), 0, stream, (const u32x4*)x_bf16, (unsigned*)scale, partial, n8, H, D / 8, d8_shift, h_mask, seq_end, i32, T);
     if (int rc = launch_status("hstu_quant_amax")) return rc;
   }
   hipLaunchKernelGGL(hstu_quant_finalize, dim3(1), dim3(1024), 0, stream, scale, (const unsigned*)partial, (int)amax_blocks, H);
   if (int rc = launch_status("hstu_quant_finalize")) return rc;
   if (n8 > 0) {
-    hipLaunchKernelGGL(hstu_quant_encode, dim3(blocks), dim3(256), 0, stream, (const u32x4*)x_bf16, (u32x2*)codes_u8, scale, n8, H, D / 8, d8_shift, h_mask);
+    hipLaunchKernelGGL(hstu_quant_encode, dim3(blocks), dim3(256), 0, stream, (const u32x4*)x_bf16, (u32x2*)codes_u8, scale, n8, H, D / 8, d8_shift, h_mask, seq_end, i32, T);
     if (int rc = launch_status("hstu_quant_encode")) return rc;
   }
   return RECIR_HSTU_OK;

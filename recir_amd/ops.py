@@ -78,7 +78,7 @@ _FP8_SCHEMA = (
     "Tensor q_scale, Tensor k_scale, Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, "
     "int contextual_seq_len, Tensor? rab=None, int max_attn_len=0, int full_attn_size=0) -> (Tensor, Tensor)"
 )
-_QUANT_SCHEMA = "hstu_quantize_e4m3_per_head(Tensor x) -> (Tensor, Tensor)"
+_QUANT_SCHEMA = "hstu_quantize_e4m3_per_head(Tensor x, Tensor? seq_offsets=None) -> (Tensor, Tensor)"
 _BWD_SCHEMA = (
     "hstu_jagged_attention_bwd(Tensor dout, int N, float alpha, Tensor q, Tensor k, Tensor v, "
     "Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, int contextual_seq_len, "
@@ -413,7 +413,7 @@ def _fp8_fwd_device(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, nu
     return out, torch.zeros((1,), dtype=torch.float32, device=v.device)
 
 
-def _quant_device(x):
+def _quant_device(x, seq_offsets=None):
     L = _lib.load()
     if x.device.type != "cuda":
         raise RuntimeError("recir::hstu_quantize_e4m3_per_head runs on the GPU only")
@@ -424,9 +424,13 @@ def _quant_device(x):
     codes = torch.empty((T, H, D), dtype=torch.uint8, device=x.device)
     scale = torch.empty((H,), dtype=torch.float32, device=x.device)
     stream = torch.cuda.current_stream(x.device).cuda_stream
+    off, flags, B = None, 0, 0
+    if seq_offsets is not None:  # rows at and after seq_offsets[-1] are padding: kept out of the scales
+        off, _, flags = _index_tensors(seq_offsets, None, x.device)
+        B = off.shape[0] - 1
     with torch.cuda.device(x.device):
-        rc = L.recir_hstu_quantize_e4m3_per_head(x.data_ptr(), codes.data_ptr(), scale.data_ptr(),
-                                                 T, H, D, stream)
+        rc = L.recir_hstu_quantize_e4m3_per_head_rows(x.data_ptr(), codes.data_ptr(), scale.data_ptr(),
+                                                      T, H, D, _ptr(off), B, flags, stream)
     if rc != 0:
         raise (ValueError if rc < 0 else RuntimeError)(
             f"recir_hstu_quantize_e4m3_per_head failed ({rc}): {_lib.last_error()}")
@@ -485,7 +489,7 @@ def _fp8_fwd_fake(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, num_
 
 
 @torch.library.register_fake("recir::hstu_quantize_e4m3_per_head")
-def _quant_fake(x):
+def _quant_fake(x, seq_offsets=None):
     return x.new_empty(x.shape, dtype=torch.float8_e4m3fn), x.new_empty((x.shape[1],), dtype=torch.float32)
 
 
@@ -608,12 +612,13 @@ def jagged_hstu_attention_backward(dout, q, k, v, seq_offsets, num_targets=None,
                                      int(max_attn_len), int(full_attn_size))
 
 
-def quantize_e4m3_per_head(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+def quantize_e4m3_per_head(x: torch.Tensor, seq_offsets: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """bf16 ``[T,H,D]`` -> (float8_e4m3fn codes, float32 scale ``[H]``), scale = amax_h / 448.
 
     The arithmetic is the reference's row-wise recipe (recir/ops/kjt_split_per_feature.cpp:493-502)
-    at per-head granularity."""
-    return torch.ops.recir.hstu_quantize_e4m3_per_head(x)
+    at per-head granularity.  With ``seq_offsets`` the rows at and after ``seq_offsets[-1]`` (padding,
+    possibly uninitialised) stay out of the maxima and get zero codes."""
+    return torch.ops.recir.hstu_quantize_e4m3_per_head(x, seq_offsets)
 
 
 def jagged_hstu_attention_fp8(q, k, v, seq_offsets, num_targets=None, *, max_seq_len: int,
@@ -627,8 +632,8 @@ def jagged_hstu_attention_fp8(q, k, v, seq_offsets, num_targets=None, *, max_seq
         alpha = 1.0 / math.sqrt(q.shape[2])
     if attn_scale is not None and not isinstance(attn_scale, torch.Tensor):
         attn_scale = torch.tensor(float(attn_scale), dtype=torch.float32, device=q.device)
-    q8, qs = quantize_e4m3_per_head(q)
-    k8, ks = quantize_e4m3_per_head(k)
+    q8, qs = quantize_e4m3_per_head(q, seq_offsets)
+    k8, ks = quantize_e4m3_per_head(k, seq_offsets)
     out, _ = torch.ops.recir.hstu_jagged_attention_fp8_fwd(
         int(max_seq_len), float(alpha), q8, k8, v, qs, ks, seq_offsets, num_targets, attn_scale,
         int(contextual_seq_len), rab, int(max_attn_len), int(full_attn_size))
@@ -661,8 +666,8 @@ def attention_via_fp8(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, nu
         raise ValueError("softmax attention heads are unsupported")
     if invalid_attn_mask_type != "lower_triangular":
         raise ValueError("only the causal mask ('lower_triangular') is supported")
-    q8, qs = quantize_e4m3_per_head(q)
-    k8, ks = quantize_e4m3_per_head(k)
+    q8, qs = quantize_e4m3_per_head(q, seq_offsets)
+    k8, ks = quantize_e4m3_per_head(k, seq_offsets)
     return torch.ops.recir.hstu_jagged_attention_fp8_fwd(
         int(N), float(alpha), q8, k8, v, qs, ks, seq_offsets, num_targets, attn_scale,
         int(contextual_seq_len), rab, int(max_attn_len), int(full_attn_size))

@@ -430,3 +430,51 @@ def test_autograd_reaches_a_learned_bias_table(oracle):
     st = error_stats(rab.grad, want[3])
     assert rab.grad.shape == rab.shape and st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL, st
     assert error_stats(q.grad, want[0])["rel_fro"] <= BF16_REL
+
+
+def test_backward_with_more_sequences_than_the_single_block_work_list_builder_holds(oracle):
+    """1300 sequences: both backward work lists (query tiles with the shifted cut, key tiles in
+    reverse order) come from the general builder."""
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    rng = np.random.default_rng(15)
+    lengths = rng.integers(0, 40, size=1300)
+    lengths[11] = 300
+    lengths[700] = 129
+    targets = np.minimum(rng.integers(0, 4, size=1300), lengths)
+    wl = make_jagged(lengths, targets, 2, 128, 128, max_seq_len=320, alpha=1 / 128, dtype="bf16", seed=19)
+    dout = torch.randn(wl.T, wl.H, 128, generator=torch.Generator().manual_seed(4)).bfloat16().float()
+    got = run_hip_bwd(wl, dout)
+    assert _lib.last_kernel().startswith("bwd_tiled_d128")
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha)
+    assert_grads_close(got, want, int(wl.seq_offsets[-1]), BF16_REL, "B=1300 backward")
+
+
+def test_no_sequences_through_the_c_abi_zero_the_outputs():
+    """B = 0 with T > 0 rows of padding: the C entry points fill the outputs with zeros (the Python
+    front ends reject an offsets tensor without a sequence, as the reference's validator does,
+    recir/ops/pallas/jagged_hstu_attention.py:1498-1515)."""
+    import ctypes
+
+    from recir_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    T, H, D = 5, 2, 128
+    x = torch.randn(T, H, D, device=dev).bfloat16()
+    off = torch.zeros(1, dtype=torch.int64, device=dev)
+    out = torch.full_like(x, float("nan"))
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.recir_hstu_attn_fwd(p(x), p(x), p(x), p(out), p(off), None, None, None, None, None, T, 0, H, D, D, 16, 0, 0, 0,
+                                 0.1, _lib.DTYPE_BF16, 0, None, 0, s)
+    assert rc == 0, lib.recir_hstu_last_error().decode()
+    grads = [torch.full_like(x, float("nan")) for _ in range(3)]
+    rc = lib.recir_hstu_attn_bwd(p(x), p(x), p(x), p(x), p(grads[0]), p(grads[1]), p(grads[2]), None, p(off), None, None, None,
+                                 T, 0, H, D, D, 16, 0, 0, 0, 0.1, _lib.DTYPE_BF16, 0, None, 0, s)
+    assert rc == 0, lib.recir_hstu_last_error().decode()
+    torch.cuda.synchronize()
+    for t in [out] + grads:
+        assert not t.float().abs().any().item() and torch.isfinite(t.float()).all().item()

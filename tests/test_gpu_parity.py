@@ -573,3 +573,29 @@ def test_semilocal_is_rejected_by_the_tilings_without_it():
     for variant in (ops.KERNEL_TILED,):
         with ops.force_kernel(variant), pytest.raises(ValueError, match="semi-local"):
             run_hip(wl)
+
+
+def test_fp8_scales_ignore_padding_rows(oracle):
+    """Rows at and after seq_offsets[-1] are padding the caller may have left uninitialised: NaN there
+    must not reach a head's scale (it would poison every valid row), and the padding gets zero codes."""
+    import recir_amd
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([150, 64, 33], [10, 0, 33], 2, 128, 128, max_seq_len=256, alpha=1 / 128, dtype="bf16", seed=71,
+                     tail_rows=6)
+    end = int(wl.seq_offsets[-1])
+    wl.q[end:] = 0  # the oracle's quantiser looks at every row it is given
+    wl.k[end:] = 0
+    q, k, v, off, nt = to_device(wl)
+    q[end:] = float("nan")
+    k[end:] = float("inf")
+    v[end:] = float("nan")
+    codes, scale = recir_amd.quantize_e4m3_per_head(q, off)
+    codes_ref, scale_ref = recir_amd.quantize_e4m3_per_head(q[:end].contiguous())
+    assert torch.equal(scale, scale_ref) and torch.isfinite(scale).all().item()
+    assert torch.equal(codes[:end].view(torch.uint8), codes_ref.view(torch.uint8))
+    assert not codes[end:].view(torch.uint8).any().item()
+    out = recir_amd.jagged_hstu_attention_fp8(q, k, v, off, nt, max_seq_len=wl.max_seq_len, alpha=wl.alpha)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all().item() and not out[end:].float().abs().any().item()
+    assert_bf16_close(out[:end], _fp8_reference(oracle, wl)[:end], "fp8 with NaN padding")
