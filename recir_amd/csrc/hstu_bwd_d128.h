@@ -18,9 +18,10 @@
 //                        P  = silu(S) keep, dS = dP keep silu'(S), both rounded to bf16
 //                        dV^T += dO^T P      A = dO^T, transposing LDS read of the dO tile
 //                        dK^T += Q^T dS      A = Q^T, transposing LDS read of the Q tile
-// The operand that multiplies the scores (Q in the first kernel, K in the second) is pre-multiplied
-// by alpha * log2(e) and rounded back to bf16, so sigmoid needs exp2 only; alpha and the output
-// scale are applied once to the fp32 accumulators.
+// The products run on the bf16 values as given; alpha (and log2(e), so that sigmoid needs exp2 only)
+// multiply the fp32 score, alpha and the output scale are applied once to the fp32 accumulators.
+// (Scaling an operand and rounding it back to bf16 perturbs every term of q.k by 2^-9 of itself:
+// an error of the score that does not shrink with the score, visible in rows with one kept pair.)
 //
 // LDS tile layout, shared by all four staged matrices: [64 rows][256 bytes], 16-byte chunk c of row
 // r stored at chunk c ^ f(r & 7) with f(r) = ((r & 3) << 1) | (r >> 2).  Eight consecutive rows then
@@ -146,7 +147,7 @@ __device__ __forceinline__ float bwd_output_scale(const Params& p) {
 // the 191 entries rab[h, m - j + N - 1] one (128-row, 64-row) tile pair can touch are staged in LDS,
 // two stages like the tiles: the load goes out before the tile's copies, the store (scaled by
 // log2(e), index clamped to the row) follows at the end of the tile, where everything is waited for
-// anyway; the scores start at the bias (LDS reads straight into the accumulator).
+// anyway; the bias joins the fp32 score in the fused multiply-add that applies alpha * log2(e).
 constexpr int BWD_BAND = BWD_BM + BWD_BN;  // 191 used
 __device__ __forceinline__ float bwd_band_load(const float* __restrict__ rab_row, int rab_w, int first_idx, int tid) {
   return rab_row[min(max(first_idx + tid, 0), rab_w - 1)];
@@ -262,12 +263,12 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     if (it < nkv) issue_tile(it, std::integral_constant<int, 0>{});
 
     bf16x8 qf[8], gf[8];
-    bwd_load_row_frags(p.q, (size_t)si.s + m, p.H, h, half, m < q_end, true, p.alpha * kLog2e, qf);
-    // a per-token output scale multiplies row m of P, hence row m of dS: fold it into this lane's
-    // dO row
+    bwd_load_row_frags(p.q, (size_t)si.s + m, p.H, h, half, m < q_end, false, 1.0f, qf);
+    // a per-token output scale multiplies row m of P, hence row m of dS (this lane's row)
     constexpr bool per_token = PER_TOKEN;
     const float row_scale = per_token ? p.attn_scale[si.s + min(m, si.n - 1)] : 1.0f;
-    bwd_load_row_frags(bp.dout, (size_t)si.s + m, p.H, h, half, m < q_end, per_token, row_scale, gf);
+    bwd_load_row_frags(bp.dout, (size_t)si.s + m, p.H, h, half, m < q_end, false, 1.0f, gf);
+    const float score_c = p.alpha * kLog2e, neg_c = -score_c;
 
     f32x16 acc[4];
 #pragma unroll
@@ -309,10 +310,19 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
         for (int r = 0; r < 16; ++r) {
           // (the bias is added here, not taken as the accumulator's start: by now the fragment
           // registers of the products are free, before them the kernel is at its register limit)
-          const float u = HAS_RAB ? st[r] + *(lds_cfloat*)(band_addr + 4u * (unsigned)(kvb * 32 + 8 * (r >> 2) + (r & 3))) : st[r];
-          const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
-          const float sv = u * kLn2;
-          float g = dpt[r] * (sig * (1.0f + sv * (1.0f - sig)));
+          // silu'(x) = sig (1 + x (1 - sig)), x = alpha s (+ bias): without a bias alpha goes into
+          // (1 - sig), so no instruction is spent on x itself
+          float sig, inner;
+          if (HAS_RAB) {
+            const float u = __builtin_fmaf(st[r], score_c, *(lds_cfloat*)(band_addr + 4u * (unsigned)(kvb * 32 + 8 * (r >> 2) + (r & 3))));
+            sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
+            inner = __builtin_fmaf(u * kLn2, 1.0f - sig, 1.0f);
+          } else {
+            sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(st[r] * neg_c));
+            inner = __builtin_fmaf(st[r], __builtin_fmaf(sig, -p.alpha, p.alpha), 1.0f);
+          }
+          float g = dpt[r] * (sig * inner);
+          if (per_token) g *= row_scale;
           if (MASKED) {
             const int c = kvb * 32 + 8 * (r >> 2) + (r & 3);
             const int j = k0 + 4 * half + c;
@@ -503,7 +513,8 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     if (it < nq) issue_tile(it, std::integral_constant<int, 0>{});
 
     bf16x8 kf[8], vf[8];
-    bwd_load_row_frags(p.k, (size_t)si.s + j, p.H, h, half, j < si.n, true, p.alpha * kLog2e, kf);
+    bwd_load_row_frags(p.k, (size_t)si.s + j, p.H, h, half, j < si.n, false, 1.0f, kf);
+    const float score_c = p.alpha * kLog2e, neg_c = -score_c;
     bwd_load_row_frags(p.v, (size_t)si.s + j, p.H, h, half, j < si.n, false, 1.0f, vf);
 
     f32x16 acck[4], accv[4];
@@ -522,10 +533,11 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
 #pragma unroll
       for (int qb32 = 0; qb32 < 2; ++qb32) {
         f32x16 s = zero, dp = zero;
+        float bias[16];
         if (HAS_RAB) {
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            s[r] = bandt[(qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3)) - (j - j0) + (BWD_BM - 1)];
+            bias[r] = bandt[(qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3)) - (j - j0) + (BWD_BM - 1)];
         }
         float ts[16];
         if (PER_TOKEN) {
@@ -542,11 +554,22 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
         float pv[16], ds[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float u = s[r];
-          const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
-          const float sv = u * kLn2;
-          float pe = sv * sig;
-          float g = dp[r] * (sig * (1.0f + sv * (1.0f - sig)));
+          // P = x sig and silu'(x) = sig (1 + x (1 - sig)), x = alpha s (+ bias).  Without a bias no
+          // instruction is spent on x: alpha goes into (1 - sig), and P is kept as s sig, its alpha
+          // applied to the dV accumulators at the end
+          float sig, inner, pe;
+          if (HAS_RAB) {
+            const float u = __builtin_fmaf(s[r], score_c, bias[r]);
+            sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
+            const float sv = u * kLn2;
+            inner = __builtin_fmaf(sv, 1.0f - sig, 1.0f);
+            pe = sv * sig;
+          } else {
+            sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(s[r] * neg_c));
+            inner = __builtin_fmaf(s[r], __builtin_fmaf(sig, -p.alpha, p.alpha), 1.0f);
+            pe = s[r] * sig;
+          }
+          float g = dp[r] * (sig * inner);
           if (PER_TOKEN) { pe *= ts[r]; g *= ts[r]; }
           if (MASKED) {
             const int c = qb32 * 32 + 8 * (r >> 2) + (r & 3);
@@ -627,8 +650,9 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     }
 
     if (j < si.n) {
-      const float vscale = PER_TOKEN ? 1.0f : bwd_output_scale(p);
-      const float kscale = p.alpha * vscale;
+      const float oscale = PER_TOKEN ? 1.0f : bwd_output_scale(p);
+      const float kscale = p.alpha * oscale;
+      const float vscale = HAS_RAB ? oscale : kscale;  // without a bias P was kept without its alpha
       unsigned short* krow = (unsigned short*)bp.dk + ((size_t)(si.s + j) * p.H + h) * HD;
       unsigned short* vrow = (unsigned short*)bp.dv + ((size_t)(si.s + j) * p.H + h) * HD;
 #pragma unroll
