@@ -214,8 +214,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
       const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
       float s = sv[r];
       if (HAS_RAB) s += rabs[buf][(m - q0) - jl + (BN - 1)];  // bias staged divided by alpha
-      const float ex = __builtin_amdgcn_exp2f(s * neg_c);
-      float pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
+      const float t = s * neg_c;  // -x log2(e); P is kept as t sigmoid(x), its factor -1 / log2(e) goes on the output
+      float pe = t * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
       if (MASKED) {
         const int j = k0 + jl;
         // branch-free keep(m, j) & (j < n)
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128(Params p) {
     float oscale = 1.0f / (float)p.N;
     if (p.attn_scale)
       oscale = (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) ? p.attn_scale[si.s + m] : p.attn_scale[0];
-    oscale *= p.alpha;
+    oscale *= -1.0f / kLog2e;
     unsigned short* orow = (unsigned short*)p.out + ((size_t)(si.s + m) * p.H + h) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {

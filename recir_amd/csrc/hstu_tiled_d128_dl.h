@@ -97,6 +97,18 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
 #ifndef HSTU_DL_PDV
 #define HSTU_DL_PDV 10  // V fragments (slots 16..31) likewise
 #endif
+#ifndef HSTU_DL_SKEW
+#define HSTU_DL_SKEW 1  // leading unmasked tiles of an item run the loop skewed by one tile (bf16, no bias, causal)
+#endif
+#ifndef HSTU_DL_SKEW_MIN
+#define HSTU_DL_SKEW_MIN 2  // fewest leading tiles worth the loop's entry and exit
+#endif
+#ifndef HSTU_DL_SKEW_PRIO
+#define HSTU_DL_SKEW_PRIO 0  // wave priority around its MFMAs: none (two instructions per slot that cost more than they gain there)
+#endif
+#ifndef HSTU_DL_SKEW_PD
+#define HSTU_DL_SKEW_PD 4  // its fragment prefetch distance in slots
+#endif
 #define HSTU_DL_TILE_SYNC() do { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); __syncthreads(); } while (0)
 #ifndef HSTU_DL_C0
 #define HSTU_DL_C0 0     // slot of the first copy instruction of the next tile
@@ -170,9 +182,11 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     const char* __restrict__ vgb = (const char*)p.v + ((size_t)si.s * p.H + h) * (HD * 2);
     const int rab_w = 2 * p.N - 1;
     const float* __restrict__ rabg = HAS_RAB ? p.rab + (size_t)h * rab_w : nullptr;
-    // score_c: the factor between an accumulator value S' and the argument of exp2,
+    // score_c: the factor between an accumulator value S' and x log2(e), x the argument of SiLU:
     //   alpha log2(e) (fp8: alpha q_scale[h] k_scale[h] log2(e)); bias_mul: what the bias is staged with
-    //   (log2(e) / score_c); the output carries score_c / log2(e) on top of the scale
+    //   (log2(e) / score_c).  With t = -score_c S' = -x log2(e): sigmoid(x) = 1 / (1 + exp2(t)), and P is
+    //   kept as t sigmoid(x) = -log2(e) silu(x), so the score itself is read once; the output carries
+    //   -1 / log2(e) on top of the scale
     float score_c = p.alpha * kLog2e;
     if (FP8) score_c *= p.q_scale[h] * p.k_scale[h];
     const float neg_c = -score_c;
@@ -319,6 +333,40 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     if (HAS_RAB && it < nkv) band_first = band_load(it);
     if (it < nkv) issue_tile(it, std::integral_constant<int, 0>{});
 
+    // Leading key tiles that are unmasked for every row of the workgroup (64 t + 63 <= q0 and
+    // 64 t + 64 <= cap), lie in the first contiguous run of the walk and are followed by a tile that
+    // exists and is whole: an even number of them runs the skewed loop further down, all four waves
+    // together, since that loop moves K and V in half tiles on a schedule of its own.
+    constexpr bool SKEW = HSTU_DL_SKEW && !HAS_RAB && !FP8 && !SEMI;
+    int skew_tiles = 0;
+    if (SKEW && it == 0) {
+      const int run_end = has_skip ? skip_a : nkv;
+      const int f = min(min((q0 + 1) / BN, cap0 / BN), min(run_end - 1, si.n / BN - 1));
+      skew_tiles = max(f, 0) & ~1;
+      if (skew_tiles < HSTU_DL_SKEW_MIN) skew_tiles = 0;
+    }
+    // One copy instruction of the skewed loop's trip i (LDS stage BUF = i & 1); this wave moves rows
+    // 8 wave + 4 idx .. + 3 of a half tile.  parts 0, 1: K rows 0..31 of tile i + 2 (stage BUF);
+    // 2, 3: K rows 32..63 of tile i + 1 (other stage); 4, 5: V rows 0..31 of tile i + 1 (other stage);
+    // 6, 7: V rows 32..63 of tile i (stage BUF).  None of the four regions is read during trip i.
+    auto skew_copy = [&](int i, auto buf_tag, int part) __attribute__((always_inline)) {
+      constexpr int BUF = decltype(buf_tag)::value;
+      const int idx = part & 1, sel = part >> 1;
+      const bool is_v = sel >= 2, hi = (sel & 1) != 0, to_cur = (sel == 0 || sel == 3);
+      const int tile = sel == 0 ? i + 2 : (sel == 3 ? i : i + 1);
+      const int stage = to_cur ? BUF : (BUF ^ 1);
+      const int jr = 8 * (int)hi + 2 * wave + idx;  // rows 4 jr .. 4 jr + 3 of the tile
+      const int r0 = 4 * jr;
+      unsigned short* dst = is_v ? (stage ? Vs1 : Vs0) : (stage ? Ks1 : Ks0);
+      const char* src = (is_v ? vgb : kgb) + (size_t)(tile * BN + r0) * row_bytes;
+      const unsigned off = is_v ? v_off : (k_off ^ (unsigned)(64 * (jr & (KSWZ >> 2))));
+      copy16(src, off, (unsigned)(size_t)&dst[r0 * HD]);
+    };
+    if (SKEW && skew_tiles) {  // K rows 0..31 of tile 1: the first trip's scores of its second tile
+      skew_copy(-1, std::integral_constant<int, 1>{}, 0);
+      skew_copy(-1, std::integral_constant<int, 1>{}, 1);
+    }
+
     // ---- Q fragments (B operand): lane holds row qw0 + l32 ----
     // bf16: d = 16 kk + 8 half .. +7, as stored;  fp8: d = 64 st + 32 half .. +31 (raw bytes)
     bf16x8 qf[FP8 ? 1 : 8];
@@ -361,8 +409,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         const int jl = kvb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
         float s = sv[r];
         if (HAS_RAB) s += *(lds_cfloat*)(rab_addr + 4u * (unsigned)(kvb * 32 + 8 * (r >> 2) + (r & 3)));
-        const float ex = __builtin_amdgcn_exp2f(s * neg_c);
-        float pe = s * __builtin_amdgcn_rcpf(1.0f + ex);
+        const float t = s * neg_c;
+        float pe = t * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
         if (MASKED) pe = kept(k0, kvb * 32 + 8 * (r >> 2) + (r & 3)) ? pe : 0.f;
         pv[r] = pe;
       }
@@ -444,8 +492,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
             const int r = 2 * e + t;
             const int jl = blk * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
             const float sv = sblk[blk][r];  // the bias is already in there, see bias_block
-            const float ex = __builtin_amdgcn_exp2f(sv * neg_c);
-            float pv = sv * __builtin_amdgcn_rcpf(1.0f + ex);
+            const float tv = sv * neg_c;
+            float pv = tv * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(tv));
             if (MASKED) pv = kept(k0, blk * 32 + 8 * (r >> 2) + (r & 3)) ? pv : 0.f;
             pe[t] = pv;
           }
@@ -616,6 +664,112 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       if (HAS_RAB && (FAST || nxt < nkv)) band_store(other, band_nxt);
     };
 
+    // ---- the skewed loop ----
+    // Trip i (tile i in LDS stage i & 1), one MFMA per slot, a scheduling fence after each:
+    //   slots  0..7   D(i-1): O^T += V^T[:, 32:64] P1(i-1)     second half of the previous tile
+    //   slots  8..15  B(i)  : S1 = K(i)[32:64] Q^T
+    //   slots 16..23  A(i+1): S0 = K(i+1)[0:32] Q^T            first half of the next tile
+    //   slots 24..31  C(i)  : O^T += V^T[:, 0:32] P0(i)
+    // so every slot has an MFMA and SiLU work for it to hide: one score enters a five-stage pipeline
+    // per slot (t = s neg_c | exp2 | + 1 | rcp | t r and, every other slot, the bf16 pack), the 16 of
+    // S0(i) in slots 0..15, the 16 of S1(i) in slots 16..31; the last of them leave it in slots 0..3
+    // of the next trip, one slot before D(i) needs them.  The order of the accumulation into O is
+    // that of the plain loop.  KIND: 0 first trip (no D), 1 middle, 2 last (no A), 3 the eight slots
+    // of D after the last trip.
+    f32x16 sk_s0, sk_s1;
+    unsigned sk_pw0[8], sk_pw1[8];
+    float sk_t[8], sk_r[8];
+    auto skew_body = [&](auto buf_tag, auto kind_tag, int i) __attribute__((always_inline)) {
+      constexpr int BUF = decltype(buf_tag)::value;
+      constexpr int KIND = decltype(kind_tag)::value;
+      constexpr int NSLOT = KIND == 3 ? 8 : 32;
+      constexpr int PD = HSTU_DL_SKEW_PD;
+      const char* kc = (const char*)(BUF ? Ks1 : Ks0);
+      const char* ko = (const char*)(BUF ? Ks0 : Ks1);
+      const char* vc = (const char*)(BUF ? Vs1 : Vs0);
+      const char* vo = (const char*)(BUF ? Vs0 : Vs1);
+      const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      auto k_frag_at = [&](const char* kb, int kvb, int kk) __attribute__((always_inline)) {
+#if HSTU_DL_SWZ64
+        return *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)(kk * 32)));
+#else
+        return *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)((kk & 3) * 32)) + (kk >> 2) * 128);
+#endif
+      };
+      auto v_frag_at = [&](const char* vb, int db, int s2) __attribute__((always_inline)) {
+#if HSTU_DL_SWZ64
+        const char* a = vb + (vt_rd ^ (unsigned)(db * 64)) + s2 * 16 * HD * 2;
+#else
+        const char* a = vb + ((db & 1) ? vt_rd_o : vt_rd_e) + db * 64 + s2 * 16 * HD * 2;
+#endif
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)a);
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a + 8 * HD * 2));
+        const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return __builtin_bit_cast(bf16x8, both);
+      };
+      auto has_mfma = [](int s) constexpr {
+        return KIND == 3 ? s < 8 : (KIND == 0 ? s >= 8 : (KIND == 2 ? (s < 16 || s >= 24) : true));
+      };
+      auto slot_frag = [&](int s) __attribute__((always_inline)) {
+        if (s < 8) return v_frag_at(vo, s & 3, 2 + (s >> 2));
+        if (s < 16) return k_frag_at(kc, 1, s - 8);
+        if (s < 24) return k_frag_at(ko, 0, s - 16);
+        return v_frag_at(vc, (s - 24) & 3, (s - 24) >> 2);
+      };
+      // SiLU pipeline stage `stage` (1..5) of the slot: it works on score n = s - (stage - 1) of this
+      // trip, or on score n + 32 of the previous one
+      auto silu_stage = [&](int s, int stage) __attribute__((always_inline)) {
+        const int n = s - (stage - 1);
+        if (n >= 0 ? KIND == 3 : KIND == 0) return;
+        const int nn = (n + 32) & 31, e = nn & 7;
+        if (stage == 1) sk_t[e] = (nn < 16 ? sk_s0[nn] : sk_s1[nn - 16]) * neg_c;
+        else if (stage == 2) sk_r[e] = __builtin_amdgcn_exp2f(sk_t[e]);
+        else if (stage == 3) sk_r[e] = 1.0f + sk_r[e];
+        else if (stage == 4) sk_r[e] = __builtin_amdgcn_rcpf(sk_r[e]);
+        else {
+          sk_t[e] = sk_t[e] * sk_r[e];
+          if (nn & 1) {
+            const unsigned w = pack_bf16x2(sk_t[e - 1], sk_t[e]);
+            if (nn < 16) sk_pw0[nn >> 1] = w; else sk_pw1[(nn - 16) >> 1] = w;
+          }
+        }
+      };
+      bf16x8 F[32];
+#pragma unroll
+      for (int s = 0; s < NSLOT; ++s)
+        if (has_mfma(s) && s < PD) F[s] = slot_frag(s);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < NSLOT; ++s) {
+        if (s + PD < NSLOT && has_mfma(s + PD)) F[s + PD] = slot_frag(s + PD);
+        if (has_mfma(s)) {
+#if HSTU_DL_SKEW_PRIO
+          __builtin_amdgcn_s_setprio(HSTU_DL_SKEW_PRIO);
+#endif
+          if (s < 8) {
+            const int w0 = 4 * (s >> 2), db = s & 3;
+            const u32x4 w = {sk_pw1[w0], sk_pw1[w0 + 1], sk_pw1[w0 + 2], sk_pw1[w0 + 3]};
+            acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], __builtin_bit_cast(bf16x8, w), acc[db], 0, 0, 0);
+          } else if (s < 16) {
+            sk_s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], qf[s - 8], s == 8 ? zero : sk_s1, 0, 0, 0);
+          } else if (s < 24) {
+            sk_s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], qf[s - 16], s == 16 ? zero : sk_s0, 0, 0, 0);
+          } else {
+            const int w0 = 4 * ((s - 24) >> 2), db = (s - 24) & 3;
+            const u32x4 w = {sk_pw0[w0], sk_pw0[w0 + 1], sk_pw0[w0 + 2], sk_pw0[w0 + 3]};
+            acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], __builtin_bit_cast(bf16x8, w), acc[db], 0, 0, 0);
+          }
+#if HSTU_DL_SKEW_PRIO
+          __builtin_amdgcn_s_setprio(0);
+#endif
+        }
+        if (KIND != 3 && s < 8 && !(KIND == 0 && s >= 6) && !(KIND == 2 && s < 2)) skew_copy(i, buf_tag, s);
+#pragma unroll
+        for (int stage = 5; stage >= 1; --stage) silu_stage(s, stage);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+
     auto compute_tile = [&](int it, auto buf_tag, int nxt) __attribute__((always_inline)) {
       constexpr int BUF = decltype(buf_tag)::value;
       const int k0 = it * BN;
@@ -651,6 +805,42 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       if (HAS_RAB) band_store(std::integral_constant<int, 0>{}, band_first);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      if (SKEW && skew_tiles) {
+        const std::integral_constant<int, 0> st0{};
+        const std::integral_constant<int, 1> st1{};
+        {  // S0 of tile 0
+          const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          bf16x8 f0[8];
+#pragma unroll
+          for (int kk = 0; kk < 8; ++kk) {
+#if HSTU_DL_SWZ64
+            f0[kk] = *(const bf16x8*)((const char*)Ks0 + (ks_rd ^ (unsigned)(kk * 32)));
+#else
+            f0[kk] = *(const bf16x8*)((const char*)Ks0 + (ks_rd ^ (unsigned)((kk & 3) * 32)) + (kk >> 2) * 128);
+#endif
+          }
+#pragma unroll
+          for (int kk = 0; kk < 8; ++kk) sk_s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0[kk], qf[kk], kk == 0 ? zero : sk_s0, 0, 0, 0);
+        }
+        __syncthreads();  // the first trip refills the K rows just read
+        skew_body(st0, std::integral_constant<int, 0>{}, 0);
+        HSTU_DL_TILE_SYNC();
+        for (int i = 1; i + 1 < skew_tiles; i += 2) {
+          skew_body(st1, std::integral_constant<int, 1>{}, i);
+          HSTU_DL_TILE_SYNC();
+          skew_body(st0, std::integral_constant<int, 1>{}, i + 1);
+          HSTU_DL_TILE_SYNC();
+        }
+        skew_body(st1, std::integral_constant<int, 2>{}, skew_tiles - 1);
+        HSTU_DL_TILE_SYNC();
+        // V rows 32..63 of the tile the plain loop takes over with; the second half of the last skewed tile
+        skew_copy(skew_tiles, st0, 6);
+        skew_copy(skew_tiles, st0, 7);
+        skew_body(st0, std::integral_constant<int, 3>{}, skew_tiles);
+        HSTU_DL_TILE_SYNC();
+        it = skew_tiles;
+        fast_pairs = 0;
+      }
       for (int pi = 0; pi < fast_pairs; ++pi) {
         tile_body(std::false_type{}, std::integral_constant<int, 0>{}, it * BN, it + 1, std::true_type{});
         HSTU_DL_TILE_SYNC();
@@ -680,7 +870,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       float oscale = 1.0f / (float)p.N;
       if (p.attn_scale)
         oscale = (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) ? p.attn_scale[si.s + m] : p.attn_scale[0];
-      oscale *= score_c * (1.0f / kLog2e);
+      oscale *= -1.0f / kLog2e;
       unsigned short* orow = (unsigned short*)p.out + ((size_t)(si.s + m) * p.H + h) * HD;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
