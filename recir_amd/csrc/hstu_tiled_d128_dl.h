@@ -63,9 +63,10 @@ __device__ __forceinline__ void copy16(const void* base, unsigned lane_off, unsi
 }
 // LDS swizzle of the bf16 K and V tiles: 1 = free of bank conflicts on the 64-bank LDS
 // (K chunk ^ (row & 15), V slot ^ 2 (row & 3)); 0 = the 32-bank forms (K chunk ^ (row & 7), V slot ^
-// (row & 3)), which run the LDS reads at half rate but need six address registers fewer.
+// (row & 3)), which run the LDS reads at half rate.  The 64-bank forms need six address registers more;
+// with the short prefetch distances below nothing spills, and they measure 1-2 % faster.
 #ifndef HSTU_DL_SWZ64
-#define HSTU_DL_SWZ64 0
+#define HSTU_DL_SWZ64 1
 #endif
 constexpr int KSWZ = HSTU_DL_SWZ64 ? 15 : 7;
 constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
@@ -80,7 +81,7 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
                              // body (the other body adds the bias in the SiLU arithmetic; measured 2-3 % slower)
 #endif
 #ifndef HSTU_DL_PD_SLOW
-#define HSTU_DL_PD_SLOW 6  // fragment prefetch distance of the bodies that carry mask or clamping state
+#define HSTU_DL_PD_SLOW 3  // fragment prefetch distance of the bodies that carry mask or clamping state
 #endif
 #ifndef HSTU_DL_PDK_RAB
 #define HSTU_DL_PDK_RAB 6  // K fragments in flight when a tile opens, bias instantiations (the bias block needs registers too)
@@ -107,7 +108,15 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
 #define HSTU_DL_SKEW_PRIO 0  // wave priority around its MFMAs: none (two instructions per slot that cost more than they gain there)
 #endif
 #ifndef HSTU_DL_SKEW_PD
-#define HSTU_DL_SKEW_PD 4  // its fragment prefetch distance in slots
+#define HSTU_DL_SKEW_PD 3  // its fragment prefetch distance in slots
+#endif
+#ifndef HSTU_SK_ABL
+#define HSTU_SK_ABL 0  // measurement builds only: 1 no fragment reads, 2 no copies, 4 no barrier, 8 no SiLU in the skewed loop (wrong results)
+#endif
+#if HSTU_SK_ABL & 4
+#define HSTU_SK_SYNC() do { } while (0)
+#else
+#define HSTU_SK_SYNC() HSTU_DL_TILE_SYNC()
 #endif
 #define HSTU_DL_TILE_SYNC() do { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); __syncthreads(); } while (0)
 #ifndef HSTU_DL_C0
@@ -711,6 +720,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         return KIND == 3 ? s < 8 : (KIND == 0 ? s >= 8 : (KIND == 2 ? (s < 16 || s >= 24) : true));
       };
       auto slot_frag = [&](int s) __attribute__((always_inline)) {
+#if HSTU_SK_ABL & 1
+        return qf[(s * 5 + 3) & 7];
+#endif
         if (s < 8) return v_frag_at(vo, s & 3, 2 + (s >> 2));
         if (s < 16) return k_frag_at(kc, 1, s - 8);
         if (s < 24) return k_frag_at(ko, 0, s - 16);
@@ -763,9 +775,13 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           __builtin_amdgcn_s_setprio(0);
 #endif
         }
+#if !(HSTU_SK_ABL & 2)
         if (KIND != 3 && s < 8 && !(KIND == 0 && s >= 6) && !(KIND == 2 && s < 2)) skew_copy(i, buf_tag, s);
+#endif
+#if !(HSTU_SK_ABL & 8)
 #pragma unroll
         for (int stage = 5; stage >= 1; --stage) silu_stage(s, stage);
+#endif
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -824,20 +840,20 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         }
         __syncthreads();  // the first trip refills the K rows just read
         skew_body(st0, std::integral_constant<int, 0>{}, 0);
-        HSTU_DL_TILE_SYNC();
+        HSTU_SK_SYNC();
         for (int i = 1; i + 1 < skew_tiles; i += 2) {
           skew_body(st1, std::integral_constant<int, 1>{}, i);
-          HSTU_DL_TILE_SYNC();
+          HSTU_SK_SYNC();
           skew_body(st0, std::integral_constant<int, 1>{}, i + 1);
-          HSTU_DL_TILE_SYNC();
+          HSTU_SK_SYNC();
         }
         skew_body(st1, std::integral_constant<int, 2>{}, skew_tiles - 1);
-        HSTU_DL_TILE_SYNC();
+        HSTU_SK_SYNC();
         // V rows 32..63 of the tile the plain loop takes over with; the second half of the last skewed tile
         skew_copy(skew_tiles, st0, 6);
         skew_copy(skew_tiles, st0, 7);
         skew_body(st0, std::integral_constant<int, 3>{}, skew_tiles);
-        HSTU_DL_TILE_SYNC();
+        HSTU_SK_SYNC();
         it = skew_tiles;
         fast_pairs = 0;
       }
