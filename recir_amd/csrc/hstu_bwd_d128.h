@@ -38,6 +38,7 @@
 
 #include "hstu_common.h"
 #include "hstu_tiled_d128.h"     // HD, kLog2e
+#include "hstu_bwd_acc_regs.h"
 #include "hstu_tiled_d128_dl.h"  // i16x4, i16x8, lds_void, lds_i16x4
 
 namespace recir_hstu {
@@ -517,11 +518,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     const float score_c = p.alpha * kLog2e, neg_c = -score_c;
     bwd_load_row_frags(p.v, (size_t)si.s + j, p.H, h, half, j < si.n, false, 1.0f, vf);
 
-    f32x16 acck[4], accv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acck[i][r] = accv[i][r] = 0.f;
+    bwd_acc_zero();  // dK^T and dV^T accumulators (fixed AGPRs)
 
     auto tile_body = [&](auto masked_tag, auto buf_tag, int m0) __attribute__((always_inline)) {
       constexpr bool MASKED = decltype(masked_tag)::value;
@@ -532,7 +529,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int qb32 = 0; qb32 < 2; ++qb32) {
-        f32x16 s = zero, dp = zero;
+        f32x16 s, dp;
         float bias[16];
         if (HAS_RAB) {
 #pragma unroll
@@ -545,11 +542,26 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
           for (int r = 0; r < 16; ++r)
             ts[r] = p.attn_scale[si.s + min(m0 + qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3), si.n - 1)];
         }
+        // The products are written out as instructions with their register classes named: scores in
+        // VGPRs (the arithmetic below reads them), the dK and dV accumulators in fixed AGPRs
+        // (hstu_bwd_acc_regs.h).  Left to choose, the compiler puts every MFMA result of this
+        // 512-register kernel into AGPRs and moves them: 250 of a tile's 570 VALU instructions were
+        // such moves.
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
-          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(qb, lc, qb32, kk), kf[kk], s, 0, 0, 0);
-          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(gb, lc, qb32, kk), vf[kk], dp, 0, 0, 0);
+          const bf16x8 fq = bwd_row_frag(qb, lc, qb32, kk), fg = bwd_row_frag(gb, lc, qb32, kk);
+          const bf16x8 kfr = kf[kk], vfr = vf[kk];
+          if (kk == 0) {
+            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(s) : "v"(fq), "v"(kfr));
+            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(dp) : "v"(fg), "v"(vfr));
+          } else {
+            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(s) : "v"(fq), "v"(kfr));
+            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(dp) : "v"(fg), "v"(vfr));
+          }
         }
+        // an MFMA result may be read by other instructions 11 cycles after the MFMA at the earliest; the
+        // compiler does not count for instructions it did not place
+        asm volatile("s_nop 15" : "+v"(s), "+v"(dp));
         // element r of the block is query row m0 + 32 qb32 + 8 (r / 4) + 4 half + r % 4, this lane's key
         float pv[16], ds[16];
 #pragma unroll
@@ -593,13 +605,13 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
         }
         const bf16x8 pb0 = __builtin_bit_cast(bf16x8, p0), pb1 = __builtin_bit_cast(bf16x8, p1);
         const bf16x8 db0 = __builtin_bit_cast(bf16x8, d0), db1 = __builtin_bit_cast(bf16x8, d1);
+        bf16x8 fg[8], fq[8];
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          accv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(gb, lc, db, 2 * qb32), pb0, accv[db], 0, 0, 0);
-          accv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(gb, lc, db, 2 * qb32 + 1), pb1, accv[db], 0, 0, 0);
-          acck[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(qb, lc, db, 2 * qb32), db0, acck[db], 0, 0, 0);
-          acck[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(qb, lc, db, 2 * qb32 + 1), db1, acck[db], 0, 0, 0);
+          fg[2 * db] = bwd_tr_frag(gb, lc, db, 2 * qb32); fg[2 * db + 1] = bwd_tr_frag(gb, lc, db, 2 * qb32 + 1);
+          fq[2 * db] = bwd_tr_frag(qb, lc, db, 2 * qb32); fq[2 * db + 1] = bwd_tr_frag(qb, lc, db, 2 * qb32 + 1);
         }
+        bwd_acc_mfma16(fg, fq, pb0, pb1, db0, db1);
       }
     };
 
@@ -657,14 +669,17 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       unsigned short* vrow = (unsigned short*)bp.dv + ((size_t)(si.s + j) * p.H + h) * HD;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
+        float av[16], ak[16];
+        bwd_acc_read(db, av);
+        bwd_acc_read(4 + db, ak);
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq) {
           u32x2 o;
-          o.x = pack_bf16x2(acck[db][4 * rq + 0] * kscale, acck[db][4 * rq + 1] * kscale);
-          o.y = pack_bf16x2(acck[db][4 * rq + 2] * kscale, acck[db][4 * rq + 3] * kscale);
+          o.x = pack_bf16x2(ak[4 * rq + 0] * kscale, ak[4 * rq + 1] * kscale);
+          o.y = pack_bf16x2(ak[4 * rq + 2] * kscale, ak[4 * rq + 3] * kscale);
           *(u32x2*)(krow + db * 32 + 8 * rq + 4 * half) = o;
-          o.x = pack_bf16x2(accv[db][4 * rq + 0] * vscale, accv[db][4 * rq + 1] * vscale);
-          o.y = pack_bf16x2(accv[db][4 * rq + 2] * vscale, accv[db][4 * rq + 3] * vscale);
+          o.x = pack_bf16x2(av[4 * rq + 0] * vscale, av[4 * rq + 1] * vscale);
+          o.y = pack_bf16x2(av[4 * rq + 2] * vscale, av[4 * rq + 3] * vscale);
           *(u32x2*)(vrow + db * 32 + 8 * rq + 4 * half) = o;
         }
       }
