@@ -526,92 +526,139 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       const char* qb = (const char*)(BUF ? Qs1 : Qs0);
       const char* gb = (const char*)(BUF ? Gs1 : Gs0);
       const float* bandt = BUF ? band1 : band0;
-      const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int qb32 = 0; qb32 < 2; ++qb32) {
-        f32x16 s, dp;
-        float bias[16];
+      // The products are written out as instructions with their register classes named: scores in
+      // VGPRs (the arithmetic reads them), the dK and dV accumulators in fixed AGPRs
+      // (hstu_bwd_acc_regs.h).  Left to choose, the compiler puts every MFMA result of this
+      // 512-register kernel into AGPRs and moves them: 250 of a tile's 570 VALU instructions were
+      // such moves.
+      // The two 32-row query blocks of the tile are software-pipelined, one wave per SIMD having
+      // nothing else to hide its arithmetic behind:
+      //   1: S, dP of block 0                           (16 MFMAs)
+      //   2: S, dP of block 1   | P, dS of block 0      (one element per MFMA)
+      //   3: dV, dK += block 0  | P, dS of block 1
+      //   4: dV, dK += block 1
+      auto score_mfma = [&](int qb32, int i, f32x16& s, f32x16& dp, bf16x8 f) __attribute__((always_inline)) {
+        // i = 2 kk: S += Q[kk] K[kk];  i = 2 kk + 1: dP += dO[kk] V[kk]
+        const int kk = i >> 1;
+        const bf16x8 kfr = kf[kk], vfr = vf[kk];
+        if (!(i & 1)) {
+          if (kk == 0) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(s) : "v"(f), "v"(kfr));
+          else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(s) : "v"(f), "v"(kfr));
+        } else {
+          if (kk == 0) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(dp) : "v"(f), "v"(vfr));
+          else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(dp) : "v"(f), "v"(vfr));
+        }
+      };
+      auto score_frag = [&](int qb32, int i) __attribute__((always_inline)) {
+        return (i & 1) ? bwd_row_frag(gb, lc, qb32, i >> 1) : bwd_row_frag(qb, lc, qb32, i >> 1);
+      };
+      // product i of a block's sixteen into the accumulators: key step i / 8, block (i / 2) % 4, dV (even) or dK (odd)
+      auto acc_frag = [&](int qb32, int i) __attribute__((always_inline)) {
+        return bwd_tr_frag((i & 1) ? qb : gb, lc, (i >> 1) & 3, 2 * qb32 + (i >> 3));
+      };
+      // P and dS of element r of block qb32 (query row m0 + 32 qb32 + 8 (r / 4) + 4 half + r % 4, this lane's key)
+      auto element = [&](int qb32, int r, float sv_raw, float dpv, float biasv, float tsv, float& pe, float& g) __attribute__((always_inline)) {
+        // P = x sig and silu'(x) = sig (1 + x (1 - sig)), x = alpha s (+ bias).  Without a bias no
+        // instruction is spent on x: alpha goes into (1 - sig), and P is kept as s sig, its alpha
+        // applied to the dV accumulators at the end
+        float sig, inner;
         if (HAS_RAB) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            bias[r] = bandt[(qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3)) - (j - j0) + (BWD_BM - 1)];
+          const float u = __builtin_fmaf(sv_raw, score_c, biasv);
+          sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
+          const float sv = u * kLn2;
+          inner = __builtin_fmaf(sv, 1.0f - sig, 1.0f);
+          pe = sv * sig;
+        } else {
+          sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(sv_raw * neg_c));
+          inner = __builtin_fmaf(sv_raw, __builtin_fmaf(sig, -p.alpha, p.alpha), 1.0f);
+          pe = sv_raw * sig;
         }
-        float ts[16];
-        if (PER_TOKEN) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            ts[r] = p.attn_scale[si.s + min(m0 + qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3), si.n - 1)];
+        g = dpv * (sig * inner);
+        if (PER_TOKEN) { pe *= tsv; g *= tsv; }
+        if (MASKED) {
+          const int c = qb32 * 32 + 8 * (r >> 2) + (r & 3);
+          const int m = m0 + 4 * half + c;
+          const int idm = min(m, si.cap);
+          const bool kp = SEMI ? ((m == j) | ((j < idm) & ((idm - j <= si.win) | (idm >= si.tail0))) | (j < si.ctx_eff)) & (m < si.n)
+                               : ((c >= mk_from - m0) | (c == mk_own - m0)) & (c < mk_end - m0);
+          pe = kp ? pe : 0.f;
+          g = kp ? g : 0.f;
         }
-        // The products are written out as instructions with their register classes named: scores in
-        // VGPRs (the arithmetic below reads them), the dK and dV accumulators in fixed AGPRs
-        // (hstu_bwd_acc_regs.h).  Left to choose, the compiler puts every MFMA result of this
-        // 512-register kernel into AGPRs and moves them: 250 of a tile's 570 VALU instructions were
-        // such moves.
+      };
+      auto load_bias = [&](int qb32, float (&bias)[16]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const bf16x8 fq = bwd_row_frag(qb, lc, qb32, kk), fg = bwd_row_frag(gb, lc, qb32, kk);
-          const bf16x8 kfr = kf[kk], vfr = vf[kk];
-          if (kk == 0) {
-            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(s) : "v"(fq), "v"(kfr));
-            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(dp) : "v"(fg), "v"(vfr));
-          } else {
-            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(s) : "v"(fq), "v"(kfr));
-            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(dp) : "v"(fg), "v"(vfr));
-          }
-        }
-        // an MFMA result may be read by other instructions 11 cycles after the MFMA at the earliest; the
-        // compiler does not count for instructions it did not place
-        asm volatile("s_nop 15" : "+v"(s), "+v"(dp));
-        // element r of the block is query row m0 + 32 qb32 + 8 (r / 4) + 4 half + r % 4, this lane's key
-        float pv[16], ds[16];
+        for (int r = 0; r < 16; ++r)
+          bias[r] = HAS_RAB ? bandt[(qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3)) - (j - j0) + (BWD_BM - 1)] : 0.f;
+      };
+      auto load_ts = [&](int qb32, float (&ts)[16]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          // P = x sig and silu'(x) = sig (1 + x (1 - sig)), x = alpha s (+ bias).  Without a bias no
-          // instruction is spent on x: alpha goes into (1 - sig), and P is kept as s sig, its alpha
-          // applied to the dV accumulators at the end
-          float sig, inner, pe;
-          if (HAS_RAB) {
-            const float u = __builtin_fmaf(s[r], score_c, bias[r]);
-            sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
-            const float sv = u * kLn2;
-            inner = __builtin_fmaf(sv, 1.0f - sig, 1.0f);
-            pe = sv * sig;
-          } else {
-            sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(s[r] * neg_c));
-            inner = __builtin_fmaf(s[r], __builtin_fmaf(sig, -p.alpha, p.alpha), 1.0f);
-            pe = s[r] * sig;
-          }
-          float g = dp[r] * (sig * inner);
-          if (PER_TOKEN) { pe *= ts[r]; g *= ts[r]; }
-          if (MASKED) {
-            const int c = qb32 * 32 + 8 * (r >> 2) + (r & 3);
-            const int m = m0 + 4 * half + c;
-            const int idm = min(m, si.cap);
-            const bool kp = SEMI ? ((m == j) | ((j < idm) & ((idm - j <= si.win) | (idm >= si.tail0))) | (j < si.ctx_eff)) & (m < si.n)
-                                 : ((c >= mk_from - m0) | (c == mk_own - m0)) & (c < mk_end - m0);
-            pe = kp ? pe : 0.f;
-            g = kp ? g : 0.f;
-          }
-          pv[r] = pe;
-          ds[r] = g;
-        }
-        u32x4 p0, p1, d0, d1;
+        for (int r = 0; r < 16; ++r)
+          ts[r] = PER_TOKEN ? p.attn_scale[si.s + min(m0 + qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3), si.n - 1)] : 1.0f;
+      };
+      constexpr int PD = 3;  // fragments requested this many products ahead in the pipelined phases
+      f32x16 sA, dpA, sB, dpB;
+      float bias[16], ts[16];
+      unsigned pwA[8], dwA[8], pwB[8], dwB[8];  // packed P and dS of the two blocks
+      // phase 1
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p0[i] = pack_bf16x2(pv[2 * i], pv[2 * i + 1]);
-          p1[i] = pack_bf16x2(pv[8 + 2 * i], pv[8 + 2 * i + 1]);
-          d0[i] = pack_bf16x2(ds[2 * i], ds[2 * i + 1]);
-          d1[i] = pack_bf16x2(ds[8 + 2 * i], ds[8 + 2 * i + 1]);
-        }
-        const bf16x8 pb0 = __builtin_bit_cast(bf16x8, p0), pb1 = __builtin_bit_cast(bf16x8, p1);
-        const bf16x8 db0 = __builtin_bit_cast(bf16x8, d0), db1 = __builtin_bit_cast(bf16x8, d1);
-        bf16x8 fg[8], fq[8];
+      for (int i = 0; i < 16; ++i) score_mfma(0, i, sA, dpA, score_frag(0, i));
+      load_bias(0, bias);
+      load_ts(0, ts);
+      // an MFMA result may be read by other instructions 11 cycles after the MFMA at the earliest; the
+      // compiler does not count for instructions it did not place
+      asm volatile("s_nop 15" : "+v"(sA), "+v"(dpA));
+      // phase 2
+      {
+        bf16x8 F[16];
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          fg[2 * db] = bwd_tr_frag(gb, lc, db, 2 * qb32); fg[2 * db + 1] = bwd_tr_frag(gb, lc, db, 2 * qb32 + 1);
-          fq[2 * db] = bwd_tr_frag(qb, lc, db, 2 * qb32); fq[2 * db + 1] = bwd_tr_frag(qb, lc, db, 2 * qb32 + 1);
+        for (int i = 0; i < PD; ++i) F[i] = score_frag(1, i);
+        float pe_prev = 0.f, g_prev = 0.f;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (i + PD < 16) F[i + PD] = score_frag(1, i + PD);
+          score_mfma(1, i, sB, dpB, F[i]);
+          float pe, g;
+          element(0, i, sA[i], dpA[i], bias[i], ts[i], pe, g);
+          if (i & 1) { pwA[i >> 1] = pack_bf16x2(pe_prev, pe); dwA[i >> 1] = pack_bf16x2(g_prev, g); }
+          pe_prev = pe; g_prev = g;
+          __builtin_amdgcn_sched_barrier(0);
         }
-        bwd_acc_mfma16(fg, fq, pb0, pb1, db0, db1);
+      }
+      load_bias(1, bias);
+      load_ts(1, ts);
+      asm volatile("s_nop 15" : "+v"(sB), "+v"(dpB));
+      // phase 3
+      {
+        const u32x4 pa0 = {pwA[0], pwA[1], pwA[2], pwA[3]}, pa1 = {pwA[4], pwA[5], pwA[6], pwA[7]};
+        const u32x4 da0 = {dwA[0], dwA[1], dwA[2], dwA[3]}, da1 = {dwA[4], dwA[5], dwA[6], dwA[7]};
+        const bf16x8 opA[4] = {__builtin_bit_cast(bf16x8, pa0), __builtin_bit_cast(bf16x8, da0),
+                               __builtin_bit_cast(bf16x8, pa1), __builtin_bit_cast(bf16x8, da1)};
+        bf16x8 F[16];
+#pragma unroll
+        for (int i = 0; i < PD; ++i) F[i] = acc_frag(0, i);
+        float pe_prev = 0.f, g_prev = 0.f;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (i + PD < 16) F[i + PD] = acc_frag(0, i + PD);
+          bwd_acc_mfma1(((i & 1) ? 4 : 0) + ((i >> 1) & 3), F[i], opA[2 * (i >> 3) + (i & 1)]);
+          float pe, g;
+          element(1, i, sB[i], dpB[i], bias[i], ts[i], pe, g);
+          if (i & 1) { pwB[i >> 1] = pack_bf16x2(pe_prev, pe); dwB[i >> 1] = pack_bf16x2(g_prev, g); }
+          pe_prev = pe; g_prev = g;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      // phase 4
+      {
+        const u32x4 pb0 = {pwB[0], pwB[1], pwB[2], pwB[3]}, pb1 = {pwB[4], pwB[5], pwB[6], pwB[7]};
+        const u32x4 db0 = {dwB[0], dwB[1], dwB[2], dwB[3]}, db1 = {dwB[4], dwB[5], dwB[6], dwB[7]};
+        const bf16x8 opB[4] = {__builtin_bit_cast(bf16x8, pb0), __builtin_bit_cast(bf16x8, db0),
+                               __builtin_bit_cast(bf16x8, pb1), __builtin_bit_cast(bf16x8, db1)};
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          bwd_acc_mfma1(((i & 1) ? 4 : 0) + ((i >> 1) & 3), acc_frag(1, i), opB[2 * (i >> 3) + (i & 1)]);
       }
     };
 
