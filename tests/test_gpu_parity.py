@@ -599,3 +599,35 @@ def test_fp8_scales_ignore_padding_rows(oracle):
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all().item() and not out[end:].float().abs().any().item()
     assert_bf16_close(out[:end], _fp8_reference(oracle, wl)[:end], "fp8 with NaN padding")
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_long_sequences_randomized(oracle, seed):
+    """Sequences long enough for the leading-tile loop of the direct-to-LDS kernel (eight or more key
+    tiles that are unmasked for a whole query tile), with what decides where that loop starts and
+    stops drawn at random: lengths off the tile grid, target counts that cut the history short or
+    leave query tiles of targets only, contextual prefixes, tail rows, the kind of output scale."""
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    rng = np.random.default_rng(7000 + seed)
+    B = int(rng.integers(1, 4))
+    lengths = [int(rng.integers(600, 2300)) for _ in range(B)]
+    if seed % 3 == 0:
+        lengths[0] = int(rng.choice([640, 704, 768, 1024, 1279, 1281]))
+    targets = []
+    for n in lengths:
+        kind = rng.random()
+        targets.append(0 if kind < 0.3 else int(rng.integers(1, 200)) if kind < 0.7 else int(rng.integers(n // 2, n)))
+    H = int(rng.integers(1, 3))
+    ctx = int(rng.choice([0, 0, 5, 70, 700]))
+    N = max(lengths) + int(rng.integers(0, 70))
+    wl = make_jagged(lengths, targets, H, 128, 128, max_seq_len=N, alpha=1.0 / 128, dtype="bf16", seed=300 + seed,
+                     contextual_seq_len=ctx, tail_rows=int(rng.integers(0, 4)))
+    scale = None
+    if seed % 2:
+        scale = (0.5 + torch.rand(wl.T, generator=torch.Generator().manual_seed(seed))) / 100
+    out = run_hip(wl, attn_scale=scale)
+    assert _lib.last_kernel() == "tiled_d128_bf16"
+    ref = run_oracle(oracle, wl, attn_scale=scale)
+    assert_bf16_close(out, ref, f"long seed {seed}: lengths {lengths} targets {targets} H {H} ctx {ctx}")
