@@ -310,10 +310,10 @@ size_t max_items(int T, int B, int H) { return ((size_t)((T + BM - 1) / BM) + (s
 constexpr size_t WS_HEADER = 64;
 
 template <bool SEMI, bool HAS_RAB>
-void launch_bwd_tiled_as(dim3 grid, hipStream_t stream, const BwdParams& bk, const BwdParams& bq) {
+void launch_bwd_tiled_as(dim3 grid, dim3 grid_k, hipStream_t stream, const BwdParams& bk, const BwdParams& bq) {
   const bool per_token = bk.f.attn_scale && (bk.f.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
-  if (per_token) hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB, true>), grid, dim3(256), 0, stream, bk);
-  else hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB, false>), grid, dim3(256), 0, stream, bk);
+  if (per_token) hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB, true>), grid_k, dim3(256), 0, stream, bk);
+  else hipLaunchKernelGGL((hstu_bwd_dkv_d128<SEMI, HAS_RAB, false>), grid_k, dim3(256), 0, stream, bk);
   if constexpr (HAS_RAB) {
     if (bq.drab) {  // the query-tile kernel also sums dS along the diagonals
       if (per_token) hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, true, true, true>), grid, dim3(256), 0, stream, bq);
@@ -324,13 +324,13 @@ void launch_bwd_tiled_as(dim3 grid, hipStream_t stream, const BwdParams& bk, con
   if (per_token) hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, HAS_RAB, true>), grid, dim3(256), 0, stream, bq);
   else hipLaunchKernelGGL((hstu_bwd_dq_d128<SEMI, HAS_RAB, false>), grid, dim3(256), 0, stream, bq);
 }
-void launch_bwd_tiled(bool semi, bool has_rab, dim3 grid, hipStream_t stream, const BwdParams& bk, const BwdParams& bq) {
+void launch_bwd_tiled(bool semi, bool has_rab, dim3 grid, dim3 grid_k, hipStream_t stream, const BwdParams& bk, const BwdParams& bq) {
   if (semi) {
-    if (has_rab) launch_bwd_tiled_as<true, true>(grid, stream, bk, bq);
-    else launch_bwd_tiled_as<true, false>(grid, stream, bk, bq);
+    if (has_rab) launch_bwd_tiled_as<true, true>(grid, grid_k, stream, bk, bq);
+    else launch_bwd_tiled_as<true, false>(grid, grid_k, stream, bk, bq);
   } else {
-    if (has_rab) launch_bwd_tiled_as<false, true>(grid, stream, bk, bq);
-    else launch_bwd_tiled_as<false, false>(grid, stream, bk, bq);
+    if (has_rab) launch_bwd_tiled_as<false, true>(grid, grid_k, stream, bk, bq);
+    else launch_bwd_tiled_as<false, false>(grid, grid_k, stream, bk, bq);
   }
 }
 
@@ -639,7 +639,10 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     bk.f.ws_counts = (int*)((char*)workspace + half_ws);
     bk.f.ws_items = (WorkItem*)((char*)workspace + half_ws + WS_HEADER);
     bq.f.items_cap = bk.f.items_cap = (int)items;
-    bq.f.grid_slots = bk.f.grid_slots = (int)slots;
+    bq.f.grid_slots = (int)slots;
+    // the key-tile kernel's workgroups (one per CU) stay and draw further items from the lists' counters
+    const size_t kslots = slots < (size_t)BWD_DKV_WG_PER_XCD ? slots : (size_t)BWD_DKV_WG_PER_XCD;
+    bk.f.grid_slots = (int)kslots;
     if (!(flags & RECIR_HSTU_FLAG_REUSE_PLAN)) {
       if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS) {
         hipLaunchKernelGGL(hstu_plan_pair_kernel, dim3(2), dim3(PLAN_THREADS), 0, stream, bq.f, PLAN_SHIFT_ODD, bk.f, PLAN_REVERSE, BWD_BM);
@@ -652,8 +655,8 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
         }
       }
     }
-    const dim3 grid((unsigned)(slots * NUM_XCD));
-    launch_bwd_tiled(semi, rab != nullptr, grid, stream, bk, bq);
+    const dim3 grid((unsigned)(slots * NUM_XCD)), grid_k((unsigned)(kslots * NUM_XCD));
+    launch_bwd_tiled(semi, rab != nullptr, grid, grid_k, stream, bk, bq);
     if (int rc = launch_status("hstu_bwd_d128")) return rc;
     g_last_kernel = rab ? "bwd_tiled_d128_bf16_rab" : "bwd_tiled_d128_bf16";
     return RECIR_HSTU_OK;

@@ -150,6 +150,7 @@ __device__ __forceinline__ float bwd_output_scale(const Params& p) {
 // log2(e), index clamped to the row) follows at the end of the tile, where everything is waited for
 // anyway; the bias joins the fp32 score in the fused multiply-add that applies alpha * log2(e).
 constexpr int BWD_BAND = BWD_BM + BWD_BN;  // 191 used
+constexpr int BWD_DKV_WG_PER_XCD = 32;     // the key-tile kernel runs one workgroup per CU
 __device__ __forceinline__ float bwd_band_load(const float* __restrict__ rab_row, int rab_w, int first_idx, int tid) {
   return rab_row[min(max(first_idx + tid, 0), rab_w - 1)];
 }
@@ -446,6 +447,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
   __shared__ __attribute__((aligned(1024))) unsigned short Gs1[BWD_BN * HD];
   __shared__ float band0[HAS_RAB ? BWD_BAND : 1];
   __shared__ float band1[HAS_RAB ? BWD_BAND : 1];
+  __shared__ int next_rec[16];  // the next item of this workgroup: its record (8 words), then its list position
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -457,11 +459,50 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
   zero_tail_rows_of<256>(p, bp.dk, (size_t)p.H * HD * 2);
   zero_tail_rows_of<256>(p, bp.dv, (size_t)p.H * HD * 2);
 
+  // One workgroup per CU, so nothing hides what a workgroup waits for between two items.  The
+  // workgroups stay: the first item of each is the list position of its index, after that it draws
+  // positions from the list's counter (heaviest first, whoever is free first), one draw per item it
+  // runs, issued two query tiles before the item ends; the drawn item's record is fetched into LDS
+  // during the last tile.  The workgroup whose draw returns the last value any draw of this launch
+  // can return puts the counter back for the next launch (work lists reused or not).
   const int xcd = blockIdx.x % NUM_XCD;
   const int list_len = p.ws_counts[xcd];
+  int* const draw_ctr = p.ws_counts + NUM_XCD + xcd;
   const WorkItem* __restrict__ list = p.ws_items + (size_t)xcd * p.items_cap;
-  for (int slot = blockIdx.x / NUM_XCD; slot < list_len; slot += p.grid_slots) {
-    const WorkItem wi = list[slot];
+  int slot = blockIdx.x / NUM_XCD;
+  WorkItem wi;
+  if (slot < list_len) wi = list[slot];
+  while (slot < list_len) {
+    int drawn_v = 0;    // (wave 0) value of this item's draw, in flight until the tile ends
+    int drawn = 0;      // 0: not drawn yet, 1: draw issued, 2: value read and record requested
+    int next_slot = 0;
+    auto draw_value_arrived = [&]() __attribute__((always_inline)) {
+      next_slot = __builtin_amdgcn_readfirstlane(drawn_v);
+      if (next_slot == p.grid_slots + list_len - 1 && lane == 0) *draw_ctr = p.grid_slots;  // nobody draws after this one
+      // eight lanes fetch the eight words of the record straight into LDS; word 8 is the list position
+      if (next_slot < list_len && lane < 8)
+        copy4((const char*)(list + next_slot), (unsigned)lane * 4u, (unsigned)(size_t)&next_rec[0]);
+      if (lane == 0) next_rec[8] = next_slot;
+      drawn = 2;
+    };
+    auto draw_step = [&](int left) __attribute__((always_inline)) {
+      if (wave != 0) return;
+      if (drawn == 0 && left <= 2) {
+        if (lane == 0) drawn_v = atomicAdd(draw_ctr, 1);
+        drawn = 1;
+      } else if (drawn == 1) {  // the tile in between ended with a wait for everything in flight
+        draw_value_arrived();
+      }
+    };
+    auto draw_finish = [&]() __attribute__((always_inline)) {
+      if (wave != 0) return;
+      if (drawn == 0) {
+        if (lane == 0) drawn_v = atomicAdd(draw_ctr, 1);
+        drawn = 1;
+      }
+      if (drawn == 1) draw_value_arrived();
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
     SeqInfo si;
     si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
     si.win = WIN_ALL; si.tail0 = 0x7fffffff;
@@ -694,6 +735,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       float band_nxt = 0.f;
       if (HAS_RAB && nxt < nq) band_nxt = band_of(nxt);
       if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 1>{});
+      draw_step(nq - it);
       compute_tile(it, std::integral_constant<int, 0>{});
       if (HAS_RAB && nxt < nq) bwd_band_store<false>(band1, band_nxt, tid);
       it = nxt;
@@ -703,10 +745,12 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       nxt = it + 1;
       if (HAS_RAB && nxt < nq) band_nxt = band_of(nxt);
       if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 0>{});
+      draw_step(nq - it);
       compute_tile(it, std::integral_constant<int, 1>{});
       if (HAS_RAB && nxt < nq) bwd_band_store<false>(band0, band_nxt, tid);
       it = nxt;
     }
+    draw_finish();
 
     if (j < si.n) {
       const float oscale = PER_TOKEN ? 1.0f : bwd_output_scale(p);
@@ -731,7 +775,15 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
         }
       }
     }
-    __syncthreads();
+    __syncthreads();  // LDS is reused by the next item; its record is in
+    // (the same for every lane: said so, because the tile copies take their base address in scalar registers)
+    auto uni = [](int x) { return __builtin_amdgcn_readfirstlane(x); };
+    slot = uni(next_rec[8]);
+    if (slot < list_len) {
+      wi.s = uni(next_rec[0]); wi.n = uni(next_rec[1]); wi.cap = uni(next_rec[2]); wi.ctx_eff = uni(next_rec[3]);
+      wi.q0 = uni(next_rec[4]); wi.h = uni(next_rec[5]); wi.b = uni(next_rec[6]); wi.q_end = uni(next_rec[7]);
+    }
+    __syncthreads();  // next_rec is written again during the item
   }
 }
 

@@ -42,7 +42,8 @@ struct Params {
   const float* attn_scale;
   const float* q_scale;
   const float* k_scale;
-  int* ws_counts;             // [NUM_XCD] length of each per-XCD work list
+  int* ws_counts;             // [NUM_XCD] length of each per-XCD work list, then [NUM_XCD] the next list position to draw
+                              // (kernels whose workgroups stay and draw their items)
   struct WorkItem* ws_items;  // [NUM_XCD][items_cap]
   int items_cap;              // capacity of one per-XCD list
   int grid_slots;             // slots per XCD the launch covers (gridDim.x = NUM_XCD * grid_slots)

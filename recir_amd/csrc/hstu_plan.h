@@ -160,6 +160,7 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
     if (tid < NUM_XCD) {
       const int n_items = items_s, part = n_items % (2 * NUM_XCD);
       p.ws_counts[tid] = 2 * (n_items / (2 * NUM_XCD)) + (tid < part ? 1 : 0) + (tid >= 2 * NUM_XCD - part ? 1 : 0);
+      p.ws_counts[NUM_XCD + tid] = p.grid_slots;  // first list position a persistent kernel's workgroups draw
     }
     return;
   }
@@ -197,6 +198,7 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
     int total = 0;
     for (int k = 0; k < per_list; ++k) total += xnt[tid][k];
     p.ws_counts[tid] = total;
+    p.ws_counts[NUM_XCD + tid] = p.grid_slots;
   }
 }
 
@@ -244,6 +246,7 @@ __global__ __launch_bounds__(256) void hstu_plan_kernel_general(Params p, int bm
     for (int pr = 0; pr < pairs; ++pr)
       if (snake_xcd(pr) == x) total += (seq_info(p, pr / H).n + bm - 1) / bm;
     p.ws_counts[x] = total;
+    p.ws_counts[NUM_XCD + x] = p.grid_slots;
   }
 }
 

@@ -61,6 +61,10 @@ typedef __attribute__((ext_vector_type(8))) int i32x8;
 __device__ __forceinline__ void copy16(const void* base, unsigned lane_off, unsigned lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_addr), "v"(lane_off), "s"(base) : "memory");
 }
+// The same with four bytes per lane (lane i lands at lds_addr + 4 i).
+__device__ __forceinline__ void copy4(const void* base, unsigned lane_off, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_addr), "v"(lane_off), "s"(base) : "memory");
+}
 // LDS swizzle of the bf16 K and V tiles: 1 = free of bank conflicts on the 64-bank LDS
 // (K chunk ^ (row & 15), V slot ^ 2 (row & 3)); 0 = the 32-bank forms (K chunk ^ (row & 7), V slot ^
 // (row & 3)), which run the LDS reads at half rate.  The 64-bank forms need six address registers more;
