@@ -46,6 +46,12 @@ extern "C" {
                                                      call built for the same seq_offsets, T, B and
                                                      kernel variant: skip rebuilding it (the layers
                                                      of one model step share their offsets)        */
+#define RECIR_HSTU_FLAG_GROUPED_LISTS 0x10000u    /* walk each XCD's work list by groups of eight
+                                                     (sequence, head) pairs instead of all pairs at
+                                                     once (L2 locality against balance).  The library
+                                                     chooses this by itself when the tensors of a call
+                                                     exceed the last-level cache; the flag forces it
+                                                     (tests, tuning).  No effect on results.          */
 #define RECIR_HSTU_FLAG_KERNEL_SHIFT 8            /* bits 8..15: kernel selector for tests/tuning  */
 #define RECIR_HSTU_FLAG_KERNEL_MASK 0xff00u       /* 0 auto, 1 generic, 2.. tiled variants         */
 

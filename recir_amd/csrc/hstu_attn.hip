@@ -305,6 +305,16 @@ int launch_status(const char* what) {
   return 0;
 }
 
+// Do the tensors one call streams (n_qk of [T, H, Dqk] with qk_bytes per element, n_v of [T, H, Dv] in
+// bf16) exceed the 256 MB last-level cache?
+bool tensors_exceed_llc(int T, int H, int Dqk, int Dv, int qk_bytes, int n_each) {
+  const size_t bytes = (size_t)T * H * ((size_t)Dqk * qk_bytes + (size_t)Dv * 2) * n_each;
+  return bytes > ((size_t)256 << 20);
+}
+
+#ifndef BWD_GROUP_TENSORS
+#define BWD_GROUP_TENSORS 1000000  // backward: grouped lists only on request until measured
+#endif
 // upper bound on the (sequence, query tile, head) items of a call
 size_t max_items(int T, int B, int H) { return ((size_t)((T + BM - 1) / BM) + (size_t)B) * (size_t)H; }
 constexpr size_t WS_HEADER = 64;
@@ -435,7 +445,9 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     p.items_cap = (int)items;
     const int bm = BM;
     // only the direct-to-LDS kernel reads the row bound of an item
-    const int plan_mode = (variant == 0 || variant == 3) ? PLAN_SHIFT_ODD : 0;
+    int plan_mode = (variant == 0 || variant == 3) ? PLAN_SHIFT_ODD : 0;
+    // q, k, v and out beyond the last-level cache: lists ordered by groups of pairs (hstu_plan.h)
+    if ((flags & RECIR_HSTU_FLAG_GROUPED_LISTS) || tensors_exceed_llc(T, H, Dqk, Dv, fp8 ? 1 : 2, 2)) plan_mode |= PLAN_GROUP;
     // slots per XCD the launch covers: an even share of the items plus the imbalance the dealing of
     // whole (sequence, head) pairs can leave (about one sequence's worth of tiles); longer lists,
     // possible only with sequences above max_seq_len, are walked by the workgroups' stride loop
@@ -645,7 +657,9 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     bk.f.grid_slots = (int)kslots;
     if (!(flags & RECIR_HSTU_FLAG_REUSE_PLAN)) {
       if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS) {
-        hipLaunchKernelGGL(hstu_plan_pair_kernel, dim3(2), dim3(PLAN_THREADS), 0, stream, bq.f, PLAN_SHIFT_ODD, bk.f, PLAN_REVERSE, BWD_BM);
+        // q, k, v, dout and the three gradients beyond the last-level cache: lists ordered by groups of pairs
+        const int grp = ((flags & RECIR_HSTU_FLAG_GROUPED_LISTS) || tensors_exceed_llc(T, H, Dqk, Dv, 2, BWD_GROUP_TENSORS)) ? PLAN_GROUP : 0;
+        hipLaunchKernelGGL(hstu_plan_pair_kernel, dim3(2), dim3(PLAN_THREADS), 0, stream, bq.f, PLAN_SHIFT_ODD | grp, bk.f, PLAN_REVERSE | grp, BWD_BM);
         if (int rc = launch_status("hstu_plan_pair_kernel")) return rc;
       } else {
         for (int rev = 0; rev < 2; ++rev) {

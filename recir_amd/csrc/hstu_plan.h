@@ -38,6 +38,8 @@ __device__ __forceinline__ int snake_slot(int pr) {
 constexpr int PLAN_REVERSE = 1;     // item at the position of tile t carries tile nt - 1 - t
 constexpr int PLAN_SHIFT_ODD = 2;   // see tile_rows
 constexpr int PLAN_NO_SPREAD = 4;   // always deal whole (sequence, head) pairs
+constexpr int PLAN_GROUP = 8;       // order a list by groups of PLAN_GROUP_PAIRS pairs (see plan_one_block)
+constexpr int PLAN_GROUP_PAIRS = 8;
 #ifndef HSTU_PLAN_SPREAD_AT
 #define HSTU_PLAN_SPREAD_AT 1.05f
 #endif
@@ -72,6 +74,7 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
   __shared__ int nt_by_rank[PLAN_MAX_B];
   __shared__ int xnt[NUM_XCD][PLAN_MAX_PAIRS / NUM_XCD + 2];  // tiles of the k-th pair of list x
   __shared__ int above[NUM_XCD][PLAN_MAX_TILES + 1];          // tiles of list x with index > t
+  __shared__ int gbase[NUM_XCD][PLAN_MAX_PAIRS / NUM_XCD / PLAN_GROUP_PAIRS + 2];  // items of list x ahead of its group g
   __shared__ int tmax_s, spread_s, items_s;
   __shared__ float list_work[NUM_XCD];
   __shared__ int seq_s[PLAN_MAX_B], seq_n[PLAN_MAX_B], seq_cap[PLAN_MAX_B], seq_ctx[PLAN_MAX_B];
@@ -170,9 +173,26 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
     return a;
   };
   const int ttab = min(tmax, PLAN_MAX_TILES) + 1;  // tabulated tile indices; beyond: computed in place
-  for (int i = tid; i < NUM_XCD * ttab; i += PLAN_THREADS) {
-    const int x = i / ttab, t = i - x * ttab;
-    above[x][t] = tiles_above(x, t);
+  // Grouped order (PLAN_GROUP): a list is walked group by group of PLAN_GROUP_PAIRS pairs, tile index
+  // descending inside a group.  All pairs at once is the better order for balance (2-4 % at
+  // configuration 2), but their K and V rows together are several times an XCD's L2; once the tensors
+  // of a call no longer fit the last-level cache either, the re-fetches cost more than the balance
+  // (four times configuration 2: 348 -> 317 us).  The caller decides by the size of the tensors.
+  const bool grouped = (mode & PLAN_GROUP) != 0;
+  if (grouped) {
+    const int ngroups = (per_list + PLAN_GROUP_PAIRS - 1) / PLAN_GROUP_PAIRS;
+    for (int i = tid; i < NUM_XCD; i += PLAN_THREADS) {
+      int run = 0;
+      for (int g = 0; g <= ngroups; ++g) {
+        gbase[i][g] = run;
+        for (int k = g * PLAN_GROUP_PAIRS; k < (g + 1) * PLAN_GROUP_PAIRS && k < per_list; ++k) run += xnt[i][k];
+      }
+    }
+  } else {
+    for (int i = tid; i < NUM_XCD * ttab; i += PLAN_THREADS) {
+      const int x = i / ttab, t = i - x * ttab;
+      above[x][t] = tiles_above(x, t);
+    }
   }
   __syncthreads();
   // one thread per (rank, tile, head)
@@ -189,7 +209,14 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
     const int x = snake_xcd(pr), k = snake_slot(pr);
     // pairs enter a list in rank order, so the k pairs ahead of this one in its list have at least
     // as many tiles: each of them owns a tile t, and all of those come first
-    const int pos = (t < ttab ? above[x][t] : tiles_above(x, t)) + k;
+    int pos;
+    if (grouped) {
+      const int g = k / PLAN_GROUP_PAIRS, k0 = g * PLAN_GROUP_PAIRS;
+      pos = gbase[x][g] + (k - k0);
+      for (int kk = k0; kk < k0 + PLAN_GROUP_PAIRS && kk < per_list; ++kk) pos += max(0, xnt[x][kk] - 1 - t);
+    } else {
+      pos = (t < ttab ? above[x][t] : tiles_above(x, t)) + k;
+    }
     WorkItem w;
     fill_item(w, si, bm, t, my_nt, mode, h, b);
     p.ws_items[(size_t)x * p.items_cap + pos] = w;

@@ -29,7 +29,27 @@ KERNEL_TILED = 2         # tiled MFMA kernel, K/V staged through registers
 KERNEL_TILED_DIRECT = 3  # tiled MFMA kernel, K/V copied global -> LDS directly
 
 _forced_kernel = KERNEL_AUTO
+_extra_flags = 0
 _ctx_reference_rule = False
+
+
+class extra_flags:
+    """Context manager for tests and tuning: C-ABI flag bits added to every call (for example
+    ``_lib.FLAG_GROUPED_LISTS``)."""
+
+    def __init__(self, flags: int):
+        self.flags = int(flags)
+
+    def __enter__(self):
+        global _extra_flags
+        self._prev = _extra_flags
+        _extra_flags = self._prev | self.flags
+        return self
+
+    def __exit__(self, *exc):
+        global _extra_flags
+        _extra_flags = self._prev
+        return False
 
 
 class force_kernel:
@@ -173,6 +193,7 @@ def _prepare(opname, q, k, v, seq_offsets, num_targets, attn_scale, rab, N, ctx_
     if _ctx_reference_rule or ctx_reference:
         flags |= _lib.FLAG_CTX_REFERENCE
     flags |= (_forced_kernel & 0xFF) << _lib.FLAG_KERNEL_SHIFT
+    flags |= _extra_flags
     sc = None
     if attn_scale is not None:
         sc = attn_scale.to(device=dev, dtype=torch.float32).contiguous()

@@ -631,3 +631,33 @@ def test_long_sequences_randomized(oracle, seed):
     assert _lib.last_kernel() == "tiled_d128_bf16"
     ref = run_oracle(oracle, wl, attn_scale=scale)
     assert_bf16_close(out, ref, f"long seed {seed}: lengths {lengths} targets {targets} H {H} ctx {ctx}")
+
+
+def test_grouped_work_lists_give_the_same_output(oracle):
+    """RECIR_HSTU_FLAG_GROUPED_LISTS only changes the order in which an XCD's work list is walked
+    (groups of eight (sequence, head) pairs): bit-identical output, forward and backward, with more
+    pairs per list than one group holds and with lists that tiles are dealt to."""
+    import recir_amd
+    from recir_amd import _lib, ops
+    from recir_amd.workloads import make_jagged
+
+    rng = np.random.default_rng(5)
+    for lengths in ([int(x) for x in rng.integers(1, 700, size=40)], [900] + [70] * 20):
+        targets = [int(rng.integers(0, n // 3 + 1)) for n in lengths]
+        wl = make_jagged(lengths, targets, 4, 128, 128, max_seq_len=max(lengths) + 3, alpha=1.0 / 128, dtype="bf16",
+                         seed=77, tail_rows=2)
+        out = run_hip(wl)
+        assert _lib.last_kernel() == "tiled_d128_bf16"
+        assert_bf16_close(out, run_oracle(oracle, wl), f"{len(lengths)} sequences, lists as built")
+        q, k, v, off, nt = to_device(wl)
+        dout = torch.randn(wl.T, wl.H, 128, generator=torch.Generator().manual_seed(1)).to(q.device, q.dtype)
+        grads = recir_amd.jagged_hstu_attention_backward(dout, q, k, v, off, nt, None, max_seq_len=wl.max_seq_len,
+                                                         alpha=wl.alpha)
+        with ops.extra_flags(_lib.FLAG_GROUPED_LISTS):
+            out_g = run_hip(wl)
+            grads_g = recir_amd.jagged_hstu_attention_backward(dout, q, k, v, off, nt, None,
+                                                               max_seq_len=wl.max_seq_len, alpha=wl.alpha)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out_g)
+        for a, b in zip(grads, grads_g):
+            assert torch.equal(a, b)
