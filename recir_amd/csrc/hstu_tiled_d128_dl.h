@@ -114,14 +114,6 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
 #ifndef HSTU_DL_SKEW_PD
 #define HSTU_DL_SKEW_PD 3  // its fragment prefetch distance in slots
 #endif
-#ifndef HSTU_SK_ABL
-#define HSTU_SK_ABL 0  // measurement builds only: 1 no fragment reads, 2 no copies, 4 no barrier, 8 no SiLU in the skewed loop (wrong results)
-#endif
-#if HSTU_SK_ABL & 4
-#define HSTU_SK_SYNC() do { } while (0)
-#else
-#define HSTU_SK_SYNC() HSTU_DL_TILE_SYNC()
-#endif
 #define HSTU_DL_TILE_SYNC() do { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); __syncthreads(); } while (0)
 #ifndef HSTU_DL_C0
 #define HSTU_DL_C0 0     // slot of the first copy instruction of the next tile
@@ -724,9 +716,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         return KIND == 3 ? s < 8 : (KIND == 0 ? s >= 8 : (KIND == 2 ? (s < 16 || s >= 24) : true));
       };
       auto slot_frag = [&](int s) __attribute__((always_inline)) {
-#if HSTU_SK_ABL & 1
-        return qf[(s * 5 + 3) & 7];
-#endif
         if (s < 8) return v_frag_at(vo, s & 3, 2 + (s >> 2));
         if (s < 16) return k_frag_at(kc, 1, s - 8);
         if (s < 24) return k_frag_at(ko, 0, s - 16);
@@ -779,13 +768,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           __builtin_amdgcn_s_setprio(0);
 #endif
         }
-#if !(HSTU_SK_ABL & 2)
         if (KIND != 3 && s < 8 && !(KIND == 0 && s >= 6) && !(KIND == 2 && s < 2)) skew_copy(i, buf_tag, s);
-#endif
-#if !(HSTU_SK_ABL & 8)
 #pragma unroll
         for (int stage = 5; stage >= 1; --stage) silu_stage(s, stage);
-#endif
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -844,20 +829,20 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         }
         __syncthreads();  // the first trip refills the K rows just read
         skew_body(st0, std::integral_constant<int, 0>{}, 0);
-        HSTU_SK_SYNC();
+        HSTU_DL_TILE_SYNC();
         for (int i = 1; i + 1 < skew_tiles; i += 2) {
           skew_body(st1, std::integral_constant<int, 1>{}, i);
-          HSTU_SK_SYNC();
+          HSTU_DL_TILE_SYNC();
           skew_body(st0, std::integral_constant<int, 1>{}, i + 1);
-          HSTU_SK_SYNC();
+          HSTU_DL_TILE_SYNC();
         }
         skew_body(st1, std::integral_constant<int, 2>{}, skew_tiles - 1);
-        HSTU_SK_SYNC();
+        HSTU_DL_TILE_SYNC();
         // V rows 32..63 of the tile the plain loop takes over with; the second half of the last skewed tile
         skew_copy(skew_tiles, st0, 6);
         skew_copy(skew_tiles, st0, 7);
         skew_body(st0, std::integral_constant<int, 3>{}, skew_tiles);
-        HSTU_SK_SYNC();
+        HSTU_DL_TILE_SYNC();
         it = skew_tiles;
         fast_pairs = 0;
       }
