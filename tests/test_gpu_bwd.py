@@ -500,3 +500,30 @@ def test_no_sequences_through_the_c_abi_zero_the_outputs():
     torch.cuda.synchronize()
     for t in [out] + grads:
         assert not t.float().abs().any().item() and torch.isfinite(t.float()).all().item()
+
+
+def test_backward_with_reused_work_lists_repeats_itself(oracle):
+    """The key-tile kernel's workgroups draw their items from counters in the workspace and the launch
+    puts them back itself: with the work lists reused (no plan kernel between the calls) a second and a
+    third call must still visit every item exactly once."""
+    import recir_amd
+    from recir_amd import ops
+
+    wl = _mid_workload(81, [700, 130, 64, 1, 333, 255] * 11, [9, 0, 64, 1, 40, 0] * 11, 0)  # 41 items per list: more than workgroups
+    g = torch.Generator().manual_seed(12)
+    dout = torch.randn(wl.T, wl.H, 128, generator=g).to(torch.bfloat16).float()
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                           attn_scale=np.float32(0.02), contextual_seq_len=0)
+    q, k, v, off, nt = to_device(wl)
+    d = dout.to(q.device, q.dtype)
+    with recir_amd.plan_cache_scope():
+        before = dict(ops.plan_cache_stats)
+        runs = [recir_amd.jagged_hstu_attention_backward(d, q, k, v, off, nt, torch.tensor(0.02),
+                                                         max_seq_len=wl.max_seq_len, alpha=wl.alpha) for _ in range(3)]
+        torch.cuda.synchronize()
+        assert ops.plan_cache_stats["hits"] - before["hits"] == 2
+    assert_grads_close(runs[0], want, int(wl.seq_offsets[-1]), BF16_REL, "lists built")
+    for later in runs[1:]:
+        for a, b in zip(runs[0], later):
+            assert torch.equal(a, b)
