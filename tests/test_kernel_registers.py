@@ -36,7 +36,7 @@ def _kernels(asm, name_part):
         m = re.match(r"^(_Z\w*" + name_part + r"\w*):", lines[i])
         if m:
             j = i + 1
-            while j < len(lines) and "s_endpgm" not in lines[j]:
+            while j < len(lines) and not lines[j].startswith(".Lfunc_end"):  # (a kernel may end in several places)
                 j += 1
             found.append((m.group(1), lines[i:j + 1]))
             i = j
