@@ -336,9 +336,33 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
         }
         if constexpr (RAB_GRAD) {
           const unsigned gaddr = (unsigned)(size_t)(BUF ? gband1 : gband0) + band_lane;
+          // Element 4 g + i of lane l (query row l, key 8 g + i of its half) lies on diagonal i - l: the four
+          // elements of lanes l .. l + 3 with i = 0 .. 3 share one.  They are summed across lanes first
+          // (three shifted additions inside a row of 16 lanes; a_k of lane l collects i - l' = k - l), so
+          // a lane adds one value per group to the band instead of four, and the first lane of each row
+          // also adds the three partial sums whose left neighbours are in another row.  The LDS additions
+          // were what this gradient cost: 1024 lane operations per block before, 304 now.
+          float a1s[4], a2s[4], a3s[4];
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8 * (r >> 2) + (r & 3))), ds[r], 0, 0, false);
+          for (int g4 = 0; g4 < 4; ++g4) {
+            auto shl1 = [](float x) {  // lane l receives the value of lane l + 1 of its row, the last lane 0
+              return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x101, 0xf, 0xf, true));
+            };
+            const float a3 = ds[4 * g4 + 3];
+            const float a2 = ds[4 * g4 + 2] + shl1(a3);
+            const float a1 = ds[4 * g4 + 1] + shl1(a2);
+            const float a0 = ds[4 * g4 + 0] + shl1(a1);
+            a1s[g4] = a1; a2s[g4] = a2; a3s[g4] = a3;
+            __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8 * g4)), a0, 0, 0, false);
+          }
+          if ((lane & 15) == 0) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8 * g4 + 1)), a1s[g4], 0, 0, false);
+              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8 * g4 + 2)), a2s[g4], 0, 0, false);
+              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8 * g4 + 3)), a3s[g4], 0, 0, false);
+            }
+          }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
