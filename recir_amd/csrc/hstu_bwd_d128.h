@@ -342,7 +342,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
           // a lane adds one value per group to the band instead of four, and the first lane of each row
           // also adds the three partial sums whose left neighbours are in another row.  The LDS additions
           // were what this gradient cost: 1024 lane operations per block before, 304 now.
-          float a1s[4], a2s[4], a3s[4];
+          float a0s[4], a1s[4], a2s[4], a3s[4];
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
             auto shl1 = [](float x) {  // lane l receives the value of lane l + 1 of its row, the last lane 0
@@ -352,8 +352,23 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
             const float a2 = ds[4 * g4 + 2] + shl1(a3);
             const float a1 = ds[4 * g4 + 1] + shl1(a2);
             const float a0 = ds[4 * g4 + 0] + shl1(a1);
-            a1s[g4] = a1; a2s[g4] = a2; a3s[g4] = a3;
-            __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8 * g4)), a0, 0, 0, false);
+            a1s[g4] = a1; a2s[g4] = a2; a3s[g4] = a3; a0s[g4] = a0;
+          }
+          // Group g + 1 of lane l + 8 lies on the diagonals of group g of lane l: lanes 0 .. 7 of a row take
+          // them over, and lanes 8 .. 15 are left with their group 0 only.
+          {
+            auto shl8 = [](float x) {
+              return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x108, 0xf, 0xf, true));
+            };
+            const float c0 = a0s[0] + shl8(a0s[1]), c1 = a0s[1] + shl8(a0s[2]), c2 = a0s[2] + shl8(a0s[3]);
+            if ((lane & 8) == 0) {
+              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 0)), c0, 0, 0, false);
+              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8)), c1, 0, 0, false);
+              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 16)), c2, 0, 0, false);
+              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 24)), a0s[3], 0, 0, false);
+            } else {
+              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 0)), a0s[0], 0, 0, false);
+            }
           }
           if ((lane & 15) == 0) {
 #pragma unroll
