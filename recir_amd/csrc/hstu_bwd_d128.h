@@ -341,7 +341,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
           // (three shifted additions inside a row of 16 lanes; a_k of lane l collects i - l' = k - l), so
           // a lane adds one value per group to the band instead of four, and the first lane of each row
           // also adds the three partial sums whose left neighbours are in another row.  The LDS additions
-          // were what this gradient cost: 1024 lane operations per block before, 304 now.
+          // were what this gradient cost: 1024 lane operations per block before, 208 with both stages.
           float a0s[4], a1s[4], a2s[4], a3s[4];
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
