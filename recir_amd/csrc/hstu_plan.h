@@ -75,23 +75,22 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
   __shared__ int xnt[NUM_XCD][PLAN_MAX_PAIRS / NUM_XCD + 2];  // tiles of the k-th pair of list x
   __shared__ int above[NUM_XCD][PLAN_MAX_TILES + 1];          // tiles of list x with index > t
   __shared__ int gbase[NUM_XCD][PLAN_MAX_PAIRS / NUM_XCD / PLAN_GROUP_PAIRS + 2];  // items of list x ahead of its group g
-  __shared__ int tmax_s, spread_s, items_s;
   __shared__ float list_work[NUM_XCD];
+  __shared__ int list_total[NUM_XCD];
   __shared__ int seq_s[PLAN_MAX_B], seq_n[PLAN_MAX_B], seq_cap[PLAN_MAX_B], seq_ctx[PLAN_MAX_B];
   const int tid = threadIdx.x;
   const int B = p.B, H = p.H;
   const int pairs = B * H;
   const int per_list = (pairs + NUM_XCD - 1) / NUM_XCD + 1;  // upper bound on pairs per list
 
-  if (tid == 0) tmax_s = 0;
-  for (int i = tid; i < NUM_XCD * (PLAN_MAX_PAIRS / NUM_XCD + 2); i += PLAN_THREADS) (&xnt[0][0])[i] = 0;
-  __syncthreads();
+  // The kernel is a chain of short phases on one CU, so its time is the number of barriers and the
+  // longest thing a single thread does between two of them: no phase has a loop over the batch or
+  // over a list in one thread that the others wait for.
+  for (int i = tid; i < NUM_XCD * per_list; i += PLAN_THREADS) xnt[i / per_list][i - (i / per_list) * per_list] = 0;
   for (int b = tid; b < B; b += PLAN_THREADS) {
     const SeqInfo si = seq_info(p, b);  // kept in LDS: the item phase needs it again
     seq_s[b] = si.s; seq_n[b] = si.n; seq_cap[b] = si.cap; seq_ctx[b] = si.ctx_eff;
-    const int v = (si.n + bm - 1) / bm;
-    nt[b] = v;
-    atomicMax(&tmax_s, v);
+    nt[b] = (si.n + bm - 1) / bm;
   }
   __syncthreads();
   for (int b = tid; b < B; b += PLAN_THREADS) {
@@ -105,39 +104,62 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
     nt_by_rank[r] = mine;
   }
   __syncthreads();
-  for (int r = tid; r < B; r += PLAN_THREADS) {
-    const int v = nt_by_rank[r];
-    for (int h = 0; h < H; ++h) {
-      const int pr = r * H + h;
-      xnt[snake_xcd(pr)][snake_slot(pr)] = v;
+  for (int i = tid; i < pairs; i += PLAN_THREADS) xnt[snake_xcd(i)][snake_slot(i)] = nt_by_rank[i / H];
+  __syncthreads();
+  const int tmax = B > 0 ? nt_by_rank[0] : 0;
+  // Work of a pair with v tiles ~ v (v + 1) / 2 (tile t meets t + 1 key tiles).  When dealing whole
+  // pairs leaves the lists unequal (few pairs, or one sequence far longer than the rest), tiles are
+  // dealt instead: see below.  Wave x sums list x.
+  if (tid < NUM_XCD * 64) {
+    const int x = tid >> 6;
+    float w = 0.f;
+    int total = 0;
+    for (int k = tid & 63; k < per_list; k += 64) { const int v = xnt[x][k]; w += (float)v * ((float)v + 1.f); total += v; }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) { w += __shfl_xor(w, d, 64); total += __shfl_xor(total, d, 64); }
+    if ((tid & 63) == 0) { list_work[x] = w; list_total[x] = total; }
+  }
+  // (the tables of the whole-pair order do not depend on that decision and are filled in the same phase)
+  auto tiles_above = [&](int x, int t) {
+    int a = 0;
+    for (int k = 0; k < per_list; ++k) a += max(0, xnt[x][k] - 1 - t);
+    return a;
+  };
+  const int ttab = min(tmax, PLAN_MAX_TILES) + 1;  // tabulated tile indices; beyond: computed in place
+  // Grouped order (PLAN_GROUP): a list is walked group by group of PLAN_GROUP_PAIRS pairs, tile index
+  // descending inside a group.  All pairs at once is the better order for balance (2-4 % at
+  // configuration 2), but their K and V rows together are several times an XCD's L2; once the tensors
+  // of a call no longer fit the last-level cache either, the re-fetches cost more than the balance
+  // (four times configuration 2: 348 -> 317 us).  The caller decides by the size of the tensors.
+  const bool grouped = (mode & PLAN_GROUP) != 0;
+  const int ngroups = (per_list + PLAN_GROUP_PAIRS - 1) / PLAN_GROUP_PAIRS;
+  if (grouped) {
+    // items of list x in its groups before g: one thread per (list, group)
+    for (int i = tid; i < NUM_XCD * (ngroups + 1); i += PLAN_THREADS) {
+      const int x = i / (ngroups + 1), g = i - x * (ngroups + 1);
+      int run = 0;
+      for (int k = 0; k < g * PLAN_GROUP_PAIRS && k < per_list; ++k) run += xnt[x][k];
+      gbase[x][g] = run;
+    }
+  } else {
+    for (int i = tid; i < NUM_XCD * ttab; i += PLAN_THREADS) {
+      const int x = i / ttab, t = i - x * ttab;
+      above[x][t] = tiles_above(x, t);
     }
   }
   __syncthreads();
-  const int tmax = tmax_s;
-  // Work of a pair with v tiles ~ v (v + 1) / 2 (tile t meets t + 1 key tiles).  When dealing whole
-  // pairs leaves the lists unequal (few pairs, or one sequence far longer than the rest), tiles are
-  // dealt instead: see below.
-  if (tid < NUM_XCD) {
-    float w = 0.f;
-    for (int k = 0; k < per_list; ++k) { const float v = (float)xnt[tid][k]; w += v * (v + 1.f); }
-    list_work[tid] = w;
-  }
-  __syncthreads();
-  if (tid == 0) {
+  bool spread = false;
+  int n_items = 0;
+  {
     float mx = 0.f, sum = 0.f;
-    for (int x = 0; x < NUM_XCD; ++x) { mx = fmaxf(mx, list_work[x]); sum += list_work[x]; }
-    int n_items = 0;
-    for (int r = 0; r < B; ++r) n_items += nt_by_rank[r];
-    items_s = n_items * H;
-    spread_s = (mode & PLAN_NO_SPREAD) ? 0 : (mx * NUM_XCD > sum * PLAN_SPREAD_AT);
+    for (int x = 0; x < NUM_XCD; ++x) { mx = fmaxf(mx, list_work[x]); sum += list_work[x]; n_items += list_total[x]; }
+    spread = !(mode & PLAN_NO_SPREAD) && (mx * NUM_XCD > sum * PLAN_SPREAD_AT);
   }
-  __syncthreads();
-  if (spread_s) {
+  if (spread) {
     // All tiles of all pairs in one order, tile index descending and pair rank ascending inside one
     // index, dealt to the lists in the same boustrophedon order: every list is still heaviest
     // first, the list sums differ by at most one tile's work, and a pair's K and V rows are read
     // through several L2s, which costs little when few pairs carry the work.
-    const int ttab = min(tmax, PLAN_MAX_TILES) + 1;
     auto all_above = [&](int t) {
       int a = 0;
       for (int r = 0; r < B; ++r) a += max(0, nt_by_rank[r] - 1 - t);
@@ -161,40 +183,12 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
       p.ws_items[(size_t)snake_xcd(g) * p.items_cap + snake_slot(g)] = w;
     }
     if (tid < NUM_XCD) {
-      const int n_items = items_s, part = n_items % (2 * NUM_XCD);
+      const int part = n_items % (2 * NUM_XCD);
       p.ws_counts[tid] = 2 * (n_items / (2 * NUM_XCD)) + (tid < part ? 1 : 0) + (tid >= 2 * NUM_XCD - part ? 1 : 0);
       p.ws_counts[NUM_XCD + tid] = p.grid_slots;  // first list position a persistent kernel's workgroups draw
     }
     return;
   }
-  auto tiles_above = [&](int x, int t) {
-    int a = 0;
-    for (int k = 0; k < per_list; ++k) a += max(0, xnt[x][k] - 1 - t);
-    return a;
-  };
-  const int ttab = min(tmax, PLAN_MAX_TILES) + 1;  // tabulated tile indices; beyond: computed in place
-  // Grouped order (PLAN_GROUP): a list is walked group by group of PLAN_GROUP_PAIRS pairs, tile index
-  // descending inside a group.  All pairs at once is the better order for balance (2-4 % at
-  // configuration 2), but their K and V rows together are several times an XCD's L2; once the tensors
-  // of a call no longer fit the last-level cache either, the re-fetches cost more than the balance
-  // (four times configuration 2: 348 -> 317 us).  The caller decides by the size of the tensors.
-  const bool grouped = (mode & PLAN_GROUP) != 0;
-  if (grouped) {
-    const int ngroups = (per_list + PLAN_GROUP_PAIRS - 1) / PLAN_GROUP_PAIRS;
-    for (int i = tid; i < NUM_XCD; i += PLAN_THREADS) {
-      int run = 0;
-      for (int g = 0; g <= ngroups; ++g) {
-        gbase[i][g] = run;
-        for (int k = g * PLAN_GROUP_PAIRS; k < (g + 1) * PLAN_GROUP_PAIRS && k < per_list; ++k) run += xnt[i][k];
-      }
-    }
-  } else {
-    for (int i = tid; i < NUM_XCD * ttab; i += PLAN_THREADS) {
-      const int x = i / ttab, t = i - x * ttab;
-      above[x][t] = tiles_above(x, t);
-    }
-  }
-  __syncthreads();
   // one thread per (rank, tile, head)
   const int per_rank = tmax * H;
   for (int i = tid; i < B * per_rank; i += PLAN_THREADS) {
@@ -222,9 +216,7 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
     p.ws_items[(size_t)x * p.items_cap + pos] = w;
   }
   if (tid < NUM_XCD) {
-    int total = 0;
-    for (int k = 0; k < per_list; ++k) total += xnt[tid][k];
-    p.ws_counts[tid] = total;
+    p.ws_counts[tid] = list_total[tid];
     p.ws_counts[NUM_XCD + tid] = p.grid_slots;
   }
 }
