@@ -22,6 +22,7 @@ namespace recir_hstu {
 #define HSTU_PLAN_THREADS 1024
 #endif
 constexpr int PLAN_THREADS = HSTU_PLAN_THREADS;
+static_assert(PLAN_THREADS >= NUM_XCD * 64 && PLAN_THREADS % 64 == 0, "one wave per XCD list sums that list");
 constexpr int PLAN_MAX_B = 1024;      // fast path: sequences ...
 constexpr int PLAN_MAX_PAIRS = 4096;  // ... (sequence, head) pairs ...
 constexpr int PLAN_MAX_TILES = 256;   // ... and query tiles per sequence that fit the LDS tables
