@@ -52,6 +52,15 @@ extern "C" {
                                                      chooses this by itself when the tensors of a call
                                                      exceed the last-level cache; the flag forces it
                                                      (tests, tuning).  No effect on results.          */
+#define RECIR_HSTU_FLAG_MASK_NONCAUSAL 0x20000u   /* the mask the reference builds for any
+                                                     invalid_attn_mask_type other than
+                                                     "lower_triangular" (kjt_split_per_feature.cpp:
+                                                     650-660): absolute distance of the target-clamped
+                                                     ids within max_attn_len, either way round (the
+                                                     diagonal alone when max_attn_len is 0), the rows
+                                                     of full_attn_size and the contextual keys as in
+                                                     the causal case.  Generic kernels only (any head
+                                                     dim, bf16 or fp32; forward and backward).       */
 #define RECIR_HSTU_FLAG_KERNEL_SHIFT 8            /* bits 8..15: kernel selector for tests/tuning  */
 #define RECIR_HSTU_FLAG_KERNEL_MASK 0xff00u       /* 0 auto, 1 generic, 2.. tiled variants         */
 
@@ -72,7 +81,8 @@ extern "C" {
  *   kernel entry pallas_jagged_hstu_attention (recir/ops/pallas/jagged_hstu_attention.py:1518-1591)
  *   / hstu_ragged_attention_fwd_jax_fn (recir/ops/helion/jagged_hstu_attention.py:830-872).
  *   The causal ("lower_triangular") mask with num_softmax_heads = 0 is covered, plain or
- *   semi-local (max_attn_len, full_attn_size); the host wrapper rejects anything else.
+ *   semi-local (max_attn_len, full_attn_size), and the mask of any other invalid_attn_mask_type
+ *   string (RECIR_HSTU_FLAG_MASK_NONCAUSAL, generic kernels); the host wrapper rejects softmax heads.
  *
  * q, k          device, [T, H, Dqk] row-major contiguous, element type `dtype`
  * v, out        device, [T, H, Dv]; out is written in full: rows < seq_offsets[B] get the result,

@@ -14,6 +14,10 @@
  *                               the semi-local mask (max_attn_len, full_attn_size) of
  *                               recir/ops/kjt_split_per_feature.cpp:654-668 and
  *                               recir/ops/helion/jagged_hstu_attention.py:124-147
+ *   hstu_oracle_keep_nc, hstu_oracle_keep_nc_clamp_id
+ *                               the mask of any invalid_attn_mask_type other than "lower_triangular"
+ *                               (recir/ops/kjt_split_per_feature.cpp:650-671: absolute distance of the
+ *                               clamped ids; without max_attn_len only the diagonal is kept)
  *   hstu_oracle_attn_fwd        recir/ops/kjt_split_per_feature.cpp:602-693 (per-sequence loop,
  *                               alpha on the scores, x*sigmoid(x), attn_scale or 1/max_seq_len,
  *                               mask multiply, weights @ v) with the packed [T,H,Dv] output and
@@ -49,6 +53,7 @@
 
 #define HSTU_CTX_PREFIX 0  /* keys j < ctx visible to every query               */
 #define HSTU_CTX_REFCPP 1  /* reference C++: keys whose clamped id is 0 visible  */
+#define HSTU_MASK_NONCAUSAL 2 /* added to the ctx mode: the mask of a mask type other than "lower_triangular" */
 
 /* keep(m, j) in the "causal and key-is-history, or diagonal" form. */
 int hstu_oracle_keep(int64_t m, int64_t j, int64_t n, int64_t t, int64_t ctx, int ctx_mode) {
@@ -84,6 +89,60 @@ int hstu_oracle_keep_clamp_id(int64_t m, int64_t j, int64_t n, int64_t t, int64_
 }
 
 /*
+ * Mask of a mask type other than "lower_triangular", as the reference builds it
+ * (kjt_split_per_feature.cpp:639-674): clamped ids, their absolute distance, a window only when
+ * max_attn_len > 0 (without one nothing but the diagonal is kept), the "global" rows of
+ * full_attn_size unchanged from the causal case, and the contextual switch.
+ */
+int hstu_oracle_keep_nc_clamp_id(int64_t m, int64_t j, int64_t n, int64_t t, int64_t ctx,
+                                 int ctx_mode, int64_t A, int64_t F) {
+  if (m < 0 || j < 0 || m >= n || j >= n) return 0;
+  const int64_t bound = n - t;
+  const int64_t idm = m < bound ? m : bound;
+  const int64_t idj = j < bound ? j : bound;
+  int64_t distance = idm - idj;
+  if (distance < 0) distance = -distance;
+  int keep = (m == j);
+  if (A > 0) {
+    keep = keep || (distance >= -A && distance <= A);
+    if (F > 0) {
+      const int64_t boundary = bound - F;
+      const int64_t gr = idm < boundary ? 0 : idm;
+      const int64_t gc = idj < boundary ? 0 : idj;
+      keep = keep || (gr - gc > 0);
+    }
+  }
+  if (ctx > 0) {
+    if (ctx_mode & HSTU_CTX_REFCPP) keep = keep || (idj == 0);
+    else keep = keep || (j < ctx);
+  }
+  return keep;
+}
+
+/* The same mask said in words: with a window, a pair is kept when the two positions (targets all
+ * standing at the first target's position) are at most A apart, either way round, or when the query
+ * stands in the last F history positions or beyond and the key stands strictly before it; the
+ * diagonal and the contextual keys always. */
+int hstu_oracle_keep_nc(int64_t m, int64_t j, int64_t n, int64_t t, int64_t ctx, int ctx_mode,
+                        int64_t A, int64_t F) {
+  if (m < 0 || j < 0 || m >= n || j >= n) return 0;
+  const int64_t cap = n - t;
+  const int64_t pm = m < cap ? m : cap, pj = j < cap ? j : cap;
+  int keep = (m == j);
+  if (A > 0) {
+    const int near = (pm >= pj ? pm - pj : pj - pm) <= A;
+    /* below the boundary a key counts as position 0: before every tail row but row 0 itself */
+    const int tail = F > 0 && pm >= cap - F && (pj < cap - F ? pm > 0 : pj < pm);
+    keep = keep || near || tail;
+  }
+  if (ctx > 0) {
+    if (ctx_mode & HSTU_CTX_REFCPP) keep = keep || (pj == 0);
+    else keep = keep || (j < ctx);
+  }
+  return keep;
+}
+
+/*
  * Semi-local variant (max_attn_len A > 0): a history key is visible to a query when it lies within
  * the last A positions before the query's target-clamped id, or -- with full_attn_size F > 0 --
  * when the query's clamped id is in the last F history positions or beyond (those rows keep full
@@ -92,6 +151,7 @@ int hstu_oracle_keep_clamp_id(int64_t m, int64_t j, int64_t n, int64_t t, int64_
  */
 int hstu_oracle_keep_sl(int64_t m, int64_t j, int64_t n, int64_t t, int64_t ctx, int ctx_mode,
                         int64_t A, int64_t F) {
+  if (ctx_mode & HSTU_MASK_NONCAUSAL) return hstu_oracle_keep_nc(m, j, n, t, ctx, ctx_mode, A, F);
   if (A <= 0) return hstu_oracle_keep(m, j, n, t, ctx, ctx_mode);
   if (m < 0 || j < 0 || m >= n || j >= n) return 0;
   const int64_t cap = n - t;
@@ -115,6 +175,7 @@ int hstu_oracle_keep_sl(int64_t m, int64_t j, int64_t n, int64_t t, int64_t ctx,
  * clamped ids, distance window, and the "global" rows/columns zeroed below the boundary. */
 int hstu_oracle_keep_sl_clamp_id(int64_t m, int64_t j, int64_t n, int64_t t, int64_t ctx,
                                  int ctx_mode, int64_t A, int64_t F) {
+  if (ctx_mode & HSTU_MASK_NONCAUSAL) return hstu_oracle_keep_nc_clamp_id(m, j, n, t, ctx, ctx_mode, A, F);
   if (m < 0 || j < 0 || m >= n || j >= n) return 0;
   const int64_t bound = n - t;
   const int64_t idm = m < bound ? m : bound;

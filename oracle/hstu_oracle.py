@@ -28,6 +28,11 @@ _REF_SO = os.path.join(_HERE, "_ref", "libkjt_ref.so")
 
 CTX_PREFIX = 0  # keys j < contextual_seq_len are visible to every query
 CTX_REFCPP = 1  # reference C++ rule: keys whose clamped id is 0 are visible
+MASK_NONCAUSAL = 2  # added to a ctx mode: the mask of a mask type other than "lower_triangular"
+
+
+def _mode(ctx_mode, mask_type):
+    return int(ctx_mode) | (0 if mask_type == "lower_triangular" else MASK_NONCAUSAL)
 
 _lib = None
 
@@ -63,7 +68,8 @@ def lib() -> ctypes.CDLL:
         L.hstu_oracle_attn_bwd_sl.restype = c_int
         L.hstu_oracle_attn_bwd_rab.argtypes = [vp] * 11 + [c_int, vp] + [i64] * 7 + [c_int, ctypes.c_double, c_int, i64, i64]
         L.hstu_oracle_attn_bwd_rab.restype = c_int
-        for name in ("hstu_oracle_keep_sl", "hstu_oracle_keep_sl_clamp_id"):
+        for name in ("hstu_oracle_keep_sl", "hstu_oracle_keep_sl_clamp_id", "hstu_oracle_keep_nc",
+                     "hstu_oracle_keep_nc_clamp_id"):
             fn = getattr(L, name)
             fn.argtypes = [i64, i64, i64, i64, i64, c_int, i64, i64]
             fn.restype = c_int
@@ -83,16 +89,30 @@ def keep(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX) -> bool:
     return bool(lib().hstu_oracle_keep(m, j, n, t, ctx, ctx_mode))
 
 
-def keep_sl(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX, max_attn_len=0, full_attn_size=0) -> bool:
-    return bool(lib().hstu_oracle_keep_sl(m, j, n, t, ctx, ctx_mode, max_attn_len, full_attn_size))
+def keep_sl(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX, max_attn_len=0, full_attn_size=0,
+            mask_type="lower_triangular") -> bool:
+    return bool(lib().hstu_oracle_keep_sl(m, j, n, t, ctx, _mode(ctx_mode, mask_type), max_attn_len, full_attn_size))
 
 
-def keep_sl_clamp_id(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX, max_attn_len=0, full_attn_size=0) -> bool:
-    return bool(lib().hstu_oracle_keep_sl_clamp_id(m, j, n, t, ctx, ctx_mode, max_attn_len, full_attn_size))
+def keep_sl_clamp_id(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX, max_attn_len=0, full_attn_size=0,
+                     mask_type="lower_triangular") -> bool:
+    return bool(lib().hstu_oracle_keep_sl_clamp_id(m, j, n, t, ctx, _mode(ctx_mode, mask_type), max_attn_len,
+                                                   full_attn_size))
 
 
-def count_pairs_sl(n, t, ctx=0, ctx_mode=CTX_PREFIX, max_attn_len=0, full_attn_size=0) -> int:
-    return int(lib().hstu_oracle_count_pairs_sl(n, t, ctx, ctx_mode, max_attn_len, full_attn_size))
+def keep_nc(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX, max_attn_len=0, full_attn_size=0) -> bool:
+    """Mask of a mask type other than "lower_triangular", in words."""
+    return bool(lib().hstu_oracle_keep_nc(m, j, n, t, ctx, ctx_mode, max_attn_len, full_attn_size))
+
+
+def keep_nc_clamp_id(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX, max_attn_len=0, full_attn_size=0) -> bool:
+    """The same mask built the way the reference builds it."""
+    return bool(lib().hstu_oracle_keep_nc_clamp_id(m, j, n, t, ctx, ctx_mode, max_attn_len, full_attn_size))
+
+
+def count_pairs_sl(n, t, ctx=0, ctx_mode=CTX_PREFIX, max_attn_len=0, full_attn_size=0,
+                   mask_type="lower_triangular") -> int:
+    return int(lib().hstu_oracle_count_pairs_sl(n, t, ctx, _mode(ctx_mode, mask_type), max_attn_len, full_attn_size))
 
 
 def keep_clamp_id(m, j, n, t, ctx=0, ctx_mode=CTX_PREFIX) -> bool:
@@ -113,10 +133,12 @@ def _ptr(a):
 
 def attn_fwd(q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn_scale=None,
              rab=None, contextual_seq_len=0, ctx_mode=CTX_PREFIX, round_p_bf16=False,
-             max_attn_len=0, full_attn_size=0):
+             max_attn_len=0, full_attn_size=0, mask_type="lower_triangular"):
     """Per-sequence loop oracle.  q,k [T,H,Dqk], v [T,H,Dv] float arrays -> out [T,H,Dv] float32.
 
     ``attn_scale``: None (1/max_seq_len), a python/0-d scalar, or a [T] per-token array.
+    ``mask_type``: "lower_triangular" is the causal mask, any other string the reference's other
+    branch (absolute distances; kjt_split_per_feature.cpp:650-660).
     """
     q, k, v = _f32(q), _f32(k), _f32(v)
     T, H, Dqk = q.shape
@@ -140,7 +162,7 @@ def attn_fwd(q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn
     out = np.empty((T, H, Dv), dtype=np.float32)
     rc = lib().hstu_oracle_attn_fwd_sl(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(off), _ptr(nt),
                                        _ptr(rb), kind, _ptr(sc), T, B, H, Dqk, Dv, int(max_seq_len),
-                                       int(contextual_seq_len), int(ctx_mode), float(alpha),
+                                       int(contextual_seq_len), _mode(ctx_mode, mask_type), float(alpha),
                                        1 if round_p_bf16 else 0, int(max_attn_len), int(full_attn_size))
     if rc != 0:
         raise ValueError("invalid jagged range in seq_offsets")
@@ -149,7 +171,7 @@ def attn_fwd(q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn
 
 def attn_bwd(dout, q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn_scale=None,
              rab=None, contextual_seq_len=0, ctx_mode=CTX_PREFIX, round_bf16=False,
-             max_attn_len=0, full_attn_size=0, rab_grad=False):
+             max_attn_len=0, full_attn_size=0, rab_grad=False, mask_type="lower_triangular"):
     """Gradients (dq, dk, dv) of ``attn_fwd`` for the upstream gradient ``dout`` [T,H,Dv]; float32 arrays.
 
     Same argument conventions as ``attn_fwd``.  ``round_bf16`` rounds P and dS to bf16 before the
@@ -184,7 +206,7 @@ def attn_bwd(dout, q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha
         drab = np.zeros((H, 2 * max_seq_len - 1), dtype=np.float64)
     rc = lib().hstu_oracle_attn_bwd_rab(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv),
                                         _ptr(drab), _ptr(off), _ptr(nt), _ptr(rb), kind, _ptr(sc), T, B, H, Dqk, Dv,
-                                        int(max_seq_len), int(contextual_seq_len), int(ctx_mode),
+                                        int(max_seq_len), int(contextual_seq_len), _mode(ctx_mode, mask_type),
                                         float(alpha), 1 if round_bf16 else 0, int(max_attn_len),
                                         int(full_attn_size))
     if rc != 0:
@@ -323,10 +345,10 @@ def ref_op():
 
 
 def ref_attn_fwd(q, k, v, seq_offsets, num_targets=None, *, max_seq_len, alpha, attn_scale=None,
-                 contextual_seq_len=0, max_attn_len=0, full_attn_size=0):
+                 contextual_seq_len=0, max_attn_len=0, full_attn_size=0, mask_type="lower_triangular"):
     """Run the reference C++ op on torch CPU tensors; returns out [seq_offsets[-1], H, Dv]."""
     op = ref_op()
-    out, _aux = op(int(max_seq_len), float(alpha), q, k, v, seq_offsets, "lower_triangular",
+    out, _aux = op(int(max_seq_len), float(alpha), q, k, v, seq_offsets, str(mask_type),
                    num_targets, attn_scale, int(max_attn_len), int(contextual_seq_len),
                    int(full_attn_size), 0)
     return out

@@ -243,11 +243,12 @@ __global__ __launch_bounds__(64) void hstu_fwd_generic(Params p) {
 #pragma unroll
   for (int i = 0; i < GENERIC_MAX_D / 64; ++i) acc[i] = 0.f;
 
-  const int jend = max(m + 1, si.ctx_eff);
+  const bool noncausal = p.flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL;  // then keys after the query count too
+  const int jend = noncausal ? si.n : max(m + 1, si.ctx_eff);
   for (int j0 = 0; j0 < jend; j0 += 64) {
     const int j = j0 + lane;
     float pj = 0.f;
-    if (j < si.n && keep_pair(m, j, si)) {
+    if (j < si.n && keep_pair(m, j, si, noncausal)) {
       const size_t krow = ((size_t)(si.s + j) * p.H + h) * p.Dqk;
       float dot = 0.f;
       for (int d = 0; d < p.Dqk; ++d) dot = fmaf(qrow[d], load_elem<BF16>(p.k, krow + d), dot);
@@ -427,6 +428,11 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
   if (bias_needs_generic && (fp8 || variant >= 2))
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "a bias with alpha = %g runs on the generic kernel only", (double)alpha);
   if (variant == 1 && !fp8) use_tiled = false;
+  if (flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL) {
+    if (fp8 || variant >= 2)
+      return fail(RECIR_HSTU_ERR_UNSUPPORTED, "a mask type other than the causal one runs on the generic kernel only (bf16 or fp32)");
+    use_tiled = false;
+  }
   if (fp8 && variant == 2) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "fp8 q/k runs on the direct-to-LDS tiled kernel only");
   if (variant >= 2 && !tiled_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "tiled kernel needs bf16, Dqk = Dv = 128 and 16-byte aligned tensors");
@@ -632,7 +638,10 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
                         (((size_t)dout | (size_t)q | (size_t)k | (size_t)v | (size_t)dq | (size_t)dk | (size_t)dv) & 15) == 0;
   if (variant >= 2 && !tiled_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "tiled backward needs bf16, Dqk = Dv = 128 and 16-byte aligned tensors");
-  if (tiled_ok && variant != 1) {
+  const bool noncausal = (flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL) != 0;
+  if (noncausal && variant >= 2)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "a mask type other than the causal one runs on the generic kernels only");
+  if (tiled_ok && variant != 1 && !noncausal) {
     const size_t half_ws = (recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype) + 255) & ~(size_t)255;
     if (!workspace || workspace_bytes < 2 * half_ws || ((size_t)workspace & 15))
       return fail(RECIR_HSTU_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu at %p",

@@ -68,11 +68,12 @@ __global__ __launch_bounds__(64) void hstu_bwd_generic_dq(BwdParams bp) {
   float acc[BWD_GENERIC_MAX_D / 64];
 #pragma unroll
   for (int i = 0; i < BWD_GENERIC_MAX_D / 64; ++i) acc[i] = 0.f;
-  const int jend = max(m + 1, si.ctx_eff);
+  const bool noncausal = p.flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL;  // then keys after the query count too
+  const int jend = noncausal ? si.n : max(m + 1, si.ctx_eff);
   for (int j0 = 0; j0 < jend; j0 += 64) {
     const int j = j0 + lane;
     float ds = 0.f;
-    if (j < si.n && keep_pair(m, j, si)) {
+    if (j < si.n && keep_pair(m, j, si, noncausal)) {
       const size_t krow = ((size_t)(si.s + j) * p.H + h) * p.Dqk;
       const size_t vrow = ((size_t)(si.s + j) * p.H + h) * p.Dv;
       float dot = 0.f, dp = 0.f;
@@ -139,13 +140,15 @@ __global__ __launch_bounds__(64) void hstu_bwd_generic_dkv(BwdParams bp) {
 #pragma unroll
   for (int i = 0; i < BWD_GENERIC_MAX_D / 64; ++i) acck[i] = accv[i] = 0.f;
   // queries that see key j: all of them for a contextual key, m >= j for a history key, m == j else
-  const bool ctx_key = j < si.ctx_eff;
+  // (every query is tried under a mask type other than the causal one)
+  const bool noncausal = p.flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL;
+  const bool ctx_key = j < si.ctx_eff || noncausal;
   const int mbeg = ctx_key ? 0 : j;
   const int mend = (ctx_key || j < si.cap) ? si.n : j + 1;
   for (int m0 = mbeg; m0 < mend; m0 += 64) {
     const int m = m0 + lane;
     float pw = 0.f, ds = 0.f;
-    if (m < mend && keep_pair(m, j, si)) {
+    if (m < mend && keep_pair(m, j, si, noncausal)) {
       const size_t qrow = ((size_t)(si.s + m) * p.H + h) * p.Dqk;
       const size_t grow = ((size_t)(si.s + m) * p.H + h) * p.Dv;
       float dot = 0.f, dp = 0.f;

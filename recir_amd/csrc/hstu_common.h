@@ -117,6 +117,27 @@ __device__ __forceinline__ bool keep_pair(int m, int j, const SeqInfo& si) {
   return (m == j) || (j < idm && (idm - j <= si.win || idm >= si.tail0)) || (j < si.ctx_eff);
 }
 
+// The mask of a mask type other than "lower_triangular" (recir/ops/kjt_split_per_feature.cpp:650-671):
+// the distance of the clamped ids counts either way round and only under a window (without one the
+// diagonal is all there is); the rows of the full-attention tail see the keys whose id is below
+// theirs, ids below the tail's start counting as 0.
+__device__ __forceinline__ bool keep_pair_noncausal(int m, int j, const SeqInfo& si) {
+  const int idm = min(m, si.cap), idj = min(j, si.cap);
+  bool kp = (m == j) || (j < si.ctx_eff);
+  if (si.win != WIN_ALL) {
+    kp = kp || abs(idm - idj) <= si.win;
+    if (si.tail0 != 0x7fffffff) {
+      const int gr = idm < si.tail0 ? 0 : idm, gc = idj < si.tail0 ? 0 : idj;
+      kp = kp || gr - gc > 0;
+    }
+  }
+  return kp;
+}
+
+__device__ __forceinline__ bool keep_pair(int m, int j, const SeqInfo& si, bool noncausal) {
+  return noncausal ? keep_pair_noncausal(m, j, si) : keep_pair(m, j, si);
+}
+
 __device__ __forceinline__ float bf16_bits_to_float(unsigned short b) {
   return __uint_as_float((unsigned)b << 16);
 }

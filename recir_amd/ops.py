@@ -102,7 +102,8 @@ _QUANT_SCHEMA = "hstu_quantize_e4m3_per_head(Tensor x, Tensor? seq_offsets=None)
 _BWD_SCHEMA = (
     "hstu_jagged_attention_bwd(Tensor dout, int N, float alpha, Tensor q, Tensor k, Tensor v, "
     "Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, int contextual_seq_len, "
-    "Tensor? rab=None, int max_attn_len=0, int full_attn_size=0) -> (Tensor, Tensor, Tensor)"
+    "Tensor? rab=None, int max_attn_len=0, int full_attn_size=0, "
+    "str invalid_attn_mask_type=\"lower_triangular\") -> (Tensor, Tensor, Tensor)"
 )
 
 # The reference's own schema (recir/ops/kjt_split_per_feature.cpp:780-783), argument for argument and
@@ -116,14 +117,16 @@ _REF_SCHEMA = (
 _REF_BWD_SCHEMA = (
     "triton_ragged_attention_bwd(Tensor dout, int N, float alpha, Tensor q, Tensor k, Tensor v, "
     "Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, int contextual_seq_len, "
-    "int max_attn_len=0, int full_attn_size=0) -> (Tensor, Tensor, Tensor)"
+    "int max_attn_len=0, int full_attn_size=0, str invalid_attn_mask_type=\"lower_triangular\") "
+    "-> (Tensor, Tensor, Tensor)"
 )
 
 # the backward with the gradient of the bias table as a fourth output
 _BWD_RAB_SCHEMA = (
     "hstu_jagged_attention_bwd_rab(Tensor dout, int N, float alpha, Tensor q, Tensor k, Tensor v, "
     "Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, int contextual_seq_len, "
-    "Tensor rab, int max_attn_len=0, int full_attn_size=0) -> (Tensor, Tensor, Tensor, Tensor)"
+    "Tensor rab, int max_attn_len=0, int full_attn_size=0, "
+    "str invalid_attn_mask_type=\"lower_triangular\") -> (Tensor, Tensor, Tensor, Tensor)"
 )
 
 _LIBRARY = torch.library.Library("recir", "FRAGMENT")
@@ -179,7 +182,8 @@ def _check_same_device(dev, **tensors):
             raise ValueError(f"{name} is on {t.device}, q on {dev}")
 
 
-def _prepare(opname, q, k, v, seq_offsets, num_targets, attn_scale, rab, N, ctx_reference=False):
+def _prepare(opname, q, k, v, seq_offsets, num_targets, attn_scale, rab, N, ctx_reference=False,
+             mask_type="lower_triangular"):
     """Checks and device-side argument tensors shared by the forward and backward launches."""
     dev = q.device
     if dev.type != "cuda":
@@ -194,6 +198,9 @@ def _prepare(opname, q, k, v, seq_offsets, num_targets, attn_scale, rab, N, ctx_
         flags |= _lib.FLAG_CTX_REFERENCE
     flags |= (_forced_kernel & 0xFF) << _lib.FLAG_KERNEL_SHIFT
     flags |= _extra_flags
+    if mask_type != "lower_triangular":
+        # any other string selects the reference's other branch (kjt_split_per_feature.cpp:650-660)
+        flags |= _lib.FLAG_MASK_NONCAUSAL
     sc = None
     if attn_scale is not None:
         sc = attn_scale.to(device=dev, dtype=torch.float32).contiguous()
@@ -298,12 +305,13 @@ def _workspace(kind, seq_offsets, num_targets, layout, ws_bytes, dev, stream):
 
 
 def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale, N, alpha,
-            contextual_seq_len, dtype_code, max_attn_len=0, full_attn_size=0, ctx_reference=False) -> torch.Tensor:
+            contextual_seq_len, dtype_code, max_attn_len=0, full_attn_size=0, ctx_reference=False,
+            mask_type="lower_triangular") -> torch.Tensor:
     _check_window(max_attn_len, full_attn_size)
     L = _lib.load()
     dev = q.device
     B, off, nt, sc, rb, flags = _prepare("hstu_jagged_attention_fwd", q, k, v, seq_offsets, num_targets,
-                                         attn_scale, rab, N, ctx_reference)
+                                         attn_scale, rab, N, ctx_reference, mask_type)
     T, H, Dqk = q.shape
     Dv = v.shape[2]
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
@@ -341,13 +349,14 @@ def _dtype_code(q, k, v):
 
 
 def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
-                rab=None, max_attn_len=0, full_attn_size=0, ctx_reference=False, rab_grad=False):
+                rab=None, max_attn_len=0, full_attn_size=0, ctx_reference=False, rab_grad=False,
+                mask_type="lower_triangular"):
     _check_window(max_attn_len, full_attn_size)
     L = _lib.load()
     dev = q.device
     code = _dtype_code(q, k, v)
     B, off, nt, sc, rb, flags = _prepare("hstu_jagged_attention_bwd", q, k, v, seq_offsets, num_targets,
-                                         attn_scale, rab, N, ctx_reference)
+                                         attn_scale, rab, N, ctx_reference, mask_type)
     if dout.shape != v.shape:
         raise ValueError("dout must have the shape of v, [T, H, Dv]")
     if dout.device != dev:
@@ -382,24 +391,28 @@ def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, c
     return (dq, dk, dv, drab) if rab_grad else (dq, dk, dv)
 
 
-def _bwd_rab_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
-                    rab, max_attn_len=0, full_attn_size=0):
+def _bwd_op_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
+                   rab=None, max_attn_len=0, full_attn_size=0, invalid_attn_mask_type="lower_triangular"):
     return _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
-                       rab, max_attn_len, full_attn_size, False, True)
+                       rab, max_attn_len, full_attn_size, False, False, invalid_attn_mask_type)
+
+
+def _bwd_rab_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
+                    rab, max_attn_len=0, full_attn_size=0, invalid_attn_mask_type="lower_triangular"):
+    return _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
+                       rab, max_attn_len, full_attn_size, False, True, invalid_attn_mask_type)
 
 
 def _fwd_device(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
                 max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads=0, rab=None,
                 ctx_reference=False):
-    # same rejections as the reference fallback (kjt_split_per_feature.cpp:616-622) plus the
-    # non-causal mask types
+    # same rejections as the reference fallback (kjt_split_per_feature.cpp:616-622); like it, any
+    # mask type other than "lower_triangular" selects its other branch (:650-660)
     if num_softmax_heads != 0:
         raise ValueError("softmax attention heads are unsupported")
-    if invalid_attn_mask_type != "lower_triangular":
-        raise ValueError("only the causal mask ('lower_triangular') is supported")
     code = _dtype_code(q, k, v)
     out = _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, None, None, N, alpha,
-                  contextual_seq_len, code, max_attn_len, full_attn_size, ctx_reference)
+                  contextual_seq_len, code, max_attn_len, full_attn_size, ctx_reference, invalid_attn_mask_type)
     return out, torch.zeros((1,), dtype=torch.float32, device=q.device)
 
 
@@ -410,9 +423,9 @@ def _ref_fwd_device(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_
 
 
 def _ref_bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
-                    max_attn_len=0, full_attn_size=0):
+                    max_attn_len=0, full_attn_size=0, invalid_attn_mask_type="lower_triangular"):
     return _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
-                       None, max_attn_len, full_attn_size, True)
+                       None, max_attn_len, full_attn_size, True, False, invalid_attn_mask_type)
 
 
 def _fp8_fwd_device(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, num_targets,
@@ -467,7 +480,7 @@ def _no_cpu(*args, **kwargs):
 _LIBRARY.impl("hstu_jagged_attention_fwd", _fwd_device, "CUDA")
 _LIBRARY.impl("hstu_jagged_attention_fp8_fwd", _fp8_fwd_device, "CUDA")
 _LIBRARY.impl("hstu_quantize_e4m3_per_head", _quant_device, "CUDA")
-_LIBRARY.impl("hstu_jagged_attention_bwd", _bwd_device, "CUDA")
+_LIBRARY.impl("hstu_jagged_attention_bwd", _bwd_op_device, "CUDA")
 _LIBRARY.impl("hstu_jagged_attention_bwd_rab", _bwd_rab_device, "CUDA")
 _LIBRARY.impl("hstu_jagged_attention_bwd_rab", _no_cpu, "CPU")
 _LIBRARY.impl("triton_ragged_attention_fwd", _ref_fwd_device, "CUDA")
@@ -497,7 +510,7 @@ def _ref_fwd_fake(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_ta
 
 @torch.library.register_fake("recir::triton_ragged_attention_bwd")
 def _ref_bwd_fake(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
-                  max_attn_len=0, full_attn_size=0):
+                  max_attn_len=0, full_attn_size=0, invalid_attn_mask_type="lower_triangular"):
     _check_common(q, k, v, seq_offsets, num_targets, N)
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
@@ -516,38 +529,38 @@ def _quant_fake(x, seq_offsets=None):
 
 @torch.library.register_fake("recir::hstu_jagged_attention_bwd")
 def _bwd_fake(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab=None,
-              max_attn_len=0, full_attn_size=0):
+              max_attn_len=0, full_attn_size=0, invalid_attn_mask_type="lower_triangular"):
     _check_common(q, k, v, seq_offsets, num_targets, N)
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 @torch.library.register_fake("recir::hstu_jagged_attention_bwd_rab")
 def _bwd_rab_fake(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab,
-                  max_attn_len=0, full_attn_size=0):
+                  max_attn_len=0, full_attn_size=0, invalid_attn_mask_type="lower_triangular"):
     _check_common(q, k, v, seq_offsets, num_targets, N)
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), rab.new_empty(rab.shape, dtype=torch.float32)
 
 
 def _setup_context(ctx, inputs, output):
-    (N, alpha, q, k, v, seq_offsets, _mask_type, num_targets, attn_scale, max_attn_len,
+    (N, alpha, q, k, v, seq_offsets, mask_type, num_targets, attn_scale, max_attn_len,
      contextual_seq_len, full_attn_size, _num_softmax_heads, rab) = inputs
     ctx.save_for_backward(q, k, v, seq_offsets, num_targets, attn_scale, rab)
-    ctx.hstu_args = (int(N), float(alpha), int(contextual_seq_len), int(max_attn_len), int(full_attn_size))
+    ctx.hstu_args = (int(N), float(alpha), int(contextual_seq_len), int(max_attn_len), int(full_attn_size), str(mask_type))
 
 
 def _autograd_backward(ctx, grad_out, _grad_aux):
     q, k, v, seq_offsets, num_targets, attn_scale, rab = ctx.saved_tensors
-    N, alpha, contextual_seq_len, max_attn_len, full_attn_size = ctx.hstu_args
+    N, alpha, contextual_seq_len, max_attn_len, full_attn_size, mask_type = ctx.hstu_args
     drab = None
     if rab is not None and ctx.needs_input_grad[13]:  # a learned bias table: its gradient as well
         dq, dk, dv, drab = torch.ops.recir.hstu_jagged_attention_bwd_rab(
             grad_out, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab,
-            max_attn_len, full_attn_size)
+            max_attn_len, full_attn_size, mask_type)
         drab = drab.to(rab.dtype)
     else:
         dq, dk, dv = torch.ops.recir.hstu_jagged_attention_bwd(
             grad_out, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len, rab,
-            max_attn_len, full_attn_size)
+            max_attn_len, full_attn_size, mask_type)
     # one gradient slot per forward argument; attn_scale receives none
     return (None, None, dq, dk, dv, None, None, None, None, None, None, None, None, drab)
 
@@ -560,18 +573,18 @@ torch.library.register_autograd("recir::hstu_jagged_attention_fwd", _autograd_ba
 
 
 def _ref_setup_context(ctx, inputs, output):
-    (N, alpha, q, k, v, seq_offsets, _mask_type, num_targets, attn_scale, max_attn_len,
+    (N, alpha, q, k, v, seq_offsets, mask_type, num_targets, attn_scale, max_attn_len,
      contextual_seq_len, full_attn_size, _num_softmax_heads) = inputs
     ctx.save_for_backward(q, k, v, seq_offsets, num_targets, attn_scale)
-    ctx.hstu_args = (int(N), float(alpha), int(contextual_seq_len), int(max_attn_len), int(full_attn_size))
+    ctx.hstu_args = (int(N), float(alpha), int(contextual_seq_len), int(max_attn_len), int(full_attn_size), str(mask_type))
 
 
 def _ref_autograd_backward(ctx, grad_out, _grad_aux):
     q, k, v, seq_offsets, num_targets, attn_scale = ctx.saved_tensors
-    N, alpha, contextual_seq_len, max_attn_len, full_attn_size = ctx.hstu_args
+    N, alpha, contextual_seq_len, max_attn_len, full_attn_size, mask_type = ctx.hstu_args
     dq, dk, dv = torch.ops.recir.triton_ragged_attention_bwd(
         grad_out, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, contextual_seq_len,
-        max_attn_len, full_attn_size)
+        max_attn_len, full_attn_size, mask_type)
     return (None, None, dq, dk, dv, None, None, None, None, None, None, None, None)
 
 
@@ -586,7 +599,7 @@ triton_ragged_attention_fwd = torch.ops.recir.triton_ragged_attention_fwd
 def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len: int,
                           alpha: Optional[float] = None, attn_scale=None,
                           contextual_seq_len: int = 0, rab=None, max_attn_len: int = 0,
-                          full_attn_size: int = 0) -> torch.Tensor:
+                          full_attn_size: int = 0, invalid_attn_mask_type: str = "lower_triangular") -> torch.Tensor:
     """Packed HSTU attention with the defaults of the accelerator entry point it replaces
     (recir/ops/pallas/jagged_hstu_attention.py:1550-1555, recir/ops/helion/jagged_hstu_attention.py:
     798-804): ``num_targets=None`` means no targets, ``alpha=None`` means ``1/sqrt(Dqk)``,
@@ -596,6 +609,10 @@ def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len
     (recir/ops/kjt_split_per_feature.cpp:654-668; the reference's accelerator kernels fix it to 256 /
     256, recir/ops/helion/jagged_hstu_attention.py:95-147): history keys within ``max_attn_len``
     positions, and full causal attention for the rows from ``full_attn_size`` before the targets on.
+    ``invalid_attn_mask_type`` other than ``"lower_triangular"`` selects, as in the reference operator
+    (recir/ops/kjt_split_per_feature.cpp:650-660), the mask on absolute distances: positions at most
+    ``max_attn_len`` apart either way round, only the diagonal without a window.  That mask runs on
+    the generic kernels (any head dim, no MFMA).
     """
     _check_common(q, k, v, seq_offsets, num_targets, max_seq_len)
     if alpha is None:
@@ -603,7 +620,7 @@ def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len
     if attn_scale is not None and not isinstance(attn_scale, torch.Tensor):
         attn_scale = torch.tensor(float(attn_scale), dtype=torch.float32, device=q.device)
     out, _ = hstu_jagged_attention_fwd(int(max_seq_len), float(alpha), q, k, v, seq_offsets,
-                                       "lower_triangular", num_targets, attn_scale, int(max_attn_len),
+                                       str(invalid_attn_mask_type), num_targets, attn_scale, int(max_attn_len),
                                        int(contextual_seq_len), int(full_attn_size), 0, rab)
     return out
 
@@ -611,7 +628,8 @@ def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len
 def jagged_hstu_attention_backward(dout, q, k, v, seq_offsets, num_targets=None, attn_scale=None, *,
                                    max_seq_len: int, alpha: Optional[float] = None,
                                    contextual_seq_len: int = 0, rab=None, max_attn_len: int = 0,
-                                   full_attn_size: int = 0, rab_grad: bool = False):
+                                   full_attn_size: int = 0, rab_grad: bool = False,
+                                   invalid_attn_mask_type: str = "lower_triangular"):
     """``(dq, dk, dv)`` of ``jagged_hstu_attention`` for the upstream gradient ``dout [T, H, Dv]``;
     argument order and defaults of ``pallas_jagged_hstu_attention_backward``
     (recir/ops/pallas/jagged_hstu_attention.py:1343-1358; called that way by its own test,
@@ -627,10 +645,11 @@ def jagged_hstu_attention_backward(dout, q, k, v, seq_offsets, num_targets=None,
     if rab_grad:
         return torch.ops.recir.hstu_jagged_attention_bwd_rab(dout, int(max_seq_len), float(alpha), q, k, v, seq_offsets,
                                                              num_targets, attn_scale, int(contextual_seq_len), rab,
-                                                             int(max_attn_len), int(full_attn_size))
+                                                             int(max_attn_len), int(full_attn_size),
+                                                             str(invalid_attn_mask_type))
     return hstu_jagged_attention_bwd(dout, int(max_seq_len), float(alpha), q, k, v, seq_offsets,
                                      num_targets, attn_scale, int(contextual_seq_len), rab,
-                                     int(max_attn_len), int(full_attn_size))
+                                     int(max_attn_len), int(full_attn_size), str(invalid_attn_mask_type))
 
 
 def quantize_e4m3_per_head(x: torch.Tensor, seq_offsets: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -686,7 +705,7 @@ def attention_via_fp8(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, nu
     if num_softmax_heads != 0:
         raise ValueError("softmax attention heads are unsupported")
     if invalid_attn_mask_type != "lower_triangular":
-        raise ValueError("only the causal mask ('lower_triangular') is supported")
+        raise ValueError("the fp8 kernel covers the causal mask ('lower_triangular') only")
     q8, qs = quantize_e4m3_per_head(q, seq_offsets)
     k8, ks = quantize_e4m3_per_head(k, seq_offsets)
     return torch.ops.recir.hstu_jagged_attention_fp8_fwd(

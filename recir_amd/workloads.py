@@ -31,6 +31,7 @@ class Workload:
     lengths: np.ndarray = field(default=None)  # [B] full sequence lengths (history + targets)
     max_attn_len: int = 0    # > 0: semi-local window over the history
     full_attn_size: int = 0  # > 0 (with max_attn_len > 0): the last rows keep full causal attention
+    mask_type: str = "lower_triangular"  # any other string: the reference's mask on absolute distances
 
     @property
     def T(self) -> int:
@@ -113,7 +114,7 @@ _SPEC = {
 
 def make_jagged(lengths, num_targets, H, Dqk, Dv, *, max_seq_len, alpha, dtype="fp32", seed=0,
                 contextual_seq_len=0, with_rab=False, rab_std=0.02, tail_rows=0, name="custom",
-                max_attn_len=0, full_attn_size=0):
+                max_attn_len=0, full_attn_size=0, mask_type="lower_triangular"):
     """Build a workload from explicit full lengths (history + targets) and target counts."""
     lengths = np.asarray(lengths, dtype=np.int64)
     T = int(lengths.sum()) + int(tail_rows)
@@ -133,7 +134,7 @@ def make_jagged(lengths, num_targets, H, Dqk, Dv, *, max_seq_len, alpha, dtype="
                     num_targets=torch.as_tensor(np.asarray(num_targets, dtype=np.int64)),
                     max_seq_len=int(max_seq_len), alpha=float(alpha), dtype=dtype,
                     contextual_seq_len=int(contextual_seq_len), rab=rab, lengths=lengths,
-                    max_attn_len=int(max_attn_len), full_attn_size=int(full_attn_size))
+                    max_attn_len=int(max_attn_len), full_attn_size=int(full_attn_size), mask_type=str(mask_type))
 
 
 def make_config(config: int, seed: int = 0) -> Workload:

@@ -14,13 +14,13 @@ SMALL_CASES = {}
 
 def _add(name, lengths, targets, N, *, H=2, Dqk=8, Dv=6, alpha=None, attn_scale=0.17, ctx=0,
          per_token_scale=False, seed=0, tail_rows=0, no_targets=False, bf16_inputs=False,
-         max_attn_len=0, full_attn_size=0):
+         max_attn_len=0, full_attn_size=0, mask_type="lower_triangular"):
     SMALL_CASES[name] = dict(lengths=list(lengths), targets=list(targets), N=N, H=H, Dqk=Dqk, Dv=Dv,
                              alpha=(1.0 / math.sqrt(Dqk)) if alpha is None else alpha,
                              attn_scale=attn_scale, ctx=ctx, per_token_scale=per_token_scale,
                              seed=seed, tail_rows=tail_rows, no_targets=no_targets,
                              bf16_inputs=bf16_inputs, max_attn_len=max_attn_len,
-                             full_attn_size=full_attn_size)
+                             full_attn_size=full_attn_size, mask_type=mask_type)
 
 
 _add("ref_nonuniform_causal", [7, 3, 9], [0, 0, 0], 9)
@@ -56,6 +56,25 @@ _add("d128_semilocal", [300, 130, 64, 257, 1], [10, 0, 64, 30, 0], 320, H=2, Dqk
      attn_scale=None, tail_rows=2, bf16_inputs=True, max_attn_len=70, full_attn_size=40, seed=45)
 _add("d128_semilocal_window_only", [260, 200], [0, 33], 300, H=1, Dqk=128, Dv=128, alpha=1.0 / 128,
      attn_scale=0.02, bf16_inputs=True, max_attn_len=64, seed=46)
+# A mask type other than "lower_triangular" (kjt_split_per_feature.cpp:650-660: absolute distances):
+# the diagonal alone without a window, a window either way round, window plus tail, targets beyond
+# the length, the contextual switch, and head dim 128 in bf16.  Their expected outputs are kept in
+# files of their own (fixture_file).
+_add("nc_diagonal_only", [7, 3, 9], [2, 0, 1], 9, mask_type="full", seed=60)
+_add("nc_window", [12, 3, 9, 20], [2, 0, 1, 5], 20, max_attn_len=3, mask_type="full", seed=61)
+_add("nc_window_and_tail", [12, 3, 9, 20], [2, 0, 1, 5], 20, max_attn_len=3, full_attn_size=4, mask_type="full", seed=62)
+_add("nc_tail_exceeds_history", [7, 3, 9], [2, 3, 0], 9, max_attn_len=2, full_attn_size=50, mask_type="full", seed=63)
+_add("nc_targets_exceed_length", [5, 3, 6], [7, 3, 0], 8, max_attn_len=1, full_attn_size=2, mask_type="full", seed=64)
+_add("nc_ctx_refrule", [10, 6, 1], [3, 6, 0], 10, max_attn_len=2, full_attn_size=2, ctx=1, mask_type="full", seed=65)
+_add("nc_ctx_without_window", [10, 6, 1], [3, 6, 0], 10, ctx=1, per_token_scale=True, mask_type="upper_triangular", seed=66)
+_add("nc_d128", [150, 70, 33, 1, 0], [20, 70, 0, 0, 0], 256, H=2, Dqk=128, Dv=128, alpha=1.0 / 128, attn_scale=0.01,
+     bf16_inputs=True, max_attn_len=40, full_attn_size=16, tail_rows=2, mask_type="full", seed=67)
+
+
+def fixture_file(case, backward=False):
+    """Name of the .npz that holds the expected output (or gradients) of a case."""
+    stem = "small_cases" if case["mask_type"] == "lower_triangular" else "noncausal_cases"
+    return stem + ("_bwd.npz" if backward else ".npz")
 
 
 def build_inputs(case):
@@ -68,7 +87,8 @@ def build_inputs(case):
                      max_seq_len=case["N"], alpha=case["alpha"],
                      dtype="bf16" if case["bf16_inputs"] else "fp32", seed=case["seed"],
                      contextual_seq_len=case["ctx"], tail_rows=case["tail_rows"],
-                     max_attn_len=case["max_attn_len"], full_attn_size=case["full_attn_size"])
+                     max_attn_len=case["max_attn_len"], full_attn_size=case["full_attn_size"],
+                     mask_type=case["mask_type"])
     if case["per_token_scale"]:
         g = torch.Generator().manual_seed(1000 + case["seed"])
         scale = torch.rand(wl.T, generator=g) * 0.5 + 0.05

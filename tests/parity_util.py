@@ -36,7 +36,8 @@ def run_hip(wl, *, attn_scale=None, num_targets="default", rab="default", ctx="d
     fn = recir_amd.jagged_hstu_attention_fp8 if fp8 else recir_amd.jagged_hstu_attention
     out = fn(q, k, v, off, nt, max_seq_len=wl.max_seq_len, alpha=wl.alpha, attn_scale=sc,
              contextual_seq_len=wl.contextual_seq_len if ctx == "default" else ctx, rab=rb,
-             max_attn_len=wl.max_attn_len, full_attn_size=wl.full_attn_size)
+             max_attn_len=wl.max_attn_len, full_attn_size=wl.full_attn_size,
+             **({} if fp8 else {"invalid_attn_mask_type": wl.mask_type}))
     torch.cuda.synchronize()
     return out
 
@@ -55,7 +56,7 @@ def run_oracle(oracle, wl, *, attn_scale=None, num_targets="default", rab="defau
                            alpha=wl.alpha, attn_scale=sc, rab=None if rb is None else rb.numpy(),
                            contextual_seq_len=wl.contextual_seq_len if ctx == "default" else ctx,
                            ctx_mode=ctx_mode, max_attn_len=wl.max_attn_len,
-                           full_attn_size=wl.full_attn_size, **kw)
+                           full_attn_size=wl.full_attn_size, mask_type=wl.mask_type, **kw)
 
 
 def error_stats(out, ref):

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from tests.golden.cases import SMALL_CASES, build_inputs, upstream_gradient
+from tests.golden.cases import SMALL_CASES, build_inputs, fixture_file, upstream_gradient
 from tests.parity_util import BF16_REL, error_stats, report, to_device
 
 pytestmark = pytest.mark.gpu
@@ -46,7 +46,7 @@ def run_hip_bwd(wl, dout, *, attn_scale=None, num_targets="default", rab=None, c
         dout.to(q.device, q.dtype), q, k, v, off, nt, sc, max_seq_len=wl.max_seq_len, alpha=wl.alpha,
         contextual_seq_len=wl.contextual_seq_len if ctx is None else ctx,
         rab=None if rab is None else rab.cuda(), max_attn_len=wl.max_attn_len,
-        full_attn_size=wl.full_attn_size)
+        full_attn_size=wl.full_attn_size, invalid_attn_mask_type=wl.mask_type)
     torch.cuda.synchronize()
     return grads
 
@@ -73,14 +73,15 @@ def test_small_cases_match_backward_oracle_and_golden(oracle, name):
                            None if nt is None else nt.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
                            attn_scale=_scale_np(scale), contextual_seq_len=case["ctx"],
                            ctx_mode=oracle.CTX_REFCPP, max_attn_len=case["max_attn_len"],
-                           full_attn_size=case["full_attn_size"])
+                           full_attn_size=case["full_attn_size"], mask_type=case["mask_type"])
     end = int(wl.seq_offsets[-1])
+    causal = case["mask_type"] == "lower_triangular"  # the other mask types run on the generic kernels
     with ops.reference_contextual_rule():
         got = run_hip_bwd(wl, dout, attn_scale=scale, num_targets=ntd, dtype="fp32")
     assert all(g.dtype == torch.float32 for g in got)
     assert_grads_close(got, want, end, BWD_FP32_TOL, name)
     if case["Dqk"] < 128:  # golden gradients: autograd through the reference's C++ forward
-        fx = np.load(os.path.join(GOLDEN, "small_cases_bwd.npz"))
+        fx = np.load(os.path.join(GOLDEN, fixture_file(case, backward=True)))
         assert_grads_close(got, [fx[f"{name}/{k}"] for k in ("dq", "dk", "dv")], end, BWD_FP32_TOL, name + " golden")
     if case["bf16_inputs"]:
         with ops.reference_contextual_rule():
@@ -88,7 +89,7 @@ def test_small_cases_match_backward_oracle_and_golden(oracle, name):
         assert all(g.dtype == torch.bfloat16 for g in gotb)
         assert_grads_close(gotb, want, end, BF16_REL, name + " bf16")
         from recir_amd import _lib
-        assert _lib.last_kernel() == "bwd_tiled_d128_bf16"
+        assert _lib.last_kernel() == ("bwd_tiled_d128_bf16" if causal else "bwd_generic_bf16")
         with ops.reference_contextual_rule(), ops.force_kernel(ops.KERNEL_GENERIC):
             gotg = run_hip_bwd(wl, dout, attn_scale=scale, num_targets=ntd, dtype="bf16")
         assert _lib.last_kernel() == "bwd_generic_bf16"
@@ -527,3 +528,41 @@ def test_backward_with_reused_work_lists_repeats_itself(oracle):
     for later in runs[1:]:
         for a, b in zip(runs[0], later):
             assert torch.equal(a, b)
+
+
+def test_noncausal_mask_through_autograd_and_with_a_bias(oracle):
+    """A mask type other than "lower_triangular": the operator's autograd formula hands the type on to
+    the backward operator, and the gradient of a bias table follows the same mask."""
+    import recir_amd
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([90, 33, 1, 0, 140], [10, 33, 0, 0, 150], 2, 128, 128, max_seq_len=160, alpha=1 / 128,
+                     dtype="bf16", seed=71, with_rab=True, rab_std=0.5, contextual_seq_len=2, tail_rows=2,
+                     max_attn_len=12, full_attn_size=5, mask_type="full")
+    dout = torch.randn(wl.T, wl.H, 128, generator=torch.Generator().manual_seed(9)).bfloat16().float()
+    q, k, v, off, nt = to_device(wl)
+    q.requires_grad_(True); k.requires_grad_(True); v.requires_grad_(True)
+    rab = wl.rab.cuda().requires_grad_(True)
+    out = recir_amd.jagged_hstu_attention(q, k, v, off, nt, max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                                          contextual_seq_len=2, rab=rab, max_attn_len=12, full_attn_size=5,
+                                          invalid_attn_mask_type="full")
+    assert _lib.last_kernel() == "generic_bf16"
+    out.backward(dout.to(out.device, out.dtype))
+    torch.cuda.synchronize()  # (the backward ran on autograd's thread: the kernel name kept per thread is not this thread's)
+    kw = dict(max_seq_len=wl.max_seq_len, alpha=wl.alpha, rab=wl.rab.numpy(), contextual_seq_len=2, max_attn_len=12,
+              full_attn_size=5, mask_type="full")
+    ref = oracle.attn_fwd(wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(), wl.num_targets.numpy(), **kw)
+    from tests.parity_util import assert_bf16_close
+    assert_bf16_close(out.detach(), ref, "non-causal forward")
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), rab_grad=True, **kw)
+    assert_grads_close((q.grad, k.grad, v.grad), want[:3], int(wl.seq_offsets[-1]), BF16_REL, "non-causal autograd")
+    st = error_stats(rab.grad, want[3])
+    print(f"[parity] d rab non-causal: {st}", flush=True)
+    assert st["ref_max"] > 0 and st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL, st
+    # the causal call on the same tensors differs: the type is not ignored
+    out_c = recir_amd.jagged_hstu_attention(q.detach(), k.detach(), v.detach(), off, nt, max_seq_len=wl.max_seq_len,
+                                            alpha=wl.alpha, contextual_seq_len=2, rab=wl.rab.cuda(), max_attn_len=12,
+                                            full_attn_size=5)
+    assert not torch.equal(out_c, out.detach())

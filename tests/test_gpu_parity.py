@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from tests.golden.cases import SMALL_CASES, build_inputs
+from tests.golden.cases import SMALL_CASES, build_inputs, fixture_file
 from tests.parity_util import (BF16_REL, FP8_MAX_ABS, FP32_ATOL, FP32_RTOL, assert_bf16_close, assert_same_zero_structure,
                                error_stats, run_hip, run_oracle, to_device)
 
@@ -38,7 +38,7 @@ def test_small_cases_match_reference_golden(oracle, name):
     from recir_amd import ops
 
     case = SMALL_CASES[name]
-    golden = np.load(os.path.join(GOLDEN, "small_cases.npz"))[name]
+    golden = np.load(os.path.join(GOLDEN, fixture_file(case)))[name]
     wl, scale, nt = build_inputs(case)
     ntd = None if nt is None else nt.cuda()
     # goldens with ctx > 0 pin the reference's contextual rule
@@ -55,7 +55,8 @@ def test_small_cases_match_reference_golden(oracle, name):
         assert_bf16_close(outb[:end], golden, name)
         assert not outb[end:].float().cpu().numpy().any()
         from recir_amd import _lib
-        assert _lib.last_kernel().startswith("tiled_d128")
+        # a mask type other than the causal one runs on the generic kernel
+        assert _lib.last_kernel().startswith("tiled_d128" if case["mask_type"] == "lower_triangular" else "generic")
 
 
 def test_config1_smoke_shape_fp32(oracle):
@@ -661,3 +662,52 @@ def test_grouped_work_lists_give_the_same_output(oracle):
         assert torch.equal(out, out_g)
         for a, b in zip(grads, grads_g):
             assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("A,F,ctx", [(0, 0, 0), (0, 0, 5), (7, 0, 0), (40, 16, 0), (3, 300, 2)])
+def test_noncausal_mask_is_bit_exact(oracle, A, F, ctx):
+    """The mask of a mask type other than "lower_triangular" (kjt_split_per_feature.cpp:650-671), read
+    off the zero pattern of the output as in test_mask_is_bit_exact.  Generic kernel."""
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    lengths = [130, 64, 65, 1, 0, 97]
+    targets = [30, 64, 1, 0, 0, 120]
+    wl = make_jagged(lengths, targets, 1, 128, 128, max_seq_len=140, alpha=1.0 / 128, dtype="bf16",
+                     contextual_seq_len=ctx, tail_rows=3, max_attn_len=A, full_attn_size=F, mask_type="full")
+    wl.q.fill_(0.5)
+    wl.k.fill_(0.25)
+    wl.v.zero_()
+    off = wl.seq_offsets.numpy()
+    for b, n in enumerate(lengths):
+        for j in range(n):
+            wl.v[off[b] + j, 0, j % 128] = 1.0
+    out = run_hip(wl).float().cpu().numpy()
+    assert _lib.last_kernel() == "generic_bf16"
+    want = np.zeros((wl.T, 128), dtype=bool)
+    for b, (n, t) in enumerate(zip(lengths, targets)):
+        for m in range(n):
+            for j in range(n):
+                if oracle.keep_nc(m, j, n, t, ctx, oracle.CTX_PREFIX, A, F):
+                    want[off[b] + m, j % 128] = True
+    np.testing.assert_array_equal(out[:, 0, :] != 0, want)
+
+
+def test_noncausal_mask_is_rejected_where_it_does_not_run():
+    """fp8 q/k and the tiled kernel selectors cover the causal mask only: an error, never another mask."""
+    import recir_amd
+    from recir_amd import ops
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([70, 30], [5, 0], 2, 128, 128, max_seq_len=80, alpha=1 / 128, dtype="bf16", mask_type="full",
+                     max_attn_len=9)
+    q, k, v, off, nt = to_device(wl)
+    for variant in (ops.KERNEL_TILED, ops.KERNEL_TILED_DIRECT):
+        with ops.force_kernel(variant), pytest.raises(ValueError, match="generic kernel"):
+            run_hip(wl)
+    with pytest.raises(ValueError, match="causal"):
+        ops.attention_via_fp8(80, 1 / 128, q, k, v, off, "full", nt, None, 9, 0, 0)
+    dout = torch.ones_like(v)
+    with ops.force_kernel(ops.KERNEL_TILED_DIRECT), pytest.raises(ValueError, match="generic kernels"):
+        recir_amd.jagged_hstu_attention_backward(dout, q, k, v, off, nt, max_seq_len=80, alpha=1 / 128,
+                                                 max_attn_len=9, invalid_attn_mask_type="full")

@@ -180,3 +180,41 @@ def test_workload_pair_count_matches_brute_force_with_windows(oracle):
                          max_attn_len=A, full_attn_size=F)
         want = sum(oracle.count_pairs_sl(int(n), int(t), c, 0, A, F) for n, t in zip(lengths, targets))
         assert wl.pairs() == want
+
+
+def test_two_forms_of_the_noncausal_mask_agree_exhaustively(oracle):
+    """Mask of a mask type other than "lower_triangular" (kjt_split_per_feature.cpp:650-671): the form
+    that follows the reference line by line against the one said in words."""
+    L = oracle.lib()
+    for n in range(0, 21):
+        for t in list(range(0, n + 1)) + [n + 1, n + 5]:
+            for ctx, mode in ((0, 0), (3, 0), (1, 1)):
+                for A, F in ((0, 0), (0, 3), (1, 0), (3, 0), (3, 2), (2, 50), (50, 1)):
+                    for m in range(n):
+                        for j in range(n):
+                            a = L.hstu_oracle_keep_nc(m, j, n, t, ctx, mode, A, F)
+                            b = L.hstu_oracle_keep_nc_clamp_id(m, j, n, t, ctx, mode, A, F)
+                            assert a == b, (n, t, ctx, mode, A, F, m, j)
+
+
+def test_noncausal_mask_properties(oracle):
+    """What the reference's other branch comes to: without a window only the diagonal (and the
+    contextual keys); with a window and no tail it is symmetric, every pair of targets is kept (they
+    all stand at one position), and it contains the semi-local causal mask of the same window."""
+    n, t = 14, 4
+    for m in range(n):
+        for j in range(n):
+            assert oracle.keep_nc(m, j, n, t) == (m == j)
+            assert oracle.keep_nc(m, j, n, t, 3, oracle.CTX_PREFIX) == (m == j or j < 3)
+            for A in (1, 3, 20):
+                k = oracle.keep_nc(m, j, n, t, 0, 0, A, 0)
+                assert k == oracle.keep_nc(j, m, n, t, 0, 0, A, 0)
+                assert k == (abs(min(m, n - t) - min(j, n - t)) <= A or m == j)
+                if m >= n - t and j >= n - t:
+                    assert k
+                for F in (0, 2):
+                    if oracle.keep_sl(m, j, n, t, 0, 0, A, F):
+                        assert oracle.keep_nc(m, j, n, t, 0, 0, A, F)
+    # the dispatch by mask type reaches the same functions
+    assert oracle.keep_sl(2, 5, 9, 0, 0, 0, 3, 0, mask_type="full") and not oracle.keep_sl(2, 5, 9, 0, 0, 0, 3, 0)
+    assert oracle.count_pairs_sl(9, 0, mask_type="full") == 9

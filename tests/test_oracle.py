@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from tests.golden.cases import SMALL_CASES, build_inputs
+from tests.golden.cases import SMALL_CASES, build_inputs, fixture_file
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
@@ -27,13 +27,13 @@ def _run_case(oracle, case, ctx_mode=None, **kw):
                           None if nt is None else nt.numpy(), max_seq_len=wl.max_seq_len,
                           alpha=wl.alpha, attn_scale=sc, contextual_seq_len=case["ctx"],
                           ctx_mode=mode, max_attn_len=case["max_attn_len"],
-                          full_attn_size=case["full_attn_size"], **kw)
+                          full_attn_size=case["full_attn_size"], mask_type=case["mask_type"], **kw)
     return wl, out
 
 
 @pytest.mark.parametrize("name", sorted(SMALL_CASES))
 def test_oracle_matches_reference_golden(oracle, name):
-    golden = np.load(os.path.join(GOLDEN, "small_cases.npz"))[name]
+    golden = np.load(os.path.join(GOLDEN, fixture_file(SMALL_CASES[name])))[name]
     wl, out = _run_case(oracle, SMALL_CASES[name])
     end = int(wl.seq_offsets[-1])
     assert golden.shape == (end, wl.H, wl.v.shape[2])  # the C++ op returns seq_offsets[B] rows

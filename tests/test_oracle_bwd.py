@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from tests.golden.cases import SMALL_CASES, build_inputs, upstream_gradient
+from tests.golden.cases import SMALL_CASES, build_inputs, fixture_file, upstream_gradient
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
@@ -32,13 +32,14 @@ def _oracle_bwd(oracle, case, ctx_mode=None, **kw):
     grads = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
                             None if nt is None else nt.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
                             attn_scale=_scale_arg(scale), contextual_seq_len=case["ctx"], ctx_mode=mode,
-                            max_attn_len=case["max_attn_len"], full_attn_size=case["full_attn_size"], **kw)
+                            max_attn_len=case["max_attn_len"], full_attn_size=case["full_attn_size"],
+                            mask_type=case["mask_type"], **kw)
     return wl, dout, grads
 
 
 @pytest.mark.parametrize("name", sorted(n for n, c in SMALL_CASES.items() if c["Dqk"] < 128))
 def test_backward_oracle_matches_reference_autograd_golden(oracle, name):
-    fx = np.load(os.path.join(GOLDEN, "small_cases_bwd.npz"))
+    fx = np.load(os.path.join(GOLDEN, fixture_file(SMALL_CASES[name], backward=True)))
     wl, _dout, grads = _oracle_bwd(oracle, SMALL_CASES[name])
     end = int(wl.seq_offsets[-1])
     for g, key in zip(grads, ("dq", "dk", "dv")):
@@ -49,7 +50,7 @@ def test_backward_oracle_matches_reference_autograd_golden(oracle, name):
 
 
 @pytest.mark.parametrize("name", ["per_token_scale", "d128_mixed", "d128_ctx_refrule", "d128_semilocal",
-                                  "sl_window_and_tail"])
+                                  "sl_window_and_tail", "nc_d128", "nc_window_and_tail"])
 def test_live_reference_autograd_when_built(oracle, name):
     if not oracle.ref_available():
         pytest.skip("oracle/_ref not built")
@@ -59,7 +60,8 @@ def test_live_reference_autograd_when_built(oracle, name):
     q, k, v = (t.clone().requires_grad_(True) for t in (wl.q, wl.k, wl.v))
     out = oracle.ref_attn_fwd(q, k, v, wl.seq_offsets, nt, max_seq_len=wl.max_seq_len, alpha=wl.alpha,
                               attn_scale=scale, contextual_seq_len=case["ctx"],
-                              max_attn_len=case["max_attn_len"], full_attn_size=case["full_attn_size"])
+                              max_attn_len=case["max_attn_len"], full_attn_size=case["full_attn_size"],
+                              mask_type=case["mask_type"])
     out.backward(dout[: out.shape[0]])
     _, _, grads = _oracle_bwd(oracle, case)
     for g, want in zip(grads, (q.grad, k.grad, v.grad)):
