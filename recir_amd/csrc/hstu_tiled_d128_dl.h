@@ -77,6 +77,9 @@ constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
 #ifndef HSTU_DL_PRIO
 #define HSTU_DL_PRIO 1  // wave priority while an MFMA is waiting to issue (0: leave it alone)
 #endif
+#ifndef HSTU_DL_RANGE_SLOTS
+#define HSTU_DL_RANGE_SLOTS 1  // tiles under the range form of the semi-local mask use the slot schedule
+#endif
 #ifndef HSTU_DL_SLOTS_UNMASKED
 #define HSTU_DL_SLOTS_UNMASKED 1  // full tiles outside the leading run use the slot schedule too (-1.5 % at configuration 2)
 #endif
@@ -233,6 +236,13 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       }
       return (bool)((c < mk_top - k0) | (c == mk_eq - k0));
     };
+    // Semi-local mask of a history row (m < cap) against keys that are not contextual: key j is kept
+    // iff m - win <= j <= m (0 <= j <= m for a row of the full-attention tail), one unsigned
+    // comparison of j - lo with m - lo.  Per tile the lane keeps k0 + 4 half - lo, per element the
+    // compile-time c is added: three instructions per score instead of the predicate's dozen.
+    const int rng_lo = tail_row ? 0 : m - si.win;
+    const unsigned rng_w = (unsigned)(m - rng_lo);
+    const int rng_lane = 4 * half - rng_lo;
 
     // key tiles [0, nkv) minus the run [skip_a, skip_b) that holds only target keys off this query
     // tile's diagonal (and no contextual key)
@@ -407,7 +417,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     // silu + mask + bf16 packing of one 32 x 32 score block (accumulator layout) into two B operands
     auto silu_pack = [&](auto masked_tag, const f32x16& sv, int k0, int kvb, unsigned rab_addr, bf16x8& o0,
                          bf16x8& o1) __attribute__((always_inline)) {
-      constexpr bool MASKED = decltype(masked_tag)::value;
+      constexpr int MASKED = decltype(masked_tag)::value;  // 0 none, 1 general predicate, 2 range of a history row
+      const int rng_base = k0 + rng_lane;
       f32x16 pv;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -416,7 +427,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         if (HAS_RAB) s += *(lds_cfloat*)(rab_addr + 4u * (unsigned)(kvb * 32 + 8 * (r >> 2) + (r & 3)));
         const float t = s * neg_c;
         float pe = t * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
-        if (MASKED) pe = kept(k0, kvb * 32 + 8 * (r >> 2) + (r & 3)) ? pe : 0.f;
+        if (MASKED == 1) pe = kept(k0, kvb * 32 + 8 * (r >> 2) + (r & 3)) ? pe : 0.f;
+        if (MASKED == 2) pe = (unsigned)(rng_base + (kvb * 32 + 8 * (r >> 2) + (r & 3))) <= rng_w ? pe : 0.f;
         pv[r] = pe;
       }
       u32x4 w0, w1;
@@ -465,7 +477,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         return __builtin_bit_cast(bf16x8, both);
       };
 #if HSTU_DL_SLOTS
-      if constexpr (!FP8 && (!HAS_RAB || HSTU_DL_RAB_SLOTS) && (FAST || HSTU_DL_SLOTS > 1 || (HSTU_DL_SLOTS_UNMASKED && !decltype(masked_tag)::value) || (HAS_RAB && HSTU_DL_RAB_SLOTS > 1))) {  // (mask state leaves this schedule too few registers)
+      if constexpr (!FP8 && (!HAS_RAB || HSTU_DL_RAB_SLOTS) && (FAST || HSTU_DL_SLOTS > 1 || (HSTU_DL_SLOTS_UNMASKED && (decltype(masked_tag)::value == 0 || (HSTU_DL_RANGE_SLOTS && decltype(masked_tag)::value == 2))) || (HAS_RAB && HSTU_DL_RAB_SLOTS > 1))) {  // (mask state leaves this schedule too few registers)
         // Hand-placed schedule, one MFMA per slot with a scheduling fence after each:
         //   slots  0..7   S0 = K[0:32] Q^T            slots  8..15  S1 = K[32:64] Q^T
         //   slots 16..31  O^T[db] += V^T[db, s2] P^T[s2], key step s2 = (slot - 16) / 4, db = slot & 3
@@ -475,6 +487,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         f32x16 sblk[2];
         unsigned pw[2][8];
         bf16x8 F[32];
+        const int rng_base = k0 + rng_lane;
         // slot in which the LDS fragment of slot s is requested (-1: before slot 0).  Six K fragments
         // open a tile; all sixteen would fit the registers that scores and packed P leave free at
         // that point, but measured 1-3 % slower (configurations 2 and 4).  V fragments run ten slots
@@ -489,7 +502,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           return s < 16 ? k_frag(s >> 3, s & 7) : v_frag(pv_db(s), pv_s2(s));
         };
         auto silu_unit = [&](int u) __attribute__((always_inline)) {
-          constexpr bool MASKED = decltype(masked_tag)::value;
+          constexpr int MASKED = decltype(masked_tag)::value;
           const int blk = u >> 3, e = u & 7;
           float pe[2];
 #pragma unroll
@@ -499,7 +512,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
             const float sv = sblk[blk][r];  // the bias is already in there, see bias_block
             const float tv = sv * neg_c;
             float pv = tv * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(tv));
-            if (MASKED) pv = kept(k0, blk * 32 + 8 * (r >> 2) + (r & 3)) ? pv : 0.f;
+            if (MASKED == 1) pv = kept(k0, blk * 32 + 8 * (r >> 2) + (r & 3)) ? pv : 0.f;
+            if (MASKED == 2) pv = (unsigned)(rng_base + (blk * 32 + 8 * (r >> 2) + (r & 3))) <= rng_w ? pv : 0.f;
             pe[t] = pv;
           }
           pw[blk][e] = pack_bf16x2(pe[0], pe[1]);
@@ -792,8 +806,11 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       }
       bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
       if (SEMI) full = full && (idlo_w >= si.tail0 || k0 >= idhi_w - si.win);  // inside every row's window
-      if (full) tile_body(std::false_type{}, buf_tag, k0, nxt, std::false_type{});
-      else tile_body(std::true_type{}, buf_tag, k0, nxt, std::false_type{});
+      // semi-local, history rows only and no contextual key in the tile: the range form of the mask
+      const bool range_mask = SEMI && m_hi < si.cap && k0 >= si.ctx_eff;
+      if (full) tile_body(std::integral_constant<int, 0>{}, buf_tag, k0, nxt, std::false_type{});
+      else if (SEMI && range_mask) tile_body(std::integral_constant<int, 2>{}, buf_tag, k0, nxt, std::false_type{});
+      else tile_body(std::integral_constant<int, 1>{}, buf_tag, k0, nxt, std::false_type{});
     };
 
     // Leading tiles this wave runs without classifying them: unmasked for all of its rows
@@ -847,9 +864,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         fast_pairs = 0;
       }
       for (int pi = 0; pi < fast_pairs; ++pi) {
-        tile_body(std::false_type{}, std::integral_constant<int, 0>{}, it * BN, it + 1, std::true_type{});
+        tile_body(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, it * BN, it + 1, std::true_type{});
         HSTU_DL_TILE_SYNC();
-        tile_body(std::false_type{}, std::integral_constant<int, 1>{}, (it + 1) * BN, it + 2, std::true_type{});
+        tile_body(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, (it + 1) * BN, it + 2, std::true_type{});
         HSTU_DL_TILE_SYNC();
         it += 2;
       }
