@@ -284,8 +284,15 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
 #endif
     }
 
+    // Semi-local mask of a history row (m < cap) against keys that are not contextual: key j is kept
+    // iff m - win <= j <= m (0 <= j <= m for a row of the full-attention tail): one unsigned
+    // comparison of j - lo with m - lo, as in the forward kernel
+    const int rng_lo = tail_row ? 0 : m - si.win;
+    const unsigned rng_w = (unsigned)(m - rng_lo);
+    const int rng_lane = 4 * half - rng_lo;
     auto tile_body = [&](auto masked_tag, auto buf_tag, int k0) __attribute__((always_inline)) {
-      constexpr bool MASKED = decltype(masked_tag)::value;
+      constexpr int MASKED = decltype(masked_tag)::value;  // 0 none, 1 general predicate, 2 range of a history row
+      const int rng_base = k0 + rng_lane;
       constexpr int BUF = decltype(buf_tag)::value;
       const char* kb = (const char*)(BUF ? Ks1 : Ks0);
       const char* vb = (const char*)(BUF ? Vs1 : Vs0);
@@ -325,13 +332,14 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
           }
           float g = dpt[r] * (sig * inner);
           if (per_token) g *= row_scale;
-          if (MASKED) {
+          if (MASKED == 1) {
             const int c = kvb * 32 + 8 * (r >> 2) + (r & 3);
             const int j = k0 + 4 * half + c;
             const bool kp = SEMI ? ((m == j) | ((j < idm) & ((idm - j <= si.win) | tail_row)) | (j < si.ctx_eff)) & (j < si.n)
                                  : ((c < mk_top - k0) | (c == mk_eq - k0));
             g = kp ? g : 0.f;
           }
+          if (MASKED == 2) g = (unsigned)(rng_base + (kvb * 32 + 8 * (r >> 2) + (r & 3))) <= rng_w ? g : 0.f;
           ds[r] = g;
         }
         if constexpr (RAB_GRAD) {
@@ -407,8 +415,9 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       if (!any_kept) return;
       bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
       if (SEMI) full = full && (idlo_w >= si.tail0 || k0 >= idhi_w - si.win);
-      if (full) tile_body(std::false_type{}, buf_tag, k0);
-      else tile_body(std::true_type{}, buf_tag, k0);
+      if (full) tile_body(std::integral_constant<int, 0>{}, buf_tag, k0);
+      else if (SEMI && m_hi < si.cap && k0 >= si.ctx_eff) tile_body(std::integral_constant<int, 2>{}, buf_tag, k0);
+      else tile_body(std::integral_constant<int, 1>{}, buf_tag, k0);
     };
 
     // Gradient band of a finished key tile t -> drab (entry 190 - i of the stage is rab index
@@ -601,7 +610,13 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     bwd_acc_zero();  // dK^T and dV^T accumulators (fixed AGPRs)
 
     auto tile_body = [&](auto masked_tag, auto buf_tag, int m0) __attribute__((always_inline)) {
-      constexpr bool MASKED = decltype(masked_tag)::value;
+      // 0 no mask; 1 the general predicate; 2 (semi-local) keys of the wave all history keys outside the
+      // contextual prefix and the query tile whole and either all window rows (history rows below the
+      // full-attention tail: kept iff 0 <= m - j <= win) or all tail rows (kept iff m >= j): one
+      // unsigned comparison of m - j with a bound that is the same for the whole wave
+      constexpr int MASKED = decltype(masked_tag)::value;
+      const int rng_base = m0 + 4 * half - j;
+      const unsigned rng_w = min(m0, si.cap) >= si.tail0 ? 0x7fffffffu : (unsigned)si.win;
       constexpr int BUF = decltype(buf_tag)::value;
       const char* qb = (const char*)(BUF ? Qs1 : Qs0);
       const char* gb = (const char*)(BUF ? Gs1 : Gs0);
@@ -655,7 +670,12 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
         }
         g = dpv * (sig * inner);
         if (PER_TOKEN) { pe *= tsv; g *= tsv; }
-        if (MASKED) {
+        if (MASKED == 2) {
+          const bool kp = (unsigned)(rng_base + (qb32 * 32 + 8 * (r >> 2) + (r & 3))) <= rng_w;
+          pe = kp ? pe : 0.f;
+          g = kp ? g : 0.f;
+        }
+        if (MASKED == 1) {
           const int c = qb32 * 32 + 8 * (r >> 2) + (r & 3);
           const int m = m0 + 4 * half + c;
           const int idm = min(m, si.cap);
@@ -762,8 +782,11 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       if (SEMI)
         full = full && ((jw0 + 31 < si.ctx_eff) || min(m0, si.cap) >= si.tail0 ||
                         min(m0 + BWD_BN - 1, si.cap) - jw0 <= si.win);
-      if (full) tile_body(std::false_type{}, buf_tag, m0);
-      else tile_body(std::true_type{}, buf_tag, m0);
+      const bool range_mask = SEMI && jw0 + 31 < si.cap && jw0 >= si.ctx_eff && m0 + BWD_BN <= si.n &&
+                              (min(m0, si.cap) >= si.tail0 || m0 + BWD_BN - 1 < min(si.cap, si.tail0));
+      if (full) tile_body(std::integral_constant<int, 0>{}, buf_tag, m0);
+      else if (SEMI && range_mask) tile_body(std::integral_constant<int, 2>{}, buf_tag, m0);
+      else tile_body(std::integral_constant<int, 1>{}, buf_tag, m0);
     };
 
     if (HAS_RAB && it < nq) bwd_band_store<false>(band0, band_first, tid);

@@ -63,7 +63,10 @@ def error_stats(out, ref):
     """Error of ``out`` against ``ref`` over the whole tensor and per row.  A row is one (token, head)
     vector of the last dimension: ``worst_row_rel`` is the largest ``max|err row| / (max|ref row| +
     floor)`` with ``floor`` the smallest non-zero row maximum of the reference, so that a short-prefix
-    row of magnitude 1e-4 counts as much as a row of magnitude 1e-2."""
+    row of magnitude 1e-4 counts as much as a row of magnitude 1e-2.  The floor is not taken below
+    1e-5 of the largest reference magnitude: a gradient row whose only pair sits where silu' crosses
+    zero (x = -1.278) is ten orders below its neighbours by cancellation, and its relative error says
+    nothing (seen once in 4,300 random cases: row maximum 3e-12 against 1e-2)."""
     out = out.detach().float().cpu().numpy().astype(np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     err = np.abs(out - ref)
@@ -75,7 +78,7 @@ def error_stats(out, ref):
         row_ref = np.abs(ref).reshape(-1, d).max(axis=1)
         row_err = err.reshape(-1, d).max(axis=1)
         nz = row_ref[row_ref > 0]
-        row_floor = float(nz.min()) if nz.size else 0.0
+        row_floor = max(float(nz.min()), 1e-5 * float(ref_max)) if nz.size else 0.0
         denom = row_ref + row_floor
         ok = denom > 0
         worst_row_rel = float((row_err[ok] / denom[ok]).max()) if ok.any() else 0.0

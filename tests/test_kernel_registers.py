@@ -63,8 +63,10 @@ def test_key_tile_kernel_accumulators_are_untouched_by_the_compiler(device_asm):
             if "v_mfma" in text:
                 assert in_asm, f"{name}: an MFMA the compiler placed: {line.strip()}"
                 hand_mfma += 1
-        # four tile bodies (two LDS stages x masked / unmasked) of 64 products each
-        assert hand_mfma == 256, (name, hand_mfma)
+        # tile bodies of 64 products each: two LDS stages x (unmasked, masked), and for the semi-local
+        # instantiations a third mask form
+        bodies = 6 if "hstu_bwd_dkv_d128ILb1E" in name else 4
+        assert hand_mfma == 64 * bodies, (name, hand_mfma)
         assert hand_acc >= 128 + 128 + 128, (name, hand_acc)  # clear, accumulate, read back
 
 
