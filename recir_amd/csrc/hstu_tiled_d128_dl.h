@@ -240,9 +240,15 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     // iff m - win <= j <= m (0 <= j <= m for a row of the full-attention tail), one unsigned
     // comparison of j - lo with m - lo.  Per tile the lane keeps k0 + 4 half - lo, per element the
     // compile-time c is added: three instructions per score instead of the predicate's dozen.
-    const int rng_lo = tail_row ? 0 : m - si.win;
-    const unsigned rng_w = (unsigned)(m - rng_lo);
-    const int rng_lane = 4 * half - rng_lo;
+    // (Derived again in every tile from a copy of m the compiler cannot see through: kept across the
+    // tile loop the three values cost the kernel's last registers and the loop reloaded spills.)
+    auto rng_of = [&](int k0, int& base, unsigned& w) __attribute__((always_inline)) {
+      int mm = m;
+      asm volatile("" : "+v"(mm));
+      const int lo = min(mm, si.cap) >= si.tail0 ? 0 : mm - si.win;
+      w = (unsigned)(mm - lo);
+      base = k0 + 4 * half - lo;
+    };
 
     // key tiles [0, nkv) minus the run [skip_a, skip_b) that holds only target keys off this query
     // tile's diagonal (and no contextual key)
@@ -418,7 +424,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     auto silu_pack = [&](auto masked_tag, const f32x16& sv, int k0, int kvb, unsigned rab_addr, bf16x8& o0,
                          bf16x8& o1) __attribute__((always_inline)) {
       constexpr int MASKED = decltype(masked_tag)::value;  // 0 none, 1 general predicate, 2 range of a history row
-      const int rng_base = k0 + rng_lane;
+      int rng_base = 0;
+      unsigned rng_w = 0;
+      if (MASKED == 2) rng_of(k0, rng_base, rng_w);
       f32x16 pv;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -487,7 +495,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         f32x16 sblk[2];
         unsigned pw[2][8];
         bf16x8 F[32];
-        const int rng_base = k0 + rng_lane;
+        int rng_base = 0;
+        unsigned rng_w = 0;
+        if (decltype(masked_tag)::value == 2) rng_of(k0, rng_base, rng_w);
         // slot in which the LDS fragment of slot s is requested (-1: before slot 0).  Six K fragments
         // open a tile; all sixteen would fit the registers that scores and packed P leave free at
         // that point, but measured 1-3 % slower (configurations 2 and 4).  V fragments run ten slots
