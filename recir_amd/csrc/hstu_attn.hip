@@ -641,7 +641,12 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   const bool noncausal = (flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL) != 0;
   if (noncausal && variant >= 2)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "a mask type other than the causal one runs on the generic kernels only");
-  if (tiled_ok && variant != 1 && !noncausal) {
+  // the tiled kernels start their score accumulators from bias / alpha: a bias with alpha = 0 (scores
+  // that are the bias alone) is the generic kernels' case, as in the forward
+  const bool bias_needs_generic = rab && !std::isnormal(1.0f / alpha);
+  if (bias_needs_generic && variant >= 2)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "a bias with alpha = %g runs on the generic kernels only", (double)alpha);
+  if (tiled_ok && variant != 1 && !noncausal && !bias_needs_generic) {
     const size_t half_ws = (recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype) + 255) & ~(size_t)255;
     if (!workspace || workspace_bytes < 2 * half_ws || ((size_t)workspace & 15))
       return fail(RECIR_HSTU_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu at %p",

@@ -157,9 +157,9 @@ __device__ __forceinline__ float bwd_band_load(const float* __restrict__ rab_row
 // REVERSED: entry 190 - i holds index first + i, for the kernel whose elements run over keys (the
 // index falls with the key): a lane's elements then sit at ascending addresses.
 template <bool REVERSED>
-__device__ __forceinline__ void bwd_band_store(float* band, float val, int tid) {
+__device__ __forceinline__ void bwd_band_store(float* band, float val, int tid, float mul) {
   asm volatile("" : "+v"(val));  // first use of the loaded value: the wait for it stays here
-  if (tid < BWD_BAND - 1) band[REVERSED ? (BWD_BAND - 2) - tid : tid] = val * kLog2e;
+  if (tid < BWD_BAND - 1) band[REVERSED ? (BWD_BAND - 2) - tid : tid] = val * mul;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -271,6 +271,8 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     const float row_scale = per_token ? p.attn_scale[si.s + min(m, si.n - 1)] : 1.0f;
     bwd_load_row_frags(bp.dout, (size_t)si.s + m, p.H, h, half, m < q_end, false, 1.0f, gf);
     const float score_c = p.alpha * kLog2e, neg_c = -score_c;
+    // the bias is staged multiplied by log2(e) and joins the score in the multiply-add that applies alpha log2(e)
+    const float bias_mul = kLog2e;
 
     f32x16 acc[4];
 #pragma unroll
@@ -317,8 +319,9 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
         float ds[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          // (the bias is added here, not taken as the accumulator's start: by now the fragment
-          // registers of the products are free, before them the kernel is at its register limit)
+          // (the bias is added here, not taken as the accumulator's start as the dK/dV kernel does: by
+          // now the fragment registers of the products are free, before them this kernel is at its
+          // register limit; measured: 3 % slower at configuration 3, 9 % with the bias-table gradient)
           // silu'(x) = sig (1 + x (1 - sig)), x = alpha s (+ bias): without a bias alpha goes into
           // (1 - sig), so no instruction is spent on x itself
           float sig, inner;
@@ -434,7 +437,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     };
     int prev_tile = -1;
     // two tiles per trip so that the stage index is a compile-time constant
-    if (HAS_RAB && it < nkv) bwd_band_store<true>(band0, band_first, tid);
+    if (HAS_RAB && it < nkv) bwd_band_store<true>(band0, band_first, tid, bias_mul);
     while (it < nkv) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile `it` have landed
       __syncthreads();                                   // everybody's; the other stage is free again
@@ -444,7 +447,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       if (HAS_RAB && nxt < nkv) band_nxt = band_of(nxt);
       if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, 1>{});
       compute_tile(it, std::integral_constant<int, 0>{});
-      if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band1, band_nxt, tid);
+      if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band1, band_nxt, tid, bias_mul);
       prev_tile = it;
       it = nxt;
       if (it >= nkv) {
@@ -458,7 +461,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       if (HAS_RAB && nxt < nkv) band_nxt = band_of(nxt);
       if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, 0>{});
       compute_tile(it, std::integral_constant<int, 1>{});
-      if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band0, band_nxt, tid);
+      if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band0, band_nxt, tid, bias_mul);
       prev_tile = it;
       it = nxt;
       if (RAB_GRAD && it >= nkv) { __syncthreads(); flush_gband(prev_tile, gband1); }
@@ -605,6 +608,10 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     bf16x8 kf[8], vf[8];
     bwd_load_row_frags(p.k, (size_t)si.s + j, p.H, h, half, j < si.n, false, 1.0f, kf);
     const float score_c = p.alpha * kLog2e, neg_c = -score_c;
+    // The bias is staged divided by alpha and starts the score accumulators: alpha (s + bias / alpha)
+    // is the biased score, and the arithmetic below is that of the kernel without a bias.  (The host
+    // sends a bias with alpha = 0 to the generic kernels.)
+    const float bias_mul = HAS_RAB ? 1.0f / p.alpha : 0.f;
     bwd_load_row_frags(p.v, (size_t)si.s + j, p.H, h, half, j < si.n, false, 1.0f, vf);
 
     bwd_acc_zero();  // dK^T and dV^T accumulators (fixed AGPRs)
@@ -637,8 +644,8 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
         const int kk = i >> 1;
         const bf16x8 kfr = kf[kk], vfr = vf[kk];
         if (!(i & 1)) {
-          if (kk == 0) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(s) : "v"(f), "v"(kfr));
-          else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(s) : "v"(f), "v"(kfr));
+          if (kk == 0 && !HAS_RAB) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(s) : "v"(f), "v"(kfr));
+          else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(s) : "v"(f), "v"(kfr));  // (with a bias: s starts from it)
         } else {
           if (kk == 0) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(dp) : "v"(f), "v"(vfr));
           else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(dp) : "v"(f), "v"(vfr));
@@ -652,22 +659,13 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
         return bwd_tr_frag((i & 1) ? qb : gb, lc, (i >> 1) & 3, 2 * qb32 + (i >> 3));
       };
       // P and dS of element r of block qb32 (query row m0 + 32 qb32 + 8 (r / 4) + 4 half + r % 4, this lane's key)
-      auto element = [&](int qb32, int r, float sv_raw, float dpv, float biasv, float tsv, float& pe, float& g) __attribute__((always_inline)) {
-        // P = x sig and silu'(x) = sig (1 + x (1 - sig)), x = alpha s (+ bias).  Without a bias no
-        // instruction is spent on x: alpha goes into (1 - sig), and P is kept as s sig, its alpha
-        // applied to the dV accumulators at the end
-        float sig, inner;
-        if (HAS_RAB) {
-          const float u = __builtin_fmaf(sv_raw, score_c, biasv);
-          sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
-          const float sv = u * kLn2;
-          inner = __builtin_fmaf(sv, 1.0f - sig, 1.0f);
-          pe = sv * sig;
-        } else {
-          sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(sv_raw * neg_c));
-          inner = __builtin_fmaf(sv_raw, __builtin_fmaf(sig, -p.alpha, p.alpha), 1.0f);
-          pe = sv_raw * sig;
-        }
+      auto element = [&](int qb32, int r, float sv_raw, float dpv, float tsv, float& pe, float& g) __attribute__((always_inline)) {
+        // P = x sig and silu'(x) = sig (1 + x (1 - sig)), x = alpha s (s with the bias / alpha it started
+        // from).  No instruction is spent on x: alpha goes into (1 - sig), and P is kept as s sig, its
+        // alpha applied to the dV accumulators at the end
+        const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(sv_raw * neg_c));
+        const float inner = __builtin_fmaf(sv_raw, __builtin_fmaf(sig, -p.alpha, p.alpha), 1.0f);
+        pe = sv_raw * sig;
         g = dpv * (sig * inner);
         if (PER_TOKEN) { pe *= tsv; g *= tsv; }
         if (MASKED == 2) {
@@ -685,10 +683,12 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
           g = kp ? g : 0.f;
         }
       };
-      auto load_bias = [&](int qb32, float (&bias)[16]) __attribute__((always_inline)) {
+      // the staged bias (already divided by alpha) as the start of a block's score accumulators
+      auto load_bias = [&](int qb32, f32x16& sacc) __attribute__((always_inline)) {
+        if (!HAS_RAB) return;
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          bias[r] = HAS_RAB ? bandt[(qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3)) - (j - j0) + (BWD_BM - 1)] : 0.f;
+          sacc[r] = bandt[(qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3)) - (j - j0) + (BWD_BM - 1)];
       };
       auto load_ts = [&](int qb32, float (&ts)[16]) __attribute__((always_inline)) {
 #pragma unroll
@@ -697,12 +697,12 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       };
       constexpr int PD = 3;  // fragments requested this many products ahead in the pipelined phases
       f32x16 sA, dpA, sB, dpB;
-      float bias[16], ts[16];
+      float ts[16];
       unsigned pwA[8], dwA[8], pwB[8], dwB[8];  // packed P and dS of the two blocks
       // phase 1
+      load_bias(0, sA);
 #pragma unroll
       for (int i = 0; i < 16; ++i) score_mfma(0, i, sA, dpA, score_frag(0, i));
-      load_bias(0, bias);
       load_ts(0, ts);
       // an MFMA result may be read by other instructions 11 cycles after the MFMA at the earliest; the
       // compiler does not count for instructions it did not place
@@ -713,19 +713,19 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
 #pragma unroll
         for (int i = 0; i < PD; ++i) F[i] = score_frag(1, i);
         float pe_prev = 0.f, g_prev = 0.f;
+        load_bias(1, sB);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           if (i + PD < 16) F[i + PD] = score_frag(1, i + PD);
           score_mfma(1, i, sB, dpB, F[i]);
           float pe, g;
-          element(0, i, sA[i], dpA[i], bias[i], ts[i], pe, g);
+          element(0, i, sA[i], dpA[i], ts[i], pe, g);
           if (i & 1) { pwA[i >> 1] = pack_bf16x2(pe_prev, pe); dwA[i >> 1] = pack_bf16x2(g_prev, g); }
           pe_prev = pe; g_prev = g;
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      load_bias(1, bias);
       load_ts(1, ts);
       asm volatile("s_nop 15" : "+v"(sB), "+v"(dpB));
       // phase 3
@@ -744,7 +744,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
           if (i + PD < 16) F[i + PD] = acc_frag(0, i + PD);
           bwd_acc_mfma1(((i & 1) ? 4 : 0) + ((i >> 1) & 3), F[i], opA[2 * (i >> 3) + (i & 1)]);
           float pe, g;
-          element(1, i, sB[i], dpB[i], bias[i], ts[i], pe, g);
+          element(1, i, sB[i], dpB[i], ts[i], pe, g);
           if (i & 1) { pwB[i >> 1] = pack_bf16x2(pe_prev, pe); dwB[i >> 1] = pack_bf16x2(g_prev, g); }
           pe_prev = pe; g_prev = g;
           __builtin_amdgcn_sched_barrier(0);
@@ -789,7 +789,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       else tile_body(std::integral_constant<int, 1>{}, buf_tag, m0);
     };
 
-    if (HAS_RAB && it < nq) bwd_band_store<false>(band0, band_first, tid);
+    if (HAS_RAB && it < nq) bwd_band_store<false>(band0, band_first, tid, bias_mul);
     while (it < nq) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -799,7 +799,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 1>{});
       draw_step(nq - it);
       compute_tile(it, std::integral_constant<int, 0>{});
-      if (HAS_RAB && nxt < nq) bwd_band_store<false>(band1, band_nxt, tid);
+      if (HAS_RAB && nxt < nq) bwd_band_store<false>(band1, band_nxt, tid, bias_mul);
       it = nxt;
       if (it >= nq) break;
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -809,7 +809,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 0>{});
       draw_step(nq - it);
       compute_tile(it, std::integral_constant<int, 1>{});
-      if (HAS_RAB && nxt < nq) bwd_band_store<false>(band0, band_nxt, tid);
+      if (HAS_RAB && nxt < nq) bwd_band_store<false>(band0, band_nxt, tid, bias_mul);
       it = nxt;
     }
     draw_finish();
@@ -817,7 +817,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     if (j < si.n) {
       const float oscale = PER_TOKEN ? 1.0f : bwd_output_scale(p);
       const float kscale = p.alpha * oscale;
-      const float vscale = HAS_RAB ? oscale : kscale;  // without a bias P was kept without its alpha
+      const float vscale = kscale;  // P was kept without its alpha
       unsigned short* krow = (unsigned short*)bp.dk + ((size_t)(si.s + j) * p.H + h) * HD;
       unsigned short* vrow = (unsigned short*)bp.dv + ((size_t)(si.s + j) * p.H + h) * HD;
 #pragma unroll

@@ -566,3 +566,29 @@ def test_noncausal_mask_through_autograd_and_with_a_bias(oracle):
                                             alpha=wl.alpha, contextual_seq_len=2, rab=wl.rab.cuda(), max_attn_len=12,
                                             full_attn_size=5)
     assert not torch.equal(out_c, out.detach())
+
+
+def test_a_bias_with_alpha_zero_runs_on_the_generic_kernels(oracle):
+    """The tiled kernels keep the bias divided by alpha in their score accumulators; with alpha = 0 the
+    scores are the bias alone and the call goes to the generic kernels, forward and backward."""
+    from recir_amd import _lib, ops
+    from recir_amd.workloads import make_jagged
+    from tests.parity_util import assert_bf16_close, run_hip, run_oracle
+
+    wl = make_jagged([150, 64, 1, 0, 200], [20, 64, 0, 0, 7], 2, 128, 128, max_seq_len=256, alpha=0.0, dtype="bf16",
+                     seed=81, with_rab=True, rab_std=0.7, contextual_seq_len=2, tail_rows=1)
+    out = run_hip(wl)
+    assert _lib.last_kernel() == "generic_bf16"
+    assert_bf16_close(out, run_oracle(oracle, wl), "alpha 0 forward")
+    dout = torch.randn(wl.T, wl.H, 128, generator=torch.Generator().manual_seed(5)).bfloat16().float()
+    got = run_hip_bwd(wl, dout, rab=wl.rab)
+    assert _lib.last_kernel() == "bwd_generic_bf16"
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=0.0, rab=wl.rab.numpy(),
+                           contextual_seq_len=2)
+    # dq and dk are exactly zero (the scores do not depend on q or k); dv follows the bias
+    assert not got[0].float().abs().max().item() and not got[1].float().abs().max().item()
+    st = error_stats(got[2], want[2])
+    assert st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL, st
+    with ops.force_kernel(ops.KERNEL_TILED_DIRECT), pytest.raises(ValueError, match="generic kernels only"):
+        run_hip_bwd(wl, dout, rab=wl.rab)
