@@ -328,7 +328,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
           if (HAS_RAB) {
             const float u = __builtin_fmaf(st[r], score_c, *(lds_cfloat*)(band_addr + 4u * (unsigned)(kvb * 32 + 8 * (r >> 2) + (r & 3))));
             sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-u));
-            inner = __builtin_fmaf(u * kLn2, 1.0f - sig, 1.0f);
+            inner = __builtin_fmaf(u, __builtin_fmaf(sig, -kLn2, kLn2), 1.0f);  // x (1 - sig) with x = u ln 2
           } else {
             sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(st[r] * neg_c));
             inner = __builtin_fmaf(st[r], __builtin_fmaf(sig, -p.alpha, p.alpha), 1.0f);
