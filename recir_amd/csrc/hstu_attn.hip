@@ -451,7 +451,7 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     p.items_cap = (int)items;
     const int bm = BM;
     // only the direct-to-LDS kernel reads the row bound of an item
-    int plan_mode = (variant == 0 || variant == 3) ? PLAN_SHIFT_ODD : 0;
+    int plan_mode = ((variant == 0 || variant == 3) ? PLAN_SHIFT_ODD : 0) | PLAN_PAIR_CU;  // (two workgroups per CU)
     // q, k, v and out beyond the last-level cache: lists ordered by groups of pairs (hstu_plan.h)
     if ((flags & RECIR_HSTU_FLAG_GROUPED_LISTS) || tensors_exceed_llc(T, H, Dqk, Dv, fp8 ? 1 : 2, 2)) plan_mode |= PLAN_GROUP;
     // slots per XCD the launch covers: an even share of the items plus the imbalance the dealing of
@@ -673,7 +673,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
       if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS) {
         // q, k, v, dout and the three gradients beyond the last-level cache: lists ordered by groups of pairs
         const int grp = ((flags & RECIR_HSTU_FLAG_GROUPED_LISTS) || tensors_exceed_llc(T, H, Dqk, Dv, 2, BWD_GROUP_TENSORS)) ? PLAN_GROUP : 0;
-        hipLaunchKernelGGL(hstu_plan_pair_kernel, dim3(2), dim3(PLAN_THREADS), 0, stream, bq.f, PLAN_SHIFT_ODD | grp, bk.f, PLAN_REVERSE | grp, BWD_BM);
+        hipLaunchKernelGGL(hstu_plan_pair_kernel, dim3(2), dim3(PLAN_THREADS), 0, stream, bq.f, PLAN_SHIFT_ODD | PLAN_PAIR_CU | grp, bk.f, PLAN_REVERSE | grp, BWD_BM);
         if (int rc = launch_status("hstu_plan_pair_kernel")) return rc;
       } else {
         for (int rev = 0; rev < 2; ++rev) {

@@ -41,6 +41,20 @@ constexpr int PLAN_SHIFT_ODD = 2;   // see tile_rows
 constexpr int PLAN_NO_SPREAD = 4;   // always deal whole (sequence, head) pairs
 constexpr int PLAN_GROUP = 8;       // order a list by groups of PLAN_GROUP_PAIRS pairs (see plan_one_block)
 constexpr int PLAN_GROUP_PAIRS = 8;
+constexpr int PLAN_PAIR_CU = 16;    // see pair_pos
+constexpr int CUS_PER_XCD = 32;
+
+// A launch with two workgroups per CU places list positions s and s + 32 of an XCD on the same CU
+// (read off the hardware ids of a 512-workgroup launch: the first 32 workgroups of an XCD take one
+// CU each, the next 32 the same CUs in the same order; later workgroups go wherever a slot frees).
+// With PLAN_PAIR_CU the second run of 32 positions is reversed, so that the heaviest item shares its
+// CU with the lightest of the first 64 instead of the 33rd heaviest.  Worth 1-5 % where 64 heavy
+// items open a list (long sequences), nothing at configuration 2.
+__device__ __forceinline__ int pair_pos(int pos, int list_len, int mode) {
+  if (!(mode & PLAN_PAIR_CU) || pos < CUS_PER_XCD) return pos;
+  const int hi = min(list_len, 2 * CUS_PER_XCD);
+  return pos < hi ? CUS_PER_XCD + (hi - 1 - pos) : pos;
+}
 #ifndef HSTU_PLAN_SPREAD_AT
 #define HSTU_PLAN_SPREAD_AT 1.05f
 #endif
@@ -168,6 +182,11 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
     };
     for (int t = tid; t < ttab; t += PLAN_THREADS) above[0][t] = all_above(t);
     __syncthreads();
+    // length of list x when n_items are dealt in boustrophedon order
+    auto dealt_len = [&](int x) {
+      const int part = n_items % (2 * NUM_XCD);
+      return 2 * (n_items / (2 * NUM_XCD)) + (x < part ? 1 : 0) + (x >= 2 * NUM_XCD - part ? 1 : 0);
+    };
     const int per_rank = tmax * H;
     for (int i = tid; i < B * per_rank; i += PLAN_THREADS) {
       const int r = i / per_rank, rem = i - r * per_rank;
@@ -181,11 +200,11 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
       const int g = (t < ttab ? above[0][t] : all_above(t)) + r * H + h;
       WorkItem w;
       fill_item(w, si, bm, t, my_nt, mode, h, b);
-      p.ws_items[(size_t)snake_xcd(g) * p.items_cap + snake_slot(g)] = w;
+      const int x = snake_xcd(g);
+      p.ws_items[(size_t)x * p.items_cap + pair_pos(snake_slot(g), dealt_len(x), mode)] = w;
     }
     if (tid < NUM_XCD) {
-      const int part = n_items % (2 * NUM_XCD);
-      p.ws_counts[tid] = 2 * (n_items / (2 * NUM_XCD)) + (tid < part ? 1 : 0) + (tid >= 2 * NUM_XCD - part ? 1 : 0);
+      p.ws_counts[tid] = dealt_len(tid);
       p.ws_counts[NUM_XCD + tid] = p.grid_slots;  // first list position a persistent kernel's workgroups draw
     }
     return;
@@ -210,7 +229,7 @@ __device__ __forceinline__ void plan_one_block(const Params& p, int bm, int mode
       pos = gbase[x][g] + (k - k0);
       for (int kk = k0; kk < k0 + PLAN_GROUP_PAIRS && kk < per_list; ++kk) pos += max(0, xnt[x][kk] - 1 - t);
     } else {
-      pos = (t < ttab ? above[x][t] : tiles_above(x, t)) + k;
+      pos = pair_pos((t < ttab ? above[x][t] : tiles_above(x, t)) + k, list_total[x], mode);
     }
     WorkItem w;
     fill_item(w, si, bm, t, my_nt, mode, h, b);
