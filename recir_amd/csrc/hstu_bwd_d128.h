@@ -196,6 +196,23 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
 
   zero_tail_rows_of<256>(p, bp.dq, (size_t)p.H * HD * 2);
   if (RAB_GRAD && tid < BWD_BAND) { gband0[tid] = 0.f; gband1[tid] = 0.f; }  // published by the first tile's barrier
+  // Gradient of the bias table with a scalar output scale: the sums along the diagonals are kept in
+  // LDS as fixed-point integers.  An LDS float atomic takes three cycles per lane, one lane at a time
+  // (192 cycles for a wave's instruction), an integer one 4-16 cycles for the whole instruction.  The
+  // scale is a power of two chosen so that a tile's sum cannot overflow: |dS| <= 1.1 |dP|,
+  // |dP| <= 128 max|dout| max|v|, and a diagonal meets at most 64 pairs of a (128-row, 64-key) tile.
+  // What the conversion drops is below 2^-30 of that bound per pair.  Non-finite inputs make the
+  // scale zero and every flushed value NaN.
+  constexpr bool FIXED = RAB_GRAD && !PER_TOKEN;
+  float fx_scale = 0.f, fx_inv = 0.f;
+  if constexpr (FIXED) {
+    const float bound = __uint_as_float(bp.absmax[0]) * __uint_as_float(bp.absmax[1]) * (128.0f * 1.1f * 64.0f);
+    const int eb = (int)((__float_as_uint(bound) >> 23) & 0xffu) - 126;  // bound < 2^eb
+    const bool usable = bound > 0.f && bound < 3.0e38f;
+    const int sh = min(max(30 - eb, -120), 120);
+    fx_scale = usable ? __uint_as_float((unsigned)(127 + sh) << 23) : 0.f;
+    fx_inv = usable ? __uint_as_float((unsigned)(127 - sh) << 23) : (bound == 0.f ? 0.f : __uint_as_float(0x7fc00000u));
+  }
 
   const int xcd = blockIdx.x % NUM_XCD;
   const int list_len = p.ws_counts[xcd];
@@ -345,7 +362,12 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
           if (MASKED == 2) g = (unsigned)(rng_base + (kvb * 32 + 8 * (r >> 2) + (r & 3))) <= rng_w ? g : 0.f;
           ds[r] = g;
         }
-        if constexpr (RAB_GRAD) {
+        if constexpr (FIXED) {
+          int* gi = (int*)(BUF ? gband1 : gband0) + (band_lane >> 2);
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            __hip_atomic_fetch_add(gi + (kvb * 32 + 8 * (r >> 2) + (r & 3)), (int)(ds[r] * fx_scale), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else if constexpr (RAB_GRAD) {
           const unsigned gaddr = (unsigned)(size_t)(BUF ? gband1 : gband0) + band_lane;
           // Element 4 g + i of lane l (query row l, key 8 g + i of its half) lies on diagonal i - l: the four
           // elements of lanes l .. l + 3 with i = 0 .. 3 share one.  They are summed across lanes first
@@ -429,7 +451,8 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     const float drab_scale = per_token ? 1.0f : bwd_output_scale(p);
     auto flush_gband = [&](int t, float* g) __attribute__((always_inline)) {
       if (tid < BWD_BAND - 1) {
-        const float val = g[(BWD_BAND - 2) - tid];
+        float val = g[(BWD_BAND - 2) - tid];
+        if constexpr (FIXED) val = (float)__float_as_int(val) * fx_inv;  // (NaN for every entry when the inputs are not finite)
         g[(BWD_BAND - 2) - tid] = 0.f;
         const int idx = q0 - t * BWD_BN - (BWD_BN - 1) + p.N - 1 + tid;
         if (val != 0.f && idx >= 0 && idx < rab_w) unsafeAtomicAdd(&bp.drab[(size_t)h * rab_w + idx], val * drab_scale);

@@ -199,6 +199,8 @@ struct BwdParams {
   void* dk;          // [T,H,Dqk]
   void* dv;          // [T,H,Dv]
   float* drab;       // [H, 2N-1] gradient of the bias table, zeroed by the entry point, or null
+  const unsigned* absmax;  // with drab (tiled kernels, scalar scale): the largest |dout| and |v| of the
+                           // call's rows as bf16 magnitudes << 16, i.e. the bits of a float
 };
 
 }  // namespace recir_hstu
