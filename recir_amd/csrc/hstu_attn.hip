@@ -186,32 +186,6 @@ __global__ __launch_bounds__(256) void hstu_calibration_copy(u32x4* dst, const u
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
 }
 
-// Largest magnitude of the valid rows of two bf16 tensors of n8 16-byte chunks each (out[0], out[1]:
-// bf16 bits << 16, cleared by the caller).  Magnitudes compare as integers.
-__global__ __launch_bounds__(256) void hstu_absmax2_bf16(const u32x4* a, const u32x4* b, unsigned* out, size_t n8_all, const void* seq_end,
-                                                        int i32, int T, int H, int D8) {
-  const size_t n8 = quant_valid_chunks(n8_all, seq_end, i32, T, H, D8);
-  const u32x4* x = blockIdx.y ? b : a;
-  const size_t stride = (size_t)gridDim.x * blockDim.x;
-  unsigned run = 0;
-  constexpr int U = 4;
-  for (size_t i0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < n8; i0 += stride * U) {
-    u32x4 v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const size_t i = i0 + u * stride;
-      v[u] = i < n8 ? x[i] : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) run = max(run, max(v[u][w] & 0x7fffu, (v[u][w] >> 16) & 0x7fffu));
-  }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) run = max(run, (unsigned)__shfl_xor((int)run, d, 64));
-  if ((threadIdx.x & 63) == 0 && run) atomicMax(out + blockIdx.y, run << 16);
-}
-
 __global__ void hstu_fill_zero(unsigned short* out, size_t n2) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n2; i += stride) out[i] = 0;
@@ -595,7 +569,7 @@ int recir_hstu_attn_fwd_noalloc(const void* q, const void* k, const void* v, voi
                              (size_t)RECIR_HSTU_NOALLOC_SCRATCH_BYTES, hip_stream);
 }
 
-constexpr size_t BWD_WS_TAIL = 256;  // behind the two lists: the largest |dout| and |v| of the call (see drab)
+constexpr size_t BWD_WS_TAIL = 256;  // behind the two lists: the largest |v| of the call (see drab)
 size_t recir_hstu_attn_bwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk, int32_t Dv,
                                            int32_t dtype) {
   // two work lists: query tiles for dQ, key tiles for dK/dV
@@ -713,16 +687,11 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     if (drab && !(attn_scale && (flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN))) {
       // The query-tile kernel sums dS along the diagonals in LDS as fixed-point integers (LDS float
       // atomics run one lane at a time); the scale comes from a bound on |dS|, which needs the largest
-      // magnitudes of dout and v.
+      // magnitude of v: the key-tile kernel, which runs first and holds every v row once, leaves it here.
       unsigned* am = (unsigned*)((char*)workspace + 2 * half_ws);
       hipLaunchKernelGGL(hstu_fill_zero, dim3(1), dim3(64), 0, stream, (unsigned short*)am, (size_t)4);
-      const size_t n8 = (size_t)T * H * (HD / 8);
-      const int i32 = (flags & RECIR_HSTU_FLAG_OFFSETS_I32) ? 1 : 0;
-      const void* seq_end = (const char*)seq_offsets + (size_t)B * (i32 ? 4 : 8);  // rows from seq_offsets[B] on are padding
-      hipLaunchKernelGGL(hstu_absmax2_bf16, dim3(512, 2), dim3(256), 0, stream, (const u32x4*)dout, (const u32x4*)v, am, n8, seq_end,
-                         i32, T, H, HD / 8);
-      if (int rc = launch_status("hstu_absmax2_bf16")) return rc;
-      bq.absmax = am;
+      if (int rc = launch_status("hstu_fill_zero")) return rc;
+      bq.absmax = bk.absmax = am;
     }
     const dim3 grid((unsigned)(slots * NUM_XCD)), grid_k((unsigned)(kslots * NUM_XCD));
     launch_bwd_tiled(semi, rab != nullptr, grid, grid_k, stream, bk, bq);

@@ -138,6 +138,18 @@ __device__ __forceinline__ void bwd_load_row_frags(const void* base, size_t row,
   }
 }
 
+// largest bf16 magnitude (15 bits) among the 64 values a lane holds of a row
+__device__ __forceinline__ unsigned bwd_frag_absmax(const bf16x8 (&f)[8]) {
+  unsigned mx = 0;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    const u32x4 w = __builtin_bit_cast(u32x4, f[kk]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx = max(mx, max(w[i] & 0x7fffu, (w[i] >> 16) & 0x7fffu));
+  }
+  return mx;
+}
+
 __device__ __forceinline__ float bwd_output_scale(const Params& p) {
   return p.attn_scale ? p.attn_scale[0] : 1.0f / (float)p.N;
 }
@@ -199,20 +211,13 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
   // Gradient of the bias table with a scalar output scale: the sums along the diagonals are kept in
   // LDS as fixed-point integers.  An LDS float atomic takes three cycles per lane, one lane at a time
   // (192 cycles for a wave's instruction), an integer one 4-16 cycles for the whole instruction.  The
-  // scale is a power of two chosen so that a tile's sum cannot overflow: |dS| <= 1.1 |dP|,
-  // |dP| <= 128 max|dout| max|v|, and a diagonal meets at most 64 pairs of a (128-row, 64-key) tile.
-  // What the conversion drops is below 2^-30 of that bound per pair.  Non-finite inputs make the
-  // scale zero and every flushed value NaN.
+  // scale is a power of two, chosen per item so that a tile's sum cannot overflow: |dS| <= 1.1 |dP|,
+  // |dP| <= 128 max|dout row of the item| max|v|, and a diagonal meets at most 64 pairs of a
+  // (128-row, 64-key) tile.  What the conversion drops is below 2^-30 of that bound per pair.
+  // Non-finite inputs make the scale zero and every flushed value NaN.
   constexpr bool FIXED = RAB_GRAD && !PER_TOKEN;
+  __shared__ unsigned do_max_s[4];  // per wave: largest |dout| magnitude of its rows of the item
   float fx_scale = 0.f, fx_inv = 0.f;
-  if constexpr (FIXED) {
-    const float bound = __uint_as_float(bp.absmax[0]) * __uint_as_float(bp.absmax[1]) * (128.0f * 1.1f * 64.0f);
-    const int eb = (int)((__float_as_uint(bound) >> 23) & 0xffu) - 126;  // bound < 2^eb
-    const bool usable = bound > 0.f && bound < 3.0e38f;
-    const int sh = min(max(30 - eb, -120), 120);
-    fx_scale = usable ? __uint_as_float((unsigned)(127 + sh) << 23) : 0.f;
-    fx_inv = usable ? __uint_as_float((unsigned)(127 - sh) << 23) : (bound == 0.f ? 0.f : __uint_as_float(0x7fc00000u));
-  }
 
   const int xcd = blockIdx.x % NUM_XCD;
   const int list_len = p.ws_counts[xcd];
@@ -287,6 +292,12 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     constexpr bool per_token = PER_TOKEN;
     const float row_scale = per_token ? p.attn_scale[si.s + min(m, si.n - 1)] : 1.0f;
     bwd_load_row_frags(bp.dout, (size_t)si.s + m, p.H, h, half, m < q_end, false, 1.0f, gf);
+    if constexpr (FIXED) {  // read after the first tile's barrier
+      unsigned mx = bwd_frag_absmax(gf);
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) mx = max(mx, (unsigned)__shfl_xor((int)mx, d, 64));
+      if (lane == 0) do_max_s[wave] = mx;
+    }
     const float score_c = p.alpha * kLog2e, neg_c = -score_c;
     // the bias is staged multiplied by log2(e) and joins the score in the multiply-add that applies alpha log2(e)
     const float bias_mul = kLog2e;
@@ -464,6 +475,18 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     while (it < nkv) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile `it` have landed
       __syncthreads();                                   // everybody's; the other stage is free again
+      if constexpr (FIXED) {
+        if (prev_tile < 0) {  // first tile of the item: the fixed-point scale of its diagonal sums
+          const unsigned dmx = max(max(do_max_s[0], do_max_s[1]), max(do_max_s[2], do_max_s[3]));
+          const float bound = __uint_as_float(dmx << 16) * __uint_as_float(__hip_atomic_load(bp.absmax + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) *
+                              (128.0f * 1.1f * 64.0f);
+          const int eb = (int)((__float_as_uint(bound) >> 23) & 0xffu) - 126;  // bound < 2^eb
+          const bool usable = bound > 0.f && bound < 3.0e38f;
+          const int sh = min(max(30 - eb, -120), 120);
+          fx_scale = usable ? __uint_as_float((unsigned)(127 + sh) << 23) : 0.f;
+          fx_inv = usable ? __uint_as_float((unsigned)(127 - sh) << 23) : (bound == 0.f ? 0.f : __uint_as_float(0x7fc00000u));
+        }
+      }
       if (RAB_GRAD && prev_tile >= 0) flush_gband(prev_tile, gband1);
       int nxt = next_tile(it);
       float band_nxt = 0.f;
@@ -836,6 +859,15 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       it = nxt;
     }
     draw_finish();
+    // (here, where everything in flight has been waited for: at the item's start the wait for the word's
+    // value would also wait for the first tile's copies)
+    if (bp.absmax) {  // the query-tile kernel's fixed-point sums need the largest |v| of the call
+      unsigned mx = bwd_frag_absmax(vf);
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) mx = max(mx, (unsigned)__shfl_xor((int)mx, d, 64));
+      mx <<= 16;
+      if (lane == 0 && mx > __hip_atomic_load(bp.absmax + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) atomicMax(bp.absmax + 1, mx);
+    }
 
     if (j < si.n) {
       const float oscale = PER_TOKEN ? 1.0f : bwd_output_scale(p);

@@ -199,8 +199,9 @@ struct BwdParams {
   void* dk;          // [T,H,Dqk]
   void* dv;          // [T,H,Dv]
   float* drab;       // [H, 2N-1] gradient of the bias table, zeroed by the entry point, or null
-  const unsigned* absmax;  // with drab (tiled kernels, scalar scale): the largest |dout| and |v| of the
-                           // call's rows as bf16 magnitudes << 16, i.e. the bits of a float
+  unsigned* absmax;  // with drab (tiled kernels, scalar scale): word 1 receives the largest |v| of the call's
+                     // rows as a bf16 magnitude << 16, i.e. the bits of a float (key-tile kernel), and
+                     // is read by the query-tile kernel; else null
 };
 
 }  // namespace recir_hstu

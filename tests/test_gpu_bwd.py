@@ -592,3 +592,52 @@ def test_a_bias_with_alpha_zero_runs_on_the_generic_kernels(oracle):
     assert st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL, st
     with ops.force_kernel(ops.KERNEL_TILED_DIRECT), pytest.raises(ValueError, match="generic kernels only"):
         run_hip_bwd(wl, dout, rab=wl.rab)
+
+
+@pytest.mark.parametrize("dout_mul,v_mul", [(3.0e4, 1.0e-3), (1.0e-5, 1.0), (1.0, 2.0e3)])
+def test_bias_table_gradient_far_from_unit_scale(oracle, dout_mul, v_mul):
+    """With a scalar output scale the tiled dQ kernel sums dS along the diagonals as fixed-point
+    integers whose scale follows the data (largest |dout| of the item's rows, largest |v| of the call):
+    the result must not depend on the magnitude of either."""
+    import recir_amd
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([300, 129, 64, 1, 0, 517], [40, 129, 0, 0, 0, 6], 2, 128, 128, max_seq_len=600, alpha=1 / 128,
+                     dtype="bf16", seed=91, with_rab=True, rab_std=0.5, contextual_seq_len=3, tail_rows=2)
+    wl.v.mul_(v_mul)
+    wl.v.copy_(wl.v.bfloat16().float())
+    dout = (torch.randn(wl.T, wl.H, 128, generator=torch.Generator().manual_seed(11)) * dout_mul).bfloat16().float()
+    # a few rows far above the rest: the scale must follow the largest, the small ones keep their share
+    dout[5] *= 64.0
+    dout = dout.bfloat16().float()
+    q, k, v, off, nt = to_device(wl)
+    kw = dict(max_seq_len=wl.max_seq_len, alpha=wl.alpha, contextual_seq_len=3, rab=wl.rab.cuda())
+    dq, dk, dv, drab = recir_amd.jagged_hstu_attention_backward(dout.to(q.device, q.dtype), q, k, v, off, nt, rab_grad=True, **kw)
+    torch.cuda.synchronize()
+    assert _lib.last_kernel() == "bwd_tiled_d128_bf16_rab"
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha, rab=wl.rab.numpy(),
+                           contextual_seq_len=3, rab_grad=True)
+    st = error_stats(drab, want[3])
+    print(f"[parity] d rab, dout x {dout_mul:g}, v x {v_mul:g}: {st}", flush=True)
+    assert st["ref_max"] > 0 and st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL, st
+    assert not drab.cpu().numpy()[np.asarray(want[3]) == 0].any()
+
+
+def test_bias_table_gradient_of_non_finite_input_is_not_finite():
+    """A NaN in dout must not come out as a plausible number (the fixed-point sums cannot carry it: the
+    scale is then zero and the flushed values are NaN)."""
+    import recir_amd
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([200, 70], [10, 0], 2, 128, 128, max_seq_len=256, alpha=1 / 128, dtype="bf16", seed=92,
+                     with_rab=True, rab_std=0.5)
+    dout = torch.randn(wl.T, wl.H, 128, generator=torch.Generator().manual_seed(12)).bfloat16()
+    dout[17, 1, 5] = float("nan")
+    q, k, v, off, nt = to_device(wl)
+    out = recir_amd.jagged_hstu_attention_backward(dout.cuda(), q, k, v, off, nt, rab_grad=True, max_seq_len=256,
+                                                   alpha=1 / 128, rab=wl.rab.cuda())
+    torch.cuda.synchronize()
+    assert torch.isnan(out[3][1]).any()  # head 1 holds the NaN
+    assert torch.isfinite(out[3][0]).all()  # head 0 is untouched by it
