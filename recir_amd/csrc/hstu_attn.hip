@@ -684,7 +684,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
         }
       }
     }
-    if (drab && !(attn_scale && (flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN))) {
+    if (drab) {
       // The query-tile kernel sums dS along the diagonals in LDS as fixed-point integers (LDS float
       // atomics run one lane at a time); the scale comes from a bound on |dS|, which needs the largest
       // magnitude of v: the key-tile kernel, which runs first and holds every v row once, leaves it here.

@@ -208,15 +208,15 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
 
   zero_tail_rows_of<256>(p, bp.dq, (size_t)p.H * HD * 2);
   if (RAB_GRAD && tid < BWD_BAND) { gband0[tid] = 0.f; gband1[tid] = 0.f; }  // published by the first tile's barrier
-  // Gradient of the bias table with a scalar output scale: the sums along the diagonals are kept in
-  // LDS as fixed-point integers.  An LDS float atomic takes three cycles per lane, one lane at a time
+  // Gradient of the bias table: the sums along the diagonals are kept in LDS as fixed-point integers.  An LDS float atomic takes three cycles per lane, one lane at a time
   // (192 cycles for a wave's instruction), an integer one 4-16 cycles for the whole instruction.  The
   // scale is a power of two, chosen per item so that a tile's sum cannot overflow: |dS| <= 1.1 |dP|,
-  // |dP| <= 128 max|dout row of the item| max|v|, and a diagonal meets at most 64 pairs of a
-  // (128-row, 64-key) tile.  What the conversion drops is below 2^-30 of that bound per pair.
+  // |dP| <= 128 max|dout row of the item| max|v| (times the largest per-token scale of the item's rows,
+  // where there is one), and a diagonal meets at most 64 pairs of a (128-row, 64-key) tile.  What the conversion drops is below 2^-30 of that bound per pair.
   // Non-finite inputs make the scale zero and every flushed value NaN.
-  constexpr bool FIXED = RAB_GRAD && !PER_TOKEN;
+  constexpr bool FIXED = RAB_GRAD;
   __shared__ unsigned do_max_s[4];  // per wave: largest |dout| magnitude of its rows of the item
+  __shared__ float rs_max_s[4];     // per wave: largest |per-token scale| of its rows
   float fx_scale = 0.f, fx_inv = 0.f;
 
   const int xcd = blockIdx.x % NUM_XCD;
@@ -296,7 +296,12 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       unsigned mx = bwd_frag_absmax(gf);
 #pragma unroll
       for (int d = 32; d >= 1; d >>= 1) mx = max(mx, (unsigned)__shfl_xor((int)mx, d, 64));
-      if (lane == 0) do_max_s[wave] = mx;
+      float rs = per_token ? __builtin_fabsf(row_scale) : 1.0f;
+      if (per_token) {
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) rs = fmaxf(rs, __shfl_xor(rs, d, 64));
+      }
+      if (lane == 0) { do_max_s[wave] = mx; rs_max_s[wave] = rs; }
     }
     const float score_c = p.alpha * kLog2e, neg_c = -score_c;
     // the bias is staged multiplied by log2(e) and joins the score in the multiply-add that applies alpha log2(e)
@@ -378,50 +383,6 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
 #pragma unroll
           for (int r = 0; r < 16; ++r)
             __hip_atomic_fetch_add(gi + (kvb * 32 + 8 * (r >> 2) + (r & 3)), (int)(ds[r] * fx_scale), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        } else if constexpr (RAB_GRAD) {
-          const unsigned gaddr = (unsigned)(size_t)(BUF ? gband1 : gband0) + band_lane;
-          // Element 4 g + i of lane l (query row l, key 8 g + i of its half) lies on diagonal i - l: the four
-          // elements of lanes l .. l + 3 with i = 0 .. 3 share one.  They are summed across lanes first
-          // (three shifted additions inside a row of 16 lanes; a_k of lane l collects i - l' = k - l), so
-          // a lane adds one value per group to the band instead of four, and the first lane of each row
-          // also adds the three partial sums whose left neighbours are in another row.  The LDS additions
-          // were what this gradient cost: 1024 lane operations per block before, 208 with both stages.
-          float a0s[4], a1s[4], a2s[4], a3s[4];
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            auto shl1 = [](float x) {  // lane l receives the value of lane l + 1 of its row, the last lane 0
-              return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x101, 0xf, 0xf, true));
-            };
-            const float a3 = ds[4 * g4 + 3];
-            const float a2 = ds[4 * g4 + 2] + shl1(a3);
-            const float a1 = ds[4 * g4 + 1] + shl1(a2);
-            const float a0 = ds[4 * g4 + 0] + shl1(a1);
-            a1s[g4] = a1; a2s[g4] = a2; a3s[g4] = a3; a0s[g4] = a0;
-          }
-          // Group g + 1 of lane l + 8 lies on the diagonals of group g of lane l: lanes 0 .. 7 of a row take
-          // them over, and lanes 8 .. 15 are left with their group 0 only.
-          {
-            auto shl8 = [](float x) {
-              return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x108, 0xf, 0xf, true));
-            };
-            const float c0 = a0s[0] + shl8(a0s[1]), c1 = a0s[1] + shl8(a0s[2]), c2 = a0s[2] + shl8(a0s[3]);
-            if ((lane & 8) == 0) {
-              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 0)), c0, 0, 0, false);
-              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8)), c1, 0, 0, false);
-              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 16)), c2, 0, 0, false);
-              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 24)), a0s[3], 0, 0, false);
-            } else {
-              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 0)), a0s[0], 0, 0, false);
-            }
-          }
-          if ((lane & 15) == 0) {
-#pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8 * g4 + 1)), a1s[g4], 0, 0, false);
-              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8 * g4 + 2)), a2s[g4], 0, 0, false);
-              __builtin_amdgcn_ds_faddf((lds_float*)(gaddr + 4u * (unsigned)(kvb * 32 + 8 * g4 + 3)), a3s[g4], 0, 0, false);
-            }
-          }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -478,8 +439,9 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       if constexpr (FIXED) {
         if (prev_tile < 0) {  // first tile of the item: the fixed-point scale of its diagonal sums
           const unsigned dmx = max(max(do_max_s[0], do_max_s[1]), max(do_max_s[2], do_max_s[3]));
+          const float rmx = fmaxf(fmaxf(rs_max_s[0], rs_max_s[1]), fmaxf(rs_max_s[2], rs_max_s[3]));
           const float bound = __uint_as_float(dmx << 16) * __uint_as_float(__hip_atomic_load(bp.absmax + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) *
-                              (128.0f * 1.1f * 64.0f);
+                              rmx * (128.0f * 1.1f * 64.0f);
           const int eb = (int)((__float_as_uint(bound) >> 23) & 0xffu) - 126;  // bound < 2^eb
           const bool usable = bound > 0.f && bound < 3.0e38f;
           const int sh = min(max(30 - eb, -120), 120);
