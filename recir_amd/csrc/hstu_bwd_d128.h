@@ -181,11 +181,11 @@ __device__ __forceinline__ void bwd_band_store(float* band, float val, int tid, 
 // HAS_RAB: scores carry the relative bias rab[h, query - key + N - 1] (no gradient flows to it).
 // PER_TOKEN: the output scale is a [T] vector; P and dS of query row m carry attn_scale[m].
 // RAB_GRAD (with HAS_RAB): also the gradient of the bias table, drab[h, m - j + N - 1] += dS(m, j).
-//   The dS of a tile are added into an LDS band with the bias band's own indexing (ds_add_f32; the
-//   elements one instruction adds lie on different diagonals up to a two-way overlap of the lane
-//   halves), and the band of a finished tile is flushed to global memory with one float atomic
-//   per diagonal while the next tile computes into the other stage.  Sums of floats in
-//   arrival order: not bitwise reproducible, unlike dq, dk and dv.
+//   The dS of a tile are added, as fixed-point integers, into an LDS band with the bias band's own
+//   indexing (ds_add_u32; the elements one instruction adds lie on different diagonals up to a
+//   two-way overlap of the lane halves), and the band of a finished tile is flushed to global
+//   memory with one float atomic per diagonal while the next tile computes into the other stage.
+//   The flush sums floats in arrival order: not bitwise reproducible, unlike dq, dk and dv.
 template <bool SEMI, bool HAS_RAB, bool PER_TOKEN, bool RAB_GRAD = false>
 __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp) {
   const Params& p = bp.f;
