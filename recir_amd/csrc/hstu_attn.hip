@@ -186,9 +186,19 @@ __global__ __launch_bounds__(256) void hstu_calibration_copy(u32x4* dst, const u
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
 }
 
+// n2 two-byte words := 0: 16-byte stores for the aligned middle, two-byte stores for what is left at
+// either end
 __global__ void hstu_fill_zero(unsigned short* out, size_t n2) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n2; i += stride) out[i] = 0;
+  const size_t first = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t head = (size_t)((16 - ((size_t)out & 15)) & 15) / 2;  // words before the first 16-byte boundary
+  if (head > n2) head = n2;
+  const size_t n16 = (n2 - head) / 8;
+  u32x4* mid = (u32x4*)(out + head);
+  for (size_t i = first; i < n16; i += stride) mid[i] = u32x4{0u, 0u, 0u, 0u};
+  const size_t tail0 = head + n16 * 8;
+  for (size_t i = first; i < head; i += stride) out[i] = 0;
+  for (size_t i = tail0 + first; i < n2; i += stride) out[i] = 0;
 }
 
 // ---------------------------------------------------------------------------------------------
