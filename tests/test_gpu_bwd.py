@@ -345,9 +345,11 @@ def _random_case(seed):
     with_rab = bool(rng.random() < 0.4)
     scale_kind = str(rng.choice(["default", "scalar", "per_token"]))
     N = max(max(lengths), 1) + int(rng.integers(0, 9))
+    # (seeds from 24 on also draw the mask type; the first 24 keep the cases they always had)
+    mask_type = "full" if seed >= 24 and rng.random() < 0.2 else "lower_triangular"
     wl = make_jagged(lengths, targets, H, 128, 128, max_seq_len=N, alpha=1.0 / 128, dtype="bf16", seed=seed,
                      contextual_seq_len=ctx, tail_rows=int(rng.integers(0, 4)), max_attn_len=A, full_attn_size=F,
-                     with_rab=with_rab, rab_std=0.5)
+                     with_rab=with_rab, rab_std=0.5, mask_type=mask_type)
     g = torch.Generator().manual_seed(seed)
     scale = None
     if scale_kind == "scalar":
@@ -358,7 +360,7 @@ def _random_case(seed):
     return wl, scale, dout
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(48))
 def test_randomized_cases_forward_and_backward(oracle, seed):
     """Forward and backward of the tiled kernels against the oracle on seeded random cases."""
     from recir_amd import _lib
@@ -366,20 +368,21 @@ def test_randomized_cases_forward_and_backward(oracle, seed):
 
     wl, scale, dout = _random_case(seed)
     what = (f"seed {seed}: lengths {wl.lengths.tolist()} targets {wl.num_targets.tolist()} H {wl.H} ctx "
-            f"{wl.contextual_seq_len} A {wl.max_attn_len} F {wl.full_attn_size} rab {wl.rab is not None}")
+            f"{wl.contextual_seq_len} A {wl.max_attn_len} F {wl.full_attn_size} rab {wl.rab is not None} mask {wl.mask_type}")
+    causal = wl.mask_type == "lower_triangular"
     out = run_hip(wl, attn_scale=scale)
     if wl.T:
-        assert _lib.last_kernel().startswith("tiled_d128"), what
+        assert _lib.last_kernel().startswith("tiled_d128" if causal else "generic"), what
     assert_bf16_close(out, run_oracle(oracle, wl, attn_scale=scale), what)
     want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
                            wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
                            attn_scale=_scale_np(scale), rab=None if wl.rab is None else wl.rab.numpy(),
                            contextual_seq_len=wl.contextual_seq_len, max_attn_len=wl.max_attn_len,
-                           full_attn_size=wl.full_attn_size)
+                           full_attn_size=wl.full_attn_size, mask_type=wl.mask_type)
     got = run_hip_bwd(wl, dout, attn_scale=scale, rab=wl.rab)
     if wl.T:
-        assert _lib.last_kernel().startswith("bwd_tiled_d128"), what
-    if np.abs(want[0]).max() > 0:
+        assert _lib.last_kernel().startswith("bwd_tiled_d128" if causal else "bwd_generic"), what
+    if want[0].size and np.abs(want[0]).max() > 0:
         assert_grads_close(got, want, int(wl.seq_offsets[-1]), BF16_REL, what)
 
 
