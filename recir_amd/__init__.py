@@ -18,6 +18,7 @@ from .ops import (  # noqa: F401
     set_plan_cache,
     hstu_attention_matcher,
     attention_via_fp8,
+    attention_via_fp8_reference_rule,
     fp8_attention_region,
     KERNEL_AUTO,
     KERNEL_GENERIC,
@@ -49,5 +50,6 @@ __all__ = [
     "set_plan_cache",
     "hstu_attention_matcher",
     "attention_via_fp8",
+    "attention_via_fp8_reference_rule",
     "fp8_attention_region",
 ]

@@ -28,62 +28,64 @@ KERNEL_GENERIC = 1
 KERNEL_TILED = 2         # tiled MFMA kernel, K/V staged through registers
 KERNEL_TILED_DIRECT = 3  # tiled MFMA kernel, K/V copied global -> LDS directly
 
-_forced_kernel = KERNEL_AUTO
-_extra_flags = 0
-_ctx_reference_rule = False
+class _CallState(threading.local):
+    """Per-thread switches the context managers below set and every launch reads: a thread that
+    enters ``reference_contextual_rule()`` or ``force_kernel()`` changes its own calls only."""
+
+    forced_kernel = KERNEL_AUTO
+    extra_flags = 0
+    ctx_reference_rule = False
+
+
+_state = _CallState()
 
 
 class extra_flags:
-    """Context manager for tests and tuning: C-ABI flag bits added to every call (for example
-    ``_lib.FLAG_GROUPED_LISTS``)."""
+    """Context manager for tests and tuning: C-ABI flag bits added to every call of this thread
+    (for example ``_lib.FLAG_GROUPED_LISTS``)."""
 
     def __init__(self, flags: int):
         self.flags = int(flags)
 
     def __enter__(self):
-        global _extra_flags
-        self._prev = _extra_flags
-        _extra_flags = self._prev | self.flags
+        self._prev = _state.extra_flags
+        _state.extra_flags = self._prev | self.flags
         return self
 
     def __exit__(self, *exc):
-        global _extra_flags
-        _extra_flags = self._prev
+        _state.extra_flags = self._prev
         return False
 
 
 class force_kernel:
-    """Context manager for tests and tuning: pin the kernel variant the C ABI selects."""
+    """Context manager for tests and tuning: pin the kernel variant the C ABI selects (calls of
+    this thread)."""
 
     def __init__(self, variant: int):
         self.variant = int(variant)
 
     def __enter__(self):
-        global _forced_kernel
-        self._prev = _forced_kernel
-        _forced_kernel = self.variant
+        self._prev = _state.forced_kernel
+        _state.forced_kernel = self.variant
         return self
 
     def __exit__(self, *exc):
-        global _forced_kernel
-        _forced_kernel = self._prev
+        _state.forced_kernel = self._prev
         return False
 
 
 class reference_contextual_rule:
     """Context manager: use the contextual-prefix rule of the reference C++ fallback
     (kjt_split_per_feature.cpp:672-674: keys whose target-clamped id is 0 are visible to all)
-    instead of "keys j < contextual_seq_len are visible to all"."""
+    instead of "keys j < contextual_seq_len are visible to all", for the calls of this thread."""
 
     def __enter__(self):
-        global _ctx_reference_rule
-        self._prev = _ctx_reference_rule
-        _ctx_reference_rule = True
+        self._prev = _state.ctx_reference_rule
+        _state.ctx_reference_rule = True
         return self
 
     def __exit__(self, *exc):
-        global _ctx_reference_rule
-        _ctx_reference_rule = self._prev
+        _state.ctx_reference_rule = self._prev
         return False
 
 
@@ -96,7 +98,8 @@ _SCHEMA = (
 _FP8_SCHEMA = (
     "hstu_jagged_attention_fp8_fwd(int N, float alpha, Tensor q_fp8, Tensor k_fp8, Tensor v, "
     "Tensor q_scale, Tensor k_scale, Tensor seq_offsets, Tensor? num_targets, Tensor? attn_scale, "
-    "int contextual_seq_len, Tensor? rab=None, int max_attn_len=0, int full_attn_size=0) -> (Tensor, Tensor)"
+    "int contextual_seq_len, Tensor? rab=None, int max_attn_len=0, int full_attn_size=0, "
+    "bool reference_contextual_rule=False) -> (Tensor, Tensor)"
 )
 _QUANT_SCHEMA = "hstu_quantize_e4m3_per_head(Tensor x, Tensor? seq_offsets=None) -> (Tensor, Tensor)"
 _BWD_SCHEMA = (
@@ -194,10 +197,10 @@ def _prepare(opname, q, k, v, seq_offsets, num_targets, attn_scale, rab, N, ctx_
     B = _check_common(q, k, v, seq_offsets, num_targets, N)
     T, H, _ = q.shape
     off, nt, flags = _index_tensors(seq_offsets, num_targets, dev)
-    if _ctx_reference_rule or ctx_reference:
+    if _state.ctx_reference_rule or ctx_reference:
         flags |= _lib.FLAG_CTX_REFERENCE
-    flags |= (_forced_kernel & 0xFF) << _lib.FLAG_KERNEL_SHIFT
-    flags |= _extra_flags
+    flags |= (_state.forced_kernel & 0xFF) << _lib.FLAG_KERNEL_SHIFT
+    flags |= _state.extra_flags
     if mask_type != "lower_triangular":
         # any other string selects the reference's other branch (kjt_split_per_feature.cpp:650-660)
         flags |= _lib.FLAG_MASK_NONCAUSAL
@@ -429,7 +432,10 @@ def _ref_bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scal
 
 
 def _fp8_fwd_device(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, num_targets,
-                    attn_scale, contextual_seq_len, rab=None, max_attn_len=0, full_attn_size=0):
+                    attn_scale, contextual_seq_len, rab=None, max_attn_len=0, full_attn_size=0,
+                    reference_contextual_rule=False):
+    # reference_contextual_rule: the rule of the reference operator (keys whose target-clamped id is
+    # 0, kjt_split_per_feature.cpp:672-674) instead of "keys j < contextual_seq_len"
     ok = (torch.float8_e4m3fn, torch.uint8)
     if q_fp8.dtype not in ok or k_fp8.dtype not in ok:
         raise ValueError("q_fp8 and k_fp8 must be float8_e4m3fn (or its uint8 bytes)")
@@ -443,7 +449,7 @@ def _fp8_fwd_device(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, nu
     ks = k_scale.to(device=v.device, dtype=torch.float32).contiguous()
     out = _launch(q_fp8.view(torch.uint8), k_fp8.view(torch.uint8), v, seq_offsets, num_targets,
                   attn_scale, rab, qs, ks, N, alpha, contextual_seq_len, _lib.DTYPE_FP8_E4M3,
-                  max_attn_len, full_attn_size)
+                  max_attn_len, full_attn_size, bool(reference_contextual_rule))
     return out, torch.zeros((1,), dtype=torch.float32, device=v.device)
 
 
@@ -517,7 +523,8 @@ def _ref_bwd_fake(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale,
 
 @torch.library.register_fake("recir::hstu_jagged_attention_fp8_fwd")
 def _fp8_fwd_fake(N, alpha, q_fp8, k_fp8, v, q_scale, k_scale, seq_offsets, num_targets, attn_scale,
-                  contextual_seq_len, rab=None, max_attn_len=0, full_attn_size=0):
+                  contextual_seq_len, rab=None, max_attn_len=0, full_attn_size=0,
+                  reference_contextual_rule=False):
     _check_common(q_fp8, k_fp8, v, seq_offsets, num_targets, N)
     return v.new_empty((q_fp8.shape[0], q_fp8.shape[1], v.shape[2])), v.new_empty((1,), dtype=torch.float32)
 
@@ -680,28 +687,30 @@ def jagged_hstu_attention_fp8(q, k, v, seq_offsets, num_targets=None, *, max_seq
     return out
 
 
+def _reference_rule_targets():
+    """Operators whose contextual rule is the reference's (kjt_split_per_feature.cpp:672-674): the
+    reference's own ``hammer::`` operator when it is loaded, and this package's drop-in for it."""
+    targets = [triton_ragged_attention_fwd, triton_ragged_attention_fwd.default]
+    try:
+        src = torch.ops.hammer.triton_ragged_attention_fwd
+        targets += [src, src.default]
+    except (AttributeError, RuntimeError):
+        pass
+    return targets
+
+
 def hstu_attention_matcher(node) -> bool:
     """``OpMatcher`` of RecIR's training-to-inference swap
     (recir/region_transforms/inference_swap.py:73-77): true for a graph node that calls the HSTU
     attention operator, under this package's name or the reference's."""
     if node.op != "call_function":
         return False
-    targets = [hstu_jagged_attention_fwd, hstu_jagged_attention_fwd.default,
-               triton_ragged_attention_fwd, triton_ragged_attention_fwd.default]
-    try:
-        src = torch.ops.hammer.triton_ragged_attention_fwd
-        targets += [src, src.default]
-    except (AttributeError, RuntimeError):
-        pass
+    targets = [hstu_jagged_attention_fwd, hstu_jagged_attention_fwd.default] + _reference_rule_targets()
     return any(node.target is t for t in targets)
 
 
-def attention_via_fp8(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
-                      max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads=0, rab=None):
-    """The attention operator's positional signature, computed with q and k quantised per head to
-    fp8 e4m3 (v, the accumulation and the output stay as they are).  Module level on purpose: it
-    becomes a ``call_function`` target of the inference graph, and a saved GraphModule names its
-    targets by qualified name (recir/region_transforms/inference_swap.py:89-104)."""
+def _via_fp8(reference_rule, N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
+             max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads, rab):
     if num_softmax_heads != 0:
         raise ValueError("softmax attention heads are unsupported")
     if invalid_attn_mask_type != "lower_triangular":
@@ -710,13 +719,35 @@ def attention_via_fp8(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, nu
     k8, ks = quantize_e4m3_per_head(k, seq_offsets)
     return torch.ops.recir.hstu_jagged_attention_fp8_fwd(
         int(N), float(alpha), q8, k8, v, qs, ks, seq_offsets, num_targets, attn_scale,
-        int(contextual_seq_len), rab, int(max_attn_len), int(full_attn_size))
+        int(contextual_seq_len), rab, int(max_attn_len), int(full_attn_size), bool(reference_rule))
+
+
+def attention_via_fp8(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
+                      max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads=0, rab=None):
+    """The positional signature of ``recir::hstu_jagged_attention_fwd`` and its contextual rule (keys
+    ``j < contextual_seq_len``), computed with q and k quantised per head to fp8 e4m3 (v, the
+    accumulation and the output stay as they are).  Module level on purpose: it becomes a
+    ``call_function`` target of the inference graph, and a saved GraphModule names its targets by
+    qualified name (recir/region_transforms/inference_swap.py:89-104)."""
+    return _via_fp8(False, N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
+                    max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads, rab)
+
+
+def attention_via_fp8_reference_rule(N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets,
+                                     attn_scale, max_attn_len, contextual_seq_len, full_attn_size,
+                                     num_softmax_heads=0):
+    """The same for a node that called the reference's operator (``hammer::`` or
+    ``recir::triton_ragged_attention_fwd``): its signature (no bias) and its contextual rule, keys
+    whose target-clamped id is 0 (recir/ops/kjt_split_per_feature.cpp:672-674), so that the swapped
+    node keeps the set of pairs of the node it replaces for every ``contextual_seq_len``."""
+    return _via_fp8(True, N, alpha, q, k, v, seq_offsets, invalid_attn_mask_type, num_targets, attn_scale,
+                    max_attn_len, contextual_seq_len, full_attn_size, num_softmax_heads, None)
 
 
 class Fp8AttentionRegion:
     """Callable the factory below returns.  It is spliced into the host graph as a ``call_function``
     target (recir/region_transforms/core.py:358-362), which needs a ``__name__``; it holds a copy of
-    the region in which every attention node runs ``attention_via_fp8``.  It pickles by value (the
+    the region in which every attention node runs ``attention_via_fp8`` (or its reference-rule twin).  It pickles by value (the
     class and the rewritten region are importable); a host graph that names it as a target can be
     run, not re-loaded from a file in another process."""
 
@@ -739,7 +770,9 @@ def fp8_attention_region(region_gm):
     hits = 0
     for node in gm.graph.nodes:
         if hstu_attention_matcher(node):
-            node.target = attention_via_fp8
+            # the replacement keeps the contextual rule of the operator the node called
+            by_reference_rule = any(node.target is t for t in _reference_rule_targets())
+            node.target = attention_via_fp8_reference_rule if by_reference_rule else attention_via_fp8
             hits += 1
     if hits == 0:
         raise ValueError("the region holds no HSTU attention node")

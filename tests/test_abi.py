@@ -207,6 +207,61 @@ def test_fake_kernel_and_schema():
         assert aux.shape == (1,) and aux.dtype == torch.float32
 
 
+def test_every_registered_operator_has_a_meta_kernel():
+    """RecIR's lowering keeps a custom operator inside a lowered region only if FakeTensorMode can run
+    it; its predicate (recir/lowering/lowering_utils.py:19-27) is the computed dispatch table's entry
+    for the Meta key.  Evaluated here for every operator this package defines in ``recir::``."""
+    import recir_amd  # noqa: F401
+
+    names = [n for n in torch._C._dispatch_get_all_op_names() if n.startswith("recir::")]
+    # the attention family, the quantiser and the jagged neighbours
+    for must in ("recir::hstu_jagged_attention_fwd", "recir::hstu_jagged_attention_bwd",
+                 "recir::hstu_jagged_attention_bwd_rab", "recir::triton_ragged_attention_fwd",
+                 "recir::triton_ragged_attention_bwd", "recir::hstu_jagged_attention_fp8_fwd",
+                 "recir::hstu_quantize_e4m3_per_head", "recir::concat_2d_jagged", "recir::split_2d_jagged"):
+        assert must in names, must
+    assert len(names) >= 12, names
+    for name in names:
+        assert torch._C._dispatch_has_computed_kernel_for_dispatch_key(name, "Meta"), name
+
+
+def test_fp8_region_follows_the_contextual_rule_of_the_matched_operator():
+    """A region cut around ``recir::triton_ragged_attention_fwd`` (the drop-in for the reference's
+    operator, whose contextual rule is recir/ops/kjt_split_per_feature.cpp:672-674) is rewritten to
+    the reference-rule fp8 entry, one around ``recir::hstu_jagged_attention_fwd`` to the prefix-rule
+    one; the fp8 operator's schema carries the switch."""
+    import torch.fx as fx
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    import recir_amd
+
+    assert "bool reference_contextual_rule=False" in str(torch.ops.recir.hstu_jagged_attention_fp8_fwd.default._schema)
+    for op, via in ((recir_amd.triton_ragged_attention_fwd.default, recir_amd.attention_via_fp8_reference_rule),
+                    (recir_amd.hstu_jagged_attention_fwd.default, recir_amd.attention_via_fp8)):
+        def f(q, k, v, off, nt):
+            return op(16, 0.25, q, k, v, off, "lower_triangular", nt, None, 0, 4, 0)[0]
+
+        q, k, v = (torch.empty(12, 2, 128, dtype=torch.bfloat16) for _ in range(3))
+        gm = make_fx(f, tracing_mode="fake")(q, k, v, torch.empty(3, dtype=torch.int64), torch.empty(2, dtype=torch.int64))
+        node = next(n for n in gm.graph.nodes if recir_amd.hstu_attention_matcher(n))
+        region = fx.Graph()
+        env = {a: region.placeholder(a.name) for a in node.args if isinstance(a, fx.Node)}
+        region.output(region.node_copy(node, lambda n: env[n]))
+        run = recir_amd.fp8_attention_region(fx.GraphModule(torch.nn.Module(), region))
+        calls = [n for n in run.gm.graph.nodes if n.op == "call_function" and callable(n.target)
+                 and getattr(n.target, "__module__", "") == "recir_amd.ops"]
+        assert [c.target for c in calls] == [via]
+        assert calls[0].args[10] == 4  # contextual_seq_len travels unchanged
+        # traces with fake tensors end to end (quantiser and fp8 operator both have Meta kernels)
+        from torch._subclasses.fake_tensor import FakeTensorMode
+
+        with FakeTensorMode():
+            qf = torch.empty(12, 2, 128, dtype=torch.bfloat16)
+            out = via(16, 0.25, qf, qf, qf, torch.empty(3, dtype=torch.int64), "lower_triangular",
+                      torch.empty(2, dtype=torch.int64), None, 0, 4, 0)[0]
+            assert out.shape == (12, 2, 128)
+
+
 def test_swap_registry_retargets_a_traced_node():
     """swap_ops rewrites node.target only (recir/lowering/op_swap.py:78-97): the replacement must
     accept the source operator's positional arguments unchanged."""

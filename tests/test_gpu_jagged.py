@@ -63,7 +63,7 @@ def test_pad_and_unpad(tail, dtype, off_dtype):
     np.testing.assert_array_equal(_np(got), jo.dense_to_jagged(_np(narrow), off))
 
 
-@pytest.mark.parametrize("tail,dtype", CASES)
+@pytest.mark.parametrize("tail,dtype", [c for c in CASES if len(c[0]) > 0])  # the 2-D operators take [rows, D] values
 @pytest.mark.parametrize("npre", [0, 2])
 def test_concat_and_split(tail, dtype, npre):
     import recir_amd
@@ -75,8 +75,6 @@ def test_concat_and_split(tail, dtype, npre):
     a, b = _values(rng, int(oa[-1]), tail, dtype), _values(rng, int(ob[-1]), tail, dtype)
     ad, bd = a.to(DEV), b.to(DEV)
     oad, obd = torch.tensor(oa, device=DEV), torch.tensor(ob, device=DEV)
-    if a.dim() < 2:
-        pytest.skip("the 2-D operators take [rows, D] values")
     cat = recir_amd.concat_2D_jagged_fwd(16, ad, bd, oad, obd, False, npre)
     want = jo.concat_2d_jagged(_np(a), _np(b), oa, ob, False, npre)
     np.testing.assert_array_equal(_np(cat), want)

@@ -531,6 +531,58 @@ def test_fp8_region_swap_in_a_traced_graph(oracle):
     assert error_stats(ref_bf16, want)["rel_fro"] <= 2e-2
 
 
+def test_fp8_region_swap_keeps_the_reference_contextual_rule(oracle):
+    """A node that calls the reference's operator with ``contextual_seq_len = 4`` means "keys whose
+    target-clamped id is 0" (kjt_split_per_feature.cpp:672-674): key 0, or every key of a sequence
+    that is all targets.  The fp8 region built from it must keep that rule, not the prefix rule of
+    ``recir::hstu_jagged_attention_fwd`` -- checked against the oracle in the reference's mode on the
+    dequantised operands; the same inputs under the prefix rule differ, so the test tells them apart."""
+    import torch.fx as fx
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    import recir_amd
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    # sequences 1 and 3 are all targets (cap = 0): there the two rules keep different pairs
+    wl = make_jagged([200, 70, 5, 131, 9], [16, 70, 0, 131, 2], 2, 128, 128, max_seq_len=256, alpha=1.0 / 128,
+                     dtype="bf16", seed=37, tail_rows=2)
+    q, k, v, off, nt = to_device(wl)
+    ctx = 4
+    for op, rule, via in ((recir_amd.triton_ragged_attention_fwd.default, oracle.CTX_REFCPP,
+                           recir_amd.attention_via_fp8_reference_rule),
+                          (recir_amd.hstu_jagged_attention_fwd.default, oracle.CTX_PREFIX,
+                           recir_amd.attention_via_fp8)):
+        def f(q, k, v, off, nt):
+            out, _aux = op(wl.max_seq_len, wl.alpha, q, k, v, off, "lower_triangular", nt, None, 0, ctx, 0)
+            return out
+
+        gm = make_fx(f, tracing_mode="fake")(q, k, v, off, nt)
+        node = next(n for n in gm.graph.nodes if recir_amd.hstu_attention_matcher(n))
+        region = fx.Graph()
+        env = {a: region.placeholder(a.name) for a in node.args if isinstance(a, fx.Node)}
+        region.output(region.node_copy(node, lambda n: env[n]))
+        run = recir_amd.fp8_attention_region(fx.GraphModule(torch.nn.Module(), region))
+        calls = [n for n in run.gm.graph.nodes if n.op == "call_function" and n.target in (
+            recir_amd.attention_via_fp8, recir_amd.attention_via_fp8_reference_rule)]
+        assert len(calls) == 1 and calls[0].target is via
+        got = run(q, k, v, off, nt)[0]
+        torch.cuda.synchronize()
+        assert _lib.last_kernel().startswith("tiled_d128_fp8qk")
+        q8, qs = oracle.quant_e4m3_per_head(wl.q.numpy())
+        k8, ks = oracle.quant_e4m3_per_head(wl.k.numpy())
+        qd = torch.from_numpy(oracle.e4m3_decode(q8) * qs.reshape(1, -1, 1))
+        kd = torch.from_numpy(oracle.e4m3_decode(k8) * ks.reshape(1, -1, 1))
+        want = run_oracle(oracle, wl, q=qd, k=kd, ctx=ctx, ctx_mode=rule)
+        other = run_oracle(oracle, wl, q=qd, k=kd, ctx=ctx, ctx_mode=1 - rule)
+        assert np.abs(want - other).max() > 1e-3  # the two rules differ on these inputs
+        assert_bf16_close(got, want, f"fp8 region, contextual rule {rule}")
+        assert_same_zero_structure(got, want, int(wl.seq_offsets[-1]))
+        # and the unquantised graph it replaced, against the fp32 oracle at the fp8 tolerance
+        st = error_stats(got, run_oracle(oracle, wl, ctx=ctx, ctx_mode=rule))
+        assert st["max_abs"] <= FP8_MAX_ABS, st
+
+
 def test_semilocal_full_size_matches_oracle(oracle):
     """Configuration 2 with the reference's semi-local shape (256 local + 256 full tail): the tiled
     kernel (which skips key tiles below the window) against the oracle."""

@@ -154,14 +154,9 @@ def _attention_fn(N, alpha, nt_targets=True):
     return f
 
 
-@pytest.mark.gpu
-@pytest.mark.timeout(600)
-def test_operator_under_torch_compile_fullgraph_forward_and_backward():
-    """``torch.compile(fullgraph=True)`` of pointwise -> attention -> pointwise: no graph break, and
-    forward and gradients equal to eager bit for bit (the operator is one opaque node with a Meta
-    kernel and an autograd formula; Inductor generates code only for the pointwise ops around it).
-    Falls back to ``backend="aot_eager"`` (AOTAutograd without code generation) where Inductor cannot
-    generate code on the box, and says so."""
+def _compiled_against_eager(backend):
+    """pointwise -> attention -> pointwise under ``torch.compile(fullgraph=True, backend=...)``: no
+    graph break; forward and gradients against eager.  An exception from the backend propagates."""
     import torch._dynamo as dynamo
 
     import recir_amd  # noqa: F401
@@ -188,17 +183,9 @@ def test_operator_under_torch_compile_fullgraph_forward_and_backward():
     explanation = dynamo.explain(f)(q, k, v, off, nt)
     assert explanation.graph_break_count == 0 and explanation.graph_count == 1, str(explanation)
     dynamo.reset()
-    backend = "inductor"
-    try:
-        got = run(torch.compile(f, fullgraph=True, backend=backend))
-    except Exception as e:  # no code generator for the pointwise kernels on this box
-        print(f"[compile] inductor unavailable ({type(e).__name__}: {str(e)[:200]}); using aot_eager", flush=True)
-        dynamo.reset()
-        backend = "aot_eager"
-        got = run(torch.compile(f, fullgraph=True, backend=backend))
-    print(f"[compile] backend {backend}", flush=True)
-    names = ("out", "dq", "dk", "dv")
-    for name, a, b in zip(names, got, want):
+    got = run(torch.compile(f, fullgraph=True, backend=backend))
+    dynamo.reset()
+    for name, a, b in zip(("out", "dq", "dk", "dv"), got, want):
         if name == "out" or backend == "aot_eager":
             assert torch.equal(a, b), name
         else:
@@ -207,6 +194,21 @@ def test_operator_under_torch_compile_fullgraph_forward_and_backward():
             # to a tolerance of one bf16 ulp of the largest value instead of bit for bit
             assert (a.float() - b.float()).abs().max().item() <= 2 ** -7 * b.float().abs().max().item(), name
     assert got[0].abs().sum().item() > 0 and got[1].abs().sum().item() > 0
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(600)
+def test_operator_under_torch_compile_inductor_fullgraph_forward_and_backward():
+    """The operator is one opaque node with a Meta kernel and an autograd formula; Inductor generates
+    code only for the pointwise operations around it.  No fallback: if Inductor raises, this fails."""
+    _compiled_against_eager("inductor")
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(600)
+def test_operator_under_torch_compile_aot_eager_fullgraph_forward_and_backward():
+    """The same through AOTAutograd without code generation: bit for bit equal to eager."""
+    _compiled_against_eager("aot_eager")
 
 
 @pytest.mark.gpu
