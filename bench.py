@@ -40,6 +40,7 @@ def describe(wl, cfg):
         4: "config4: B=8, history Zipf(1.2) clipped [128,8064] + 128 targets, max_seq_len 8192, H=4, D=128, bf16",
         5: "config5: config2 with q,k in fp8 e4m3 (per-head scale amax/448), v bf16",
         6: "config6: config2 with the semi-local mask (max_attn_len 256, full_attn_size 256)",
+        7: "config7: 16 sequences of 4096 history tokens, no targets, H=4, D=128, bf16 (steady state: two workgroups per CU throughout)",
     }
     return names[cfg]
 
@@ -134,6 +135,229 @@ def steady_state_warmup(call, stream, min_ms=MIN_WARMUP_MS):
         torch.cuda.synchronize()
         spent += e0.elapsed_time(e1)
     return spent
+
+
+CAL_KINDS = {0: "mfma_only", 1: "tile_loop_plain", 2: "tile_loop_skewed"}
+CAL_PIECES = {0: "everything", 1: "no SiLU", 2: "no LDS fragment reads", 12: "no copies, no barrier", 14: "MFMAs and SiLU only"}
+
+
+class CalibrationLoops:
+    """The library's stand-alone loops (``recir_hstu_calibration_mfma_loop``): bf16 MFMAs alone, and
+    the forward's tile loop without any of its bookkeeping, on operands of the caller's choice.  One
+    launch = 512 workgroups (two per CU) x ``tiles`` key tiles; FLOPs = workgroups * tiles * 4 waves *
+    32 MFMAs * 32768."""
+
+    WORKGROUPS, SEQUENCES, SEQ_TILES = 512, 16, 32
+
+    def __init__(self, L, dev, alpha=1.0 / 128):
+        import torch
+
+        self.L, self.dev, self.alpha = L, dev, alpha
+        rows = self.SEQUENCES * self.SEQ_TILES * 64
+        g = torch.Generator().manual_seed(7)
+        self.rows = rows
+        self.random = [torch.randn(rows, 4, 128, generator=g).to(torch.bfloat16).to(dev) for _ in range(3)]
+        self.zeros = [torch.zeros(rows, 4, 128, dtype=torch.bfloat16, device=dev) for _ in range(3)]
+        self.stats = torch.zeros(self.WORKGROUPS, 4, dtype=torch.int64, device=dev)
+        self.sink = torch.empty(self.WORKGROUPS * 256, dtype=torch.float32, device=dev)
+        self.stream = torch.cuda.current_stream(dev)
+
+    def launch(self, kind, pieces, operands, tiles):
+        from recir_amd import _lib
+
+        k, v, q = self.random if operands == "random" else self.zeros
+        rc = self.L.recir_hstu_calibration_mfma_loop(kind, pieces, k.data_ptr(), v.data_ptr(), q.data_ptr(), self.rows,
+                                                     self.SEQUENCES, tiles, self.WORKGROUPS, self.alpha,
+                                                     self.stats.data_ptr(), self.sink.data_ptr(),
+                                                     ctypes.c_void_p(self.stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"recir_hstu_calibration_mfma_loop failed ({rc}): {_lib.last_error()}")
+
+    def measure(self, kind, pieces=0, operands="random", tiles=256, launches=20, min_warm_ms=30.0):
+        """Sustained rate of one loop: warm clocks first, then ``launches`` launches between two HIP
+        events on the launch stream; the shader clock from the counters the kernel itself reads."""
+        import numpy as np
+        import torch
+
+        spent = 0.0
+        while spent < min_warm_ms:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(self.stream)
+            for _ in range(5):
+                self.launch(kind, pieces, operands, tiles)
+            e1.record(self.stream)
+            torch.cuda.synchronize()
+            spent += e0.elapsed_time(e1)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(self.stream)
+        for _ in range(launches):
+            self.launch(kind, pieces, operands, tiles)
+        e1.record(self.stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / launches
+        st = self.stats.cpu().numpy().astype("float64")
+        flops = self.WORKGROUPS * tiles * 4 * 32 * 32768.0
+        # a tile round: the two workgroups of a CU each finish one 128-row x 64-key tile
+        return {"loop": CAL_KINDS[kind], "pieces": CAL_PIECES[pieces], "operands": operands, "tiles": tiles,
+                "ms_per_launch": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+                "ns_per_tile_round": ms * 1e6 / tiles,
+                "cycles_per_tile_round": float(st[:, 0].mean()) / tiles,
+                "sclk_mhz": float((st[:, 0] / st[:, 1].clip(min=1)).mean() * 100.0),
+                # when the workgroups' loops started and ended, in microseconds after the first start
+                "loop_start_us": {"median": float(np.median(st[:, 2] - st[:, 2].min()) / 100.0),
+                                  "max": float((st[:, 2].max() - st[:, 2].min()) / 100.0)},
+                "loop_end_us": {"min": float((st[:, 3].min() - st[:, 2].min()) / 100.0),
+                                "max": float((st[:, 3].max() - st[:, 2].min()) / 100.0)}}
+
+
+def bench_mfma_ceiling(args, L, dev):
+    """What the chip sustains: bf16 MFMAs alone and the forward's tile loop stand-alone (both
+    arrangements, random and zero operands, with pieces removed), next to the forward kernel itself
+    on 16 sequences of 4,096 (its steady state: every CU holds two workgroups throughout) and on
+    configuration 2."""
+    cal = CalibrationLoops(L, dev)
+    rows = []
+    for operands in ("random", "zeros"):
+        rows.append(cal.measure(0, 0, operands))
+    for kind in (1, 2):
+        for operands in ("random", "zeros"):
+            rows.append(cal.measure(kind, 0, operands))
+        for pieces in (1, 2, 12, 14):
+            rows.append(cal.measure(kind, pieces, "random"))
+    print(json.dumps({"metric": "sustained bf16 MFMA rate of the calibration loops", "unit": "TFLOP/s", "n_gpus": 1,
+                      "peak": PEAK_TFLOPS["bf16"], "workgroups": cal.WORKGROUPS, "loops": rows}))
+
+
+def bench_phase_trace(args, wl, dev):
+    """Where the forward kernel's time goes, from the phase-trace build of the library (the same sources
+    with -DHSTU_TRACE: every wave stamps the 100 MHz counter at the phases of every work item).  The
+    figures are slot time -- a CU holds two workgroups, the chip 512 -- divided by 512, so that the rows
+    add up to the span of the launch."""
+    import numpy as np
+    import torch
+
+    from recir_amd import _lib, build
+
+    if not os.path.exists(build.TRACE_LIB_PATH):
+        print(f"{build.TRACE_LIB_PATH} not found: build it with `python -m recir_amd.build --trace`", file=sys.stderr)
+        sys.exit(2)
+    L = _lib.load()  # (main() pointed the loader at the trace build)
+    L.recir_hstu_trace_buffer.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    words = L.recir_hstu_trace_words_per_record()
+    q, k, v = (t.to(dev, torch.bfloat16) for t in (wl.q, wl.k, wl.v))
+    off, nt = wl.seq_offsets.to(dev), wl.num_targets.to(dev)
+    rab = None if wl.rab is None else wl.rab.to(dev)
+    T, H, D = q.shape
+    out = torch.empty_like(v)
+    ws = torch.empty((max(L.recir_hstu_attn_fwd_workspace_bytes(T, wl.B, H, D, D, _lib.DTYPE_BF16), 16),), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    items_cap = ((T + 127) // 128 + wl.B) * H
+    trace = torch.zeros(items_cap * 8 * 4 * words, dtype=torch.int64, device=dev)
+
+    def call(flags=0):
+        rc = L.recir_hstu_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), off.data_ptr(), nt.data_ptr(),
+                                   None if rab is None else rab.data_ptr(), None, None, None, T, wl.B, H, D, D, wl.max_seq_len,
+                                   wl.contextual_seq_len, wl.max_attn_len, wl.full_attn_size, wl.alpha, _lib.DTYPE_BF16, flags,
+                                   ws.data_ptr(), ws.numel(), ctypes.c_void_p(stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"recir_hstu_attn_fwd failed ({rc}): {_lib.last_error()}")
+
+    steady_state_warmup(call, stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(200):
+        call(_lib.FLAG_REUSE_PLAN)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    untraced_us = e0.elapsed_time(e1) / 200 * 1e3
+    L.recir_hstu_trace_buffer(trace.data_ptr(), trace.numel())
+    for _ in range(3):  # the last launch's records stay
+        call(_lib.FLAG_REUSE_PLAN)
+    torch.cuda.synchronize()
+    L.recir_hstu_trace_buffer(None, 0)
+    rec = trace.cpu().numpy().reshape(-1, 4, words).astype(np.float64)
+    rec = rec[rec[:, 0, 0] > 0]
+    n_items = len(rec)
+    tick_us = 0.01  # 100 MHz
+    start, ready = rec[:, :, 0].min(1), rec[:, :, 1].max(1)
+    loop_end, end = rec[:, :, 2].max(1), rec[:, :, 3].max(1)
+    t0, t1 = start.min(), end.max()
+    span = (t1 - t0) * tick_us
+    slots = 512.0
+    counts = rec[:, :, 9].astype(np.int64)
+    n_cls = np.stack([(counts >> (8 * i)) & 0xFF for i in range(5)], axis=-1)  # [items, waves, class]
+    ticks = rec[:, :, 4:9]  # [items, waves, class]
+    names = ("skewed trips", "leading unmasked tiles (plain loop)", "other unmasked tiles", "partial tiles", "tiles the wave skips")
+    rows = {}
+    rows["start-up (item record, query rows, first tile, first barrier)"] = (ready - start).sum() * tick_us / slots
+    for i, nm in enumerate(names):
+        rows[nm] = ticks[:, :, i].mean(1).sum() * tick_us / slots
+    in_loop = (loop_end - ready).sum() * tick_us / slots
+    rows["waiting for the slowest wave at the loop's end"] = in_loop - sum(rows[nm] for nm in names)
+    rows["epilogue (output rows)"] = (end - loop_end).sum() * tick_us / slots
+    occupied = (end - start).sum() * tick_us / slots
+    # idle slot time per CU: before its first item, between items, after its last item has started
+    hw = rec[:, 0, 10].astype(np.int64)
+    cu_key = ((hw >> 32) << 16) | ((hw >> 8) & 0xFF) | (((hw >> 13) & 7) << 8)
+    ramp = gaps = tail = 0.0
+    n_cus = 0
+
+    def overlap(a0, a1, b0, b1):
+        return max(0.0, min(a1, b1) - max(a0, b0))
+
+    for key in np.unique(cu_key):
+        sel = cu_key == key
+        s_, e_ = start[sel], end[sel]
+        n_cus += 1
+        first, last_start = s_.min(), s_.max()
+        ev = sorted([(x, 1) for x in s_] + [(x, -1) for x in e_]) + [(t1, 0)]
+        occ, prev = 0, t0
+        for x, d in ev:
+            free = 2 - min(occ, 2)
+            if free and x > prev:
+                ramp += free * overlap(prev, x, t0, first)
+                gaps += free * overlap(prev, x, first, last_start)
+                tail += free * overlap(prev, x, last_start, t1)
+            occ += d
+            prev = x
+    rows["slots empty before a CU's first workgroup starts"] = ramp * tick_us / slots
+    rows["slots empty between workgroups"] = gaps * tick_us / slots
+    rows["slots empty after a CU's last workgroup has started (tail)"] = tail * tick_us / slots
+    # the CU's view: how long at least one / both of its workgroups are inside the key-tile loop, how
+    # many wave tiles it computes, when it goes idle for good
+    one = two = 0.0
+    cu_tiles, cu_last_end, cu_items = [], [], []
+    computed = n_cls[:, :, :4].sum(axis=(1, 2))  # wave tiles with arithmetic, per item
+    for key in np.unique(cu_key):
+        sel = cu_key == key
+        ev = sorted([(x, 1) for x in ready[sel]] + [(x, -1) for x in loop_end[sel]])
+        occ, prev = 0, t0
+        for x, d in ev:
+            if occ >= 1:
+                one += x - prev
+            if occ >= 2:
+                two += x - prev
+            occ += d
+            prev = x
+        cu_tiles.append(float(computed[sel].sum()))
+        cu_last_end.append(float((end[sel].max() - t0) * tick_us))
+        cu_items.append(int(sel.sum()))
+    cu_view = {"at_least_one_workgroup_in_the_loop_us": one * tick_us / n_cus, "both_in_the_loop_us": two * tick_us / n_cus,
+               "wave_tiles_per_cu": {"min": min(cu_tiles), "mean": float(np.mean(cu_tiles)), "max": max(cu_tiles)},
+               "items_per_cu": {"min": min(cu_items), "max": max(cu_items)},
+               "last_end_us": {"min": min(cu_last_end), "mean": float(np.mean(cu_last_end)), "max": max(cu_last_end)}}
+    if args.trace_dump:
+        np.save(args.trace_dump, trace.cpu().numpy().reshape(-1, 4, words))
+    cyc = rec[:, :, 11].sum()
+    loop_ticks = (rec[:, :, 2] - rec[:, :, 1]).sum()
+    tiles = {nm: int(n_cls[:, :, i].sum()) for i, nm in enumerate(names)}
+    per_tile = {nm: (ticks[:, :, i].sum() * tick_us * 1e3 / max(tiles[nm], 1)) for i, nm in enumerate(names)}
+    print(json.dumps({
+        "metric": "phase budget of the forward kernel (slot time / 512, microseconds; rows add up to span_us)",
+        "config": describe(wl, args.config), "kernel_us_untraced_build_of_the_trace_library": untraced_us,
+        "span_us": span, "items": n_items, "cus_seen": n_cus, "budget_us": rows, "sum_us": sum(rows.values()),
+        "occupied_us": occupied, "cu_view": cu_view, "wave_tiles": tiles, "ns_per_wave_tile": per_tile,
+        "sclk_mhz_in_the_loops": cyc / max(loop_ticks, 1) * 100.0}))
 
 
 def bench_backward(args, wl, L, dev):
@@ -265,7 +489,7 @@ def main():
     # of configuration 2 run up to 20 % slower): the default warm-up covers that
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6])
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6, 7])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", type=int, default=0, help="kernel selector (0 auto)")
     ap.add_argument("--rab-grad", action="store_true", help="with --backward and a configuration that has a bias table: its gradient too")
@@ -275,6 +499,14 @@ def main():
     ap.add_argument("--jagged", action="store_true",
                     help="measure the jagged row-gather operators on the workload's [T, H*D] rows "
                          "against the HBM roofline; prints its own JSON line")
+    ap.add_argument("--phase-trace", action="store_true",
+                    help="print where the forward kernel's time goes at --config (needs the phase-trace build: "
+                         "python -m recir_amd.build --trace)")
+    ap.add_argument("--trace-dump", default=None, metavar="FILE.npy", help="with --phase-trace: also save the raw records")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="run the library's calibration loops (bf16 MFMAs alone; the forward's tile loop "
+                         "stand-alone, plain and skewed, random and zero operands) and print their sustained "
+                         "TFLOP/s, ns and cycles per tile round and the shader clock they ran at")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="BYTES",
                     help="only launch the library's plain copy kernel on BYTES bytes a few times "
                          "(for scaling FETCH_SIZE / WRITE_SIZE counter readings) and exit")
@@ -289,6 +521,10 @@ def main():
     from recir_amd import _lib
     from recir_amd.workloads import make_config
 
+    if args.phase_trace:
+        from recir_amd import build
+
+        _lib.LIB_PATH = build.TRACE_LIB_PATH
     L = _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -303,7 +539,11 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibration_copy_bytes": n, "launches": 5}))
         return
+    if args.mfma_ceiling:
+        return bench_mfma_ceiling(args, L, dev)
     wl = make_config(args.config)
+    if args.phase_trace:
+        return bench_phase_trace(args, wl, dev)
     if args.backward:
         return bench_backward(args, wl, L, dev)
     if args.jagged:
@@ -383,6 +623,9 @@ def main():
     peak = PEAK_TFLOPS[wl.dtype]
     achieved = flops / (kern_ms * 1e-3) / 1e12
     traffic, traffic_source = measured_traffic(args.config, kernel_name)
+    # what the chip sustains on bf16 MFMAs alone (random operands, same run, warm clocks): the ceiling
+    # under the power limit, beside the data-sheet peak
+    sustained = CalibrationLoops(L, dev).measure(0, 0, "random")
     result = {
         "metric": "HSTU jagged attention fwd, achieved TFLOP/s on unmasked FLOPs (ms/call in ms_per_step; % of MFMA peak in roofline.frac)",
         "value": flops / (ms_per_step * 1e-3) / 1e12,
@@ -399,6 +642,9 @@ def main():
                        "mean": sum(lat) / len(lat)},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
                      "frac": achieved / peak, "traffic": traffic, "traffic_source": traffic_source, "kernel_ms": kern_ms,
+                     "sustained_peak": sustained["tflops"], "sustained_peak_sclk_mhz": sustained["sclk_mhz"],
+                     "frac_of_sustained": achieved / sustained["tflops"],
+                     "sustained_peak_source": "recir_hstu_calibration_mfma_loop kind 0 (bf16 MFMAs only, random operands), this run",
                      "hbm_gbs_algorithmic": abytes / (kern_ms * 1e-3) / 1e9,
                      "hbm_frac_algorithmic": abytes / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBS},
     }

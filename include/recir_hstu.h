@@ -197,6 +197,28 @@ int recir_hstu_quantize_e4m3_per_head_rows(const void* x_bf16, void* codes_u8, f
  */
 int recir_hstu_calibration_copy(void* dst, const void* src, size_t bytes, void* hip_stream);
 
+/*
+ * Measurement aid, no counterpart in the reference: stand-alone loops with the instruction mix of the
+ * tiled forward kernel and none of its bookkeeping, to price that kernel against what the chip
+ * sustains rather than against the data-sheet peak alone.
+ *   kind 0  bf16 MFMAs only (v_mfma_f32_32x32x16_bf16 back to back, operands in registers)
+ *   kind 1  the forward's tile loop, plain arrangement: per 32-row x 64-key wave tile 32 MFMAs, SiLU of
+ *           32 scores per lane, 48 LDS fragment reads, 8 global -> LDS copies, one barrier
+ *   kind 2  the same work in the skewed arrangement of the forward's leading unmasked tiles
+ * pieces (kinds 1, 2) removes parts, timing only: 1 no SiLU, 2 no LDS fragment reads, 12 no copies and
+ * no barrier, 14 MFMAs + SiLU only; 0 keeps everything.
+ * k, v: device, [rows, 4, 128] bf16, read as `sequences` runs of rows / 64 / sequences key tiles;
+ * q: device, at least [128, 4, 128] bf16.  What they hold is the caller's choice (random values or
+ * zeros: the clock the chip grants depends on the operands).  `workgroups` workgroups of 256 threads
+ * (two fit a CU) each run `tiles` (even) key tiles: FLOPs = workgroups * tiles * 4 * 32 * 32768.
+ * stats: device, [workgroups][4] uint64: shader-clock cycles and 100 MHz ticks of one wave's loop, then
+ * the loop's start and end on the 100 MHz counter (one time base for all workgroups of a launch).
+ * sink: device, [workgroups * 256] float, written once at the end.
+ */
+int recir_hstu_calibration_mfma_loop(int32_t kind, int32_t pieces, const void* k, const void* v, const void* q,
+                                     size_t rows, int32_t sequences, int32_t tiles, int32_t workgroups, float alpha,
+                                     uint64_t* stats, float* sink, void* hip_stream);
+
 /* Thread-local, NUL-terminated description of the last non-zero status on this thread. */
 const char* recir_hstu_last_error(void);
 

@@ -34,6 +34,7 @@ EXPORTS = (
     "recir_hstu_quantize_e4m3_per_head",
     "recir_hstu_quantize_e4m3_per_head_rows",
     "recir_hstu_calibration_copy",
+    "recir_hstu_calibration_mfma_loop",
     "recir_hstu_last_error",
     "recir_hstu_abi_version",
     "recir_hstu_last_kernel",
@@ -83,6 +84,8 @@ def load() -> ctypes.CDLL:
     L.recir_hstu_quantize_e4m3_per_head_rows.restype = ctypes.c_int
     L.recir_hstu_calibration_copy.argtypes = [vp, vp, sz, vp]
     L.recir_hstu_calibration_copy.restype = ctypes.c_int
+    L.recir_hstu_calibration_mfma_loop.argtypes = [i32, i32, vp, vp, vp, sz, i32, i32, i32, f32, vp, vp, vp]
+    L.recir_hstu_calibration_mfma_loop.restype = ctypes.c_int
     i64 = ctypes.c_int64
     L.recir_jagged_to_padded_dense.argtypes = [vp, vp, vp, i64, i32, i32, i64, i32, ctypes.c_uint64, u32, vp]
     L.recir_dense_to_jagged.argtypes = [vp, vp, vp, i64, i32, i32, i64, u32, vp]

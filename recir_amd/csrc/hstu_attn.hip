@@ -32,6 +32,7 @@
 #include "hstu_tiled_d128_dl.h"
 #include "hstu_bwd_generic.h"
 #include "hstu_bwd_d128.h"
+#include "hstu_calibration.h"
 #include "jagged_rows.h"
 #include "ts_pos_embeddings.h"
 #include "counting_sort.h"
@@ -301,6 +302,10 @@ __global__ __launch_bounds__(64) void hstu_fwd_generic(Params p) {
 // ---------------------------------------------------------------------------------------------
 thread_local char g_err[512] = "";
 thread_local const char* g_last_kernel = "";
+#ifdef HSTU_TRACE
+unsigned long long* g_trace_buffer = nullptr;  // device memory of the next forward launches' phase records
+size_t g_trace_words = 0;
+#endif
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -481,6 +486,13 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
         hipLaunchKernelGGL(hstu_plan_kernel_general, dim3(((size_t)B * H + 255) / 256), dim3(256), 0, stream, p, bm, plan_mode);
       if (int rc = launch_status("hstu_plan_kernel")) return rc;
     }
+#ifdef HSTU_TRACE
+    if (g_trace_buffer) {
+      if (g_trace_words < items * NUM_XCD * 4 * TRACE_WORDS)
+        return fail(RECIR_HSTU_ERR_WORKSPACE, "trace buffer of %zu words, %zu needed", g_trace_words, items * NUM_XCD * 4 * TRACE_WORDS);
+      p.trace = g_trace_buffer;
+    }
+#endif
     const dim3 grid((unsigned)(slots * NUM_XCD));
     if (variant == 2) {  // register-staged tiles (kept for comparison and tiling-invariance tests)
       if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128<true>), grid, dim3(256), 0, stream, p);
@@ -724,6 +736,18 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   return RECIR_HSTU_OK;
 }
 
+#ifdef HSTU_TRACE
+// Phase-trace builds only (a second library, never the one the operators load): device buffer that
+// the next forward launches of the direct-to-LDS tiled kernel fill with one record of TRACE_WORDS
+// 64-bit words per (XCD, list slot, wave); null switches the records off.
+int recir_hstu_trace_buffer(void* device_words, size_t words) {
+  g_trace_buffer = (unsigned long long*)device_words;
+  g_trace_words = words;
+  return RECIR_HSTU_OK;
+}
+int recir_hstu_trace_words_per_record(void) { return TRACE_WORDS; }
+#endif
+
 int recir_hstu_calibration_copy(void* dst, const void* src, size_t bytes, void* hip_stream) {
   if (!dst || !src || (bytes & 15) || (((size_t)dst | (size_t)src) & 15))
     return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "calibration copy needs 16-byte aligned pointers and size");
@@ -731,6 +755,58 @@ int recir_hstu_calibration_copy(void* dst, const void* src, size_t bytes, void* 
   hipLaunchKernelGGL(hstu_calibration_copy, dim3(4096), dim3(256), 0, (hipStream_t)hip_stream, (u32x4*)dst,
                      (const u32x4*)src, bytes / 16);
   return launch_status("hstu_calibration_copy");
+}
+
+}  // extern "C"
+
+namespace {
+template <int KIND>
+int launch_calibration(int pieces, unsigned grid, hipStream_t stream, const CalParams& c) {
+  const dim3 g(grid), b(256);
+  switch (pieces) {
+    case 0: hipLaunchKernelGGL((hstu_calibration_loop<KIND, 0>), g, b, 0, stream, c); return 0;
+    case CAL_NO_SILU: hipLaunchKernelGGL((hstu_calibration_loop<KIND, CAL_NO_SILU>), g, b, 0, stream, c); return 0;
+    case CAL_NO_LDS_READS: hipLaunchKernelGGL((hstu_calibration_loop<KIND, CAL_NO_LDS_READS>), g, b, 0, stream, c); return 0;
+    case CAL_NO_COPIES | CAL_NO_BARRIER:
+      hipLaunchKernelGGL((hstu_calibration_loop<KIND, CAL_NO_COPIES | CAL_NO_BARRIER>), g, b, 0, stream, c); return 0;
+    case CAL_NO_LDS_READS | CAL_NO_COPIES | CAL_NO_BARRIER:
+      hipLaunchKernelGGL((hstu_calibration_loop<KIND, CAL_NO_LDS_READS | CAL_NO_COPIES | CAL_NO_BARRIER>), g, b, 0, stream, c); return 0;
+    default: return -1;
+  }
+}
+}  // namespace
+
+extern "C" {
+
+int recir_hstu_calibration_mfma_loop(int32_t kind, int32_t pieces, const void* k, const void* v, const void* q, size_t rows,
+                                     int32_t sequences, int32_t tiles, int32_t workgroups, float alpha, uint64_t* stats,
+                                     float* sink, void* hip_stream) {
+  if (kind < 0 || kind > 2) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "calibration kind must be 0, 1 or 2, got %d", kind);
+  if (!k || !v || !q || !stats || !sink) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "calibration buffers must be non-null");
+  if ((((size_t)k | (size_t)v | (size_t)q) & 15) || ((size_t)stats & 7))
+    return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "calibration buffers must be 16-byte aligned");
+  if (sequences <= 0 || workgroups <= 0 || tiles <= 0 || (tiles & 1))
+    return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "sequences, workgroups and an even number of tiles must be positive");
+  const size_t seq_tiles = rows / BN / (size_t)sequences;
+  if (seq_tiles < 2 || rows < (size_t)BM) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "the buffers must hold at least two key tiles of 64 rows per sequence");
+  if (seq_tiles > 0x7fffffffull) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "buffers too large");
+  CalParams c;
+  c.k = (const char*)k; c.v = (const char*)v; c.q = (const char*)q;
+  c.sink = sink; c.stats = (unsigned long long*)stats;
+  c.tiles = tiles; c.seq_tiles = (int)seq_tiles; c.sequences = sequences;
+  c.neg_c = -alpha * kLog2e;
+  hipStream_t stream = (hipStream_t)hip_stream;
+  int rc = 0;
+  if (kind == 0) {
+    if (pieces != 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "the MFMA-only loop has no pieces to remove");
+    hipLaunchKernelGGL((hstu_calibration_loop<0, 0>), dim3((unsigned)workgroups), dim3(256), 0, stream, c);
+  } else if (kind == 1) {
+    rc = launch_calibration<1>(pieces, (unsigned)workgroups, stream, c);
+  } else {
+    rc = launch_calibration<2>(pieces, (unsigned)workgroups, stream, c);
+  }
+  if (rc) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "pieces %d is not one of the built combinations (0, 1, 2, 12, 14)", pieces);
+  return launch_status("hstu_calibration_loop");
 }
 
 int recir_hstu_quantize_e4m3_per_head(const void* x_bf16, void* codes_u8, float* scale, int32_t T,

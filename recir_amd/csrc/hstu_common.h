@@ -53,7 +53,22 @@ struct Params {
                        //      positions keep full causal attention
   float alpha;
   unsigned flags;
+  unsigned long long* trace;  // phase-trace builds (HSTU_TRACE) only: one TRACE_WORDS record per (work item, wave); else null
 };
+
+// Phase-trace builds: the forward kernel stamps the 100 MHz counter at the phases of every work item.
+// Record of (XCD x, list slot s, wave w) at trace[((x * items_cap + s) * 4 + w) * TRACE_WORDS]:
+//   0 item start   1 first tile resident (query rows loaded, first barrier passed)   2 key-tile loop left
+//   3 output rows stored   4..7 ticks spent in skewed trips / unclassified leading tiles / other unmasked
+//   tiles / partial tiles (each with its barrier)   8 ticks in tiles this wave skipped (copies and barrier only)
+//   9 tile counts, one byte each: skewed, leading, unmasked, partial, skipped   10 hardware id (XCC id << 32 | HW_ID)
+//   11 shader-clock cycles of the key-tile loop
+constexpr int TRACE_WORDS = 12;
+#ifdef HSTU_TRACE
+#define HSTU_TR(...) __VA_ARGS__
+#else
+#define HSTU_TR(...)
+#endif
 
 struct SeqInfo {
   int s;        // first packed token

@@ -144,8 +144,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
   const int l32 = lane & 31;
   const int half = lane >> 5;
 
-  zero_tail_rows<256>(p, (size_t)p.H * HD * 2);
-
   // ---- per-lane constants of the LDS access patterns ----
   // K fragment (ds_read_b128): row 32 kvb + l32, chunk (2 kk + half) ^ (l32 & 15); kk enters as an
   // XOR of address bits 5..7
@@ -169,13 +167,28 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
   const unsigned k8_rd = (unsigned)l32 * 128u + (unsigned)(((2 * half) ^ ((l32 >> 1) & 7)) * 16);
   const int ld8_row = lane >> 3, ld8_chunk = lane & 7;
 
-  // Work list of the XCD this workgroup runs on.  Normally one item per workgroup; the stride loop
-  // only matters when a list is longer than the launch assumed (sequences above max_seq_len).
+  // Work list of the XCD this workgroup runs on.  The list length and the workgroup's item are written by an earlier launch and only read here:
+  // both go through the constant address space (scalar loads, issued side by side before anything
+  // is waited for; the item is fetched whether or not its slot is inside the list, the slot always
+  // being inside the list's storage).
+  typedef const __attribute__((address_space(4))) int* const_ints;
   const int xcd = blockIdx.x % NUM_XCD;
-  const int list_len = p.ws_counts[xcd];
-  const WorkItem* __restrict__ list = p.ws_items + (size_t)xcd * p.items_cap;
-  for (int slot = blockIdx.x / NUM_XCD; slot < list_len; slot += p.grid_slots) {
-    const WorkItem wi = list[slot];
+  const int slot0 = blockIdx.x / NUM_XCD;  // < grid_slots <= items_cap
+  const WorkItem* list = p.ws_items + (size_t)xcd * p.items_cap;
+  auto load_item = [&](int slot) __attribute__((always_inline)) {
+    const_ints w = (const_ints)(size_t)(list + slot);
+    WorkItem it;
+    it.s = w[0]; it.n = w[1]; it.cap = w[2]; it.ctx_eff = w[3]; it.q0 = w[4]; it.h = w[5]; it.b = w[6]; it.q_end = w[7];
+    return it;
+  };
+  WorkItem wi = load_item(slot0);
+  const int list_len = ((const_ints)(size_t)p.ws_counts)[xcd];
+  // Normally one item per workgroup; the stride loop only matters when a list is longer than the
+  // launch assumed (sequences above max_seq_len).
+  for (int slot = slot0; slot < list_len; slot += p.grid_slots) {
+    HSTU_TR(const unsigned long long tr_start = wall_clock64(); unsigned long long tr_ready = tr_start, tr_ticks[5] = {0, 0, 0, 0, 0};
+            unsigned tr_count[5] = {0, 0, 0, 0, 0}; long long tr_c0_item = clock64();)
+    if (slot != slot0) wi = load_item(slot);
     SeqInfo si;
     si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
     si.win = WIN_ALL; si.tail0 = 0x7fffffff;
@@ -812,7 +825,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
                                      (k0 < idhi_w && (wave_has_tail || k1 > idlo_w - si.win)));
       if (!any_kept) {
         if (nxt < nkv) issue_tile_and_band(nxt, std::integral_constant<int, BUF ^ 1>{});  // this wave still copies its share
-        return;
+        return 4;
       }
       bool full = (k1 - 1 <= m_lo) && (k1 <= si.cap);  // implies k1 <= n
       if (SEMI) full = full && (idlo_w >= si.tail0 || k0 >= idhi_w - si.win);  // inside every row's window
@@ -821,6 +834,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       if (full) tile_body(std::integral_constant<int, 0>{}, buf_tag, k0, nxt, std::false_type{});
       else if (SEMI && range_mask) tile_body(std::integral_constant<int, 2>{}, buf_tag, k0, nxt, std::false_type{});
       else tile_body(std::integral_constant<int, 1>{}, buf_tag, k0, nxt, std::false_type{});
+      return full ? 2 : 3;  // class of the tile for this wave (phase-trace builds): 2 unmasked, 3 partial, 4 skipped
     };
 
     // Leading tiles this wave runs without classifying them: unmasked for all of its rows
@@ -837,6 +851,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       if (HAS_RAB) band_store(std::integral_constant<int, 0>{}, band_first);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      HSTU_TR(tr_ready = wall_clock64(); tr_c0_item = clock64(); unsigned long long tr_t = tr_ready;)
       if (SKEW && skew_tiles) {
         const std::integral_constant<int, 0> st0{};
         const std::integral_constant<int, 1> st1{};
@@ -872,6 +887,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         HSTU_DL_TILE_SYNC();
         it = skew_tiles;
         fast_pairs = 0;
+        HSTU_TR({ const unsigned long long t = wall_clock64(); tr_ticks[0] += t - tr_t; tr_t = t; tr_count[0] += skew_tiles; })
       }
       for (int pi = 0; pi < fast_pairs; ++pi) {
         tile_body(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, it * BN, it + 1, std::true_type{});
@@ -880,23 +896,31 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         HSTU_DL_TILE_SYNC();
         it += 2;
       }
+      HSTU_TR(if (fast_pairs) { const unsigned long long t = wall_clock64(); tr_ticks[1] += t - tr_t; tr_t = t; tr_count[1] += 2 * fast_pairs; })
       // two tiles per trip so that the stage index is a compile-time constant
       while (true) {
         int nxt = next_tile(it);
-        compute_tile(it, std::integral_constant<int, 0>{}, nxt);
+        int cls = compute_tile(it, std::integral_constant<int, 0>{}, nxt);
+        if (nxt < nkv) {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile nxt have landed
+          __syncthreads();                                   // ... and everybody's; tile it is no longer read
+        }
+        HSTU_TR({ const unsigned long long t = wall_clock64(); tr_ticks[cls] += t - tr_t; tr_t = t; tr_count[cls] += 1; })
         if (nxt >= nkv) break;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile nxt have landed
-        __syncthreads();                                   // ... and everybody's; tile it is no longer read
         it = nxt;
         nxt = next_tile(it);
-        compute_tile(it, std::integral_constant<int, 1>{}, nxt);
+        cls = compute_tile(it, std::integral_constant<int, 1>{}, nxt);
+        if (nxt < nkv) {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          __syncthreads();
+        }
+        HSTU_TR({ const unsigned long long t = wall_clock64(); tr_ticks[cls] += t - tr_t; tr_t = t; tr_count[cls] += 1; })
         if (nxt >= nkv) break;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
         it = nxt;
       }
     }
 
+    HSTU_TR(const unsigned long long tr_loop_end = wall_clock64(); const long long tr_c1 = clock64();)
     // ---- epilogue: O^T accumulators -> out[s + m, h, :] ----
     if (m < q_end) {
       float oscale = 1.0f / (float)p.N;
@@ -915,8 +939,25 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         }
       }
     }
+#ifdef HSTU_TRACE
+    if (p.trace && lane == 0) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the output rows have left
+      unsigned hwid, xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+      unsigned long long* rec = p.trace + (((size_t)xcd * p.items_cap + slot) * 4 + wave) * TRACE_WORDS;
+      rec[0] = tr_start; rec[1] = tr_ready; rec[2] = tr_loop_end; rec[3] = wall_clock64();
+      for (int i = 0; i < 5; ++i) rec[4 + i] = tr_ticks[i];
+      rec[9] = (unsigned long long)tr_count[0] | ((unsigned long long)tr_count[1] << 8) | ((unsigned long long)tr_count[2] << 16) |
+               ((unsigned long long)tr_count[3] << 24) | ((unsigned long long)tr_count[4] << 32);
+      rec[10] = ((unsigned long long)xcc << 32) | hwid;
+      rec[11] = (unsigned long long)(tr_c1 - tr_c0_item);
+    }
+#endif
     __syncthreads();  // LDS buffers are reused by the next item
   }  // work items
+  // rows behind the last sequence: after the items, so that no workgroup waits for seq_offsets[B] before it starts
+  zero_tail_rows<256>(p, (size_t)p.H * HD * 2);
 }
 
 }  // namespace recir_hstu

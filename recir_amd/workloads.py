@@ -1,5 +1,7 @@
 """Synthetic inputs for the benchmark configurations of the HSTU attention path (1-5 from the
-baseline; 6 = configuration 2 with the reference's semi-local mask, 256 local + 256 full tail).
+baseline; 6 = configuration 2 with the reference's semi-local mask, 256 local + 256 full tail;
+7 = 16 sequences of 4,096 history tokens, the kernel's steady state: two workgroups on every CU
+from the start of the launch to its end).
 
 Sequence lengths come from ``numpy.random.Generator(PCG64(seed))``; q, k, v (and the relative
 attention bias) from ``torch.Generator().manual_seed(seed)`` on the CPU in the order q, k, v, rab.
@@ -98,6 +100,8 @@ def history_lengths(config: int, seed: int = 0) -> np.ndarray:
         return rng.integers(256, 1985, size=32).astype(np.int64)
     if config == 4:
         return np.clip(rng.zipf(1.2, size=8), 128, 8064).astype(np.int64)
+    if config == 7:
+        return np.full((16,), 4096, dtype=np.int64)
     raise ValueError(f"unknown config {config}")
 
 
@@ -109,6 +113,7 @@ _SPEC = {
     4: (128, 8192, 4, 128, "bf16", 1.0 / 128),
     5: (64, 2048, 4, 128, "fp8", 1.0 / 128),
     6: (64, 2048, 4, 128, "bf16", 1.0 / 128),  # config 2 with the semi-local mask (256 local, 256 full tail)
+    7: (0, 4096, 4, 128, "bf16", 1.0 / 128),   # steady state of the tiled kernel: 16 x 4,096, no targets
 }
 
 
