@@ -499,6 +499,9 @@ def main():
     ap.add_argument("--jagged", action="store_true",
                     help="measure the jagged row-gather operators on the workload's [T, H*D] rows "
                          "against the HBM roofline; prints its own JSON line")
+    ap.add_argument("--lib", default=None, metavar="PATH",
+                    help="measure another build of the library (same ABI) instead of recir_amd/librecir_hstu.so, "
+                         "for A/B runs on one box")
     ap.add_argument("--phase-trace", action="store_true",
                     help="print where the forward kernel's time goes at --config (needs the phase-trace build: "
                          "python -m recir_amd.build --trace)")
@@ -525,6 +528,8 @@ def main():
         from recir_amd import build
 
         _lib.LIB_PATH = build.TRACE_LIB_PATH
+    if args.lib:
+        _lib.LIB_PATH = os.path.abspath(args.lib)
     L = _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

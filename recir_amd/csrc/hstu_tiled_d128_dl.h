@@ -19,12 +19,12 @@
 // tile i run and must have landed (vmcnt) before the barrier that ends tile i.
 //
 // LDS layouts (both tiles are [BN rows][256 bytes], swizzled in place of padding):
-//   K  16-byte chunk c of row r sits at chunk c ^ (r & 7)
-//   V  32-byte slot  s of row r sits at slot  s ^ (r & 3)
-// These are free of bank conflicts for 32 banks.  gfx950's LDS has 64 (256 bytes per clock), where
-// they run at half rate; the conflict-free forms (K: c ^ (r & 15), V: s ^ 2 (r & 3), HSTU_DL_SWZ64)
-// halve the LDS busy time but need six more address registers, and the kernel, which is bound by
-// VALU issue and not by LDS bandwidth, is slower with them.
+//   K  16-byte chunk c of row r sits at chunk c ^ (r & 15)
+//   V  32-byte slot  s of row r sits at slot  s ^ 2 (r & 3)
+// These are free of bank conflicts on gfx950's 64 banks (256 bytes per clock) for the K fragment
+// reads (ds_read_b128) and the transposing V reads.  (The forms for 32 banks, c ^ (r & 7) and
+// s ^ (r & 3), run those reads at half rate; they need six address registers fewer and measured
+// 1-2 % slower once nothing spilled.)
 // A global_load_lds instruction writes 64 lanes x 16 bytes to consecutive LDS addresses, so the
 // swizzle is applied to the global address each lane fetches.
 #pragma once
@@ -50,9 +50,6 @@ typedef __attribute__((ext_vector_type(8))) int i32x8;
 // contraction stay bf16.  The K tile is then [BN rows][128 bytes], chunk c of row r at c ^ (r & 7).
 // SEMI: the semi-local mask (max_attn_len > 0) -- window test in the partial tiles, key tiles below
 // every row's window not walked; the causal instantiation carries none of it.
-#ifndef HSTU_DL_ASM_COPY
-#define HSTU_DL_ASM_COPY 1
-#endif
 // One global -> LDS copy instruction: 64 lanes x 16 bytes from base + per-lane offset to 1 KB of
 // consecutive LDS.  Written as assembly so that the compiler does not treat it as an access that
 // may touch both memories: with the builtin every later wait for an LDS read becomes a wait for
@@ -65,69 +62,26 @@ __device__ __forceinline__ void copy16(const void* base, unsigned lane_off, unsi
 __device__ __forceinline__ void copy4(const void* base, unsigned lane_off, unsigned lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_addr), "v"(lane_off), "s"(base) : "memory");
 }
-// LDS swizzle of the bf16 K and V tiles: 1 = free of bank conflicts on the 64-bank LDS
-// (K chunk ^ (row & 15), V slot ^ 2 (row & 3)); 0 = the 32-bank forms (K chunk ^ (row & 7), V slot ^
-// (row & 3)), which run the LDS reads at half rate.  The 64-bank forms need six address registers more;
-// with the short prefetch distances below nothing spills, and they measure 1-2 % faster.
-#ifndef HSTU_DL_SWZ64
-#define HSTU_DL_SWZ64 1
-#endif
-constexpr int KSWZ = HSTU_DL_SWZ64 ? 15 : 7;
-constexpr int VSWZ = HSTU_DL_SWZ64 ? 4 : 2;
-#ifndef HSTU_DL_PRIO
-#define HSTU_DL_PRIO 1  // wave priority while an MFMA is waiting to issue (0: leave it alone)
-#endif
-#ifndef HSTU_DL_RANGE_SLOTS
-#define HSTU_DL_RANGE_SLOTS 1  // tiles under the range form of the semi-local mask use the slot schedule
-#endif
-#ifndef HSTU_DL_SLOTS_UNMASKED
-#define HSTU_DL_SLOTS_UNMASKED 1  // full tiles outside the leading run use the slot schedule too (-1.5 % at configuration 2)
-#endif
-#ifndef HSTU_DL_RAB_SLOTS
-#define HSTU_DL_RAB_SLOTS 2  // bias instantiations: 1 = slot schedule where the unbiased kernel has it, 2 = in every bf16 tile
-                             // body (the other body adds the bias in the SiLU arithmetic; measured 2-3 % slower)
-#endif
-#ifndef HSTU_DL_PD_SLOW
-#define HSTU_DL_PD_SLOW 3  // fragment prefetch distance of the bodies that carry mask or clamping state
-#endif
-#ifndef HSTU_DL_PDK_RAB
-#define HSTU_DL_PDK_RAB 6  // K fragments in flight when a tile opens, bias instantiations (the bias block needs registers too)
-#endif
-#ifndef HSTU_DL_B1
-#define HSTU_DL_B1 5  // slot in which the bias of the second score block is read (first used in slot 8)
-#endif
-#ifndef HSTU_DL_SLOTS
-#define HSTU_DL_SLOTS 1
-#endif
-#ifndef HSTU_DL_PDK
-#define HSTU_DL_PDK 6  // K fragments (slots 0..15) are requested this many slots ahead
-#endif
-#ifndef HSTU_DL_PDV
-#define HSTU_DL_PDV 10  // V fragments (slots 16..31) likewise
-#endif
+constexpr int KSWZ = 15;  // K chunk ^ (row & 15)
+constexpr int VSWZ = 4;   // V 16-byte chunk ^ 4 (row & 3), i.e. 32-byte slot ^ 2 (row & 3)
+
+// Schedule constants of the tile bodies, each the best of a measured range (configurations 2 and 4).
+constexpr int DL_PDK = 6;       // K fragments (slots 0..15) are requested this many slots ahead
+constexpr int DL_PDV = 10;      // V fragments (slots 16..31) likewise
+constexpr int DL_PDK_RAB = 6;   // K fragments in flight when a tile opens, bias instantiations
+constexpr int DL_PD_SLOW = 3;   // fragment prefetch distance of the bodies that carry mask or clamping state
+constexpr int DL_B1 = 5;        // slot in which the bias of the second score block is read (first used in slot 8)
+constexpr int DL_U0 = 9;        // slot of the first SiLU unit
+constexpr int DL_SKEW_MIN = 2;  // fewest leading tiles worth the skewed loop's entry and exit
+constexpr int DL_SKEW_PD = 3;   // the skewed loop's fragment prefetch distance in slots
+// Measurement switch (python -m recir_amd.build --trace -DHSTU_DL_SKEW=0): 0 walks the leading
+// unmasked tiles with the plain loop, for timing the two loops against each other.
 #ifndef HSTU_DL_SKEW
-#define HSTU_DL_SKEW 1  // leading unmasked tiles of an item run the loop skewed by one tile (bf16, no bias, causal)
-#endif
-#ifndef HSTU_DL_SKEW_MIN
-#define HSTU_DL_SKEW_MIN 2  // fewest leading tiles worth the loop's entry and exit
-#endif
-#ifndef HSTU_DL_SKEW_PRIO
-#define HSTU_DL_SKEW_PRIO 0  // wave priority around its MFMAs: none (two instructions per slot that cost more than they gain there)
-#endif
-#ifndef HSTU_DL_SKEW_PD
-#define HSTU_DL_SKEW_PD 3  // its fragment prefetch distance in slots
+#define HSTU_DL_SKEW 1
 #endif
 #define HSTU_DL_TILE_SYNC() do { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); __syncthreads(); } while (0)
-#ifndef HSTU_DL_C0
-#define HSTU_DL_C0 0     // slot of the first copy instruction of the next tile
-#define HSTU_DL_CSTEP 1  // slots between copy instructions
-#endif
-#ifndef HSTU_DL_U0
-#define HSTU_DL_U0 9  // slot of the first SiLU unit
-#endif
 template <bool HAS_RAB, bool FP8, bool SEMI>
 __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
-  constexpr bool ASM_COPY = HSTU_DL_ASM_COPY != 0;
   // The two pipeline stages are separate objects and every access names its stage at compile time:
   // the compiler then knows that an LDS read of one stage cannot alias the global -> LDS copies in
   // flight into the other, and does not wait for them.
@@ -151,13 +105,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
   // V^T fragment (two ds_read_b64_tr_b16): source lane s = lane & 15 of a 16-lane group supplies the
   // 8 bytes at row 4 half + (s >> 2) (+ 16 s2 + 8 rd), d = 32 db + 16 dgrp + 4 (s & 3) .. +3
   const int tr_s = lane & 15, tr_r = tr_s >> 2, tr_c = tr_s & 3, tr_dgrp = (lane >> 4) & 1;
-#if HSTU_DL_SWZ64
   const unsigned vt_rd = (unsigned)(4 * half + tr_r) * (HD * 2) + (unsigned)tr_r * 64u + (unsigned)tr_dgrp * 32u + (unsigned)tr_c * 8u;
-#else
-  const unsigned vt_base = (unsigned)(4 * half + tr_r) * (HD * 2) + (unsigned)((tr_dgrp ^ (tr_r & 1)) * 32) + (unsigned)tr_c * 8u;
-  const unsigned vt_rd_e = vt_base + (unsigned)((tr_r >> 1) * 64);  // even db: slot bit 1 flipped upwards
-  const unsigned vt_rd_o = vt_base - (unsigned)((tr_r >> 1) * 64);  // odd db: downwards
-#endif
   // global -> LDS copies: instruction j of a tile (16 per matrix, wave w issues j = 4 w + ps) fills rows
   // 4 j .. 4 j + 3; lane i lands at row 4 j + (i >> 4), physical chunk i & 15
   const int ld_row = lane >> 4, ld_chunk = lane & 15;
@@ -302,13 +250,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           kr = kt;
           vr = vt;
         }
-        if constexpr (ASM_COPY) {
-          if (!is_v) { if (!FP8) copy16(kr, ko, (unsigned)(size_t)&Kd[r0 * HD]); }
-          else copy16(vr, vo, (unsigned)(size_t)&Vd[r0 * HD]);
-        } else {
-          if (!is_v) { if (!FP8) __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)&Kd[r0 * HD], 16, 0, 0); }
-          else __builtin_amdgcn_global_load_lds((const unsigned*)(vr + vo), (lds_void*)&Vd[r0 * HD], 16, 0, 0);
-        }
+        if (!is_v) { if (!FP8) copy16(kr, ko, (unsigned)(size_t)&Kd[r0 * HD]); }
+        else copy16(vr, vo, (unsigned)(size_t)&Vd[r0 * HD]);
         return;
       }
       if (FP8) {
@@ -322,8 +265,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
             ko = (unsigned)min(r0 + ld8_row, last) * krow_bytes + (unsigned)((ld8_chunk ^ (((r0 + ld8_row) >> 1) & 7)) * 16);
             kr = kt;
           }
-          if constexpr (ASM_COPY) copy16(kr, ko, (unsigned)(size_t)((char*)Kd + r0 * 128));
-          else __builtin_amdgcn_global_load_lds((const unsigned*)(kr + ko), (lds_void*)((char*)Kd + r0 * 128), 16, 0, 0);
+          copy16(kr, ko, (unsigned)(size_t)((char*)Kd + r0 * 128));
         }
       }
     };
@@ -377,7 +319,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       const int run_end = has_skip ? skip_a : nkv;
       const int f = min(min((q0 + 1) / BN, cap0 / BN), min(run_end - 1, si.n / BN - 1));
       skew_tiles = max(f, 0) & ~1;
-      if (skew_tiles < HSTU_DL_SKEW_MIN) skew_tiles = 0;
+      if (skew_tiles < DL_SKEW_MIN) skew_tiles = 0;
     }
     // One copy instruction of the skewed loop's trip i (LDS stage BUF = i & 1); this wave moves rows
     // 8 wave + 4 idx .. + 3 of a half tile.  parts 0, 1: K rows 0..31 of tile i + 2 (stage BUF);
@@ -480,25 +422,19 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       const std::integral_constant<int, BUF ^ 1> other{};
       const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       auto k_frag = [&](int kvb, int kk) __attribute__((always_inline)) {
-#if HSTU_DL_SWZ64
         return *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)(kk * 32)));
-#else
-        return *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)((kk & 3) * 32)) + (kk >> 2) * 128);
-#endif
       };
       auto v_frag = [&](int db, int s2) __attribute__((always_inline)) {
-#if HSTU_DL_SWZ64
         const char* a = vb + (vt_rd ^ (unsigned)(db * 64)) + s2 * 16 * HD * 2;
-#else
-        const char* a = vb + ((db & 1) ? vt_rd_o : vt_rd_e) + db * 64 + s2 * 16 * HD * 2;
-#endif
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)a);
         const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a + 8 * HD * 2));
         const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         return __builtin_bit_cast(bf16x8, both);
       };
-#if HSTU_DL_SLOTS
-      if constexpr (!FP8 && (!HAS_RAB || HSTU_DL_RAB_SLOTS) && (FAST || HSTU_DL_SLOTS > 1 || (HSTU_DL_SLOTS_UNMASKED && (decltype(masked_tag)::value == 0 || (HSTU_DL_RANGE_SLOTS && decltype(masked_tag)::value == 2))) || (HAS_RAB && HSTU_DL_RAB_SLOTS > 1))) {  // (mask state leaves this schedule too few registers)
+      // The slot schedule: every bf16 tile body but the one with the general mask predicate and no bias
+      // (its mask state leaves this schedule too few registers: 7 % slower there); with a bias every
+      // body (the other schedule would add the bias in the SiLU arithmetic: 2-3 % slower).
+      if constexpr (!FP8 && (decltype(masked_tag)::value != 1 || HAS_RAB)) {
         // Hand-placed schedule, one MFMA per slot with a scheduling fence after each:
         //   slots  0..7   S0 = K[0:32] Q^T            slots  8..15  S1 = K[32:64] Q^T
         //   slots 16..31  O^T[db] += V^T[db, s2] P^T[s2], key step s2 = (slot - 16) / 4, db = slot & 3
@@ -515,7 +451,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         // open a tile; all sixteen would fit the registers that scores and packed P leave free at
         // that point, but measured 1-3 % slower (configurations 2 and 4).  V fragments run ten slots
         // ahead.  (The bodies that carry mask or clamping state: distance 6 for both.)
-        constexpr int PDK = FAST ? (HAS_RAB ? HSTU_DL_PDK_RAB : HSTU_DL_PDK) : HSTU_DL_PD_SLOW, PDV = FAST ? HSTU_DL_PDV : HSTU_DL_PD_SLOW;
+        constexpr int PDK = FAST ? (HAS_RAB ? DL_PDK_RAB : DL_PDK) : DL_PD_SLOW, PDV = FAST ? DL_PDV : DL_PD_SLOW;
         auto frag_req = [](int s) constexpr { return s < PDK ? -1 : (s < 16 ? s - PDK : max(s - PDV, 0)); };
         // slot 16 + j of the second contraction: accumulator db, key step s2
         auto pv_db = [](int s) constexpr { return (s - 16) & 3; };
@@ -570,10 +506,8 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
 #pragma unroll
           for (int t = s + 1; t < 32; ++t)
             if (frag_req(t) == s) F[t] = slot_frag(t);
-          if (HAS_RAB && s == HSTU_DL_B1) bias_block(1);
-#if HSTU_DL_PRIO
-          __builtin_amdgcn_s_setprio(HSTU_DL_PRIO);
-#endif
+          if (HAS_RAB && s == DL_B1) bias_block(1);
+          __builtin_amdgcn_s_setprio(1);  // while an MFMA waits to issue
           if (s < 16) {
             sblk[s >> 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], qf[s & 7], (!HAS_RAB && (s & 7) == 0) ? zero : sblk[s >> 3], 0, 0, 0);
           } else {
@@ -582,17 +516,14 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
                              pw[s2 >> 1][4 * (s2 & 1) + 3]};
             acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], __builtin_bit_cast(bf16x8, w), acc[db], 0, 0, 0);
           }
-#if HSTU_DL_PRIO
           __builtin_amdgcn_s_setprio(0);
-#endif
-          if (s >= HSTU_DL_C0 && s < HSTU_DL_C0 + 8 * HSTU_DL_CSTEP && (s - HSTU_DL_C0) % HSTU_DL_CSTEP == 0) issue_slot((s - HSTU_DL_C0) / HSTU_DL_CSTEP);
-          if (s >= HSTU_DL_U0 && s < HSTU_DL_U0 + 16) silu_unit(s - HSTU_DL_U0);
+          if (s < 8) issue_slot(s);  // one copy instruction of the next tile behind each of the first MFMAs
+          if (s >= DL_U0 && s < DL_U0 + 16) silu_unit(s - DL_U0);
           if (HAS_RAB && s == 31 && copy_next) band_store(other, band_next);
           __builtin_amdgcn_sched_barrier(0);
         }
         return;
       }
-#endif
       f32x16 s0, s1;
       bf16x8 pb0, pb1, pb2, pb3;
       float band_nxt = 0.f;
@@ -725,25 +656,17 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       constexpr int BUF = decltype(buf_tag)::value;
       constexpr int KIND = decltype(kind_tag)::value;
       constexpr int NSLOT = KIND == 3 ? 8 : 32;
-      constexpr int PD = HSTU_DL_SKEW_PD;
+      constexpr int PD = DL_SKEW_PD;
       const char* kc = (const char*)(BUF ? Ks1 : Ks0);
       const char* ko = (const char*)(BUF ? Ks0 : Ks1);
       const char* vc = (const char*)(BUF ? Vs1 : Vs0);
       const char* vo = (const char*)(BUF ? Vs0 : Vs1);
       const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       auto k_frag_at = [&](const char* kb, int kvb, int kk) __attribute__((always_inline)) {
-#if HSTU_DL_SWZ64
         return *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)(kk * 32)));
-#else
-        return *(const bf16x8*)(kb + kvb * 32 * HD * 2 + (ks_rd ^ (unsigned)((kk & 3) * 32)) + (kk >> 2) * 128);
-#endif
       };
       auto v_frag_at = [&](const char* vb, int db, int s2) __attribute__((always_inline)) {
-#if HSTU_DL_SWZ64
         const char* a = vb + (vt_rd ^ (unsigned)(db * 64)) + s2 * 16 * HD * 2;
-#else
-        const char* a = vb + ((db & 1) ? vt_rd_o : vt_rd_e) + db * 64 + s2 * 16 * HD * 2;
-#endif
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)a);
         const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a + 8 * HD * 2));
         const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -785,9 +708,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       for (int s = 0; s < NSLOT; ++s) {
         if (s + PD < NSLOT && has_mfma(s + PD)) F[s + PD] = slot_frag(s + PD);
         if (has_mfma(s)) {
-#if HSTU_DL_SKEW_PRIO
-          __builtin_amdgcn_s_setprio(HSTU_DL_SKEW_PRIO);
-#endif
           if (s < 8) {
             const int w0 = 4 * (s >> 2), db = s & 3;
             const u32x4 w = {sk_pw1[w0], sk_pw1[w0 + 1], sk_pw1[w0 + 2], sk_pw1[w0 + 3]};
@@ -801,9 +721,6 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
             const u32x4 w = {sk_pw0[w0], sk_pw0[w0 + 1], sk_pw0[w0 + 2], sk_pw0[w0 + 3]};
             acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[s], __builtin_bit_cast(bf16x8, w), acc[db], 0, 0, 0);
           }
-#if HSTU_DL_SKEW_PRIO
-          __builtin_amdgcn_s_setprio(0);
-#endif
         }
         if (KIND != 3 && s < 8 && !(KIND == 0 && s >= 6) && !(KIND == 2 && s < 2)) skew_copy(i, buf_tag, s);
 #pragma unroll
@@ -860,11 +777,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           bf16x8 f0[8];
 #pragma unroll
           for (int kk = 0; kk < 8; ++kk) {
-#if HSTU_DL_SWZ64
             f0[kk] = *(const bf16x8*)((const char*)Ks0 + (ks_rd ^ (unsigned)(kk * 32)));
-#else
-            f0[kk] = *(const bf16x8*)((const char*)Ks0 + (ks_rd ^ (unsigned)((kk & 3) * 32)) + (kk >> 2) * 128);
-#endif
           }
 #pragma unroll
           for (int kk = 0; kk < 8; ++kk) sk_s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0[kk], qf[kk], kk == 0 ? zero : sk_s0, 0, 0, 0);
