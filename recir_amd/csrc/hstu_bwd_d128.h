@@ -382,7 +382,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
           int* gi = (int*)(BUF ? gband1 : gband0) + (band_lane >> 2);
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            __hip_atomic_fetch_add(gi + (kvb * 32 + 8 * (r >> 2) + (r & 3)), (int)(ds[r] * fx_scale), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_add(gi + (kvb * 32 + 8 * (r >> 2) + (r & 3)), __float2int_rn(ds[r] * fx_scale), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -595,6 +595,22 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     const int t_first = has_ctx ? 0 : j0 / BWD_BN;
     const int t_last = (has_hist || has_ctx) ? (si.n - 1) / BWD_BN : (j_end - 1) / BWD_BN;  // inclusive
     const int nq = t_last + 1;
+    // Semi-local mask: the last of this tile's keys is inside the window of the rows up to
+    // j_end - 1 + win; after them no row sees any of the keys until the rows of the full-attention
+    // tail begin (rows from tail0 on, which include the target rows; without a tail: no row at all).
+    // The query tiles in between, [gap_a, gap_b), are not walked.  (Unless the window reaches the
+    // target rows, whose position is cap, or the tile holds a contextual key.)
+    int gap_a = nq, gap_b = nq;
+    if (SEMI && has_hist && !has_ctx) {
+      const long long reach = (long long)(j_end - 1) + si.win;
+      if (reach < (long long)si.cap) {
+        const int resume_row = si.tail0 == 0x7fffffff ? si.n : max(si.tail0, 0);
+        const int a = (int)(reach / BWD_BN) + 1, b = min(resume_row / BWD_BN, nq);
+        if (a < b) { gap_a = a; gap_b = b; }
+      }
+    }
+    auto next_tile = [&](int t) { return t + 1 == gap_a ? gap_b : t + 1; };
+    auto tiles_left = [&](int t) { return t < gap_a ? (gap_a - t) + (nq - gap_b) : nq - t; };  // from t on, t included
 
     auto issue_tile = [&](int it, auto buf_tag) __attribute__((always_inline)) {
       constexpr int BUF = decltype(buf_tag)::value;
@@ -801,21 +817,21 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     while (it < nq) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      int nxt = it + 1;
+      int nxt = next_tile(it);
       float band_nxt = 0.f;
       if (HAS_RAB && nxt < nq) band_nxt = band_of(nxt);
       if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 1>{});
-      draw_step(nq - it);
+      draw_step(tiles_left(it));
       compute_tile(it, std::integral_constant<int, 0>{});
       if (HAS_RAB && nxt < nq) bwd_band_store<false>(band1, band_nxt, tid, bias_mul);
       it = nxt;
       if (it >= nq) break;
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      nxt = it + 1;
+      nxt = next_tile(it);
       if (HAS_RAB && nxt < nq) band_nxt = band_of(nxt);
       if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 0>{});
-      draw_step(nq - it);
+      draw_step(tiles_left(it));
       compute_tile(it, std::integral_constant<int, 1>{});
       if (HAS_RAB && nxt < nq) bwd_band_store<false>(band0, band_nxt, tid, bias_mul);
       it = nxt;

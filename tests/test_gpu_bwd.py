@@ -628,6 +628,34 @@ def test_bias_table_gradient_far_from_unit_scale(oracle, dout_mul, v_mul):
     assert not drab.cpu().numpy()[np.asarray(want[3]) == 0].any()
 
 
+def test_bias_table_gradient_with_one_outlier_in_v(oracle):
+    """One value of v a thousand times the rest coarsens the fixed-point resolution of every item (the
+    scale follows the call's largest |v|); the terms are rounded to nearest, so what is left is noise
+    without a sign: the table's gradient stays inside the bf16 bounds, whole tensor and per head."""
+    import recir_amd
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([300, 129, 64, 517], [40, 129, 0, 6], 2, 128, 128, max_seq_len=600, alpha=1 / 128,
+                     dtype="bf16", seed=93, with_rab=True, rab_std=0.5, contextual_seq_len=3, tail_rows=2)
+    wl.v[401, 1, 17] = 1.0e3
+    dout = torch.randn(wl.T, wl.H, 128, generator=torch.Generator().manual_seed(13)).bfloat16().float()
+    q, k, v, off, nt = to_device(wl)
+    kw = dict(max_seq_len=wl.max_seq_len, alpha=wl.alpha, contextual_seq_len=3, rab=wl.rab.cuda())
+    drab = recir_amd.jagged_hstu_attention_backward(dout.to(q.device, q.dtype), q, k, v, off, nt, rab_grad=True, **kw)[3]
+    torch.cuda.synchronize()
+    assert _lib.last_kernel() == "bwd_tiled_d128_bf16_rab"
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha, rab=wl.rab.numpy(),
+                           contextual_seq_len=3, rab_grad=True)[3]
+    st = error_stats(drab, want)
+    print(f"[parity] d rab with one outlier in v: {st}", flush=True)
+    assert st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL and st["worst_row_rel"] <= BF16_REL, st
+    # no bias towards zero: the summed error is small against the summed magnitude
+    err = drab.double().cpu().numpy() - np.asarray(want, dtype=np.float64)
+    assert abs(err.sum()) <= 1e-3 * np.abs(want).sum(), (err.sum(), np.abs(want).sum())
+
+
 def test_bias_table_gradient_of_non_finite_input_is_not_finite():
     """A NaN in dout must not come out as a plausible number (the fixed-point sums cannot carry it: the
     scale is then zero and the flushed values are NaN)."""
