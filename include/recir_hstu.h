@@ -61,6 +61,15 @@ extern "C" {
                                                      of full_attn_size and the contextual keys as in
                                                      the causal case.  Generic kernels only (any head
                                                      dim, bf16 or fp32; forward and backward).       */
+#define RECIR_HSTU_FLAG_TILED_ONLY 0x40000u       /* reject (RECIR_HSTU_ERR_UNSUPPORTED, with the reason
+                                                     in recir_hstu_last_error) a call that only the
+                                                     generic kernels cover -- one wave per (token,
+                                                     head), tens of times slower than the MFMA
+                                                     kernels -- instead of running it there: fp32
+                                                     tensors, head dims other than 128, tensors not
+                                                     16-byte aligned, the mask of
+                                                     RECIR_HSTU_FLAG_MASK_NONCAUSAL, a bias with
+                                                     alpha = 0.  Forward and backward.               */
 #define RECIR_HSTU_FLAG_KERNEL_SHIFT 8            /* bits 8..15: kernel selector for tests/tuning  */
 #define RECIR_HSTU_FLAG_KERNEL_MASK 0xff00u       /* 0 auto, 1 generic, 2.. tiled variants         */
 

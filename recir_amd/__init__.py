@@ -16,6 +16,7 @@ from .ops import (  # noqa: F401
     register_swaps,
     plan_cache_scope,
     set_plan_cache,
+    set_generic_kernel_policy,
     hstu_attention_matcher,
     attention_via_fp8,
     attention_via_fp8_reference_rule,
@@ -48,6 +49,7 @@ __all__ = [
     "register_swaps",
     "plan_cache_scope",
     "set_plan_cache",
+    "set_generic_kernel_policy",
     "hstu_attention_matcher",
     "attention_via_fp8",
     "attention_via_fp8_reference_rule",

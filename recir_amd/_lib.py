@@ -21,6 +21,7 @@ FLAG_SCALE_PER_TOKEN = 0x4
 FLAG_REUSE_PLAN = 0x8
 FLAG_GROUPED_LISTS = 0x10000
 FLAG_MASK_NONCAUSAL = 0x20000
+FLAG_TILED_ONLY = 0x40000
 FLAG_KERNEL_SHIFT = 8
 NOALLOC_SCRATCH_BYTES = 4 << 20
 

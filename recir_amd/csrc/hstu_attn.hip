@@ -513,6 +513,11 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
 
   if (dtype == RECIR_HSTU_DTYPE_FP8_E4M3)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "fp8 q/k is implemented for Dqk = Dv = 128 only");
+  if (flags & RECIR_HSTU_FLAG_TILED_ONLY)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED,
+                "only the generic kernel covers this call (the MFMA kernels need bf16 or fp8 q/k, Dqk = Dv = 128, 16-byte aligned "
+                "tensors, the causal or semi-local mask, and alpha != 0 with a bias): dtype=%d Dqk=%d Dv=%d",
+                dtype, Dqk, Dv);
   if (Dqk > GENERIC_MAX_D || Dv > GENERIC_MAX_D)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "head dims above %d are not supported (Dqk=%d Dv=%d)", GENERIC_MAX_D, Dqk, Dv);
   if (H > 65535) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "more than 65535 heads");
@@ -721,6 +726,10 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     g_last_kernel = rab ? "bwd_tiled_d128_bf16_rab" : "bwd_tiled_d128_bf16";
     return RECIR_HSTU_OK;
   }
+  if (flags & RECIR_HSTU_FLAG_TILED_ONLY)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED,
+                "only the generic kernels cover this call (the MFMA kernels need bf16, Dqk = Dv = 128, 16-byte aligned tensors, "
+                "the causal or semi-local mask, and alpha != 0 with a bias): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
   const dim3 grid((unsigned)T, (unsigned)H);
   if (bf16) {
     hipLaunchKernelGGL(hstu_bwd_generic_dq<true>, grid, dim3(64), 0, stream, bp);

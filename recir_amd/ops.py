@@ -17,6 +17,7 @@ from __future__ import annotations
 import collections
 import math
 import threading
+import warnings
 from typing import Optional, Tuple
 
 import torch
@@ -38,6 +39,44 @@ class _CallState(threading.local):
 
 
 _state = _CallState()
+
+# What happens when a bf16 call can only run on the generic kernels (one wave per token and head, tens of
+# times slower than the MFMA kernels: head dims other than 128, unaligned tensors, a mask type other than
+# "lower_triangular", a bias with alpha = 0): "warn" (once per process and reason), "error" (the C ABI
+# rejects the call, RECIR_HSTU_FLAG_TILED_ONLY) or "silent".  fp32 tensors are the smoke path and never warn.
+_generic_policy = "warn"
+_generic_warned = set()
+
+
+def set_generic_kernel_policy(policy: str) -> str:
+    """Choose what a bf16 call that only the slow generic kernels cover does: ``"warn"`` (default),
+    ``"error"`` or ``"silent"``.  Returns the previous setting."""
+    global _generic_policy
+    if policy not in ("warn", "error", "silent"):
+        raise ValueError("policy must be 'warn', 'error' or 'silent'")
+    prev, _generic_policy = _generic_policy, policy
+    return prev
+
+
+def _note_generic(kernel: str, q, v, mask_type, alpha, rab) -> None:
+    if _generic_policy != "warn" or not kernel.startswith(("generic_bf16", "bwd_generic_bf16")):
+        return
+    if _state.forced_kernel == KERNEL_GENERIC:
+        return
+    if q.shape[2] != 128 or v.shape[2] != 128:
+        reason = f"head dims {q.shape[2]} / {v.shape[2]} (the MFMA kernels take 128 / 128)"
+    elif mask_type != "lower_triangular":
+        reason = f"mask type '{mask_type}'"
+    elif rab is not None and alpha == 0:
+        reason = "a bias with alpha = 0"
+    else:
+        reason = "tensors that are not 16-byte aligned"
+    if reason in _generic_warned:
+        return
+    _generic_warned.add(reason)
+    warnings.warn(f"recir HSTU attention ran on the generic kernel ({kernel}), tens of times slower than the MFMA "
+                  f"kernels, because of {reason}; recir_amd.set_generic_kernel_policy('error') rejects such calls, "
+                  f"'silent' stops this message", RuntimeWarning, stacklevel=3)
 
 
 class extra_flags:
@@ -201,6 +240,8 @@ def _prepare(opname, q, k, v, seq_offsets, num_targets, attn_scale, rab, N, ctx_
         flags |= _lib.FLAG_CTX_REFERENCE
     flags |= (_state.forced_kernel & 0xFF) << _lib.FLAG_KERNEL_SHIFT
     flags |= _state.extra_flags
+    if _generic_policy == "error" and q.dtype != torch.float32 and _state.forced_kernel != KERNEL_GENERIC:
+        flags |= _lib.FLAG_TILED_ONLY
     if mask_type != "lower_triangular":
         # any other string selects the reference's other branch (kjt_split_per_feature.cpp:650-660)
         flags |= _lib.FLAG_MASK_NONCAUSAL
@@ -336,6 +377,7 @@ def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale
             with _plan_cache_lock:
                 _plan_cache.pop(key, None)
         _raise_status("recir_hstu_attn_fwd", rc)
+    _note_generic(_lib.last_kernel(), q, v, mask_type, alpha, rab)
     return out
 
 
@@ -391,6 +433,7 @@ def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, c
             with _plan_cache_lock:
                 _plan_cache.pop(key, None)
         _raise_status("recir_hstu_attn_bwd", rc)
+    _note_generic(_lib.last_kernel(), q, v, mask_type, alpha, rab)
     return (dq, dk, dv, drab) if rab_grad else (dq, dk, dv)
 
 

@@ -583,6 +583,55 @@ def test_fp8_region_swap_keeps_the_reference_contextual_rule(oracle):
         assert st["max_abs"] <= FP8_MAX_ABS, st
 
 
+def test_generic_kernel_policy_warns_or_rejects(oracle):
+    """A bf16 call that only the slow generic kernels cover (here: head dim 64) says so once by default,
+    is rejected by the C ABI under the 'error' policy (RECIR_HSTU_FLAG_TILED_ONLY), and is silent under
+    'silent'; the result is the oracle's in every case that runs.  fp32 calls never warn."""
+    import warnings
+
+    import recir_amd
+    from recir_amd import _lib, ops
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([70, 33, 0, 129], [8, 33, 0, 3], 2, 64, 64, max_seq_len=160, alpha=1.0 / 64, dtype="bf16", seed=41)
+    want = run_oracle(oracle, wl)
+    ops._generic_warned.clear()
+    prev = recir_amd.set_generic_kernel_policy("warn")
+    try:
+        with warnings.catch_warnings(record=True) as rec:
+            warnings.simplefilter("always")
+            out = run_hip(wl)
+            out2 = run_hip(wl)
+        assert _lib.last_kernel() == "generic_bf16"
+        msgs = [str(w.message) for w in rec if issubclass(w.category, RuntimeWarning)]
+        assert len(msgs) == 1 and "head dims 64 / 64" in msgs[0], msgs  # once per reason
+        assert_bf16_close(out, want, "generic kernel, head dim 64")
+        assert torch.equal(out, out2)
+        recir_amd.set_generic_kernel_policy("error")
+        with pytest.raises(ValueError, match="only the generic kernel"):
+            run_hip(wl)
+        with ops.force_kernel(ops.KERNEL_GENERIC):  # an explicit choice of the generic kernel is not rejected
+            assert torch.equal(run_hip(wl), out)
+        # a call the MFMA kernels cover passes under the same policy
+        wl128 = make_jagged([70, 33], [8, 33], 2, 128, 128, max_seq_len=160, alpha=1.0 / 128, dtype="bf16", seed=42)
+        assert_bf16_close(run_hip(wl128), run_oracle(oracle, wl128), "tiled kernel under the error policy")
+        assert _lib.last_kernel() == "tiled_d128_bf16"
+        recir_amd.set_generic_kernel_policy("silent")
+        ops._generic_warned.clear()
+        with warnings.catch_warnings(record=True) as rec:
+            warnings.simplefilter("always")
+            run_hip(wl)
+        assert not [w for w in rec if issubclass(w.category, RuntimeWarning)]
+        recir_amd.set_generic_kernel_policy("warn")
+        with warnings.catch_warnings(record=True) as rec:  # the fp32 smoke path is the generic kernel by design
+            warnings.simplefilter("always")
+            wl32 = make_jagged([20, 20], [4, 4], 2, 32, 32, max_seq_len=20, alpha=1.0 / 32, dtype="fp32", seed=43)
+            run_hip(wl32)
+        assert not [w for w in rec if issubclass(w.category, RuntimeWarning)]
+    finally:
+        recir_amd.set_generic_kernel_policy(prev)
+
+
 def test_semilocal_full_size_matches_oracle(oracle):
     """Configuration 2 with the reference's semi-local shape (256 local + 256 full tail): the tiled
     kernel (which skips key tiles below the window) against the oracle."""
