@@ -382,7 +382,10 @@ def bench_backward(args, wl, L, dev):
     T, H, Dqk = q.shape
     Dv = v.shape[2]
     code = _lib.DTYPE_FP32 if wl.dtype == "fp32" else _lib.DTYPE_BF16
-    ws = torch.empty((max(L.recir_hstu_attn_bwd_workspace_bytes(T, wl.B, H, Dqk, Dv, code), 16),), dtype=torch.uint8, device=dev)
+    ws_bytes = L.recir_hstu_attn_bwd_workspace_bytes(T, wl.B, H, Dqk, Dv, code)
+    if drab is not None:
+        ws_bytes += L.recir_hstu_attn_bwd_rab_grad_workspace_bytes(H, wl.max_seq_len)
+    ws = torch.empty((max(ws_bytes, 16),), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
     flags0 = (args.kernel & 0xFF) << _lib.FLAG_KERNEL_SHIFT
 

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define RECIR_HSTU_ABI_VERSION 4
+#define RECIR_HSTU_ABI_VERSION 5
 
 /* element types of q/k (v and out follow: bf16 for BF16 and FP8_E4M3, fp32 for FP32) */
 #define RECIR_HSTU_DTYPE_BF16 0
@@ -160,12 +160,15 @@ size_t recir_hstu_attn_fwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int3
  * rab           enters S as in the forward
  * drab          device float [H, 2*max_seq_len-1] or NULL: gradient of rab (needs rab),
  *               drab[h, i] = sum of dS(m, j) over the kept pairs of all sequences with
- *               m - j + max_seq_len - 1 == i.  Written in full (zeroed first); accumulated with
- *               float atomics, so its last bits may differ from run to run, unlike dq, dk and dv.
- *               No counterpart in the reference (which has no rab).  No gradient is produced for
- *               attn_scale.
+ *               m - j + max_seq_len - 1 == i.  Written in full.  The MFMA kernels sum in fixed
+ *               point (one power-of-two scale per head, from the head's largest |dout| and the
+ *               call's largest |v|; integer additions, so the result is the same bit for bit
+ *               whatever the order of the workgroups, like dq, dk and dv); the generic kernels add
+ *               floats atomically and may differ in the last bits from run to run.  No counterpart in
+ *               the reference (which has no rab).  No gradient is produced for attn_scale.
  * attn_scale, flags, sizes, workspace, hip_stream: as for the forward; workspace of at least
- *               recir_hstu_attn_bwd_workspace_bytes(...) bytes
+ *               recir_hstu_attn_bwd_workspace_bytes(...) bytes, plus, with drab,
+ *               recir_hstu_attn_bwd_rab_grad_workspace_bytes(H, max_seq_len)
  */
 int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const void* v, void* dq,
                         void* dk, void* dv, float* drab, const void* seq_offsets, const void* num_targets,
@@ -173,6 +176,10 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
                         int32_t Dqk, int32_t Dv, int32_t max_seq_len, int32_t contextual_seq_len,
                         int32_t max_attn_len, int32_t full_attn_size, float alpha, int32_t dtype,
                         uint32_t flags, void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* Additional scratch recir_hstu_attn_bwd needs when drab is requested (the fixed-point table of the
+ * sums along the diagonals and the per-head maxima of dout), appended to the scratch below. */
+size_t recir_hstu_attn_bwd_rab_grad_workspace_bytes(int32_t H, int32_t max_seq_len);
 
 /* Scratch size recir_hstu_attn_bwd needs for these sizes. */
 size_t recir_hstu_attn_bwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk,

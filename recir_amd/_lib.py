@@ -9,7 +9,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 # elsewhere, A/B measurements of two builds); there is still no fallback if it is missing
 LIB_PATH = os.environ.get("RECIR_HSTU_LIB") or os.path.join(_PKG, "librecir_hstu.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_BF16 = 0
 DTYPE_FP32 = 1
@@ -32,6 +32,7 @@ EXPORTS = (
     "recir_hstu_attn_fwd_workspace_bytes",
     "recir_hstu_attn_bwd",
     "recir_hstu_attn_bwd_workspace_bytes",
+    "recir_hstu_attn_bwd_rab_grad_workspace_bytes",
     "recir_hstu_quantize_e4m3_per_head",
     "recir_hstu_quantize_e4m3_per_head_rows",
     "recir_hstu_calibration_copy",
@@ -79,6 +80,8 @@ def load() -> ctypes.CDLL:
     L.recir_hstu_attn_bwd.restype = ctypes.c_int
     L.recir_hstu_attn_bwd_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     L.recir_hstu_attn_bwd_workspace_bytes.restype = sz
+    L.recir_hstu_attn_bwd_rab_grad_workspace_bytes.argtypes = [i32, i32]
+    L.recir_hstu_attn_bwd_rab_grad_workspace_bytes.restype = sz
     L.recir_hstu_quantize_e4m3_per_head.argtypes = [vp, vp, vp, i32, i32, i32, vp]
     L.recir_hstu_quantize_e4m3_per_head.restype = ctypes.c_int
     L.recir_hstu_quantize_e4m3_per_head_rows.argtypes = [vp, vp, vp, i32, i32, i32, vp, i32, u32, vp]

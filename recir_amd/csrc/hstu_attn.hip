@@ -596,11 +596,18 @@ int recir_hstu_attn_fwd_noalloc(const void* q, const void* k, const void* v, voi
                              (size_t)RECIR_HSTU_NOALLOC_SCRATCH_BYTES, hip_stream);
 }
 
-constexpr size_t BWD_WS_TAIL = 256;  // behind the two lists: the largest |v| of the call (see drab)
+constexpr size_t BWD_WS_TAIL = 256;  // behind the two lists: the largest |v| and |per-token scale| of the call (see drab)
 size_t recir_hstu_attn_bwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int32_t Dqk, int32_t Dv,
                                            int32_t dtype) {
   // two work lists: query tiles for dQ, key tiles for dK/dV
   return 2 * ((recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype) + 255) & ~(size_t)255) + BWD_WS_TAIL;
+}
+
+// behind that, with drab: [H] largest |dout| per head, then the [H, 2N-1] fixed-point table
+static size_t drab_head_words_bytes(int32_t H) { return (((size_t)H * 4) + 255) & ~(size_t)255; }
+size_t recir_hstu_attn_bwd_rab_grad_workspace_bytes(int32_t H, int32_t max_seq_len) {
+  if (H <= 0 || max_seq_len <= 0) return 0;
+  return drab_head_words_bytes(H) + (size_t)H * (2 * (size_t)max_seq_len - 1) * sizeof(long long);
 }
 
 int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const void* v, void* dq,
@@ -622,12 +629,15 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     return fail(dtype == RECIR_HSTU_DTYPE_FP8_E4M3 ? RECIR_HSTU_ERR_UNSUPPORTED : RECIR_HSTU_ERR_INVALID_ARGUMENT,
                 "backward supports bf16 and fp32 tensors, got dtype %d", dtype);
   if (drab && !rab) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "drab (the gradient of rab) needs rab");
-  if (drab) {  // written in full whatever follows: zeros, then the kernels add
+  // drab is written in full whatever follows: by the last kernel of the MFMA path, and on every other
+  // path as zeros first, to which the generic kernel adds
+  auto zero_drab = [&]() -> int {
+    if (!drab) return 0;
     const size_t n = (size_t)H * (2 * (size_t)max_seq_len - 1);
     hipLaunchKernelGGL(hstu_fill_zero, dim3(64), dim3(256), 0, stream, (unsigned short*)drab, n * 2);
-    if (int rc = launch_status("hstu_fill_zero")) return rc;
-  }
-  if (T == 0) return RECIR_HSTU_OK;
+    return launch_status("hstu_fill_zero");
+  };
+  if (T == 0) return zero_drab();
   if (!dout || !q || !k || !v || !dq || !dk || !dv)
     return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "dout, q, k, v, dq, dk, dv must be non-null");
   if (!seq_offsets) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "seq_offsets must be non-null");
@@ -647,6 +657,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   const bool bf16 = dtype == RECIR_HSTU_DTYPE_BF16;
   const size_t esz = bf16 ? 2 : 4;
   if (B == 0) {
+    if (int rc = zero_drab()) return rc;
     void* outs[3] = {dq, dk, dv};
     const int dims[3] = {Dqk, Dqk, Dv};
     for (int i = 0; i < 3; ++i) {
@@ -711,18 +722,46 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
         }
       }
     }
+    const bool per_token = attn_scale && (flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
     if (drab) {
-      // The query-tile kernel sums dS along the diagonals in LDS as fixed-point integers (LDS float
-      // atomics run one lane at a time); the scale comes from a bound on |dS|, which needs the largest
-      // magnitude of v: the key-tile kernel, which runs first and holds every v row once, leaves it here.
+      // The query-tile kernel sums dS along the diagonals as fixed-point integers, in LDS (float LDS
+      // atomics run one lane at a time) and then in a 64-bit table per head (integer additions commute:
+      // the gradient does not depend on the order of the workgroups).  The scale of a head comes from a
+      // bound on |dS|: the head's largest |dout| (a pass over dout, here), the call's largest |v| (the
+      // key-tile kernel, which runs first and holds every v row once, leaves it in word 1) and, with a
+      // per-token output scale, its largest magnitude (word 2).
+      const size_t base = 2 * half_ws + BWD_WS_TAIL;
+      const size_t need = base + recir_hstu_attn_bwd_rab_grad_workspace_bytes(H, max_seq_len);
+      if (workspace_bytes < need)
+        return fail(RECIR_HSTU_ERR_WORKSPACE,
+                    "with drab the workspace must hold recir_hstu_attn_bwd_workspace_bytes + "
+                    "recir_hstu_attn_bwd_rab_grad_workspace_bytes = %zu bytes, got %zu", need, workspace_bytes);
       unsigned* am = (unsigned*)((char*)workspace + 2 * half_ws);
-      hipLaunchKernelGGL(hstu_fill_zero, dim3(1), dim3(64), 0, stream, (unsigned short*)am, (size_t)4);
-      if (int rc = launch_status("hstu_fill_zero")) return rc;
+      unsigned* dmax = (unsigned*)((char*)workspace + base);
+      long long* tab = (long long*)((char*)workspace + base + drab_head_words_bytes(H));
+      const size_t tab_words = (size_t)H * (2 * (size_t)max_seq_len - 1);
+      hipLaunchKernelGGL(hstu_drab_prepare, dim3(128), dim3(256), 0, stream, am, dmax, H, tab, tab_words);
+      if (int rc = launch_status("hstu_drab_prepare")) return rc;
+      const int i32 = (flags & RECIR_HSTU_FLAG_OFFSETS_I32) ? 1 : 0;
+      const void* seq_end = (const char*)seq_offsets + (size_t)B * (i32 ? 4 : 8);
+      const size_t n8 = (size_t)T * H * (HD / 8);
+      const unsigned blocks = (unsigned)((n8 + 255) / 256 < 256 ? (n8 + 255) / 256 : 256);  // (each ends with H global atomics)
+      const int h_mask = (H & (H - 1)) == 0 ? H - 1 : -1;
+      hipLaunchKernelGGL(hstu_quant_amax, dim3(blocks), dim3(256), 0, stream, (const u32x4*)dout, dmax, (unsigned*)nullptr, n8, H, HD / 8, 4,
+                         h_mask, seq_end, i32, T);
+      if (per_token) hipLaunchKernelGGL(hstu_scale_absmax, dim3(64), dim3(256), 0, stream, attn_scale, seq_end, i32, T, am + 2);
+      if (int rc = launch_status("hstu_quant_amax")) return rc;
       bq.absmax = bk.absmax = am;
+      bq.dout_max = dmax;
+      bq.drab_fx = tab;
     }
     const dim3 grid((unsigned)(slots * NUM_XCD)), grid_k((unsigned)(kslots * NUM_XCD));
     launch_bwd_tiled(semi, rab != nullptr, grid, grid_k, stream, bk, bq);
     if (int rc = launch_status("hstu_bwd_d128")) return rc;
+    if (drab) {
+      hipLaunchKernelGGL(hstu_drab_finalize, dim3(256), dim3(256), 0, stream, bq, per_token ? 1 : 0);
+      if (int rc = launch_status("hstu_drab_finalize")) return rc;
+    }
     g_last_kernel = rab ? "bwd_tiled_d128_bf16_rab" : "bwd_tiled_d128_bf16";
     return RECIR_HSTU_OK;
   }
@@ -730,6 +769,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
                 "only the generic kernels cover this call (the MFMA kernels need bf16, Dqk = Dv = 128, 16-byte aligned tensors, "
                 "the causal or semi-local mask, and alpha != 0 with a bias): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
+  if (int rc = zero_drab()) return rc;
   const dim3 grid((unsigned)T, (unsigned)H);
   if (bf16) {
     hipLaunchKernelGGL(hstu_bwd_generic_dq<true>, grid, dim3(64), 0, stream, bp);

@@ -210,13 +210,12 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
   if (RAB_GRAD && tid < BWD_BAND) { gband0[tid] = 0.f; gband1[tid] = 0.f; }  // published by the first tile's barrier
   // Gradient of the bias table: the sums along the diagonals are kept in LDS as fixed-point integers.  An LDS float atomic takes three cycles per lane, one lane at a time
   // (192 cycles for a wave's instruction), an integer one 4-16 cycles for the whole instruction.  The
-  // scale is a power of two, chosen per item so that a tile's sum cannot overflow: |dS| <= 1.1 |dP|,
-  // |dP| <= 128 max|dout row of the item| max|v| (times the largest per-token scale of the item's rows,
-  // where there is one), and a diagonal meets at most 64 pairs of a (128-row, 64-key) tile.  What the conversion drops is below 2^-30 of that bound per pair.
-  // Non-finite inputs make the scale zero and every flushed value NaN.
+  // scale is a power of two per head, the same for every item of the call (drab_fx_bound): the tile
+  // sums are flushed as 64-bit integer additions to a table of the same scale, so the result does not
+  // depend on the order in which tiles and workgroups arrive, and a last kernel turns the table into
+  // floats.  What the conversion drops is below 2^-30 of the bound per pair, rounded to nearest.
+  // Non-finite inputs make the scale zero and every value of the head NaN.
   constexpr bool FIXED = RAB_GRAD;
-  __shared__ unsigned do_max_s[4];  // per wave: largest |dout| magnitude of its rows of the item
-  __shared__ float rs_max_s[4];     // per wave: largest |per-token scale| of its rows
   float fx_scale = 0.f, fx_inv = 0.f;
 
   const int xcd = blockIdx.x % NUM_XCD;
@@ -292,17 +291,6 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     constexpr bool per_token = PER_TOKEN;
     const float row_scale = per_token ? p.attn_scale[si.s + min(m, si.n - 1)] : 1.0f;
     bwd_load_row_frags(bp.dout, (size_t)si.s + m, p.H, h, half, m < q_end, false, 1.0f, gf);
-    if constexpr (FIXED) {  // read after the first tile's barrier
-      unsigned mx = bwd_frag_absmax(gf);
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) mx = max(mx, (unsigned)__shfl_xor((int)mx, d, 64));
-      float rs = per_token ? __builtin_fabsf(row_scale) : 1.0f;
-      if (per_token) {
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) rs = fmaxf(rs, __shfl_xor(rs, d, 64));
-      }
-      if (lane == 0) { do_max_s[wave] = mx; rs_max_s[wave] = rs; }
-    }
     const float score_c = p.alpha * kLog2e, neg_c = -score_c;
     // the bias is staged multiplied by log2(e) and joins the score in the multiply-add that applies alpha log2(e)
     const float bias_mul = kLog2e;
@@ -417,17 +405,16 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       else tile_body(std::integral_constant<int, 1>{}, buf_tag, k0);
     };
 
-    // Gradient band of a finished key tile t -> drab (entry 190 - i of the stage is rab index
-    // first + i, as in the bias band), and the stage is cleared for the tile after the next.  The
-    // global scale of P (not the per-token one, which the dO rows carry) comes in here.
-    const float drab_scale = per_token ? 1.0f : bwd_output_scale(p);
+    // Gradient band of a finished key tile t -> the head's fixed-point table (entry 190 - i of the
+    // stage is rab index first + i, as in the bias band), and the stage is cleared for the tile after
+    // the next.  Integer additions: the table does not depend on who arrives first.
     auto flush_gband = [&](int t, float* g) __attribute__((always_inline)) {
       if (tid < BWD_BAND - 1) {
-        float val = g[(BWD_BAND - 2) - tid];
-        if constexpr (FIXED) val = (float)__float_as_int(val) * fx_inv;  // (NaN for every entry when the inputs are not finite)
+        const int iv = __float_as_int(g[(BWD_BAND - 2) - tid]);
         g[(BWD_BAND - 2) - tid] = 0.f;
         const int idx = q0 - t * BWD_BN - (BWD_BN - 1) + p.N - 1 + tid;
-        if (val != 0.f && idx >= 0 && idx < rab_w) unsafeAtomicAdd(&bp.drab[(size_t)h * rab_w + idx], val * drab_scale);
+        if (iv != 0 && idx >= 0 && idx < rab_w)
+          atomicAdd((unsigned long long*)&bp.drab_fx[(size_t)h * rab_w + idx], (unsigned long long)(long long)iv);
       }
     };
     int prev_tile = -1;
@@ -437,17 +424,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile `it` have landed
       __syncthreads();                                   // everybody's; the other stage is free again
       if constexpr (FIXED) {
-        if (prev_tile < 0) {  // first tile of the item: the fixed-point scale of its diagonal sums
-          const unsigned dmx = max(max(do_max_s[0], do_max_s[1]), max(do_max_s[2], do_max_s[3]));
-          const float rmx = fmaxf(fmaxf(rs_max_s[0], rs_max_s[1]), fmaxf(rs_max_s[2], rs_max_s[3]));
-          const float bound = __uint_as_float(dmx << 16) * __uint_as_float(__hip_atomic_load(bp.absmax + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) *
-                              rmx * (128.0f * 1.1f * 64.0f);
-          const int eb = (int)((__float_as_uint(bound) >> 23) & 0xffu) - 126;  // bound < 2^eb
-          const bool usable = bound > 0.f && bound < 3.0e38f;
-          const int sh = min(max(30 - eb, -120), 120);
-          fx_scale = usable ? __uint_as_float((unsigned)(127 + sh) << 23) : 0.f;
-          fx_inv = usable ? __uint_as_float((unsigned)(127 - sh) << 23) : (bound == 0.f ? 0.f : __uint_as_float(0x7fc00000u));
-        }
+        if (prev_tile < 0) drab_fx_scales(drab_fx_bound(bp, h, per_token), fx_scale, fx_inv);  // (the head's scale)
       }
       if (RAB_GRAD && prev_tile >= 0) flush_gband(prev_tile, gband1);
       int nxt = next_tile(it);
@@ -879,6 +856,46 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       wi.q0 = uni(next_rec[4]); wi.h = uni(next_rec[5]); wi.b = uni(next_rec[6]); wi.q_end = uni(next_rec[7]);
     }
     __syncthreads();  // next_rec is written again during the item
+  }
+}
+
+// Everything the bias-table gradient accumulates into, cleared by one launch: the three maxima words,
+// the per-head maxima of dout and the fixed-point table.
+__global__ __launch_bounds__(256) void hstu_drab_prepare(unsigned* am, unsigned* dout_max, int H, long long* tab, size_t tab_words) {
+  const size_t first = (size_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = first; i < tab_words; i += stride) tab[i] = 0;
+  if (blockIdx.x == 0) {
+    if (threadIdx.x < 4) am[threadIdx.x] = 0u;
+    for (int h = threadIdx.x; h < H; h += blockDim.x) dout_max[h] = 0u;
+  }
+}
+
+// Largest |attn_scale[r]| over the rows of the sequences (per-token scale), as the bits of a float,
+// merged into *out with an integer maximum (the bits of non-negative floats order like integers;
+// a NaN's bits are above every finite value's, so it ends up in the bound and makes it unusable).
+__global__ __launch_bounds__(256) void hstu_scale_absmax(const float* scale, const void* seq_end, int i32, int T, unsigned* out) {
+  const long long e = i32 ? (long long)*(const int*)seq_end : *(const long long*)seq_end;
+  const int rows = (int)(e < 0 ? 0 : (e > T ? T : e));
+  unsigned mx = 0;
+  for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x)
+    mx = max(mx, __float_as_uint(scale[r]) & 0x7fffffffu);
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) mx = max(mx, (unsigned)__shfl_xor((int)mx, d, 64));
+  if ((threadIdx.x & 63) == 0 && mx) atomicMax(out, mx);
+}
+
+// Fixed-point table of the bias-table gradient -> drab[h, i] in floats: the head's scale taken out,
+// then the global output scale of P (a per-token scale is already inside the sums).
+__global__ __launch_bounds__(256) void hstu_drab_finalize(BwdParams bp, int per_token) {
+  const Params& p = bp.f;
+  const int rab_w = 2 * p.N - 1;
+  const size_t n = (size_t)p.H * rab_w;
+  const float out_scale = per_token ? 1.0f : bwd_output_scale(p);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const int h = (int)(i / rab_w);
+    float fx_scale, fx_inv;
+    drab_fx_scales(drab_fx_bound(bp, h, per_token != 0), fx_scale, fx_inv);
+    bp.drab[i] = (float)((double)bp.drab_fx[i]) * fx_inv * out_scale;
   }
 }
 

@@ -420,8 +420,11 @@ def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, c
     if T == 0:
         return (dq, dk, dv, drab) if rab_grad else (dq, dk, dv)
     ws_bytes = L.recir_hstu_attn_bwd_workspace_bytes(T, B, H, Dqk, Dv, code)
+    if rab_grad:  # the fixed-point table of the sums along the diagonals, behind the work lists
+        ws_bytes += L.recir_hstu_attn_bwd_rab_grad_workspace_bytes(H, int(N))
     stream = torch.cuda.current_stream(dev).cuda_stream
-    layout = (T, B, H, Dqk, Dv, code, int(N), int(contextual_seq_len), int(max_attn_len), int(full_attn_size), flags)
+    layout = (T, B, H, Dqk, Dv, code, int(N), int(contextual_seq_len), int(max_attn_len), int(full_attn_size), flags,
+              bool(rab_grad))
     ws, reuse, key = _workspace("bwd", seq_offsets, num_targets, layout, ws_bytes, dev, stream)
     with torch.cuda.device(dev):
         rc = L.recir_hstu_attn_bwd(_ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(drab),

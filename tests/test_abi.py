@@ -53,7 +53,7 @@ def test_jagged_header_symbols_are_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.recir_hstu_abi_version() == 4
+    assert lib.recir_hstu_abi_version() == 5
 
 
 def test_workspace_size_is_host_arithmetic(lib):

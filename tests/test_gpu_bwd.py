@@ -628,6 +628,77 @@ def test_bias_table_gradient_far_from_unit_scale(oracle, dout_mul, v_mul):
     assert not drab.cpu().numpy()[np.asarray(want[3]) == 0].any()
 
 
+@pytest.mark.parametrize("per_token", [False, True])
+def test_bias_table_gradient_is_the_same_bit_for_bit_whatever_the_order(oracle, per_token):
+    """The tiled kernels sum the table's gradient in fixed point with one scale per head: repeated
+    calls, and a call whose work lists are ordered differently (grouped lists), give the same bits --
+    the property the reference asks of its kernels (block-size invariance,
+    recir/ops/pallas/tests/test_jagged_hstu_attention.py:178-195).  Checked against the oracle too."""
+    import recir_amd
+    from recir_amd import _lib, ops
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([700, 129, 64, 1, 0, 517, 1000, 333], [40, 129, 0, 0, 0, 6, 64, 3], 4, 128, 128, max_seq_len=1024,
+                     alpha=1 / 128, dtype="bf16", seed=97, with_rab=True, rab_std=0.5, contextual_seq_len=3, tail_rows=2)
+    dout = torch.randn(wl.T, wl.H, 128, generator=torch.Generator().manual_seed(17)).bfloat16().float()
+    q, k, v, off, nt = to_device(wl)
+    sc = None
+    if per_token:
+        sc = (torch.rand(wl.T, generator=torch.Generator().manual_seed(18)) * 0.02 + 0.001)
+    kw = dict(max_seq_len=wl.max_seq_len, alpha=wl.alpha, contextual_seq_len=3, rab=wl.rab.cuda(),
+              attn_scale=None if sc is None else sc.cuda())
+
+    def run():
+        out = recir_amd.jagged_hstu_attention_backward(dout.to(q.device, q.dtype), q, k, v, off, nt, rab_grad=True, **kw)
+        torch.cuda.synchronize()
+        assert _lib.last_kernel() == "bwd_tiled_d128_bf16_rab"
+        return out[3].clone()
+
+    first = run()
+    for _ in range(4):
+        assert torch.equal(run(), first)
+    with ops.extra_flags(_lib.FLAG_GROUPED_LISTS):
+        assert torch.equal(run(), first)
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha, rab=wl.rab.numpy(),
+                           contextual_seq_len=3, rab_grad=True, attn_scale=None if sc is None else sc.numpy())[3]
+    st = error_stats(first, want)
+    print(f"[parity] d rab, fixed-point table, per_token={per_token}: {st}", flush=True)
+    assert st["ref_max"] > 0 and st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL, st
+
+
+def test_bias_table_gradient_needs_its_workspace():
+    """Through the C ABI: with drab the workspace must also hold the fixed-point table; a workspace of
+    the plain backward's size is rejected before any launch."""
+    import ctypes
+
+    from recir_amd import _lib
+
+    L = _lib.load()
+    T, B, H, N = 300, 2, 2, 256
+    dev = torch.device("cuda:0")
+    z = lambda: torch.zeros(T, H, 128, dtype=torch.bfloat16, device=dev)
+    q, k, v, dout, dq, dk, dv = (z() for _ in range(7))
+    off = torch.tensor([0, 200, 300], dtype=torch.int64, device=dev)
+    rab = torch.zeros(H, 2 * N - 1, dtype=torch.float32, device=dev)
+    drab = torch.empty_like(rab)
+    plain = L.recir_hstu_attn_bwd_workspace_bytes(T, B, H, 128, 128, _lib.DTYPE_BF16)
+    extra = L.recir_hstu_attn_bwd_rab_grad_workspace_bytes(H, N)
+    assert extra >= H * (2 * N - 1) * 8
+    ws = torch.empty(plain + extra, dtype=torch.uint8, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def call(nbytes):
+        return L.recir_hstu_attn_bwd(dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                                     dv.data_ptr(), drab.data_ptr(), off.data_ptr(), None, rab.data_ptr(), None, T, B, H, 128, 128,
+                                     N, 0, 0, 0, 1 / 128, _lib.DTYPE_BF16, 0, ws.data_ptr(), nbytes, st)
+
+    assert call(plain) == -3 and "recir_hstu_attn_bwd_rab_grad_workspace_bytes" in _lib.last_error()
+    assert call(plain + extra) == 0
+    torch.cuda.synchronize()
+    assert not drab.any()  # zero inputs: zero gradient, every entry written
+
+
 def test_bias_table_gradient_with_one_outlier_in_v(oracle):
     """One value of v a thousand times the rest coarsens the fixed-point resolution of every item (the
     scale follows the call's largest |v|); the terms are rounded to nearest, so what is left is noise
