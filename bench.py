@@ -137,7 +137,7 @@ def steady_state_warmup(call, stream, min_ms=MIN_WARMUP_MS):
     return spent
 
 
-CAL_KINDS = {0: "mfma_only", 1: "tile_loop_plain", 2: "tile_loop_skewed"}
+CAL_KINDS = {0: "mfma_only", 1: "tile_loop_plain", 2: "tile_loop_skewed", 3: "tile_loop_skewed_64_rows_per_wave"}
 CAL_PIECES = {0: "everything", 1: "no SiLU", 2: "no LDS fragment reads", 12: "no copies, no barrier", 14: "MFMAs and SiLU only"}
 
 
@@ -166,8 +166,10 @@ class CalibrationLoops:
         from recir_amd import _lib
 
         k, v, q = self.random if operands == "random" else self.zeros
+        # kind 3 holds 256 query rows per workgroup and one workgroup per CU: half the workgroups, the same work
+        wgs = self.WORKGROUPS // 2 if kind == 3 else self.WORKGROUPS
         rc = self.L.recir_hstu_calibration_mfma_loop(kind, pieces, k.data_ptr(), v.data_ptr(), q.data_ptr(), self.rows,
-                                                     self.SEQUENCES, tiles, self.WORKGROUPS, self.alpha,
+                                                     self.SEQUENCES, tiles, wgs, self.alpha,
                                                      self.stats.data_ptr(), self.sink.data_ptr(),
                                                      ctypes.c_void_p(self.stream.cuda_stream))
         if rc != 0:
@@ -195,7 +197,7 @@ class CalibrationLoops:
         e1.record(self.stream)
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / launches
-        st = self.stats.cpu().numpy().astype("float64")
+        st = self.stats.cpu().numpy().astype("float64")[: self.WORKGROUPS // 2 if kind == 3 else self.WORKGROUPS]
         flops = self.WORKGROUPS * tiles * 4 * 32 * 32768.0
         # a tile round: the two workgroups of a CU each finish one 128-row x 64-key tile
         return {"loop": CAL_KINDS[kind], "pieces": CAL_PIECES[pieces], "operands": operands, "tiles": tiles,
@@ -224,6 +226,9 @@ def bench_mfma_ceiling(args, L, dev):
             rows.append(cal.measure(kind, 0, operands))
         for pieces in (1, 2, 12, 14):
             rows.append(cal.measure(kind, pieces, "random"))
+    for operands in ("random", "zeros"):
+        rows.append(cal.measure(3, 0, operands))
+    rows.append(cal.measure(3, 2, "random"))
     print(json.dumps({"metric": "sustained bf16 MFMA rate of the calibration loops", "unit": "TFLOP/s", "n_gpus": 1,
                       "peak": PEAK_TFLOPS["bf16"], "workgroups": cal.WORKGROUPS, "loops": rows}))
 

@@ -221,8 +221,11 @@ int recir_hstu_calibration_copy(void* dst, const void* src, size_t bytes, void* 
  *   kind 1  the forward's tile loop, plain arrangement: per 32-row x 64-key wave tile 32 MFMAs, SiLU of
  *           32 scores per lane, 48 LDS fragment reads, 8 global -> LDS copies, one barrier
  *   kind 2  the same work in the skewed arrangement of the forward's leading unmasked tiles
+ *   kind 3  kind 2 with 64 query rows per wave, one workgroup (256 rows) per CU, one wave per SIMD: every
+ *           LDS fragment feeds two MFMAs (a design the attention kernels do not use; priced here).  A
+ *           workgroup does twice the work: FLOPs = workgroups * tiles * 4 * 64 * 32768
  * pieces (kinds 1, 2) removes parts, timing only: 1 no SiLU, 2 no LDS fragment reads, 12 no copies and
- * no barrier, 14 MFMAs + SiLU only; 0 keeps everything.
+ * no barrier, 14 MFMAs + SiLU only; 0 keeps everything (kind 3: 0 or 2).
  * k, v: device, [rows, 4, 128] bf16, read as `sequences` runs of rows / 64 / sequences key tiles;
  * q: device, at least [128, 4, 128] bf16.  What they hold is the caller's choice (random values or
  * zeros: the clock the chip grants depends on the operands).  `workgroups` workgroups of 256 threads

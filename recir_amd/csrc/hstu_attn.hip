@@ -830,7 +830,7 @@ extern "C" {
 int recir_hstu_calibration_mfma_loop(int32_t kind, int32_t pieces, const void* k, const void* v, const void* q, size_t rows,
                                      int32_t sequences, int32_t tiles, int32_t workgroups, float alpha, uint64_t* stats,
                                      float* sink, void* hip_stream) {
-  if (kind < 0 || kind > 2) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "calibration kind must be 0, 1 or 2, got %d", kind);
+  if (kind < 0 || kind > 3) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "calibration kind must be 0, 1, 2 or 3, got %d", kind);
   if (!k || !v || !q || !stats || !sink) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "calibration buffers must be non-null");
   if ((((size_t)k | (size_t)v | (size_t)q) & 15) || ((size_t)stats & 7))
     return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "calibration buffers must be 16-byte aligned");
@@ -851,8 +851,13 @@ int recir_hstu_calibration_mfma_loop(int32_t kind, int32_t pieces, const void* k
     hipLaunchKernelGGL((hstu_calibration_loop<0, 0>), dim3((unsigned)workgroups), dim3(256), 0, stream, c);
   } else if (kind == 1) {
     rc = launch_calibration<1>(pieces, (unsigned)workgroups, stream, c);
-  } else {
+  } else if (kind == 2) {
     rc = launch_calibration<2>(pieces, (unsigned)workgroups, stream, c);
+  } else {
+    const dim3 g((unsigned)workgroups), b(256);
+    if (pieces == 0) hipLaunchKernelGGL((hstu_calibration_loop64<0>), g, b, 0, stream, c);
+    else if (pieces == CAL_NO_LDS_READS) hipLaunchKernelGGL((hstu_calibration_loop64<CAL_NO_LDS_READS>), g, b, 0, stream, c);
+    else rc = -1;
   }
   if (rc) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "pieces %d is not one of the built combinations (0, 1, 2, 12, 14)", pieces);
   return launch_status("hstu_calibration_loop");

@@ -80,3 +80,53 @@ def test_key_tile_kernel_register_budget(device_asm):
         assert agprs == 128, (name, agprs)
         assert spills == 0, (name, spills)
         assert total <= 512, (name, total)
+
+
+def _vgprs(text):
+    """Indices of the VGPRs an instruction's operands name (v7, v[12:27]); AGPRs are not meant."""
+    regs = set()
+    for a, b in re.findall(r"(?<![\w\]])v\[(\d+):(\d+)\]", text):
+        regs.update(range(int(a), int(b) + 1))
+    for a in re.findall(r"(?<![\w\[])v(\d+)\b", text):
+        regs.add(int(a))
+    return regs
+
+
+def test_nothing_the_compiler_placed_touches_a_hand_written_score_product_before_its_wait(device_asm):
+    """The score products of the key-tile kernel are MFMAs written as assembly with VGPR results; the
+    compiler's hazard recogniser does not see them, so the wait an MFMA result needs before another
+    instruction may read it is written by hand too (an ``s_nop 15`` behind each chain).  That only
+    holds while the compiler places no instruction of its own that names those result registers
+    between the chain's first MFMA and that wait -- a copy, a spill -- which is checked here."""
+    kernels = _kernels(device_asm, "hstu_bwd_dkv_d128")
+    assert len(kernels) == 8
+    for name, body in kernels:
+        in_asm = False
+        pending = set()   # result VGPRs of hand MFMAs whose wait has not been seen yet
+        chains = waits = 0
+        for line in body:
+            if "#ASMSTART" in line:
+                in_asm = True
+                continue
+            if "#ASMEND" in line:
+                in_asm = False
+                continue
+            text = line.split(";")[0].strip()
+            if not text or text.startswith("."):
+                continue
+            if in_asm:
+                m = re.match(r"v_mfma_f32_32x32x16_bf16\s+v\[(\d+):(\d+)\]", text)
+                if m:
+                    if not pending:
+                        chains += 1
+                    pending.update(range(int(m.group(1)), int(m.group(2)) + 1))
+                elif text.startswith("s_nop 15"):
+                    waits += 1
+                    pending.clear()
+                continue
+            if pending:
+                operands = text.split(None, 1)[1] if " " in text else ""
+                hit = _vgprs(operands) & pending
+                assert not hit, f"{name}: `{text}` names v{sorted(hit)[:4]} while a hand-written MFMA into them has no wait yet"
+        assert chains >= 4 and waits >= chains, (name, chains, waits)
+        assert not pending, f"{name}: a chain of score products without its wait"
