@@ -656,7 +656,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
                      "frac": achieved / peak, "traffic": traffic, "traffic_source": traffic_source, "kernel_ms": kern_ms,
                      "sustained_peak": sustained["tflops"], "sustained_peak_sclk_mhz": sustained["sclk_mhz"],
-                     "frac_of_sustained": achieved / sustained["tflops"],
+                     "frac_of_sustained": achieved / sustained["tflops"] if wl.dtype == "bf16" else None,
                      "sustained_peak_source": "recir_hstu_calibration_mfma_loop kind 0 (bf16 MFMAs only, random operands), this run",
                      "hbm_gbs_algorithmic": abytes / (kern_ms * 1e-3) / 1e9,
                      "hbm_frac_algorithmic": abytes / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBS},
