@@ -27,12 +27,25 @@
 extern "C" {
 #endif
 
-#define RECIR_HSTU_ABI_VERSION 5
+#define RECIR_HSTU_ABI_VERSION 6
 
-/* element types of q/k (v and out follow: bf16 for BF16 and FP8_E4M3, fp32 for FP32) */
+/* element types of q/k (v and out follow: bf16 for BF16 and FP8_E4M3, fp32 for FP32, fp16 for FP16) */
 #define RECIR_HSTU_DTYPE_BF16 0
 #define RECIR_HSTU_DTYPE_FP32 1
 #define RECIR_HSTU_DTYPE_FP8_E4M3 2 /* q,k are OCP e4m3fn bytes with per-head scales; v,out bf16 */
+#define RECIR_HSTU_DTYPE_FP16 3     /* IEEE half; MFMA kernels only (head dims that are multiples of 8) */
+
+/*
+ * Which kernels run a call (recir_hstu_last_kernel names the one that did):
+ *   - the kernels written for head dim 128 ("tiled_d128_*", "bwd_tiled_d128_*"): bf16 (forward also
+ *     fp8 q/k), Dqk = Dv = 128, 16-byte aligned tensors, the causal or semi-local mask, alpha != 0
+ *     when there is a bias; the only ones that produce the gradient of the bias table on MFMAs;
+ *   - the general MFMA kernels ("mfma_*", "bwd_mfma_*"): bf16 or fp16, Dqk and Dv any multiples of
+ *     8 up to 256 (backward: 128) and independent of each other, 16-byte aligned tensors, every
+ *     mask, any alpha; a few times slower than the first group at its own shape;
+ *   - the generic kernels ("generic_*", "bwd_generic_*"): one wave per (token, head), bf16 or fp32,
+ *     any head dim up to 512; two orders of magnitude slower.  fp32 tensors always run here.
+ */
 
 /* flags */
 #define RECIR_HSTU_FLAG_OFFSETS_I32 0x1u          /* seq_offsets / num_targets are int32, not int64 */
@@ -59,19 +72,18 @@ extern "C" {
                                                      ids within max_attn_len, either way round (the
                                                      diagonal alone when max_attn_len is 0), the rows
                                                      of full_attn_size and the contextual keys as in
-                                                     the causal case.  Generic kernels only (any head
-                                                     dim, bf16 or fp32; forward and backward).       */
+                                                     the causal case.  General MFMA kernels or
+                                                     generic kernels; forward and backward.          */
 #define RECIR_HSTU_FLAG_TILED_ONLY 0x40000u       /* reject (RECIR_HSTU_ERR_UNSUPPORTED, with the reason
                                                      in recir_hstu_last_error) a call that only the
-                                                     generic kernels cover -- one wave per (token,
-                                                     head), tens of times slower than the MFMA
-                                                     kernels -- instead of running it there: fp32
-                                                     tensors, head dims other than 128, tensors not
-                                                     16-byte aligned, the mask of
-                                                     RECIR_HSTU_FLAG_MASK_NONCAUSAL, a bias with
-                                                     alpha = 0.  Forward and backward.               */
+                                                     generic kernels cover instead of running it
+                                                     there: fp32 tensors, head dims that are not
+                                                     multiples of 8 or exceed 256 (backward: 128),
+                                                     tensors not 16-byte aligned, the gradient of the
+                                                     bias table outside the head-dim-128 kernels'
+                                                     domain.  Forward and backward.                  */
 #define RECIR_HSTU_FLAG_KERNEL_SHIFT 8            /* bits 8..15: kernel selector for tests/tuning  */
-#define RECIR_HSTU_FLAG_KERNEL_MASK 0xff00u       /* 0 auto, 1 generic, 2.. tiled variants         */
+#define RECIR_HSTU_FLAG_KERNEL_MASK 0xff00u       /* 0 auto, 1 generic, 2 general MFMA, 3 head dim 128 */
 
 /* status codes: 0 ok, negative = rejected before any launch, positive = hipError_t of a launch */
 #define RECIR_HSTU_OK 0
@@ -91,7 +103,7 @@ extern "C" {
  *   / hstu_ragged_attention_fwd_jax_fn (recir/ops/helion/jagged_hstu_attention.py:830-872).
  *   The causal ("lower_triangular") mask with num_softmax_heads = 0 is covered, plain or
  *   semi-local (max_attn_len, full_attn_size), and the mask of any other invalid_attn_mask_type
- *   string (RECIR_HSTU_FLAG_MASK_NONCAUSAL, generic kernels); the host wrapper rejects softmax heads.
+ *   string (RECIR_HSTU_FLAG_MASK_NONCAUSAL); the host wrapper rejects softmax heads.
  *
  * q, k          device, [T, H, Dqk] row-major contiguous, element type `dtype`
  * v, out        device, [T, H, Dv]; out is written in full: rows < seq_offsets[B] get the result,

@@ -23,7 +23,7 @@ from .ops import (  # noqa: F401
     fp8_attention_region,
     KERNEL_AUTO,
     KERNEL_GENERIC,
-    KERNEL_TILED,
+    KERNEL_MFMA_GENERAL,
     KERNEL_TILED_DIRECT,
 )
 

@@ -9,11 +9,12 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 # elsewhere, A/B measurements of two builds); there is still no fallback if it is missing
 LIB_PATH = os.environ.get("RECIR_HSTU_LIB") or os.path.join(_PKG, "librecir_hstu.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_BF16 = 0
 DTYPE_FP32 = 1
 DTYPE_FP8_E4M3 = 2
+DTYPE_FP16 = 3
 
 FLAG_OFFSETS_I32 = 0x1
 FLAG_CTX_REFERENCE = 0x2

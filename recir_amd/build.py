@@ -11,37 +11,56 @@ LIB_PATH = os.path.join(_PKG, "librecir_hstu.so")
 # the same sources with the forward kernel's phase stamps compiled in (bench.py --phase-trace); never
 # loaded by the operators
 TRACE_LIB_PATH = os.path.join(_PKG, "librecir_hstu_trace.so")
-SOURCES = [os.path.join(_PKG, "csrc", "hstu_attn.hip")]
+SOURCES = [os.path.join(_PKG, "csrc", "hstu_attn.hip"), os.path.join(_PKG, "csrc", "hstu_mfma_any.hip")]
 
 
 def hipcc_path() -> str:
     return shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 
-def compile_command(out: str = LIB_PATH, trace: bool = False, defines=()) -> list:
+def _common_flags(trace: bool, defines) -> list:
     return [
-        hipcc_path(), "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+        "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
         # no compiler-generated packed fp32 arithmetic
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
         "-I", os.path.join(_ROOT, "include"),
         *(["-DHSTU_TRACE=1"] if trace else []), *defines,
-        *SOURCES, "-o", out,
     ]
 
 
+def compile_commands(out: str = LIB_PATH, trace: bool = False, defines=(), obj_dir: str = "") -> list:
+    """One compile command per source (they run side by side) and the link command, last."""
+    objs = [os.path.join(obj_dir, os.path.splitext(os.path.basename(s))[0] + ".o") for s in SOURCES]
+    flags = _common_flags(trace, defines)
+    cmds = [[hipcc_path(), *flags, "-c", src, "-o", obj] for src, obj in zip(SOURCES, objs)]
+    cmds.append([hipcc_path(), "--offload-arch=gfx950", "-fPIC", "-shared", *objs, "-o", out])
+    return cmds
+
+
 def build_library(verbose: bool = False, trace: bool = False, defines=()) -> str:
-    """Always recompiles (a minute); returns the path of the shared library.  ``trace=True`` builds
-    the phase-trace variant instead."""
+    """Always recompiles (a minute or two); returns the path of the shared library.  ``trace=True``
+    builds the phase-trace variant instead."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+
     out = TRACE_LIB_PATH if trace else LIB_PATH
-    cmd = compile_command(out, trace, defines)
-    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     noise = "is not a recognized feature for this target"
-    log = "\n".join(l for l in res.stdout.splitlines() if noise not in l)
-    if res.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + log)
-    if verbose and log.strip():
-        print(log)
+
+    def run(cmd):
+        res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+        log = "\n".join(l for l in res.stdout.splitlines() if noise not in l)
+        if res.returncode != 0:
+            raise RuntimeError("hipcc failed:\n" + log)
+        return log
+
+    with tempfile.TemporaryDirectory(prefix="recir_hstu_build_") as obj_dir:
+        *compiles, link = compile_commands(out, trace, defines, obj_dir)
+        with ThreadPoolExecutor(max_workers=len(compiles)) as pool:
+            logs = list(pool.map(run, compiles))
+        logs.append(run(link))
+    if verbose and any(l.strip() for l in logs):
+        print("\n".join(l for l in logs if l.strip()))
     return out
 
 

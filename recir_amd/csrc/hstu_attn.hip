@@ -28,9 +28,9 @@
 
 #include "hstu_common.h"
 #include "hstu_plan.h"
-#include "hstu_tiled_d128.h"
 #include "hstu_tiled_d128_dl.h"
 #include "hstu_bwd_generic.h"
+#include "hstu_mfma_any.h"
 #include "hstu_bwd_d128.h"
 #include "hstu_calibration.h"
 #include "jagged_rows.h"
@@ -360,6 +360,22 @@ void launch_bwd_tiled(bool semi, bool has_rab, dim3 grid, dim3 grid_k, hipStream
   }
 }
 
+// Padded head dim of the general MFMA kernels for a call, 0 when they do not take it: both dims
+// multiples of 8 (16-byte rows), the larger one at most max_dim.
+int mfma_any_padded_dim(int Dqk, int Dv, int max_dim) {
+  if (Dqk % 8 || Dv % 8) return 0;
+  const int d = Dqk > Dv ? Dqk : Dv;
+  if (d > max_dim) return 0;
+  return d <= 32 ? 32 : (d <= 64 ? 64 : (d <= 128 ? 128 : 256));
+}
+const char* mfma_any_name(bool bwd, bool f16, int dp) {
+  static const char* const names[2][2][4] = {
+      {{"mfma_bf16_d32", "mfma_bf16_d64", "mfma_bf16_d128", "mfma_bf16_d256"}, {"mfma_fp16_d32", "mfma_fp16_d64", "mfma_fp16_d128", "mfma_fp16_d256"}},
+      {{"bwd_mfma_bf16_d32", "bwd_mfma_bf16_d64", "bwd_mfma_bf16_d128", "bwd_mfma_bf16_d256"},
+       {"bwd_mfma_fp16_d32", "bwd_mfma_fp16_d64", "bwd_mfma_fp16_d128", "bwd_mfma_fp16_d256"}}};
+  return names[bwd ? 1 : 0][f16 ? 1 : 0][dp == 32 ? 0 : (dp == 64 ? 1 : (dp == 128 ? 2 : 3))];
+}
+
 template <bool FP8>
 void launch_dl(bool has_rab, bool semi, dim3 grid, hipStream_t stream, const Params& p) {
   if (semi) {
@@ -403,7 +419,8 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "H, Dqk, Dv must be positive: H=%d Dqk=%d Dv=%d", H, Dqk, Dv);
   if (max_seq_len <= 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "max_seq_len must be positive, got %d", max_seq_len);
   if (contextual_seq_len < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "contextual_seq_len must be >= 0, got %d", contextual_seq_len);
-  if (dtype != RECIR_HSTU_DTYPE_BF16 && dtype != RECIR_HSTU_DTYPE_FP32 && dtype != RECIR_HSTU_DTYPE_FP8_E4M3)
+  if (dtype != RECIR_HSTU_DTYPE_BF16 && dtype != RECIR_HSTU_DTYPE_FP32 && dtype != RECIR_HSTU_DTYPE_FP8_E4M3 &&
+      dtype != RECIR_HSTU_DTYPE_FP16)
     return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
   if (T == 0) return RECIR_HSTU_OK;
   if (!q || !k || !v || !out) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "q, k, v, out must be non-null");
@@ -433,29 +450,36 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
   }
 
   const bool fp8 = dtype == RECIR_HSTU_DTYPE_FP8_E4M3;
-  const bool tiled_ok = (dtype == RECIR_HSTU_DTYPE_BF16 || fp8) && Dqk == HD && Dv == HD &&
-                        (((size_t)q | (size_t)k | (size_t)v | (size_t)out) & 15) == 0;
-  bool use_tiled = tiled_ok;
-  // The tiled kernels keep a bias divided by the score multiplier in their accumulators: not
-  // possible with alpha = 0 (the scores are then the bias alone), which the generic kernel handles.
-  const bool bias_needs_generic = rab && !std::isnormal(1.0f / alpha);
-  if (bias_needs_generic && !fp8) use_tiled = false;
-  if (bias_needs_generic && (fp8 || variant >= 2))
-    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "a bias with alpha = %g runs on the generic kernel only", (double)alpha);
-  if (variant == 1 && !fp8) use_tiled = false;
-  if (flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL) {
-    if (fp8 || variant >= 2)
-      return fail(RECIR_HSTU_ERR_UNSUPPORTED, "a mask type other than the causal one runs on the generic kernel only (bf16 or fp32)");
-    use_tiled = false;
-  }
-  if (fp8 && variant == 2) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "fp8 q/k runs on the direct-to-LDS tiled kernel only");
-  if (variant >= 2 && !tiled_ok)
-    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "tiled kernel needs bf16, Dqk = Dv = 128 and 16-byte aligned tensors");
+  const bool f16 = dtype == RECIR_HSTU_DTYPE_FP16;
+  const bool noncausal = (flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL) != 0;
+  const bool aligned = (((size_t)q | (size_t)k | (size_t)v | (size_t)out) & 15) == 0;
+  // The kernels written for head dim 128 keep a bias divided by the score multiplier in their
+  // accumulators: not possible with alpha = 0 (the scores are then the bias alone).
+  const bool bias_needs_other = rab && !std::isnormal(1.0f / alpha);
+  const bool d128_ok = (dtype == RECIR_HSTU_DTYPE_BF16 || fp8) && Dqk == HD && Dv == HD && aligned && !noncausal && !bias_needs_other;
+  // the MFMA kernels for other head dims, fp16 and the remaining masks (hstu_mfma_any.h)
+  const int any_dp = mfma_any_padded_dim(Dqk, Dv, 256);
+  const bool any_ok = (dtype == RECIR_HSTU_DTYPE_BF16 || f16) && any_dp != 0 && aligned;
   if (variant > 3) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "unknown kernel selector %u", variant);
-  if (semi && variant == 2)
-    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "the semi-local mask runs on the direct-to-LDS tiled kernel or the generic one");
+  if (variant == 3 && !d128_ok)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED,
+                "the head-dim-128 kernel needs bf16 or fp8 q/k, Dqk = Dv = 128, 16-byte aligned tensors, the causal or "
+                "semi-local mask and alpha != 0 with a bias");
+  if (variant == 2 && !any_ok)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED,
+                "the general MFMA kernel needs bf16 or fp16, head dims that are multiples of 8 up to 256 and 16-byte aligned tensors");
+  if (fp8 && !d128_ok)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED,
+                "fp8 q/k is implemented for Dqk = Dv = 128, 16-byte aligned tensors, the causal or semi-local mask (and alpha != 0 with a bias)");
+  if (fp8 && (variant == 1 || variant == 2)) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "fp8 q/k runs on the head-dim-128 kernel only");
+  if (f16 && (variant == 1 || !any_ok))
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED,
+                "fp16 runs on the general MFMA kernel only: head dims that are multiples of 8 up to 256, 16-byte aligned tensors "
+                "(Dqk=%d Dv=%d)", Dqk, Dv);
+  const bool use_tiled = d128_ok && (variant == 0 || variant == 3);
+  const bool use_any = !use_tiled && any_ok && variant != 1;
 
-  if (use_tiled) {
+  if (use_tiled || use_any) {
     const size_t need = recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype);
     if (!workspace || workspace_bytes < need || ((size_t)workspace & 15))
       return fail(RECIR_HSTU_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu at %p", need,
@@ -465,8 +489,7 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     p.ws_items = (WorkItem*)((char*)workspace + WS_HEADER);
     p.items_cap = (int)items;
     const int bm = BM;
-    // only the direct-to-LDS kernel reads the row bound of an item
-    int plan_mode = ((variant == 0 || variant == 3) ? PLAN_SHIFT_ODD : 0) | PLAN_PAIR_CU;  // (two workgroups per CU)
+    int plan_mode = PLAN_SHIFT_ODD | PLAN_PAIR_CU;  // (two workgroups per CU)
     // q, k, v and out beyond the last-level cache: lists ordered by groups of pairs (hstu_plan.h)
     if ((flags & RECIR_HSTU_FLAG_GROUPED_LISTS) || tensors_exceed_llc(T, H, Dqk, Dv, fp8 ? 1 : 2, 2)) plan_mode |= PLAN_GROUP;
     // slots per XCD the launch covers: an even share of the items plus the imbalance the dealing of
@@ -494,30 +517,24 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     }
 #endif
     const dim3 grid((unsigned)(slots * NUM_XCD));
-    if (variant == 2) {  // register-staged tiles (kept for comparison and tiling-invariance tests)
-      if (rab) hipLaunchKernelGGL((hstu_fwd_tiled_d128<true>), grid, dim3(256), 0, stream, p);
-      else hipLaunchKernelGGL((hstu_fwd_tiled_d128<false>), grid, dim3(256), 0, stream, p);
-      g_last_kernel = rab ? "tiled_d128_bf16_regstage_rab" : "tiled_d128_bf16_regstage";
+    if (use_any) {
+      if (!launch_mfma_any_fwd(dtype, any_dp, grid, stream, p)) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "no general MFMA kernel for dtype %d, padded head dim %d", dtype, any_dp);
+      g_last_kernel = mfma_any_name(false, f16, any_dp);
+    } else if (fp8) {
+      launch_dl<true>(rab != nullptr, semi, grid, stream, p);
+      g_last_kernel = rab ? "tiled_d128_fp8qk_rab" : "tiled_d128_fp8qk";
     } else {
-      if (dtype == RECIR_HSTU_DTYPE_FP8_E4M3) {
-        launch_dl<true>(rab != nullptr, semi, grid, stream, p);
-        g_last_kernel = rab ? "tiled_d128_fp8qk_rab" : "tiled_d128_fp8qk";
-      } else {
-        launch_dl<false>(rab != nullptr, semi, grid, stream, p);
-        g_last_kernel = rab ? "tiled_d128_bf16_rab" : "tiled_d128_bf16";
-      }
+      launch_dl<false>(rab != nullptr, semi, grid, stream, p);
+      g_last_kernel = rab ? "tiled_d128_bf16_rab" : "tiled_d128_bf16";
     }
     if (int rc = launch_status("hstu_fwd_tiled_d128")) return rc;
     return RECIR_HSTU_OK;
   }
 
-  if (dtype == RECIR_HSTU_DTYPE_FP8_E4M3)
-    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "fp8 q/k is implemented for Dqk = Dv = 128 only");
   if (flags & RECIR_HSTU_FLAG_TILED_ONLY)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "only the generic kernel covers this call (the MFMA kernels need bf16 or fp8 q/k, Dqk = Dv = 128, 16-byte aligned "
-                "tensors, the causal or semi-local mask, and alpha != 0 with a bias): dtype=%d Dqk=%d Dv=%d",
-                dtype, Dqk, Dv);
+                "only the generic kernel covers this call (the MFMA kernels need bf16, fp16 or fp8 q/k, head dims that are "
+                "multiples of 8 up to 256 and 16-byte aligned tensors): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
   if (Dqk > GENERIC_MAX_D || Dv > GENERIC_MAX_D)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "head dims above %d are not supported (Dqk=%d Dv=%d)", GENERIC_MAX_D, Dqk, Dv);
   if (H > 65535) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "more than 65535 heads");
@@ -625,9 +642,9 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "H, Dqk, Dv must be positive: H=%d Dqk=%d Dv=%d", H, Dqk, Dv);
   if (max_seq_len <= 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "max_seq_len must be positive, got %d", max_seq_len);
   if (contextual_seq_len < 0) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "contextual_seq_len must be >= 0, got %d", contextual_seq_len);
-  if (dtype != RECIR_HSTU_DTYPE_BF16 && dtype != RECIR_HSTU_DTYPE_FP32)
+  if (dtype != RECIR_HSTU_DTYPE_BF16 && dtype != RECIR_HSTU_DTYPE_FP32 && dtype != RECIR_HSTU_DTYPE_FP16)
     return fail(dtype == RECIR_HSTU_DTYPE_FP8_E4M3 ? RECIR_HSTU_ERR_UNSUPPORTED : RECIR_HSTU_ERR_INVALID_ARGUMENT,
-                "backward supports bf16 and fp32 tensors, got dtype %d", dtype);
+                "backward supports bf16, fp16 and fp32 tensors, got dtype %d", dtype);
   if (drab && !rab) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "drab (the gradient of rab) needs rab");
   // drab is written in full whatever follows: by the last kernel of the MFMA path, and on every other
   // path as zeros first, to which the generic kernel adds
@@ -655,7 +672,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   bp.dout = dout; bp.dq = dq; bp.dk = dk; bp.dv = dv; bp.drab = drab; bp.absmax = nullptr;
 
   const bool bf16 = dtype == RECIR_HSTU_DTYPE_BF16;
-  const size_t esz = bf16 ? 2 : 4;
+  const size_t esz = dtype == RECIR_HSTU_DTYPE_FP32 ? 4 : 2;
   if (B == 0) {
     if (int rc = zero_drab()) return rc;
     void* outs[3] = {dq, dk, dv};
@@ -672,20 +689,32 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "head dims above %d are not supported (Dqk=%d Dv=%d)", BWD_GENERIC_MAX_D, Dqk, Dv);
   if ((unsigned)H > 65535u) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "more than 65535 heads");
   const unsigned variant = (flags & RECIR_HSTU_FLAG_KERNEL_MASK) >> RECIR_HSTU_FLAG_KERNEL_SHIFT;
-  // the tiled kernels cover bf16 at head dim 128
-  const bool tiled_ok = bf16 && Dqk == HD && Dv == HD &&
-                        (((size_t)dout | (size_t)q | (size_t)k | (size_t)v | (size_t)dq | (size_t)dk | (size_t)dv) & 15) == 0;
-  if (variant >= 2 && !tiled_ok)
-    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "tiled backward needs bf16, Dqk = Dv = 128 and 16-byte aligned tensors");
+  const bool f16 = dtype == RECIR_HSTU_DTYPE_FP16;
   const bool noncausal = (flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL) != 0;
-  if (noncausal && variant >= 2)
-    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "a mask type other than the causal one runs on the generic kernels only");
-  // the tiled kernels start their score accumulators from bias / alpha: a bias with alpha = 0 (scores
-  // that are the bias alone) is the generic kernels' case, as in the forward
-  const bool bias_needs_generic = rab && !std::isnormal(1.0f / alpha);
-  if (bias_needs_generic && variant >= 2)
-    return fail(RECIR_HSTU_ERR_UNSUPPORTED, "a bias with alpha = %g runs on the generic kernels only", (double)alpha);
-  if (tiled_ok && variant != 1 && !noncausal && !bias_needs_generic) {
+  const bool aligned = (((size_t)dout | (size_t)q | (size_t)k | (size_t)v | (size_t)dq | (size_t)dk | (size_t)dv) & 15) == 0;
+  // the kernels written for head dim 128 start their score accumulators from bias / alpha: a bias
+  // with alpha = 0 (scores that are the bias alone) is not theirs, as in the forward
+  const bool bias_needs_other = rab && !std::isnormal(1.0f / alpha);
+  const bool d128_ok = bf16 && Dqk == HD && Dv == HD && aligned && !noncausal && !bias_needs_other;
+  // the general MFMA kernels (hstu_mfma_any.h): no gradient of the bias table
+  const int any_dp = mfma_any_padded_dim(Dqk, Dv, 128);
+  const bool any_ok = (bf16 || f16) && any_dp != 0 && aligned && !drab;
+  if (variant > 3) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "unknown kernel selector %u", variant);
+  if (variant == 3 && !d128_ok)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED,
+                "the head-dim-128 backward needs bf16, Dqk = Dv = 128, 16-byte aligned tensors, the causal or semi-local mask "
+                "and alpha != 0 with a bias");
+  if (variant == 2 && !any_ok)
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED,
+                "the general MFMA backward needs bf16 or fp16, head dims that are multiples of 8 up to 128, 16-byte aligned "
+                "tensors and no gradient of the bias table");
+  if (f16 && (variant == 1 || !any_ok))
+    return fail(RECIR_HSTU_ERR_UNSUPPORTED,
+                "the fp16 backward runs on the general MFMA kernels only: head dims that are multiples of 8 up to 128, 16-byte "
+                "aligned tensors, no gradient of the bias table (Dqk=%d Dv=%d)", Dqk, Dv);
+  const bool use_tiled = d128_ok && (variant == 0 || variant == 3);
+  const bool use_any = !use_tiled && any_ok && variant != 1;
+  if (use_tiled || use_any) {
     const size_t half_ws = (recir_hstu_attn_fwd_workspace_bytes(T, B, H, Dqk, Dv, dtype) + 255) & ~(size_t)255;
     if (!workspace || workspace_bytes < 2 * half_ws + BWD_WS_TAIL || ((size_t)workspace & 15))
       return fail(RECIR_HSTU_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu at %p",
@@ -707,7 +736,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     bq.f.grid_slots = (int)slots;
     // the key-tile kernel's workgroups (one per CU) stay and draw further items from the lists' counters
     const size_t kslots = slots < (size_t)BWD_DKV_WG_PER_XCD ? slots : (size_t)BWD_DKV_WG_PER_XCD;
-    bk.f.grid_slots = (int)kslots;
+    bk.f.grid_slots = (int)(use_any ? slots : kslots);
     if (!(flags & RECIR_HSTU_FLAG_REUSE_PLAN)) {
       if (B <= PLAN_MAX_B && (size_t)B * H <= PLAN_MAX_PAIRS) {
         // q, k, v, dout and the three gradients beyond the last-level cache: lists ordered by groups of pairs
@@ -721,6 +750,14 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
           if (int rc = launch_status("hstu_plan_kernel")) return rc;
         }
       }
+    }
+    if (use_any) {
+      const dim3 grid((unsigned)(slots * NUM_XCD));
+      if (!launch_mfma_any_bwd(dtype, any_dp, grid, grid, stream, bq, bk))
+        return fail(RECIR_HSTU_ERR_UNSUPPORTED, "no general MFMA backward for dtype %d, padded head dim %d", dtype, any_dp);
+      if (int rc = launch_status("hstu_mfma_any (backward)")) return rc;
+      g_last_kernel = mfma_any_name(true, f16, any_dp);
+      return RECIR_HSTU_OK;
     }
     const bool per_token = attn_scale && (flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
     if (drab) {
@@ -767,8 +804,9 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   }
   if (flags & RECIR_HSTU_FLAG_TILED_ONLY)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "only the generic kernels cover this call (the MFMA kernels need bf16, Dqk = Dv = 128, 16-byte aligned tensors, "
-                "the causal or semi-local mask, and alpha != 0 with a bias): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
+                "only the generic kernels cover this call (the MFMA kernels need bf16 or fp16, head dims that are multiples of 8 "
+                "up to 128, 16-byte aligned tensors, and for the gradient of the bias table bf16, Dqk = Dv = 128, the causal or "
+                "semi-local mask and alpha != 0): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
   if (int rc = zero_drab()) return rc;
   const dim3 grid((unsigned)T, (unsigned)H);
   if (bf16) {

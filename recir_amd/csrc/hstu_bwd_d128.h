@@ -37,7 +37,6 @@
 #include <type_traits>
 
 #include "hstu_common.h"
-#include "hstu_tiled_d128.h"     // HD, kLog2e
 #include "hstu_bwd_acc_regs.h"
 #include "hstu_tiled_d128_dl.h"  // i16x4, i16x8, lds_void, lds_i16x4
 

@@ -18,6 +18,13 @@ typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
 // MI355X: 8 accelerator dies (XCDs), each with its own L2; workgroup i of a launch runs on XCD i % 8.
 constexpr int NUM_XCD = 8;
 
+// Tile shape of the kernels written for head dim 128: a workgroup owns BM query rows and walks the
+// keys in tiles of BN.
+constexpr int BM = 128;
+constexpr int BN = 64;
+constexpr int HD = 128;
+constexpr float kLog2e = 1.4426950408889634f;
+
 // One unit of work of the tiled kernels: a query tile of one (sequence, head), with everything the
 // workgroup needs about its sequence so that it starts with a single uniform load.
 struct WorkItem {

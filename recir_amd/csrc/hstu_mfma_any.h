@@ -1,0 +1,389 @@
+// MFMA kernels of the HSTU attention forward and backward for everything the kernels written for
+// head dim 128 do not take: head dims that are multiples of 8 up to 256 (forward) or 128 (backward),
+// Dqk and Dv independent, bf16 or fp16 values, every mask the operator knows (causal with targets
+// and contextual prefix, semi-local, the non-causal forms), a bias with any alpha.  One template,
+// three modes; nothing here is hand-scheduled: the point is to keep such calls on the matrix
+// cores (a few times slower than the head-dim-128 kernels) instead of on the one-wave-per-token
+// kernels (two orders of magnitude slower).
+//
+// A workgroup (4 waves) owns 128 "stationary" rows of one (sequence, head), 32 per wave, one per lane
+// of a 32-lane half; their operands stay in registers.  The other side is streamed through LDS in
+// tiles of 64 rows.  With c a stationary row and r a streamed row:
+//   FWD  c = query, r = key     S^T[r,c] = K[r,:] . Q[c,:]
+//                               O^T[:,c] += V^T[:,r] P^T[r,c]
+//   DQ   c = query, r = key     S^T as above, dP^T[r,c] = V[r,:] . dO[c,:]
+//                               dQ^T[:,c] += K^T[:,r] dS^T[r,c]
+//   DKV  c = key,   r = query   S[r,c] = Q[r,:] . K[c,:],  dP[r,c] = dO[r,:] . V[c,:]
+//                               dV^T[:,c] += dO^T[:,r] P[r,c],  dK^T[:,c] += Q^T[:,r] dS[r,c]
+// Every product is v_mfma_f32_32x32x16 with the streamed tile as the A operand: rows of the tile for
+// the score products (ds_read_b128), the transposed tile for the accumulating products
+// (ds_read_b64_tr_b16 on the same row-major tile).  The 32 x 32 accumulator layout of a score block
+// (lane = c, registers = r) is the B-operand layout of the accumulating product, so P and dS go from
+// one MFMA to the next through registers only.
+//
+// Head dims are padded to DP in {32, 64, 128, 256} with zeros (chunks of 8 elements past Dqk or Dv
+// are not loaded); both dims share the larger padding.
+//   x = alpha S + bias;  P = silu(x) keep;  dS = dP silu'(x) keep   (dO . V is dP)
+//   out = scale P V;  dQ = alpha scale dS K;  dK = alpha (scale dS)^T Q;  dV = (scale P)^T dO
+// The scale of a query row multiplies a column in FWD and DQ (applied to the accumulators at the
+// end) and a streamed row in DKV (applied per element when it is per token).
+#pragma once
+#include <type_traits>
+
+#include "hstu_common.h"
+
+namespace recir_hstu {
+
+typedef __attribute__((ext_vector_type(8))) _Float16 any_f16x8;
+typedef __attribute__((ext_vector_type(2))) _Float16 any_f16x2;
+typedef __attribute__((ext_vector_type(4))) short any_i16x4;
+typedef __attribute__((address_space(3))) any_i16x4 any_lds_i16x4;
+
+constexpr int ANY_FWD = 0, ANY_DQ = 1, ANY_DKV = 2;
+constexpr int ANY_BM = 128;  // stationary rows per workgroup
+constexpr int ANY_BN = 64;   // streamed rows per tile
+constexpr float kAnyLog2e = 1.4426950408889634f;
+
+template <bool F16>
+__device__ __forceinline__ f32x16 any_mfma(const u32x4& a, const u32x4& b, const f32x16& c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(any_f16x8, a), __builtin_bit_cast(any_f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+template <bool F16>
+__device__ __forceinline__ unsigned any_pack2(float lo, float hi) {
+  if constexpr (F16) {
+    const f32x2 t = {lo, hi};
+    const any_f16x2 y = __builtin_convertvector(t, any_f16x2);
+    return __builtin_bit_cast(unsigned, y);
+  } else {
+    return pack_bf16x2(lo, hi);
+  }
+}
+
+template <int MODE, bool F16, int DP>
+__global__ __launch_bounds__(256, (MODE == ANY_FWD && DP <= 128) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
+  const Params& p = bp.f;
+  constexpr bool BWD = MODE != ANY_FWD;
+  constexpr int NK = DP / 16;       // steps of 16 along the head dim in a score product
+  constexpr int NB = DP / 32;       // 32-row blocks of a transposed accumulator
+  constexpr int RS = DP * 2 + 16;   // bytes between tile rows in LDS (the 16 spread the rows over the banks)
+  constexpr int CPR = DP / 8;       // 16-byte chunks per tile row
+  constexpr int NCH = DP / 32;      // chunks of one tile that one thread stages
+  static_assert(DP == 32 || DP == 64 || DP == 128 || DP == 256, "padded head dim");
+  __shared__ __attribute__((aligned(16))) unsigned char Y1s[2][ANY_BN * RS];
+  __shared__ __attribute__((aligned(16))) unsigned char Y2s[2][ANY_BN * RS];
+  __shared__ float bias_s[2][ANY_BM + ANY_BN];
+  __shared__ float scale_s[2][ANY_BN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int half = lane >> 5;
+  // row fragment (A operand, 32 rows x 16 elements): lane reads row l32 (+ 32 blk), elements 16 kk + 8 half .. + 7
+  const unsigned row_rd = (unsigned)l32 * RS + (unsigned)half * 16u;
+  // transposed fragment (A operand, 32 columns of the tile x 16 rows): lane s = lane & 15 of a 16-lane
+  // group supplies the 8 bytes at row 4 half + (s >> 2) (+ 16 s2, + 8 for the second read), column
+  // 32 db + 16 group + 4 (s & 3) .. + 3; the lanes receive rows {4 half .. + 3, 8 + 4 half .. + 3} of
+  // column 32 db + l32, which is the row order of the accumulator registers that feed the B operand
+  const int tr_s = lane & 15;
+  const unsigned tr_rd = (unsigned)(4 * half + (tr_s >> 2)) * RS + (unsigned)(32 * ((lane >> 4) & 1) + 8 * (tr_s & 3));
+
+  if (MODE == ANY_FWD) zero_tail_rows_of<256>(p, p.out, (size_t)p.H * p.Dv * 2);
+  if (MODE == ANY_DQ) zero_tail_rows_of<256>(p, bp.dq, (size_t)p.H * p.Dqk * 2);
+  if (MODE == ANY_DKV) {
+    zero_tail_rows_of<256>(p, bp.dk, (size_t)p.H * p.Dqk * 2);
+    zero_tail_rows_of<256>(p, bp.dv, (size_t)p.H * p.Dv * 2);
+  }
+
+  const bool noncausal = (p.flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL) != 0;
+  const bool per_token = p.attn_scale && (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
+  const bool semi = p.max_attn_len > 0;
+  const float neg_log2e = -kAnyLog2e;
+  const int rab_w = 2 * p.N - 1;
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+
+  const int xcd = blockIdx.x % NUM_XCD;
+  const int list_len = p.ws_counts[xcd];
+  const WorkItem* __restrict__ list = p.ws_items + (size_t)xcd * p.items_cap;
+  for (int slot = blockIdx.x / NUM_XCD; slot < list_len; slot += p.grid_slots) {
+    const WorkItem wi = list[slot];
+    SeqInfo si;
+    si.s = wi.s; si.n = wi.n; si.cap = wi.cap; si.ctx_eff = wi.ctx_eff;
+    mask_window(p, si.cap, si.win, si.tail0);
+    const int c0 = wi.q0, c_end = wi.q_end, h = wi.h;  // stationary rows [c0, c_end) of the sequence
+    const int cap0 = si.cap > 0 ? si.cap : 0;
+
+    // tensors by role: *1 has Dqk elements per row, *2 has Dv
+    const char* __restrict__ X1g = (const char*)(MODE == ANY_DKV ? p.k : p.q);
+    const char* __restrict__ X2g = (const char*)(MODE == ANY_DKV ? p.v : bp.dout);
+    const char* __restrict__ Y1g = (const char*)(MODE == ANY_DKV ? p.q : p.k);
+    const char* __restrict__ Y2g = (const char*)(MODE == ANY_DKV ? bp.dout : p.v);
+    const size_t rb1 = (size_t)p.H * p.Dqk * 2, rb2 = (size_t)p.H * p.Dv * 2;
+    const size_t hb1 = (size_t)h * p.Dqk * 2, hb2 = (size_t)h * p.Dv * 2;
+    const float* __restrict__ rabg = p.rab ? p.rab + (size_t)h * rab_w : nullptr;
+
+    // ---- stationary operands (B operand of the score products): lane holds row c ----
+    const int cw0 = c0 + wave * 32;
+    const int c = cw0 + l32;
+    const bool c_valid = c < c_end;
+    const int c_lo = cw0, c_hi = min(cw0 + 31, c_end - 1);
+    const bool wave_has_rows = c_lo < c_end;
+    u32x4 x1[NK], x2[BWD ? NK : 1];
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
+      const int d0 = kk * 16 + half * 8;
+      x1[kk] = (c_valid && d0 < p.Dqk) ? *(const u32x4*)(X1g + (size_t)(si.s + c) * rb1 + hb1 + (size_t)d0 * 2) : zero4;
+      if constexpr (BWD) x2[kk] = (c_valid && d0 < p.Dv) ? *(const u32x4*)(X2g + (size_t)(si.s + c) * rb2 + hb2 + (size_t)d0 * 2) : zero4;
+    }
+
+    f32x16 acc1[BWD ? NB : 1];  // DQ: dQ^T   DKV: dK^T
+    f32x16 acc2[MODE == ANY_DQ ? 1 : NB];  // FWD: O^T   DKV: dV^T
+#pragma unroll
+    for (int i = 0; i < (BWD ? NB : 1); ++i) acc1[i] = zero16;
+#pragma unroll
+    for (int i = 0; i < (MODE == ANY_DQ ? 1 : NB); ++i) acc2[i] = zero16;
+
+    // ---- streamed rows: tiles [t_begin, t_end) of 64, minus the run [skip_a, skip_b) ----
+    int t_begin = 0, t_end = 0, skip_a = 0, skip_b = 0;
+    if (noncausal) {
+      // mirrored window on the target-clamped ids (the diagonal alone without a window); a contextual
+      // key or a row of the full-attention tail opens the whole sequence
+      const bool tail_set = si.tail0 != 0x7fffffff;
+      const int idc_lo = min(c0, si.cap), idc_hi = min(c_end - 1, si.cap);
+      const bool whole = MODE == ANY_DKV ? (c0 < si.ctx_eff || tail_set) : (si.ctx_eff > 0 || (tail_set && idc_hi >= si.tail0));
+      int r_begin = 0, r_end = si.n;
+      if (!whole) {
+        if (si.win == WIN_ALL) {
+          r_begin = c0;
+          r_end = c_end;
+        } else {
+          r_begin = max(idc_lo - si.win, 0);
+          r_end = idc_hi + si.win >= si.cap ? si.n : idc_hi + si.win + 1;
+        }
+      }
+      t_begin = r_begin / ANY_BN;
+      t_end = (r_end + ANY_BN - 1) / ANY_BN;
+    } else if (MODE != ANY_DKV) {  // keys
+      const int r_end = min(si.n, max(c_end, si.ctx_eff));
+      t_end = (r_end + ANY_BN - 1) / ANY_BN;
+      // semi-local: keys below the window of the first row, unless a row of the full-attention
+      // tail or a contextual key needs them
+      if (semi && si.ctx_eff <= 0 && min(c_end - 1, si.cap) < si.tail0) t_begin = max(min(c0, si.cap) - si.win, 0) / ANY_BN;
+      // tiles that hold only target keys off this item's diagonal (and no contextual key)
+      skip_a = (max(cap0, si.ctx_eff) + ANY_BN - 1) / ANY_BN;
+      skip_b = c0 / ANY_BN;
+    } else {  // queries
+      const int r_begin = c0 < si.ctx_eff ? 0 : c0;  // a key is seen by its own and later rows (a contextual key by all)
+      const int r_end = c0 >= max(cap0, si.ctx_eff) ? c_end : si.n;  // target keys: only by their own rows
+      t_begin = r_begin / ANY_BN;
+      t_end = (r_end + ANY_BN - 1) / ANY_BN;
+    }
+    const bool has_skip = skip_a < skip_b;
+    auto next_tile = [&](int t) { return (has_skip && t + 1 == skip_a) ? skip_b : t + 1; };
+
+    // ---- staging: global -> registers -> LDS ----
+    struct Staged {
+      u32x4 y1[NCH], y2[NCH];
+      float bias, scale;
+    };
+    auto load_tiles = [&](int t, Staged& st) __attribute__((always_inline)) {
+      const int r0 = t * ANY_BN;
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const int idx = tid + 256 * i;
+        const int row = idx / CPR, ch = idx % CPR;
+        const int rr = min(r0 + row, si.n - 1);  // rows past the sequence re-read its last row; the mask drops them
+        st.y1[i] = ch * 8 < p.Dqk ? *(const u32x4*)(Y1g + (size_t)(si.s + rr) * rb1 + hb1 + (size_t)ch * 16) : zero4;
+        st.y2[i] = ch * 8 < p.Dv ? *(const u32x4*)(Y2g + (size_t)(si.s + rr) * rb2 + hb2 + (size_t)ch * 16) : zero4;
+      }
+      st.bias = 0.f;
+      if (rabg && tid < ANY_BM + ANY_BN - 1) {
+        // entry e of the band holds the bias of m - j = dmin + e
+        const int dmin = MODE == ANY_DKV ? r0 - c0 - (ANY_BM - 1) : c0 - r0 - (ANY_BN - 1);
+        int idx = dmin + tid + p.N - 1;
+        idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
+        st.bias = rabg[idx];
+      }
+      st.scale = 1.0f;
+      if (MODE == ANY_DKV && per_token && tid < ANY_BN) st.scale = p.attn_scale[si.s + min(r0 + tid, si.n - 1)];
+    };
+    auto store_tiles = [&](int buf, const Staged& st) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const int idx = tid + 256 * i;
+        const int row = idx / CPR, ch = idx % CPR;
+        *(u32x4*)(&Y1s[buf][row * RS + ch * 16]) = st.y1[i];
+        *(u32x4*)(&Y2s[buf][row * RS + ch * 16]) = st.y2[i];
+      }
+      if (tid < ANY_BM + ANY_BN - 1) bias_s[buf][tid] = st.bias;
+      if (MODE == ANY_DKV && tid < ANY_BN) scale_s[buf][tid] = st.scale;
+    };
+
+    auto row_frag = [&](const unsigned char* y, int blk, int kk) __attribute__((always_inline)) {
+      return *(const u32x4*)(y + blk * 32 * RS + row_rd + kk * 32);
+    };
+    auto tr_frag = [&](const unsigned char* y, int db, int s2) __attribute__((always_inline)) {
+      const unsigned char* a = y + tr_rd + s2 * 16 * RS + db * 64;
+      const any_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((any_lds_i16x4*)a);
+      const any_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((any_lds_i16x4*)(a + 8 * RS));
+      u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      return (u32x4){l2.x, l2.y, h2.x, h2.y};
+    };
+
+    // One (64 streamed rows) x (32 stationary rows) block of this wave.  MASKED: the predicate is
+    // evaluated per pair; otherwise every pair of the block is known to be kept.
+    auto tile_body = [&](auto masked_tag, int r0, int buf) __attribute__((always_inline)) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      const unsigned char* y1 = &Y1s[buf][0];
+      const unsigned char* y2 = &Y2s[buf][0];
+      f32x16 S[2], dP[BWD ? 2 : 1];
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) S[blk] = any_mfma<F16>(row_frag(y1, blk, kk), x1[kk], kk == 0 ? zero16 : S[blk]);
+        if constexpr (BWD) {
+#pragma unroll
+          for (int kk = 0; kk < NK; ++kk) dP[blk] = any_mfma<F16>(row_frag(y2, blk, kk), x2[kk], kk == 0 ? zero16 : dP[blk]);
+        }
+      }
+      unsigned pw[2][8], dsw[BWD ? 2 : 1][8];
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        float pv[16], dsv[BWD ? 16 : 1];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rl = 32 * blk + 8 * (r >> 2) + 4 * half + (r & 3);  // streamed row of this register
+          float x = S[blk][r] * p.alpha;
+          if (rabg) x += bias_s[buf][MODE == ANY_DKV ? rl - (c - c0) + (ANY_BM - 1) : (c - c0) - rl + (ANY_BN - 1)];
+          const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * neg_log2e));
+          float pe = x * sig;
+          float de = 0.f;
+          if constexpr (BWD) de = dP[blk][r] * (sig + pe * (1.0f - sig));  // silu'(x) = sig (1 + x (1 - sig))
+          if (MODE == ANY_DKV && per_token) {
+            const float rs = scale_s[buf][rl];
+            pe *= rs;
+            de *= rs;
+          }
+          if (MASKED) {
+            const int rr = r0 + rl;
+            const int m = MODE == ANY_DKV ? rr : c, j = MODE == ANY_DKV ? c : rr;
+            const bool kp = keep_pair(m, j, si, noncausal) && rr < si.n && c < si.n;
+            pe = kp ? pe : 0.f;
+            de = kp ? de : 0.f;
+          }
+          pv[r] = pe;
+          if constexpr (BWD) dsv[r] = de;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          pw[blk][i] = any_pack2<F16>(pv[2 * i], pv[2 * i + 1]);
+          if constexpr (BWD) dsw[blk][i] = any_pack2<F16>(dsv[2 * i], dsv[2 * i + 1]);
+        }
+      }
+      // accumulating products: step s2 covers streamed rows 16 s2 .. + 15 = registers 8 (s2 & 1) .. + 7 of block s2 >> 1
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const int blk = s2 >> 1, w0 = 4 * (s2 & 1);
+        const u32x4 pb = {pw[blk][w0], pw[blk][w0 + 1], pw[blk][w0 + 2], pw[blk][w0 + 3]};
+        u32x4 db_ = zero4;
+        if constexpr (BWD) db_ = (u32x4){dsw[blk][w0], dsw[blk][w0 + 1], dsw[blk][w0 + 2], dsw[blk][w0 + 3]};
+#pragma unroll
+        for (int db = 0; db < NB; ++db) {
+          if constexpr (MODE != ANY_DQ) acc2[db] = any_mfma<F16>(tr_frag(y2, db, s2), pb, acc2[db]);
+          if constexpr (BWD) acc1[db] = any_mfma<F16>(tr_frag(y1, db, s2), db_, acc1[db]);
+        }
+      }
+    };
+
+    // wave-level classification of a block: skipped, every pair kept, or the predicate per pair
+    auto compute_tile = [&](int t, int buf) __attribute__((always_inline)) {
+      if (!wave_has_rows) return;
+      const int r0 = t * ANY_BN, r1 = r0 + ANY_BN;
+      bool full = false;
+      // (m_lo, m_hi) and (j_lo, j_hi): query rows and keys of the block, inclusive
+      const int m_lo = MODE == ANY_DKV ? r0 : c_lo, m_hi = MODE == ANY_DKV ? min(r1, si.n) - 1 : c_hi;
+      const int j_lo = MODE == ANY_DKV ? c_lo : r0, j_hi = MODE == ANY_DKV ? c_hi : min(r1, si.n) - 1;
+      const int id_lo = min(m_lo, si.cap), id_hi = min(m_hi, si.cap);
+      const bool diagonal = m_lo <= j_hi && j_lo <= m_hi;
+      if (!noncausal) {
+        const bool history = j_lo < id_hi && (id_hi >= si.tail0 || id_lo - j_hi <= si.win);
+        if (!(diagonal || history || j_lo < si.ctx_eff)) return;
+        full = !semi && j_hi < m_lo && j_hi < si.cap && r1 <= si.n;
+      } else {
+        const int idj_lo = min(j_lo, si.cap), idj_hi = min(j_hi, si.cap);
+        bool window = false, tail = false;
+        if (si.win != WIN_ALL) {
+          window = idj_lo - id_hi <= si.win && id_lo - idj_hi <= si.win;  // the two id ranges come within the window
+          if (si.tail0 != 0x7fffffff) tail = id_hi >= si.tail0 && (idj_lo < si.tail0 ? 0 : idj_lo) < id_hi;
+        }
+        if (!(diagonal || window || tail || j_lo < si.ctx_eff)) return;
+      }
+      if (full) tile_body(std::false_type{}, r0, buf);
+      else tile_body(std::true_type{}, r0, buf);
+    };
+
+    Staged st;
+    int t = (has_skip && t_begin >= skip_a) ? max(t_begin, skip_b) : t_begin;
+    int buf = 0;
+    if (t < t_end) {
+      load_tiles(t, st);
+      store_tiles(0, st);
+      __syncthreads();
+      int nxt = next_tile(t);
+      if (nxt < t_end) load_tiles(nxt, st);
+      while (true) {
+        compute_tile(t, buf);
+        if (nxt >= t_end) break;
+        store_tiles(buf ^ 1, st);
+        __syncthreads();
+        t = nxt;
+        buf ^= 1;
+        nxt = next_tile(t);
+        if (nxt < t_end) load_tiles(nxt, st);
+      }
+    }
+
+    // ---- epilogue: transposed accumulators -> rows of the outputs ----
+    if (c_valid) {
+      float uni = 1.0f / (float)p.N;  // the scale where it is the same for every row
+      if (p.attn_scale && !per_token) uni = p.attn_scale[0];
+      const float col_scale = MODE == ANY_DKV ? (per_token ? 1.0f : uni) : (per_token ? p.attn_scale[si.s + c] : uni);
+      auto store_rows = [&](void* base, int D, const f32x16* acc, float f) __attribute__((always_inline)) {
+        unsigned short* orow = (unsigned short*)base + ((size_t)(si.s + c) * p.H + h) * D;
+#pragma unroll
+        for (int db = 0; db < NB; ++db) {
+#pragma unroll
+          for (int rq = 0; rq < 4; ++rq) {
+            const int d0 = db * 32 + 8 * rq + 4 * half;
+            if (d0 < D) {
+              u32x2 o;
+              o.x = any_pack2<F16>(acc[db][4 * rq + 0] * f, acc[db][4 * rq + 1] * f);
+              o.y = any_pack2<F16>(acc[db][4 * rq + 2] * f, acc[db][4 * rq + 3] * f);
+              *(u32x2*)(orow + d0) = o;
+            }
+          }
+        }
+      };
+      if constexpr (MODE == ANY_FWD) store_rows(p.out, p.Dv, acc2, col_scale);
+      if constexpr (MODE == ANY_DQ) store_rows(bp.dq, p.Dqk, acc1, col_scale * p.alpha);
+      if constexpr (MODE == ANY_DKV) {
+        store_rows(bp.dk, p.Dqk, acc1, col_scale * p.alpha);
+        store_rows(bp.dv, p.Dv, acc2, col_scale);
+      }
+    }
+    __syncthreads();  // the LDS tiles are reused by the next item
+  }
+}
+
+// Launchers (defined in hstu_mfma_any.hip).  dtype: RECIR_HSTU_DTYPE_BF16 or RECIR_HSTU_DTYPE_FP16;
+// dp: padded head dim (32, 64, 128 or 256; the backward takes up to 128).  Return false when the
+// combination has no instantiation.
+bool launch_mfma_any_fwd(int dtype, int dp, dim3 grid, hipStream_t stream, const Params& p);
+bool launch_mfma_any_bwd(int dtype, int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk);
+
+}  // namespace recir_hstu

@@ -31,7 +31,6 @@
 #include <type_traits>
 
 #include "hstu_common.h"
-#include "hstu_tiled_d128.h"  // BM, BN, HD, kLog2e
 
 namespace recir_hstu {
 

@@ -26,8 +26,8 @@ from . import _lib
 
 KERNEL_AUTO = 0
 KERNEL_GENERIC = 1
-KERNEL_TILED = 2         # tiled MFMA kernel, K/V staged through registers
-KERNEL_TILED_DIRECT = 3  # tiled MFMA kernel, K/V copied global -> LDS directly
+KERNEL_MFMA_GENERAL = 2  # MFMA kernels for any head dim (multiples of 8), bf16 or fp16, every mask
+KERNEL_TILED_DIRECT = 3  # MFMA kernels written for head dim 128 (bf16, fp8 q/k), K/V copied global -> LDS directly
 
 class _CallState(threading.local):
     """Per-thread switches the context managers below set and every launch reads: a thread that
@@ -40,10 +40,11 @@ class _CallState(threading.local):
 
 _state = _CallState()
 
-# What happens when a bf16 call can only run on the generic kernels (one wave per token and head, tens of
-# times slower than the MFMA kernels: head dims other than 128, unaligned tensors, a mask type other than
-# "lower_triangular", a bias with alpha = 0): "warn" (once per process and reason), "error" (the C ABI
-# rejects the call, RECIR_HSTU_FLAG_TILED_ONLY) or "silent".  fp32 tensors are the smoke path and never warn.
+# What happens when a bf16 call can only run on the generic kernels (one wave per token and head, two orders
+# of magnitude slower than the MFMA kernels: head dims that are not multiples of 8 or exceed 256 (backward:
+# 128), unaligned tensors, the gradient of the bias table outside bf16 at head dim 128 with the causal or
+# semi-local mask): "warn" (once per process and reason), "error" (the C ABI rejects the call,
+# RECIR_HSTU_FLAG_TILED_ONLY) or "silent".  fp32 tensors are the smoke path and never warn.
 _generic_policy = "warn"
 _generic_warned = set()
 
@@ -58,23 +59,23 @@ def set_generic_kernel_policy(policy: str) -> str:
     return prev
 
 
-def _note_generic(kernel: str, q, v, mask_type, alpha, rab) -> None:
+def _note_generic(kernel: str, q, v, rab_grad=False) -> None:
     if _generic_policy != "warn" or not kernel.startswith(("generic_bf16", "bwd_generic_bf16")):
         return
     if _state.forced_kernel == KERNEL_GENERIC:
         return
-    if q.shape[2] != 128 or v.shape[2] != 128:
-        reason = f"head dims {q.shape[2]} / {v.shape[2]} (the MFMA kernels take 128 / 128)"
-    elif mask_type != "lower_triangular":
-        reason = f"mask type '{mask_type}'"
-    elif rab is not None and alpha == 0:
-        reason = "a bias with alpha = 0"
+    bwd = kernel.startswith("bwd_")
+    top = 128 if bwd else 256
+    if q.shape[2] % 8 or v.shape[2] % 8 or max(q.shape[2], v.shape[2]) > top:
+        reason = f"head dims {q.shape[2]} / {v.shape[2]} (the MFMA kernels take multiples of 8 up to {top})"
+    elif bwd and rab_grad:
+        reason = "the gradient of the bias table (on MFMAs only for bf16, head dims 128 / 128, the causal or semi-local mask, alpha != 0)"
     else:
         reason = "tensors that are not 16-byte aligned"
     if reason in _generic_warned:
         return
     _generic_warned.add(reason)
-    warnings.warn(f"recir HSTU attention ran on the generic kernel ({kernel}), tens of times slower than the MFMA "
+    warnings.warn(f"recir HSTU attention ran on the generic kernel ({kernel}), two orders of magnitude slower than the MFMA "
                   f"kernels, because of {reason}; recir_amd.set_generic_kernel_policy('error') rejects such calls, "
                   f"'silent' stops this message", RuntimeWarning, stacklevel=3)
 
@@ -377,7 +378,7 @@ def _launch(q, k, v, seq_offsets, num_targets, attn_scale, rab, q_scale, k_scale
             with _plan_cache_lock:
                 _plan_cache.pop(key, None)
         _raise_status("recir_hstu_attn_fwd", rc)
-    _note_generic(_lib.last_kernel(), q, v, mask_type, alpha, rab)
+    _note_generic(_lib.last_kernel(), q, v)
     return out
 
 
@@ -386,8 +387,10 @@ def _dtype_code(q, k, v):
         code = _lib.DTYPE_BF16
     elif q.dtype == torch.float32:
         code = _lib.DTYPE_FP32
+    elif q.dtype == torch.float16:
+        code = _lib.DTYPE_FP16
     else:
-        raise ValueError(f"q must be bfloat16 or float32, got {q.dtype}")
+        raise ValueError(f"q must be bfloat16, float16 or float32, got {q.dtype}")
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("q, k and v must share one dtype")
     return code
@@ -436,7 +439,7 @@ def _bwd_device(dout, N, alpha, q, k, v, seq_offsets, num_targets, attn_scale, c
             with _plan_cache_lock:
                 _plan_cache.pop(key, None)
         _raise_status("recir_hstu_attn_bwd", rc)
-    _note_generic(_lib.last_kernel(), q, v, mask_type, alpha, rab)
+    _note_generic(_lib.last_kernel(), q, v, rab_grad)
     return (dq, dk, dv, drab) if rab_grad else (dq, dk, dv)
 
 

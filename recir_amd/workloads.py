@@ -20,14 +20,14 @@ import torch
 @dataclass
 class Workload:
     name: str
-    q: torch.Tensor  # [T,H,Dqk] float32 master copy (already rounded to `dtype` where that is bf16)
+    q: torch.Tensor  # [T,H,Dqk] float32 master copy (already rounded to `dtype` where that is bf16 or fp16)
     k: torch.Tensor
     v: torch.Tensor
     seq_offsets: torch.Tensor  # [B+1] int64
     num_targets: torch.Tensor  # [B] int64
     max_seq_len: int
     alpha: float
-    dtype: str  # "fp32" | "bf16" | "fp8"
+    dtype: str  # "fp32" | "bf16" | "fp16" | "fp8"
     contextual_seq_len: int = 0
     rab: Optional[torch.Tensor] = None  # [H, 2*max_seq_len-1] float32
     lengths: np.ndarray = field(default=None)  # [B] full sequence lengths (history + targets)
@@ -83,7 +83,7 @@ class Workload:
         """q, k, v read once and out written once, plus offsets, targets and the bias table."""
         T, H, Dqk = self.q.shape
         Dv = self.v.shape[2]
-        qk_size = {"fp32": 4, "bf16": 2, "fp8": 1}[self.dtype]
+        qk_size = {"fp32": 4, "bf16": 2, "fp16": 2, "fp8": 1}[self.dtype]
         v_size = 4 if self.dtype == "fp32" else 2
         b = 2 * Dqk * H * T * qk_size + 2 * Dv * H * T * v_size
         b += 8 * (self.B + 1) + 8 * self.B
@@ -134,6 +134,10 @@ def make_jagged(lengths, num_targets, H, Dqk, Dv, *, max_seq_len, alpha, dtype="
         q = q.bfloat16().float()
         k = k.bfloat16().float()
         v = v.bfloat16().float()
+    if dtype == "fp16":
+        q = q.half().float()
+        k = k.half().float()
+        v = v.half().float()
     off = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
     return Workload(name=name, q=q, k=k, v=v, seq_offsets=torch.from_numpy(off),
                     num_targets=torch.as_tensor(np.asarray(num_targets, dtype=np.int64)),

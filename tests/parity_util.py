@@ -6,12 +6,25 @@ import torch
 # Stated tolerances (output vs the fp32 oracle on identical inputs)
 BF16_MAX_ABS = 1e-2   # absolute
 BF16_REL = 2e-2       # relative to the largest reference magnitude, and of the Frobenius norm
+FP16_REL = 4e-3       # fp16 operands (11 significant bits against bf16's 8): the same three relative bounds
 FP8_MAX_ABS = 5e-2
 FP32_RTOL, FP32_ATOL = 2e-4, 2e-6
 
 
+def expected_kernel(dqk, dv, dtype="bf16", *, causal=True, bwd=False, rab=False, alpha=1.0, rab_grad=False, fp8=False):
+    """Name of the kernel the library picks for a call (recir_hstu_last_kernel), from the rule in
+    include/recir_hstu.h: the head-dim-128 kernels, else the general MFMA kernels, else the generic ones."""
+    pre = "bwd_" if bwd else ""
+    if (dtype == "bf16" or fp8) and dqk == dv == 128 and causal and not (rab and alpha == 0):
+        return pre + "tiled_d128_" + ("fp8qk" if fp8 else "bf16") + ("_rab" if rab else "")
+    d = max(dqk, dv)
+    if dtype in ("bf16", "fp16") and dqk % 8 == 0 and dv % 8 == 0 and d <= (128 if bwd else 256) and not (bwd and rab_grad):
+        return f"{pre}mfma_{dtype}_d{32 if d <= 32 else 64 if d <= 64 else 128 if d <= 128 else 256}"
+    return f"{pre}generic_{dtype}"
+
+
 def to_device(wl, dtype=None):
-    dt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp8": torch.bfloat16}[dtype or wl.dtype]
+    dt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16, "fp8": torch.bfloat16}[dtype or wl.dtype]
     dev = torch.device("cuda:0")
     return (wl.q.to(dev, dt), wl.k.to(dev, dt), wl.v.to(dev, dt), wl.seq_offsets.to(dev),
             wl.num_targets.to(dev))

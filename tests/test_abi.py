@@ -53,7 +53,7 @@ def test_jagged_header_symbols_are_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.recir_hstu_abi_version() == 5
+    assert lib.recir_hstu_abi_version() == 6
 
 
 def test_workspace_size_is_host_arithmetic(lib):
@@ -91,7 +91,7 @@ def test_invalid_arguments_are_rejected_before_launch(lib, kw, needle):
     (dict(H=0), "must be positive"),
     (dict(N=0), "max_seq_len"),
     (dict(F=-1), "max_attn_len and full_attn_size"),
-    (dict(dtype=2), "bf16 and fp32"),
+    (dict(dtype=2), "bf16, fp16 and fp32"),
     (dict(dq=None), "non-null"),
     (dict(off=None), "seq_offsets"),
 ])

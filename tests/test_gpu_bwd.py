@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from tests.golden.cases import SMALL_CASES, build_inputs, fixture_file, upstream_gradient
-from tests.parity_util import BF16_REL, error_stats, report, to_device
+from tests.parity_util import BF16_REL, error_stats, expected_kernel, report, to_device
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
@@ -75,7 +75,7 @@ def test_small_cases_match_backward_oracle_and_golden(oracle, name):
                            ctx_mode=oracle.CTX_REFCPP, max_attn_len=case["max_attn_len"],
                            full_attn_size=case["full_attn_size"], mask_type=case["mask_type"])
     end = int(wl.seq_offsets[-1])
-    causal = case["mask_type"] == "lower_triangular"  # the other mask types run on the generic kernels
+    causal = case["mask_type"] == "lower_triangular"  # the other mask types run on the general MFMA kernels
     with ops.reference_contextual_rule():
         got = run_hip_bwd(wl, dout, attn_scale=scale, num_targets=ntd, dtype="fp32")
     assert all(g.dtype == torch.float32 for g in got)
@@ -89,7 +89,7 @@ def test_small_cases_match_backward_oracle_and_golden(oracle, name):
         assert all(g.dtype == torch.bfloat16 for g in gotb)
         assert_grads_close(gotb, want, end, BF16_REL, name + " bf16")
         from recir_amd import _lib
-        assert _lib.last_kernel() == ("bwd_tiled_d128_bf16" if causal else "bwd_generic_bf16")
+        assert _lib.last_kernel() == expected_kernel(case["Dqk"], case["Dv"], causal=causal, bwd=True)
         with ops.reference_contextual_rule(), ops.force_kernel(ops.KERNEL_GENERIC):
             gotg = run_hip_bwd(wl, dout, attn_scale=scale, num_targets=ntd, dtype="bf16")
         assert _lib.last_kernel() == "bwd_generic_bf16"
@@ -372,7 +372,7 @@ def test_randomized_cases_forward_and_backward(oracle, seed):
     causal = wl.mask_type == "lower_triangular"
     out = run_hip(wl, attn_scale=scale)
     if wl.T:
-        assert _lib.last_kernel().startswith("tiled_d128" if causal else "generic"), what
+        assert _lib.last_kernel().startswith("tiled_d128" if causal else "mfma_bf16_d128"), what
     assert_bf16_close(out, run_oracle(oracle, wl, attn_scale=scale), what)
     want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
                            wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
@@ -381,7 +381,7 @@ def test_randomized_cases_forward_and_backward(oracle, seed):
                            full_attn_size=wl.full_attn_size, mask_type=wl.mask_type)
     got = run_hip_bwd(wl, dout, attn_scale=scale, rab=wl.rab)
     if wl.T:
-        assert _lib.last_kernel().startswith("bwd_tiled_d128" if causal else "bwd_generic"), what
+        assert _lib.last_kernel().startswith("bwd_tiled_d128" if causal else "bwd_mfma_bf16_d128"), what
     if want[0].size and np.abs(want[0]).max() > 0:
         assert_grads_close(got, want, int(wl.seq_offsets[-1]), BF16_REL, what)
 
@@ -550,7 +550,7 @@ def test_noncausal_mask_through_autograd_and_with_a_bias(oracle):
     out = recir_amd.jagged_hstu_attention(q, k, v, off, nt, max_seq_len=wl.max_seq_len, alpha=wl.alpha,
                                           contextual_seq_len=2, rab=rab, max_attn_len=12, full_attn_size=5,
                                           invalid_attn_mask_type="full")
-    assert _lib.last_kernel() == "generic_bf16"
+    assert _lib.last_kernel() == "mfma_bf16_d128"
     out.backward(dout.to(out.device, out.dtype))
     torch.cuda.synchronize()  # (the backward ran on autograd's thread: the kernel name kept per thread is not this thread's)
     kw = dict(max_seq_len=wl.max_seq_len, alpha=wl.alpha, rab=wl.rab.numpy(), contextual_seq_len=2, max_attn_len=12,
@@ -571,9 +571,9 @@ def test_noncausal_mask_through_autograd_and_with_a_bias(oracle):
     assert not torch.equal(out_c, out.detach())
 
 
-def test_a_bias_with_alpha_zero_runs_on_the_generic_kernels(oracle):
-    """The tiled kernels keep the bias divided by alpha in their score accumulators; with alpha = 0 the
-    scores are the bias alone and the call goes to the generic kernels, forward and backward."""
+def test_a_bias_with_alpha_zero_runs_on_the_general_kernels(oracle):
+    """The head-dim-128 kernels keep the bias divided by alpha in their score accumulators; with alpha = 0 the
+    scores are the bias alone and the call goes to the general MFMA kernels, forward and backward."""
     from recir_amd import _lib, ops
     from recir_amd.workloads import make_jagged
     from tests.parity_util import assert_bf16_close, run_hip, run_oracle
@@ -581,11 +581,11 @@ def test_a_bias_with_alpha_zero_runs_on_the_generic_kernels(oracle):
     wl = make_jagged([150, 64, 1, 0, 200], [20, 64, 0, 0, 7], 2, 128, 128, max_seq_len=256, alpha=0.0, dtype="bf16",
                      seed=81, with_rab=True, rab_std=0.7, contextual_seq_len=2, tail_rows=1)
     out = run_hip(wl)
-    assert _lib.last_kernel() == "generic_bf16"
+    assert _lib.last_kernel() == "mfma_bf16_d128"
     assert_bf16_close(out, run_oracle(oracle, wl), "alpha 0 forward")
     dout = torch.randn(wl.T, wl.H, 128, generator=torch.Generator().manual_seed(5)).bfloat16().float()
     got = run_hip_bwd(wl, dout, rab=wl.rab)
-    assert _lib.last_kernel() == "bwd_generic_bf16"
+    assert _lib.last_kernel() == "bwd_mfma_bf16_d128"
     want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
                            wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=0.0, rab=wl.rab.numpy(),
                            contextual_seq_len=2)
@@ -593,7 +593,7 @@ def test_a_bias_with_alpha_zero_runs_on_the_generic_kernels(oracle):
     assert not got[0].float().abs().max().item() and not got[1].float().abs().max().item()
     st = error_stats(got[2], want[2])
     assert st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL, st
-    with ops.force_kernel(ops.KERNEL_TILED_DIRECT), pytest.raises(ValueError, match="generic kernels only"):
+    with ops.force_kernel(ops.KERNEL_TILED_DIRECT), pytest.raises(ValueError, match="head-dim-128 backward needs"):
         run_hip_bwd(wl, dout, rab=wl.rab)
 
 

@@ -1,0 +1,224 @@
+"""GPU parity of the general MFMA kernels (recir_amd/csrc/hstu_mfma_any.h): head dims other than 128,
+Dqk != Dv, fp16, the non-causal mask forms and a bias with alpha = 0, forward and backward, against the
+oracle on the same values.  The reference's operator takes any head dims, any float dtype and any mask
+string (recir/ops/kjt_split_per_feature.cpp:602-693); its accelerator kernel leaves Dv free
+(recir/ops/pallas/jagged_hstu_attention.py:1498-1503)."""
+import numpy as np
+import pytest
+import torch
+
+from tests.parity_util import BF16_REL, FP16_REL, error_stats, report, run_hip, run_oracle, to_device
+from tests.test_gpu_bwd import _scale_np, run_hip_bwd
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def oracle():
+    from oracle import hstu_oracle
+
+    hstu_oracle.build()
+    return hstu_oracle
+
+
+LENGTHS = [300, 129, 64, 1, 0, 517, 33]
+TARGETS = [40, 129, 0, 0, 0, 6, 50]
+
+# (Dqk, Dv): multiples of 8; the padded tile is the next of 32, 64, 128, 256 of the larger one
+DIMS = [(64, 64), (32, 32), (8, 8), (24, 40), (96, 96), (64, 128), (128, 64), (256, 256), (200, 72), (136, 128)]
+# (mask_type, max_attn_len, full_attn_size, contextual_seq_len)
+MASKS = {
+    "causal": ("lower_triangular", 0, 0, 0),
+    "causal_ctx": ("lower_triangular", 0, 0, 5),
+    "semilocal": ("lower_triangular", 70, 30, 0),
+    "semilocal_ctx": ("lower_triangular", 33, 0, 3),
+    "noncausal_window": ("full", 50, 20, 2),
+    "noncausal_diagonal": ("full", 0, 0, 0),
+}
+
+
+def _workload(dqk, dv, dtype, mask, seed, with_rab=False, H=2):
+    from recir_amd.workloads import make_jagged
+
+    mask_type, A, F, ctx = MASKS[mask]
+    return make_jagged(LENGTHS, TARGETS, H, dqk, dv, max_seq_len=600, alpha=1.0 / np.sqrt(dqk), dtype=dtype, seed=seed,
+                       with_rab=with_rab, rab_std=0.5, contextual_seq_len=ctx, tail_rows=5, max_attn_len=A,
+                       full_attn_size=F, mask_type=mask_type)
+
+
+FP16_QUANTUM = 2.0 ** -24  # spacing of fp16 below 2^-14: an absolute error no fp16 result can avoid
+
+
+def _assert_close(out, ref, tol, what):
+    """The three relative bounds of the bf16 parity tests; for fp16 results the per-row bound allows the
+    absolute spacing of fp16's subnormal range on top (a row that keeps one pair with a score near zero
+    is of the order of 1e-6 at these sizes, where fp16 has a handful of bits)."""
+    st = error_stats(out, ref)
+    report(what, st)
+    assert st["rel_to_max"] <= tol and st["rel_fro"] <= tol, (what, st)
+    if out.dtype != torch.float16:
+        assert st["worst_row_rel"] <= tol, (what, st)
+        return
+    o = out.detach().float().cpu().numpy().astype(np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    d = r.shape[-1]
+    row_err = np.abs(o - r).reshape(-1, d).max(axis=1)
+    row_ref = np.abs(r).reshape(-1, d).max(axis=1)
+    assert (row_err <= tol * (row_ref + st["row_floor"]) + FP16_QUANTUM).all(), (what, st)
+
+
+def _expected_kernel(dtype, dqk, dv, bwd=False):
+    d = max(dqk, dv)
+    dp = 32 if d <= 32 else 64 if d <= 64 else 128 if d <= 128 else 256
+    return f"{'bwd_' if bwd else ''}mfma_{dtype}_d{dp}"
+
+
+@pytest.mark.parametrize("dims", DIMS, ids=lambda d: f"{d[0]}x{d[1]}")
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_forward_head_dims(oracle, dims, dtype):
+    from recir_amd import _lib
+
+    dqk, dv = dims
+    wl = _workload(dqk, dv, dtype, "causal_ctx", seed=dqk + dv, with_rab=(dqk % 16 == 8))
+    out = run_hip(wl)
+    assert _lib.last_kernel() == _expected_kernel(dtype, dqk, dv), _lib.last_kernel()
+    assert out.dtype == (torch.bfloat16 if dtype == "bf16" else torch.float16)
+    ref = run_oracle(oracle, wl)
+    _assert_close(out, ref, BF16_REL if dtype == "bf16" else FP16_REL, f"fwd {dtype} {dqk}x{dv}")
+    assert not out[int(wl.seq_offsets[-1]):].float().cpu().numpy().any()
+
+
+@pytest.mark.parametrize("mask", sorted(MASKS))
+@pytest.mark.parametrize("dtype,dims", [("bf16", (64, 64)), ("fp16", (128, 128)), ("bf16", (128, 128))])
+def test_forward_masks(oracle, mask, dtype, dims):
+    from recir_amd import _lib, ops
+
+    wl = _workload(dims[0], dims[1], dtype, mask, seed=11, with_rab=mask.endswith("ctx"))
+    g = torch.Generator().manual_seed(5)
+    scale = (0.5 + torch.rand(wl.T, generator=g)) / 50 if mask.startswith("semilocal") else None
+    with ops.force_kernel(ops.KERNEL_MFMA_GENERAL):
+        out = run_hip(wl, attn_scale=scale)
+    assert _lib.last_kernel() == _expected_kernel(dtype, *dims)
+    ref = run_oracle(oracle, wl, attn_scale=scale)
+    _assert_close(out, ref, BF16_REL if dtype == "bf16" else FP16_REL, f"fwd {mask} {dtype} {dims}")
+    # the zero rows of the reference (rows that keep no pair cannot exist: a row keeps itself) and the tail
+    assert not out[int(wl.seq_offsets[-1]):].float().cpu().numpy().any()
+
+
+def test_noncausal_mask_runs_on_the_matrix_cores_by_default(oracle):
+    """Neither a forced selector nor the generic kernel: bf16 at head dim 128 under a non-causal mask."""
+    from recir_amd import _lib
+
+    wl = _workload(128, 128, "bf16", "noncausal_window", seed=3)
+    out = run_hip(wl)
+    assert _lib.last_kernel() == "mfma_bf16_d128"
+    _assert_close(out, run_oracle(oracle, wl), BF16_REL, "noncausal default")
+
+
+def test_bias_with_alpha_zero(oracle):
+    """alpha = 0: the scores are the bias alone; the head-dim-128 kernels cannot stage bias / alpha."""
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([200, 70], [10, 0], 2, 128, 128, max_seq_len=256, alpha=0.0, dtype="bf16", seed=4, with_rab=True,
+                     rab_std=1.0)
+    out = run_hip(wl)
+    assert _lib.last_kernel() == "mfma_bf16_d128"
+    _assert_close(out, run_oracle(oracle, wl), BF16_REL, "alpha 0")
+
+
+def _backward_reference(oracle, wl, dout, scale):
+    return oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha, attn_scale=_scale_np(scale),
+                           rab=None if wl.rab is None else wl.rab.numpy(), contextual_seq_len=wl.contextual_seq_len,
+                           max_attn_len=wl.max_attn_len, full_attn_size=wl.full_attn_size, mask_type=wl.mask_type)
+
+
+def _assert_grads(got, want, end, tol, what):
+    for g, w, name in zip(got, want, ("dq", "dk", "dv")):
+        _assert_close(g, w, tol, f"{what} {name}")
+        assert not g[end:].float().cpu().numpy().any(), (what, name, "tail rows must be zero")
+
+
+def _upstream(wl, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    d = torch.randn(wl.T, wl.H, wl.v.shape[2], generator=g)
+    return (d.bfloat16() if dtype == "bf16" else d.half()).float()
+
+
+@pytest.mark.parametrize("dims", [(64, 64), (32, 32), (8, 16), (96, 96), (64, 128), (128, 64), (24, 40)],
+                         ids=lambda d: f"{d[0]}x{d[1]}")
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_backward_head_dims(oracle, dims, dtype):
+    from recir_amd import _lib
+
+    dqk, dv = dims
+    wl = _workload(dqk, dv, dtype, "causal_ctx", seed=2 * dqk + dv, with_rab=(dqk % 16 == 8))
+    dout = _upstream(wl, dtype, 9)
+    got = run_hip_bwd(wl, dout, rab=wl.rab)
+    assert _lib.last_kernel() == _expected_kernel(dtype, dqk, dv, bwd=True), _lib.last_kernel()
+    want = _backward_reference(oracle, wl, dout, None)
+    _assert_grads(got, want[:3], int(wl.seq_offsets[-1]), BF16_REL if dtype == "bf16" else FP16_REL,
+                       f"bwd {dtype} {dqk}x{dv}")
+
+
+@pytest.mark.parametrize("mask", sorted(MASKS))
+@pytest.mark.parametrize("dtype,dims", [("bf16", (64, 64)), ("fp16", (128, 128)), ("bf16", (128, 128))])
+@pytest.mark.parametrize("scale_kind", ["default", "per_token"])
+def test_backward_masks(oracle, mask, dtype, dims, scale_kind):
+    from recir_amd import _lib, ops
+
+    wl = _workload(dims[0], dims[1], dtype, mask, seed=21, with_rab=mask.endswith("ctx"))
+    g = torch.Generator().manual_seed(6)
+    scale = (0.5 + torch.rand(wl.T, generator=g)) / 50 if scale_kind == "per_token" else None
+    dout = _upstream(wl, dtype, 10)
+    with ops.force_kernel(ops.KERNEL_MFMA_GENERAL):
+        got = run_hip_bwd(wl, dout, attn_scale=scale, rab=wl.rab)
+    assert _lib.last_kernel() == _expected_kernel(dtype, *dims, bwd=True)
+    want = _backward_reference(oracle, wl, dout, scale)
+    _assert_grads(got, want[:3], int(wl.seq_offsets[-1]), BF16_REL if dtype == "bf16" else FP16_REL,
+                       f"bwd {mask} {dtype} {dims} {scale_kind}")
+
+
+def test_general_and_head_dim_128_kernels_agree_at_full_size(oracle):
+    """Configuration 2 (the benchmark's shapes) through both MFMA families, forward and backward."""
+    from recir_amd import ops
+    from recir_amd.workloads import make_config
+
+    wl = make_config(2)
+    dout = _upstream(wl, "bf16", 12)
+    with ops.force_kernel(ops.KERNEL_TILED_DIRECT):
+        a = run_hip(wl, dtype="bf16")
+        ga = run_hip_bwd(wl, dout, dtype="bf16")
+    with ops.force_kernel(ops.KERNEL_MFMA_GENERAL):
+        b = run_hip(wl, dtype="bf16")
+        gb = run_hip_bwd(wl, dout, dtype="bf16")
+    assert error_stats(b, a.float().cpu().numpy())["rel_to_max"] <= 2 ** -7
+    for x, y, name in zip(ga, gb, ("dq", "dk", "dv")):
+        st = error_stats(y, x.float().cpu().numpy())
+        report(f"config 2 {name}: general against head-dim-128 kernels", st)
+        assert st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL, (name, st)
+
+
+def test_what_still_runs_on_the_generic_kernels():
+    """Head dims that are not multiples of 8, and the gradient of the bias table away from head dim 128."""
+    import recir_amd
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    prev = recir_amd.set_generic_kernel_policy("silent")
+    try:
+        wl = make_jagged([50, 20], [5, 0], 2, 20, 12, max_seq_len=64, alpha=0.2, dtype="bf16", seed=1)
+        run_hip(wl)
+        assert _lib.last_kernel() == "generic_bf16"
+        wl = make_jagged([50, 20], [5, 0], 2, 64, 64, max_seq_len=64, alpha=0.2, dtype="bf16", seed=1, with_rab=True)
+        q, k, v, off, nt = to_device(wl)
+        recir_amd.jagged_hstu_attention_backward(torch.ones_like(v), q, k, v, off, nt, max_seq_len=64, alpha=0.2,
+                                                 rab=wl.rab.cuda(), rab_grad=True)
+        assert _lib.last_kernel() == "bwd_generic_bf16"
+        # fp16 has no generic kernel: a clear error instead
+        wl = make_jagged([50, 20], [5, 0], 2, 20, 12, max_seq_len=64, alpha=0.2, dtype="fp16", seed=1)
+        with pytest.raises(ValueError, match="fp16 runs on the general MFMA kernel only"):
+            run_hip(wl)
+    finally:
+        recir_amd.set_generic_kernel_policy(prev)

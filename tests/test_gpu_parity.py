@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from tests.golden.cases import SMALL_CASES, build_inputs, fixture_file
-from tests.parity_util import (BF16_REL, FP8_MAX_ABS, FP32_ATOL, FP32_RTOL, assert_bf16_close, assert_same_zero_structure,
+from tests.parity_util import (BF16_REL, FP8_MAX_ABS, expected_kernel, FP32_ATOL, FP32_RTOL, assert_bf16_close, assert_same_zero_structure,
                                error_stats, run_hip, run_oracle, to_device)
 
 pytestmark = pytest.mark.gpu
@@ -55,8 +55,8 @@ def test_small_cases_match_reference_golden(oracle, name):
         assert_bf16_close(outb[:end], golden, name)
         assert not outb[end:].float().cpu().numpy().any()
         from recir_amd import _lib
-        # a mask type other than the causal one runs on the generic kernel
-        assert _lib.last_kernel().startswith("tiled_d128" if case["mask_type"] == "lower_triangular" else "generic")
+        # a mask type other than the causal one, or a head dim other than 128, runs on the general MFMA kernel
+        assert _lib.last_kernel() == expected_kernel(case["Dqk"], case["Dv"], causal=case["mask_type"] == "lower_triangular")
 
 
 def test_config1_smoke_shape_fp32(oracle):
@@ -97,14 +97,12 @@ def test_tiled_and_generic_kernels_agree(oracle, config):
                      contextual_seq_len=8 if config == 3 else 0, tail_rows=7)
     with ops.force_kernel(ops.KERNEL_TILED_DIRECT):
         a = run_hip(wl)
-        assert _lib.last_kernel().startswith("tiled_d128") and "regstage" not in _lib.last_kernel()
-    with ops.force_kernel(ops.KERNEL_TILED):
+        assert _lib.last_kernel().startswith("tiled_d128")
+    with ops.force_kernel(ops.KERNEL_MFMA_GENERAL):
         a2 = run_hip(wl)
-        assert "regstage" in _lib.last_kernel()
-    if config == 3:  # the direct tiling starts its score accumulators at the bias, this one adds it last
-        assert error_stats(a2, a.float().cpu().numpy())["rel_to_max"] <= 2 ** -7
-    else:
-        assert torch.equal(a, a2)  # same arithmetic in the same order: only the staging differs
+        assert _lib.last_kernel() == "mfma_bf16_d128"
+    # two tilings with their own order of the elementwise arithmetic: equal to bf16 rounding of P
+    assert error_stats(a2, a.float().cpu().numpy())["rel_to_max"] <= 2 ** -7
     with ops.force_kernel(ops.KERNEL_GENERIC):
         b = run_hip(wl)
         assert _lib.last_kernel() == "generic_bf16"
@@ -116,7 +114,7 @@ def test_tiled_and_generic_kernels_agree(oracle, config):
     np.testing.assert_array_equal(za, zb)
 
 
-@pytest.mark.parametrize("kernel", ["tiled", "tiled_regstage", "generic"])
+@pytest.mark.parametrize("kernel", ["tiled", "mfma_general", "generic"])
 @pytest.mark.parametrize("ctx", [0, 5, 200])
 def test_mask_is_bit_exact(oracle, kernel, ctx):
     """Positive constant scores and one-hot values make out[m, c] non-zero exactly when row m keeps a
@@ -135,7 +133,7 @@ def test_mask_is_bit_exact(oracle, kernel, ctx):
     for b, n in enumerate(lengths):
         for j in range(n):
             wl.v[off[b] + j, 0, j % 128] = 1.0
-    variant = {"tiled": ops.KERNEL_TILED_DIRECT, "tiled_regstage": ops.KERNEL_TILED, "generic": ops.KERNEL_GENERIC}[kernel]
+    variant = {"tiled": ops.KERNEL_TILED_DIRECT, "mfma_general": ops.KERNEL_MFMA_GENERAL, "generic": ops.KERNEL_GENERIC}[kernel]
     with ops.force_kernel(variant):
         out = run_hip(wl).float().cpu().numpy()
     want = np.zeros((wl.T, 128), dtype=bool)
@@ -259,7 +257,7 @@ def test_alpha_default_is_inverse_sqrt_of_head_dim(oracle, D, dtype):
     q, k, v, off, nt = to_device(wl)
     out = recir_amd.jagged_hstu_attention(q, k, v, off, nt, max_seq_len=wl.max_seq_len)  # alpha, attn_scale left out
     torch.cuda.synchronize()
-    assert _lib.last_kernel().startswith("tiled_d128" if D == 128 else "generic")
+    assert _lib.last_kernel() == expected_kernel(D, D, dtype)
     ref = run_oracle(oracle, wl)  # the oracle gets 1/sqrt(D) explicitly
     if dtype == "bf16":
         assert_bf16_close(out, ref, f"alpha=None D={D}")
@@ -584,7 +582,7 @@ def test_fp8_region_swap_keeps_the_reference_contextual_rule(oracle):
 
 
 def test_generic_kernel_policy_warns_or_rejects(oracle):
-    """A bf16 call that only the slow generic kernels cover (here: head dim 64) says so once by default,
+    """A bf16 call that only the slow generic kernels cover (here: head dims 20 / 12) says so once by default,
     is rejected by the C ABI under the 'error' policy (RECIR_HSTU_FLAG_TILED_ONLY), and is silent under
     'silent'; the result is the oracle's in every case that runs.  fp32 calls never warn."""
     import warnings
@@ -593,7 +591,7 @@ def test_generic_kernel_policy_warns_or_rejects(oracle):
     from recir_amd import _lib, ops
     from recir_amd.workloads import make_jagged
 
-    wl = make_jagged([70, 33, 0, 129], [8, 33, 0, 3], 2, 64, 64, max_seq_len=160, alpha=1.0 / 64, dtype="bf16", seed=41)
+    wl = make_jagged([70, 33, 0, 129], [8, 33, 0, 3], 2, 20, 12, max_seq_len=160, alpha=1.0 / 20, dtype="bf16", seed=41)
     want = run_oracle(oracle, wl)
     ops._generic_warned.clear()
     prev = recir_amd.set_generic_kernel_policy("warn")
@@ -604,8 +602,8 @@ def test_generic_kernel_policy_warns_or_rejects(oracle):
             out2 = run_hip(wl)
         assert _lib.last_kernel() == "generic_bf16"
         msgs = [str(w.message) for w in rec if issubclass(w.category, RuntimeWarning)]
-        assert len(msgs) == 1 and "head dims 64 / 64" in msgs[0], msgs  # once per reason
-        assert_bf16_close(out, want, "generic kernel, head dim 64")
+        assert len(msgs) == 1 and "head dims 20 / 12" in msgs[0], msgs  # once per reason
+        assert_bf16_close(out, want, "generic kernel, head dims 20 / 12")
         assert torch.equal(out, out2)
         recir_amd.set_generic_kernel_policy("error")
         with pytest.raises(ValueError, match="only the generic kernel"):
@@ -661,20 +659,13 @@ def test_semilocal_windows_across_tiles(oracle, A, F, ctx):
     with ops.force_kernel(ops.KERNEL_GENERIC):
         outg = run_hip(wl)
     assert_bf16_close(outg, ref, f"generic A{A} F{F}")
+    with ops.force_kernel(ops.KERNEL_MFMA_GENERAL):  # its own walk of the key tiles under the window
+        outm = run_hip(wl)
+    assert_bf16_close(outm, ref, f"general MFMA kernel A{A} F{F}")
     # fp8 q/k variant shares the tile walk
     out8 = run_hip(wl, fp8=True)
     st = error_stats(out8, ref)
     assert st["max_abs"] <= FP8_MAX_ABS, st
-
-
-def test_semilocal_is_rejected_by_the_tilings_without_it():
-    from recir_amd import ops
-    from recir_amd.workloads import make_jagged
-
-    wl = make_jagged([200], [10], 1, 128, 128, max_seq_len=256, alpha=1.0 / 128, dtype="bf16", max_attn_len=8)
-    for variant in (ops.KERNEL_TILED,):
-        with ops.force_kernel(variant), pytest.raises(ValueError, match="semi-local"):
-            run_hip(wl)
 
 
 def test_fp8_scales_ignore_padding_rows(oracle):
@@ -765,11 +756,13 @@ def test_grouped_work_lists_give_the_same_output(oracle):
             assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("kernel", ["mfma_general", "generic"])
 @pytest.mark.parametrize("A,F,ctx", [(0, 0, 0), (0, 0, 5), (7, 0, 0), (40, 16, 0), (3, 300, 2)])
-def test_noncausal_mask_is_bit_exact(oracle, A, F, ctx):
+def test_noncausal_mask_is_bit_exact(oracle, A, F, ctx, kernel):
     """The mask of a mask type other than "lower_triangular" (kjt_split_per_feature.cpp:650-671), read
-    off the zero pattern of the output as in test_mask_is_bit_exact.  Generic kernel."""
-    from recir_amd import _lib
+    off the zero pattern of the output as in test_mask_is_bit_exact: the general MFMA kernel (which the
+    library picks, and which leaves out the key tiles no row of a wave can see) and the generic one."""
+    from recir_amd import _lib, ops
     from recir_amd.workloads import make_jagged
 
     lengths = [130, 64, 65, 1, 0, 97]
@@ -783,8 +776,9 @@ def test_noncausal_mask_is_bit_exact(oracle, A, F, ctx):
     for b, n in enumerate(lengths):
         for j in range(n):
             wl.v[off[b] + j, 0, j % 128] = 1.0
-    out = run_hip(wl).float().cpu().numpy()
-    assert _lib.last_kernel() == "generic_bf16"
+    with ops.force_kernel(ops.KERNEL_AUTO if kernel == "mfma_general" else ops.KERNEL_GENERIC):
+        out = run_hip(wl).float().cpu().numpy()
+    assert _lib.last_kernel() == ("mfma_bf16_d128" if kernel == "mfma_general" else "generic_bf16")
     want = np.zeros((wl.T, 128), dtype=bool)
     for b, (n, t) in enumerate(zip(lengths, targets)):
         for m in range(n):
@@ -795,7 +789,7 @@ def test_noncausal_mask_is_bit_exact(oracle, A, F, ctx):
 
 
 def test_noncausal_mask_is_rejected_where_it_does_not_run():
-    """fp8 q/k and the tiled kernel selectors cover the causal mask only: an error, never another mask."""
+    """fp8 q/k and the head-dim-128 kernel selector cover the causal mask only: an error, never another mask."""
     import recir_amd
     from recir_amd import ops
     from recir_amd.workloads import make_jagged
@@ -803,12 +797,11 @@ def test_noncausal_mask_is_rejected_where_it_does_not_run():
     wl = make_jagged([70, 30], [5, 0], 2, 128, 128, max_seq_len=80, alpha=1 / 128, dtype="bf16", mask_type="full",
                      max_attn_len=9)
     q, k, v, off, nt = to_device(wl)
-    for variant in (ops.KERNEL_TILED, ops.KERNEL_TILED_DIRECT):
-        with ops.force_kernel(variant), pytest.raises(ValueError, match="generic kernel"):
-            run_hip(wl)
+    with ops.force_kernel(ops.KERNEL_TILED_DIRECT), pytest.raises(ValueError, match="head-dim-128 kernel needs"):
+        run_hip(wl)
     with pytest.raises(ValueError, match="causal"):
         ops.attention_via_fp8(80, 1 / 128, q, k, v, off, "full", nt, None, 9, 0, 0)
     dout = torch.ones_like(v)
-    with ops.force_kernel(ops.KERNEL_TILED_DIRECT), pytest.raises(ValueError, match="generic kernels"):
+    with ops.force_kernel(ops.KERNEL_TILED_DIRECT), pytest.raises(ValueError, match="head-dim-128 backward needs"):
         recir_amd.jagged_hstu_attention_backward(dout, q, k, v, off, nt, max_seq_len=80, alpha=1 / 128,
                                                  max_attn_len=9, invalid_attn_mask_type="full")

@@ -20,8 +20,15 @@ from recir_amd import build
 def device_asm(tmp_path_factory):
     if not (shutil.which("hipcc") or os.path.exists("/opt/rocm/bin/hipcc")):
         pytest.skip("hipcc not available")
-    out = tmp_path_factory.mktemp("asm") / "hstu_attn.s"
-    cmd = [a for a in build.compile_command(str(out)) if a not in ("-fPIC", "-shared")] + ["-S", "--cuda-device-only"]
+    return _device_asm_of(tmp_path_factory, "hstu_attn")
+
+
+def _device_asm_of(tmp_path_factory, unit):
+    """Device assembly of one translation unit of the library, with the library's own compile flags."""
+    out = tmp_path_factory.mktemp("asm") / (unit + ".s")
+    compiles = build.compile_commands(obj_dir=str(out.parent))[:-1]
+    (cmd,) = [c for c in compiles if os.path.basename(c[c.index("-c") + 1]) == unit + ".hip"]
+    cmd = [a for a in cmd[:cmd.index("-o")] if a not in ("-fPIC", "-c")] + ["-S", "--cuda-device-only", "-o", str(out)]
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     assert res.returncode == 0, res.stdout[-2000:]
     return out.read_text()
