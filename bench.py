@@ -28,7 +28,7 @@ if ROOT not in sys.path:
 
 # MI355X dense MFMA peaks.  The fp8 variant runs Q.K^T in fp8 and P.V in bf16 (equal FLOPs), so its
 # ceiling is the harmonic blend 2 / (1/5000 + 1/2500) = 3333 TFLOP/s.
-PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 2.0 / (1.0 / 5000.0 + 1.0 / 2500.0), "fp32": 157.3}
+PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp8": 2.0 / (1.0 / 5000.0 + 1.0 / 2500.0), "fp32": 157.3}
 PEAK_HBM_GBS = 8000.0
 
 
@@ -41,6 +41,8 @@ def describe(wl, cfg):
         5: "config5: config2 with q,k in fp8 e4m3 (per-head scale amax/448), v bf16",
         6: "config6: config2 with the semi-local mask (max_attn_len 256, full_attn_size 256)",
         7: "config7: 16 sequences of 4096 history tokens, no targets, H=4, D=128, bf16 (steady state: two workgroups per CU throughout)",
+        8: "config8: config2's sequences with H=8, Dqk=Dv=64, bf16 (general MFMA kernels)",
+        9: "config9: config2 in fp16 (general MFMA kernels)",
     }
     return names[cfg]
 
@@ -373,10 +375,10 @@ def bench_backward(args, wl, L, dev):
 
     from recir_amd import _lib
 
-    if wl.dtype not in ("bf16", "fp32"):
+    if wl.dtype not in ("bf16", "fp16", "fp32"):
         print("--backward supports the bf16/fp32 configurations", file=sys.stderr)
         sys.exit(2)
-    dt = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
+    dt = {"fp32": torch.float32, "fp16": torch.float16}.get(wl.dtype, torch.bfloat16)
     q, k, v = wl.q.to(dev, dt), wl.k.to(dev, dt), wl.v.to(dev, dt)
     g = torch.Generator().manual_seed(1)
     dout = torch.randn(wl.T, wl.H, v.shape[2], generator=g).to(dev, dt)
@@ -386,7 +388,7 @@ def bench_backward(args, wl, L, dev):
     drab = torch.empty_like(rab) if (args.rab_grad and rab is not None) else None
     T, H, Dqk = q.shape
     Dv = v.shape[2]
-    code = _lib.DTYPE_FP32 if wl.dtype == "fp32" else _lib.DTYPE_BF16
+    code = {"fp32": _lib.DTYPE_FP32, "fp16": _lib.DTYPE_FP16}.get(wl.dtype, _lib.DTYPE_BF16)
     ws_bytes = L.recir_hstu_attn_bwd_workspace_bytes(T, wl.B, H, Dqk, Dv, code)
     if drab is not None:
         ws_bytes += L.recir_hstu_attn_bwd_rab_grad_workspace_bytes(H, wl.max_seq_len)
@@ -497,7 +499,7 @@ def main():
     # of configuration 2 run up to 20 % slower): the default warm-up covers that
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6, 7])
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6, 7, 8, 9])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", type=int, default=0, help="kernel selector (0 auto)")
     ap.add_argument("--rab-grad", action="store_true", help="with --backward and a configuration that has a bias table: its gradient too")
@@ -562,12 +564,12 @@ def main():
     if args.jagged:
         return bench_jagged(args, wl, dev)
     fp8 = wl.dtype == "fp8"
-    dt = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
+    dt = {"fp32": torch.float32, "fp16": torch.float16}.get(wl.dtype, torch.bfloat16)
     q, k, v = wl.q.to(dev, dt), wl.k.to(dev, dt), wl.v.to(dev, dt)
     off, nt = wl.seq_offsets.to(dev), wl.num_targets.to(dev)
     rab = None if wl.rab is None else wl.rab.to(dev)
     q_scale = k_scale = None
-    dtype_code = {"fp32": _lib.DTYPE_FP32, "bf16": _lib.DTYPE_BF16, "fp8": _lib.DTYPE_FP8_E4M3}[wl.dtype]
+    dtype_code = {"fp32": _lib.DTYPE_FP32, "bf16": _lib.DTYPE_BF16, "fp8": _lib.DTYPE_FP8_E4M3, "fp16": _lib.DTYPE_FP16}[wl.dtype]
     if fp8:
         import recir_amd
 
@@ -610,7 +612,7 @@ def main():
     kernel_name = _lib.last_kernel()
 
     # attention kernel alone: HIP events on the launch stream around K launches with the work list reused
-    reuse = _lib.FLAG_REUSE_PLAN if kernel_name.startswith("tiled") else 0
+    reuse = _lib.FLAG_REUSE_PLAN if kernel_name.startswith(("tiled", "mfma")) else 0
     call()
     for _ in range(5):
         call(reuse)

@@ -26,7 +26,9 @@
 //   x = alpha S + bias;  P = silu(x) keep;  dS = dP silu'(x) keep   (dO . V is dP)
 //   out = scale P V;  dQ = alpha scale dS K;  dK = alpha (scale dS)^T Q;  dV = (scale P)^T dO
 // The scale of a query row multiplies a column in FWD and DQ (applied to the accumulators at the
-// end) and a streamed row in DKV (applied per element when it is per token).
+// end) and a streamed row in DKV (applied per element when it is per token; fp16: times a power of
+// two taken from the largest scale of the item's rows and divided out of the accumulators at the
+// end, so that P and dS times a scale of the order of 1 / max_seq_len stay in fp16's normal range).
 #pragma once
 #include <type_traits>
 
@@ -64,7 +66,7 @@ __device__ __forceinline__ unsigned any_pack2(float lo, float hi) {
 }
 
 template <int MODE, bool F16, int DP>
-__global__ __launch_bounds__(256, (MODE == ANY_FWD && DP <= 128) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
+__global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
   const Params& p = bp.f;
   constexpr bool BWD = MODE != ANY_FWD;
   constexpr int NK = DP / 16;       // steps of 16 along the head dim in a score product
@@ -77,6 +79,7 @@ __global__ __launch_bounds__(256, (MODE == ANY_FWD && DP <= 128) ? 2 : 1) void h
   __shared__ __attribute__((aligned(16))) unsigned char Y2s[2][ANY_BN * RS];
   __shared__ float bias_s[2][ANY_BM + ANY_BN];
   __shared__ float scale_s[2][ANY_BN];
+  __shared__ float red_s[4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -183,6 +186,25 @@ __global__ __launch_bounds__(256, (MODE == ANY_FWD && DP <= 128) ? 2 : 1) void h
       t_begin = r_begin / ANY_BN;
       t_end = (r_end + ANY_BN - 1) / ANY_BN;
     }
+    // fp16 with a per-token scale, DKV: 2^-e with 2^(e-1) <= largest |scale| of the streamed rows < 2^e
+    float pow2_up = 1.0f, pow2_down = 1.0f;
+    if constexpr (MODE == ANY_DKV && F16) {
+      if (per_token) {
+        float mx = 0.f;
+        for (int r = t_begin * ANY_BN + tid; r < min(t_end * ANY_BN, si.n); r += 256) mx = fmaxf(mx, fabsf(p.attn_scale[si.s + r]));
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
+        if (lane == 0) red_s[wave] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(red_s[0], red_s[1]), fmaxf(red_s[2], red_s[3]));
+        const int e = (int)((__float_as_uint(mx) >> 23) & 0xffu) - 126;  // mx < 2^e
+        if (mx > 0.f && mx < 3.0e38f) {
+          const int ec = min(max(e, -100), 100);
+          pow2_up = __uint_as_float((unsigned)(127 - ec) << 23);
+          pow2_down = __uint_as_float((unsigned)(127 + ec) << 23);
+        }
+      }
+    }
     const bool has_skip = skip_a < skip_b;
     auto next_tile = [&](int t) { return (has_skip && t + 1 == skip_a) ? skip_b : t + 1; };
 
@@ -210,7 +232,7 @@ __global__ __launch_bounds__(256, (MODE == ANY_FWD && DP <= 128) ? 2 : 1) void h
         st.bias = rabg[idx];
       }
       st.scale = 1.0f;
-      if (MODE == ANY_DKV && per_token && tid < ANY_BN) st.scale = p.attn_scale[si.s + min(r0 + tid, si.n - 1)];
+      if (MODE == ANY_DKV && per_token && tid < ANY_BN) st.scale = p.attn_scale[si.s + min(r0 + tid, si.n - 1)] * pow2_up;
     };
     auto store_tiles = [&](int buf, const Staged& st) __attribute__((always_inline)) {
 #pragma unroll
@@ -313,7 +335,8 @@ __global__ __launch_bounds__(256, (MODE == ANY_FWD && DP <= 128) ? 2 : 1) void h
       if (!noncausal) {
         const bool history = j_lo < id_hi && (id_hi >= si.tail0 || id_lo - j_hi <= si.win);
         if (!(diagonal || history || j_lo < si.ctx_eff)) return;
-        full = !semi && j_hi < m_lo && j_hi < si.cap && r1 <= si.n;
+        // every pair kept: history keys below every row, and under a window inside it for every row
+        full = j_hi < m_lo && j_hi < si.cap && r1 <= si.n && (!semi || id_lo >= si.tail0 || id_hi - j_lo <= si.win);
       } else {
         const int idj_lo = min(j_lo, si.cap), idj_hi = min(j_hi, si.cap);
         bool window = false, tail = false;
@@ -352,7 +375,7 @@ __global__ __launch_bounds__(256, (MODE == ANY_FWD && DP <= 128) ? 2 : 1) void h
     if (c_valid) {
       float uni = 1.0f / (float)p.N;  // the scale where it is the same for every row
       if (p.attn_scale && !per_token) uni = p.attn_scale[0];
-      const float col_scale = MODE == ANY_DKV ? (per_token ? 1.0f : uni) : (per_token ? p.attn_scale[si.s + c] : uni);
+      const float col_scale = MODE == ANY_DKV ? (per_token ? pow2_down : uni) : (per_token ? p.attn_scale[si.s + c] : uni);
       auto store_rows = [&](void* base, int D, const f32x16* acc, float f) __attribute__((always_inline)) {
         unsigned short* orow = (unsigned short*)base + ((size_t)(si.s + c) * p.H + h) * D;
 #pragma unroll

@@ -180,6 +180,23 @@ def test_backward_masks(oracle, mask, dtype, dims, scale_kind):
                        f"bwd {mask} {dtype} {dims} {scale_kind}")
 
 
+def test_fp16_backward_with_small_per_token_scales(oracle):
+    """Per-token scales of the order of 1 / max_seq_len times P or dS fall below fp16's normal range (6e-5):
+    the key-stationary kernel multiplies by a power of two taken from the largest scale of the rows it
+    streams and divides it out of the fp32 accumulators.  Rows with a single pair (the diagonal-only mask)
+    show the difference: their gradient is one product."""
+    from recir_amd import _lib
+
+    wl = _workload(64, 24, "fp16", "noncausal_diagonal", seed=31, with_rab=True)
+    g = torch.Generator().manual_seed(7)
+    scale = (0.5 + torch.rand(wl.T, generator=g)) / 2000
+    dout = _upstream(wl, "fp16", 13)
+    got = run_hip_bwd(wl, dout, attn_scale=scale, rab=wl.rab)
+    assert _lib.last_kernel() == "bwd_mfma_fp16_d64"
+    want = _backward_reference(oracle, wl, dout, scale)
+    _assert_grads(got, want[:3], int(wl.seq_offsets[-1]), FP16_REL, "fp16 small per-token scales")
+
+
 def test_general_and_head_dim_128_kernels_agree_at_full_size(oracle):
     """Configuration 2 (the benchmark's shapes) through both MFMA families, forward and backward."""
     from recir_amd import ops
