@@ -65,6 +65,8 @@ __device__ __forceinline__ unsigned any_pack2(float lo, float hi) {
   }
 }
 
+// Two workgroups per CU where the registers allow it (a few spills included: one workgroup per CU
+// measured 20-35 % slower at these shapes).
 template <int MODE, bool F16, int DP>
 __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
   const Params& p = bp.f;
@@ -259,47 +261,64 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
 
     // One (64 streamed rows) x (32 stationary rows) block of this wave.  MASKED: the predicate is
     // evaluated per pair; otherwise every pair of the block is known to be kept.
+    // MASKED: 0 every pair kept, 1 the causal / semi-local predicate per pair, 2 the non-causal one.
+    // The predicates are written with bitwise operators on 0 / 1 values: the short-circuit forms of
+    // hstu_common.h compile to a divergent branch per pair here.
     auto tile_body = [&](auto masked_tag, int r0, int buf) __attribute__((always_inline)) {
-      constexpr bool MASKED = decltype(masked_tag)::value;
+      constexpr int MASKED = decltype(masked_tag)::value;
       const unsigned char* y1 = &Y1s[buf][0];
       const unsigned char* y2 = &Y2s[buf][0];
-      f32x16 S[2], dP[BWD ? 2 : 1];
+      unsigned pw[2][8], dsw[BWD ? 2 : 1][8];
+      // first streamed row of this lane half; opaque, so that the rows of the 32 registers are derived
+      // from it inside the tile instead of being kept in 32 registers across the loop
+      int rbase = r0 + 4 * half;
+      if (MASKED) asm volatile("" : "+v"(rbase));
+      // one 32-row block of scores at a time (both at once cost the masked bodies their registers)
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
+        f32x16 Sb, dPb;
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) S[blk] = any_mfma<F16>(row_frag(y1, blk, kk), x1[kk], kk == 0 ? zero16 : S[blk]);
+        for (int kk = 0; kk < NK; ++kk) Sb = any_mfma<F16>(row_frag(y1, blk, kk), x1[kk], kk == 0 ? zero16 : Sb);
         if constexpr (BWD) {
 #pragma unroll
-          for (int kk = 0; kk < NK; ++kk) dP[blk] = any_mfma<F16>(row_frag(y2, blk, kk), x2[kk], kk == 0 ? zero16 : dP[blk]);
+          for (int kk = 0; kk < NK; ++kk) dPb = any_mfma<F16>(row_frag(y2, blk, kk), x2[kk], kk == 0 ? zero16 : dPb);
         }
-      }
-      unsigned pw[2][8], dsw[BWD ? 2 : 1][8];
-#pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
         float pv[16], dsv[BWD ? 16 : 1];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int rl = 32 * blk + 8 * (r >> 2) + 4 * half + (r & 3);  // streamed row of this register
-          float x = S[blk][r] * p.alpha;
+          float x = Sb[r] * p.alpha;
           if (rabg) x += bias_s[buf][MODE == ANY_DKV ? rl - (c - c0) + (ANY_BM - 1) : (c - c0) - rl + (ANY_BN - 1)];
           const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * neg_log2e));
           float pe = x * sig;
           float de = 0.f;
-          if constexpr (BWD) de = dP[blk][r] * (sig + pe * (1.0f - sig));  // silu'(x) = sig (1 + x (1 - sig))
+          if constexpr (BWD) de = dPb[r] * (sig + pe * (1.0f - sig));  // silu'(x) = sig (1 + x (1 - sig))
           if (MODE == ANY_DKV && per_token) {
             const float rs = scale_s[buf][rl];
             pe *= rs;
             de *= rs;
           }
           if (MASKED) {
-            const int rr = r0 + rl;
+            const int rr = rbase + (32 * blk + 8 * (r >> 2) + (r & 3));
             const int m = MODE == ANY_DKV ? rr : c, j = MODE == ANY_DKV ? c : rr;
-            const bool kp = keep_pair(m, j, si, noncausal) && rr < si.n && c < si.n;
+            const int idm = min(m, si.cap);
+            int kp = (int)(m == j) | (int)(j < si.ctx_eff);
+            if (MASKED == 1) {
+              kp |= (int)(j < idm) & ((int)(idm - j <= si.win) | (int)(idm >= si.tail0));
+            } else if (si.win != WIN_ALL) {
+              // (without a full-attention tail tail0 is INT_MAX: both ids below count as 0 and the last term is never true)
+              const int idj = min(j, si.cap);
+              const int gr = idm < si.tail0 ? 0 : idm, gc = idj < si.tail0 ? 0 : idj;
+              kp |= (int)(abs(idm - idj) <= si.win) | (int)(gr - gc > 0);
+            }
+            kp &= (int)(rr < si.n) & (int)(c < si.n);
             pe = kp ? pe : 0.f;
             de = kp ? de : 0.f;
           }
           pv[r] = pe;
           if constexpr (BWD) dsv[r] = de;
+          // the masked bodies four pairs at a time: left to itself the scheduler interleaves all 32 and spills
+          if (MASKED && (r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -345,9 +364,12 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
           if (si.tail0 != 0x7fffffff) tail = id_hi >= si.tail0 && (idj_lo < si.tail0 ? 0 : idj_lo) < id_hi;
         }
         if (!(diagonal || window || tail || j_lo < si.ctx_eff)) return;
+        // every pair kept: the two id ranges lie within the window of each other all along
+        full = si.win != WIN_ALL && id_hi - idj_lo <= si.win && idj_hi - id_lo <= si.win && r1 <= si.n;
       }
-      if (full) tile_body(std::false_type{}, r0, buf);
-      else tile_body(std::true_type{}, r0, buf);
+      if (full) tile_body(std::integral_constant<int, 0>{}, r0, buf);
+      else if (!noncausal) tile_body(std::integral_constant<int, 1>{}, r0, buf);
+      else tile_body(std::integral_constant<int, 2>{}, r0, buf);
     };
 
     Staged st;
