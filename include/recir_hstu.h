@@ -41,8 +41,8 @@ extern "C" {
  *     fp8 q/k), Dqk = Dv = 128, 16-byte aligned tensors, the causal or semi-local mask, alpha != 0
  *     when there is a bias; the only ones that produce the gradient of the bias table on MFMAs;
  *   - the general MFMA kernels ("mfma_*", "bwd_mfma_*"): bf16 or fp16, Dqk and Dv any multiples of
- *     8 up to 256 (backward: 128) and independent of each other, 16-byte aligned tensors, every
- *     mask, any alpha; a few times slower than the first group at its own shape;
+ *     8 up to 256 and independent of each other, 16-byte aligned tensors, every mask, any alpha;
+ *     about twice the time of the first group at its own shape;
  *   - the generic kernels ("generic_*", "bwd_generic_*"): one wave per (token, head), bf16 or fp32,
  *     any head dim up to 512; two orders of magnitude slower.  fp32 tensors always run here.
  */
@@ -78,7 +78,7 @@ extern "C" {
                                                      in recir_hstu_last_error) a call that only the
                                                      generic kernels cover instead of running it
                                                      there: fp32 tensors, head dims that are not
-                                                     multiples of 8 or exceed 256 (backward: 128),
+                                                     multiples of 8 or exceed 256,
                                                      tensors not 16-byte aligned, the gradient of the
                                                      bias table outside the head-dim-128 kernels'
                                                      domain.  Forward and backward.                  */

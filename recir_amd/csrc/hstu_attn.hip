@@ -697,7 +697,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   const bool bias_needs_other = rab && !std::isnormal(1.0f / alpha);
   const bool d128_ok = bf16 && Dqk == HD && Dv == HD && aligned && !noncausal && !bias_needs_other;
   // the general MFMA kernels (hstu_mfma_any.h): no gradient of the bias table
-  const int any_dp = mfma_any_padded_dim(Dqk, Dv, 128);
+  const int any_dp = mfma_any_padded_dim(Dqk, Dv, 256);
   const bool any_ok = (bf16 || f16) && any_dp != 0 && aligned && !drab;
   if (variant > 3) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "unknown kernel selector %u", variant);
   if (variant == 3 && !d128_ok)
@@ -706,11 +706,11 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
                 "and alpha != 0 with a bias");
   if (variant == 2 && !any_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "the general MFMA backward needs bf16 or fp16, head dims that are multiples of 8 up to 128, 16-byte aligned "
+                "the general MFMA backward needs bf16 or fp16, head dims that are multiples of 8 up to 256, 16-byte aligned "
                 "tensors and no gradient of the bias table");
   if (f16 && (variant == 1 || !any_ok))
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "the fp16 backward runs on the general MFMA kernels only: head dims that are multiples of 8 up to 128, 16-byte "
+                "the fp16 backward runs on the general MFMA kernels only: head dims that are multiples of 8 up to 256, 16-byte "
                 "aligned tensors, no gradient of the bias table (Dqk=%d Dv=%d)", Dqk, Dv);
   const bool use_tiled = d128_ok && (variant == 0 || variant == 3);
   const bool use_any = !use_tiled && any_ok && variant != 1;
@@ -805,7 +805,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   if (flags & RECIR_HSTU_FLAG_TILED_ONLY)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
                 "only the generic kernels cover this call (the MFMA kernels need bf16 or fp16, head dims that are multiples of 8 "
-                "up to 128, 16-byte aligned tensors, and for the gradient of the bias table bf16, Dqk = Dv = 128, the causal or "
+                "up to 256, 16-byte aligned tensors, and for the gradient of the bias table bf16, Dqk = Dv = 128, the causal or "
                 "semi-local mask and alpha != 0): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
   if (int rc = zero_drab()) return rc;
   const dim3 grid((unsigned)T, (unsigned)H);

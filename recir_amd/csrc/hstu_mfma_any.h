@@ -1,5 +1,5 @@
 // MFMA kernels of the HSTU attention forward and backward for everything the kernels written for
-// head dim 128 do not take: head dims that are multiples of 8 up to 256 (forward) or 128 (backward),
+// head dim 128 do not take: head dims that are multiples of 8 up to 256,
 // Dqk and Dv independent, bf16 or fp16 values, every mask the operator knows (causal with targets
 // and contextual prefix, semi-local, the non-causal forms), a bias with any alpha.  One template,
 // three modes; nothing here is hand-scheduled: the point is to keep such calls on the matrix
@@ -15,6 +15,8 @@
 //                               dQ^T[:,c] += K^T[:,r] dS^T[r,c]
 //   DKV  c = key,   r = query   S[r,c] = Q[r,:] . K[c,:],  dP[r,c] = dO[r,:] . V[c,:]
 //                               dV^T[:,c] += dO^T[:,r] P[r,c],  dK^T[:,c] += Q^T[:,r] dS[r,c]
+//   DV, DK                      the two halves of DKV as passes of their own (padded head dim 256, where
+//                               both accumulators and both operand sets do not fit one wave's registers)
 // Every product is v_mfma_f32_32x32x16 with the streamed tile as the A operand: rows of the tile for
 // the score products (ds_read_b128), the transposed tile for the accumulating products
 // (ds_read_b64_tr_b16 on the same row-major tile).  The 32 x 32 accumulator layout of a score block
@@ -41,7 +43,7 @@ typedef __attribute__((ext_vector_type(2))) _Float16 any_f16x2;
 typedef __attribute__((ext_vector_type(4))) short any_i16x4;
 typedef __attribute__((address_space(3))) any_i16x4 any_lds_i16x4;
 
-constexpr int ANY_FWD = 0, ANY_DQ = 1, ANY_DKV = 2;
+constexpr int ANY_FWD = 0, ANY_DQ = 1, ANY_DKV = 2, ANY_DV = 3, ANY_DK = 4;  // DV, DK: the two halves of DKV as passes of their own
 constexpr int ANY_BM = 128;  // stationary rows per workgroup
 constexpr int ANY_BN = 64;   // streamed rows per tile
 constexpr float kAnyLog2e = 1.4426950408889634f;
@@ -70,7 +72,9 @@ __device__ __forceinline__ unsigned any_pack2(float lo, float hi) {
 template <int MODE, bool F16, int DP>
 __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
   const Params& p = bp.f;
-  constexpr bool BWD = MODE != ANY_FWD;
+  constexpr bool KEYS = MODE >= ANY_DKV;                                  // the stationary rows are keys
+  constexpr bool HAS_DP = MODE == ANY_DQ || MODE == 2 || MODE == ANY_DK;   // dP, dS and the product that dS feeds
+  constexpr bool HAS_P = MODE == ANY_FWD || MODE == 2 || MODE == ANY_DV;   // the product that P feeds
   constexpr int NK = DP / 16;       // steps of 16 along the head dim in a score product
   constexpr int NB = DP / 32;       // 32-row blocks of a transposed accumulator
   constexpr int RS = DP * 2 + 16;   // bytes between tile rows in LDS (the 16 spread the rows over the banks)
@@ -99,10 +103,8 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
 
   if (MODE == ANY_FWD) zero_tail_rows_of<256>(p, p.out, (size_t)p.H * p.Dv * 2);
   if (MODE == ANY_DQ) zero_tail_rows_of<256>(p, bp.dq, (size_t)p.H * p.Dqk * 2);
-  if (MODE == ANY_DKV) {
-    zero_tail_rows_of<256>(p, bp.dk, (size_t)p.H * p.Dqk * 2);
-    zero_tail_rows_of<256>(p, bp.dv, (size_t)p.H * p.Dv * 2);
-  }
+  if (KEYS && HAS_DP) zero_tail_rows_of<256>(p, bp.dk, (size_t)p.H * p.Dqk * 2);
+  if (KEYS && HAS_P) zero_tail_rows_of<256>(p, bp.dv, (size_t)p.H * p.Dv * 2);
 
   const bool noncausal = (p.flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL) != 0;
   const bool per_token = p.attn_scale && (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
@@ -124,10 +126,10 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
     const int cap0 = si.cap > 0 ? si.cap : 0;
 
     // tensors by role: *1 has Dqk elements per row, *2 has Dv
-    const char* __restrict__ X1g = (const char*)(MODE == ANY_DKV ? p.k : p.q);
-    const char* __restrict__ X2g = (const char*)(MODE == ANY_DKV ? p.v : bp.dout);
-    const char* __restrict__ Y1g = (const char*)(MODE == ANY_DKV ? p.q : p.k);
-    const char* __restrict__ Y2g = (const char*)(MODE == ANY_DKV ? bp.dout : p.v);
+    const char* __restrict__ X1g = (const char*)(KEYS ? p.k : p.q);
+    const char* __restrict__ X2g = (const char*)(KEYS ? p.v : bp.dout);
+    const char* __restrict__ Y1g = (const char*)(KEYS ? p.q : p.k);
+    const char* __restrict__ Y2g = (const char*)(KEYS ? bp.dout : p.v);
     const size_t rb1 = (size_t)p.H * p.Dqk * 2, rb2 = (size_t)p.H * p.Dv * 2;
     const size_t hb1 = (size_t)h * p.Dqk * 2, hb2 = (size_t)h * p.Dv * 2;
     const float* __restrict__ rabg = p.rab ? p.rab + (size_t)h * rab_w : nullptr;
@@ -138,20 +140,20 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
     const bool c_valid = c < c_end;
     const int c_lo = cw0, c_hi = min(cw0 + 31, c_end - 1);
     const bool wave_has_rows = c_lo < c_end;
-    u32x4 x1[NK], x2[BWD ? NK : 1];
+    u32x4 x1[NK], x2[HAS_DP ? NK : 1];
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
       const int d0 = kk * 16 + half * 8;
       x1[kk] = (c_valid && d0 < p.Dqk) ? *(const u32x4*)(X1g + (size_t)(si.s + c) * rb1 + hb1 + (size_t)d0 * 2) : zero4;
-      if constexpr (BWD) x2[kk] = (c_valid && d0 < p.Dv) ? *(const u32x4*)(X2g + (size_t)(si.s + c) * rb2 + hb2 + (size_t)d0 * 2) : zero4;
+      if constexpr (HAS_DP) x2[kk] = (c_valid && d0 < p.Dv) ? *(const u32x4*)(X2g + (size_t)(si.s + c) * rb2 + hb2 + (size_t)d0 * 2) : zero4;
     }
 
-    f32x16 acc1[BWD ? NB : 1];  // DQ: dQ^T   DKV: dK^T
-    f32x16 acc2[MODE == ANY_DQ ? 1 : NB];  // FWD: O^T   DKV: dV^T
+    f32x16 acc1[HAS_DP ? NB : 1];  // DQ: dQ^T   DKV, DK: dK^T
+    f32x16 acc2[HAS_P ? NB : 1];   // FWD: O^T   DKV, DV: dV^T
 #pragma unroll
-    for (int i = 0; i < (BWD ? NB : 1); ++i) acc1[i] = zero16;
+    for (int i = 0; i < (HAS_DP ? NB : 1); ++i) acc1[i] = zero16;
 #pragma unroll
-    for (int i = 0; i < (MODE == ANY_DQ ? 1 : NB); ++i) acc2[i] = zero16;
+    for (int i = 0; i < (HAS_P ? NB : 1); ++i) acc2[i] = zero16;
 
     // ---- streamed rows: tiles [t_begin, t_end) of 64, minus the run [skip_a, skip_b) ----
     int t_begin = 0, t_end = 0, skip_a = 0, skip_b = 0;
@@ -160,7 +162,7 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
       // key or a row of the full-attention tail opens the whole sequence
       const bool tail_set = si.tail0 != 0x7fffffff;
       const int idc_lo = min(c0, si.cap), idc_hi = min(c_end - 1, si.cap);
-      const bool whole = MODE == ANY_DKV ? (c0 < si.ctx_eff || tail_set) : (si.ctx_eff > 0 || (tail_set && idc_hi >= si.tail0));
+      const bool whole = KEYS ? (c0 < si.ctx_eff || tail_set) : (si.ctx_eff > 0 || (tail_set && idc_hi >= si.tail0));
       int r_begin = 0, r_end = si.n;
       if (!whole) {
         if (si.win == WIN_ALL) {
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
       }
       t_begin = r_begin / ANY_BN;
       t_end = (r_end + ANY_BN - 1) / ANY_BN;
-    } else if (MODE != ANY_DKV) {  // keys
+    } else if (!KEYS) {  // keys
       const int r_end = min(si.n, max(c_end, si.ctx_eff));
       t_end = (r_end + ANY_BN - 1) / ANY_BN;
       // semi-local: keys below the window of the first row, unless a row of the full-attention
@@ -190,7 +192,7 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
     }
     // fp16 with a per-token scale, DKV: 2^-e with 2^(e-1) <= largest |scale| of the streamed rows < 2^e
     float pow2_up = 1.0f, pow2_down = 1.0f;
-    if constexpr (MODE == ANY_DKV && F16) {
+    if constexpr (KEYS && F16) {
       if (per_token) {
         float mx = 0.f;
         for (int r = t_begin * ANY_BN + tid; r < min(t_end * ANY_BN, si.n); r += 256) mx = fmaxf(mx, fabsf(p.attn_scale[si.s + r]));
@@ -228,13 +230,13 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
       st.bias = 0.f;
       if (rabg && tid < ANY_BM + ANY_BN - 1) {
         // entry e of the band holds the bias of m - j = dmin + e
-        const int dmin = MODE == ANY_DKV ? r0 - c0 - (ANY_BM - 1) : c0 - r0 - (ANY_BN - 1);
+        const int dmin = KEYS ? r0 - c0 - (ANY_BM - 1) : c0 - r0 - (ANY_BN - 1);
         int idx = dmin + tid + p.N - 1;
         idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
         st.bias = rabg[idx];
       }
       st.scale = 1.0f;
-      if (MODE == ANY_DKV && per_token && tid < ANY_BN) st.scale = p.attn_scale[si.s + min(r0 + tid, si.n - 1)] * pow2_up;
+      if (KEYS && per_token && tid < ANY_BN) st.scale = p.attn_scale[si.s + min(r0 + tid, si.n - 1)] * pow2_up;
     };
     auto store_tiles = [&](int buf, const Staged& st) __attribute__((always_inline)) {
 #pragma unroll
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
         *(u32x4*)(&Y2s[buf][row * RS + ch * 16]) = st.y2[i];
       }
       if (tid < ANY_BM + ANY_BN - 1) bias_s[buf][tid] = st.bias;
-      if (MODE == ANY_DKV && tid < ANY_BN) scale_s[buf][tid] = st.scale;
+      if (KEYS && tid < ANY_BN) scale_s[buf][tid] = st.scale;
     };
 
     auto row_frag = [&](const unsigned char* y, int blk, int kk) __attribute__((always_inline)) {
@@ -268,7 +270,7 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
       constexpr int MASKED = decltype(masked_tag)::value;
       const unsigned char* y1 = &Y1s[buf][0];
       const unsigned char* y2 = &Y2s[buf][0];
-      unsigned pw[2][8], dsw[BWD ? 2 : 1][8];
+      unsigned pw[2][8], dsw[HAS_DP ? 2 : 1][8];
       // first streamed row of this lane half; opaque, so that the rows of the 32 registers are derived
       // from it inside the tile instead of being kept in 32 registers across the loop
       int rbase = r0 + 4 * half;
@@ -279,28 +281,28 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
         f32x16 Sb, dPb;
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk) Sb = any_mfma<F16>(row_frag(y1, blk, kk), x1[kk], kk == 0 ? zero16 : Sb);
-        if constexpr (BWD) {
+        if constexpr (HAS_DP) {
 #pragma unroll
           for (int kk = 0; kk < NK; ++kk) dPb = any_mfma<F16>(row_frag(y2, blk, kk), x2[kk], kk == 0 ? zero16 : dPb);
         }
-        float pv[16], dsv[BWD ? 16 : 1];
+        float pv[16], dsv[HAS_DP ? 16 : 1];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int rl = 32 * blk + 8 * (r >> 2) + 4 * half + (r & 3);  // streamed row of this register
           float x = Sb[r] * p.alpha;
-          if (rabg) x += bias_s[buf][MODE == ANY_DKV ? rl - (c - c0) + (ANY_BM - 1) : (c - c0) - rl + (ANY_BN - 1)];
+          if (rabg) x += bias_s[buf][KEYS ? rl - (c - c0) + (ANY_BM - 1) : (c - c0) - rl + (ANY_BN - 1)];
           const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * neg_log2e));
           float pe = x * sig;
           float de = 0.f;
-          if constexpr (BWD) de = dPb[r] * (sig + pe * (1.0f - sig));  // silu'(x) = sig (1 + x (1 - sig))
-          if (MODE == ANY_DKV && per_token) {
+          if constexpr (HAS_DP) de = dPb[r] * (sig + pe * (1.0f - sig));  // silu'(x) = sig (1 + x (1 - sig))
+          if (KEYS && per_token) {
             const float rs = scale_s[buf][rl];
             pe *= rs;
             de *= rs;
           }
           if (MASKED) {
             const int rr = rbase + (32 * blk + 8 * (r >> 2) + (r & 3));
-            const int m = MODE == ANY_DKV ? rr : c, j = MODE == ANY_DKV ? c : rr;
+            const int m = KEYS ? rr : c, j = KEYS ? c : rr;
             const int idm = min(m, si.cap);
             int kp = (int)(m == j) | (int)(j < si.ctx_eff);
             if (MASKED == 1) {
@@ -316,14 +318,14 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
             de = kp ? de : 0.f;
           }
           pv[r] = pe;
-          if constexpr (BWD) dsv[r] = de;
+          if constexpr (HAS_DP) dsv[r] = de;
           // the masked bodies four pairs at a time: left to itself the scheduler interleaves all 32 and spills
           if (MASKED && (r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           pw[blk][i] = any_pack2<F16>(pv[2 * i], pv[2 * i + 1]);
-          if constexpr (BWD) dsw[blk][i] = any_pack2<F16>(dsv[2 * i], dsv[2 * i + 1]);
+          if constexpr (HAS_DP) dsw[blk][i] = any_pack2<F16>(dsv[2 * i], dsv[2 * i + 1]);
         }
       }
       // accumulating products: step s2 covers streamed rows 16 s2 .. + 15 = registers 8 (s2 & 1) .. + 7 of block s2 >> 1
@@ -332,11 +334,11 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
         const int blk = s2 >> 1, w0 = 4 * (s2 & 1);
         const u32x4 pb = {pw[blk][w0], pw[blk][w0 + 1], pw[blk][w0 + 2], pw[blk][w0 + 3]};
         u32x4 db_ = zero4;
-        if constexpr (BWD) db_ = (u32x4){dsw[blk][w0], dsw[blk][w0 + 1], dsw[blk][w0 + 2], dsw[blk][w0 + 3]};
+        if constexpr (HAS_DP) db_ = (u32x4){dsw[blk][w0], dsw[blk][w0 + 1], dsw[blk][w0 + 2], dsw[blk][w0 + 3]};
 #pragma unroll
         for (int db = 0; db < NB; ++db) {
-          if constexpr (MODE != ANY_DQ) acc2[db] = any_mfma<F16>(tr_frag(y2, db, s2), pb, acc2[db]);
-          if constexpr (BWD) acc1[db] = any_mfma<F16>(tr_frag(y1, db, s2), db_, acc1[db]);
+          if constexpr (HAS_P) acc2[db] = any_mfma<F16>(tr_frag(y2, db, s2), pb, acc2[db]);
+          if constexpr (HAS_DP) acc1[db] = any_mfma<F16>(tr_frag(y1, db, s2), db_, acc1[db]);
         }
       }
     };
@@ -347,8 +349,8 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
       const int r0 = t * ANY_BN, r1 = r0 + ANY_BN;
       bool full = false;
       // (m_lo, m_hi) and (j_lo, j_hi): query rows and keys of the block, inclusive
-      const int m_lo = MODE == ANY_DKV ? r0 : c_lo, m_hi = MODE == ANY_DKV ? min(r1, si.n) - 1 : c_hi;
-      const int j_lo = MODE == ANY_DKV ? c_lo : r0, j_hi = MODE == ANY_DKV ? c_hi : min(r1, si.n) - 1;
+      const int m_lo = KEYS ? r0 : c_lo, m_hi = KEYS ? min(r1, si.n) - 1 : c_hi;
+      const int j_lo = KEYS ? c_lo : r0, j_hi = KEYS ? c_hi : min(r1, si.n) - 1;
       const int id_lo = min(m_lo, si.cap), id_hi = min(m_hi, si.cap);
       const bool diagonal = m_lo <= j_hi && j_lo <= m_hi;
       if (!noncausal) {
@@ -397,7 +399,7 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
     if (c_valid) {
       float uni = 1.0f / (float)p.N;  // the scale where it is the same for every row
       if (p.attn_scale && !per_token) uni = p.attn_scale[0];
-      const float col_scale = MODE == ANY_DKV ? (per_token ? pow2_down : uni) : (per_token ? p.attn_scale[si.s + c] : uni);
+      const float col_scale = KEYS ? (per_token ? pow2_down : uni) : (per_token ? p.attn_scale[si.s + c] : uni);
       auto store_rows = [&](void* base, int D, const f32x16* acc, float f) __attribute__((always_inline)) {
         unsigned short* orow = (unsigned short*)base + ((size_t)(si.s + c) * p.H + h) * D;
 #pragma unroll
@@ -416,18 +418,15 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
       };
       if constexpr (MODE == ANY_FWD) store_rows(p.out, p.Dv, acc2, col_scale);
       if constexpr (MODE == ANY_DQ) store_rows(bp.dq, p.Dqk, acc1, col_scale * p.alpha);
-      if constexpr (MODE == ANY_DKV) {
-        store_rows(bp.dk, p.Dqk, acc1, col_scale * p.alpha);
-        store_rows(bp.dv, p.Dv, acc2, col_scale);
-      }
+      if constexpr (KEYS && HAS_DP) store_rows(bp.dk, p.Dqk, acc1, col_scale * p.alpha);
+      if constexpr (KEYS && HAS_P) store_rows(bp.dv, p.Dv, acc2, col_scale);
     }
     __syncthreads();  // the LDS tiles are reused by the next item
   }
 }
 
 // Launchers (defined in hstu_mfma_any.hip).  dtype: RECIR_HSTU_DTYPE_BF16 or RECIR_HSTU_DTYPE_FP16;
-// dp: padded head dim (32, 64, 128 or 256; the backward takes up to 128).  Return false when the
-// combination has no instantiation.
+// dp: padded head dim (32, 64, 128 or 256).  Return false when the combination has no instantiation.
 bool launch_mfma_any_fwd(int dtype, int dp, dim3 grid, hipStream_t stream, const Params& p);
 bool launch_mfma_any_bwd(int dtype, int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk);
 

@@ -11,18 +11,31 @@ namespace {
 
 template <int MODE, bool F16>
 bool launch_mode(int dp, dim3 grid, hipStream_t stream, const BwdParams& bp) {
+  // the key-stationary mode that produces dK and dV together stops at 128; its halves take 256
+  constexpr bool small = MODE != ANY_DV && MODE != ANY_DK;
+  constexpr bool large = MODE != ANY_DKV;
   switch (dp) {
-    case 32: hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 32>), grid, dim3(256), 0, stream, bp); return true;
-    case 64: hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 64>), grid, dim3(256), 0, stream, bp); return true;
-    case 128: hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 128>), grid, dim3(256), 0, stream, bp); return true;
+    case 32:
+      if constexpr (small) { hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 32>), grid, dim3(256), 0, stream, bp); return true; }
+      return false;
+    case 64:
+      if constexpr (small) { hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 64>), grid, dim3(256), 0, stream, bp); return true; }
+      return false;
+    case 128:
+      if constexpr (small) { hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 128>), grid, dim3(256), 0, stream, bp); return true; }
+      return false;
     case 256:
-      if constexpr (MODE == ANY_FWD) {
-        hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 256>), grid, dim3(256), 0, stream, bp);
-        return true;
-      }
+      if constexpr (large) { hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 256>), grid, dim3(256), 0, stream, bp); return true; }
       return false;
     default: return false;
   }
+}
+
+template <bool F16>
+bool launch_bwd(int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk) {
+  if (dp <= 128) return launch_mode<ANY_DKV, F16>(dp, grid_k, stream, bk) && launch_mode<ANY_DQ, F16>(dp, grid_q, stream, bq);
+  return launch_mode<ANY_DV, F16>(dp, grid_k, stream, bk) && launch_mode<ANY_DK, F16>(dp, grid_k, stream, bk) &&
+         launch_mode<ANY_DQ, F16>(dp, grid_q, stream, bq);
 }
 
 }  // namespace
@@ -37,11 +50,8 @@ bool launch_mfma_any_fwd(int dtype, int dp, dim3 grid, hipStream_t stream, const
 }
 
 bool launch_mfma_any_bwd(int dtype, int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk) {
-  if (dp > 128) return false;
-  if (dtype == RECIR_HSTU_DTYPE_FP16)
-    return launch_mode<ANY_DKV, true>(dp, grid_k, stream, bk) && launch_mode<ANY_DQ, true>(dp, grid_q, stream, bq);
-  if (dtype == RECIR_HSTU_DTYPE_BF16)
-    return launch_mode<ANY_DKV, false>(dp, grid_k, stream, bk) && launch_mode<ANY_DQ, false>(dp, grid_q, stream, bq);
+  if (dtype == RECIR_HSTU_DTYPE_FP16) return launch_bwd<true>(dp, grid_q, grid_k, stream, bq, bk);
+  if (dtype == RECIR_HSTU_DTYPE_BF16) return launch_bwd<false>(dp, grid_q, grid_k, stream, bq, bk);
   return false;
 }
 

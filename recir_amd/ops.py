@@ -41,8 +41,7 @@ class _CallState(threading.local):
 _state = _CallState()
 
 # What happens when a bf16 call can only run on the generic kernels (one wave per token and head, two orders
-# of magnitude slower than the MFMA kernels: head dims that are not multiples of 8 or exceed 256 (backward:
-# 128), unaligned tensors, the gradient of the bias table outside bf16 at head dim 128 with the causal or
+# of magnitude slower than the MFMA kernels: head dims that are not multiples of 8 or exceed 256, unaligned tensors, the gradient of the bias table outside bf16 at head dim 128 with the causal or
 # semi-local mask): "warn" (once per process and reason), "error" (the C ABI rejects the call,
 # RECIR_HSTU_FLAG_TILED_ONLY) or "silent".  fp32 tensors are the smoke path and never warn.
 _generic_policy = "warn"
@@ -65,7 +64,7 @@ def _note_generic(kernel: str, q, v, rab_grad=False) -> None:
     if _state.forced_kernel == KERNEL_GENERIC:
         return
     bwd = kernel.startswith("bwd_")
-    top = 128 if bwd else 256
+    top = 256
     if q.shape[2] % 8 or v.shape[2] % 8 or max(q.shape[2], v.shape[2]) > top:
         reason = f"head dims {q.shape[2]} / {v.shape[2]} (the MFMA kernels take multiples of 8 up to {top})"
     elif bwd and rab_grad:

@@ -18,7 +18,7 @@ def expected_kernel(dqk, dv, dtype="bf16", *, causal=True, bwd=False, rab=False,
     if (dtype == "bf16" or fp8) and dqk == dv == 128 and causal and not (rab and alpha == 0):
         return pre + "tiled_d128_" + ("fp8qk" if fp8 else "bf16") + ("_rab" if rab else "")
     d = max(dqk, dv)
-    if dtype in ("bf16", "fp16") and dqk % 8 == 0 and dv % 8 == 0 and d <= (128 if bwd else 256) and not (bwd and rab_grad):
+    if dtype in ("bf16", "fp16") and dqk % 8 == 0 and dv % 8 == 0 and d <= 256 and not (bwd and rab_grad):
         return f"{pre}mfma_{dtype}_d{32 if d <= 32 else 64 if d <= 64 else 128 if d <= 128 else 256}"
     return f"{pre}generic_{dtype}"
 

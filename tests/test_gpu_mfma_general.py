@@ -146,7 +146,7 @@ def _upstream(wl, dtype, seed):
     return (d.bfloat16() if dtype == "bf16" else d.half()).float()
 
 
-@pytest.mark.parametrize("dims", [(64, 64), (32, 32), (8, 16), (96, 96), (64, 128), (128, 64), (24, 40)],
+@pytest.mark.parametrize("dims", [(64, 64), (32, 32), (8, 16), (96, 96), (64, 128), (128, 64), (24, 40), (256, 256), (200, 72), (136, 128)],
                          ids=lambda d: f"{d[0]}x{d[1]}")
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 def test_backward_head_dims(oracle, dims, dtype):
