@@ -40,11 +40,12 @@ extern "C" {
  *   - the kernels written for head dim 128 ("tiled_d128_*", "bwd_tiled_d128_*"): bf16 (forward also
  *     fp8 q/k), Dqk = Dv = 128, 16-byte aligned tensors, the causal or semi-local mask, alpha != 0
  *     when there is a bias; the only ones that produce the gradient of the bias table on MFMAs;
- *   - the general MFMA kernels ("mfma_*", "bwd_mfma_*"): bf16 or fp16, Dqk and Dv any multiples of
- *     8 up to 256 and independent of each other, 16-byte aligned tensors, every mask, any alpha;
+ *   - the general MFMA kernels ("mfma_*", "bwd_mfma_*"): bf16 or fp16 with Dqk and Dv any multiples
+ *     of 8 up to 256, fp32 with multiples of 4 up to 128 (fp32 MFMAs, a sixteenth of the bf16 rate);
+ *     Dqk and Dv independent of each other, 16-byte aligned tensors, every mask, any alpha; in bf16
  *     about twice the time of the first group at its own shape;
  *   - the generic kernels ("generic_*", "bwd_generic_*"): one wave per (token, head), bf16 or fp32,
- *     any head dim up to 512; two orders of magnitude slower.  fp32 tensors always run here.
+ *     any head dim up to 512; one to two orders of magnitude slower.
  */
 
 /* flags */
@@ -77,8 +78,8 @@ extern "C" {
 #define RECIR_HSTU_FLAG_TILED_ONLY 0x40000u       /* reject (RECIR_HSTU_ERR_UNSUPPORTED, with the reason
                                                      in recir_hstu_last_error) a call that only the
                                                      generic kernels cover instead of running it
-                                                     there: fp32 tensors, head dims that are not
-                                                     multiples of 8 or exceed 256,
+                                                     there: head dims whose rows are not multiples
+                                                     of 16 bytes or that exceed 256 (fp32: 128),
                                                      tensors not 16-byte aligned, the gradient of the
                                                      bias table outside the head-dim-128 kernels'
                                                      domain.  Forward and backward.                  */

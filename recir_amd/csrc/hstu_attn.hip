@@ -360,20 +360,27 @@ void launch_bwd_tiled(bool semi, bool has_rab, dim3 grid, dim3 grid_k, hipStream
   }
 }
 
-// Padded head dim of the general MFMA kernels for a call, 0 when they do not take it: both dims
-// multiples of 8 (16-byte rows), the larger one at most max_dim.
-int mfma_any_padded_dim(int Dqk, int Dv, int max_dim) {
-  if (Dqk % 8 || Dv % 8) return 0;
+// Padded head dim of the general MFMA kernels for a call, 0 when they do not take it: rows of both
+// tensors multiples of 16 bytes, the larger head dim at most 256 (fp32: 128, its tiles are twice as wide).
+int mfma_any_padded_dim(int Dqk, int Dv, int dtype) {
+  const bool f32 = dtype == RECIR_HSTU_DTYPE_FP32;
+  if (dtype != RECIR_HSTU_DTYPE_BF16 && dtype != RECIR_HSTU_DTYPE_FP16 && !f32) return 0;
+  const int per_chunk = f32 ? 4 : 8;
+  if (Dqk % per_chunk || Dv % per_chunk) return 0;
   const int d = Dqk > Dv ? Dqk : Dv;
-  if (d > max_dim) return 0;
+  if (d > (f32 ? 128 : 256)) return 0;
   return d <= 32 ? 32 : (d <= 64 ? 64 : (d <= 128 ? 128 : 256));
 }
-const char* mfma_any_name(bool bwd, bool f16, int dp) {
-  static const char* const names[2][2][4] = {
-      {{"mfma_bf16_d32", "mfma_bf16_d64", "mfma_bf16_d128", "mfma_bf16_d256"}, {"mfma_fp16_d32", "mfma_fp16_d64", "mfma_fp16_d128", "mfma_fp16_d256"}},
+const char* mfma_any_name(bool bwd, int dtype, int dp) {
+  static const char* const names[2][3][4] = {
+      {{"mfma_bf16_d32", "mfma_bf16_d64", "mfma_bf16_d128", "mfma_bf16_d256"},
+       {"mfma_fp16_d32", "mfma_fp16_d64", "mfma_fp16_d128", "mfma_fp16_d256"},
+       {"mfma_fp32_d32", "mfma_fp32_d64", "mfma_fp32_d128", "mfma_fp32_d256"}},
       {{"bwd_mfma_bf16_d32", "bwd_mfma_bf16_d64", "bwd_mfma_bf16_d128", "bwd_mfma_bf16_d256"},
-       {"bwd_mfma_fp16_d32", "bwd_mfma_fp16_d64", "bwd_mfma_fp16_d128", "bwd_mfma_fp16_d256"}}};
-  return names[bwd ? 1 : 0][f16 ? 1 : 0][dp == 32 ? 0 : (dp == 64 ? 1 : (dp == 128 ? 2 : 3))];
+       {"bwd_mfma_fp16_d32", "bwd_mfma_fp16_d64", "bwd_mfma_fp16_d128", "bwd_mfma_fp16_d256"},
+       {"bwd_mfma_fp32_d32", "bwd_mfma_fp32_d64", "bwd_mfma_fp32_d128", "bwd_mfma_fp32_d256"}}};
+  const int t = dtype == RECIR_HSTU_DTYPE_FP16 ? 1 : (dtype == RECIR_HSTU_DTYPE_FP32 ? 2 : 0);
+  return names[bwd ? 1 : 0][t][dp == 32 ? 0 : (dp == 64 ? 1 : (dp == 128 ? 2 : 3))];
 }
 
 template <bool FP8>
@@ -458,8 +465,8 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
   const bool bias_needs_other = rab && !std::isnormal(1.0f / alpha);
   const bool d128_ok = (dtype == RECIR_HSTU_DTYPE_BF16 || fp8) && Dqk == HD && Dv == HD && aligned && !noncausal && !bias_needs_other;
   // the MFMA kernels for other head dims, fp16 and the remaining masks (hstu_mfma_any.h)
-  const int any_dp = mfma_any_padded_dim(Dqk, Dv, 256);
-  const bool any_ok = (dtype == RECIR_HSTU_DTYPE_BF16 || f16) && any_dp != 0 && aligned;
+  const int any_dp = mfma_any_padded_dim(Dqk, Dv, dtype);
+  const bool any_ok = any_dp != 0 && aligned;
   if (variant > 3) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "unknown kernel selector %u", variant);
   if (variant == 3 && !d128_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
@@ -467,7 +474,8 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
                 "semi-local mask and alpha != 0 with a bias");
   if (variant == 2 && !any_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "the general MFMA kernel needs bf16 or fp16, head dims that are multiples of 8 up to 256 and 16-byte aligned tensors");
+                "the general MFMA kernel needs bf16, fp16 or fp32, head dims whose rows are multiples of 16 bytes, up to 256 "
+                "(fp32: 128), and 16-byte aligned tensors");
   if (fp8 && !d128_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
                 "fp8 q/k is implemented for Dqk = Dv = 128, 16-byte aligned tensors, the causal or semi-local mask (and alpha != 0 with a bias)");
@@ -519,7 +527,7 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     const dim3 grid((unsigned)(slots * NUM_XCD));
     if (use_any) {
       if (!launch_mfma_any_fwd(dtype, any_dp, grid, stream, p)) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "no general MFMA kernel for dtype %d, padded head dim %d", dtype, any_dp);
-      g_last_kernel = mfma_any_name(false, f16, any_dp);
+      g_last_kernel = mfma_any_name(false, dtype, any_dp);
     } else if (fp8) {
       launch_dl<true>(rab != nullptr, semi, grid, stream, p);
       g_last_kernel = rab ? "tiled_d128_fp8qk_rab" : "tiled_d128_fp8qk";
@@ -533,8 +541,8 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
 
   if (flags & RECIR_HSTU_FLAG_TILED_ONLY)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "only the generic kernel covers this call (the MFMA kernels need bf16, fp16 or fp8 q/k, head dims that are "
-                "multiples of 8 up to 256 and 16-byte aligned tensors): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
+                "only the generic kernel covers this call (the MFMA kernels need head dims whose rows are multiples of 16 bytes, up to "
+                "256 (fp32: 128), and 16-byte aligned tensors): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
   if (Dqk > GENERIC_MAX_D || Dv > GENERIC_MAX_D)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "head dims above %d are not supported (Dqk=%d Dv=%d)", GENERIC_MAX_D, Dqk, Dv);
   if (H > 65535) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "more than 65535 heads");
@@ -697,8 +705,8 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   const bool bias_needs_other = rab && !std::isnormal(1.0f / alpha);
   const bool d128_ok = bf16 && Dqk == HD && Dv == HD && aligned && !noncausal && !bias_needs_other;
   // the general MFMA kernels (hstu_mfma_any.h): no gradient of the bias table
-  const int any_dp = mfma_any_padded_dim(Dqk, Dv, 256);
-  const bool any_ok = (bf16 || f16) && any_dp != 0 && aligned && !drab;
+  const int any_dp = mfma_any_padded_dim(Dqk, Dv, dtype);
+  const bool any_ok = any_dp != 0 && aligned && !drab;
   if (variant > 3) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "unknown kernel selector %u", variant);
   if (variant == 3 && !d128_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
@@ -706,8 +714,8 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
                 "and alpha != 0 with a bias");
   if (variant == 2 && !any_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "the general MFMA backward needs bf16 or fp16, head dims that are multiples of 8 up to 256, 16-byte aligned "
-                "tensors and no gradient of the bias table");
+                "the general MFMA backward needs bf16, fp16 or fp32, head dims whose rows are multiples of 16 bytes, up to 256 "
+                "(fp32: 128), 16-byte aligned tensors and no gradient of the bias table");
   if (f16 && (variant == 1 || !any_ok))
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
                 "the fp16 backward runs on the general MFMA kernels only: head dims that are multiples of 8 up to 256, 16-byte "
@@ -756,7 +764,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
       if (!launch_mfma_any_bwd(dtype, any_dp, grid, grid, stream, bq, bk))
         return fail(RECIR_HSTU_ERR_UNSUPPORTED, "no general MFMA backward for dtype %d, padded head dim %d", dtype, any_dp);
       if (int rc = launch_status("hstu_mfma_any (backward)")) return rc;
-      g_last_kernel = mfma_any_name(true, f16, any_dp);
+      g_last_kernel = mfma_any_name(true, dtype, any_dp);
       return RECIR_HSTU_OK;
     }
     const bool per_token = attn_scale && (flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
@@ -804,9 +812,9 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   }
   if (flags & RECIR_HSTU_FLAG_TILED_ONLY)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "only the generic kernels cover this call (the MFMA kernels need bf16 or fp16, head dims that are multiples of 8 "
-                "up to 256, 16-byte aligned tensors, and for the gradient of the bias table bf16, Dqk = Dv = 128, the causal or "
-                "semi-local mask and alpha != 0): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
+                "only the generic kernels cover this call (the MFMA kernels need head dims whose rows are multiples of 16 bytes, up to "
+                "256 (fp32: 128), 16-byte aligned tensors, and for the gradient of the bias table bf16, Dqk = Dv = 128, the causal "
+                "or semi-local mask and alpha != 0): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
   if (int rc = zero_drab()) return rc;
   const dim3 grid((unsigned)T, (unsigned)H);
   if (bf16) {

@@ -1,5 +1,5 @@
 // MFMA kernels of the HSTU attention forward and backward for everything the kernels written for
-// head dim 128 do not take: head dims that are multiples of 8 up to 256,
+// head dim 128 do not take: head dims whose rows are multiples of 16 bytes, up to 256 (fp32: 128),
 // Dqk and Dv independent, bf16 or fp16 values, every mask the operator knows (causal with targets
 // and contextual prefix, semi-local, the non-causal forms), a bias with any alpha.  One template,
 // three modes; nothing here is hand-scheduled: the point is to keep such calls on the matrix
@@ -23,8 +23,14 @@
 // (lane = c, registers = r) is the B-operand layout of the accumulating product, so P and dS go from
 // one MFMA to the next through registers only.
 //
-// Head dims are padded to DP in {32, 64, 128, 256} with zeros (chunks of 8 elements past Dqk or Dv
-// are not loaded); both dims share the larger padding.
+// Head dims are padded to DP in {32, 64, 128, 256} with zeros (16-byte chunks past Dqk or Dv are not
+// loaded); both dims share the larger padding.
+//
+// fp32 tensors (DP up to 128) take the same walk with v_mfma_f32_32x32x2_f32, one element per lane and
+// operand: lane half h contracts elements h DP / 2 .. of the head dim in the score products and its
+// own streamed rows in the accumulating ones, whose B operand is the score block's register as it
+// is and whose A operand is a plain 4-byte LDS read (consecutive lanes, consecutive columns); P and
+// dS are not rounded.  A sixteenth of the bf16 rate, and still some twenty times the generic kernel.
 //   x = alpha S + bias;  P = silu(x) keep;  dS = dP silu'(x) keep   (dO . V is dP)
 //   out = scale P V;  dQ = alpha scale dS K;  dK = alpha (scale dS)^T Q;  dV = (scale P)^T dO
 // The scale of a query row multiplies a column in FWD and DQ (applied to the accumulators at the
@@ -56,6 +62,8 @@ __device__ __forceinline__ f32x16 any_mfma(const u32x4& a, const u32x4& b, const
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+constexpr int ANY_BF16 = 0, ANY_F16 = 1, ANY_F32 = 2;  // element types (the template's ELT)
+
 template <bool F16>
 __device__ __forceinline__ unsigned any_pack2(float lo, float hi) {
   if constexpr (F16) {
@@ -69,18 +77,23 @@ __device__ __forceinline__ unsigned any_pack2(float lo, float hi) {
 
 // Two workgroups per CU where the registers allow it (a few spills included: one workgroup per CU
 // measured 20-35 % slower at these shapes).
-template <int MODE, bool F16, int DP>
-__global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
+template <int MODE, int ELT, int DP>
+__global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 128) || DP <= 64)) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
   const Params& p = bp.f;
+  constexpr bool F16 = ELT == ANY_F16;
+  constexpr bool F32 = ELT == ANY_F32;  // v_mfma_f32_32x32x2_f32: one element per lane and operand, see below
+  constexpr int ES = F32 ? 4 : 2;       // bytes per element
   constexpr bool KEYS = MODE >= ANY_DKV;                                  // the stationary rows are keys
   constexpr bool HAS_DP = MODE == ANY_DQ || MODE == 2 || MODE == ANY_DK;   // dP, dS and the product that dS feeds
   constexpr bool HAS_P = MODE == ANY_FWD || MODE == 2 || MODE == ANY_DV;   // the product that P feeds
-  constexpr int NK = DP / 16;       // steps of 16 along the head dim in a score product
+  constexpr int NK = DP * ES / 32;  // 16-byte registers-quads of a stationary row per lane (bf16, fp16: steps of 16 along the head dim)
   constexpr int NB = DP / 32;       // 32-row blocks of a transposed accumulator
-  constexpr int RS = DP * 2 + 16;   // bytes between tile rows in LDS (the 16 spread the rows over the banks)
-  constexpr int CPR = DP / 8;       // 16-byte chunks per tile row
-  constexpr int NCH = DP / 32;      // chunks of one tile that one thread stages
+  constexpr int RS = DP * ES + 16;  // bytes between tile rows in LDS (the 16 spread the rows over the banks)
+  constexpr int CPR = DP * ES / 16; // 16-byte chunks per tile row
+  constexpr int NCH = DP * ES / 64; // chunks of one tile that one thread stages
+  constexpr int EPC = 16 / ES;      // elements per chunk
   static_assert(DP == 32 || DP == 64 || DP == 128 || DP == 256, "padded head dim");
+  static_assert(!F32 || DP <= 128, "fp32 tiles of 256 columns do not fit the LDS");
   __shared__ __attribute__((aligned(16))) unsigned char Y1s[2][ANY_BN * RS];
   __shared__ __attribute__((aligned(16))) unsigned char Y2s[2][ANY_BN * RS];
   __shared__ float bias_s[2][ANY_BM + ANY_BN];
@@ -101,10 +114,10 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
   const int tr_s = lane & 15;
   const unsigned tr_rd = (unsigned)(4 * half + (tr_s >> 2)) * RS + (unsigned)(32 * ((lane >> 4) & 1) + 8 * (tr_s & 3));
 
-  if (MODE == ANY_FWD) zero_tail_rows_of<256>(p, p.out, (size_t)p.H * p.Dv * 2);
-  if (MODE == ANY_DQ) zero_tail_rows_of<256>(p, bp.dq, (size_t)p.H * p.Dqk * 2);
-  if (KEYS && HAS_DP) zero_tail_rows_of<256>(p, bp.dk, (size_t)p.H * p.Dqk * 2);
-  if (KEYS && HAS_P) zero_tail_rows_of<256>(p, bp.dv, (size_t)p.H * p.Dv * 2);
+  if (MODE == ANY_FWD) zero_tail_rows_of<256>(p, p.out, (size_t)p.H * p.Dv * ES);
+  if (MODE == ANY_DQ) zero_tail_rows_of<256>(p, bp.dq, (size_t)p.H * p.Dqk * ES);
+  if (KEYS && HAS_DP) zero_tail_rows_of<256>(p, bp.dk, (size_t)p.H * p.Dqk * ES);
+  if (KEYS && HAS_P) zero_tail_rows_of<256>(p, bp.dv, (size_t)p.H * p.Dv * ES);
 
   const bool noncausal = (p.flags & RECIR_HSTU_FLAG_MASK_NONCAUSAL) != 0;
   const bool per_token = p.attn_scale && (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
@@ -130,8 +143,8 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
     const char* __restrict__ X2g = (const char*)(KEYS ? p.v : bp.dout);
     const char* __restrict__ Y1g = (const char*)(KEYS ? p.q : p.k);
     const char* __restrict__ Y2g = (const char*)(KEYS ? bp.dout : p.v);
-    const size_t rb1 = (size_t)p.H * p.Dqk * 2, rb2 = (size_t)p.H * p.Dv * 2;
-    const size_t hb1 = (size_t)h * p.Dqk * 2, hb2 = (size_t)h * p.Dv * 2;
+    const size_t rb1 = (size_t)p.H * p.Dqk * ES, rb2 = (size_t)p.H * p.Dv * ES;
+    const size_t hb1 = (size_t)h * p.Dqk * ES, hb2 = (size_t)h * p.Dv * ES;
     const float* __restrict__ rabg = p.rab ? p.rab + (size_t)h * rab_w : nullptr;
 
     // ---- stationary operands (B operand of the score products): lane holds row c ----
@@ -143,9 +156,11 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
     u32x4 x1[NK], x2[HAS_DP ? NK : 1];
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
-      const int d0 = kk * 16 + half * 8;
-      x1[kk] = (c_valid && d0 < p.Dqk) ? *(const u32x4*)(X1g + (size_t)(si.s + c) * rb1 + hb1 + (size_t)d0 * 2) : zero4;
-      if constexpr (HAS_DP) x2[kk] = (c_valid && d0 < p.Dv) ? *(const u32x4*)(X2g + (size_t)(si.s + c) * rb2 + hb2 + (size_t)d0 * 2) : zero4;
+      // bf16, fp16: elements 16 kk + 8 half .. + 7 (one MFMA step);  fp32: lane half h owns elements
+      // h DP / 2 .. + DP / 2 - 1, four per register quad (one MFMA step each)
+      const int d0 = F32 ? half * (DP / 2) + 4 * kk : kk * 16 + half * 8;
+      x1[kk] = (c_valid && d0 < p.Dqk) ? *(const u32x4*)(X1g + (size_t)(si.s + c) * rb1 + hb1 + (size_t)d0 * ES) : zero4;
+      if constexpr (HAS_DP) x2[kk] = (c_valid && d0 < p.Dv) ? *(const u32x4*)(X2g + (size_t)(si.s + c) * rb2 + hb2 + (size_t)d0 * ES) : zero4;
     }
 
     f32x16 acc1[HAS_DP ? NB : 1];  // DQ: dQ^T   DKV, DK: dK^T
@@ -224,8 +239,8 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
         const int idx = tid + 256 * i;
         const int row = idx / CPR, ch = idx % CPR;
         const int rr = min(r0 + row, si.n - 1);  // rows past the sequence re-read its last row; the mask drops them
-        st.y1[i] = ch * 8 < p.Dqk ? *(const u32x4*)(Y1g + (size_t)(si.s + rr) * rb1 + hb1 + (size_t)ch * 16) : zero4;
-        st.y2[i] = ch * 8 < p.Dv ? *(const u32x4*)(Y2g + (size_t)(si.s + rr) * rb2 + hb2 + (size_t)ch * 16) : zero4;
+        st.y1[i] = ch * EPC < p.Dqk ? *(const u32x4*)(Y1g + (size_t)(si.s + rr) * rb1 + hb1 + (size_t)ch * 16) : zero4;
+        st.y2[i] = ch * EPC < p.Dv ? *(const u32x4*)(Y2g + (size_t)(si.s + rr) * rb2 + hb2 + (size_t)ch * 16) : zero4;
       }
       st.bias = 0.f;
       if (rabg && tid < ANY_BM + ANY_BN - 1) {
@@ -261,8 +276,25 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
       return (u32x4){l2.x, l2.y, h2.x, h2.y};
     };
 
-    // One (64 streamed rows) x (32 stationary rows) block of this wave.  MASKED: the predicate is
-    // evaluated per pair; otherwise every pair of the block is known to be kept.
+    // scores of one 32-row block of a tile against the stationary rows: y rows as the A operand
+    auto row_product = [&](const unsigned char* y, int blk, const u32x4 (&x)[NK]) __attribute__((always_inline)) {
+      f32x16 acc;
+      if constexpr (F32) {
+        // lane (row l32, half h) reads elements h DP / 2 + 4 kk .. + 3 of its row: four MFMA steps of one element each
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) {
+          const u32x4 a = *(const u32x4*)(y + (blk * 32 + l32) * RS + (half * (DP / 2) + 4 * kk) * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[e]), __uint_as_float(x[kk][e]), (kk == 0 && e == 0) ? zero16 : acc, 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) acc = any_mfma<F16>(row_frag(y, blk, kk), x[kk], kk == 0 ? zero16 : acc);
+      }
+      return acc;
+    };
+
     // MASKED: 0 every pair kept, 1 the causal / semi-local predicate per pair, 2 the non-causal one.
     // The predicates are written with bitwise operators on 0 / 1 values: the short-circuit forms of
     // hstu_common.h compile to a divergent branch per pair here.
@@ -278,13 +310,8 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
       // one 32-row block of scores at a time (both at once cost the masked bodies their registers)
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
-        f32x16 Sb, dPb;
-#pragma unroll
-        for (int kk = 0; kk < NK; ++kk) Sb = any_mfma<F16>(row_frag(y1, blk, kk), x1[kk], kk == 0 ? zero16 : Sb);
-        if constexpr (HAS_DP) {
-#pragma unroll
-          for (int kk = 0; kk < NK; ++kk) dPb = any_mfma<F16>(row_frag(y2, blk, kk), x2[kk], kk == 0 ? zero16 : dPb);
-        }
+        f32x16 Sb = row_product(y1, blk, x1), dPb;
+        if constexpr (HAS_DP) dPb = row_product(y2, blk, x2);
         float pv[16], dsv[HAS_DP ? 16 : 1];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -322,12 +349,29 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
           // the masked bodies four pairs at a time: left to itself the scheduler interleaves all 32 and spills
           if (MASKED && (r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (F32) {
+          // accumulating products of this block, one streamed row per lane half and step: register r of
+          // the score block is the B operand as it is; the A operand is column 32 db + l32 of that row
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          pw[blk][i] = any_pack2<F16>(pv[2 * i], pv[2 * i + 1]);
-          if constexpr (HAS_DP) dsw[blk][i] = any_pack2<F16>(dsv[2 * i], dsv[2 * i + 1]);
+          for (int r = 0; r < 16; ++r) {
+            const int row = 32 * blk + 8 * (r >> 2) + 4 * half + (r & 3);
+#pragma unroll
+            for (int db = 0; db < NB; ++db) {
+              if constexpr (HAS_P)
+                acc2[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(*(const float*)(y2 + row * RS + (32 * db + l32) * 4), pv[r], acc2[db], 0, 0, 0);
+              if constexpr (HAS_DP)
+                acc1[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(*(const float*)(y1 + row * RS + (32 * db + l32) * 4), dsv[r], acc1[db], 0, 0, 0);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            pw[blk][i] = any_pack2<F16>(pv[2 * i], pv[2 * i + 1]);
+            if constexpr (HAS_DP) dsw[blk][i] = any_pack2<F16>(dsv[2 * i], dsv[2 * i + 1]);
+          }
         }
       }
+      if constexpr (F32) return;
       // accumulating products: step s2 covers streamed rows 16 s2 .. + 15 = registers 8 (s2 & 1) .. + 7 of block s2 >> 1
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
@@ -401,17 +445,23 @@ __global__ __launch_bounds__(256, ((MODE == ANY_FWD && DP <= 128) || DP <= 64) ?
       if (p.attn_scale && !per_token) uni = p.attn_scale[0];
       const float col_scale = KEYS ? (per_token ? pow2_down : uni) : (per_token ? p.attn_scale[si.s + c] : uni);
       auto store_rows = [&](void* base, int D, const f32x16* acc, float f) __attribute__((always_inline)) {
-        unsigned short* orow = (unsigned short*)base + ((size_t)(si.s + c) * p.H + h) * D;
+        char* orow = (char*)base + ((size_t)(si.s + c) * p.H + h) * D * ES;
 #pragma unroll
         for (int db = 0; db < NB; ++db) {
 #pragma unroll
           for (int rq = 0; rq < 4; ++rq) {
             const int d0 = db * 32 + 8 * rq + 4 * half;
             if (d0 < D) {
-              u32x2 o;
-              o.x = any_pack2<F16>(acc[db][4 * rq + 0] * f, acc[db][4 * rq + 1] * f);
-              o.y = any_pack2<F16>(acc[db][4 * rq + 2] * f, acc[db][4 * rq + 3] * f);
-              *(u32x2*)(orow + d0) = o;
+              if constexpr (F32) {
+                const u32x4 o = {__float_as_uint(acc[db][4 * rq + 0] * f), __float_as_uint(acc[db][4 * rq + 1] * f),
+                                 __float_as_uint(acc[db][4 * rq + 2] * f), __float_as_uint(acc[db][4 * rq + 3] * f)};
+                *(u32x4*)(orow + d0 * 4) = o;
+              } else {
+                u32x2 o;
+                o.x = any_pack2<F16>(acc[db][4 * rq + 0] * f, acc[db][4 * rq + 1] * f);
+                o.y = any_pack2<F16>(acc[db][4 * rq + 2] * f, acc[db][4 * rq + 3] * f);
+                *(u32x2*)(orow + d0 * 2) = o;
+              }
             }
           }
         }

@@ -9,33 +9,43 @@ namespace recir_hstu {
 
 namespace {
 
-template <int MODE, bool F16>
+// Which (mode, element type, padded head dim) are instantiated.  The key-stationary mode that produces
+// dK and dV together holds two operand sets and two accumulators: it stops at 128 (fp32: 64), and the
+// largest padded head dim (256, fp32: 128 -- its LDS tiles are twice as wide) takes its two halves.
+template <int MODE, int ELT, int DP>
+constexpr bool any_instantiated() {
+  constexpr int top = ELT == ANY_F32 ? 128 : 256;
+  if (MODE == ANY_DKV) return DP < top;
+  if (MODE == ANY_DV || MODE == ANY_DK) return DP == top;
+  return DP <= top;
+}
+
+template <int MODE, int ELT, int DP>
+bool launch_one(dim3 grid, hipStream_t stream, const BwdParams& bp) {
+  if constexpr (any_instantiated<MODE, ELT, DP>()) {
+    hipLaunchKernelGGL((hstu_mfma_any<MODE, ELT, DP>), grid, dim3(256), 0, stream, bp);
+    return true;
+  }
+  return false;
+}
+
+template <int MODE, int ELT>
 bool launch_mode(int dp, dim3 grid, hipStream_t stream, const BwdParams& bp) {
-  // the key-stationary mode that produces dK and dV together stops at 128; its halves take 256
-  constexpr bool small = MODE != ANY_DV && MODE != ANY_DK;
-  constexpr bool large = MODE != ANY_DKV;
   switch (dp) {
-    case 32:
-      if constexpr (small) { hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 32>), grid, dim3(256), 0, stream, bp); return true; }
-      return false;
-    case 64:
-      if constexpr (small) { hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 64>), grid, dim3(256), 0, stream, bp); return true; }
-      return false;
-    case 128:
-      if constexpr (small) { hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 128>), grid, dim3(256), 0, stream, bp); return true; }
-      return false;
-    case 256:
-      if constexpr (large) { hipLaunchKernelGGL((hstu_mfma_any<MODE, F16, 256>), grid, dim3(256), 0, stream, bp); return true; }
-      return false;
+    case 32: return launch_one<MODE, ELT, 32>(grid, stream, bp);
+    case 64: return launch_one<MODE, ELT, 64>(grid, stream, bp);
+    case 128: return launch_one<MODE, ELT, 128>(grid, stream, bp);
+    case 256: return launch_one<MODE, ELT, 256>(grid, stream, bp);
     default: return false;
   }
 }
 
-template <bool F16>
+template <int ELT>
 bool launch_bwd(int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk) {
-  if (dp <= 128) return launch_mode<ANY_DKV, F16>(dp, grid_k, stream, bk) && launch_mode<ANY_DQ, F16>(dp, grid_q, stream, bq);
-  return launch_mode<ANY_DV, F16>(dp, grid_k, stream, bk) && launch_mode<ANY_DK, F16>(dp, grid_k, stream, bk) &&
-         launch_mode<ANY_DQ, F16>(dp, grid_q, stream, bq);
+  if (dp < (ELT == ANY_F32 ? 128 : 256))
+    return launch_mode<ANY_DKV, ELT>(dp, grid_k, stream, bk) && launch_mode<ANY_DQ, ELT>(dp, grid_q, stream, bq);
+  return launch_mode<ANY_DV, ELT>(dp, grid_k, stream, bk) && launch_mode<ANY_DK, ELT>(dp, grid_k, stream, bk) &&
+         launch_mode<ANY_DQ, ELT>(dp, grid_q, stream, bq);
 }
 
 }  // namespace
@@ -44,14 +54,16 @@ bool launch_mfma_any_fwd(int dtype, int dp, dim3 grid, hipStream_t stream, const
   BwdParams bp;
   memset(&bp, 0, sizeof(bp));
   bp.f = p;
-  if (dtype == RECIR_HSTU_DTYPE_FP16) return launch_mode<ANY_FWD, true>(dp, grid, stream, bp);
-  if (dtype == RECIR_HSTU_DTYPE_BF16) return launch_mode<ANY_FWD, false>(dp, grid, stream, bp);
+  if (dtype == RECIR_HSTU_DTYPE_FP16) return launch_mode<ANY_FWD, ANY_F16>(dp, grid, stream, bp);
+  if (dtype == RECIR_HSTU_DTYPE_BF16) return launch_mode<ANY_FWD, ANY_BF16>(dp, grid, stream, bp);
+  if (dtype == RECIR_HSTU_DTYPE_FP32) return launch_mode<ANY_FWD, ANY_F32>(dp, grid, stream, bp);
   return false;
 }
 
 bool launch_mfma_any_bwd(int dtype, int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk) {
-  if (dtype == RECIR_HSTU_DTYPE_FP16) return launch_bwd<true>(dp, grid_q, grid_k, stream, bq, bk);
-  if (dtype == RECIR_HSTU_DTYPE_BF16) return launch_bwd<false>(dp, grid_q, grid_k, stream, bq, bk);
+  if (dtype == RECIR_HSTU_DTYPE_FP16) return launch_bwd<ANY_F16>(dp, grid_q, grid_k, stream, bq, bk);
+  if (dtype == RECIR_HSTU_DTYPE_BF16) return launch_bwd<ANY_BF16>(dp, grid_q, grid_k, stream, bq, bk);
+  if (dtype == RECIR_HSTU_DTYPE_FP32) return launch_bwd<ANY_F32>(dp, grid_q, grid_k, stream, bq, bk);
   return false;
 }
 

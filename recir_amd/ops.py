@@ -41,7 +41,8 @@ class _CallState(threading.local):
 _state = _CallState()
 
 # What happens when a bf16 call can only run on the generic kernels (one wave per token and head, two orders
-# of magnitude slower than the MFMA kernels: head dims that are not multiples of 8 or exceed 256, unaligned tensors, the gradient of the bias table outside bf16 at head dim 128 with the causal or
+# of magnitude slower than the MFMA kernels: head dims that are not multiples of 8 or exceed 256, unaligned tensors,
+# (fp32: multiples of 4 up to 128; fp32 calls never warn) the gradient of the bias table outside bf16 at head dim 128 with the causal or
 # semi-local mask): "warn" (once per process and reason), "error" (the C ABI rejects the call,
 # RECIR_HSTU_FLAG_TILED_ONLY) or "silent".  fp32 tensors are the smoke path and never warn.
 _generic_policy = "warn"

@@ -105,6 +105,30 @@ def test_forward_masks(oracle, mask, dtype, dims):
     assert not out[int(wl.seq_offsets[-1]):].float().cpu().numpy().any()
 
 
+@pytest.mark.parametrize("mask", ["causal_ctx", "semilocal", "noncausal_window"])
+@pytest.mark.parametrize("dims", [(32, 32), (64, 64), (128, 128), (20, 12), (128, 64), (36, 100)], ids=lambda d: f"{d[0]}x{d[1]}")
+def test_fp32_forward_and_backward(oracle, dims, mask):
+    """fp32 tensors on v_mfma_f32_32x32x2_f32 (head dims that are multiples of 4 up to 128): the fp32 tolerances of
+    the generic kernel's tests, forward element-wise and backward on the three relative bounds."""
+    from recir_amd import _lib
+    from tests.test_gpu_bwd import BWD_FP32_TOL, assert_grads_close
+
+    dqk, dv = dims
+    wl = _workload(dqk, dv, "fp32", mask, seed=3 * dqk + dv, with_rab=(mask == "causal_ctx"))
+    g = torch.Generator().manual_seed(8)
+    scale = (0.5 + torch.rand(wl.T, generator=g)) / 50 if mask == "semilocal" else None
+    out = run_hip(wl, attn_scale=scale)
+    assert _lib.last_kernel() == _expected_kernel("fp32", dqk, dv), _lib.last_kernel()
+    assert out.dtype == torch.float32
+    ref = run_oracle(oracle, wl, attn_scale=scale)
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=2e-4, atol=2e-6)
+    dout = torch.randn(wl.T, wl.H, dv, generator=g)
+    got = run_hip_bwd(wl, dout, attn_scale=scale, rab=wl.rab)
+    assert _lib.last_kernel() == _expected_kernel("fp32", dqk, dv, bwd=True), _lib.last_kernel()
+    want = _backward_reference(oracle, wl, dout, scale)
+    assert_grads_close(got, want[:3], int(wl.seq_offsets[-1]), BWD_FP32_TOL, f"fp32 {dims} {mask}")
+
+
 def test_noncausal_mask_runs_on_the_matrix_cores_by_default(oracle):
     """Neither a forced selector nor the generic kernel: bf16 at head dim 128 under a non-causal mask."""
     from recir_amd import _lib

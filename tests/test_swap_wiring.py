@@ -14,7 +14,7 @@ import pytest
 import torch
 import torch.fx as fx
 
-from tests.parity_util import FP32_ATOL, FP32_RTOL, assert_bf16_close
+from tests.parity_util import FP32_ATOL, FP32_RTOL, assert_bf16_close, expected_kernel
 
 
 class Registry:
@@ -137,7 +137,7 @@ def test_swapped_graph_on_the_gpu_matches_the_original_graph_on_the_cpu(case):
     torch.cuda.synchronize()
     assert got.shape == want.shape  # no padding rows here: T == seq_offsets[-1]
     if dt == torch.float32:
-        assert _lib.last_kernel() == "generic_fp32"
+        assert _lib.last_kernel() == expected_kernel(q.shape[2], v.shape[2], "fp32")
         np.testing.assert_allclose(got.cpu().numpy(), want.numpy(), rtol=FP32_RTOL, atol=FP32_ATOL)
     else:
         assert _lib.last_kernel().startswith("tiled_d128")
