@@ -39,7 +39,7 @@ extern "C" {
  * Which kernels run a call (recir_hstu_last_kernel names the one that did):
  *   - the kernels written for head dim 128 ("tiled_d128_*", "bwd_tiled_d128_*"): bf16 (forward also
  *     fp8 q/k), Dqk = Dv = 128, 16-byte aligned tensors, the causal or semi-local mask, alpha != 0
- *     when there is a bias; the only ones that produce the gradient of the bias table on MFMAs;
+ *     when there is a bias; the gradient of the bias table is reproducible bit for bit here only;
  *   - the general MFMA kernels ("mfma_*", "bwd_mfma_*"): bf16 or fp16 with Dqk and Dv any multiples
  *     of 8 up to 256, fp32 with multiples of 4 up to 128 (fp32 MFMAs, a sixteenth of the bf16 rate);
  *     Dqk and Dv independent of each other, 16-byte aligned tensors, every mask, any alpha; in bf16
@@ -80,9 +80,8 @@ extern "C" {
                                                      generic kernels cover instead of running it
                                                      there: head dims whose rows are not multiples
                                                      of 16 bytes or that exceed 256 (fp32: 128),
-                                                     tensors not 16-byte aligned, the gradient of the
-                                                     bias table outside the head-dim-128 kernels'
-                                                     domain.  Forward and backward.                  */
+                                                     tensors not 16-byte aligned.  Forward and
+                                                     backward.                                       */
 #define RECIR_HSTU_FLAG_KERNEL_SHIFT 8            /* bits 8..15: kernel selector for tests/tuning  */
 #define RECIR_HSTU_FLAG_KERNEL_MASK 0xff00u       /* 0 auto, 1 generic, 2 general MFMA, 3 head dim 128 */
 
@@ -167,18 +166,19 @@ size_t recir_hstu_attn_fwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int3
  *   dP = dO V^T,  dV = P^T dO,  dS = dP keep scale silu'(S),  dQ = alpha dS K,  dK = alpha dS^T Q
  *
  * dout          device, [T, H, Dv], the gradient of the forward's out; rows >= seq_offsets[B] ignored
- * q, k, v       the forward's inputs (bf16 or fp32; FP8_E4M3 is not supported)
+ * q, k, v       the forward's inputs (bf16, fp16 or fp32; FP8_E4M3 is not supported)
  * dq, dk        device, [T, H, Dqk]; dv device, [T, H, Dv]; same element type as q; written in full
  *               (rows >= seq_offsets[B] zeroed, recir/ops/helion/jagged_hstu_attention.py:916-920)
  * rab           enters S as in the forward
  * drab          device float [H, 2*max_seq_len-1] or NULL: gradient of rab (needs rab),
  *               drab[h, i] = sum of dS(m, j) over the kept pairs of all sequences with
- *               m - j + max_seq_len - 1 == i.  Written in full.  The MFMA kernels sum in fixed
- *               point (one power-of-two scale per head, from the head's largest |dout| and the
- *               call's largest |v|; integer additions, so the result is the same bit for bit
- *               whatever the order of the workgroups, like dq, dk and dv); the generic kernels add
- *               floats atomically and may differ in the last bits from run to run.  No counterpart in
- *               the reference (which has no rab).  No gradient is produced for attn_scale.
+ *               m - j + max_seq_len - 1 == i.  Written in full.  The kernels written for head dim
+ *               128 sum in fixed point (one power-of-two scale per head, from the head's largest
+ *               |dout| and the call's largest |v|; integer additions, so the result is the same bit
+ *               for bit whatever the order of the workgroups, like dq, dk and dv); the general MFMA
+ *               kernels and the generic kernels add floats atomically and may differ in the last
+ *               bits from run to run.  No counterpart in the reference (which has no rab).  No
+ *               gradient is produced for attn_scale.
  * attn_scale, flags, sizes, workspace, hip_stream: as for the forward; workspace of at least
  *               recir_hstu_attn_bwd_workspace_bytes(...) bytes, plus, with drab,
  *               recir_hstu_attn_bwd_rab_grad_workspace_bytes(H, max_seq_len)

@@ -704,9 +704,9 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   // with alpha = 0 (scores that are the bias alone) is not theirs, as in the forward
   const bool bias_needs_other = rab && !std::isnormal(1.0f / alpha);
   const bool d128_ok = bf16 && Dqk == HD && Dv == HD && aligned && !noncausal && !bias_needs_other;
-  // the general MFMA kernels (hstu_mfma_any.h): no gradient of the bias table
+  // the general MFMA kernels (hstu_mfma_any.h)
   const int any_dp = mfma_any_padded_dim(Dqk, Dv, dtype);
-  const bool any_ok = any_dp != 0 && aligned && !drab;
+  const bool any_ok = any_dp != 0 && aligned;
   if (variant > 3) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "unknown kernel selector %u", variant);
   if (variant == 3 && !d128_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
@@ -715,11 +715,11 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   if (variant == 2 && !any_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
                 "the general MFMA backward needs bf16, fp16 or fp32, head dims whose rows are multiples of 16 bytes, up to 256 "
-                "(fp32: 128), 16-byte aligned tensors and no gradient of the bias table");
+                "(fp32: 128), and 16-byte aligned tensors");
   if (f16 && (variant == 1 || !any_ok))
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
                 "the fp16 backward runs on the general MFMA kernels only: head dims that are multiples of 8 up to 256, 16-byte "
-                "aligned tensors, no gradient of the bias table (Dqk=%d Dv=%d)", Dqk, Dv);
+                "aligned tensors (Dqk=%d Dv=%d)", Dqk, Dv);
   const bool use_tiled = d128_ok && (variant == 0 || variant == 3);
   const bool use_any = !use_tiled && any_ok && variant != 1;
   if (use_tiled || use_any) {
@@ -760,6 +760,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
       }
     }
     if (use_any) {
+      if (int rc = zero_drab()) return rc;  // the dQ pass adds floats to it
       const dim3 grid((unsigned)(slots * NUM_XCD));
       if (!launch_mfma_any_bwd(dtype, any_dp, grid, grid, stream, bq, bk))
         return fail(RECIR_HSTU_ERR_UNSUPPORTED, "no general MFMA backward for dtype %d, padded head dim %d", dtype, any_dp);
@@ -813,8 +814,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   if (flags & RECIR_HSTU_FLAG_TILED_ONLY)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
                 "only the generic kernels cover this call (the MFMA kernels need head dims whose rows are multiples of 16 bytes, up to "
-                "256 (fp32: 128), 16-byte aligned tensors, and for the gradient of the bias table bf16, Dqk = Dv = 128, the causal "
-                "or semi-local mask and alpha != 0): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
+                "256 (fp32: 128), and 16-byte aligned tensors): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
   if (int rc = zero_drab()) return rc;
   const dim3 grid((unsigned)T, (unsigned)H);
   if (bf16) {

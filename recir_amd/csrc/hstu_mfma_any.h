@@ -99,6 +99,9 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
   __shared__ float bias_s[2][ANY_BM + ANY_BN];
   __shared__ float scale_s[2][ANY_BN];
   __shared__ float red_s[4];
+  // DQ with the gradient of the bias table: dS of a tile summed along its 191 diagonals, one band per
+  // LDS stage (float LDS atomics; the band of tile t goes out to the table while tile t + 1 is computed)
+  __shared__ float dband_s[2][MODE == ANY_DQ ? ANY_BM + ANY_BN : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -146,6 +149,7 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
     const size_t rb1 = (size_t)p.H * p.Dqk * ES, rb2 = (size_t)p.H * p.Dv * ES;
     const size_t hb1 = (size_t)h * p.Dqk * ES, hb2 = (size_t)h * p.Dv * ES;
     const float* __restrict__ rabg = p.rab ? p.rab + (size_t)h * rab_w : nullptr;
+    float* __restrict__ drabg = (MODE == ANY_DQ && bp.drab) ? bp.drab + (size_t)h * rab_w : nullptr;
 
     // ---- stationary operands (B operand of the score products): lane holds row c ----
     const int cw0 = c0 + wave * 32;
@@ -224,6 +228,12 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
         }
       }
     }
+    float uni = 1.0f / (float)p.N;  // the scale where it is the same for every row
+    if (p.attn_scale && !per_token) uni = p.attn_scale[0];
+    // scale of this lane's stationary row (queries), or what is left to apply to the key rows' sums
+    const float col_scale = KEYS ? (per_token ? pow2_down : uni) : ((per_token && c_valid) ? p.attn_scale[si.s + c] : uni);
+    const float dscale = c_valid ? col_scale : 0.f;  // DQ: the factor dS lacks where it goes into the bias table's gradient
+
     const bool has_skip = skip_a < skip_b;
     auto next_tile = [&](int t) { return (has_skip && t + 1 == skip_a) ? skip_b : t + 1; };
 
@@ -346,6 +356,10 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
           }
           pv[r] = pe;
           if constexpr (HAS_DP) dsv[r] = de;
+          if constexpr (MODE == ANY_DQ) {
+            // d score / d bias = 1: the pair's dS (with its row's scale) goes to its diagonal
+            if (drabg && de != 0.f) atomicAdd(&dband_s[buf][(c - c0) - rl + (ANY_BN - 1)], de * dscale);
+          }
           // the masked bodies four pairs at a time: left to itself the scheduler interleaves all 32 and spills
           if (MASKED && (r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
@@ -418,6 +432,22 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
       else tile_body(std::integral_constant<int, 2>{}, r0, buf);
     };
 
+    // band of tile `tile` (LDS stage b) -> the head's row of the table, and the stage cleared for the
+    // tile after the next; float additions in whatever order the workgroups arrive
+    auto flush_band = [&](int tile, int b) __attribute__((always_inline)) {
+      if constexpr (MODE == ANY_DQ) {
+        if (drabg && tid < ANY_BM + ANY_BN - 1) {
+          const float v = dband_s[b][tid];
+          dband_s[b][tid] = 0.f;
+          const int idx = c0 - tile * ANY_BN - (ANY_BN - 1) + tid + p.N - 1;  // entry e is the diagonal m - j = dmin + e
+          if (v != 0.f && idx >= 0 && idx < rab_w) unsafeAtomicAdd(&drabg[idx], v);
+        }
+      }
+    };
+    if constexpr (MODE == ANY_DQ) {
+      if (drabg && tid < ANY_BM + ANY_BN) dband_s[0][tid] = dband_s[1][tid] = 0.f;  // (published by the first tile's barrier)
+    }
+
     Staged st;
     int t = (has_skip && t_begin >= skip_a) ? max(t_begin, skip_b) : t_begin;
     int buf = 0;
@@ -432,18 +462,22 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
         if (nxt >= t_end) break;
         store_tiles(buf ^ 1, st);
         __syncthreads();
+        flush_band(t, buf);  // every wave is through tile t
         t = nxt;
         buf ^= 1;
         nxt = next_tile(t);
         if (nxt < t_end) load_tiles(nxt, st);
       }
+      if constexpr (MODE == ANY_DQ) {
+        if (drabg) {
+          __syncthreads();
+          flush_band(t, buf);
+        }
+      }
     }
 
     // ---- epilogue: transposed accumulators -> rows of the outputs ----
     if (c_valid) {
-      float uni = 1.0f / (float)p.N;  // the scale where it is the same for every row
-      if (p.attn_scale && !per_token) uni = p.attn_scale[0];
-      const float col_scale = KEYS ? (per_token ? pow2_down : uni) : (per_token ? p.attn_scale[si.s + c] : uni);
       auto store_rows = [&](void* base, int D, const f32x16* acc, float f) __attribute__((always_inline)) {
         char* orow = (char*)base + ((size_t)(si.s + c) * p.H + h) * D * ES;
 #pragma unroll

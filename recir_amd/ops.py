@@ -41,10 +41,9 @@ class _CallState(threading.local):
 _state = _CallState()
 
 # What happens when a bf16 call can only run on the generic kernels (one wave per token and head, two orders
-# of magnitude slower than the MFMA kernels: head dims that are not multiples of 8 or exceed 256, unaligned tensors,
-# (fp32: multiples of 4 up to 128; fp32 calls never warn) the gradient of the bias table outside bf16 at head dim 128 with the causal or
-# semi-local mask): "warn" (once per process and reason), "error" (the C ABI rejects the call,
-# RECIR_HSTU_FLAG_TILED_ONLY) or "silent".  fp32 tensors are the smoke path and never warn.
+# of magnitude slower than the MFMA kernels: head dims that are not multiples of 8 or exceed 256, unaligned
+# tensors): "warn" (once per process and reason), "error" (the C ABI rejects the call,
+# RECIR_HSTU_FLAG_TILED_ONLY) or "silent".  fp32 tensors (MFMA kernels at multiples of 4 up to 128) never warn.
 _generic_policy = "warn"
 _generic_warned = set()
 
@@ -68,8 +67,6 @@ def _note_generic(kernel: str, q, v, rab_grad=False) -> None:
     top = 256
     if q.shape[2] % 8 or v.shape[2] % 8 or max(q.shape[2], v.shape[2]) > top:
         reason = f"head dims {q.shape[2]} / {v.shape[2]} (the MFMA kernels take multiples of 8 up to {top})"
-    elif bwd and rab_grad:
-        reason = "the gradient of the bias table (on MFMAs only for bf16, head dims 128 / 128, the causal or semi-local mask, alpha != 0)"
     else:
         reason = "tensors that are not 16-byte aligned"
     if reason in _generic_warned:

@@ -19,7 +19,7 @@ def expected_kernel(dqk, dv, dtype="bf16", *, causal=True, bwd=False, rab=False,
         return pre + "tiled_d128_" + ("fp8qk" if fp8 else "bf16") + ("_rab" if rab else "")
     d = max(dqk, dv)
     per_chunk, top = (4, 128) if dtype == "fp32" else (8, 256)  # rows of 16-byte chunks; fp32 tiles are twice as wide
-    if dtype in ("bf16", "fp16", "fp32") and dqk % per_chunk == 0 and dv % per_chunk == 0 and d <= top and not (bwd and rab_grad):
+    if dtype in ("bf16", "fp16", "fp32") and dqk % per_chunk == 0 and dv % per_chunk == 0 and d <= top:
         return f"{pre}mfma_{dtype}_d{32 if d <= 32 else 64 if d <= 64 else 128 if d <= 128 else 256}"
     return f"{pre}generic_{dtype}"
 

@@ -204,6 +204,44 @@ def test_backward_masks(oracle, mask, dtype, dims, scale_kind):
                        f"bwd {mask} {dtype} {dims} {scale_kind}")
 
 
+@pytest.mark.parametrize("case", [("bf16", 64, 64, "causal_ctx"), ("fp16", 96, 40, "semilocal_ctx"), ("fp32", 32, 32, "causal_ctx"),
+                                  ("bf16", 128, 128, "noncausal_window"), ("bf16", 256, 256, "causal_ctx")],
+                         ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}-{c[3]}")
+@pytest.mark.parametrize("scale_kind", ["default", "per_token"])
+def test_gradient_of_the_bias_table(oracle, case, scale_kind):
+    """d rab from the dQ pass of the general kernels: dS summed along the diagonals of a tile in LDS (float
+    atomics), the band added to the table per tile.  Against the oracle; columns no pair touches stay zero."""
+    import recir_amd
+    from recir_amd import _lib
+
+    dtype, dqk, dv, mask = case
+    wl = _workload(dqk, dv, dtype, mask, seed=41, with_rab=True)
+    g = torch.Generator().manual_seed(9)
+    scale = (0.5 + torch.rand(wl.T, generator=g)) / 50 if scale_kind == "per_token" else None
+    dout = _upstream(wl, dtype, 14) if dtype != "fp32" else torch.randn(wl.T, wl.H, dv, generator=g)
+    q, k, v, off, nt = to_device(wl)
+    mask_type, A, F, ctx = MASKS[mask]
+    grads = recir_amd.jagged_hstu_attention_backward(dout.to(q.device, q.dtype), q, k, v, off, nt,
+                                                     None if scale is None else scale.cuda(), rab_grad=True,
+                                                     max_seq_len=wl.max_seq_len, alpha=wl.alpha, contextual_seq_len=ctx,
+                                                     rab=wl.rab.cuda(), max_attn_len=A, full_attn_size=F,
+                                                     invalid_attn_mask_type=mask_type)
+    torch.cuda.synchronize()
+    assert _lib.last_kernel() == _expected_kernel(dtype, dqk, dv, bwd=True), _lib.last_kernel()
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha, attn_scale=_scale_np(scale),
+                           rab=wl.rab.numpy(), contextual_seq_len=ctx, max_attn_len=A, full_attn_size=F, mask_type=mask_type,
+                           rab_grad=True)
+    tol = {"bf16": BF16_REL, "fp16": FP16_REL, "fp32": 2e-4}[dtype]
+    _assert_grads(grads[:3], want[:3], int(wl.seq_offsets[-1]), tol, f"rab grad {case} {scale_kind}")
+    drab = grads[3]
+    assert drab.shape == wl.rab.shape and drab.dtype == torch.float32
+    st = error_stats(drab, want[3])
+    report(f"d rab {case} {scale_kind}", st)
+    assert st["ref_max"] > 0 and st["rel_to_max"] <= tol and st["rel_fro"] <= tol, st
+    assert not drab.cpu().numpy()[np.asarray(want[3]) == 0].any()
+
+
 def test_fp16_backward_with_small_per_token_scales(oracle):
     """Per-token scales of the order of 1 / max_seq_len times P or dS fall below fp16's normal range (6e-5):
     the key-stationary kernel multiplies by a power of two taken from the largest scale of the rows it
@@ -242,7 +280,7 @@ def test_general_and_head_dim_128_kernels_agree_at_full_size(oracle):
 
 
 def test_what_still_runs_on_the_generic_kernels():
-    """Head dims that are not multiples of 8, and the gradient of the bias table away from head dim 128."""
+    """Head dims whose rows are not multiples of 16 bytes."""
     import recir_amd
     from recir_amd import _lib
     from recir_amd.workloads import make_jagged
@@ -252,10 +290,8 @@ def test_what_still_runs_on_the_generic_kernels():
         wl = make_jagged([50, 20], [5, 0], 2, 20, 12, max_seq_len=64, alpha=0.2, dtype="bf16", seed=1)
         run_hip(wl)
         assert _lib.last_kernel() == "generic_bf16"
-        wl = make_jagged([50, 20], [5, 0], 2, 64, 64, max_seq_len=64, alpha=0.2, dtype="bf16", seed=1, with_rab=True)
         q, k, v, off, nt = to_device(wl)
-        recir_amd.jagged_hstu_attention_backward(torch.ones_like(v), q, k, v, off, nt, max_seq_len=64, alpha=0.2,
-                                                 rab=wl.rab.cuda(), rab_grad=True)
+        recir_amd.jagged_hstu_attention_backward(torch.ones_like(v), q, k, v, off, nt, max_seq_len=64, alpha=0.2)
         assert _lib.last_kernel() == "bwd_generic_bf16"
         # fp16 has no generic kernel: a clear error instead
         wl = make_jagged([50, 20], [5, 0], 2, 20, 12, max_seq_len=64, alpha=0.2, dtype="fp16", seed=1)
