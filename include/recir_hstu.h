@@ -33,7 +33,7 @@ extern "C" {
 #define RECIR_HSTU_DTYPE_BF16 0
 #define RECIR_HSTU_DTYPE_FP32 1
 #define RECIR_HSTU_DTYPE_FP8_E4M3 2 /* q,k are OCP e4m3fn bytes with per-head scales; v,out bf16 */
-#define RECIR_HSTU_DTYPE_FP16 3     /* IEEE half; MFMA kernels only (head dims that are multiples of 8) */
+#define RECIR_HSTU_DTYPE_FP16 3     /* IEEE half */
 
 /*
  * Which kernels run a call (recir_hstu_last_kernel names the one that did):
@@ -44,8 +44,8 @@ extern "C" {
  *     of 8 up to 256, fp32 with multiples of 4 up to 128 (fp32 MFMAs, a sixteenth of the bf16 rate);
  *     Dqk and Dv independent of each other, 16-byte aligned tensors, every mask, any alpha; in bf16
  *     about twice the time of the first group at its own shape;
- *   - the generic kernels ("generic_*", "bwd_generic_*"): one wave per (token, head), bf16 or fp32,
- *     any head dim up to 512; one to two orders of magnitude slower.
+ *   - the generic kernels ("generic_*", "bwd_generic_*"): one wave per (token, head), bf16, fp16 or
+ *     fp32, any head dim up to 512; one to two orders of magnitude slower.
  */
 
 /* flags */

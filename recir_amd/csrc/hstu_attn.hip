@@ -210,13 +210,13 @@ __global__ void hstu_fill_zero(unsigned short* out, size_t n2) {
 // ---------------------------------------------------------------------------------------------
 constexpr int GENERIC_MAX_D = 512;
 
-template <bool BF16>
+template <int ELT>
 __global__ __launch_bounds__(64) void hstu_fwd_generic(Params p) {
   __shared__ float qrow[GENERIC_MAX_D];
   __shared__ float pbuf[64];
   const int lane = threadIdx.x;
   const int r = blockIdx.x, h = blockIdx.y;
-  const size_t esz = BF16 ? 2 : 4;
+  const size_t esz = ELT == ELT_FP32 ? 4 : 2;
   zero_tail_rows<64>(p, (size_t)p.H * p.Dv * esz);
   if (r >= end_of_sequences(p)) return;
 
@@ -237,13 +237,13 @@ __global__ __launch_bounds__(64) void hstu_fwd_generic(Params p) {
   }
   if (!ok) {  // only reachable with malformed offsets
     for (int d = lane; d < p.Dv; d += 64) {
-      if (BF16) ((unsigned short*)p.out)[orow + d] = 0; else ((float*)p.out)[orow + d] = 0.f;
+      store_elem<ELT>(p.out, orow + d, 0.f);
     }
     return;
   }
   const int m = r - si.s;
   for (int d = lane; d < p.Dqk; d += 64)
-    qrow[d] = load_elem<BF16>(p.q, ((size_t)r * p.H + h) * p.Dqk + d);
+    qrow[d] = load_elem<ELT>(p.q, ((size_t)r * p.H + h) * p.Dqk + d);
   __syncthreads();
 
   float scale = 1.0f / (float)p.N;
@@ -262,7 +262,7 @@ __global__ __launch_bounds__(64) void hstu_fwd_generic(Params p) {
     if (j < si.n && keep_pair(m, j, si, noncausal)) {
       const size_t krow = ((size_t)(si.s + j) * p.H + h) * p.Dqk;
       float dot = 0.f;
-      for (int d = 0; d < p.Dqk; ++d) dot = fmaf(qrow[d], load_elem<BF16>(p.k, krow + d), dot);
+      for (int d = 0; d < p.Dqk; ++d) dot = fmaf(qrow[d], load_elem<ELT>(p.k, krow + d), dot);
       float x = dot * p.alpha;
       if (p.rab) {
         int idx = m - j + p.N - 1;
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(64) void hstu_fwd_generic(Params p) {
         x += p.rab[(size_t)h * rab_w + idx];
       }
       pj = x / (1.0f + __expf(-x)) * scale;
-      if (BF16) pj = bf16_bits_to_float(float_to_bf16_bits(pj));
+      pj = round_to_elem<ELT>(pj);
     }
     __syncthreads();
     pbuf[lane] = pj;
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(64) void hstu_fwd_generic(Params p) {
 #pragma unroll
       for (int i = 0; i < GENERIC_MAX_D / 64; ++i) {
         const int d = lane + 64 * i;
-        if (d < p.Dv) acc[i] = fmaf(pv, load_elem<BF16>(p.v, vrow + d), acc[i]);
+        if (d < p.Dv) acc[i] = fmaf(pv, load_elem<ELT>(p.v, vrow + d), acc[i]);
       }
     }
   }
@@ -291,8 +291,7 @@ __global__ __launch_bounds__(64) void hstu_fwd_generic(Params p) {
   for (int i = 0; i < GENERIC_MAX_D / 64; ++i) {
     const int d = lane + 64 * i;
     if (d < p.Dv) {
-      if (BF16) ((unsigned short*)p.out)[orow + d] = float_to_bf16_bits(acc[i]);
-      else ((float*)p.out)[orow + d] = acc[i];
+      store_elem<ELT>(p.out, orow + d, acc[i]);
     }
   }
 }
@@ -480,10 +479,6 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
                 "fp8 q/k is implemented for Dqk = Dv = 128, 16-byte aligned tensors, the causal or semi-local mask (and alpha != 0 with a bias)");
   if (fp8 && (variant == 1 || variant == 2)) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "fp8 q/k runs on the head-dim-128 kernel only");
-  if (f16 && (variant == 1 || !any_ok))
-    return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "fp16 runs on the general MFMA kernel only: head dims that are multiples of 8 up to 256, 16-byte aligned tensors "
-                "(Dqk=%d Dv=%d)", Dqk, Dv);
   const bool use_tiled = d128_ok && (variant == 0 || variant == 3);
   const bool use_any = !use_tiled && any_ok && variant != 1;
 
@@ -547,10 +542,11 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "head dims above %d are not supported (Dqk=%d Dv=%d)", GENERIC_MAX_D, Dqk, Dv);
   if (H > 65535) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "more than 65535 heads");
   const dim3 grid((unsigned)T, (unsigned)H);
-  if (dtype == RECIR_HSTU_DTYPE_BF16) hipLaunchKernelGGL(hstu_fwd_generic<true>, grid, dim3(64), 0, stream, p);
-  else hipLaunchKernelGGL(hstu_fwd_generic<false>, grid, dim3(64), 0, stream, p);
+  if (dtype == RECIR_HSTU_DTYPE_BF16) hipLaunchKernelGGL(hstu_fwd_generic<ELT_BF16>, grid, dim3(64), 0, stream, p);
+  else if (f16) hipLaunchKernelGGL(hstu_fwd_generic<ELT_FP16>, grid, dim3(64), 0, stream, p);
+  else hipLaunchKernelGGL(hstu_fwd_generic<ELT_FP32>, grid, dim3(64), 0, stream, p);
   if (int rc = launch_status("hstu_fwd_generic")) return rc;
-  g_last_kernel = dtype == RECIR_HSTU_DTYPE_BF16 ? "generic_bf16" : "generic_fp32";
+  g_last_kernel = dtype == RECIR_HSTU_DTYPE_BF16 ? "generic_bf16" : (f16 ? "generic_fp16" : "generic_fp32");
   return RECIR_HSTU_OK;
 }
 
@@ -716,10 +712,6 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
                 "the general MFMA backward needs bf16, fp16 or fp32, head dims whose rows are multiples of 16 bytes, up to 256 "
                 "(fp32: 128), and 16-byte aligned tensors");
-  if (f16 && (variant == 1 || !any_ok))
-    return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "the fp16 backward runs on the general MFMA kernels only: head dims that are multiples of 8 up to 256, 16-byte "
-                "aligned tensors (Dqk=%d Dv=%d)", Dqk, Dv);
   const bool use_tiled = d128_ok && (variant == 0 || variant == 3);
   const bool use_any = !use_tiled && any_ok && variant != 1;
   if (use_tiled || use_any) {
@@ -818,16 +810,20 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   if (int rc = zero_drab()) return rc;
   const dim3 grid((unsigned)T, (unsigned)H);
   if (bf16) {
-    hipLaunchKernelGGL(hstu_bwd_generic_dq<true>, grid, dim3(64), 0, stream, bp);
+    hipLaunchKernelGGL(hstu_bwd_generic_dq<ELT_BF16>, grid, dim3(64), 0, stream, bp);
     if (int rc = launch_status("hstu_bwd_generic_dq")) return rc;
-    hipLaunchKernelGGL(hstu_bwd_generic_dkv<true>, grid, dim3(64), 0, stream, bp);
+    hipLaunchKernelGGL(hstu_bwd_generic_dkv<ELT_BF16>, grid, dim3(64), 0, stream, bp);
+  } else if (f16) {
+    hipLaunchKernelGGL(hstu_bwd_generic_dq<ELT_FP16>, grid, dim3(64), 0, stream, bp);
+    if (int rc = launch_status("hstu_bwd_generic_dq")) return rc;
+    hipLaunchKernelGGL(hstu_bwd_generic_dkv<ELT_FP16>, grid, dim3(64), 0, stream, bp);
   } else {
-    hipLaunchKernelGGL(hstu_bwd_generic_dq<false>, grid, dim3(64), 0, stream, bp);
+    hipLaunchKernelGGL(hstu_bwd_generic_dq<ELT_FP32>, grid, dim3(64), 0, stream, bp);
     if (int rc = launch_status("hstu_bwd_generic_dq")) return rc;
-    hipLaunchKernelGGL(hstu_bwd_generic_dkv<false>, grid, dim3(64), 0, stream, bp);
+    hipLaunchKernelGGL(hstu_bwd_generic_dkv<ELT_FP32>, grid, dim3(64), 0, stream, bp);
   }
   if (int rc = launch_status("hstu_bwd_generic_dkv")) return rc;
-  g_last_kernel = bf16 ? "bwd_generic_bf16" : "bwd_generic_fp32";
+  g_last_kernel = bf16 ? "bwd_generic_bf16" : (f16 ? "bwd_generic_fp16" : "bwd_generic_fp32");
   return RECIR_HSTU_OK;
 }
 

@@ -40,7 +40,7 @@ __device__ __forceinline__ float score_bias(const Params& p, int h, int m, int j
 }
 
 // dQ[r] = alpha * sum_j dS(m, j) K[j]
-template <bool BF16>
+template <int ELT>
 __global__ __launch_bounds__(64) void hstu_bwd_generic_dq(BwdParams bp) {
   const Params& p = bp.f;
   __shared__ float qrow[BWD_GENERIC_MAX_D];
@@ -48,19 +48,19 @@ __global__ __launch_bounds__(64) void hstu_bwd_generic_dq(BwdParams bp) {
   __shared__ float dsbuf[64];
   const int lane = threadIdx.x;
   const int r = blockIdx.x, h = blockIdx.y;
-  const size_t esz = BF16 ? 2 : 4;
+  const size_t esz = ELT == ELT_FP32 ? 4 : 2;
   zero_tail_rows_of<64>(p, bp.dq, (size_t)p.H * p.Dqk * esz);
   if (r >= end_of_sequences(p)) return;
   SeqInfo si = {0, 0, 0, 0};
   const size_t qoff = ((size_t)r * p.H + h) * p.Dqk;
   const size_t goff = ((size_t)r * p.H + h) * p.Dv;
   if (find_sequence(p, r, si) < 0) {  // only reachable with malformed offsets
-    for (int d = lane; d < p.Dqk; d += 64) store_elem<BF16>(bp.dq, qoff + d, 0.f);
+    for (int d = lane; d < p.Dqk; d += 64) store_elem<ELT>(bp.dq, qoff + d, 0.f);
     return;
   }
   const int m = r - si.s;
-  for (int d = lane; d < p.Dqk; d += 64) qrow[d] = load_elem<BF16>(p.q, qoff + d);
-  for (int d = lane; d < p.Dv; d += 64) grow[d] = load_elem<BF16>(bp.dout, goff + d);
+  for (int d = lane; d < p.Dqk; d += 64) qrow[d] = load_elem<ELT>(p.q, qoff + d);
+  for (int d = lane; d < p.Dv; d += 64) grow[d] = load_elem<ELT>(bp.dout, goff + d);
   __syncthreads();
   float scale = 1.0f / (float)p.N;
   if (p.attn_scale) scale = (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) ? p.attn_scale[r] : p.attn_scale[0];
@@ -77,8 +77,8 @@ __global__ __launch_bounds__(64) void hstu_bwd_generic_dq(BwdParams bp) {
       const size_t krow = ((size_t)(si.s + j) * p.H + h) * p.Dqk;
       const size_t vrow = ((size_t)(si.s + j) * p.H + h) * p.Dv;
       float dot = 0.f, dp = 0.f;
-      for (int d = 0; d < p.Dqk; ++d) dot = fmaf(qrow[d], load_elem<BF16>(p.k, krow + d), dot);
-      for (int d = 0; d < p.Dv; ++d) dp = fmaf(grow[d], load_elem<BF16>(p.v, vrow + d), dp);
+      for (int d = 0; d < p.Dqk; ++d) dot = fmaf(qrow[d], load_elem<ELT>(p.k, krow + d), dot);
+      for (int d = 0; d < p.Dv; ++d) dp = fmaf(grow[d], load_elem<ELT>(p.v, vrow + d), dp);
       const float x = dot * p.alpha + score_bias(p, h, m, j);
       const float sig = 1.0f / (1.0f + __expf(-x));
       ds = dp * scale * sig * (1.0f + x * (1.0f - sig));
@@ -98,19 +98,19 @@ __global__ __launch_bounds__(64) void hstu_bwd_generic_dq(BwdParams bp) {
 #pragma unroll
       for (int i = 0; i < BWD_GENERIC_MAX_D / 64; ++i) {
         const int d = lane + 64 * i;
-        if (d < p.Dqk) acc[i] = fmaf(w, load_elem<BF16>(p.k, krow + d), acc[i]);
+        if (d < p.Dqk) acc[i] = fmaf(w, load_elem<ELT>(p.k, krow + d), acc[i]);
       }
     }
   }
 #pragma unroll
   for (int i = 0; i < BWD_GENERIC_MAX_D / 64; ++i) {
     const int d = lane + 64 * i;
-    if (d < p.Dqk) store_elem<BF16>(bp.dq, qoff + d, acc[i] * p.alpha);
+    if (d < p.Dqk) store_elem<ELT>(bp.dq, qoff + d, acc[i] * p.alpha);
   }
 }
 
 // dK[r] = alpha * sum_m dS(m, j) Q[m],  dV[r] = sum_m P(m, j) dO[m]   for key row j = r - s
-template <bool BF16>
+template <int ELT>
 __global__ __launch_bounds__(64) void hstu_bwd_generic_dkv(BwdParams bp) {
   const Params& p = bp.f;
   __shared__ float krow_s[BWD_GENERIC_MAX_D];
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(64) void hstu_bwd_generic_dkv(BwdParams bp) {
   __shared__ float dsbuf[64];
   const int lane = threadIdx.x;
   const int r = blockIdx.x, h = blockIdx.y;
-  const size_t esz = BF16 ? 2 : 4;
+  const size_t esz = ELT == ELT_FP32 ? 4 : 2;
   zero_tail_rows_of<64>(p, bp.dk, (size_t)p.H * p.Dqk * esz);
   zero_tail_rows_of<64>(p, bp.dv, (size_t)p.H * p.Dv * esz);
   if (r >= end_of_sequences(p)) return;
@@ -127,13 +127,13 @@ __global__ __launch_bounds__(64) void hstu_bwd_generic_dkv(BwdParams bp) {
   const size_t koff = ((size_t)r * p.H + h) * p.Dqk;
   const size_t voff = ((size_t)r * p.H + h) * p.Dv;
   if (find_sequence(p, r, si) < 0) {
-    for (int d = lane; d < p.Dqk; d += 64) store_elem<BF16>(bp.dk, koff + d, 0.f);
-    for (int d = lane; d < p.Dv; d += 64) store_elem<BF16>(bp.dv, voff + d, 0.f);
+    for (int d = lane; d < p.Dqk; d += 64) store_elem<ELT>(bp.dk, koff + d, 0.f);
+    for (int d = lane; d < p.Dv; d += 64) store_elem<ELT>(bp.dv, voff + d, 0.f);
     return;
   }
   const int j = r - si.s;
-  for (int d = lane; d < p.Dqk; d += 64) krow_s[d] = load_elem<BF16>(p.k, koff + d);
-  for (int d = lane; d < p.Dv; d += 64) vrow_s[d] = load_elem<BF16>(p.v, voff + d);
+  for (int d = lane; d < p.Dqk; d += 64) krow_s[d] = load_elem<ELT>(p.k, koff + d);
+  for (int d = lane; d < p.Dv; d += 64) vrow_s[d] = load_elem<ELT>(p.v, voff + d);
   __syncthreads();
 
   float acck[BWD_GENERIC_MAX_D / 64], accv[BWD_GENERIC_MAX_D / 64];
@@ -152,8 +152,8 @@ __global__ __launch_bounds__(64) void hstu_bwd_generic_dkv(BwdParams bp) {
       const size_t qrow = ((size_t)(si.s + m) * p.H + h) * p.Dqk;
       const size_t grow = ((size_t)(si.s + m) * p.H + h) * p.Dv;
       float dot = 0.f, dp = 0.f;
-      for (int d = 0; d < p.Dqk; ++d) dot = fmaf(krow_s[d], load_elem<BF16>(p.q, qrow + d), dot);
-      for (int d = 0; d < p.Dv; ++d) dp = fmaf(vrow_s[d], load_elem<BF16>(bp.dout, grow + d), dp);
+      for (int d = 0; d < p.Dqk; ++d) dot = fmaf(krow_s[d], load_elem<ELT>(p.q, qrow + d), dot);
+      for (int d = 0; d < p.Dv; ++d) dp = fmaf(vrow_s[d], load_elem<ELT>(bp.dout, grow + d), dp);
       float scale = 1.0f / (float)p.N;
       if (p.attn_scale) scale = (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN) ? p.attn_scale[si.s + m] : p.attn_scale[0];
       const float x = dot * p.alpha + score_bias(p, h, m, j);
@@ -174,16 +174,16 @@ __global__ __launch_bounds__(64) void hstu_bwd_generic_dkv(BwdParams bp) {
 #pragma unroll
       for (int i = 0; i < BWD_GENERIC_MAX_D / 64; ++i) {
         const int d = lane + 64 * i;
-        if (d < p.Dqk) acck[i] = fmaf(u, load_elem<BF16>(p.q, qrow + d), acck[i]);
-        if (d < p.Dv) accv[i] = fmaf(w, load_elem<BF16>(bp.dout, grow + d), accv[i]);
+        if (d < p.Dqk) acck[i] = fmaf(u, load_elem<ELT>(p.q, qrow + d), acck[i]);
+        if (d < p.Dv) accv[i] = fmaf(w, load_elem<ELT>(bp.dout, grow + d), accv[i]);
       }
     }
   }
 #pragma unroll
   for (int i = 0; i < BWD_GENERIC_MAX_D / 64; ++i) {
     const int d = lane + 64 * i;
-    if (d < p.Dqk) store_elem<BF16>(bp.dk, koff + d, acck[i] * p.alpha);
-    if (d < p.Dv) store_elem<BF16>(bp.dv, voff + d, accv[i]);
+    if (d < p.Dqk) store_elem<ELT>(bp.dk, koff + d, acck[i] * p.alpha);
+    if (d < p.Dv) store_elem<ELT>(bp.dv, voff + d, accv[i]);
   }
 }
 

@@ -200,16 +200,29 @@ __device__ __forceinline__ void zero_tail_rows(const Params& p, size_t row_bytes
   zero_tail_rows_of<NTHREADS>(p, p.out, row_bytes);
 }
 
-template <bool BF16>
+// Element types of the generic kernels (the C ABI's dtype codes)
+constexpr int ELT_BF16 = RECIR_HSTU_DTYPE_BF16, ELT_FP32 = RECIR_HSTU_DTYPE_FP32, ELT_FP16 = RECIR_HSTU_DTYPE_FP16;
+
+template <int ELT>
 __device__ __forceinline__ float load_elem(const void* base, size_t idx) {
-  if (BF16) return bf16_bits_to_float(((const unsigned short*)base)[idx]);
+  if (ELT == ELT_BF16) return bf16_bits_to_float(((const unsigned short*)base)[idx]);
+  if (ELT == ELT_FP16) return (float)((const _Float16*)base)[idx];
   return ((const float*)base)[idx];
 }
 
-template <bool BF16>
+template <int ELT>
 __device__ __forceinline__ void store_elem(void* base, size_t idx, float x) {
-  if (BF16) ((unsigned short*)base)[idx] = float_to_bf16_bits(x);
+  if (ELT == ELT_BF16) ((unsigned short*)base)[idx] = float_to_bf16_bits(x);
+  else if (ELT == ELT_FP16) ((_Float16*)base)[idx] = (_Float16)x;
   else ((float*)base)[idx] = x;
+}
+
+// x as the element type holds it (P and dS are rounded like that before they meet v, dout, q or k)
+template <int ELT>
+__device__ __forceinline__ float round_to_elem(float x) {
+  if (ELT == ELT_BF16) return bf16_bits_to_float(float_to_bf16_bits(x));
+  if (ELT == ELT_FP16) return (float)(_Float16)x;
+  return x;
 }
 
 // Arguments of the backward kernels: the forward's inputs (f.out unused) plus the upstream

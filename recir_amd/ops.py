@@ -59,7 +59,7 @@ def set_generic_kernel_policy(policy: str) -> str:
 
 
 def _note_generic(kernel: str, q, v, rab_grad=False) -> None:
-    if _generic_policy != "warn" or not kernel.startswith(("generic_bf16", "bwd_generic_bf16")):
+    if _generic_policy != "warn" or not kernel.startswith(("generic_bf16", "bwd_generic_bf16", "generic_fp16", "bwd_generic_fp16")):
         return
     if _state.forced_kernel == KERNEL_GENERIC:
         return

@@ -293,9 +293,15 @@ def test_what_still_runs_on_the_generic_kernels():
         q, k, v, off, nt = to_device(wl)
         recir_amd.jagged_hstu_attention_backward(torch.ones_like(v), q, k, v, off, nt, max_seq_len=64, alpha=0.2)
         assert _lib.last_kernel() == "bwd_generic_bf16"
-        # fp16 has no generic kernel: a clear error instead
         wl = make_jagged([50, 20], [5, 0], 2, 20, 12, max_seq_len=64, alpha=0.2, dtype="fp16", seed=1)
-        with pytest.raises(ValueError, match="fp16 runs on the general MFMA kernel only"):
-            run_hip(wl)
+        out = run_hip(wl)
+        assert _lib.last_kernel() == "generic_fp16" and out.dtype == torch.float16
+        from oracle import hstu_oracle
+        hstu_oracle.build()
+        _assert_close(out, run_oracle(hstu_oracle, wl), FP16_REL, "generic fp16")
+        dout = _upstream(wl, "fp16", 3)
+        got = run_hip_bwd(wl, dout)
+        assert _lib.last_kernel() == "bwd_generic_fp16"
+        _assert_grads(got, _backward_reference(hstu_oracle, wl, dout, None)[:3], int(wl.seq_offsets[-1]), FP16_REL, "generic fp16 backward")
     finally:
         recir_amd.set_generic_kernel_policy(prev)
