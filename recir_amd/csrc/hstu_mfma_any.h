@@ -77,7 +77,9 @@ __device__ __forceinline__ unsigned any_pack2(float lo, float hi) {
 
 // Two workgroups per CU where the registers allow it (a few spills included: one workgroup per CU
 // measured 20-35 % slower at these shapes).
-template <int MODE, int ELT, int DP>
+// HAS_RAB: with a bias table (an instantiation of its own: tested per pair the pointer costs seven scalar
+// instructions a score, and as a second set of tile bodies inside one kernel it costs registers).
+template <int MODE, int ELT, int DP, bool HAS_RAB>
 __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 128) || DP <= 64)) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
   const Params& p = bp.f;
   constexpr bool F16 = ELT == ANY_F16;
@@ -148,8 +150,8 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
     const char* __restrict__ Y2g = (const char*)(KEYS ? bp.dout : p.v);
     const size_t rb1 = (size_t)p.H * p.Dqk * ES, rb2 = (size_t)p.H * p.Dv * ES;
     const size_t hb1 = (size_t)h * p.Dqk * ES, hb2 = (size_t)h * p.Dv * ES;
-    const float* __restrict__ rabg = p.rab ? p.rab + (size_t)h * rab_w : nullptr;
-    float* __restrict__ drabg = (MODE == ANY_DQ && bp.drab) ? bp.drab + (size_t)h * rab_w : nullptr;
+    const float* __restrict__ rabg = HAS_RAB ? p.rab + (size_t)h * rab_w : nullptr;
+    float* __restrict__ drabg = (HAS_RAB && MODE == ANY_DQ && bp.drab) ? bp.drab + (size_t)h * rab_w : nullptr;
 
     // ---- stationary operands (B operand of the score products): lane holds row c ----
     const int cw0 = c0 + wave * 32;
@@ -253,7 +255,7 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
         st.y2[i] = ch * EPC < p.Dv ? *(const u32x4*)(Y2g + (size_t)(si.s + rr) * rb2 + hb2 + (size_t)ch * 16) : zero4;
       }
       st.bias = 0.f;
-      if (rabg && tid < ANY_BM + ANY_BN - 1) {
+      if (HAS_RAB && tid < ANY_BM + ANY_BN - 1) {
         // entry e of the band holds the bias of m - j = dmin + e
         const int dmin = KEYS ? r0 - c0 - (ANY_BM - 1) : c0 - r0 - (ANY_BN - 1);
         int idx = dmin + tid + p.N - 1;
@@ -271,7 +273,7 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
         *(u32x4*)(&Y1s[buf][row * RS + ch * 16]) = st.y1[i];
         *(u32x4*)(&Y2s[buf][row * RS + ch * 16]) = st.y2[i];
       }
-      if (tid < ANY_BM + ANY_BN - 1) bias_s[buf][tid] = st.bias;
+      if (HAS_RAB && tid < ANY_BM + ANY_BN - 1) bias_s[buf][tid] = st.bias;
       if (KEYS && tid < ANY_BN) scale_s[buf][tid] = st.scale;
     };
 
@@ -327,7 +329,7 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
         for (int r = 0; r < 16; ++r) {
           const int rl = 32 * blk + 8 * (r >> 2) + 4 * half + (r & 3);  // streamed row of this register
           float x = Sb[r] * p.alpha;
-          if (rabg) x += bias_s[buf][KEYS ? rl - (c - c0) + (ANY_BM - 1) : (c - c0) - rl + (ANY_BN - 1)];
+          if constexpr (HAS_RAB) x += bias_s[buf][KEYS ? rl - (c - c0) + (ANY_BM - 1) : (c - c0) - rl + (ANY_BN - 1)];
           const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * neg_log2e));
           float pe = x * sig;
           float de = 0.f;
@@ -509,9 +511,14 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
   }
 }
 
-// Launchers (defined in hstu_mfma_any.hip).  dtype: RECIR_HSTU_DTYPE_BF16 or RECIR_HSTU_DTYPE_FP16;
-// dp: padded head dim (32, 64, 128 or 256).  Return false when the combination has no instantiation.
+// Launchers.  dtype: RECIR_HSTU_DTYPE_BF16, _FP16 or _FP32; dp: padded head dim (32, 64, 128 or 256).
+// Return false when the combination has no instantiation.  The instantiations with and without a bias
+// table live in two translation units (hstu_mfma_any.hip, hstu_mfma_any_rab.hip) that compile side by side.
 bool launch_mfma_any_fwd(int dtype, int dp, dim3 grid, hipStream_t stream, const Params& p);
 bool launch_mfma_any_bwd(int dtype, int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk);
+template <bool HAS_RAB>
+bool launch_mfma_any_fwd_as(int dtype, int dp, dim3 grid, hipStream_t stream, const BwdParams& bp);
+template <bool HAS_RAB>
+bool launch_mfma_any_bwd_as(int dtype, int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk);
 
 }  // namespace recir_hstu

@@ -1,70 +1,20 @@
-// Instantiations and launchers of the MFMA kernels for head dims other than 128, fp16 values and the
-// masks the head-dim-128 kernels do not take (hstu_mfma_any.h).  A translation unit of its own so
-// that it compiles beside the other one.
-#include <cstring>
-
-#include "hstu_mfma_any.h"
+// General MFMA kernels (hstu_mfma_any.h): the instantiations without a bias table, and the two entry
+// points the host code calls, which pick the translation unit by the presence of a bias.
+#define HSTU_ANY_HAS_RAB 0
+#include "hstu_mfma_any_launch.h"
 
 namespace recir_hstu {
-
-namespace {
-
-// Which (mode, element type, padded head dim) are instantiated.  The key-stationary mode that produces
-// dK and dV together holds two operand sets and two accumulators: it stops at 128 (fp32: 64), and the
-// largest padded head dim (256, fp32: 128 -- its LDS tiles are twice as wide) takes its two halves.
-template <int MODE, int ELT, int DP>
-constexpr bool any_instantiated() {
-  constexpr int top = ELT == ANY_F32 ? 128 : 256;
-  if (MODE == ANY_DKV) return DP < top;
-  if (MODE == ANY_DV || MODE == ANY_DK) return DP == top;
-  return DP <= top;
-}
-
-template <int MODE, int ELT, int DP>
-bool launch_one(dim3 grid, hipStream_t stream, const BwdParams& bp) {
-  if constexpr (any_instantiated<MODE, ELT, DP>()) {
-    hipLaunchKernelGGL((hstu_mfma_any<MODE, ELT, DP>), grid, dim3(256), 0, stream, bp);
-    return true;
-  }
-  return false;
-}
-
-template <int MODE, int ELT>
-bool launch_mode(int dp, dim3 grid, hipStream_t stream, const BwdParams& bp) {
-  switch (dp) {
-    case 32: return launch_one<MODE, ELT, 32>(grid, stream, bp);
-    case 64: return launch_one<MODE, ELT, 64>(grid, stream, bp);
-    case 128: return launch_one<MODE, ELT, 128>(grid, stream, bp);
-    case 256: return launch_one<MODE, ELT, 256>(grid, stream, bp);
-    default: return false;
-  }
-}
-
-template <int ELT>
-bool launch_bwd(int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk) {
-  if (dp < (ELT == ANY_F32 ? 128 : 256))
-    return launch_mode<ANY_DKV, ELT>(dp, grid_k, stream, bk) && launch_mode<ANY_DQ, ELT>(dp, grid_q, stream, bq);
-  return launch_mode<ANY_DV, ELT>(dp, grid_k, stream, bk) && launch_mode<ANY_DK, ELT>(dp, grid_k, stream, bk) &&
-         launch_mode<ANY_DQ, ELT>(dp, grid_q, stream, bq);
-}
-
-}  // namespace
 
 bool launch_mfma_any_fwd(int dtype, int dp, dim3 grid, hipStream_t stream, const Params& p) {
   BwdParams bp;
   memset(&bp, 0, sizeof(bp));
   bp.f = p;
-  if (dtype == RECIR_HSTU_DTYPE_FP16) return launch_mode<ANY_FWD, ANY_F16>(dp, grid, stream, bp);
-  if (dtype == RECIR_HSTU_DTYPE_BF16) return launch_mode<ANY_FWD, ANY_BF16>(dp, grid, stream, bp);
-  if (dtype == RECIR_HSTU_DTYPE_FP32) return launch_mode<ANY_FWD, ANY_F32>(dp, grid, stream, bp);
-  return false;
+  return p.rab ? launch_mfma_any_fwd_as<true>(dtype, dp, grid, stream, bp) : launch_mfma_any_fwd_as<false>(dtype, dp, grid, stream, bp);
 }
 
 bool launch_mfma_any_bwd(int dtype, int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk) {
-  if (dtype == RECIR_HSTU_DTYPE_FP16) return launch_bwd<ANY_F16>(dp, grid_q, grid_k, stream, bq, bk);
-  if (dtype == RECIR_HSTU_DTYPE_BF16) return launch_bwd<ANY_BF16>(dp, grid_q, grid_k, stream, bq, bk);
-  if (dtype == RECIR_HSTU_DTYPE_FP32) return launch_bwd<ANY_F32>(dp, grid_q, grid_k, stream, bq, bk);
-  return false;
+  return bq.f.rab ? launch_mfma_any_bwd_as<true>(dtype, dp, grid_q, grid_k, stream, bq, bk)
+                  : launch_mfma_any_bwd_as<false>(dtype, dp, grid_q, grid_k, stream, bq, bk);
 }
 
 }  // namespace recir_hstu
