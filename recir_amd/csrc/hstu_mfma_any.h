@@ -1,10 +1,10 @@
 // MFMA kernels of the HSTU attention forward and backward for everything the kernels written for
 // head dim 128 do not take: head dims whose rows are multiples of 16 bytes, up to 256 (fp32: 128),
-// Dqk and Dv independent, bf16 or fp16 values, every mask the operator knows (causal with targets
-// and contextual prefix, semi-local, the non-causal forms), a bias with any alpha.  One template,
-// three modes; nothing here is hand-scheduled: the point is to keep such calls on the matrix
-// cores (a few times slower than the head-dim-128 kernels) instead of on the one-wave-per-token
-// kernels (two orders of magnitude slower).
+// Dqk and Dv independent; bf16, fp16 or fp32 values; every mask the operator knows (causal with targets
+// and contextual prefix, semi-local, the non-causal forms); a bias with any alpha, and the gradient of
+// the bias table.  One template, five modes; nothing here is hand-scheduled: the point is to keep such
+// calls on the matrix cores (about twice the time of the head-dim-128 kernels at their own shape)
+// instead of on the one-wave-per-token kernels (two orders of magnitude slower).
 //
 // A workgroup (4 waves) owns 128 "stationary" rows of one (sequence, head), 32 per wave, one per lane
 // of a 32-lane half; their operands stay in registers.  The other side is streamed through LDS in
@@ -15,28 +15,31 @@
 //                               dQ^T[:,c] += K^T[:,r] dS^T[r,c]
 //   DKV  c = key,   r = query   S[r,c] = Q[r,:] . K[c,:],  dP[r,c] = dO[r,:] . V[c,:]
 //                               dV^T[:,c] += dO^T[:,r] P[r,c],  dK^T[:,c] += Q^T[:,r] dS[r,c]
-//   DV, DK                      the two halves of DKV as passes of their own (padded head dim 256, where
-//                               both accumulators and both operand sets do not fit one wave's registers)
-// Every product is v_mfma_f32_32x32x16 with the streamed tile as the A operand: rows of the tile for
-// the score products (ds_read_b128), the transposed tile for the accumulating products
-// (ds_read_b64_tr_b16 on the same row-major tile).  The 32 x 32 accumulator layout of a score block
-// (lane = c, registers = r) is the B-operand layout of the accumulating product, so P and dS go from
-// one MFMA to the next through registers only.
+//   DV, DK                      the two halves of DKV as passes of their own (the largest padded head
+//                               dim, where both accumulators and both operand sets do not fit one
+//                               wave's registers)
+//   x = alpha S + bias;  P = silu(x) keep;  dS = dP silu'(x) keep   (dO . V is dP)
+//   out = scale P V;  dQ = alpha scale dS K;  dK = alpha (scale dS)^T Q;  dV = (scale P)^T dO
+// The scale of a query row multiplies a column in FWD and DQ (applied to the accumulators at the
+// end) and a streamed row in the key-stationary modes (applied per element when it is per token;
+// fp16: times a power of two taken from the largest scale of the item's rows and divided out of the
+// accumulators at the end, so that P and dS times a scale of the order of 1 / max_seq_len stay in
+// fp16's normal range).
 //
-// Head dims are padded to DP in {32, 64, 128, 256} with zeros (16-byte chunks past Dqk or Dv are not
-// loaded); both dims share the larger padding.
+// bf16 and fp16: every product is v_mfma_f32_32x32x16 with the streamed tile as the A operand: rows
+// of the tile for the score products (ds_read_b128), the transposed tile for the accumulating
+// products (ds_read_b64_tr_b16 on the same row-major tile).  The 32 x 32 accumulator layout of a
+// score block (lane = c, registers = r) is the B-operand layout of the accumulating product, so P
+// and dS go from one MFMA to the next through registers only.
 //
-// fp32 tensors (DP up to 128) take the same walk with v_mfma_f32_32x32x2_f32, one element per lane and
+// fp32 (DP up to 128) takes the same walk with v_mfma_f32_32x32x2_f32, one element per lane and
 // operand: lane half h contracts elements h DP / 2 .. of the head dim in the score products and its
 // own streamed rows in the accumulating ones, whose B operand is the score block's register as it
 // is and whose A operand is a plain 4-byte LDS read (consecutive lanes, consecutive columns); P and
 // dS are not rounded.  A sixteenth of the bf16 rate, and still some twenty times the generic kernel.
-//   x = alpha S + bias;  P = silu(x) keep;  dS = dP silu'(x) keep   (dO . V is dP)
-//   out = scale P V;  dQ = alpha scale dS K;  dK = alpha (scale dS)^T Q;  dV = (scale P)^T dO
-// The scale of a query row multiplies a column in FWD and DQ (applied to the accumulators at the
-// end) and a streamed row in DKV (applied per element when it is per token; fp16: times a power of
-// two taken from the largest scale of the item's rows and divided out of the accumulators at the
-// end, so that P and dS times a scale of the order of 1 / max_seq_len stay in fp16's normal range).
+//
+// Head dims are padded to DP in {32, 64, 128, 256} with zeros (16-byte chunks past Dqk or Dv are not
+// loaded or stored); both dims share the larger padding.
 #pragma once
 #include <type_traits>
 
@@ -49,7 +52,8 @@ typedef __attribute__((ext_vector_type(2))) _Float16 any_f16x2;
 typedef __attribute__((ext_vector_type(4))) short any_i16x4;
 typedef __attribute__((address_space(3))) any_i16x4 any_lds_i16x4;
 
-constexpr int ANY_FWD = 0, ANY_DQ = 1, ANY_DKV = 2, ANY_DV = 3, ANY_DK = 4;  // DV, DK: the two halves of DKV as passes of their own
+constexpr int ANY_FWD = 0, ANY_DQ = 1, ANY_DKV = 2, ANY_DV = 3, ANY_DK = 4;  // modes (DV, DK: the two halves of DKV as passes of their own)
+constexpr int ANY_BF16 = 0, ANY_F16 = 1, ANY_F32 = 2;                        // element types (the template's ELT)
 constexpr int ANY_BM = 128;  // stationary rows per workgroup
 constexpr int ANY_BN = 64;   // streamed rows per tile
 constexpr float kAnyLog2e = 1.4426950408889634f;
@@ -61,8 +65,6 @@ __device__ __forceinline__ f32x16 any_mfma(const u32x4& a, const u32x4& b, const
   else
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
-
-constexpr int ANY_BF16 = 0, ANY_F16 = 1, ANY_F32 = 2;  // element types (the template's ELT)
 
 template <bool F16>
 __device__ __forceinline__ unsigned any_pack2(float lo, float hi) {
@@ -86,8 +88,8 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
   constexpr bool F32 = ELT == ANY_F32;  // v_mfma_f32_32x32x2_f32: one element per lane and operand, see below
   constexpr int ES = F32 ? 4 : 2;       // bytes per element
   constexpr bool KEYS = MODE >= ANY_DKV;                                  // the stationary rows are keys
-  constexpr bool HAS_DP = MODE == ANY_DQ || MODE == 2 || MODE == ANY_DK;   // dP, dS and the product that dS feeds
-  constexpr bool HAS_P = MODE == ANY_FWD || MODE == 2 || MODE == ANY_DV;   // the product that P feeds
+  constexpr bool HAS_DP = MODE == ANY_DQ || MODE == ANY_DKV || MODE == ANY_DK;   // dP, dS and the product that dS feeds
+  constexpr bool HAS_P = MODE == ANY_FWD || MODE == ANY_DKV || MODE == ANY_DV;   // the product that P feeds
   constexpr int NK = DP * ES / 32;  // 16-byte registers-quads of a stationary row per lane (bf16, fp16: steps of 16 along the head dim)
   constexpr int NB = DP / 32;       // 32-row blocks of a transposed accumulator
   constexpr int RS = DP * ES + 16;  // bytes between tile rows in LDS (the 16 spread the rows over the banks)
