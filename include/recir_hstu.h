@@ -111,7 +111,9 @@ extern "C" {
  * seq_offsets   device, [B+1] int64 (int32 with FLAG_OFFSETS_I32), non-decreasing, last <= T.
  *               Malformed entries are clamped on the device (no fault, result unspecified).
  * num_targets   device, [B] or NULL (= zeros)
- * rab           device float [H, 2*max_seq_len-1] or NULL.  No counterpart in the reference.
+ * rab           device float [H, 2*max_seq_len-1] or NULL.  No counterpart in the reference.  A pair
+ *               whose m - j falls outside the table (possible only in a sequence longer than
+ *               max_seq_len, which is out of contract) gets no bias and adds nothing to drab.
  * attn_scale    device float scalar, [T] with FLAG_SCALE_PER_TOKEN, or NULL (= 1/max_seq_len)
  * q_scale,k_scale  device float [H]; FP8_E4M3 only (dequantisation factors), else NULL
  * max_attn_len, full_attn_size   >= 0; 0, 0 is the plain causal mask; full_attn_size is ignored

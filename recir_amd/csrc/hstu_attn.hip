@@ -265,9 +265,8 @@ __global__ __launch_bounds__(64) void hstu_fwd_generic(Params p) {
       for (int d = 0; d < p.Dqk; ++d) dot = fmaf(qrow[d], load_elem<ELT>(p.k, krow + d), dot);
       float x = dot * p.alpha;
       if (p.rab) {
-        int idx = m - j + p.N - 1;
-        idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
-        x += p.rab[(size_t)h * rab_w + idx];
+        const int idx = m - j + p.N - 1;  // outside the table (sequence longer than max_seq_len): no bias
+        if (idx >= 0 && idx < rab_w) x += p.rab[(size_t)h * rab_w + idx];
       }
       pj = x / (1.0f + __expf(-x)) * scale;
       pj = round_to_elem<ELT>(pj);

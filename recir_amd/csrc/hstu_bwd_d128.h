@@ -293,6 +293,11 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     const float score_c = p.alpha * kLog2e, neg_c = -score_c;
     // the bias is staged multiplied by log2(e) and joins the score in the multiply-add that applies alpha log2(e)
     const float bias_mul = kLog2e;
+    // what the staged band is multiplied with: 0 for a diagonal outside the table (possible only in a
+    // sequence longer than max_seq_len; the load clamps its index), which then has no bias
+    auto band_mul_of = [&](int t) __attribute__((always_inline)) {
+      return (unsigned)(q0 - t * BWD_BN - (BWD_BN - 1) + p.N - 1 + tid) < (unsigned)rab_w ? bias_mul : 0.f;
+    };
 
     f32x16 acc[4];
 #pragma unroll
@@ -418,7 +423,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
     };
     int prev_tile = -1;
     // two tiles per trip so that the stage index is a compile-time constant
-    if (HAS_RAB && it < nkv) bwd_band_store<true>(band0, band_first, tid, bias_mul);
+    if (HAS_RAB && it < nkv) bwd_band_store<true>(band0, band_first, tid, band_mul_of(it));
     while (it < nkv) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile `it` have landed
       __syncthreads();                                   // everybody's; the other stage is free again
@@ -431,7 +436,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       if (HAS_RAB && nxt < nkv) band_nxt = band_of(nxt);
       if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, 1>{});
       compute_tile(it, std::integral_constant<int, 0>{});
-      if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band1, band_nxt, tid, bias_mul);
+      if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band1, band_nxt, tid, band_mul_of(nxt));
       prev_tile = it;
       it = nxt;
       if (it >= nkv) {
@@ -445,7 +450,7 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
       if (HAS_RAB && nxt < nkv) band_nxt = band_of(nxt);
       if (nxt < nkv) issue_tile(nxt, std::integral_constant<int, 0>{});
       compute_tile(it, std::integral_constant<int, 1>{});
-      if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band0, band_nxt, tid, bias_mul);
+      if (HAS_RAB && nxt < nkv) bwd_band_store<true>(band0, band_nxt, tid, band_mul_of(nxt));
       prev_tile = it;
       it = nxt;
       if (RAB_GRAD && it >= nkv) { __syncthreads(); flush_gband(prev_tile, gband1); }
@@ -612,6 +617,9 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
     // is the biased score, and the arithmetic below is that of the kernel without a bias.  (The host
     // sends a bias with alpha = 0 to the generic kernels.)
     const float bias_mul = HAS_RAB ? 1.0f / p.alpha : 0.f;
+    auto band_mul_of = [&](int t) __attribute__((always_inline)) {  // 0 for a diagonal outside the table, as in the dQ kernel
+      return (unsigned)(t * BWD_BN - j0 - (BWD_BM - 1) + p.N - 1 + tid) < (unsigned)rab_w ? bias_mul : 0.f;
+    };
     bwd_load_row_frags(p.v, (size_t)si.s + j, p.H, h, half, j < si.n, false, 1.0f, vf);
 
     bwd_acc_zero();  // dK^T and dV^T accumulators (fixed AGPRs)
@@ -789,7 +797,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       else tile_body(std::integral_constant<int, 1>{}, buf_tag, m0);
     };
 
-    if (HAS_RAB && it < nq) bwd_band_store<false>(band0, band_first, tid, bias_mul);
+    if (HAS_RAB && it < nq) bwd_band_store<false>(band0, band_first, tid, band_mul_of(it));
     while (it < nq) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -799,7 +807,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 1>{});
       draw_step(tiles_left(it));
       compute_tile(it, std::integral_constant<int, 0>{});
-      if (HAS_RAB && nxt < nq) bwd_band_store<false>(band1, band_nxt, tid, bias_mul);
+      if (HAS_RAB && nxt < nq) bwd_band_store<false>(band1, band_nxt, tid, band_mul_of(nxt));
       it = nxt;
       if (it >= nq) break;
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -809,7 +817,7 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
       if (nxt < nq) issue_tile(nxt, std::integral_constant<int, 0>{});
       draw_step(tiles_left(it));
       compute_tile(it, std::integral_constant<int, 1>{});
-      if (HAS_RAB && nxt < nq) bwd_band_store<false>(band0, band_nxt, tid, bias_mul);
+      if (HAS_RAB && nxt < nq) bwd_band_store<false>(band0, band_nxt, tid, band_mul_of(nxt));
       it = nxt;
     }
     draw_finish();

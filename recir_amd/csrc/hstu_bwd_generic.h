@@ -34,9 +34,9 @@ __device__ __forceinline__ int find_sequence(const Params& p, int r, SeqInfo& si
 __device__ __forceinline__ float score_bias(const Params& p, int h, int m, int j) {
   if (!p.rab) return 0.f;
   const int rab_w = 2 * p.N - 1;
-  int idx = m - j + p.N - 1;
-  idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
-  return p.rab[(size_t)h * rab_w + idx];
+  // a pair outside the table (possible only in a sequence longer than max_seq_len) has no bias
+  const int idx = m - j + p.N - 1;
+  return (idx >= 0 && idx < rab_w) ? p.rab[(size_t)h * rab_w + idx] : 0.f;
 }
 
 // dQ[r] = alpha * sum_j dS(m, j) K[j]

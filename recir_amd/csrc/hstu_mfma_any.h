@@ -260,9 +260,9 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
       if (HAS_RAB && tid < ANY_BM + ANY_BN - 1) {
         // entry e of the band holds the bias of m - j = dmin + e
         const int dmin = KEYS ? r0 - c0 - (ANY_BM - 1) : c0 - r0 - (ANY_BN - 1);
-        int idx = dmin + tid + p.N - 1;
-        idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
-        st.bias = rabg[idx];
+        // (a diagonal outside the table, possible only in a sequence longer than max_seq_len, has no bias)
+        const int idx = dmin + tid + p.N - 1;
+        st.bias = (idx >= 0 && idx < rab_w) ? rabg[idx] : 0.f;
       }
       st.scale = 1.0f;
       if (KEYS && per_token && tid < ANY_BN) st.scale = p.attn_scale[si.s + min(r0 + tid, si.n - 1)] * pow2_up;

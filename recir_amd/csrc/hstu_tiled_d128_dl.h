@@ -278,10 +278,13 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       idx = idx < 0 ? 0 : (idx >= rab_w ? rab_w - 1 : idx);
       return rabg[idx];  // scaled in band_store: nothing may use the value before the tile's arithmetic is over
     };
-    auto band_store = [&](auto buf_tag, float val) __attribute__((always_inline)) {
+    // (it: the tile the band belongs to.  The load clamps its index into the table; a diagonal
+    // outside it, possible only in a sequence longer than max_seq_len, gets no bias here)
+    auto band_store = [&](auto buf_tag, float val, int it) __attribute__((always_inline)) {
       constexpr int BUF = decltype(buf_tag)::value;
       asm volatile("" : "+v"(val));  // first use of the loaded value: the wait for it stays here
-      if (tid < BM + BN - 1) (BUF ? rabs1 : rabs0)[(BM + BN - 2) - tid] = val * bias_mul;
+      const bool in_table = (unsigned)(q0 - it * BN - (BN - 1) + p.N - 1 + tid) < (unsigned)rab_w;
+      if (tid < BM + BN - 1) (BUF ? rabs1 : rabs0)[(BM + BN - 2) - tid] = in_table ? val * bias_mul : 0.f;
     };
     auto issue_tile_as = [&](int it, auto buf_tag, auto whole_tag) __attribute__((always_inline)) {
 #pragma unroll
@@ -295,7 +298,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       float band = 0.f;
       if (HAS_RAB) band = band_load(it);
       issue_tile(it, buf_tag);
-      if (HAS_RAB) band_store(buf_tag, band);
+      if (HAS_RAB) band_store(buf_tag, band, it);
     };
 
     // first tile in flight before anything else is waited for
@@ -518,7 +521,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           __builtin_amdgcn_s_setprio(0);
           if (s < 8) issue_slot(s);  // one copy instruction of the next tile behind each of the first MFMAs
           if (s >= DL_U0 && s < DL_U0 + 16) silu_unit(s - DL_U0);
-          if (HAS_RAB && s == 31 && copy_next) band_store(other, band_next);
+          if (HAS_RAB && s == 31 && copy_next) band_store(other, band_next, nxt);
           __builtin_amdgcn_sched_barrier(0);
         }
         return;
@@ -633,7 +636,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       mfma_group(6, fa);
       __builtin_amdgcn_sched_barrier(0);
       mfma_group(7, fb);
-      if (HAS_RAB && (FAST || nxt < nkv)) band_store(other, band_nxt);
+      if (HAS_RAB && (FAST || nxt < nkv)) band_store(other, band_nxt, nxt);
     };
 
     // ---- the skewed loop ----
@@ -764,7 +767,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     }
 
     if (it < nkv) {
-      if (HAS_RAB) band_store(std::integral_constant<int, 0>{}, band_first);
+      if (HAS_RAB) band_store(std::integral_constant<int, 0>{}, band_first, it);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       HSTU_TR(tr_ready = wall_clock64(); tr_c0_item = clock64(); unsigned long long tr_t = tr_ready;)

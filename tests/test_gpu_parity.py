@@ -295,14 +295,27 @@ def test_work_list_dealing_by_tiles_and_by_pairs(oracle, lengths):
     assert_bf16_close(run_hip(wl), run_oracle(oracle, wl), f"lengths {lengths[:2]}...")
 
 
-def test_sequences_longer_than_max_seq_len_do_not_break_the_work_list(oracle):
+@pytest.mark.parametrize("D,with_rab", [(128, False), (128, True), (64, False), (64, True)])
+def test_sequences_longer_than_max_seq_len_do_not_break_the_work_list(oracle, D, with_rab):
     """Out of contract (n > max_seq_len), but the launch must stay in bounds: the work lists are
-    then longer than the grid assumes and the workgroups loop over them."""
+    then longer than the grid assumes and the workgroups loop over them; the index into a bias table
+    is clamped to the table.  Head dim 128 and the general MFMA kernels, forward and backward."""
+    from recir_amd import _lib
     from recir_amd.workloads import make_jagged
+    from tests.test_gpu_bwd import _scale_np, assert_grads_close, run_hip_bwd
 
-    wl = make_jagged([3000, 40, 1500], [10, 0, 0], 1, 128, 128, max_seq_len=256, alpha=1 / 128, dtype="bf16", seed=12)
+    wl = make_jagged([3000, 40, 1500], [10, 0, 0], 1, D, D, max_seq_len=256, alpha=1 / D, dtype="bf16", seed=12,
+                     with_rab=with_rab, rab_std=0.5)
     out = run_hip(wl)
+    assert _lib.last_kernel() == expected_kernel(D, D, rab=with_rab)
     assert_bf16_close(out, run_oracle(oracle, wl), "n > N")
+    dout = torch.randn(wl.T, wl.H, D, generator=torch.Generator().manual_seed(4)).bfloat16().float()
+    got = run_hip_bwd(wl, dout, rab=wl.rab)
+    assert _lib.last_kernel() == expected_kernel(D, D, bwd=True, rab=with_rab)
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,
+                           rab=None if wl.rab is None else wl.rab.numpy())
+    assert_grads_close(got, want[:3], int(wl.seq_offsets[-1]), BF16_REL, "n > N backward")
 
 
 def test_work_lists_are_reused_for_the_same_offset_tensors_and_rebuilt_when_they_change(oracle):
