@@ -43,6 +43,7 @@ def describe(wl, cfg):
         7: "config7: 16 sequences of 4096 history tokens, no targets, H=4, D=128, bf16 (steady state: two workgroups per CU throughout)",
         8: "config8: config2's sequences with H=8, Dqk=Dv=64, bf16 (general MFMA kernels)",
         9: "config9: config2 in fp16 (general MFMA kernels)",
+        10: "config10: config8 at Dqk=Dv=50, rows of 100 bytes (general MFMA kernels for rows aligned to the element only)",
     }
     return names[cfg]
 
@@ -499,7 +500,7 @@ def main():
     # of configuration 2 run up to 20 % slower): the default warm-up covers that
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6, 7, 8, 9])
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", type=int, default=0, help="kernel selector (0 auto)")
     ap.add_argument("--rab-grad", action="store_true", help="with --backward and a configuration that has a bias table: its gradient too")

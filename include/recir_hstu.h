@@ -40,12 +40,16 @@ extern "C" {
  *   - the kernels written for head dim 128 ("tiled_d128_*", "bwd_tiled_d128_*"): bf16 (forward also
  *     fp8 q/k), Dqk = Dv = 128, 16-byte aligned tensors, the causal or semi-local mask, alpha != 0
  *     when there is a bias; the gradient of the bias table is reproducible bit for bit here only;
- *   - the general MFMA kernels ("mfma_*", "bwd_mfma_*"): bf16 or fp16 with Dqk and Dv any multiples
- *     of 8 up to 256, fp32 with multiples of 4 up to 128 (fp32 MFMAs, a sixteenth of the bf16 rate);
- *     Dqk and Dv independent of each other, 16-byte aligned tensors, every mask, any alpha; in bf16
- *     about twice the time of the first group at its own shape;
+ *   - the general MFMA kernels ("mfma_*", "bwd_mfma_*"): bf16 or fp16 with Dqk and Dv up to 256,
+ *     fp32 up to 128 (fp32 MFMAs, a sixteenth of the bf16 rate); Dqk and Dv independent of each
+ *     other, every mask, any alpha; in bf16 about twice the time of the first group at its own
+ *     shape.  Where every row of every tensor starts at a multiple of 16 bytes (16-byte aligned
+ *     tensors, head dims multiples of 8, fp32: 4) rows move in aligned 16-byte pieces; otherwise
+ *     (head dims like 25 or 50, a tensor that starts in the middle of a row of a larger one) in
+ *     pieces aligned to the element only ("*_elems"), at 1.2 to 1.7 times the time;
  *   - the generic kernels ("generic_*", "bwd_generic_*"): one wave per (token, head), bf16, fp16 or
- *     fp32, any head dim up to 512; one to two orders of magnitude slower.
+ *     fp32, any head dim up to 512; one to two orders of magnitude slower.  What is left to them:
+ *     head dims above 256 (fp32: 128).
  */
 
 /* flags */
@@ -78,10 +82,8 @@ extern "C" {
 #define RECIR_HSTU_FLAG_TILED_ONLY 0x40000u       /* reject (RECIR_HSTU_ERR_UNSUPPORTED, with the reason
                                                      in recir_hstu_last_error) a call that only the
                                                      generic kernels cover instead of running it
-                                                     there: head dims whose rows are not multiples
-                                                     of 16 bytes or that exceed 256 (fp32: 128),
-                                                     tensors not 16-byte aligned.  Forward and
-                                                     backward.                                       */
+                                                     there: head dims that exceed 256 (fp32: 128).
+                                                     Forward and backward.                           */
 #define RECIR_HSTU_FLAG_KERNEL_SHIFT 8            /* bits 8..15: kernel selector for tests/tuning  */
 #define RECIR_HSTU_FLAG_KERNEL_MASK 0xff00u       /* 0 auto, 1 generic, 2 general MFMA, 3 head dim 128 */
 

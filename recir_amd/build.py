@@ -11,7 +11,7 @@ LIB_PATH = os.path.join(_PKG, "librecir_hstu.so")
 # the same sources with the forward kernel's phase stamps compiled in (bench.py --phase-trace); never
 # loaded by the operators
 TRACE_LIB_PATH = os.path.join(_PKG, "librecir_hstu_trace.so")
-SOURCES = [os.path.join(_PKG, "csrc", n) for n in ("hstu_attn.hip", "hstu_mfma_any.hip", "hstu_mfma_any_rab.hip")]
+SOURCES = [os.path.join(_PKG, "csrc", n) for n in ("hstu_attn.hip", "hstu_mfma_any.hip", "hstu_mfma_any_rab.hip", "hstu_mfma_any_elems.hip", "hstu_mfma_any_elems_rab.hip")]
 
 
 def hipcc_path() -> str:

@@ -358,27 +358,27 @@ void launch_bwd_tiled(bool semi, bool has_rab, dim3 grid, dim3 grid_k, hipStream
   }
 }
 
-// Padded head dim of the general MFMA kernels for a call, 0 when they do not take it: rows of both
-// tensors multiples of 16 bytes, the larger head dim at most 256 (fp32: 128, its tiles are twice as wide).
+// Padded head dim of the general MFMA kernels for a call, 0 when they do not take it: the larger head
+// dim at most 256 (fp32: 128, its tiles are twice as wide).
 int mfma_any_padded_dim(int Dqk, int Dv, int dtype) {
   const bool f32 = dtype == RECIR_HSTU_DTYPE_FP32;
   if (dtype != RECIR_HSTU_DTYPE_BF16 && dtype != RECIR_HSTU_DTYPE_FP16 && !f32) return 0;
-  const int per_chunk = f32 ? 4 : 8;
-  if (Dqk % per_chunk || Dv % per_chunk) return 0;
   const int d = Dqk > Dv ? Dqk : Dv;
-  if (d > (f32 ? 128 : 256)) return 0;
+  if (d < 1 || d > (f32 ? 128 : 256)) return 0;
   return d <= 32 ? 32 : (d <= 64 ? 64 : (d <= 128 ? 128 : 256));
 }
-const char* mfma_any_name(bool bwd, int dtype, int dp) {
-  static const char* const names[2][3][4] = {
-      {{"mfma_bf16_d32", "mfma_bf16_d64", "mfma_bf16_d128", "mfma_bf16_d256"},
-       {"mfma_fp16_d32", "mfma_fp16_d64", "mfma_fp16_d128", "mfma_fp16_d256"},
-       {"mfma_fp32_d32", "mfma_fp32_d64", "mfma_fp32_d128", "mfma_fp32_d256"}},
-      {{"bwd_mfma_bf16_d32", "bwd_mfma_bf16_d64", "bwd_mfma_bf16_d128", "bwd_mfma_bf16_d256"},
-       {"bwd_mfma_fp16_d32", "bwd_mfma_fp16_d64", "bwd_mfma_fp16_d128", "bwd_mfma_fp16_d256"},
-       {"bwd_mfma_fp32_d32", "bwd_mfma_fp32_d64", "bwd_mfma_fp32_d128", "bwd_mfma_fp32_d256"}}};
-  const int t = dtype == RECIR_HSTU_DTYPE_FP16 ? 1 : (dtype == RECIR_HSTU_DTYPE_FP32 ? 2 : 0);
-  return names[bwd ? 1 : 0][t][dp == 32 ? 0 : (dp == 64 ? 1 : (dp == 128 ? 2 : 3))];
+// Rows of Dqk and of Dv elements are multiples of 16 bytes (with 16-byte aligned tensors every row then
+// starts at such a multiple, and the general MFMA kernels move rows in 16-byte pieces).
+bool rows_are_16_byte_multiples(int Dqk, int Dv, int dtype) {
+  const int per_chunk = dtype == RECIR_HSTU_DTYPE_FP32 ? 4 : 8;
+  return Dqk % per_chunk == 0 && Dv % per_chunk == 0;
+}
+// "mfma_bf16_d64", "bwd_mfma_fp32_d32_elems", ...: "_elems" where the rows are aligned to the element only
+const char* mfma_any_name(bool bwd, int dtype, int dp, bool aligned) {
+  static thread_local char name[48];
+  const char* t = dtype == RECIR_HSTU_DTYPE_FP16 ? "fp16" : (dtype == RECIR_HSTU_DTYPE_FP32 ? "fp32" : "bf16");
+  snprintf(name, sizeof(name), "%smfma_%s_d%d%s", bwd ? "bwd_" : "", t, dp, aligned ? "" : "_elems");
+  return name;
 }
 
 template <bool FP8>
@@ -464,7 +464,9 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
   const bool d128_ok = (dtype == RECIR_HSTU_DTYPE_BF16 || fp8) && Dqk == HD && Dv == HD && aligned && !noncausal && !bias_needs_other;
   // the MFMA kernels for other head dims, fp16 and the remaining masks (hstu_mfma_any.h)
   const int any_dp = mfma_any_padded_dim(Dqk, Dv, dtype);
-  const bool any_ok = any_dp != 0 && aligned;
+  const bool elem_aligned = (((size_t)q | (size_t)k | (size_t)v | (size_t)out) & (esz - 1)) == 0;
+  const bool any_ok = any_dp != 0 && elem_aligned;
+  const bool any_aligned = aligned && rows_are_16_byte_multiples(Dqk, Dv, dtype);
   if (variant > 3) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "unknown kernel selector %u", variant);
   if (variant == 3 && !d128_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
@@ -472,8 +474,7 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
                 "semi-local mask and alpha != 0 with a bias");
   if (variant == 2 && !any_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "the general MFMA kernel needs bf16, fp16 or fp32, head dims whose rows are multiples of 16 bytes, up to 256 "
-                "(fp32: 128), and 16-byte aligned tensors");
+                "the general MFMA kernel needs bf16, fp16 or fp32 and head dims up to 256 (fp32: 128)");
   if (fp8 && !d128_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
                 "fp8 q/k is implemented for Dqk = Dv = 128, 16-byte aligned tensors, the causal or semi-local mask (and alpha != 0 with a bias)");
@@ -520,8 +521,9 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
 #endif
     const dim3 grid((unsigned)(slots * NUM_XCD));
     if (use_any) {
-      if (!launch_mfma_any_fwd(dtype, any_dp, grid, stream, p)) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "no general MFMA kernel for dtype %d, padded head dim %d", dtype, any_dp);
-      g_last_kernel = mfma_any_name(false, dtype, any_dp);
+      if (!launch_mfma_any_fwd(dtype, any_dp, any_aligned, grid, stream, p))
+        return fail(RECIR_HSTU_ERR_UNSUPPORTED, "no general MFMA kernel for dtype %d, padded head dim %d", dtype, any_dp);
+      g_last_kernel = mfma_any_name(false, dtype, any_dp, any_aligned);
     } else if (fp8) {
       launch_dl<true>(rab != nullptr, semi, grid, stream, p);
       g_last_kernel = rab ? "tiled_d128_fp8qk_rab" : "tiled_d128_fp8qk";
@@ -535,8 +537,8 @@ int recir_hstu_attn_fwd(const void* q, const void* k, const void* v, void* out,
 
   if (flags & RECIR_HSTU_FLAG_TILED_ONLY)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "only the generic kernel covers this call (the MFMA kernels need head dims whose rows are multiples of 16 bytes, up to "
-                "256 (fp32: 128), and 16-byte aligned tensors): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
+                "only the generic kernel covers this call (the MFMA kernels take head dims up to 256, fp32: 128): dtype=%d Dqk=%d "
+                "Dv=%d", dtype, Dqk, Dv);
   if (Dqk > GENERIC_MAX_D || Dv > GENERIC_MAX_D)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED, "head dims above %d are not supported (Dqk=%d Dv=%d)", GENERIC_MAX_D, Dqk, Dv);
   if (H > 65535) return fail(RECIR_HSTU_ERR_UNSUPPORTED, "more than 65535 heads");
@@ -701,7 +703,9 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   const bool d128_ok = bf16 && Dqk == HD && Dv == HD && aligned && !noncausal && !bias_needs_other;
   // the general MFMA kernels (hstu_mfma_any.h)
   const int any_dp = mfma_any_padded_dim(Dqk, Dv, dtype);
-  const bool any_ok = any_dp != 0 && aligned;
+  const bool elem_aligned = (((size_t)dout | (size_t)q | (size_t)k | (size_t)v | (size_t)dq | (size_t)dk | (size_t)dv) & (esz - 1)) == 0;
+  const bool any_ok = any_dp != 0 && elem_aligned;
+  const bool any_aligned = aligned && rows_are_16_byte_multiples(Dqk, Dv, dtype);
   if (variant > 3) return fail(RECIR_HSTU_ERR_INVALID_ARGUMENT, "unknown kernel selector %u", variant);
   if (variant == 3 && !d128_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
@@ -709,8 +713,7 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
                 "and alpha != 0 with a bias");
   if (variant == 2 && !any_ok)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "the general MFMA backward needs bf16, fp16 or fp32, head dims whose rows are multiples of 16 bytes, up to 256 "
-                "(fp32: 128), and 16-byte aligned tensors");
+                "the general MFMA backward needs bf16, fp16 or fp32 and head dims up to 256 (fp32: 128)");
   const bool use_tiled = d128_ok && (variant == 0 || variant == 3);
   const bool use_any = !use_tiled && any_ok && variant != 1;
   if (use_tiled || use_any) {
@@ -753,10 +756,10 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
     if (use_any) {
       if (int rc = zero_drab()) return rc;  // the dQ pass adds floats to it
       const dim3 grid((unsigned)(slots * NUM_XCD));
-      if (!launch_mfma_any_bwd(dtype, any_dp, grid, grid, stream, bq, bk))
+      if (!launch_mfma_any_bwd(dtype, any_dp, any_aligned, grid, grid, stream, bq, bk))
         return fail(RECIR_HSTU_ERR_UNSUPPORTED, "no general MFMA backward for dtype %d, padded head dim %d", dtype, any_dp);
       if (int rc = launch_status("hstu_mfma_any (backward)")) return rc;
-      g_last_kernel = mfma_any_name(true, dtype, any_dp);
+      g_last_kernel = mfma_any_name(true, dtype, any_dp, any_aligned);
       return RECIR_HSTU_OK;
     }
     const bool per_token = attn_scale && (flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
@@ -804,8 +807,8 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
   }
   if (flags & RECIR_HSTU_FLAG_TILED_ONLY)
     return fail(RECIR_HSTU_ERR_UNSUPPORTED,
-                "only the generic kernels cover this call (the MFMA kernels need head dims whose rows are multiples of 16 bytes, up to "
-                "256 (fp32: 128), and 16-byte aligned tensors): dtype=%d Dqk=%d Dv=%d", dtype, Dqk, Dv);
+                "only the generic kernels cover this call (the MFMA kernels take head dims up to 256, fp32: 128): dtype=%d Dqk=%d "
+                "Dv=%d", dtype, Dqk, Dv);
   if (int rc = zero_drab()) return rc;
   const dim3 grid((unsigned)T, (unsigned)H);
   if (bf16) {

@@ -414,7 +414,7 @@ __global__ __launch_bounds__(256, 1) void hstu_calibration_loop64(CalParams c) {
     cal_static_for<0, 64>([&](auto S_) __attribute__((always_inline)) {
       constexpr int s = decltype(S_)::value;
       constexpr int f = s >> 1, qb = s & 1, g = f >> 3, j = f & 7;
-      if (qb == 0 && f + PD < 32) F[f + PD] = slot_frag(f + PD);
+      if constexpr (qb == 0 && f + PD < 32) F[f + PD] = slot_frag(f + PD);
       if (g == 0 || g == 2) {
         const int ks = (g == 0 ? 2 : 0) + (j >> 2), db = j & 3, blk = g == 0 ? 1 : 0;
         const u32x4 w = {pw[blk][qb][4 * (ks & 1)], pw[blk][qb][4 * (ks & 1) + 1], pw[blk][qb][4 * (ks & 1) + 2], pw[blk][qb][4 * (ks & 1) + 3]};

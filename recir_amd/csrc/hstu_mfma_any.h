@@ -1,6 +1,6 @@
 // MFMA kernels of the HSTU attention forward and backward for everything the kernels written for
-// head dim 128 do not take: head dims whose rows are multiples of 16 bytes, up to 256 (fp32: 128),
-// Dqk and Dv independent; bf16, fp16 or fp32 values; every mask the operator knows (causal with targets
+// head dim 128 do not take: any head dims up to 256 (fp32: 128), Dqk and Dv independent; bf16, fp16
+// or fp32 values; tensors at any address their element type allows; every mask the operator knows (causal with targets
 // and contextual prefix, semi-local, the non-causal forms); a bias with any alpha, and the gradient of
 // the bias table.  One template, five modes; nothing here is hand-scheduled: the point is to keep such
 // calls on the matrix cores (about twice the time of the head-dim-128 kernels at their own shape)
@@ -39,7 +39,11 @@
 // dS are not rounded.  A sixteenth of the bf16 rate, and still some twenty times the generic kernel.
 //
 // Head dims are padded to DP in {32, 64, 128, 256} with zeros (16-byte chunks past Dqk or Dv are not
-// loaded or stored); both dims share the larger padding.
+// loaded or stored); both dims share the larger padding.  ALIGNED: every row of every tensor starts at
+// a multiple of 16 bytes (head dims multiples of 8 elements, fp32: 4, and aligned base addresses), and
+// rows move in 16-byte pieces that the kernel knows to be aligned; otherwise (a head dim of 25 or 50, a
+// view that starts in the middle of a row) in pieces aligned to the element only, the last few elements
+// of a row one by one, zeros in the padding, and everything after the staging is the same.
 #pragma once
 #include <type_traits>
 
@@ -77,11 +81,52 @@ __device__ __forceinline__ unsigned any_pack2(float lo, float hi) {
   }
 }
 
+// 16 bytes of a row of D elements from an address aligned to the element only; n = elements left in the
+// row from there.  A full piece is one 16-byte load (the hardware's unaligned access mode, which the
+// compiler relies on for every under-aligned global access).  The row's last piece, when it holds one
+// or two elements (head dims 25, 50), is read element by element; when it holds more, with a 16-byte
+// load moved back so that it ends with the row, and the value shifted down, zeros coming in from above
+// (distance and shift are the same for every lane: D decides).  Nothing is read outside the row (what
+// follows the last row need not be mapped).  Rows shorter than 16 bytes are read element by element.
+typedef u32x4 __attribute__((aligned(2))) any_u32x4_a2;
+typedef u32x4 __attribute__((aligned(4))) any_u32x4_a4;
+typedef u32x2 __attribute__((aligned(2))) any_u32x2_a2;
+template <int ES>
+__device__ __forceinline__ u32x4 any_load_elems(const char* src, int n, int D) {
+  constexpr int EPC = 16 / ES;
+  typedef typename std::conditional<ES == 4, any_u32x4_a4, any_u32x4_a2>::type piece;
+  typedef typename std::conditional<ES == 4, unsigned, unsigned short>::type elem;
+  const elem* s = (const elem*)src;
+  u32x4 r = {0u, 0u, 0u, 0u};
+  if (D >= EPC) {
+    const int last = D % EPC;  // elements of the row's last piece (0: every piece is full)
+    if (n >= EPC) {
+      r = *(const piece*)src;
+    } else if (n > 0) {
+      if (last <= 2) {
+        const unsigned e0 = s[0], e1 = last > 1 ? (unsigned)s[1] : 0u;
+        if constexpr (ES == 4) { r.x = e0; r.y = e1; }
+        else r.x = e0 | (e1 << 16);
+      } else {
+        r = *(const piece*)(src - (EPC - last) * ES);
+        r = __builtin_bit_cast(u32x4, __builtin_bit_cast(unsigned __int128, r) >> ((EPC - last) * ES * 8));
+      }
+    }
+  } else {
+    unsigned e[EPC];
+#pragma unroll
+    for (int i = 0; i < EPC - 1; ++i) e[i] = n > i ? (unsigned)s[i] : 0u;
+    if constexpr (ES == 4) { r.x = e[0]; r.y = e[1]; r.z = e[2]; }
+    else { r.x = e[0] | (e[1] << 16); r.y = e[2] | (e[3] << 16); r.z = e[4] | (e[5] << 16); r.w = e[6]; }
+  }
+  return r;
+}
+
 // Two workgroups per CU where the registers allow it (a few spills included: one workgroup per CU
 // measured 20-35 % slower at these shapes).
 // HAS_RAB: with a bias table (an instantiation of its own: tested per pair the pointer costs seven scalar
 // instructions a score, and as a second set of tile bodies inside one kernel it costs registers).
-template <int MODE, int ELT, int DP, bool HAS_RAB>
+template <int MODE, int ELT, int DP, bool HAS_RAB, bool ALIGNED>
 __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 128) || DP <= 64)) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
   const Params& p = bp.f;
   constexpr bool F16 = ELT == ANY_F16;
@@ -133,6 +178,11 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
   const int rab_w = 2 * p.N - 1;
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
   const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // 16 bytes of a row of D elements from element d0 on (src points at that element); zeros past D
+  auto ld16 = [&](const char* src, int d0, int D) __attribute__((always_inline)) {
+    if constexpr (ALIGNED) return d0 < D ? *(const u32x4*)src : zero4;
+    else return any_load_elems<ES>(src, D - d0, D);
+  };
 
   const int xcd = blockIdx.x % NUM_XCD;
   const int list_len = p.ws_counts[xcd];
@@ -167,8 +217,8 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
       // bf16, fp16: elements 16 kk + 8 half .. + 7 (one MFMA step);  fp32: lane half h owns elements
       // h DP / 2 .. + DP / 2 - 1, four per register quad (one MFMA step each)
       const int d0 = F32 ? half * (DP / 2) + 4 * kk : kk * 16 + half * 8;
-      x1[kk] = (c_valid && d0 < p.Dqk) ? *(const u32x4*)(X1g + (size_t)(si.s + c) * rb1 + hb1 + (size_t)d0 * ES) : zero4;
-      if constexpr (HAS_DP) x2[kk] = (c_valid && d0 < p.Dv) ? *(const u32x4*)(X2g + (size_t)(si.s + c) * rb2 + hb2 + (size_t)d0 * ES) : zero4;
+      x1[kk] = c_valid ? ld16(X1g + (size_t)(si.s + c) * rb1 + hb1 + (size_t)d0 * ES, d0, p.Dqk) : zero4;
+      if constexpr (HAS_DP) x2[kk] = c_valid ? ld16(X2g + (size_t)(si.s + c) * rb2 + hb2 + (size_t)d0 * ES, d0, p.Dv) : zero4;
     }
 
     f32x16 acc1[HAS_DP ? NB : 1];  // DQ: dQ^T   DKV, DK: dK^T
@@ -253,8 +303,8 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
         const int idx = tid + 256 * i;
         const int row = idx / CPR, ch = idx % CPR;
         const int rr = min(r0 + row, si.n - 1);  // rows past the sequence re-read its last row; the mask drops them
-        st.y1[i] = ch * EPC < p.Dqk ? *(const u32x4*)(Y1g + (size_t)(si.s + rr) * rb1 + hb1 + (size_t)ch * 16) : zero4;
-        st.y2[i] = ch * EPC < p.Dv ? *(const u32x4*)(Y2g + (size_t)(si.s + rr) * rb2 + hb2 + (size_t)ch * 16) : zero4;
+        st.y1[i] = ld16(Y1g + (size_t)(si.s + rr) * rb1 + hb1 + (size_t)ch * 16, ch * EPC, p.Dqk);
+        st.y2[i] = ld16(Y2g + (size_t)(si.s + rr) * rb2 + hb2 + (size_t)ch * 16, ch * EPC, p.Dv);
       }
       st.bias = 0.f;
       if (HAS_RAB && tid < ANY_BM + ANY_BN - 1) {
@@ -489,7 +539,29 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
 #pragma unroll
           for (int rq = 0; rq < 4; ++rq) {
             const int d0 = db * 32 + 8 * rq + 4 * half;
-            if (d0 < D) {
+            if constexpr (!ALIGNED) {
+              // four elements at once where the row holds them, the row's last few one by one
+              if (d0 + 4 <= D) {
+                if constexpr (F32) {
+                  const u32x4 o = {__float_as_uint(acc[db][4 * rq + 0] * f), __float_as_uint(acc[db][4 * rq + 1] * f),
+                                   __float_as_uint(acc[db][4 * rq + 2] * f), __float_as_uint(acc[db][4 * rq + 3] * f)};
+                  *(any_u32x4_a4*)(orow + d0 * 4) = o;
+                } else {
+                  u32x2 o;
+                  o.x = any_pack2<F16>(acc[db][4 * rq + 0] * f, acc[db][4 * rq + 1] * f);
+                  o.y = any_pack2<F16>(acc[db][4 * rq + 2] * f, acc[db][4 * rq + 3] * f);
+                  *(any_u32x2_a2*)(orow + d0 * 2) = o;
+                }
+              } else {
+#pragma unroll
+                for (int e = 0; e < 3; ++e) {
+                  if (d0 + e < D) {
+                    if constexpr (F32) *(float*)(orow + (d0 + e) * 4) = acc[db][4 * rq + e] * f;
+                    else *(unsigned short*)(orow + (d0 + e) * 2) = (unsigned short)any_pack2<F16>(acc[db][4 * rq + e] * f, 0.f);
+                  }
+                }
+              }
+            } else if (d0 < D) {
               if constexpr (F32) {
                 const u32x4 o = {__float_as_uint(acc[db][4 * rq + 0] * f), __float_as_uint(acc[db][4 * rq + 1] * f),
                                  __float_as_uint(acc[db][4 * rq + 2] * f), __float_as_uint(acc[db][4 * rq + 3] * f)};
@@ -514,13 +586,14 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
 }
 
 // Launchers.  dtype: RECIR_HSTU_DTYPE_BF16, _FP16 or _FP32; dp: padded head dim (32, 64, 128 or 256).
-// Return false when the combination has no instantiation.  The instantiations with and without a bias
-// table live in two translation units (hstu_mfma_any.hip, hstu_mfma_any_rab.hip) that compile side by side.
-bool launch_mfma_any_fwd(int dtype, int dp, dim3 grid, hipStream_t stream, const Params& p);
-bool launch_mfma_any_bwd(int dtype, int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk);
-template <bool HAS_RAB>
+// aligned: every row of every tensor starts at a multiple of 16 bytes.  Return false when the combination
+// has no instantiation.  The instantiations with and without a bias table, for aligned rows and for
+// any, live in four translation units (hstu_mfma_any*.hip) that compile side by side.
+bool launch_mfma_any_fwd(int dtype, int dp, bool aligned, dim3 grid, hipStream_t stream, const Params& p);
+bool launch_mfma_any_bwd(int dtype, int dp, bool aligned, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk);
+template <bool HAS_RAB, bool ALIGNED>
 bool launch_mfma_any_fwd_as(int dtype, int dp, dim3 grid, hipStream_t stream, const BwdParams& bp);
-template <bool HAS_RAB>
+template <bool HAS_RAB, bool ALIGNED>
 bool launch_mfma_any_bwd_as(int dtype, int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq, const BwdParams& bk);
 
 }  // namespace recir_hstu

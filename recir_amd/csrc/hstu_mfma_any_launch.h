@@ -1,5 +1,6 @@
-// Launch code of the general MFMA kernels for one value of HAS_RAB; included by the two translation
-// units that hold the instantiations (HSTU_ANY_HAS_RAB defined to 0 or 1 before the include).
+// Launch code of the general MFMA kernels for one value of HAS_RAB and of ALIGNED; included by the four
+// translation units that hold the instantiations (HSTU_ANY_HAS_RAB and HSTU_ANY_ALIGNED defined to 0 or 1
+// before the include).
 #pragma once
 #include <cstring>
 
@@ -23,7 +24,7 @@ constexpr bool any_instantiated() {
 template <int MODE, int ELT, int DP>
 bool launch_one(dim3 grid, hipStream_t stream, const BwdParams& bp) {
   if constexpr (any_instantiated<MODE, ELT, DP>()) {
-    hipLaunchKernelGGL((hstu_mfma_any<MODE, ELT, DP, HSTU_ANY_HAS_RAB != 0>), grid, dim3(256), 0, stream, bp);
+    hipLaunchKernelGGL((hstu_mfma_any<MODE, ELT, DP, HSTU_ANY_HAS_RAB != 0, HSTU_ANY_ALIGNED != 0>), grid, dim3(256), 0, stream, bp);
     return true;
   }
   return false;
@@ -51,7 +52,7 @@ bool launch_bwd(int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdP
 }  // namespace
 
 template <>
-bool launch_mfma_any_fwd_as<HSTU_ANY_HAS_RAB != 0>(int dtype, int dp, dim3 grid, hipStream_t stream, const BwdParams& bp) {
+bool launch_mfma_any_fwd_as<HSTU_ANY_HAS_RAB != 0, HSTU_ANY_ALIGNED != 0>(int dtype, int dp, dim3 grid, hipStream_t stream, const BwdParams& bp) {
   if (dtype == RECIR_HSTU_DTYPE_FP16) return launch_mode<ANY_FWD, ANY_F16>(dp, grid, stream, bp);
   if (dtype == RECIR_HSTU_DTYPE_BF16) return launch_mode<ANY_FWD, ANY_BF16>(dp, grid, stream, bp);
   if (dtype == RECIR_HSTU_DTYPE_FP32) return launch_mode<ANY_FWD, ANY_F32>(dp, grid, stream, bp);
@@ -59,8 +60,8 @@ bool launch_mfma_any_fwd_as<HSTU_ANY_HAS_RAB != 0>(int dtype, int dp, dim3 grid,
 }
 
 template <>
-bool launch_mfma_any_bwd_as<HSTU_ANY_HAS_RAB != 0>(int dtype, int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream, const BwdParams& bq,
-                                                   const BwdParams& bk) {
+bool launch_mfma_any_bwd_as<HSTU_ANY_HAS_RAB != 0, HSTU_ANY_ALIGNED != 0>(int dtype, int dp, dim3 grid_q, dim3 grid_k, hipStream_t stream,
+                                                                             const BwdParams& bq, const BwdParams& bk) {
   if (dtype == RECIR_HSTU_DTYPE_FP16) return launch_bwd<ANY_F16>(dp, grid_q, grid_k, stream, bq, bk);
   if (dtype == RECIR_HSTU_DTYPE_BF16) return launch_bwd<ANY_BF16>(dp, grid_q, grid_k, stream, bq, bk);
   if (dtype == RECIR_HSTU_DTYPE_FP32) return launch_bwd<ANY_F32>(dp, grid_q, grid_k, stream, bq, bk);

@@ -40,16 +40,16 @@ class _CallState(threading.local):
 
 _state = _CallState()
 
-# What happens when a bf16 call can only run on the generic kernels (one wave per token and head, two orders
-# of magnitude slower than the MFMA kernels: head dims that are not multiples of 8 or exceed 256, unaligned
-# tensors): "warn" (once per process and reason), "error" (the C ABI rejects the call,
-# RECIR_HSTU_FLAG_TILED_ONLY) or "silent".  fp32 tensors (MFMA kernels at multiples of 4 up to 128) never warn.
+# What happens when a bf16 or fp16 call can only run on the generic kernels (one wave per token and head, two
+# orders of magnitude slower than the MFMA kernels: head dims above 256): "warn" (once per process and
+# reason), "error" (the C ABI rejects the call, RECIR_HSTU_FLAG_TILED_ONLY) or "silent".  fp32 tensors (MFMA
+# kernels up to head dim 128) never warn.
 _generic_policy = "warn"
 _generic_warned = set()
 
 
 def set_generic_kernel_policy(policy: str) -> str:
-    """Choose what a bf16 call that only the slow generic kernels cover does: ``"warn"`` (default),
+    """Choose what a bf16 or fp16 call that only the slow generic kernels cover does: ``"warn"`` (default),
     ``"error"`` or ``"silent"``.  Returns the previous setting."""
     global _generic_policy
     if policy not in ("warn", "error", "silent"):
@@ -63,12 +63,7 @@ def _note_generic(kernel: str, q, v, rab_grad=False) -> None:
         return
     if _state.forced_kernel == KERNEL_GENERIC:
         return
-    bwd = kernel.startswith("bwd_")
-    top = 256
-    if q.shape[2] % 8 or v.shape[2] % 8 or max(q.shape[2], v.shape[2]) > top:
-        reason = f"head dims {q.shape[2]} / {v.shape[2]} (the MFMA kernels take multiples of 8 up to {top})"
-    else:
-        reason = "tensors that are not 16-byte aligned"
+    reason = f"head dims {q.shape[2]} / {v.shape[2]} (the MFMA kernels take head dims up to 256)"
     if reason in _generic_warned:
         return
     _generic_warned.add(reason)
@@ -664,8 +659,7 @@ def jagged_hstu_attention(q, k, v, seq_offsets, num_targets=None, *, max_seq_len
     positions, and full causal attention for the rows from ``full_attn_size`` before the targets on.
     ``invalid_attn_mask_type`` other than ``"lower_triangular"`` selects, as in the reference operator
     (recir/ops/kjt_split_per_feature.cpp:650-660), the mask on absolute distances: positions at most
-    ``max_attn_len`` apart either way round, only the diagonal without a window.  That mask runs on
-    the generic kernels (any head dim, no MFMA).
+    ``max_attn_len`` apart either way round, only the diagonal without a window.
     """
     _check_common(q, k, v, seq_offsets, num_targets, max_seq_len)
     if alpha is None:

@@ -96,7 +96,7 @@ def history_lengths(config: int, seed: int = 0) -> np.ndarray:
     rng = np.random.Generator(np.random.PCG64(seed))
     if config == 1:
         return np.full((4,), 16, dtype=np.int64)
-    if config in (2, 3, 5, 6, 8, 9):
+    if config in (2, 3, 5, 6, 8, 9, 10):
         return rng.integers(256, 1985, size=32).astype(np.int64)
     if config == 4:
         return np.clip(rng.zipf(1.2, size=8), 128, 8064).astype(np.int64)
@@ -116,6 +116,7 @@ _SPEC = {
     7: (0, 4096, 4, 128, "bf16", 1.0 / 128),   # steady state of the tiled kernel: 16 x 4,096, no targets
     8: (64, 2048, 8, 64, "bf16", 1.0 / 64),    # config 2's sequences at head dim 64, 8 heads (general MFMA kernels)
     9: (64, 2048, 4, 128, "fp16", 1.0 / 128),  # config 2 in fp16 (general MFMA kernels)
+    10: (64, 2048, 8, 50, "bf16", 1.0 / 50),   # config 8 at head dim 50: rows of 100 bytes (general MFMA kernels for rows aligned to the element only)
 }
 
 

@@ -11,16 +11,20 @@ FP8_MAX_ABS = 5e-2
 FP32_RTOL, FP32_ATOL = 2e-4, 2e-6
 
 
-def expected_kernel(dqk, dv, dtype="bf16", *, causal=True, bwd=False, rab=False, alpha=1.0, rab_grad=False, fp8=False):
+def expected_kernel(dqk, dv, dtype="bf16", *, causal=True, bwd=False, rab=False, alpha=1.0, rab_grad=False, fp8=False,
+                    aligned=True):
     """Name of the kernel the library picks for a call (recir_hstu_last_kernel), from the rule in
-    include/recir_hstu.h: the head-dim-128 kernels, else the general MFMA kernels, else the generic ones."""
+    include/recir_hstu.h: the head-dim-128 kernels, else the general MFMA kernels (``_elems``: rows that do
+    not all start at multiples of 16 bytes), else the generic ones.
+    ``aligned``: every tensor of the call starts at a multiple of 16 bytes."""
     pre = "bwd_" if bwd else ""
-    if (dtype == "bf16" or fp8) and dqk == dv == 128 and causal and not (rab and alpha == 0):
+    if (dtype == "bf16" or fp8) and dqk == dv == 128 and causal and not (rab and alpha == 0) and aligned:
         return pre + "tiled_d128_" + ("fp8qk" if fp8 else "bf16") + ("_rab" if rab else "")
     d = max(dqk, dv)
-    per_chunk, top = (4, 128) if dtype == "fp32" else (8, 256)  # rows of 16-byte chunks; fp32 tiles are twice as wide
-    if dtype in ("bf16", "fp16", "fp32") and dqk % per_chunk == 0 and dv % per_chunk == 0 and d <= top:
-        return f"{pre}mfma_{dtype}_d{32 if d <= 32 else 64 if d <= 64 else 128 if d <= 128 else 256}"
+    per_chunk, top = (4, 128) if dtype == "fp32" else (8, 256)  # elements in 16 bytes; fp32 tiles are twice as wide
+    if dtype in ("bf16", "fp16", "fp32") and d <= top:
+        by_16 = aligned and dqk % per_chunk == 0 and dv % per_chunk == 0
+        return f"{pre}mfma_{dtype}_d{32 if d <= 32 else 64 if d <= 64 else 128 if d <= 128 else 256}{'' if by_16 else '_elems'}"
     return f"{pre}generic_{dtype}"
 
 

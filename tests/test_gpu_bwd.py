@@ -386,7 +386,7 @@ def test_randomized_cases_forward_and_backward(oracle, seed):
         assert_grads_close(got, want, int(wl.seq_offsets[-1]), BF16_REL, what)
 
 
-@pytest.mark.parametrize("case", ["tiled", "tiled_semilocal_per_token", "general_fp32", "generic_fp32", "config3"])
+@pytest.mark.parametrize("case", ["tiled", "tiled_semilocal_per_token", "general_fp32", "general_fp32_elems", "generic_fp32", "config3"])
 def test_gradient_of_the_bias_table(oracle, case):
     """d rab[h, m - j + N - 1] = sum of dS(m, j) (no counterpart in the reference, which has no bias;
     the oracle's form is pinned by torch autograd through a dense restatement).  Float atomics: the
@@ -403,8 +403,9 @@ def test_gradient_of_the_bias_table(oracle, case):
         wl = make_jagged([260, 100], [30, 0], 2, 128, 128, max_seq_len=300, alpha=1 / 128, dtype="bf16", seed=52,
                          with_rab=True, rab_std=0.5, max_attn_len=70, full_attn_size=40)
         scale = torch.rand(wl.T, generator=torch.Generator().manual_seed(3)) * 0.01 + 0.001
-    elif case in ("general_fp32", "generic_fp32"):  # head dims 16 / 24 on fp32 MFMAs; 18 / 22 (rows not multiples of 16 bytes) on the generic kernels
-        dqk, dv = (16, 24) if case == "general_fp32" else (18, 22)
+    elif case in ("general_fp32", "general_fp32_elems", "generic_fp32"):
+        # head dims 16 / 24 on fp32 MFMAs; 18 / 22 the same with rows that are not multiples of 16 bytes; above 128 the generic kernels
+        dqk, dv = {"general_fp32": (16, 24), "general_fp32_elems": (18, 22), "generic_fp32": (132, 130)}[case]
         wl = make_jagged([70, 0, 5, 33], [9, 0, 5, 1], 2, dqk, dv, max_seq_len=80, alpha=0.2, dtype="fp32", seed=53,
                          with_rab=True, rab_std=0.5, contextual_seq_len=2)
     else:
@@ -419,7 +420,7 @@ def test_gradient_of_the_bias_table(oracle, case):
     dq, dk, dv, drab = recir_amd.jagged_hstu_attention_backward(dout.to(q.device, q.dtype), q, k, v, off, nt, sc,
                                                                 rab_grad=True, **kw)
     torch.cuda.synchronize()
-    assert _lib.last_kernel().startswith({"general_fp32": "bwd_mfma_fp32_d32", "generic_fp32": "bwd_generic_fp32"}.get(case, "bwd_tiled_d128"))
+    assert _lib.last_kernel().startswith({"general_fp32": "bwd_mfma_fp32_d32", "general_fp32_elems": "bwd_mfma_fp32_d32_elems", "generic_fp32": "bwd_generic_fp32"}.get(case, "bwd_tiled_d128"))
     assert drab.shape == wl.rab.shape and drab.dtype == torch.float32
     want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
                            wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha,

@@ -1,6 +1,6 @@
-"""GPU parity of the general MFMA kernels (recir_amd/csrc/hstu_mfma_any.h): head dims other than 128,
-Dqk != Dv, fp16, the non-causal mask forms and a bias with alpha = 0, forward and backward, against the
-oracle on the same values.  The reference's operator takes any head dims, any float dtype and any mask
+"""GPU parity of the general MFMA kernels (recir_amd/csrc/hstu_mfma_any.h): head dims other than 128
+(rows of any length, tensors at any address), Dqk != Dv, fp16, the non-causal mask forms and a bias with
+alpha = 0, forward and backward, against the oracle on the same values.  The reference's operator takes any head dims, any float dtype and any mask
 string (recir/ops/kjt_split_per_feature.cpp:602-693); its accelerator kernel leaves Dv free
 (recir/ops/pallas/jagged_hstu_attention.py:1498-1503)."""
 import numpy as np
@@ -24,8 +24,10 @@ def oracle():
 LENGTHS = [300, 129, 64, 1, 0, 517, 33]
 TARGETS = [40, 129, 0, 0, 0, 6, 50]
 
-# (Dqk, Dv): multiples of 8; the padded tile is the next of 32, 64, 128, 256 of the larger one
-DIMS = [(64, 64), (32, 32), (8, 8), (24, 40), (96, 96), (64, 128), (128, 64), (256, 256), (200, 72), (136, 128)]
+# (Dqk, Dv): the padded tile is the next of 32, 64, 128, 256 of the larger one; rows that are not multiples
+# of 16 bytes (the last five) run on the instantiations for rows aligned to the element only
+DIMS = [(64, 64), (32, 32), (8, 8), (24, 40), (96, 96), (64, 128), (128, 64), (256, 256), (200, 72), (136, 128),
+        (25, 25), (50, 30), (7, 3), (129, 64), (250, 255)]
 # (mask_type, max_attn_len, full_attn_size, contextual_seq_len)
 MASKS = {
     "causal": ("lower_triangular", 0, 0, 0),
@@ -67,10 +69,12 @@ def _assert_close(out, ref, tol, what):
     assert (row_err <= tol * (row_ref + st["row_floor"]) + FP16_QUANTUM).all(), (what, st)
 
 
-def _expected_kernel(dtype, dqk, dv, bwd=False):
+def _expected_kernel(dtype, dqk, dv, bwd=False, aligned=True):
     d = max(dqk, dv)
     dp = 32 if d <= 32 else 64 if d <= 64 else 128 if d <= 128 else 256
-    return f"{'bwd_' if bwd else ''}mfma_{dtype}_d{dp}"
+    per_16 = 4 if dtype == "fp32" else 8
+    elems = "" if (aligned and dqk % per_16 == 0 and dv % per_16 == 0) else "_elems"
+    return f"{'bwd_' if bwd else ''}mfma_{dtype}_d{dp}{elems}"
 
 
 @pytest.mark.parametrize("dims", DIMS, ids=lambda d: f"{d[0]}x{d[1]}")
@@ -106,10 +110,12 @@ def test_forward_masks(oracle, mask, dtype, dims):
 
 
 @pytest.mark.parametrize("mask", ["causal_ctx", "semilocal", "noncausal_window"])
-@pytest.mark.parametrize("dims", [(32, 32), (64, 64), (128, 128), (20, 12), (128, 64), (36, 100)], ids=lambda d: f"{d[0]}x{d[1]}")
+@pytest.mark.parametrize("dims", [(32, 32), (64, 64), (128, 128), (20, 12), (128, 64), (36, 100), (18, 22), (5, 127)],
+                         ids=lambda d: f"{d[0]}x{d[1]}")
 def test_fp32_forward_and_backward(oracle, dims, mask):
-    """fp32 tensors on v_mfma_f32_32x32x2_f32 (head dims that are multiples of 4 up to 128): the fp32 tolerances of
-    the generic kernel's tests, forward element-wise and backward on the three relative bounds."""
+    """fp32 tensors on v_mfma_f32_32x32x2_f32 (head dims up to 128; the last two with rows that are not multiples of
+    16 bytes): the fp32 tolerances of the generic kernel's tests, forward element-wise and backward on the three
+    relative bounds."""
     from recir_amd import _lib
     from tests.test_gpu_bwd import BWD_FP32_TOL, assert_grads_close
 
@@ -151,11 +157,12 @@ def test_bias_with_alpha_zero(oracle):
     _assert_close(out, run_oracle(oracle, wl), BF16_REL, "alpha 0")
 
 
-def _backward_reference(oracle, wl, dout, scale):
+def _backward_reference(oracle, wl, dout, scale, rab_grad=False):
     return oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
                            wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha, attn_scale=_scale_np(scale),
                            rab=None if wl.rab is None else wl.rab.numpy(), contextual_seq_len=wl.contextual_seq_len,
-                           max_attn_len=wl.max_attn_len, full_attn_size=wl.full_attn_size, mask_type=wl.mask_type)
+                           max_attn_len=wl.max_attn_len, full_attn_size=wl.full_attn_size, mask_type=wl.mask_type,
+                           **({"rab_grad": True} if rab_grad else {}))
 
 
 def _assert_grads(got, want, end, tol, what):
@@ -279,21 +286,109 @@ def test_general_and_head_dim_128_kernels_agree_at_full_size(oracle):
         assert st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL, (name, st)
 
 
+def test_tensors_that_start_between_16_byte_multiples(oracle):
+    """Contiguous tensors whose first element sits 2 bytes (bf16) or 4 bytes (fp32) past a 16-byte multiple, at
+    head dim 128 (not the head-dim-128 kernels' then) and at 64 / 40: the general kernels read such rows in
+    pieces aligned to the element only.  Forward and backward, with a bias, its gradient and a per-token scale."""
+    import recir_amd
+    from recir_amd import _lib
+    from tests.test_gpu_bwd import BWD_FP32_TOL, assert_grads_close
+
+    def shifted(t, dt):  # a contiguous tensor of t's values that starts one element past an aligned address
+        buf = torch.full((t.numel() + 9,), 7.0, dtype=dt, device="cuda")
+        buf[1:1 + t.numel()] = t.reshape(-1).to("cuda", dt)
+        return buf, buf[1:1 + t.numel()].view(t.shape)
+
+    for dtype, dqk, dv in (("bf16", 128, 128), ("bf16", 64, 40), ("fp32", 32, 32)):
+        dt = torch.bfloat16 if dtype == "bf16" else torch.float32
+        wl = _workload(dqk, dv, dtype, "semilocal_ctx", seed=77, with_rab=True)
+        g = torch.Generator().manual_seed(9)
+        scale = (0.5 + torch.rand(wl.T, generator=g)) / 50
+        dout = torch.randn(wl.T, wl.H, dv, generator=g).to(dt).float()
+        (_, q), (_, k), (_, v), (_, do) = (shifted(t, dt) for t in (wl.q, wl.k, wl.v, dout))
+        assert q.data_ptr() % 16 == dt.itemsize and q.is_contiguous()
+        off, nt, rab, sc = wl.seq_offsets.cuda(), wl.num_targets.cuda(), wl.rab.cuda(), scale.cuda()
+        kw = dict(max_seq_len=wl.max_seq_len, alpha=wl.alpha, contextual_seq_len=wl.contextual_seq_len, rab=rab,
+                  max_attn_len=wl.max_attn_len, full_attn_size=wl.full_attn_size)
+        out = recir_amd.jagged_hstu_attention(q, k, v, off, nt, attn_scale=sc, **kw)
+        assert _lib.last_kernel() == _expected_kernel(dtype, dqk, dv, aligned=False), _lib.last_kernel()
+        ref = run_oracle(oracle, wl, attn_scale=scale)
+        if dtype == "bf16":
+            _assert_close(out, ref, BF16_REL, f"shifted {dtype} {dqk}x{dv}")
+        else:
+            np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=2e-4, atol=2e-6)
+        got = recir_amd.jagged_hstu_attention_backward(do, q, k, v, off, nt, sc, rab_grad=True, **kw)
+        assert _lib.last_kernel() == _expected_kernel(dtype, dqk, dv, bwd=True, aligned=False), _lib.last_kernel()
+        want = _backward_reference(oracle, wl, dout, scale, rab_grad=True)
+        end = int(wl.seq_offsets[-1])
+        assert_grads_close([t.float().cpu() for t in got[:3]], want[:3], end, BF16_REL if dtype == "bf16" else BWD_FP32_TOL,
+                           f"shifted {dtype} {dqk}x{dv} backward")
+        st = error_stats(got[3], want[3])
+        assert st["rel_to_max"] <= (BF16_REL if dtype == "bf16" else 2e-4), st
+
+
+def test_outputs_between_16_byte_multiples_leave_their_surroundings_alone():
+    """The C ABI with every tensor one element past a 16-byte multiple and head dims 25 / 50: the elements
+    before and after each output stay as they were (forward and backward write whole rows, nothing else)."""
+    import ctypes
+
+    from recir_amd import _lib
+    from recir_amd.workloads import make_jagged
+
+    lib = _lib.load()
+    wl = make_jagged([130, 64, 7], [9, 0, 7], 2, 25, 50, max_seq_len=130, alpha=0.2, dtype="bf16", seed=5, tail_rows=3)
+    dev = torch.device("cuda:0")
+
+    def shifted(shape, values=None):
+        n = int(np.prod(shape))
+        buf = torch.full((n + 16,), 7.0, dtype=torch.bfloat16, device=dev)
+        view = buf[1:1 + n].view(shape)
+        if values is not None:
+            view.copy_(values.to(dev, torch.bfloat16))
+        return buf, view
+
+    T, H, Dqk = wl.q.shape
+    Dv = wl.v.shape[2]
+    (_, q), (_, k), (_, v) = shifted(wl.q.shape, wl.q), shifted(wl.k.shape, wl.k), shifted(wl.v.shape, wl.v)
+    _, dout = shifted(wl.v.shape, torch.randn(wl.v.shape, generator=torch.Generator().manual_seed(2)))
+    (ob, out), (qb, dq), (kb, dk), (vb, dv) = shifted(wl.v.shape), shifted(wl.q.shape), shifted(wl.k.shape), shifted(wl.v.shape)
+    off, nt = wl.seq_offsets.to(dev), wl.num_targets.to(dev)
+    ws = torch.empty(lib.recir_hstu_attn_bwd_workspace_bytes(T, wl.B, H, Dqk, Dv, _lib.DTYPE_BF16), dtype=torch.uint8, device=dev)
+    ptr = lambda t: ctypes.c_void_p(0 if t is None else t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    tail = (wl.max_seq_len, 0, 0, 0, wl.alpha, _lib.DTYPE_BF16, 0)
+    rc = lib.recir_hstu_attn_fwd(ptr(q), ptr(k), ptr(v), ptr(out), ptr(off), ptr(nt), None, None, None, None, T, wl.B, H, Dqk, Dv,
+                                 *tail, ptr(ws), ws.numel(), stream)
+    assert rc == 0, lib.recir_hstu_last_error().decode()
+    assert _lib.last_kernel() == "mfma_bf16_d64_elems"
+    rc = lib.recir_hstu_attn_bwd(ptr(dout), ptr(q), ptr(k), ptr(v), ptr(dq), ptr(dk), ptr(dv), None, ptr(off), ptr(nt), None, None,
+                                 T, wl.B, H, Dqk, Dv, *tail, ptr(ws), ws.numel(), stream)
+    assert rc == 0, lib.recir_hstu_last_error().decode()
+    assert _lib.last_kernel() == "bwd_mfma_bf16_d64_elems"
+    torch.cuda.synchronize()
+    for name, buf, view in (("out", ob, out), ("dq", qb, dq), ("dk", kb, dk), ("dv", vb, dv)):
+        n = view.numel()
+        assert (buf[:1] == 7.0).all() and (buf[1 + n:] == 7.0).all(), name
+        end = int(wl.seq_offsets[-1])
+        assert not view[end:].float().abs().sum().item(), name  # the rows behind the last sequence are zero
+        assert (view[:end].float() != 7.0).any(), name
+
+
 def test_what_still_runs_on_the_generic_kernels():
-    """Head dims whose rows are not multiples of 16 bytes."""
+    """Head dims above 256."""
     import recir_amd
     from recir_amd import _lib
     from recir_amd.workloads import make_jagged
 
     prev = recir_amd.set_generic_kernel_policy("silent")
     try:
-        wl = make_jagged([50, 20], [5, 0], 2, 20, 12, max_seq_len=64, alpha=0.2, dtype="bf16", seed=1)
+        wl = make_jagged([50, 20], [5, 0], 2, 264, 260, max_seq_len=64, alpha=0.05, dtype="bf16", seed=1)
         run_hip(wl)
         assert _lib.last_kernel() == "generic_bf16"
         q, k, v, off, nt = to_device(wl)
-        recir_amd.jagged_hstu_attention_backward(torch.ones_like(v), q, k, v, off, nt, max_seq_len=64, alpha=0.2)
+        recir_amd.jagged_hstu_attention_backward(torch.ones_like(v), q, k, v, off, nt, max_seq_len=64, alpha=0.05)
         assert _lib.last_kernel() == "bwd_generic_bf16"
-        wl = make_jagged([50, 20], [5, 0], 2, 20, 12, max_seq_len=64, alpha=0.2, dtype="fp16", seed=1)
+        wl = make_jagged([50, 20], [5, 0], 2, 264, 260, max_seq_len=64, alpha=0.05, dtype="fp16", seed=1)
         out = run_hip(wl)
         assert _lib.last_kernel() == "generic_fp16" and out.dtype == torch.float16
         from oracle import hstu_oracle

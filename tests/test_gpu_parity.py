@@ -226,17 +226,31 @@ def test_scalar_and_per_token_scale_tiled(oracle):
     assert_bf16_close(run_hip(wl, attn_scale=0.5), run_oracle(oracle, wl, attn_scale=0.5), "float scale")
 
 
+@pytest.mark.parametrize("generic", [False, True], ids=["default_kernel", "generic_kernel"])
 @pytest.mark.parametrize("shape", [(2, 8, 6), (3, 64, 64), (1, 128, 32), (2, 40, 200)])
-def test_generic_kernel_head_dims(oracle, shape):
+def test_other_head_dims(oracle, shape, generic):
+    """Head dims other than 128, fp32 and bf16, on the kernel the library picks (the general MFMA kernels) and
+    on the generic one."""
+    import contextlib
+
+    from recir_amd import _lib, ops
     from recir_amd.workloads import make_jagged
 
     H, Dqk, Dv = shape
     wl = make_jagged([70, 0, 5, 129], [9, 0, 5, 1], H, Dqk, Dv, max_seq_len=130, alpha=0.11, seed=8,
                      with_rab=True, rab_std=0.3, contextual_seq_len=2, tail_rows=2)
-    out = run_hip(wl)
     ref = run_oracle(oracle, wl)
+    with (ops.force_kernel(ops.KERNEL_GENERIC) if generic else contextlib.nullcontext()):
+        out = run_hip(wl)
+        k32 = _lib.last_kernel()
+        outb = run_hip(wl, dtype="bf16")
+        k16 = _lib.last_kernel()
+    if generic:
+        assert (k32, k16) == ("generic_fp32", "generic_bf16")
+    else:
+        # (fp32 tiles stop at head dim 128: 40 / 200 is the generic kernel's)
+        assert k32 == expected_kernel(Dqk, Dv, "fp32", rab=True) and k16 == expected_kernel(Dqk, Dv, "bf16", rab=True)
     np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=FP32_RTOL, atol=FP32_ATOL)
-    outb = run_hip(wl, dtype="bf16")
     wlb_ref = run_oracle(oracle, wl, q=wl.q.bfloat16().float(), k=wl.k.bfloat16().float())
     st = error_stats(outb, wlb_ref)
     assert st["rel_to_max"] <= 3e-2, st  # v is also rounded to bf16 here
@@ -269,19 +283,28 @@ def test_alpha_default_is_inverse_sqrt_of_head_dim(oracle, D, dtype):
     assert np.abs(other - ref).max() > 10 * (BF16_REL if dtype == "bf16" else FP32_RTOL) * np.abs(ref).max()
 
 
-def test_many_short_sequences_use_the_general_work_list(oracle):
-    """More sequences than the single-block work-list builder tabulates (1024)."""
+@pytest.mark.parametrize("D", [128, 64])
+def test_many_short_sequences_use_the_general_work_list(oracle, D):
+    """More sequences than the single-block work-list builder tabulates (1024): both MFMA kernel
+    families, forward and backward."""
     from recir_amd import _lib
     from recir_amd.workloads import make_jagged
+    from tests.test_gpu_bwd import assert_grads_close, run_hip_bwd
 
     rng = np.random.default_rng(5)
     lengths = rng.integers(0, 40, size=1300)
     lengths[7] = 300
     targets = np.minimum(rng.integers(0, 4, size=1300), lengths)
-    wl = make_jagged(lengths, targets, 2, 128, 128, max_seq_len=320, alpha=1 / 128, dtype="bf16", seed=11)
+    wl = make_jagged(lengths, targets, 2, D, D, max_seq_len=320, alpha=1 / D, dtype="bf16", seed=11)
     out = run_hip(wl)
-    assert _lib.last_kernel().startswith("tiled_d128")
-    assert_bf16_close(out, run_oracle(oracle, wl), "B=1300")
+    assert _lib.last_kernel() == expected_kernel(D, D)
+    assert_bf16_close(out, run_oracle(oracle, wl), f"B=1300 D={D}")
+    dout = torch.randn(wl.T, wl.H, D, generator=torch.Generator().manual_seed(6)).bfloat16().float()
+    got = run_hip_bwd(wl, dout)
+    assert _lib.last_kernel() == expected_kernel(D, D, bwd=True)
+    want = oracle.attn_bwd(dout.numpy(), wl.q.numpy(), wl.k.numpy(), wl.v.numpy(), wl.seq_offsets.numpy(),
+                           wl.num_targets.numpy(), max_seq_len=wl.max_seq_len, alpha=wl.alpha)
+    assert_grads_close(got, want[:3], int(wl.seq_offsets[-1]), BF16_REL, f"B=1300 D={D} backward")
 
 
 @pytest.mark.parametrize("lengths", [[1500] + [70] * 30, [300] * 16, [700]], ids=["one_long", "even", "single"])
@@ -298,8 +321,9 @@ def test_work_list_dealing_by_tiles_and_by_pairs(oracle, lengths):
 @pytest.mark.parametrize("D,with_rab", [(128, False), (128, True), (64, False), (64, True)])
 def test_sequences_longer_than_max_seq_len_do_not_break_the_work_list(oracle, D, with_rab):
     """Out of contract (n > max_seq_len), but the launch must stay in bounds: the work lists are
-    then longer than the grid assumes and the workgroups loop over them; the index into a bias table
-    is clamped to the table.  Head dim 128 and the general MFMA kernels, forward and backward."""
+    then longer than the grid assumes and the workgroups loop over them; a pair whose diagonal lies
+    outside the bias table has no bias, as in the oracle.  Head dim 128 and the general MFMA kernels,
+    forward and backward."""
     from recir_amd import _lib
     from recir_amd.workloads import make_jagged
     from tests.test_gpu_bwd import _scale_np, assert_grads_close, run_hip_bwd
@@ -595,7 +619,7 @@ def test_fp8_region_swap_keeps_the_reference_contextual_rule(oracle):
 
 
 def test_generic_kernel_policy_warns_or_rejects(oracle):
-    """A bf16 call that only the slow generic kernels cover (here: head dims 20 / 12) says so once by default,
+    """A bf16 call that only the slow generic kernels cover (here: head dims 264 / 260) says so once by default,
     is rejected by the C ABI under the 'error' policy (RECIR_HSTU_FLAG_TILED_ONLY), and is silent under
     'silent'; the result is the oracle's in every case that runs.  fp32 calls never warn."""
     import warnings
@@ -604,7 +628,7 @@ def test_generic_kernel_policy_warns_or_rejects(oracle):
     from recir_amd import _lib, ops
     from recir_amd.workloads import make_jagged
 
-    wl = make_jagged([70, 33, 0, 129], [8, 33, 0, 3], 2, 20, 12, max_seq_len=160, alpha=1.0 / 20, dtype="bf16", seed=41)
+    wl = make_jagged([70, 33, 0, 129], [8, 33, 0, 3], 2, 264, 260, max_seq_len=160, alpha=1.0 / 264, dtype="bf16", seed=41)
     want = run_oracle(oracle, wl)
     ops._generic_warned.clear()
     prev = recir_amd.set_generic_kernel_policy("warn")
@@ -615,8 +639,8 @@ def test_generic_kernel_policy_warns_or_rejects(oracle):
             out2 = run_hip(wl)
         assert _lib.last_kernel() == "generic_bf16"
         msgs = [str(w.message) for w in rec if issubclass(w.category, RuntimeWarning)]
-        assert len(msgs) == 1 and "head dims 20 / 12" in msgs[0], msgs  # once per reason
-        assert_bf16_close(out, want, "generic kernel, head dims 20 / 12")
+        assert len(msgs) == 1 and "head dims 264 / 260" in msgs[0], msgs  # once per reason
+        assert_bf16_close(out, want, "generic kernel, head dims 264 / 260")
         assert torch.equal(out, out2)
         recir_amd.set_generic_kernel_policy("error")
         with pytest.raises(ValueError, match="only the generic kernel"):
