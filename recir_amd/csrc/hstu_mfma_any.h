@@ -3,7 +3,7 @@
 // or fp32 values; tensors at any address their element type allows; every mask the operator knows (causal with targets
 // and contextual prefix, semi-local, the non-causal forms); a bias with any alpha, and the gradient of
 // the bias table.  One template, five modes; nothing here is hand-scheduled: the point is to keep such
-// calls on the matrix cores (about twice the time of the head-dim-128 kernels at their own shape)
+// calls on the matrix cores (1.5 to 1.8 times the time of the head-dim-128 kernels at their own shape)
 // instead of on the one-wave-per-token kernels (two orders of magnitude slower).
 //
 // A workgroup (4 waves) owns 128 "stationary" rows of one (sequence, head), 32 per wave, one per lane
@@ -141,6 +141,13 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
   constexpr int CPR = DP * ES / 16; // 16-byte chunks per tile row
   constexpr int NCH = DP * ES / 64; // chunks of one tile that one thread stages
   constexpr int EPC = 16 / ES;      // elements per chunk
+  // The accumulating products stand once, behind the three kinds of tile body, instead of inside each:
+  // as the results of several bodies the accumulators were copied once a tile (8-14 % of the time where
+  // they are few); where they are many the packed P and dS kept across the bodies' end cost more in spills.
+  // Forward without a bias in bf16 or fp32: P / alpha = s sigmoid(alpha s) goes into the second product and
+  // alpha onto the output rows (one multiplication less per score; not in fp16, whose range P / alpha could leave)
+  constexpr bool FOLD_ALPHA = MODE == ANY_FWD && !HAS_RAB && !F16;
+  constexpr bool ACC_APART = (MODE == ANY_FWD && DP <= 128) || DP <= 64;
   static_assert(DP == 32 || DP == 64 || DP == 128 || DP == 256, "padded head dim");
   static_assert(!F32 || DP <= 128, "fp32 tiles of 256 columns do not fit the LDS");
   __shared__ __attribute__((aligned(16))) unsigned char Y1s[2][ANY_BN * RS];
@@ -154,7 +161,7 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (a scalar: what depends on the wave alone then branches without lane masks)
   const int l32 = lane & 31;
   const int half = lane >> 5;
   // row fragment (A operand, 32 rows x 16 elements): lane reads row l32 (+ 32 blk), elements 16 kk + 8 half .. + 7
@@ -175,6 +182,7 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
   const bool per_token = p.attn_scale && (p.flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
   const bool semi = p.max_attn_len > 0;
   const float neg_log2e = -kAnyLog2e;
+  const float neg_alpha_log2e = -kAnyLog2e * p.alpha;
   const int rab_w = 2 * p.N - 1;
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
   const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -353,8 +361,16 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[e]), __uint_as_float(x[kk][e]), (kk == 0 && e == 0) ? zero16 : acc, 0, 0, 0);
         }
       } else {
+        // fragments read ahead in groups of up to eight (left in one loop the compiler reads and waits one at a time)
+        constexpr int G = NK < 8 ? NK : 8;
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) acc = any_mfma<F16>(row_frag(y, blk, kk), x[kk], kk == 0 ? zero16 : acc);
+        for (int k0 = 0; k0 < NK; k0 += G) {
+          u32x4 a[G];
+#pragma unroll
+          for (int kk = 0; kk < G; ++kk) a[kk] = row_frag(y, blk, k0 + kk);
+#pragma unroll
+          for (int kk = 0; kk < G; ++kk) acc = any_mfma<F16>(a[kk], x[k0 + kk], (k0 + kk) == 0 ? zero16 : acc);
+        }
       }
       return acc;
     };
@@ -362,11 +378,33 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
     // MASKED: 0 every pair kept, 1 the causal / semi-local predicate per pair, 2 the non-causal one.
     // The predicates are written with bitwise operators on 0 / 1 values: the short-circuit forms of
     // hstu_common.h compile to a divergent branch per pair here.
-    auto tile_body = [&](auto masked_tag, int r0, int buf) __attribute__((always_inline)) {
+    // P and dS of a tile, packed as the B operands of the accumulating products (bf16, fp16; fp32 feeds
+    // its accumulating products from the score registers inside tile_body)
+    struct Packed {
+      unsigned pw[2][8], dsw[HAS_DP ? 2 : 1][8];
+    };
+    // accumulating products of a tile (bf16, fp16): step s2 covers streamed rows 16 s2 .. + 15 = registers
+    // 8 (s2 & 1) .. + 7 of block s2 >> 1
+    auto accumulate = [&](int buf, const Packed& pk) __attribute__((always_inline)) {
+      const unsigned char* y1 = &Y1s[buf][0];
+      const unsigned char* y2 = &Y2s[buf][0];
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const int blk = s2 >> 1, w0 = 4 * (s2 & 1);
+        const u32x4 pb = {pk.pw[blk][w0], pk.pw[blk][w0 + 1], pk.pw[blk][w0 + 2], pk.pw[blk][w0 + 3]};
+        u32x4 db_ = zero4;
+        if constexpr (HAS_DP) db_ = (u32x4){pk.dsw[blk][w0], pk.dsw[blk][w0 + 1], pk.dsw[blk][w0 + 2], pk.dsw[blk][w0 + 3]};
+#pragma unroll
+        for (int db = 0; db < NB; ++db) {
+          if constexpr (HAS_P) acc2[db] = any_mfma<F16>(tr_frag(y2, db, s2), pb, acc2[db]);
+          if constexpr (HAS_DP) acc1[db] = any_mfma<F16>(tr_frag(y1, db, s2), db_, acc1[db]);
+        }
+      }
+    };
+    auto tile_body = [&](auto masked_tag, int r0, int buf, Packed& pk) __attribute__((always_inline)) {
       constexpr int MASKED = decltype(masked_tag)::value;
       const unsigned char* y1 = &Y1s[buf][0];
       const unsigned char* y2 = &Y2s[buf][0];
-      unsigned pw[2][8], dsw[HAS_DP ? 2 : 1][8];
       // first streamed row of this lane half; opaque, so that the rows of the 32 registers are derived
       // from it inside the tile instead of being kept in 32 registers across the loop
       int rbase = r0 + 4 * half;
@@ -377,16 +415,22 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
         f32x16 Sb = row_product(y1, blk, x1), dPb;
         if constexpr (HAS_DP) dPb = row_product(y2, blk, x2);
         float pv[16], dsv[HAS_DP ? 16 : 1];
+        // (the per-token scale of the key-stationary modes, and the bias table's gradient of the dQ mode, as
+        // a compile-time tag of the loop: tested per score they put a branch behind every score, and nothing
+        // was scheduled across them)
+        auto score_loop = [&](auto tag) __attribute__((always_inline)) {
+        constexpr bool ROW_SCALES = KEYS && decltype(tag)::value;
+        constexpr bool WITH_DRAB = MODE == ANY_DQ && decltype(tag)::value;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int rl = 32 * blk + 8 * (r >> 2) + 4 * half + (r & 3);  // streamed row of this register
-          float x = Sb[r] * p.alpha;
+          float x = FOLD_ALPHA ? Sb[r] : Sb[r] * p.alpha;
           if constexpr (HAS_RAB) x += bias_s[buf][KEYS ? rl - (c - c0) + (ANY_BM - 1) : (c - c0) - rl + (ANY_BN - 1)];
-          const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * neg_log2e));
+          const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * (FOLD_ALPHA ? neg_alpha_log2e : neg_log2e)));
           float pe = x * sig;
           float de = 0.f;
           if constexpr (HAS_DP) de = dPb[r] * (sig + pe * (1.0f - sig));  // silu'(x) = sig (1 + x (1 - sig))
-          if (KEYS && per_token) {
+          if constexpr (ROW_SCALES) {
             const float rs = scale_s[buf][rl];
             pe *= rs;
             de *= rs;
@@ -410,13 +454,17 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
           }
           pv[r] = pe;
           if constexpr (HAS_DP) dsv[r] = de;
-          if constexpr (MODE == ANY_DQ) {
+          if constexpr (WITH_DRAB) {
             // d score / d bias = 1: the pair's dS (with its row's scale) goes to its diagonal
-            if (drabg && de != 0.f) atomicAdd(&dband_s[buf][(c - c0) - rl + (ANY_BN - 1)], de * dscale);
+            if (de != 0.f) atomicAdd(&dband_s[buf][(c - c0) - rl + (ANY_BN - 1)], de * dscale);
           }
           // the masked bodies four pairs at a time: left to itself the scheduler interleaves all 32 and spills
           if (MASKED && (r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
+        };
+        constexpr bool TAGGED = KEYS || (MODE == ANY_DQ && HAS_RAB);
+        if (TAGGED && (KEYS ? per_token : drabg != nullptr)) score_loop(std::true_type{});
+        else score_loop(std::false_type{});
         if constexpr (F32) {
           // accumulating products of this block, one streamed row per lane half and step: register r of
           // the score block is the B operand as it is; the A operand is column 32 db + l32 of that row
@@ -434,27 +482,13 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
         } else {
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            pw[blk][i] = any_pack2<F16>(pv[2 * i], pv[2 * i + 1]);
-            if constexpr (HAS_DP) dsw[blk][i] = any_pack2<F16>(dsv[2 * i], dsv[2 * i + 1]);
+            pk.pw[blk][i] = any_pack2<F16>(pv[2 * i], pv[2 * i + 1]);
+            if constexpr (HAS_DP) pk.dsw[blk][i] = any_pack2<F16>(dsv[2 * i], dsv[2 * i + 1]);
           }
         }
       }
-      if constexpr (F32) return;
-      // accumulating products: step s2 covers streamed rows 16 s2 .. + 15 = registers 8 (s2 & 1) .. + 7 of block s2 >> 1
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        const int blk = s2 >> 1, w0 = 4 * (s2 & 1);
-        const u32x4 pb = {pw[blk][w0], pw[blk][w0 + 1], pw[blk][w0 + 2], pw[blk][w0 + 3]};
-        u32x4 db_ = zero4;
-        if constexpr (HAS_DP) db_ = (u32x4){dsw[blk][w0], dsw[blk][w0 + 1], dsw[blk][w0 + 2], dsw[blk][w0 + 3]};
-#pragma unroll
-        for (int db = 0; db < NB; ++db) {
-          if constexpr (HAS_P) acc2[db] = any_mfma<F16>(tr_frag(y2, db, s2), pb, acc2[db]);
-          if constexpr (HAS_DP) acc1[db] = any_mfma<F16>(tr_frag(y1, db, s2), db_, acc1[db]);
-        }
-      }
+      if constexpr (!F32 && !ACC_APART) accumulate(buf, pk);
     };
-
     // wave-level classification of a block: skipped, every pair kept, or the predicate per pair
     auto compute_tile = [&](int t, int buf) __attribute__((always_inline)) {
       if (!wave_has_rows) return;
@@ -481,9 +515,11 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
         // every pair kept: the two id ranges lie within the window of each other all along
         full = si.win != WIN_ALL && id_hi - idj_lo <= si.win && idj_hi - id_lo <= si.win && r1 <= si.n;
       }
-      if (full) tile_body(std::integral_constant<int, 0>{}, r0, buf);
-      else if (!noncausal) tile_body(std::integral_constant<int, 1>{}, r0, buf);
-      else tile_body(std::integral_constant<int, 2>{}, r0, buf);
+      Packed pk;
+      if (full) tile_body(std::integral_constant<int, 0>{}, r0, buf, pk);
+      else if (!noncausal) tile_body(std::integral_constant<int, 1>{}, r0, buf, pk);
+      else tile_body(std::integral_constant<int, 2>{}, r0, buf, pk);
+      if constexpr (!F32 && ACC_APART) accumulate(buf, pk);
     };
 
     // band of tile `tile` (LDS stage b) -> the head's row of the table, and the stage cleared for the
@@ -576,7 +612,7 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
           }
         }
       };
-      if constexpr (MODE == ANY_FWD) store_rows(p.out, p.Dv, acc2, col_scale);
+      if constexpr (MODE == ANY_FWD) store_rows(p.out, p.Dv, acc2, FOLD_ALPHA ? col_scale * p.alpha : col_scale);
       if constexpr (MODE == ANY_DQ) store_rows(bp.dq, p.Dqk, acc1, col_scale * p.alpha);
       if constexpr (KEYS && HAS_DP) store_rows(bp.dk, p.Dqk, acc1, col_scale * p.alpha);
       if constexpr (KEYS && HAS_P) store_rows(bp.dv, p.Dv, acc2, col_scale);
