@@ -3,7 +3,7 @@
 // or fp32 values; tensors at any address their element type allows; every mask the operator knows (causal with targets
 // and contextual prefix, semi-local, the non-causal forms); a bias with any alpha, and the gradient of
 // the bias table.  One template, five modes; nothing here is hand-scheduled: the point is to keep such
-// calls on the matrix cores (1.5 to 1.8 times the time of the head-dim-128 kernels at their own shape)
+// calls on the matrix cores (1.4 to 1.7 times the time of the head-dim-128 kernels at their own shape)
 // instead of on the one-wave-per-token kernels (two orders of magnitude slower).
 //
 // A workgroup (4 waves) owns 128 "stationary" rows of one (sequence, head), 32 per wave, one per lane
@@ -127,7 +127,7 @@ __device__ __forceinline__ u32x4 any_load_elems(const char* src, int n, int D) {
 // HAS_RAB: with a bias table (an instantiation of its own: tested per pair the pointer costs seven scalar
 // instructions a score, and as a second set of tile bodies inside one kernel it costs registers).
 template <int MODE, int ELT, int DP, bool HAS_RAB, bool ALIGNED>
-__global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 128) || DP <= 64)) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
+__global__ __launch_bounds__(256, ((ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 128) || DP <= 64)) || (MODE == ANY_FWD && DP <= 64)) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
   const Params& p = bp.f;
   constexpr bool F16 = ELT == ANY_F16;
   constexpr bool F32 = ELT == ANY_F32;  // v_mfma_f32_32x32x2_f32: one element per lane and operand, see below
@@ -401,6 +401,35 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
         }
       }
     };
+    // Streamed rows [ra, rb) against this wave's stationary rows: 0 no pair kept, 1 every pair kept (causal or
+    // semi-local history inside every row's window: no predicate needed), 2 the predicate per pair.  Asked
+    // once per tile and wave, and again per 32-row block inside the tiles that need the predicate.
+    auto classify = [&](int ra, int rb) __attribute__((always_inline)) {
+      if (ra >= si.n) return 0;
+      // (m_lo, m_hi) and (j_lo, j_hi): query rows and keys, inclusive
+      const int m_lo = KEYS ? ra : c_lo, m_hi = KEYS ? min(rb, si.n) - 1 : c_hi;
+      const int j_lo = KEYS ? c_lo : ra, j_hi = KEYS ? c_hi : min(rb, si.n) - 1;
+      const int id_lo = min(m_lo, si.cap), id_hi = min(m_hi, si.cap);
+      const bool diagonal = m_lo <= j_hi && j_lo <= m_hi;
+      bool full = false;
+      if (!noncausal) {
+        const bool history = j_lo < id_hi && (id_hi >= si.tail0 || id_lo - j_hi <= si.win);
+        if (!(diagonal || history || j_lo < si.ctx_eff)) return 0;
+        // every pair kept: history keys below every row, and under a window inside it for every row
+        full = j_hi < m_lo && j_hi < si.cap && rb <= si.n && (!semi || id_lo >= si.tail0 || id_hi - j_lo <= si.win);
+      } else {
+        const int idj_lo = min(j_lo, si.cap), idj_hi = min(j_hi, si.cap);
+        bool window = false, tail = false;
+        if (si.win != WIN_ALL) {
+          window = idj_lo - id_hi <= si.win && id_lo - idj_hi <= si.win;  // the two id ranges come within the window
+          if (si.tail0 != 0x7fffffff) tail = id_hi >= si.tail0 && (idj_lo < si.tail0 ? 0 : idj_lo) < id_hi;
+        }
+        if (!(diagonal || window || tail || j_lo < si.ctx_eff)) return 0;
+        // every pair kept: the two id ranges lie within the window of each other all along
+        full = si.win != WIN_ALL && id_hi - idj_lo <= si.win && idj_hi - id_lo <= si.win && rb <= si.n;
+      }
+      return full ? 1 : 2;
+    };
     auto tile_body = [&](auto masked_tag, int r0, int buf, Packed& pk) __attribute__((always_inline)) {
       constexpr int MASKED = decltype(masked_tag)::value;
       const unsigned char* y1 = &Y1s[buf][0];
@@ -412,15 +441,32 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
       // one 32-row block of scores at a time (both at once cost the masked bodies their registers)
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
+        // a tile that needs the predicate: its two blocks on their own (along the diagonal one of them keeps
+        // no pair, or every pair)
+        int block_class = 1;
+        if constexpr (MASKED != 0) {
+          block_class = classify(r0 + 32 * blk, r0 + 32 * blk + 32);
+          if (block_class == 0) {
+            if constexpr (!F32) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                pk.pw[blk][i] = 0u;
+                if constexpr (HAS_DP) pk.dsw[blk][i] = 0u;
+              }
+            }
+            continue;
+          }
+        }
         f32x16 Sb = row_product(y1, blk, x1), dPb;
         if constexpr (HAS_DP) dPb = row_product(y2, blk, x2);
         float pv[16], dsv[HAS_DP ? 16 : 1];
         // (the per-token scale of the key-stationary modes, and the bias table's gradient of the dQ mode, as
         // a compile-time tag of the loop: tested per score they put a branch behind every score, and nothing
         // was scheduled across them)
-        auto score_loop = [&](auto tag) __attribute__((always_inline)) {
+        auto score_loop = [&](auto tag, auto predicate_tag) __attribute__((always_inline)) {
         constexpr bool ROW_SCALES = KEYS && decltype(tag)::value;
         constexpr bool WITH_DRAB = MODE == ANY_DQ && decltype(tag)::value;
+        constexpr int PRED = decltype(predicate_tag)::value;  // 0: every pair kept, else MASKED
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int rl = 32 * blk + 8 * (r >> 2) + 4 * half + (r & 3);  // streamed row of this register
@@ -435,12 +481,12 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
             pe *= rs;
             de *= rs;
           }
-          if (MASKED) {
+          if constexpr (PRED != 0) {
             const int rr = rbase + (32 * blk + 8 * (r >> 2) + (r & 3));
             const int m = KEYS ? rr : c, j = KEYS ? c : rr;
             const int idm = min(m, si.cap);
             int kp = (int)(m == j) | (int)(j < si.ctx_eff);
-            if (MASKED == 1) {
+            if (PRED == 1) {
               kp |= (int)(j < idm) & ((int)(idm - j <= si.win) | (int)(idm >= si.tail0));
             } else if (si.win != WIN_ALL) {
               // (without a full-attention tail tail0 is INT_MAX: both ids below count as 0 and the last term is never true)
@@ -459,12 +505,16 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
             if (de != 0.f) atomicAdd(&dband_s[buf][(c - c0) - rl + (ANY_BN - 1)], de * dscale);
           }
           // the masked bodies four pairs at a time: left to itself the scheduler interleaves all 32 and spills
-          if (MASKED && (r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+          if (PRED != 0 && (r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
         };
         constexpr bool TAGGED = KEYS || (MODE == ANY_DQ && HAS_RAB);
-        if (TAGGED && (KEYS ? per_token : drabg != nullptr)) score_loop(std::true_type{});
-        else score_loop(std::false_type{});
+        auto scores = [&](auto predicate_tag) __attribute__((always_inline)) {
+          if (TAGGED && (KEYS ? per_token : drabg != nullptr)) score_loop(std::true_type{}, predicate_tag);
+          else score_loop(std::false_type{}, predicate_tag);
+        };
+        if (MASKED == 0 || block_class == 1) scores(std::integral_constant<int, 0>{});
+        else scores(std::integral_constant<int, MASKED>{});
         if constexpr (F32) {
           // accumulating products of this block, one streamed row per lane half and step: register r of
           // the score block is the B operand as it is; the A operand is column 32 db + l32 of that row
@@ -489,32 +539,12 @@ __global__ __launch_bounds__(256, (ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 
       }
       if constexpr (!F32 && !ACC_APART) accumulate(buf, pk);
     };
-    // wave-level classification of a block: skipped, every pair kept, or the predicate per pair
     auto compute_tile = [&](int t, int buf) __attribute__((always_inline)) {
       if (!wave_has_rows) return;
-      const int r0 = t * ANY_BN, r1 = r0 + ANY_BN;
-      bool full = false;
-      // (m_lo, m_hi) and (j_lo, j_hi): query rows and keys of the block, inclusive
-      const int m_lo = KEYS ? r0 : c_lo, m_hi = KEYS ? min(r1, si.n) - 1 : c_hi;
-      const int j_lo = KEYS ? c_lo : r0, j_hi = KEYS ? c_hi : min(r1, si.n) - 1;
-      const int id_lo = min(m_lo, si.cap), id_hi = min(m_hi, si.cap);
-      const bool diagonal = m_lo <= j_hi && j_lo <= m_hi;
-      if (!noncausal) {
-        const bool history = j_lo < id_hi && (id_hi >= si.tail0 || id_lo - j_hi <= si.win);
-        if (!(diagonal || history || j_lo < si.ctx_eff)) return;
-        // every pair kept: history keys below every row, and under a window inside it for every row
-        full = j_hi < m_lo && j_hi < si.cap && r1 <= si.n && (!semi || id_lo >= si.tail0 || id_hi - j_lo <= si.win);
-      } else {
-        const int idj_lo = min(j_lo, si.cap), idj_hi = min(j_hi, si.cap);
-        bool window = false, tail = false;
-        if (si.win != WIN_ALL) {
-          window = idj_lo - id_hi <= si.win && id_lo - idj_hi <= si.win;  // the two id ranges come within the window
-          if (si.tail0 != 0x7fffffff) tail = id_hi >= si.tail0 && (idj_lo < si.tail0 ? 0 : idj_lo) < id_hi;
-        }
-        if (!(diagonal || window || tail || j_lo < si.ctx_eff)) return;
-        // every pair kept: the two id ranges lie within the window of each other all along
-        full = si.win != WIN_ALL && id_hi - idj_lo <= si.win && idj_hi - id_lo <= si.win && r1 <= si.n;
-      }
+      const int r0 = t * ANY_BN;
+      const int cls = classify(r0, r0 + ANY_BN);
+      if (cls == 0) return;
+      const bool full = cls == 1;
       Packed pk;
       if (full) tile_body(std::integral_constant<int, 0>{}, r0, buf, pk);
       else if (!noncausal) tile_body(std::integral_constant<int, 1>{}, r0, buf, pk);
