@@ -464,49 +464,49 @@ __global__ __launch_bounds__(256, ((ELT != ANY_F32 && ((MODE == ANY_FWD && DP <=
         // a compile-time tag of the loop: tested per score they put a branch behind every score, and nothing
         // was scheduled across them)
         auto score_loop = [&](auto tag, auto predicate_tag) __attribute__((always_inline)) {
-        constexpr bool ROW_SCALES = KEYS && decltype(tag)::value;
-        constexpr bool WITH_DRAB = MODE == ANY_DQ && decltype(tag)::value;
-        constexpr int PRED = decltype(predicate_tag)::value;  // 0: every pair kept, else MASKED
+          constexpr bool ROW_SCALES = KEYS && decltype(tag)::value;
+          constexpr bool WITH_DRAB = MODE == ANY_DQ && decltype(tag)::value;
+          constexpr int PRED = decltype(predicate_tag)::value;  // 0: every pair kept, else MASKED
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int rl = 32 * blk + 8 * (r >> 2) + 4 * half + (r & 3);  // streamed row of this register
-          float x = FOLD_ALPHA ? Sb[r] : Sb[r] * p.alpha;
-          if constexpr (HAS_RAB) x += bias_s[buf][KEYS ? rl - (c - c0) + (ANY_BM - 1) : (c - c0) - rl + (ANY_BN - 1)];
-          const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * (FOLD_ALPHA ? neg_alpha_log2e : neg_log2e)));
-          float pe = x * sig;
-          float de = 0.f;
-          if constexpr (HAS_DP) de = dPb[r] * (sig + pe * (1.0f - sig));  // silu'(x) = sig (1 + x (1 - sig))
-          if constexpr (ROW_SCALES) {
-            const float rs = scale_s[buf][rl];
-            pe *= rs;
-            de *= rs;
-          }
-          if constexpr (PRED != 0) {
-            const int rr = rbase + (32 * blk + 8 * (r >> 2) + (r & 3));
-            const int m = KEYS ? rr : c, j = KEYS ? c : rr;
-            const int idm = min(m, si.cap);
-            int kp = (int)(m == j) | (int)(j < si.ctx_eff);
-            if (PRED == 1) {
-              kp |= (int)(j < idm) & ((int)(idm - j <= si.win) | (int)(idm >= si.tail0));
-            } else if (si.win != WIN_ALL) {
-              // (without a full-attention tail tail0 is INT_MAX: both ids below count as 0 and the last term is never true)
-              const int idj = min(j, si.cap);
-              const int gr = idm < si.tail0 ? 0 : idm, gc = idj < si.tail0 ? 0 : idj;
-              kp |= (int)(abs(idm - idj) <= si.win) | (int)(gr - gc > 0);
+          for (int r = 0; r < 16; ++r) {
+            const int rl = 32 * blk + 8 * (r >> 2) + 4 * half + (r & 3);  // streamed row of this register
+            float x = FOLD_ALPHA ? Sb[r] : Sb[r] * p.alpha;
+            if constexpr (HAS_RAB) x += bias_s[buf][KEYS ? rl - (c - c0) + (ANY_BM - 1) : (c - c0) - rl + (ANY_BN - 1)];
+            const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * (FOLD_ALPHA ? neg_alpha_log2e : neg_log2e)));
+            float pe = x * sig;
+            float de = 0.f;
+            if constexpr (HAS_DP) de = dPb[r] * (sig + pe * (1.0f - sig));  // silu'(x) = sig (1 + x (1 - sig))
+            if constexpr (ROW_SCALES) {
+              const float rs = scale_s[buf][rl];
+              pe *= rs;
+              de *= rs;
             }
-            kp &= (int)(rr < si.n) & (int)(c < si.n);
-            pe = kp ? pe : 0.f;
-            de = kp ? de : 0.f;
+            if constexpr (PRED != 0) {
+              const int rr = rbase + (32 * blk + 8 * (r >> 2) + (r & 3));
+              const int m = KEYS ? rr : c, j = KEYS ? c : rr;
+              const int idm = min(m, si.cap);
+              int kp = (int)(m == j) | (int)(j < si.ctx_eff);
+              if (PRED == 1) {
+                kp |= (int)(j < idm) & ((int)(idm - j <= si.win) | (int)(idm >= si.tail0));
+              } else if (si.win != WIN_ALL) {
+                // (without a full-attention tail tail0 is INT_MAX: both ids below count as 0 and the last term is never true)
+                const int idj = min(j, si.cap);
+                const int gr = idm < si.tail0 ? 0 : idm, gc = idj < si.tail0 ? 0 : idj;
+                kp |= (int)(abs(idm - idj) <= si.win) | (int)(gr - gc > 0);
+              }
+              kp &= (int)(rr < si.n) & (int)(c < si.n);
+              pe = kp ? pe : 0.f;
+              de = kp ? de : 0.f;
+            }
+            pv[r] = pe;
+            if constexpr (HAS_DP) dsv[r] = de;
+            if constexpr (WITH_DRAB) {
+              // d score / d bias = 1: the pair's dS (with its row's scale) goes to its diagonal
+              if (de != 0.f) atomicAdd(&dband_s[buf][(c - c0) - rl + (ANY_BN - 1)], de * dscale);
+            }
+            // the masked bodies four pairs at a time: left to itself the scheduler interleaves all 32 and spills
+            if (PRED != 0 && (r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
           }
-          pv[r] = pe;
-          if constexpr (HAS_DP) dsv[r] = de;
-          if constexpr (WITH_DRAB) {
-            // d score / d bias = 1: the pair's dS (with its row's scale) goes to its diagonal
-            if (de != 0.f) atomicAdd(&dband_s[buf][(c - c0) - rl + (ANY_BN - 1)], de * dscale);
-          }
-          // the masked bodies four pairs at a time: left to itself the scheduler interleaves all 32 and spills
-          if (PRED != 0 && (r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-        }
         };
         constexpr bool TAGGED = KEYS || (MODE == ANY_DQ && HAS_RAB);
         auto scores = [&](auto predicate_tag) __attribute__((always_inline)) {
