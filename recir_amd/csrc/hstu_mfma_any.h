@@ -56,6 +56,10 @@ typedef __attribute__((ext_vector_type(2))) _Float16 any_f16x2;
 typedef __attribute__((ext_vector_type(4))) short any_i16x4;
 typedef __attribute__((address_space(3))) any_i16x4 any_lds_i16x4;
 
+#ifndef HSTU_ANY_READ_AHEAD
+#define HSTU_ANY_READ_AHEAD 1  // (0: a measurement build without the fragments read ahead)
+#endif
+
 constexpr int ANY_FWD = 0, ANY_DQ = 1, ANY_DKV = 2, ANY_DV = 3, ANY_DK = 4;  // modes (DV, DK: the two halves of DKV as passes of their own)
 constexpr int ANY_BF16 = 0, ANY_F16 = 1, ANY_F32 = 2;                        // element types (the template's ELT)
 constexpr int ANY_BM = 128;  // stationary rows per workgroup
@@ -122,12 +126,18 @@ __device__ __forceinline__ u32x4 any_load_elems(const char* src, int n, int D) {
   return r;
 }
 
+template <int MODE, int ELT, int DP>
+constexpr int any_workgroups_per_cu() {
+  return ((ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 128) || DP <= 64)) || (MODE == ANY_FWD && DP <= 64)) ? 2 : 1;
+}
+
 // Two workgroups per CU where the registers allow it (a few spills included: one workgroup per CU
 // measured 20-35 % slower at these shapes).
 // HAS_RAB: with a bias table (an instantiation of its own: tested per pair the pointer costs seven scalar
 // instructions a score, and as a second set of tile bodies inside one kernel it costs registers).
 template <int MODE, int ELT, int DP, bool HAS_RAB, bool ALIGNED>
-__global__ __launch_bounds__(256, ((ELT != ANY_F32 && ((MODE == ANY_FWD && DP <= 128) || DP <= 64)) || (MODE == ANY_FWD && DP <= 64)) ? 2 : 1) void hstu_mfma_any(BwdParams bp) {
+__global__ __launch_bounds__(256, (any_workgroups_per_cu<MODE, ELT, DP>()))
+__attribute__((amdgpu_waves_per_eu((any_workgroups_per_cu<MODE, ELT, DP>()), (any_workgroups_per_cu<MODE, ELT, DP>())))) void hstu_mfma_any(BwdParams bp) {
   const Params& p = bp.f;
   constexpr bool F16 = ELT == ANY_F16;
   constexpr bool F32 = ELT == ANY_F32;  // v_mfma_f32_32x32x2_f32: one element per lane and operand, see below
@@ -147,6 +157,9 @@ __global__ __launch_bounds__(256, ((ELT != ANY_F32 && ((MODE == ANY_FWD && DP <=
   // Forward without a bias in bf16 or fp32: P / alpha = s sigmoid(alpha s) goes into the second product and
   // alpha onto the output rows (one multiplication less per score; not in fp16, whose range P / alpha could leave)
   constexpr bool FOLD_ALPHA = MODE == ANY_FWD && !HAS_RAB && !F16;
+  // LDS fragments read a step ahead of the products that take them, kept in that order by scheduling barriers:
+  // 3 % where the fragments of a step are few; at padded head dims above 64 their registers cost more
+  constexpr bool READ_AHEAD = HSTU_ANY_READ_AHEAD && DP <= 64;
   constexpr bool ACC_APART = (MODE == ANY_FWD && DP <= 128) || DP <= 64;
   static_assert(DP == 32 || DP == 64 || DP == 128 || DP == 256, "padded head dim");
   static_assert(!F32 || DP <= 128, "fp32 tiles of 256 columns do not fit the LDS");
@@ -368,6 +381,7 @@ __global__ __launch_bounds__(256, ((ELT != ANY_F32 && ((MODE == ANY_FWD && DP <=
           u32x4 a[G];
 #pragma unroll
           for (int kk = 0; kk < G; ++kk) a[kk] = row_frag(y, blk, k0 + kk);
+          if constexpr (READ_AHEAD) __builtin_amdgcn_sched_barrier(0);  // (or the reads sink back to their products, one wait each)
 #pragma unroll
           for (int kk = 0; kk < G; ++kk) acc = any_mfma<F16>(a[kk], x[k0 + kk], (k0 + kk) == 0 ? zero16 : acc);
         }
@@ -388,16 +402,46 @@ __global__ __launch_bounds__(256, ((ELT != ANY_F32 && ((MODE == ANY_FWD && DP <=
     auto accumulate = [&](int buf, const Packed& pk) __attribute__((always_inline)) {
       const unsigned char* y1 = &Y1s[buf][0];
       const unsigned char* y2 = &Y2s[buf][0];
+      if constexpr (READ_AHEAD) {
+        // the transposed fragments of step s2 + 1 are read before the products of step s2 are issued (the
+        // scheduling barriers keep that order: left alone the compiler reads each fragment right before its
+        // product and waits for it)
+        u32x4 f2[2][HAS_P ? NB : 1], f1[2][HAS_DP ? NB : 1];
+        auto read_step = [&](int s2) __attribute__((always_inline)) {
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        const int blk = s2 >> 1, w0 = 4 * (s2 & 1);
-        const u32x4 pb = {pk.pw[blk][w0], pk.pw[blk][w0 + 1], pk.pw[blk][w0 + 2], pk.pw[blk][w0 + 3]};
-        u32x4 db_ = zero4;
-        if constexpr (HAS_DP) db_ = (u32x4){pk.dsw[blk][w0], pk.dsw[blk][w0 + 1], pk.dsw[blk][w0 + 2], pk.dsw[blk][w0 + 3]};
+          for (int db = 0; db < NB; ++db) {
+            if constexpr (HAS_P) f2[s2 & 1][db] = tr_frag(y2, db, s2);
+            if constexpr (HAS_DP) f1[s2 & 1][db] = tr_frag(y1, db, s2);
+          }
+        };
+        read_step(0);
 #pragma unroll
-        for (int db = 0; db < NB; ++db) {
-          if constexpr (HAS_P) acc2[db] = any_mfma<F16>(tr_frag(y2, db, s2), pb, acc2[db]);
-          if constexpr (HAS_DP) acc1[db] = any_mfma<F16>(tr_frag(y1, db, s2), db_, acc1[db]);
+        for (int s2 = 0; s2 < 4; ++s2) {
+          if (s2 + 1 < 4) read_step(s2 + 1);
+          __builtin_amdgcn_sched_barrier(0);
+          const int blk = s2 >> 1, w0 = 4 * (s2 & 1);
+          const u32x4 pb = {pk.pw[blk][w0], pk.pw[blk][w0 + 1], pk.pw[blk][w0 + 2], pk.pw[blk][w0 + 3]};
+          u32x4 db_ = zero4;
+          if constexpr (HAS_DP) db_ = (u32x4){pk.dsw[blk][w0], pk.dsw[blk][w0 + 1], pk.dsw[blk][w0 + 2], pk.dsw[blk][w0 + 3]};
+#pragma unroll
+          for (int db = 0; db < NB; ++db) {
+            if constexpr (HAS_P) acc2[db] = any_mfma<F16>(f2[s2 & 1][db], pb, acc2[db]);
+            if constexpr (HAS_DP) acc1[db] = any_mfma<F16>(f1[s2 & 1][db], db_, acc1[db]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+          const int blk = s2 >> 1, w0 = 4 * (s2 & 1);
+          const u32x4 pb = {pk.pw[blk][w0], pk.pw[blk][w0 + 1], pk.pw[blk][w0 + 2], pk.pw[blk][w0 + 3]};
+          u32x4 db_ = zero4;
+          if constexpr (HAS_DP) db_ = (u32x4){pk.dsw[blk][w0], pk.dsw[blk][w0 + 1], pk.dsw[blk][w0 + 2], pk.dsw[blk][w0 + 3]};
+#pragma unroll
+          for (int db = 0; db < NB; ++db) {
+            if constexpr (HAS_P) acc2[db] = any_mfma<F16>(tr_frag(y2, db, s2), pb, acc2[db]);
+            if constexpr (HAS_DP) acc1[db] = any_mfma<F16>(tr_frag(y1, db, s2), db_, acc1[db]);
+          }
         }
       }
     };
@@ -466,7 +510,9 @@ __global__ __launch_bounds__(256, ((ELT != ANY_F32 && ((MODE == ANY_FWD && DP <=
         auto score_loop = [&](auto tag, auto predicate_tag) __attribute__((always_inline)) {
           constexpr bool ROW_SCALES = KEYS && decltype(tag)::value;
           constexpr bool WITH_DRAB = MODE == ANY_DQ && decltype(tag)::value;
-          constexpr int PRED = decltype(predicate_tag)::value;  // 0: every pair kept, else MASKED
+          // 0: every pair kept; 1: the causal / semi-local predicate; 2: the non-causal mask without a window
+          // (diagonal and contextual keys); 3: the non-causal mask with a window
+          constexpr int PRED = decltype(predicate_tag)::value;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int rl = 32 * blk + 8 * (r >> 2) + 4 * half + (r & 3);  // streamed row of this register
@@ -488,7 +534,7 @@ __global__ __launch_bounds__(256, ((ELT != ANY_F32 && ((MODE == ANY_FWD && DP <=
               int kp = (int)(m == j) | (int)(j < si.ctx_eff);
               if (PRED == 1) {
                 kp |= (int)(j < idm) & ((int)(idm - j <= si.win) | (int)(idm >= si.tail0));
-              } else if (si.win != WIN_ALL) {
+              } else if (PRED == 3) {
                 // (without a full-attention tail tail0 is INT_MAX: both ids below count as 0 and the last term is never true)
                 const int idj = min(j, si.cap);
                 const int gr = idm < si.tail0 ? 0 : idm, gc = idj < si.tail0 ? 0 : idj;
@@ -514,6 +560,7 @@ __global__ __launch_bounds__(256, ((ELT != ANY_F32 && ((MODE == ANY_FWD && DP <=
           else score_loop(std::false_type{}, predicate_tag);
         };
         if (MASKED == 0 || block_class == 1) scores(std::integral_constant<int, 0>{});
+        else if (MASKED == 2 && si.win != WIN_ALL) scores(std::integral_constant<int, 3>{});
         else scores(std::integral_constant<int, MASKED>{});
         if constexpr (F32) {
           // accumulating products of this block, one streamed row per lane half and step: register r of
