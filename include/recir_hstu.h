@@ -42,7 +42,7 @@ extern "C" {
  *     when there is a bias; the gradient of the bias table is reproducible bit for bit here only;
  *   - the general MFMA kernels ("mfma_*", "bwd_mfma_*"): bf16 or fp16 with Dqk and Dv up to 256,
  *     fp32 up to 128 (fp32 MFMAs, a sixteenth of the bf16 rate); Dqk and Dv independent of each
- *     other, every mask, any alpha; in bf16 1.4 to 1.7 times the time of the first group at its own
+ *     other, every mask, any alpha; in bf16 1.4 to 1.9 times the time of the first group at its own
  *     shape.  Where every row of every tensor starts at a multiple of 16 bytes (16-byte aligned
  *     tensors, head dims multiples of 8, fp32: 4) rows move in aligned 16-byte pieces; otherwise
  *     (head dims like 25 or 50, a tensor that starts in the middle of a row of a larger one) in

@@ -40,6 +40,10 @@
 #include "hstu_bwd_acc_regs.h"
 #include "hstu_tiled_d128_dl.h"  // i16x4, i16x8, lds_void, lds_i16x4
 
+#ifndef HSTU_BWD_DQ_PD
+#define HSTU_BWD_DQ_PD 2  // (0: a measurement build of the dQ kernel with every fragment read right before its product)
+#endif
+
 namespace recir_hstu {
 
 // Waves per SIMD the dQ kernel is compiled for.  Two fit once the phases of its tile body are fenced
@@ -331,13 +335,29 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
         // phases are fenced so that the fragment reads of one are not hoisted over the previous one
         // (keeps the live registers within the two-waves-per-SIMD budget)
         __builtin_amdgcn_sched_barrier(0);
+        constexpr int PD = HSTU_BWD_DQ_PD;  // fragments requested this many products ahead
+        if constexpr (PD > 0) {
+          auto frag = [&](int i) __attribute__((always_inline)) { return bwd_row_frag((i & 1) ? vb : kb, lc, kvb, i >> 1); };
+          bf16x8 F[16];
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(kb, lc, kvb, kk), qf[kk], st, 0, 0, 0);
-          dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(vb, lc, kvb, kk), gf[kk], dpt, 0, 0, 0);
-          if (kk == 3) __builtin_amdgcn_sched_barrier(0);
+          for (int i = 0; i < PD; ++i) F[i] = frag(i);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            if (i + PD < 16) F[i + PD] = frag(i + PD);
+            if (i & 1) dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[i], gf[i >> 1], dpt, 0, 0, 0);
+            else st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[i], qf[i >> 1], st, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        } else {
+#pragma unroll
+          for (int kk = 0; kk < 8; ++kk) {
+            st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(kb, lc, kvb, kk), qf[kk], st, 0, 0, 0);
+            dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_row_frag(vb, lc, kvb, kk), gf[kk], dpt, 0, 0, 0);
+            if (kk == 3) __builtin_amdgcn_sched_barrier(0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
         // dS^T = dP^T silu'(S^T) on the kept pairs; element r of the block is key
         // 32 kvb + 8 (r / 4) + 4 half + r % 4 for this lane's query row
         u32x4 w0, w1;
@@ -383,13 +403,27 @@ __global__ __launch_bounds__(256, BWD_DQ_OCC) void hstu_bwd_dq_d128(BwdParams bp
         }
         const bf16x8 b0 = __builtin_bit_cast(bf16x8, w0), b1 = __builtin_bit_cast(bf16x8, w1);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (PD > 0) {
+          auto frag = [&](int i) __attribute__((always_inline)) { return bwd_tr_frag(kb, lc, i >> 1, 2 * kvb + (i & 1)); };
+          bf16x8 F[8];
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(kb, lc, db, 2 * kvb), b0, acc[db], 0, 0, 0);
-          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(kb, lc, db, 2 * kvb + 1), b1, acc[db], 0, 0, 0);
-          if (db == 1) __builtin_amdgcn_sched_barrier(0);
+          for (int i = 0; i < PD; ++i) F[i] = frag(i);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (i + PD < 8) F[i + PD] = frag(i + PD);
+            acc[i >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[i], (i & 1) ? b1 : b0, acc[i >> 1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        } else {
+#pragma unroll
+          for (int db = 0; db < 4; ++db) {
+            acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(kb, lc, db, 2 * kvb), b0, acc[db], 0, 0, 0);
+            acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bwd_tr_frag(kb, lc, db, 2 * kvb + 1), b1, acc[db], 0, 0, 0);
+            if (db == 1) __builtin_amdgcn_sched_barrier(0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
     };
 
@@ -703,14 +737,25 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
         for (int r = 0; r < 16; ++r)
           ts[r] = PER_TOKEN ? p.attn_scale[si.s + min(m0 + qb32 * 32 + 8 * (r >> 2) + 4 * half + (r & 3), si.n - 1)] : 1.0f;
       };
-      constexpr int PD = 3;  // fragments requested this many products ahead in the pipelined phases
+      constexpr int PD = 3;  // fragments requested this many products ahead (5 and 8 measured the same)
       f32x16 sA, dpA, sB, dpB;
       float ts[16];
       unsigned pwA[8], dwA[8], pwB[8], dwB[8];  // packed P and dS of the two blocks
-      // phase 1
+      // phase 1 (its fragments requested ahead like those of the other phases: read one by one, each right
+      // before its product, they left this wave, alone on its SIMD, waiting for the LDS sixteen times a tile)
       load_bias(0, sA);
+      {
+        bf16x8 F[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) score_mfma(0, i, sA, dpA, score_frag(0, i));
+        for (int i = 0; i < PD; ++i) F[i] = score_frag(0, i);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (i + PD < 16) F[i + PD] = score_frag(0, i + PD);
+          score_mfma(0, i, sA, dpA, F[i]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
       load_ts(0, ts);
       // an MFMA result may be read by other instructions 11 cycles after the MFMA at the earliest; the
       // compiler does not count for instructions it did not place
@@ -764,9 +809,16 @@ __global__ __launch_bounds__(256, 1) void hstu_bwd_dkv_d128(BwdParams bp) {
         const u32x4 db0 = {dwB[0], dwB[1], dwB[2], dwB[3]}, db1 = {dwB[4], dwB[5], dwB[6], dwB[7]};
         const bf16x8 opB[4] = {__builtin_bit_cast(bf16x8, pb0), __builtin_bit_cast(bf16x8, db0),
                                __builtin_bit_cast(bf16x8, pb1), __builtin_bit_cast(bf16x8, db1)};
+        bf16x8 F[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          bwd_acc_mfma1(((i & 1) ? 4 : 0) + ((i >> 1) & 3), acc_frag(1, i), opB[2 * (i >> 3) + (i & 1)]);
+        for (int i = 0; i < PD; ++i) F[i] = acc_frag(1, i);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (i + PD < 16) F[i + PD] = acc_frag(1, i + PD);
+          bwd_acc_mfma1(((i & 1) ? 4 : 0) + ((i >> 1) & 3), F[i], opB[2 * (i >> 3) + (i & 1)]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     };
 

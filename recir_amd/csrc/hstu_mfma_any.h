@@ -3,7 +3,7 @@
 // or fp32 values; tensors at any address their element type allows; every mask the operator knows (causal with targets
 // and contextual prefix, semi-local, the non-causal forms); a bias with any alpha, and the gradient of
 // the bias table.  One template, five modes; nothing here is hand-scheduled: the point is to keep such
-// calls on the matrix cores (1.4 to 1.7 times the time of the head-dim-128 kernels at their own shape)
+// calls on the matrix cores (1.4 to 1.9 times the time of the head-dim-128 kernels at their own shape)
 // instead of on the one-wave-per-token kernels (two orders of magnitude slower).
 //
 // A workgroup (4 waves) owns 128 "stationary" rows of one (sequence, head), 32 per wave, one per lane
