@@ -151,15 +151,15 @@ __attribute__((amdgpu_waves_per_eu((any_workgroups_per_cu<MODE, ELT, DP>()), (an
   constexpr int CPR = DP * ES / 16; // 16-byte chunks per tile row
   constexpr int NCH = DP * ES / 64; // chunks of one tile that one thread stages
   constexpr int EPC = 16 / ES;      // elements per chunk
-  // The accumulating products stand once, behind the three kinds of tile body, instead of inside each:
-  // as the results of several bodies the accumulators were copied once a tile (8-14 % of the time where
-  // they are few); where they are many the packed P and dS kept across the bodies' end cost more in spills.
   // Forward without a bias in bf16 or fp32: P / alpha = s sigmoid(alpha s) goes into the second product and
   // alpha onto the output rows (one multiplication less per score; not in fp16, whose range P / alpha could leave)
   constexpr bool FOLD_ALPHA = MODE == ANY_FWD && !HAS_RAB && !F16;
   // LDS fragments read a step ahead of the products that take them, kept in that order by scheduling barriers:
   // 3 % where the fragments of a step are few; at padded head dims above 64 their registers cost more
   constexpr bool READ_AHEAD = HSTU_ANY_READ_AHEAD && DP <= 64;
+  // The accumulating products stand once, behind the three kinds of tile body, instead of inside each:
+  // as the results of several bodies the accumulators were copied once a tile (8-14 % of the time where
+  // they are few); where they are many the packed P and dS kept across the bodies' end cost more in spills.
   constexpr bool ACC_APART = (MODE == ANY_FWD && DP <= 128) || DP <= 64;
   static_assert(DP == 32 || DP == 64 || DP == 128 || DP == 256, "padded head dim");
   static_assert(!F32 || DP <= 128, "fp32 tiles of 256 columns do not fit the LDS");
