@@ -56,6 +56,9 @@ typedef __attribute__((ext_vector_type(2))) _Float16 any_f16x2;
 typedef __attribute__((ext_vector_type(4))) short any_i16x4;
 typedef __attribute__((address_space(3))) any_i16x4 any_lds_i16x4;
 
+#ifndef HSTU_ANY_RING
+#define HSTU_ANY_RING 2
+#endif
 #ifndef HSTU_ANY_READ_AHEAD
 #define HSTU_ANY_READ_AHEAD 1  // (0: a measurement build without the fragments read ahead)
 #endif
@@ -157,6 +160,9 @@ __attribute__((amdgpu_waves_per_eu((any_workgroups_per_cu<MODE, ELT, DP>()), (an
   // LDS fragments read a step ahead of the products that take them, kept in that order by scheduling barriers:
   // 3 % where the fragments of a step are few; at padded head dims above 64 their registers cost more
   constexpr bool READ_AHEAD = HSTU_ANY_READ_AHEAD && DP <= 64;
+  // above that, in the backward modes: each fragment requested this many products ahead of its own (0: read
+  // where it is used; the forward with a bias measured 3 % slower with it, without one 2 % faster)
+  constexpr int RING = (READ_AHEAD || MODE == ANY_FWD) ? 0 : HSTU_ANY_RING;
   // The accumulating products stand once, behind the three kinds of tile body, instead of inside each:
   // as the results of several bodies the accumulators were copied once a tile (8-14 % of the time where
   // they are few); where they are many the packed P and dS kept across the bodies' end cost more in spills.
@@ -374,6 +380,19 @@ __attribute__((amdgpu_waves_per_eu((any_workgroups_per_cu<MODE, ELT, DP>()), (an
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[e]), __uint_as_float(x[kk][e]), (kk == 0 && e == 0) ? zero16 : acc, 0, 0, 0);
         }
       } else {
+        if constexpr (!READ_AHEAD && RING > 0) {
+          u32x4 a[NK];
+#pragma unroll
+          for (int kk = 0; kk < RING; ++kk) a[kk] = row_frag(y, blk, kk);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int kk = 0; kk < NK; ++kk) {
+            if (kk + RING < NK) a[kk + RING] = row_frag(y, blk, kk + RING);
+            acc = any_mfma<F16>(a[kk], x[kk], kk == 0 ? zero16 : acc);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          return acc;
+        }
         // fragments read ahead in groups of up to eight (left in one loop the compiler reads and waits one at a time)
         constexpr int G = NK < 8 ? NK : 8;
 #pragma unroll
@@ -427,6 +446,33 @@ __attribute__((amdgpu_waves_per_eu((any_workgroups_per_cu<MODE, ELT, DP>()), (an
           for (int db = 0; db < NB; ++db) {
             if constexpr (HAS_P) acc2[db] = any_mfma<F16>(f2[s2 & 1][db], pb, acc2[db]);
             if constexpr (HAS_DP) acc1[db] = any_mfma<F16>(f1[s2 & 1][db], db_, acc1[db]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else if constexpr (RING > 0) {
+        // the products of the tile in one sequence, each fragment requested RING products ahead of its own
+        constexpr int K = (HAS_P ? 1 : 0) + (HAS_DP ? 1 : 0);  // products per (step, column block)
+        constexpr int NPROD = 4 * NB * K;
+        auto frag = [&](int i) __attribute__((always_inline)) {
+          const int s2 = i / (NB * K), db = (i / K) % NB;
+          const bool second = HAS_P && HAS_DP && (i % K) == 1;  // with both: the P-side product, then the dS-side one
+          return tr_frag((HAS_P && !second) ? y2 : y1, db, s2);
+        };
+        u32x4 F[NPROD];
+#pragma unroll
+        for (int i = 0; i < RING; ++i) F[i] = frag(i);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NPROD; ++i) {
+          if (i + RING < NPROD) F[i + RING] = frag(i + RING);
+          const int s2 = i / (NB * K), db = (i / K) % NB, blk = s2 >> 1, w0 = 4 * (s2 & 1);
+          const bool second = HAS_P && HAS_DP && (i % K) == 1;
+          if (HAS_P && !second) {
+            const u32x4 pb = {pk.pw[blk][w0], pk.pw[blk][w0 + 1], pk.pw[blk][w0 + 2], pk.pw[blk][w0 + 3]};
+            acc2[db] = any_mfma<F16>(F[i], pb, acc2[db]);
+          } else {
+            const u32x4 db_ = {pk.dsw[blk][w0], pk.dsw[blk][w0 + 1], pk.dsw[blk][w0 + 2], pk.dsw[blk][w0 + 3]};
+            acc1[db] = any_mfma<F16>(F[i], db_, acc1[db]);
           }
           __builtin_amdgcn_sched_barrier(0);
         }
