@@ -286,6 +286,25 @@ def test_general_and_head_dim_128_kernels_agree_at_full_size(oracle):
         assert st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL, (name, st)
 
 
+@pytest.mark.parametrize("alpha", [0.0, -0.1, 3.0])
+@pytest.mark.parametrize("d", [64, 128, 50])
+def test_alpha_zero_negative_and_large_without_a_bias(oracle, d, alpha):
+    """alpha = 0 without a bias gives exact zeros (silu(0) = 0) in every kernel family, also where alpha is applied
+    to the output rows instead of the scores; a negative and a large alpha match the oracle on the relative bounds
+    (the outputs are of the order of 1 at alpha = 3, so no absolute bound here)."""
+    from recir_amd.workloads import make_jagged
+
+    wl = make_jagged([300, 70, 5], [20, 0, 5], 2, d, d, max_seq_len=320, alpha=alpha, dtype="bf16", seed=3, tail_rows=2)
+    out = run_hip(wl)
+    ref = run_oracle(oracle, wl)
+    if alpha == 0.0:
+        assert not out.float().abs().sum().item() and not np.abs(ref).sum()
+        return
+    st = error_stats(out, ref)
+    report(f"alpha {alpha} head dim {d}", st)
+    assert st["rel_to_max"] <= BF16_REL and st["rel_fro"] <= BF16_REL and st["worst_row_rel"] <= BF16_REL, st
+
+
 def test_tensors_that_start_between_16_byte_multiples(oracle):
     """Contiguous tensors whose first element sits 2 bytes (bf16) or 4 bytes (fp32) past a 16-byte multiple, at
     head dim 128 (not the head-dim-128 kernels' then) and at 64 / 40: the general kernels read such rows in
