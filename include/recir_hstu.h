@@ -39,7 +39,7 @@ extern "C" {
  * Which kernels run a call (recir_hstu_last_kernel names the one that did):
  *   - the kernels written for head dim 128 ("tiled_d128_*", "bwd_tiled_d128_*"): bf16 (forward also
  *     fp8 q/k), Dqk = Dv = 128, 16-byte aligned tensors, the causal or semi-local mask, alpha != 0
- *     when there is a bias; the gradient of the bias table is reproducible bit for bit here only;
+ *     when there is a bias;
  *   - the general MFMA kernels ("mfma_*", "bwd_mfma_*"): bf16 or fp16 with Dqk and Dv up to 256,
  *     fp32 up to 128 (fp32 MFMAs, a sixteenth of the bf16 rate); Dqk and Dv independent of each
  *     other, every mask, any alpha; in bf16 1.4 to 1.9 times the time of the first group at its own
@@ -176,13 +176,13 @@ size_t recir_hstu_attn_fwd_workspace_bytes(int32_t T, int32_t B, int32_t H, int3
  * rab           enters S as in the forward
  * drab          device float [H, 2*max_seq_len-1] or NULL: gradient of rab (needs rab),
  *               drab[h, i] = sum of dS(m, j) over the kept pairs of all sequences with
- *               m - j + max_seq_len - 1 == i.  Written in full.  The kernels written for head dim
- *               128 sum in fixed point (one power-of-two scale per head, from the head's largest
- *               |dout| and the call's largest |v|; integer additions, so the result is the same bit
- *               for bit whatever the order of the workgroups, like dq, dk and dv); the general MFMA
- *               kernels and the generic kernels add floats atomically and may differ in the last
- *               bits from run to run.  No counterpart in the reference (which has no rab).  No
- *               gradient is produced for attn_scale.
+ *               m - j + max_seq_len - 1 == i.  Written in full.  The MFMA kernels (those written
+ *               for head dim 128 and the general ones) sum in fixed point (one power-of-two scale
+ *               per head, from the head's largest |dout| and the call's largest |v|; integer
+ *               additions, so the result is the same bit for bit whatever the order of the
+ *               workgroups, like dq, dk and dv); the generic kernels (head dims above 256) add
+ *               floats atomically and may differ in the last bits from run to run.  No counterpart
+ *               in the reference (which has no rab).  No gradient is produced for attn_scale.
  * attn_scale, flags, sizes, workspace, hip_stream: as for the forward; workspace of at least
  *               recir_hstu_attn_bwd_workspace_bytes(...) bytes, plus, with drab,
  *               recir_hstu_attn_bwd_rab_grad_workspace_bytes(H, max_seq_len)

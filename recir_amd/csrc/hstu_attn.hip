@@ -589,6 +589,56 @@ int scratch_of_current_device(void** out) {
   *out = ptr;
   return 0;
 }
+// Largest magnitude of x[rows, H, D] (rows = min(seq_offsets[B], T)), per head into per_head[H] or over all
+// heads into *all, as the bits of a float merged with an integer maximum (the bits of non-negative floats
+// order like integers; a NaN's are above every finite value's).  A wave keeps one head and walks its share
+// of the rows, so that it ends with one atomic.
+template <int ELT>
+__global__ __launch_bounds__(256) void hstu_rows_absmax(const void* x, unsigned* per_head, unsigned* all, int H, int D, const void* seq_end,
+                                                        int i32, int T) {
+  const long long e = i32 ? (long long)*(const int*)seq_end : *(const long long*)seq_end;
+  const int rows = (int)(e < 0 ? 0 : (e > T ? T : e));
+  const int lane = threadIdx.x & 63;
+  const int wid = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6), nwaves = (int)((gridDim.x * blockDim.x) >> 6);
+  const int slots = nwaves / H;  // (the launch has at least H waves)
+  const int h = wid % H, slot = wid / H;
+  if (slot >= slots) return;
+  unsigned mx = 0;
+  constexpr int U = 4;  // rows in flight per wave
+  for (int r0 = slot; r0 < rows; r0 += slots * U) {
+    for (int d = lane; d < D; d += 64) {
+      float f[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = r0 + u * slots;
+        f[u] = r < rows ? load_elem<ELT>(x, ((size_t)r * H + h) * D + d) : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) mx = max(mx, __float_as_uint(f[u]) & 0x7fffffffu);
+    }
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) mx = max(mx, (unsigned)__shfl_xor((int)mx, d, 64));
+  if (lane == 0 && mx) atomicMax(per_head ? per_head + h : all, mx);
+}
+static void launch_rows_absmax(int dtype, const void* x, unsigned* per_head, unsigned* all, int H, int D, const void* seq_end, int i32,
+                               int T, hipStream_t stream) {
+  if (dtype == RECIR_HSTU_DTYPE_BF16 && D % 8 == 0 && ((size_t)x & 15) == 0) {
+    // the quantiser's pass over 16-byte pieces; for the maximum over all heads a token's H rows count as one
+    const int h_eff = per_head ? H : 1, d8 = per_head ? D / 8 : H * (D / 8);
+    const size_t n8 = (size_t)T * H * (D / 8);
+    const unsigned blocks = (unsigned)((n8 + 255) / 256 < 256 ? (n8 + 255) / 256 : 256);  // (each ends with h_eff global atomics)
+    hipLaunchKernelGGL(hstu_quant_amax, dim3(blocks ? blocks : 1), dim3(256), 0, stream, (const u32x4*)x, per_head ? per_head : all, (unsigned*)nullptr, n8,
+                       h_eff, d8, -1, (h_eff & (h_eff - 1)) == 0 ? h_eff - 1 : -1, seq_end, i32, T);
+    return;
+  }
+  // 2048 waves or a multiple of H above that
+  const unsigned waves = (unsigned)(((2048 + H - 1) / H) * H), blocks = (waves + 3) / 4;
+  if (dtype == RECIR_HSTU_DTYPE_FP32) hipLaunchKernelGGL(hstu_rows_absmax<ELT_FP32>, dim3(blocks), dim3(256), 0, stream, x, per_head, all, H, D, seq_end, i32, T);
+  else if (dtype == RECIR_HSTU_DTYPE_FP16) hipLaunchKernelGGL(hstu_rows_absmax<ELT_FP16>, dim3(blocks), dim3(256), 0, stream, x, per_head, all, H, D, seq_end, i32, T);
+  else hipLaunchKernelGGL(hstu_rows_absmax<ELT_BF16>, dim3(blocks), dim3(256), 0, stream, x, per_head, all, H, D, seq_end, i32, T);
+}
+
 }  // namespace
 
 extern "C" {
@@ -753,16 +803,44 @@ int recir_hstu_attn_bwd(const void* dout, const void* q, const void* k, const vo
         }
       }
     }
+    const bool per_token = attn_scale && (flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
     if (use_any) {
-      if (int rc = zero_drab()) return rc;  // the dQ pass adds floats to it
+      if (drab) {
+        // The dQ pass sums dS along the diagonals as fixed-point integers (a band in LDS, a 64-bit table per
+        // head), as the kernels written for head dim 128 do below; the maxima that give a head its scale
+        // come from a pass over dout and one over v (any element type, any head dim).
+        const size_t base = 2 * half_ws + BWD_WS_TAIL;
+        const size_t need = base + recir_hstu_attn_bwd_rab_grad_workspace_bytes(H, max_seq_len);
+        if (workspace_bytes < need)
+          return fail(RECIR_HSTU_ERR_WORKSPACE,
+                      "with drab the workspace must hold recir_hstu_attn_bwd_workspace_bytes + "
+                      "recir_hstu_attn_bwd_rab_grad_workspace_bytes = %zu bytes, got %zu", need, workspace_bytes);
+        unsigned* am = (unsigned*)((char*)workspace + 2 * half_ws);
+        unsigned* dmax = (unsigned*)((char*)workspace + base);
+        long long* tab = (long long*)((char*)workspace + base + drab_head_words_bytes(H));
+        hipLaunchKernelGGL(hstu_drab_prepare, dim3(128), dim3(256), 0, stream, am, dmax, H, tab, (size_t)H * (2 * (size_t)max_seq_len - 1));
+        if (int rc = launch_status("hstu_drab_prepare")) return rc;
+        const int i32 = (flags & RECIR_HSTU_FLAG_OFFSETS_I32) ? 1 : 0;
+        const void* seq_end = (const char*)seq_offsets + (size_t)B * (i32 ? 4 : 8);
+        launch_rows_absmax(dtype, dout, dmax, nullptr, H, Dv, seq_end, i32, T, stream);
+        launch_rows_absmax(dtype, v, nullptr, am + 1, H, Dv, seq_end, i32, T, stream);
+        if (per_token) hipLaunchKernelGGL(hstu_scale_absmax, dim3(64), dim3(256), 0, stream, attn_scale, seq_end, i32, T, am + 2);
+        if (int rc = launch_status("hstu_rows_absmax")) return rc;
+        bq.absmax = bk.absmax = am;
+        bq.dout_max = dmax;
+        bq.drab_fx = tab;
+      }
       const dim3 grid((unsigned)(slots * NUM_XCD));
       if (!launch_mfma_any_bwd(dtype, any_dp, any_aligned, grid, grid, stream, bq, bk))
         return fail(RECIR_HSTU_ERR_UNSUPPORTED, "no general MFMA backward for dtype %d, padded head dim %d", dtype, any_dp);
       if (int rc = launch_status("hstu_mfma_any (backward)")) return rc;
+      if (drab) {
+        hipLaunchKernelGGL(hstu_drab_finalize, dim3(256), dim3(256), 0, stream, bq, per_token ? 1 : 0);
+        if (int rc = launch_status("hstu_drab_finalize")) return rc;
+      }
       g_last_kernel = mfma_any_name(true, dtype, any_dp, any_aligned);
       return RECIR_HSTU_OK;
     }
-    const bool per_token = attn_scale && (flags & RECIR_HSTU_FLAG_SCALE_PER_TOKEN);
     if (drab) {
       // The query-tile kernel sums dS along the diagonals as fixed-point integers, in LDS (float LDS
       // atomics run one lane at a time) and then in a 64-bit table per head (integer additions commute:

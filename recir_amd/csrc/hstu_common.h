@@ -238,8 +238,8 @@ struct BwdParams {
                      // bf16 magnitude << 16, i.e. the bits of a float (key-tile kernel), word 2 holds the
                      // largest |per-token scale| (bits of a float); both are read by the query-tile
                      // kernel; else null
-  const unsigned* dout_max;  // with drab (tiled kernels): [H] largest |dout| of each head, bits of a float
-  long long* drab_fx;        // with drab (tiled kernels): [H, 2N-1] fixed-point sums along the diagonals
+  const unsigned* dout_max;  // with drab (MFMA kernels): [H] largest |dout| of each head, bits of a float
+  long long* drab_fx;        // with drab (MFMA kernels): [H, 2N-1] fixed-point sums along the diagonals
 };
 
 // Fixed-point scale of the bias-table gradient of one head: a power of two 2^sh such that `bound`
@@ -252,13 +252,13 @@ __device__ __forceinline__ void drab_fx_scales(float bound, float& fx_scale, flo
   fx_scale = usable ? __uint_as_float((unsigned)(127 + sh) << 23) : 0.f;
   fx_inv = usable ? __uint_as_float((unsigned)(127 - sh) << 23) : (bound == 0.f ? 0.f : __uint_as_float(0x7fc00000u));
 }
-// The bound itself: |dS| <= 1.1 |dP|, |dP| <= 128 max|dout of the head| max|v| (times the largest
+// The bound itself: |dS| <= 1.1 |dP|, |dP| <= Dv max|dout of the head| max|v| (times the largest
 // per-token scale where there is one), and a diagonal meets at most 64 pairs of a (128-row, 64-key) tile.
 __device__ __forceinline__ float drab_fx_bound(const BwdParams& bp, int h, bool per_token) {
   const float dmx = __uint_as_float(bp.dout_max[h]);
   const float vmx = __uint_as_float(__hip_atomic_load(bp.absmax + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
   const float rmx = per_token ? __uint_as_float(__hip_atomic_load(bp.absmax + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) : 1.0f;
-  return dmx * vmx * rmx * (128.0f * 1.1f * 64.0f);
+  return dmx * vmx * rmx * ((float)bp.f.Dv * 1.1f * 64.0f);
 }
 
 }  // namespace recir_hstu

@@ -174,9 +174,11 @@ __attribute__((amdgpu_waves_per_eu((any_workgroups_per_cu<MODE, ELT, DP>()), (an
   __shared__ float bias_s[2][ANY_BM + ANY_BN];
   __shared__ float scale_s[2][ANY_BN];
   __shared__ float red_s[4];
-  // DQ with the gradient of the bias table: dS of a tile summed along its 191 diagonals, one band per
-  // LDS stage (float LDS atomics; the band of tile t goes out to the table while tile t + 1 is computed)
-  __shared__ float dband_s[2][MODE == ANY_DQ ? ANY_BM + ANY_BN : 1];
+  // DQ with the gradient of the bias table: dS of a tile summed along its 191 diagonals as fixed-point
+  // integers, one band per LDS stage (integer LDS atomics; float ones run a lane at a time and tripled the
+  // backward); the band of tile t goes out to the head's 64-bit table while tile t + 1 is computed.  Integer
+  // additions commute: the gradient does not depend on the order of the workgroups.
+  __shared__ int dband_s[2][MODE == ANY_DQ ? ANY_BM + ANY_BN : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -230,7 +232,7 @@ __attribute__((amdgpu_waves_per_eu((any_workgroups_per_cu<MODE, ELT, DP>()), (an
     const size_t rb1 = (size_t)p.H * p.Dqk * ES, rb2 = (size_t)p.H * p.Dv * ES;
     const size_t hb1 = (size_t)h * p.Dqk * ES, hb2 = (size_t)h * p.Dv * ES;
     const float* __restrict__ rabg = HAS_RAB ? p.rab + (size_t)h * rab_w : nullptr;
-    float* __restrict__ drabg = (HAS_RAB && MODE == ANY_DQ && bp.drab) ? bp.drab + (size_t)h * rab_w : nullptr;
+    long long* __restrict__ drabg = (HAS_RAB && MODE == ANY_DQ && bp.drab_fx) ? bp.drab_fx + (size_t)h * rab_w : nullptr;
 
     // ---- stationary operands (B operand of the score products): lane holds row c ----
     const int cw0 = c0 + wave * 32;
@@ -313,7 +315,17 @@ __attribute__((amdgpu_waves_per_eu((any_workgroups_per_cu<MODE, ELT, DP>()), (an
     if (p.attn_scale && !per_token) uni = p.attn_scale[0];
     // scale of this lane's stationary row (queries), or what is left to apply to the key rows' sums
     const float col_scale = KEYS ? (per_token ? pow2_down : uni) : ((per_token && c_valid) ? p.attn_scale[si.s + c] : uni);
-    const float dscale = c_valid ? col_scale : 0.f;  // DQ: the factor dS lacks where it goes into the bias table's gradient
+    // DQ: what dS is multiplied by on its way into the bias table's gradient: the head's fixed-point scale (a
+    // power of two from a bound on |dS|, hstu_common.h) and a per-token scale of its row (a scale that is the
+    // same for every row is applied when the table is converted back)
+    float dscale = 0.f;
+    if constexpr (MODE == ANY_DQ && HAS_RAB) {
+      if (drabg) {
+        float fx_scale, fx_inv;
+        drab_fx_scales(drab_fx_bound(bp, h, per_token), fx_scale, fx_inv);
+        dscale = c_valid ? (per_token ? col_scale : 1.0f) * fx_scale : 0.f;
+      }
+    }
 
     const bool has_skip = skip_a < skip_b;
     auto next_tile = [&](int t) { return (has_skip && t + 1 == skip_a) ? skip_b : t + 1; };
@@ -594,7 +606,8 @@ __attribute__((amdgpu_waves_per_eu((any_workgroups_per_cu<MODE, ELT, DP>()), (an
             if constexpr (HAS_DP) dsv[r] = de;
             if constexpr (WITH_DRAB) {
               // d score / d bias = 1: the pair's dS (with its row's scale) goes to its diagonal
-              if (de != 0.f) atomicAdd(&dband_s[buf][(c - c0) - rl + (ANY_BN - 1)], de * dscale);
+              const int iv = __float2int_rn(de * dscale);
+              if (iv != 0) __hip_atomic_fetch_add(&dband_s[buf][(c - c0) - rl + (ANY_BN - 1)], iv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
             // the masked bodies four pairs at a time: left to itself the scheduler interleaves all 32 and spills
             if (PRED != 0 && (r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
@@ -650,15 +663,15 @@ __attribute__((amdgpu_waves_per_eu((any_workgroups_per_cu<MODE, ELT, DP>()), (an
     auto flush_band = [&](int tile, int b) __attribute__((always_inline)) {
       if constexpr (MODE == ANY_DQ) {
         if (drabg && tid < ANY_BM + ANY_BN - 1) {
-          const float v = dband_s[b][tid];
-          dband_s[b][tid] = 0.f;
+          const int v = dband_s[b][tid];
+          dband_s[b][tid] = 0;
           const int idx = c0 - tile * ANY_BN - (ANY_BN - 1) + tid + p.N - 1;  // entry e is the diagonal m - j = dmin + e
-          if (v != 0.f && idx >= 0 && idx < rab_w) unsafeAtomicAdd(&drabg[idx], v);
+          if (v != 0 && idx >= 0 && idx < rab_w) atomicAdd((unsigned long long*)&drabg[idx], (unsigned long long)(long long)v);
         }
       }
     };
     if constexpr (MODE == ANY_DQ) {
-      if (drabg && tid < ANY_BM + ANY_BN) dband_s[0][tid] = dband_s[1][tid] = 0.f;  // (published by the first tile's barrier)
+      if (drabg && tid < ANY_BM + ANY_BN) dband_s[0][tid] = dband_s[1][tid] = 0;  // (published by the first tile's barrier)
     }
 
     Staged st;

@@ -216,8 +216,9 @@ def test_backward_masks(oracle, mask, dtype, dims, scale_kind):
                          ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}-{c[3]}")
 @pytest.mark.parametrize("scale_kind", ["default", "per_token"])
 def test_gradient_of_the_bias_table(oracle, case, scale_kind):
-    """d rab from the dQ pass of the general kernels: dS summed along the diagonals of a tile in LDS (float
-    atomics), the band added to the table per tile.  Against the oracle; columns no pair touches stay zero."""
+    """d rab from the dQ pass of the general kernels: dS summed along the diagonals of a tile in LDS as fixed-point
+    integers, the band added to the head's 64-bit table per tile.  Against the oracle; columns no pair touches
+    stay zero; two calls give the same bits."""
     import recir_amd
     from recir_amd import _lib
 
@@ -247,6 +248,13 @@ def test_gradient_of_the_bias_table(oracle, case, scale_kind):
     report(f"d rab {case} {scale_kind}", st)
     assert st["ref_max"] > 0 and st["rel_to_max"] <= tol and st["rel_fro"] <= tol, st
     assert not drab.cpu().numpy()[np.asarray(want[3]) == 0].any()
+    # fixed-point sums: the same bits whatever order the workgroups run in
+    again = recir_amd.jagged_hstu_attention_backward(dout.to(q.device, q.dtype), q, k, v, off, nt,
+                                                     None if scale is None else scale.cuda(), rab_grad=True,
+                                                     max_seq_len=wl.max_seq_len, alpha=wl.alpha, contextual_seq_len=ctx,
+                                                     rab=wl.rab.cuda(), max_attn_len=A, full_attn_size=F,
+                                                     invalid_attn_mask_type=mask_type)
+    assert torch.equal(again[3], drab)
 
 
 def test_fp16_backward_with_small_per_token_scales(oracle):
