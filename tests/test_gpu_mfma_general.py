@@ -212,7 +212,8 @@ def test_backward_masks(oracle, mask, dtype, dims, scale_kind):
 
 
 @pytest.mark.parametrize("case", [("bf16", 64, 64, "causal_ctx"), ("fp16", 96, 40, "semilocal_ctx"), ("fp32", 32, 32, "causal_ctx"),
-                                  ("bf16", 128, 128, "noncausal_window"), ("bf16", 256, 256, "causal_ctx")],
+                                  ("bf16", 128, 128, "noncausal_window"), ("bf16", 256, 256, "causal_ctx"),
+                                  ("bf16", 50, 50, "causal_ctx")],
                          ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}-{c[3]}")
 @pytest.mark.parametrize("scale_kind", ["default", "per_token"])
 def test_gradient_of_the_bias_table(oracle, case, scale_kind):
