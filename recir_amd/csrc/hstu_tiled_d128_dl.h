@@ -380,7 +380,13 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     // silu + mask + bf16 packing of one 32 x 32 score block (accumulator layout) into two B operands
     auto silu_pack = [&](auto masked_tag, const f32x16& sv, int k0, int kvb, unsigned rab_addr, bf16x8& o0,
                          bf16x8& o1) __attribute__((always_inline)) {
-      constexpr int MASKED = decltype(masked_tag)::value;  // 0 none, 1 general predicate, 2 range of a history row
+      constexpr int MASKED = decltype(masked_tag)::value;  // 0 none, 1 general predicate, 2 range of a history row, 5 nothing kept
+      if constexpr (MASKED == 5) {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        o0 = __builtin_bit_cast(bf16x8, z);
+        o1 = __builtin_bit_cast(bf16x8, z);
+        return;
+      }
       int rng_base = 0;
       unsigned rng_w = 0;
       if (MASKED == 2) rng_of(k0, rng_base, rng_w);
@@ -415,6 +421,11 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
     auto tile_body = [&](auto masked_tag, auto buf_tag, int k0, int nxt, auto fast_tag) __attribute__((always_inline)) {
       constexpr int BUF = decltype(buf_tag)::value;
       constexpr bool FAST = decltype(fast_tag)::value;  // the next tile exists and is whole
+      // Tags 3 and 4 are the general predicate (1) decided per 32-key block: 3 keeps every pair of the
+      // first block and tests the second, 4 tests the first and keeps none of the second.
+      constexpr int TAG = decltype(masked_tag)::value;
+      const std::integral_constant<int, TAG == 3 ? 0 : (TAG == 4 ? 1 : TAG)> blk0_tag{};
+      const std::integral_constant<int, TAG == 3 ? 1 : (TAG == 4 ? 5 : TAG)> blk1_tag{};
       const char* kb = (const char*)(BUF ? Ks1 : Ks0);
       const char* vb = (const char*)(BUF ? Vs1 : Vs0);
       // LDS byte address of this lane's part of the tile's bias band; opaque per tile, so that the
@@ -436,7 +447,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       // The slot schedule: every bf16 tile body but the one with the general mask predicate and no bias
       // (its mask state leaves this schedule too few registers: 7 % slower there); with a bias every
       // body (the other schedule would add the bias in the SiLU arithmetic: 2-3 % slower).
-      if constexpr (!FP8 && (decltype(masked_tag)::value != 1 || HAS_RAB)) {
+      if constexpr (!FP8 && ((TAG != 1 && TAG != 3 && TAG != 4) || HAS_RAB)) {
         // Hand-placed schedule, one MFMA per slot with a scheduling fence after each:
         //   slots  0..7   S0 = K[0:32] Q^T            slots  8..15  S1 = K[32:64] Q^T
         //   slots 16..31  O^T[db] += V^T[db, s2] P^T[s2], key step s2 = (slot - 16) / 4, db = slot & 3
@@ -578,7 +589,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
         load_group(4, fa);
         s1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kb0, q8[0], zero, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
         s1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kb1, q8[1], s1, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
-        silu_pack(masked_tag, s0, k0, 0, rab_addr, pb0, pb1);
+        silu_pack(blk0_tag, s0, k0, 0, rab_addr, pb0, pb1);
       } else {
       load_group(0, fa);
       if constexpr (FAST) issue_tile_as(nxt, other, std::true_type{}); else if (nxt < nkv) issue_tile(nxt, other);
@@ -591,7 +602,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       // groups 2 and 3 with silu(S0)
       load_group(3, fb);
       mfma_group(2, fa);
-      silu_pack(masked_tag, s0, k0, 0, rab_addr, pb0, pb1);
+      silu_pack(blk0_tag, s0, k0, 0, rab_addr, pb0, pb1);
       load_group(4, fa);
       mfma_group(3, fb);
       // MFMAs issue in pairs: the second of a back-to-back pair costs less issue time than a lone one
@@ -614,7 +625,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       // groups 4 and 5 with silu(S1)
       load_group(5, fb);
       mfma_group(4, fa);
-      silu_pack(masked_tag, s1, k0, 1, rab_addr, pb2, pb3);
+      silu_pack(blk1_tag, s1, k0, 1, rab_addr, pb2, pb3);
       load_group(6, fa);
       mfma_group(5, fb);
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
@@ -752,6 +763,10 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       const bool range_mask = SEMI && m_hi < si.cap && k0 >= si.ctx_eff;
       if (full) tile_body(std::integral_constant<int, 0>{}, buf_tag, k0, nxt, std::false_type{});
       else if (SEMI && range_mask) tile_body(std::integral_constant<int, 2>{}, buf_tag, k0, nxt, std::false_type{});
+      else if (!SEMI && !HAS_RAB && (k0 + 31 <= m_lo) && (k0 + 32 <= si.cap))  // first 32 keys kept by every row of the wave
+        tile_body(std::integral_constant<int, 3>{}, buf_tag, k0, nxt, std::false_type{});
+      else if (!SEMI && !HAS_RAB && (k0 + 32 > m_hi) && (k0 + 32 >= si.ctx_eff))  // last 32 keys above every row, none contextual
+        tile_body(std::integral_constant<int, 4>{}, buf_tag, k0, nxt, std::false_type{});
       else tile_body(std::integral_constant<int, 1>{}, buf_tag, k0, nxt, std::false_type{});
       return full ? 2 : 3;  // class of the tile for this wave (phase-trace builds): 2 unmasked, 3 partial, 4 skipped
     };
