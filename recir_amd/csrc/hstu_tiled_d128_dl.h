@@ -447,7 +447,7 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       // The slot schedule: every bf16 tile body but the one with the general mask predicate and no bias
       // (its mask state leaves this schedule too few registers: 7 % slower there); with a bias every
       // body (the other schedule would add the bias in the SiLU arithmetic: 2-3 % slower).
-      if constexpr (!FP8 && ((TAG != 1 && TAG != 3 && TAG != 4) || HAS_RAB)) {
+      if constexpr (!FP8 && (TAG != 1 || HAS_RAB)) {
         // Hand-placed schedule, one MFMA per slot with a scheduling fence after each:
         //   slots  0..7   S0 = K[0:32] Q^T            slots  8..15  S1 = K[32:64] Q^T
         //   slots 16..31  O^T[db] += V^T[db, s2] P^T[s2], key step s2 = (slot - 16) / 4, db = slot & 3
@@ -474,8 +474,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
           return s < 16 ? k_frag(s >> 3, s & 7) : v_frag(pv_db(s), pv_s2(s));
         };
         auto silu_unit = [&](int u) __attribute__((always_inline)) {
-          constexpr int MASKED = decltype(masked_tag)::value;
           const int blk = u >> 3, e = u & 7;
+          const int MASKED = blk ? decltype(blk1_tag)::value : decltype(blk0_tag)::value;  // (folds: u is an unrolled loop's constant)
+          if (MASKED == 5) { pw[blk][e] = 0u; return; }
           float pe[2];
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
@@ -763,9 +764,9 @@ __global__ __launch_bounds__(256, 2) void hstu_fwd_tiled_d128_dl(Params p) {
       const bool range_mask = SEMI && m_hi < si.cap && k0 >= si.ctx_eff;
       if (full) tile_body(std::integral_constant<int, 0>{}, buf_tag, k0, nxt, std::false_type{});
       else if (SEMI && range_mask) tile_body(std::integral_constant<int, 2>{}, buf_tag, k0, nxt, std::false_type{});
-      else if (!SEMI && !HAS_RAB && (k0 + 31 <= m_lo) && (k0 + 32 <= si.cap))  // first 32 keys kept by every row of the wave
+      else if (!SEMI && (k0 + 31 <= m_lo) && (k0 + 32 <= si.cap))  // first 32 keys kept by every row of the wave
         tile_body(std::integral_constant<int, 3>{}, buf_tag, k0, nxt, std::false_type{});
-      else if (!SEMI && !HAS_RAB && (k0 + 32 > m_hi) && (k0 + 32 >= si.ctx_eff))  // last 32 keys above every row, none contextual
+      else if (!SEMI && (k0 + 32 > m_hi) && (k0 + 32 >= si.ctx_eff))  // last 32 keys above every row, none contextual
         tile_body(std::integral_constant<int, 4>{}, buf_tag, k0, nxt, std::false_type{});
       else tile_body(std::integral_constant<int, 1>{}, buf_tag, k0, nxt, std::false_type{});
       return full ? 2 : 3;  // class of the tile for this wave (phase-trace builds): 2 unmasked, 3 partial, 4 skipped
